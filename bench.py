@@ -1,0 +1,190 @@
+"""Headline benchmark: streaming Taylor + merge-and-reduce coreset causal attention prefill on one
+MI355X.
+
+Workload (default): batch 1 x 32 heads, N = 65536, d = dv = 64, Taylor degree 2 (2145 monomial
+features), article block 256, scale 1/sqrt(64), sorted_pair compressor with log2(N/256) merge levels,
+fp32; q and k uniform in the radius-1 ball, v ~ N(0, 1), seed 0 (synthetic, generated on the host in
+the reference's draw order and copied to HBM before timing).
+
+One step = one full forward through the public API path (moment scan K1, level-tree compressor K3,
+fused residual + normalisation K2/K4).  Prints one JSON line:
+  value = head-tokens/s (B*H*N / step time), roofline of the dominant kernel (the moment scan, fp32
+  MFMA) from HIP events recorded around its launches inside the timed region, and the CPU baseline:
+  the reference CPU fast path (oracle restatement, flat sorted_pair coreset, stream moments) timed on
+  a bounded sample of one head on this host's cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (str(ROOT / "streaming-attention_amd"),):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import torch  # noqa: E402
+
+WORKLOAD = dict(workload="prefill_levels_c3", batch=1, heads=32, seq_len=65536, d=64, dv=64, degree=2, block=256,
+                scale=0.125, compressor="sorted_pair", semantics="merge-and-reduce levels", data="unit_ball r=1",
+                dtype="fp32", seed=0)
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+def make_inputs(batch, heads, n, d, dv, seed):
+    """randn q, k, v then ball radii rand^(1/d) for q then k (the reference's draw order)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    q = torch.randn(batch, heads, n, d, generator=g)
+    k = torch.randn(batch, heads, n, d, generator=g)
+    v = torch.randn(batch, heads, n, dv, generator=g)
+    qn = torch.clamp(torch.linalg.vector_norm(q, dim=-1, keepdim=True), min=1e-12)
+    kn = torch.clamp(torch.linalg.vector_norm(k, dim=-1, keepdim=True), min=1e-12)
+    rq = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d)
+    rk = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d)
+    return q / qn * rq, k / kn * rk, v
+
+
+def cpu_baseline(q, k, v, w):
+    """Reference CPU fast path on one head (bounded sample), via the oracle."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import reference_cpu as oracle
+
+    threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "8192"))
+    t = oracle.time_fast_path_sample(q[0, 0].contiguous(), k[0, 0].contiguous(), v[0, 0].contiguous(),
+                                     degree=w["degree"], block=w["block"], scale=w["scale"], seed=w["seed"], rows=rows)
+    n = w["seq_len"]
+    return {
+        "value": n / t["total_s"],
+        "unit": "head-tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference CPU fast path restated in oracle/ (stream moments, flat sorted_pair coreset, "
+                   f"query chunks of 2048), 1 head of the workload (N={n}); token loop, q x reps residual and "
+                   f"in-block residual timed over the first {rows} rows and scaled by N/{rows}, reps built "
+                   f"for all N; per-part seconds/head {json.dumps({k2: round(v2, 3) for k2, v2 in t.items()})}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seq-len", type=int, default=WORKLOAD["seq_len"])
+    ap.add_argument("--heads", type=int, default=WORKLOAD["heads"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (heads shard with no "
+              f"communication across GPUs; see DESIGN.md)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    import _engine
+    import _plan
+    import streaming_taylor_coreset_attention as stc
+
+    w = dict(WORKLOAD, seq_len=args.seq_len, heads=args.heads)
+    bh, n, d, dv = w["batch"] * w["heads"], w["seq_len"], w["d"], w["dv"]
+    print(f"[bench] generating inputs {w['batch']}x{w['heads']}x{n}x{d}", file=sys.stderr, flush=True)
+    q, k, v = make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"])
+    dev = torch.device("cuda:0")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    q3, k3, v3 = qd.reshape(bh, n, d), kd.reshape(bh, n, d), vd.reshape(bh, n, dv)
+
+    t_plan = time.perf_counter()
+    plan = _plan.levels_plan(n, w["block"], w["compressor"])
+    _plan.draws_for(plan, _plan.sequence_seeds(w["seed"], bh), d, w["compressor"])
+    t_plan = time.perf_counter() - t_plan
+
+    def step(timer=None):
+        return _engine.prefill(q3, k3, v3, degree=w["degree"], block=w["block"], scale=w["scale"],
+                               semantics="levels", compressor=w["compressor"], seed=w["seed"], timer=timer)
+
+    # the public API path once, checked against the engine call the timing uses
+    api_out = stc.article_causal_attention(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"],
+                                           compressor=w["compressor"], seed=w["seed"])
+    for _ in range(args.warmup):
+        res = step()
+    torch.cuda.synchronize()
+    assert torch.equal(res.out.reshape(api_out.shape), api_out)
+    print(f"[bench] warmup done", file=sys.stderr, flush=True)
+
+    timer = _engine.KernelTimer()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step(timer)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = start.elapsed_time(end) / args.steps
+    per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_step": round(tot / args.steps, 4)}
+                  for name, (tot, cnt) in timer.totals_ms().items()}
+
+    f = _plan.num_features(d, w["degree"])
+    mom_flops = 4.0 * f * (dv + 1) * bh * n  # algorithmic: update + query, 2*F*(dv+1) each per head-token
+    mom_ms = per_kernel["moments"]["ms_total"] / per_kernel["moments"]["launches"]
+    achieved = mom_flops / (mom_ms * 1e-3) / 1e12
+    value = bh * n / (ms_step * 1e-3)
+
+    line = {
+        "metric": "head-tokens/sec, N=64K d=64 deg-2; % of HBM/MFMA roofline",
+        "value": value,
+        "unit": "head-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": w,
+        "roofline": {
+            "kernel": "moments_kernel (K1, exact Taylor moment scan)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+            "traffic": None,
+            "algorithmic_flops_per_launch": mom_flops,
+            "avg_launch_ms": mom_ms,
+        },
+        "kernels": per_kernel,
+        "host_plan_and_draws_s": round(t_plan, 3),
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu_baseline:
+        print(f"[bench] timing CPU baseline", file=sys.stderr, flush=True)
+        cb = cpu_baseline(q, k, v, w)
+        line["cpu_baseline"] = cb
+        line["speedup_vs_cpu_baseline"] = value / cb["value"]
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

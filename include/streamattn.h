@@ -1,0 +1,128 @@
+/*
+ * streamattn.h -- C ABI of the MI355X (gfx950) streaming Taylor+coreset causal attention library
+ * (libstreamattn.so).
+ *
+ * The reference (PositiveLoss/streaming-attention) is pure Python/PyTorch; its only host->device
+ * crossing is the Triton launch at triton_article_attention.py:535-559.  Every entry point below is a
+ * kernel launch that replaces one piece of the reference's hot path; the Python modules of this
+ * package bind them with ctypes behind the reference's own Python API.
+ *
+ * Conventions
+ *   - All tensors are caller-owned device buffers passed as raw pointers; the library never
+ *     allocates or frees device memory.  q/k are contiguous [BH, N, D], v is [BH, N, Dv].
+ *   - dtype codes: STA_F32, STA_BF16, STA_F16 (inputs are read as such, arithmetic is fp32).
+ *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous.
+ *   - Every function returns STA_OK (0) or a positive status; sta_status_string() names it.
+ */
+#ifndef STREAMATTN_H
+#define STREAMATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STA_OK 0
+#define STA_ERR_SHAPE 1       /* inconsistent sizes / counts                          */
+#define STA_ERR_UNSUPPORTED 2 /* degree, D, Dv or block beyond the kernels' limits     */
+#define STA_ERR_DTYPE 3       /* unknown dtype code                                    */
+#define STA_ERR_HIP 4         /* a HIP runtime call failed (see sta_last_hip_error)    */
+#define STA_ERR_ARG 5         /* null pointer or out-of-range scalar argument          */
+
+#define STA_F32 0
+#define STA_BF16 1
+#define STA_F16 2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int sta_version(void);
+
+/* Human-readable name of a status code. */
+const char* sta_status_string(int status);
+
+/* hipError_t of the last failing HIP call made by this library on this thread (0 if none). */
+int sta_last_hip_error(void);
+
+/* Kernel limits: max D, max Dv, max Taylor degree, max compressor input size. */
+int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
+
+/*
+ * Exact low-degree Taylor moments over all keys *before* each row's chunk (K1).
+ * Replaces low_degree_taylor_causal_sums / _stream / _prefix (fast_article_attention.py:184-285) and
+ * TaylorMomentSketch.update/query (streaming_taylor_coreset_attention.py:265-296).
+ *   chunk c covers rows [c*chunk - shift, (c+1)*chunk - shift); chunk is 64 (D <= 64) or 32 (D <= 128)
+ *   feat_idx / feat_coef: the symmetric monomial table (fsplit * feat_per_split entries, feat_per_split
+ *     a multiple of 16): packed indices i0 | i1<<8 | i2<<16 into [x_0..x_{D-1}, 1] and the key-side
+ *     coefficient 1/prod(alpha!) (0 for padding features).
+ *   outputs: low_num [BH][fsplit][N][Dv], low_den [BH][fsplit][N] (fp32, partial over feature splits).
+ */
+int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                int degree, float scale, int chunk, int shift, int fsplit, int feat_per_split,
+                const uint32_t* feat_idx, const float* feat_coef, float* low_num, float* low_den, void* stream);
+
+/*
+ * Block compressor for one batch of coreset nodes (K3), all heads at once.
+ * Replaces _compress_one_completed_block (fast_article_attention.py:312-361) for the flat block coreset
+ * and MergeReduceCoreset._compress* (streaming_taylor_coreset_attention.py:413-467) for level merges.
+ *   batch_nodes[n_batch]: node ids to compute in this launch (their inputs must already exist).
+ *   node_desc[n_nodes][8]: kind (0 raw block, 1 merge), a, b (raw: first token; merge: child ids),
+ *     n_in, n_out, method (0 copy, 1 sorted_pair, 2 permutation), draw slot, unused.
+ *   dirs [BH][n_draws][D] (normalised projection), unif [BH][n_draws][max_in/2] (pair uniforms),
+ *   perms [BH][n_draws][max_in] (randperm draws): the seed-derived draws, replayed by the host.
+ *   outputs: node_src [BH][n_nodes][cap] (global token index of each kept item), node_w (its weight).
+ */
+int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
+                       int n_batch, const int32_t* node_desc, int n_nodes, int cap, const float* dirs,
+                       const float* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
+                       float* node_w, void* stream);
+
+/*
+ * Segment-mean representatives of completed blocks (the Triton path's coreset).
+ * Replaces build_segment_mean_coreset (triton_article_attention.py:189-245).
+ *   n_rep = ((N-1)//block) * (block/stride); outputs rep_k [BH][n_rep][D], rep_v [BH][n_rep][Dv] fp32.
+ */
+int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv, int block,
+                     int stride, int64_t n_rep, float* rep_k, float* rep_v, void* stream);
+
+/*
+ * Fused residual + normalisation per tile of 128 query rows (K2 + K4).
+ * Replaces _full_residual_tail / _block_coreset_residual_tail and the combine
+ * (fast_article_attention.py:437-514, :596-598), the query side of ArticleStreamingAttention
+ * (streaming_taylor_coreset_attention.py:581-599) and _article_direct_kernel
+ * (triton_article_attention.py:265-369).
+ *   mode: 0 flat block coreset, 1 merge-and-reduce levels, 2 exact residual (compressor "none"),
+ *     3 Taylor part only (no residual; used with out_den for the raw low-degree sums).
+ *   tiles: tile t covers rows [t*128 - shift, (t+1)*128 - shift); n_tiles = ceil((N+shift)/128).
+ *   tile_ptr[n_tiles+1] / tile_nodes: CSR list of the nodes each tile needs.
+ *   node_meta[n_nodes][4]: item count, first and last active row, materialized flag (items index
+ *     rep_k/rep_v instead of k/v).
+ *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
+ *   out: [BH][N][Dv] in out_dtype.
+ *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator
+ *     and out_den [BH][N] the denominator, unnormalised (the low_num/low_den pair of
+ *     low_degree_taylor_causal_sums, fast_article_attention.py:262-285, when mode is 3).
+ */
+int sta_block_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
+                        int dv, int degree, float scale, float eps, int mode, int block, int chunk, int shift,
+                        int exp_clamp, const float* low_num, const float* low_den, int fsplit,
+                        const int32_t* tile_ptr, const int32_t* tile_nodes, int n_tiles, const int32_t* node_meta,
+                        int n_nodes, int cap, const int32_t* node_src, const float* node_w, const float* rep_k,
+                        const float* rep_v, int64_t n_rep, void* out, int out_dtype, float* out_den,
+                        void* stream);
+
+/* Rows per block-attention tile and the moment chunk the library uses for a head dimension D. */
+int sta_tile_rows(void);
+int sta_moment_chunk(int d);
+
+/*
+ * Self-test of the matrix-core operand layout assumed by the kernels: computes D = A(16x4) * B(4x16)
+ * with one v_mfma_f32_16x16x4_f32 from a[64], b[64] given in the assumed lane layout and writes the
+ * 16x16 result row-major to d_out[256].  Device buffers, synchronous.
+ */
+int sta_selftest_mfma(const float* a, const float* b, float* d_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STREAMATTN_H */

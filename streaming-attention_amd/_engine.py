@@ -1,0 +1,240 @@
+"""Launch sequence of the prefill path on one ROCm device:
+
+    K1 moments (sta_moments)  ->  K3 compress, one launch per tree level (sta_compress_nodes)
+                              ->  K2+K4 block attention with the normalisation (sta_block_attention)
+
+All launches go to torch's current stream of the input device.  Device buffers are torch tensors
+allocated here (the C ABI never allocates); plan arrays and draw tables are cached per device.
+"""
+
+from __future__ import annotations
+
+import os
+import threading
+from dataclasses import dataclass
+from typing import Callable, Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+import _native
+import _plan
+
+SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
+
+_dev_lock = threading.Lock()
+_dev_cache: Dict[tuple, object] = {}
+
+
+def _on_device(key: tuple, device: torch.device, build: Callable[[], object]):
+    full = key + (str(device),)
+    with _dev_lock:
+        hit = _dev_cache.get(full)
+    if hit is not None:
+        return hit
+    val = build()
+    with _dev_lock:
+        if len(_dev_cache) > 128:
+            _dev_cache.clear()
+        _dev_cache[full] = val
+    return val
+
+
+def _i32(a: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(device)
+
+
+def _f32(a: np.ndarray, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+
+
+class KernelTimer:
+    """Records HIP events around each launch on the launch stream (for measured per-kernel times)."""
+
+    def __init__(self) -> None:
+        self.events: Dict[str, list] = {}
+
+    def wrap(self, name: str, fn: Callable[[], None]) -> None:
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        self.events.setdefault(name, []).append((s, e))
+
+    def totals_ms(self) -> Dict[str, Tuple[float, int]]:
+        torch.cuda.synchronize()
+        out = {}
+        for name, evs in self.events.items():
+            out[name] = (sum(s.elapsed_time(e) for s, e in evs), len(evs))
+        return out
+
+
+def _run(timer: Optional[KernelTimer], name: str, fn: Callable[[], None]) -> None:
+    if timer is None:
+        fn()
+    else:
+        timer.wrap(name, fn)
+
+
+@dataclass
+class PrefillResult:
+    out: torch.Tensor
+    node_src: Optional[torch.Tensor]
+    node_w: Optional[torch.Tensor]
+    plan: _plan.NodePlan
+    feature_count: int
+    fsplit: int
+    den: Optional[torch.Tensor] = None  # raw denominator (semantics "taylor")
+
+
+def prefill(
+    q3: torch.Tensor,
+    k3: torch.Tensor,
+    v3: torch.Tensor,
+    *,
+    degree: int,
+    block: int,
+    scale: float,
+    semantics: str,
+    compressor: str = "sorted_pair",
+    seed: int = 0,
+    eps: float = 1e-12,
+    out_dtype: torch.dtype = torch.float32,
+    stride: int = 1,
+    exp_clamp: bool = False,
+    draws: Optional[_plan.Draws] = None,
+    timer: Optional[KernelTimer] = None,
+) -> PrefillResult:
+    """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype."""
+    if semantics not in SEMANTICS:
+        raise ValueError(f"semantics must be one of {SEMANTICS}")
+    for t in (q3, k3, v3):
+        _native.require_device(t)
+    if not (q3.dtype == k3.dtype == v3.dtype) or q3.dtype not in _native.DTYPE_CODES:
+        raise ValueError("q, k, v must share one of the dtypes float32, bfloat16, float16")
+    lib = _native.lib()
+    dev = q3.device
+    bh, n, d = q3.shape
+    dv = v3.shape[-1]
+    lim = _native.limits()
+    if d > lim["max_d"] or dv > lim["max_dv"]:
+        raise ValueError(f"the HIP kernels support D <= {lim['max_d']} and Dv <= {lim['max_dv']}")
+    if degree > lim["max_degree"]:
+        raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+    dt = _native.DTYPE_CODES[q3.dtype]
+    odt = _native.DTYPE_CODES[out_dtype]
+    stream = _native.stream_handle(dev)
+    chunk = _plan.moment_chunk(d)
+
+    fsplit = int(os.environ.get("STA_FSPLIT", "0")) or _plan.choose_fsplit(d, degree, bh, dv)
+    fp = _plan.feature_plan(d, degree, fsplit)
+    fidx, fcoef = _on_device(("feat", d, degree, fsplit), dev, lambda: (_i32(fp.idx, dev), _f32(fp.coef, dev)))
+
+    raw = semantics == "taylor"
+    if semantics in ("exact", "taylor"):
+        plan = _plan.exact_plan(n)
+    elif semantics == "flat":
+        plan = _plan.flat_plan(n, block, compressor)
+    elif semantics == "levels":
+        plan = _plan.levels_plan(n, block, compressor)
+    else:
+        plan, n_rep, _rpb = _plan.segment_plan(n, block, stride)
+    shift = plan.shift
+    mode = _plan.MODE_TAYLOR if raw else plan.mode
+    if plan.call_sizes and max(plan.call_sizes) > lim["max_compress_in"]:
+        raise ValueError(f"block_size {block} needs compress calls on {max(plan.call_sizes)} items; "
+                         f"the HIP compressor handles at most {lim['max_compress_in']}")
+
+    # ---- host side first: every validation error is raised before anything is launched ----
+    pkey = (plan.mode, plan.n, plan.block, compressor if semantics != "segment" else stride)
+    meta_d, tptr_d, tnodes_d = _on_device(
+        ("plan",) + pkey, dev,
+        lambda: (_i32(plan.meta, dev), _i32(plan.tile_ptr, dev), _i32(np.maximum(plan.tile_nodes, 0) if plan.tile_nodes.size else np.zeros(1, np.int32), dev)),
+    )
+    if semantics != "segment" and plan.batches:
+        seeds = _plan.sequence_seeds(seed, bh)
+        if draws is None:
+            dr, desc = _plan.draws_for(plan, seeds, d, compressor)
+            dirs_d, unif_d, perms_d, desc_d = _on_device(
+                ("draws",) + pkey + (seeds, d), dev,
+                lambda: (_f32(dr.dirs, dev), _f32(dr.unif, dev), _i32(dr.perms, dev), _i32(desc, dev)),
+            )
+        else:
+            dr = draws
+            n_calls = max(len(plan.call_sizes), 1)
+            need = max(plan.call_sizes)
+            if (dr.dirs.shape != (bh, n_calls, d) or dr.max_in < need or dr.unif.shape != (bh, n_calls, dr.max_in // 2)
+                    or dr.perms.shape != (bh, n_calls, dr.max_in)):
+                raise ValueError("explicit draws do not match the compress-call layout of this configuration")
+            _, desc = _plan.draws_for(plan, seeds[:1], d, compressor)
+            dirs_d, unif_d, perms_d, desc_d = (_f32(dr.dirs, dev), _f32(dr.unif, dev), _i32(dr.perms, dev), _i32(desc, dev))
+        batches_d = _on_device(("batches",) + pkey, dev, lambda: [_i32(b, dev) for b in plan.batches])
+
+    low_num = torch.empty((bh, fsplit, n, dv), device=dev, dtype=torch.float32)
+    low_den = torch.empty((bh, fsplit, n), device=dev, dtype=torch.float32)
+
+    def k1():
+        st = lib.sta_moments(
+            q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), dt, bh, n, d, dv, degree, float(scale), chunk, shift,
+            fsplit, fp.per_split, fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+        _native.check(st, "sta_moments")
+
+    _run(timer, "moments", k1)
+
+    node_src = node_w = None
+    rep_k = rep_v = None
+    n_rep_arg = 0
+    if semantics == "segment":
+        n_rep_arg = n_rep
+        if n_rep > 0:
+            rep_k = torch.empty((bh, n_rep, d), device=dev, dtype=torch.float32)
+            rep_v = torch.empty((bh, n_rep, dv), device=dev, dtype=torch.float32)
+
+            def k_seg():
+                st = lib.sta_segment_mean(k3.data_ptr(), v3.data_ptr(), dt, bh, n, d, dv, block, stride, n_rep,
+                                          rep_k.data_ptr(), rep_v.data_ptr(), stream)
+                _native.check(st, "sta_segment_mean")
+
+            _run(timer, "segment_mean", k_seg)
+            rpb = block // stride
+            src_np = np.arange(plan.n_nodes * plan.cap, dtype=np.int32).reshape(plan.n_nodes, plan.cap)
+            src_np = np.where(src_np < n_rep, src_np, 0).astype(np.int32)
+            node_src, node_w = _on_device(
+                ("segnodes", n, block, stride, bh), dev,
+                lambda: (_i32(np.broadcast_to(src_np, (bh,) + src_np.shape).copy(), dev),
+                         torch.full((bh, plan.n_nodes, plan.cap), float(stride), device=dev, dtype=torch.float32)),
+            )
+            del rpb
+    elif plan.batches:
+        node_src = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.int32)
+        node_w = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.float32)
+        for bd in batches_d:
+            def k3_launch(bd=bd):
+                st = lib.sta_compress_nodes(
+                    k3.data_ptr(), dt, bh, n, d, bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(), plan.n_nodes,
+                    plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(), dr.dirs.shape[1],
+                    dr.max_in, node_src.data_ptr(), node_w.data_ptr(), stream)
+                _native.check(st, "sta_compress_nodes")
+
+            _run(timer, "compress", k3_launch)
+
+    if raw:
+        out = torch.empty((bh, n, dv), device=dev, dtype=torch.float32)
+        out_den = torch.empty((bh, n), device=dev, dtype=torch.float32)
+    else:
+        out = torch.empty((bh, n, dv), device=dev, dtype=out_dtype)
+        out_den = None
+    n_nodes_arg = plan.n_nodes if (node_src is not None) else 0
+
+    def k24():
+        st = lib.sta_block_attention(
+            q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), dt, bh, n, d, dv, degree, float(scale), float(eps), mode,
+            block, chunk, shift, 1 if exp_clamp else 0, low_num.data_ptr(), low_den.data_ptr(), fsplit,
+            tptr_d.data_ptr(), tnodes_d.data_ptr(), plan.n_tiles, meta_d.data_ptr(), n_nodes_arg, plan.cap,
+            _native.ptr(node_src), _native.ptr(node_w), _native.ptr(rep_k), _native.ptr(rep_v), n_rep_arg,
+            out.data_ptr(), odt, _native.ptr(out_den), stream)
+        _native.check(st, "sta_block_attention")
+
+    _run(timer, "block_attention", k24)
+    return PrefillResult(out, node_src, node_w, plan, fp.count, fsplit, out_den)

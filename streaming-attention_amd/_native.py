@@ -1,0 +1,122 @@
+"""ctypes binding of libstreamattn.so (the C ABI declared in include/streamattn.h).
+
+The shared library is built in-tree next to this file (see ``build_native.py``).  There is no CPU
+fallback anywhere in this package: if the library or a ROCm device is missing, ``lib()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+from typing import Optional
+
+import torch
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libstreamattn.so"
+
+STA_OK = 0
+STA_ERR_SHAPE = 1
+STA_ERR_UNSUPPORTED = 2
+STA_ERR_DTYPE = 3
+STA_ERR_HIP = 4
+STA_ERR_ARG = 5
+
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+_c_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); must mirror include/streamattn.h
+_SIGNATURES = {
+    "sta_version": (_i32, []),
+    "sta_status_string": (ctypes.c_char_p, [_i32]),
+    "sta_last_hip_error": (_i32, []),
+    "sta_limits": (_i32, [ctypes.POINTER(_i32)] * 4),
+    "sta_tile_rows": (_i32, []),
+    "sta_moment_chunk": (_i32, [_i32]),
+    "sta_moments": (
+        _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p, _c_p],
+    ),
+    "sta_compress_nodes": (
+        _i32,
+        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],
+    ),
+    "sta_segment_mean": (_i32, [_c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _c_p, _c_p, _c_p]),
+    "sta_block_attention": (
+        _i32,
+        [
+            _c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32,  # q k v dtype bh n d dv
+            _i32, _f32, _f32, _i32, _i32, _i32, _i32, _i32,  # degree scale eps mode block chunk shift clamp
+            _c_p, _c_p, _i32,  # low_num low_den fsplit
+            _c_p, _c_p, _i32, _c_p, _i32, _i32,  # tile_ptr tile_nodes n_tiles node_meta n_nodes cap
+            _c_p, _c_p, _c_p, _c_p, _i64,  # node_src node_w rep_k rep_v n_rep
+            _c_p, _i32, _c_p, _c_p,  # out out_dtype out_den stream
+        ],
+    ),
+    "sta_selftest_mfma": (_i32, [_c_p, _c_p, _c_p]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class NativeError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Load the shared library and attach the argument types (no device is touched)."""
+    p = pathlib.Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise ImportError(
+            f"libstreamattn.so not found at {p}; build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    handle = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (cached)."""
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == STA_OK:
+        return
+    l = lib()
+    msg = l.sta_status_string(status).decode()
+    if status == STA_ERR_HIP:
+        msg += f" (hipError {l.sta_last_hip_error()})"
+    raise NativeError(f"{what} failed: {msg}")
+
+
+def require_device(t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise ValueError("the HIP kernels require tensors on a ROCm GPU device")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def limits() -> dict:
+    vals = [_i32() for _ in range(4)]
+    lib().sta_limits(*[ctypes.byref(x) for x in vals])
+    return {"max_d": vals[0].value, "max_dv": vals[1].value, "max_degree": vals[2].value, "max_compress_in": vals[3].value}

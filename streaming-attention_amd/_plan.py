@@ -1,0 +1,368 @@
+"""Host-side plans for the HIP kernels: feature tables, seed-derived draws, coreset node DAGs and the
+per-tile node lists.  Everything here is a pure function of sizes and seeds (never of q/k/v), so it
+is computed once per configuration and cached.
+
+Random draws follow the reference's torch CPU generator call order exactly:
+  * flat block coreset: one generator seeded with `seed`; for every completed block that has a later
+    query, in block order: sorted_pair -> randn(d), rand(B//2); random (or sorted_pair with n <= 2)
+    -> randperm(n)   (fast_article_attention.py:339, :348, :328, :335, :395-419);
+  * merge-and-reduce levels: one generator seeded with `seed` at construction; one compress call per
+    completed block and one per cascade merge, in the order the binary counter produces them
+    (streaming_taylor_coreset_attention.py:367-368, :387-411, :427-467).
+The projection direction is normalised with the same torch ops as the reference
+(fast_article_attention.py:340), so it is bit-identical.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+import threading
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+TILE_ROWS = 128  # must equal sta_tile_rows()
+NODE_DESC = 8
+NODE_META = 4
+METHOD_COPY, METHOD_SORTED_PAIR, METHOD_PERM = 0, 1, 2
+KIND_RAW, KIND_MERGE = 0, 1
+MODE_FLAT, MODE_LEVELS, MODE_EXACT, MODE_TAYLOR = 0, 1, 2, 3
+COMPRESSORS = ("sorted_pair", "random", "none")
+
+_lock = threading.Lock()
+_cache: Dict[tuple, object] = {}
+
+
+def _cached(key, build):
+    with _lock:
+        hit = _cache.get(key)
+    if hit is not None:
+        return hit
+    val = build()
+    with _lock:
+        if len(_cache) > 256:
+            _cache.clear()
+        _cache[key] = val
+    return val
+
+
+def moment_chunk(d: int) -> int:
+    return 64 if d <= 64 else 32
+
+
+def num_features(d: int, degree: int) -> int:
+    return sum(math.comb(d + l - 1, l) if l > 0 else 1 for l in range(degree + 1))
+
+
+def _factorial_inverse(combo: Tuple[int, ...]) -> float:
+    """1 / prod_j alpha_j! for a non-decreasing multi-index."""
+    inv = 1.0
+    for _, run in itertools.groupby(combo):
+        inv /= math.factorial(len(list(run)))
+    return inv
+
+
+# ----------------------------------------------------------------------------- feature table
+
+@dataclass(frozen=True)
+class FeaturePlan:
+    d: int
+    degree: int
+    count: int
+    fsplit: int
+    per_split: int
+    idx: np.ndarray  # uint32 [fsplit * per_split]
+    coef: np.ndarray  # float32
+
+
+def choose_fsplit(d: int, degree: int, bh: int, dv: int, target_workgroups: int = 256) -> int:
+    ntile = -(-num_features(d, degree) // 16)
+    groups = -(-dv // 16)
+    fs_min = -(-ntile // (17 * 8))
+    fs_fill = -(-target_workgroups // max(1, bh * groups))
+    return max(fs_min, min(fs_fill, -(-ntile // 8)))
+
+
+def feature_plan(d: int, degree: int, fsplit: int) -> FeaturePlan:
+    """Monomial order [1, x_0..x_{d-1}, x_a x_b (a<=b, row-major), x_a x_b x_c (a<=b<=c, lexicographic)]:
+    the fast path's order for degree <= 2 (fast_article_attention.py:167-181) and
+    combinations_with_replacement for every degree (streaming_taylor_coreset_attention.py:170-178)."""
+
+    def build():
+        one = d  # slot d of a staged row holds the constant 1
+        idx: List[int] = []
+        coef: List[float] = []
+        for l in range(degree + 1):
+            for combo in itertools.combinations_with_replacement(range(d), l):
+                ids = list(combo) + [one] * (3 - l)
+                idx.append(ids[0] | (ids[1] << 8) | (ids[2] << 16))
+                coef.append(_factorial_inverse(combo))
+        count = len(idx)
+        per = -(-count // fsplit)
+        per = -(-per // 16) * 16
+        total = per * fsplit
+        pad = one | (one << 8) | (one << 16)
+        idx_a = np.full(total, pad, dtype=np.uint32)
+        coef_a = np.zeros(total, dtype=np.float32)
+        idx_a[:count] = np.asarray(idx, dtype=np.uint32)
+        coef_a[:count] = np.asarray(coef, dtype=np.float32)
+        return FeaturePlan(d, degree, count, fsplit, per, idx_a, coef_a)
+
+    if degree > 3 or d > 255:
+        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 255")
+    return _cached(("feat", d, degree, fsplit), build)
+
+
+# ----------------------------------------------------------------------------- draws
+
+def _compressed_size(n_in: int, compressor: str) -> int:
+    if compressor == "none" or n_in <= 1:
+        return n_in
+    return (n_in + 1) // 2
+
+
+@dataclass
+class Draws:
+    """Seed-derived randomness of every compress call, per sequence, in reference call order."""
+
+    dirs: np.ndarray  # float32 [BH, n_calls, d]
+    unif: np.ndarray  # float32 [BH, n_calls, max_in // 2]
+    perms: np.ndarray  # int32 [BH, n_calls, max_in]
+    n_calls: int
+    max_in: int
+
+
+def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str):
+    """Consume the generator exactly as one reference compress call on n_in items does."""
+    if compressor == "none" or n_in <= 1:
+        return METHOD_COPY, None, None, None
+    if compressor == "random" or n_in <= 2:
+        perm = torch.randperm(n_in, generator=g)
+        return METHOD_PERM, None, None, perm.numpy().astype(np.int32)
+    if compressor != "sorted_pair":
+        raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
+    direction = torch.randn(d, generator=g, dtype=torch.float32)
+    direction = direction / torch.clamp(torch.linalg.vector_norm(direction), min=1e-12)
+    u = torch.rand(n_in // 2, generator=g, dtype=torch.float32)
+    return METHOD_SORTED_PAIR, direction.numpy(), u.numpy(), None
+
+
+def _collect_draws(seeds: List[int], call_sizes: List[int], d: int, compressor: str) -> Tuple[Draws, List[int]]:
+    n_calls = len(call_sizes)
+    max_in = max(call_sizes) if call_sizes else 2
+    max_in = max(max_in, 2)
+    bh = len(seeds)
+    dirs = np.zeros((bh, max(n_calls, 1), d), dtype=np.float32)
+    unif = np.zeros((bh, max(n_calls, 1), max_in // 2), dtype=np.float32)
+    perms = np.zeros((bh, max(n_calls, 1), max_in), dtype=np.int32)
+    methods: List[int] = []
+    for h, seed in enumerate(seeds):
+        g = torch.Generator(device="cpu")
+        g.manual_seed(int(seed))
+        for c, n_in in enumerate(call_sizes):
+            method, dvec, u, perm = _draw_one_call(g, n_in, d, compressor)
+            if h == 0:
+                methods.append(method)
+            if dvec is not None:
+                dirs[h, c] = dvec
+                unif[h, c, : u.shape[0]] = u
+            if perm is not None:
+                perms[h, c, : perm.shape[0]] = perm
+    return Draws(dirs, unif, perms, n_calls, max_in), methods
+
+
+# ----------------------------------------------------------------------------- node DAGs
+
+@dataclass
+class NodePlan:
+    mode: int
+    n: int
+    block: int
+    shift: int
+    n_nodes: int
+    cap: int
+    desc: np.ndarray  # int32 [n_nodes, NODE_DESC]
+    meta: np.ndarray  # int32 [n_nodes, NODE_META]: size, lo, hi, materialized
+    batches: List[np.ndarray]  # node ids per compress launch, in dependency order
+    tile_ptr: np.ndarray  # int32 [n_tiles + 1]
+    tile_nodes: np.ndarray  # int32
+    n_tiles: int
+    call_sizes: List[int] = field(default_factory=list)  # n_in of each draw slot (call order)
+    level_of: Optional[np.ndarray] = None  # level of each node (levels mode)
+
+
+def _tile_lists(meta: np.ndarray, n: int, shift: int) -> Tuple[np.ndarray, np.ndarray, int]:
+    n_tiles = -(-(n + shift) // TILE_ROWS)
+    tiles: List[np.ndarray] = []
+    nodes: List[np.ndarray] = []
+    for node in range(meta.shape[0]):
+        size, lo, hi = int(meta[node, 0]), int(meta[node, 1]), int(meta[node, 2])
+        if size <= 0 or lo > hi:
+            continue
+        t0 = (lo + shift) // TILE_ROWS
+        t1 = (hi + shift) // TILE_ROWS
+        tiles.append(np.arange(t0, t1 + 1, dtype=np.int64))
+        nodes.append(np.full(t1 - t0 + 1, node, dtype=np.int64))
+    if tiles:
+        tt = np.concatenate(tiles)
+        nn = np.concatenate(nodes)
+        order = np.lexsort((nn, tt))
+        tt, nn = tt[order], nn[order]
+    else:
+        tt = np.zeros(0, np.int64)
+        nn = np.zeros(0, np.int64)
+    counts = np.bincount(tt, minlength=n_tiles)
+    ptr = np.zeros(n_tiles + 1, dtype=np.int32)
+    ptr[1:] = np.cumsum(counts)
+    return ptr, nn.astype(np.int32), n_tiles
+
+
+def flat_plan(n: int, block: int, compressor: str) -> NodePlan:
+    """Flat block coreset (fast_article_attention.py:364-434): block b (every block with a later
+    query) is compressed once; its reps are active for rows >= (b+1)*B."""
+
+    def build():
+        if compressor == "none":
+            return exact_plan(n)
+        nbf = (n - 1) // block if n > 0 else 0
+        cap = max(1, _compressed_size(block, compressor))
+        desc = np.zeros((max(nbf, 1), NODE_DESC), dtype=np.int32)
+        meta = np.zeros((max(nbf, 1), NODE_META), dtype=np.int32)
+        call_sizes = []
+        for b in range(nbf):
+            m = _compressed_size(block, compressor)
+            desc[b] = [KIND_RAW, b * block, 0, block, m, 0, b, 0]
+            meta[b] = [m, (b + 1) * block, n - 1, 0]
+            call_sizes.append(block)
+        if nbf == 0:
+            meta[0] = [0, 1, 0, 0]
+        ptr, tn, nt = _tile_lists(meta[:nbf], n, 0)
+        batches = [np.arange(nbf, dtype=np.int32)] if nbf else []
+        return NodePlan(MODE_FLAT, n, block, 0, max(nbf, 1), cap, desc, meta, batches, ptr, tn, nt, call_sizes)
+
+    return _cached(("flat", n, block, compressor), build)
+
+
+def exact_plan(n: int) -> NodePlan:
+    def build():
+        desc = np.zeros((1, NODE_DESC), dtype=np.int32)
+        meta = np.array([[0, 1, 0, 0]], dtype=np.int32)
+        ptr, tn, nt = _tile_lists(meta[:0], n, 0)
+        return NodePlan(MODE_EXACT, n, 1, 0, 1, 1, desc, meta, [], ptr, tn, nt, [])
+
+    return _cached(("exact", n), build)
+
+
+def levels_plan(n: int, block: int, compressor: str) -> NodePlan:
+    """Merge-and-reduce level tree computed level-parallel.  node(0, j) = compress(block j);
+    node(l, j) = compress(cat(node(l-1, 2j), node(l-1, 2j+1))).  After c completed blocks level l holds
+    node(l, (c >> l) - 1) iff bit l of c is set, so a node (l, j) with j even is visible to the rows
+    whose counter (i+1)//B lies in [(j+1) 2^l, (j+2) 2^l - 1]; nodes with odd j are merge inputs only."""
+
+    def build():
+        if compressor == "none":
+            return exact_plan(n)
+        nb = n // block
+        counts = []
+        l = 0
+        while (nb >> l) > 0:
+            counts.append(nb >> l)
+            l += 1
+        offs = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64) if counts else np.zeros(1, np.int64)
+        n_nodes = int(offs[-1]) if counts else 0
+        nid = lambda lev, j: int(offs[lev] + j)
+
+        sizes = [0] * n_nodes
+        n_in_of = [0] * n_nodes
+        for lev, cnt in enumerate(counts):
+            for j in range(cnt):
+                i = nid(lev, j)
+                n_in_of[i] = block if lev == 0 else sizes[nid(lev - 1, 2 * j)] + sizes[nid(lev - 1, 2 * j + 1)]
+                sizes[i] = _compressed_size(n_in_of[i], compressor)
+
+        # reference call order: block c completes -> node(0, c-1), then one merge per carry
+        slot = [0] * n_nodes
+        call_sizes: List[int] = []
+        for c in range(1, nb + 1):
+            lev, j = 0, c - 1
+            while True:
+                i = nid(lev, j)
+                slot[i] = len(call_sizes)
+                call_sizes.append(n_in_of[i])
+                if j % 2 == 1:  # the level was occupied: merge into the next level
+                    lev, j = lev + 1, j // 2
+                else:
+                    break
+
+        cap = max([1] + sizes)
+        desc = np.zeros((max(n_nodes, 1), NODE_DESC), dtype=np.int32)
+        meta = np.zeros((max(n_nodes, 1), NODE_META), dtype=np.int32)
+        level_of = np.zeros(max(n_nodes, 1), dtype=np.int32)
+        for lev, cnt in enumerate(counts):
+            for j in range(cnt):
+                i = nid(lev, j)
+                if lev == 0:
+                    desc[i] = [KIND_RAW, j * block, 0, n_in_of[i], sizes[i], 0, slot[i], 0]
+                else:
+                    desc[i] = [KIND_MERGE, nid(lev - 1, 2 * j), nid(lev - 1, 2 * j + 1), n_in_of[i], sizes[i], 0, slot[i], 0]
+                level_of[i] = lev
+                if j % 2 == 0:
+                    lo = (j + 1) * (1 << lev) * block - 1
+                    hi = min((j + 2) * (1 << lev) * block - 2, n - 1)
+                else:
+                    lo, hi = 1, 0
+                meta[i] = [sizes[i], lo, hi, 0]
+        if n_nodes == 0:
+            meta[0] = [0, 1, 0, 0]
+        ptr, tn, nt = _tile_lists(meta[:n_nodes], n, 1)
+        batches = [np.arange(offs[lev], offs[lev] + counts[lev], dtype=np.int32) for lev in range(len(counts))]
+        return NodePlan(MODE_LEVELS, n, block, 1, max(n_nodes, 1), cap, desc, meta, batches, ptr, tn, nt, call_sizes, level_of)
+
+    return _cached(("levels", n, block, compressor), build)
+
+
+def segment_plan(n: int, block: int, stride: int) -> Tuple[NodePlan, int, int]:
+    """Segment-mean reps of completed blocks with a later query (triton_article_attention.py:189-245,
+    active for i >= (rep_block+1)*B with weight = stride, :353-357)."""
+
+    def build():
+        rpb = block // stride
+        nbk = max(0, (n - 1) // block)
+        n_rep = nbk * rpb
+        nn = max(nbk, 1)
+        desc = np.zeros((nn, NODE_DESC), dtype=np.int32)
+        meta = np.zeros((nn, NODE_META), dtype=np.int32)
+        for b in range(nbk):
+            meta[b] = [rpb, (b + 1) * block, n - 1, 1]
+        if nbk == 0:
+            meta[0] = [0, 1, 0, 1]
+        ptr, tn, nt = _tile_lists(meta[:nbk], n, 0)
+        plan = NodePlan(MODE_FLAT, n, block, 0, nn, max(rpb, 1), desc, meta, [], ptr, tn, nt, [])
+        return plan, n_rep, rpb
+
+    return _cached(("segment", n, block, stride), build)
+
+
+def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str) -> Tuple[Draws, np.ndarray]:
+    """Draw table for every sequence plus the node descriptors with their compress method filled in."""
+
+    def build():
+        draws, methods = _collect_draws(list(seeds), plan.call_sizes, d, compressor)
+        desc = plan.desc.copy()
+        if plan.mode in (MODE_FLAT, MODE_LEVELS) and plan.call_sizes:
+            for i in range(desc.shape[0]):
+                if plan.meta[i, 0] == 0 and desc[i, 3] == 0:
+                    continue
+                desc[i, 5] = methods[desc[i, 6]]
+        return draws, desc
+
+    return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor), build)
+
+
+def sequence_seeds(seed: int, bh: int) -> Tuple[int, ...]:
+    """Per-sequence seeds seed + b*H + h (fast_article_attention.py:693,
+    streaming_taylor_coreset_attention.py:743), i.e. seed + flattened (b, h) index."""
+    return tuple(int(seed) + i for i in range(bh))

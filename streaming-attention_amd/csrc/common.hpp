@@ -1,0 +1,76 @@
+// Shared device helpers for the streaming Taylor+coreset attention kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this library:
+//   * q, k, v are contiguous [BH, N, D] / [BH, N, Dv] tensors in fp32, bf16 or fp16; all arithmetic
+//     is fp32 (scores for the block compressor are accumulated in fp64).
+//   * Matrix-core work uses v_mfma_f32_16x16x4_f32 (64-wide wavefront).  Operand layouts, for a lane
+//     l = 16*g + i (i = l % 16, g = l / 16):
+//         A (16x4):  lane holds A[i][g]
+//         B (4x16):  lane holds B[g][i]
+//         D (16x16): lane holds D[4*g + r][i] in element r of the float4 accumulator.
+//     A D-tile produced by one MFMA is re-used as the B operand of the next contraction without any
+//     data movement by visiting the contraction index in the order {4*g + s}, s = 0..3: for K-step s
+//     the B value lane l needs is exactly element s of its own accumulator.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sta {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+enum DType : int { F32 = 0, BF16 = 1, F16 = 2 };
+
+__device__ __forceinline__ float load_elem(const void* base, int64_t idx, int dtype) {
+  if (dtype == F32) return static_cast<const float*>(base)[idx];
+  if (dtype == BF16) {
+    uint32_t bits = static_cast<uint32_t>(static_cast<const uint16_t*>(base)[idx]) << 16;
+    return __uint_as_float(bits);
+  }
+  return static_cast<float>(static_cast<const _Float16*>(base)[idx]);
+}
+
+__device__ __forceinline__ void store_elem(void* base, int64_t idx, int dtype, float x) {
+  if (dtype == F32) {
+    static_cast<float*>(base)[idx] = x;
+  } else if (dtype == BF16) {
+    // round-to-nearest-even, NaN kept quiet
+    uint32_t u = __float_as_uint(x);
+    uint16_t h;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+      h = static_cast<uint16_t>((u >> 16) | 0x40u);
+    } else {
+      u += 0x7fffu + ((u >> 16) & 1u);
+      h = static_cast<uint16_t>(u >> 16);
+    }
+    static_cast<uint16_t*>(base)[idx] = h;
+  } else {
+    static_cast<_Float16*>(base)[idx] = static_cast<_Float16>(x);
+  }
+}
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Taylor truncation sum_{r<=deg} x^r / r!, evaluated term by term (term = term * x / r) so that the
+// fp32 rounding sequence is the one of the reference's exp_taylor.
+__device__ __forceinline__ float taylor_poly(float x, int deg) {
+  float out = 1.0f;
+  float term = 1.0f;
+  for (int r = 1; r <= deg; ++r) {
+    term = __fdiv_rn(__fmul_rn(term, x), static_cast<float>(r));
+    out = __fadd_rn(out, term);
+  }
+  return out;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on XCD w % 8).  This maps
+// the hardware workgroup id to a logical id such that consecutive logical ids share an XCD, so the
+// workgroups that read the same head's rows share one L2.
+__device__ __forceinline__ int xcd_remap(int wg, int total) {
+  if ((total & 7) != 0) return wg;
+  return (wg & 7) * (total >> 3) + (wg >> 3);
+}
+
+}  // namespace sta

@@ -1,0 +1,210 @@
+// K3: block compressor (sorted_pair / random / copy) for the flat block coreset and for the
+// merge-and-reduce level tree.
+//
+// Reference semantics:
+//   flat : _compress_one_completed_block (fast_article_attention.py:312-361)
+//   levels: MergeReduceCoreset._compress / _compress_random / _compress_sorted_pair
+//           (streaming_taylor_coreset_attention.py:413-467), merge input = cat(old, new) (:404-408).
+// A coreset item is represented by the global token index it came from plus its weight, so a merge
+// node only needs its two children's (index, weight) lists; key rows are gathered from k for the
+// projection score.  Random draws (normalised projection direction, pair uniforms, permutations) are
+// inputs: they are a pure function of the seed and are replayed on the host in the reference order.
+//
+// sorted_pair on n items: score_i = <k_i, dir> accumulated in fp64 in index order then rounded to
+// fp32; stable ascending sort of (score, position); pair p = sorted positions (2p, 2p+1); keep the
+// first with probability w_a / max(w_a + w_b, 1e-30) (u_p < prob); the kept item carries w_a + w_b;
+// an odd last item is kept with its own weight.
+#include "common.hpp"
+
+namespace sta {
+
+enum NodeKind : int { KIND_RAW = 0, KIND_MERGE = 1 };
+enum NodeMethod : int { M_COPY = 0, M_SORTED_PAIR = 1, M_PERM = 2 };
+constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, unused
+constexpr int CMP_MAX_IN = 1024;
+constexpr int CMP_THREADS = 256;
+constexpr int CMP_STAGE = 32;  // key rows staged in LDS at a time for the scores
+
+struct CompressArgs {
+  const void* k;
+  int dtype;
+  int64_t n;
+  int d;
+  const int32_t* batch;  // node ids handled by this launch (one workgroup per node and head)
+  const int32_t* desc;   // [n_nodes][NODE_DESC]
+  int n_nodes;
+  int cap;
+  const float* dirs;      // [BH][n_draws][d]
+  const float* unif;      // [BH][n_draws][max_in / 2]
+  const int32_t* perms;   // [BH][n_draws][max_in]
+  int n_draws;
+  int max_in;
+  int32_t* node_src;  // [BH][n_nodes][cap]
+  float* node_w;      // [BH][n_nodes][cap]
+};
+
+__device__ __forceinline__ bool key_greater(float sa, int pa, float sb, int pb) {
+  return sa > sb || (sa == sb && pa > pb);
+}
+
+__global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
+  __shared__ int src_s[CMP_MAX_IN];
+  __shared__ float w_s[CMP_MAX_IN];
+  __shared__ float key_s[CMP_MAX_IN];
+  __shared__ int pos_s[CMP_MAX_IN];
+  __shared__ float rows[CMP_STAGE * 129];
+  __shared__ float dir_s[128];
+
+  const int node = a.batch[blockIdx.x];
+  const int64_t bh = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int32_t* dsc = a.desc + static_cast<int64_t>(node) * NODE_DESC;
+  const int kind = dsc[0], ia = dsc[1], ib = dsc[2], n_in = dsc[3], n_out = dsc[4];
+  const int method = dsc[5], slot = dsc[6];
+  // descriptors come from the host plan; refuse anything the LDS arrays cannot hold (uniform exit)
+  if (n_in <= 0 || n_in > CMP_MAX_IN || n_in > a.max_in || n_out > a.cap) return;
+  if (kind == KIND_RAW && (ia < 0 || ia + n_in > a.n)) return;
+
+  // ---- gather the input item list ----
+  if (kind == KIND_RAW) {
+    for (int i = tid; i < n_in; i += CMP_THREADS) {
+      src_s[i] = ia + i;
+      w_s[i] = 1.0f;
+    }
+  } else {
+    const int na = a.desc[static_cast<int64_t>(ia) * NODE_DESC + 4];
+    const int64_t baseA = (bh * a.n_nodes + ia) * a.cap;
+    const int64_t baseB = (bh * a.n_nodes + ib) * a.cap;
+    for (int i = tid; i < n_in; i += CMP_THREADS) {
+      const int64_t p = i < na ? baseA + i : baseB + (i - na);
+      src_s[i] = a.node_src[p];
+      w_s[i] = a.node_w[p];
+    }
+  }
+  __syncthreads();
+
+  const int64_t obase = (bh * a.n_nodes + node) * a.cap;
+  if (method == M_COPY) {
+    for (int i = tid; i < n_in; i += CMP_THREADS) {
+      a.node_src[obase + i] = src_s[i];
+      a.node_w[obase + i] = w_s[i];
+    }
+    return;
+  }
+  if (method == M_PERM) {
+    const int32_t* perm = a.perms + (bh * a.n_draws + slot) * a.max_in;
+    const float factor = static_cast<float>(static_cast<double>(n_in) / static_cast<double>(n_out));
+    for (int i = tid; i < n_out; i += CMP_THREADS) {
+      const int p = perm[i];
+      a.node_src[obase + i] = src_s[p];
+      a.node_w[obase + i] = w_s[p] * factor;
+    }
+    return;
+  }
+
+  // ---- sorted_pair: projection scores (fp64 accumulation, fixed index order) ----
+  const float* dir = a.dirs + (bh * a.n_draws + slot) * a.d;
+  for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = dir[e];
+  const int LD = a.d + 1;
+  for (int base = 0; base < n_in; base += CMP_STAGE) {
+    const int cnt = min(CMP_STAGE, n_in - base);
+    __syncthreads();
+    for (int e = tid; e < cnt * a.d; e += CMP_THREADS) {
+      const int r = e / a.d, col = e - r * a.d;
+      const int64_t tok = src_s[base + r];
+      rows[r * LD + col] = load_elem(a.k, (bh * a.n + tok) * a.d + col, a.dtype);
+    }
+    __syncthreads();
+    if (tid < cnt) {
+      double acc = 0.0;
+      for (int col = 0; col < a.d; ++col)
+        acc = fma(static_cast<double>(rows[tid * LD + col]), static_cast<double>(dir_s[col]), acc);
+      key_s[base + tid] = static_cast<float>(acc);
+      pos_s[base + tid] = base + tid;
+    }
+  }
+  int np = 1;
+  while (np < n_in) np <<= 1;
+  for (int i = n_in + tid; i < np; i += CMP_THREADS) {
+    key_s[i] = __builtin_huge_valf();
+    pos_s[i] = i;
+  }
+  __syncthreads();
+
+  // ---- bitonic sort of (score, position), ascending ----
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (np >> 1); t += CMP_THREADS) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int j = i + stride;
+        const bool up = (i & size) == 0;
+        const float si = key_s[i], sj = key_s[j];
+        const int pi = pos_s[i], pj = pos_s[j];
+        if (key_greater(si, pi, sj, pj) == up) {
+          key_s[i] = sj;
+          key_s[j] = si;
+          pos_s[i] = pj;
+          pos_s[j] = pi;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- pair selection with weight transfer ----
+  const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);
+  const int pc = n_in / 2;
+  for (int p = tid; p < pc; p += CMP_THREADS) {
+    const int ia2 = pos_s[2 * p], ib2 = pos_s[2 * p + 1];
+    const float wa = w_s[ia2], wb = w_s[ib2];
+    const float wsum = wa + wb;
+    const float prob = __fdiv_rn(wa, fmaxf(wsum, 1e-30f));
+    const bool choose_a = u[p] < prob;
+    a.node_src[obase + p] = choose_a ? src_s[ia2] : src_s[ib2];
+    a.node_w[obase + p] = wsum;
+  }
+  if ((n_in & 1) && tid == 0) {
+    const int il = pos_s[n_in - 1];
+    a.node_src[obase + pc] = src_s[il];
+    a.node_w[obase + pc] = w_s[il];
+  }
+}
+
+// Segment-mean representatives (triton_article_attention.py:189-245): completed blocks that have a
+// later query ((n-1)//block of them) are cut into block/stride segments of `stride` consecutive tokens;
+// each representative is the mean key and mean value of its segment.  Output is fp32 [BH][R][d|dv].
+struct SegMeanArgs {
+  const void* k;
+  const void* v;
+  int dtype;
+  int64_t n;
+  int d;
+  int dv;
+  int stride;
+  int64_t n_rep;  // R = ((n-1)//block) * (block/stride)
+  float* rep_k;
+  float* rep_v;
+};
+
+__global__ __launch_bounds__(256) void segment_mean_kernel(const SegMeanArgs a) {
+  const int64_t bh = blockIdx.y;
+  const int width = a.d + a.dv;
+  const int64_t total = a.n_rep * width;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = e / width;
+    const int col = static_cast<int>(e - r * width);
+    const int64_t tok0 = r * a.stride;  // segments tile the usable prefix contiguously
+    float acc = 0.f;
+    if (col < a.d) {
+      for (int s = 0; s < a.stride; ++s) acc += load_elem(a.k, (bh * a.n + tok0 + s) * a.d + col, a.dtype);
+      a.rep_k[(bh * a.n_rep + r) * a.d + col] = acc / static_cast<float>(a.stride);
+    } else {
+      const int cv = col - a.d;
+      for (int s = 0; s < a.stride; ++s) acc += load_elem(a.v, (bh * a.n + tok0 + s) * a.dv + cv, a.dtype);
+      a.rep_v[(bh * a.n_rep + r) * a.dv + cv] = acc / static_cast<float>(a.stride);
+    }
+  }
+}
+
+}  // namespace sta

@@ -1,0 +1,222 @@
+"""Drop-in for the reference's GPU module (triton_article_attention.py) -- same public API, served by
+hand-written HIP kernels for MI355X instead of Triton (there is no Triton in this package).
+
+`triton_article_causal_attention` computes what the reference's fused kernel computes
+(triton_article_attention.py:265-369, :447-577): the exact degree-<=2 Taylor term over the whole causal
+prefix, the exact residual inside the current article block, and deterministic segment-mean
+representatives (weight = compress_stride) for completed blocks with a later query, with
+exp(min(x, 80)).  The Taylor term comes from the exact moment scan rather than an O(N^2) sweep.
+Accumulation is fp32 (the reference uses tf32 dots); the output dtype is `output_dtype`.
+"""
+
+from __future__ import annotations
+
+import argparse
+import math
+import statistics
+from dataclasses import dataclass
+from typing import List, Optional, Sequence, Tuple, Union
+
+import torch
+
+import _engine
+import _native
+from fast_article_attention import safe_relative_l2  # noqa: F401  (re-exported like the reference)
+
+Tensor = torch.Tensor
+
+__all__ = ["TritonArticleStats", "build_segment_mean_coreset", "torch_classical_causal_attention",
+           "triton_article_causal_attention", "exp_taylor", "safe_relative_l2"]
+
+
+def _require_backend() -> None:
+    """The reference raises ImportError without Triton (triton_article_attention.py:72-77); here the
+    backend is the HIP library."""
+    _native.lib()
+
+
+def _require_device(*tensors: Tensor) -> None:
+    for x in tensors:
+        if not x.is_cuda:
+            raise ValueError("HIP kernels require GPU (cuda/ROCm) tensors")
+
+
+def _ceil_div(a: int, b: int) -> int:
+    return (int(a) + int(b) - 1) // int(b)
+
+
+def _attention_scale(scale: Optional[float], dim: int) -> float:
+    return float(1.0 / math.sqrt(dim) if scale is None else scale)
+
+
+def _human_bytes(num_bytes: int) -> str:
+    x = float(num_bytes)
+    for unit in ("B", "KiB", "MiB", "GiB", "TiB"):
+        if abs(x) < 1024.0 or unit == "TiB":
+            return f"{x:.2f} {unit}"
+        x /= 1024.0
+    return f"{x:.2f} TiB"
+
+
+def exp_taylor(x: Tensor, degree: int) -> Tensor:
+    total = torch.ones_like(x)
+    term = torch.ones_like(x)
+    for r in range(1, degree + 1):
+        term = term * x / float(r)
+        total = total + term
+    return total
+
+
+def torch_classical_causal_attention(q: Tensor, k: Tensor, v: Tensor, *, scale: Optional[float] = None) -> Tensor:
+    """Exact torch reference for [N,D] or [B,H,N,D] (triton_article_attention.py:123-143); the
+    batched product uses a contiguous right operand."""
+    if q.shape != k.shape:
+        raise ValueError("q and k must have identical shape")
+    if q.ndim == 2:
+        n, dim = q.shape
+        logits = (q @ k.T.contiguous()) * _attention_scale(scale, dim)
+        mask = torch.ones(n, n, device=q.device, dtype=torch.bool).tril()
+        return torch.softmax(logits.masked_fill(~mask, float("-inf")), dim=-1) @ v
+    if q.ndim == 4:
+        b, h, n, dim = q.shape
+        if v.shape[:3] != q.shape[:3]:
+            raise ValueError("v must have shape [B,H,N,Dv]")
+        logits = torch.matmul(q, k.transpose(-1, -2).contiguous()) * _attention_scale(scale, dim)
+        mask = torch.ones(n, n, device=q.device, dtype=torch.bool).tril()
+        return torch.matmul(torch.softmax(logits.masked_fill(~mask[None, None], float("-inf")), dim=-1), v)
+    raise ValueError("q/k/v must be [N,D] or [B,H,N,D]")
+
+
+def _flatten_bh_qkv(q: Tensor, k: Tensor, v: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tuple[int, ...], bool]:
+    """Contiguous [BH,N,D], [BH,N,D], [BH,N,Dv] (triton_article_attention.py:146-162)."""
+    if q.shape != k.shape:
+        raise ValueError(f"q and k must match, got {tuple(q.shape)} and {tuple(k.shape)}")
+    if q.ndim == 2:
+        if v.ndim != 2 or v.shape[0] != q.shape[0]:
+            raise ValueError("for [N,D] q/k, v must be [N,Dv]")
+        return q[None].contiguous(), k[None].contiguous(), v[None].contiguous(), tuple(q.shape), False
+    if q.ndim == 4:
+        if v.ndim != 4 or v.shape[:3] != q.shape[:3]:
+            raise ValueError("for [B,H,N,D] q/k, v must be [B,H,N,Dv]")
+        b, h, n, d = q.shape
+        return (q.contiguous().view(b * h, n, d), k.contiguous().view(b * h, n, d),
+                v.contiguous().view(b * h, n, v.shape[-1]), tuple(q.shape), True)
+    raise ValueError("q/k/v must be [N,D] or [B,H,N,D]")
+
+
+def _unflatten_output(out3: Tensor, original_q_shape: Tuple[int, ...], had_bh: bool) -> Tensor:
+    if not had_bh:
+        return out3[0]
+    b, h, n, _ = original_q_shape
+    return out3.view(b, h, n, out3.shape[-1])
+
+
+@dataclass(frozen=True)
+class TritonArticleStats:
+    """triton_article_attention.py:172-181"""
+
+    degree: int
+    block_size: int
+    compress_stride: int
+    coreset_items_per_sequence: int
+    coreset_bytes_per_sequence: int
+    kv_bytes_per_sequence: int
+    score_matrix_bytes_per_sequence: int
+    output_bytes_per_sequence: int
+
+
+@torch.no_grad()
+def build_segment_mean_coreset(k_bhn: Tensor, v_bhn: Tensor, *, block_size: int,
+                               compress_stride: int) -> Tuple[Tensor, Tensor, int]:
+    """Segment-mean reps [BH,R,D], [BH,R,Dv] of completed blocks with a later query
+    (triton_article_attention.py:189-245), computed by the HIP segment-mean kernel.  CPU inputs are
+    processed on the first ROCm device and returned on the CPU."""
+    if k_bhn.ndim != 3 or v_bhn.ndim != 3:
+        raise ValueError("k_bhn and v_bhn must be [BH,N,D] and [BH,N,Dv]")
+    if k_bhn.shape[:2] != v_bhn.shape[:2]:
+        raise ValueError("k_bhn and v_bhn must have the same [BH,N]")
+    if block_size <= 0 or compress_stride <= 0:
+        raise ValueError("block_size and compress_stride must be positive")
+    if block_size % compress_stride != 0:
+        raise ValueError("for the Triton kernel, block_size must be divisible by compress_stride")
+    bh, n, dim = k_bhn.shape
+    dv = v_bhn.shape[-1]
+    rpb = block_size // compress_stride
+    nb = max(0, (n - 1) // block_size)
+    n_rep = nb * rpb
+    home = k_bhn.device
+    if n_rep == 0:
+        return (torch.empty(bh, 0, dim, device=home, dtype=k_bhn.dtype),
+                torch.empty(bh, 0, dv, device=home, dtype=v_bhn.dtype), rpb)
+    if home.type == "cuda":
+        kg, vg = k_bhn.contiguous(), v_bhn.contiguous()
+    else:
+        if not torch.cuda.is_available():
+            raise RuntimeError("streaming-attention HIP kernels need a ROCm GPU; none is visible")
+        kg, vg = k_bhn.cuda().contiguous(), v_bhn.cuda().contiguous()
+    if kg.dtype not in _native.DTYPE_CODES or vg.dtype != kg.dtype:
+        kg, vg = kg.float(), vg.float()
+    rep_k = torch.empty(bh, n_rep, dim, device=kg.device, dtype=torch.float32)
+    rep_v = torch.empty(bh, n_rep, dv, device=kg.device, dtype=torch.float32)
+    st = _native.lib().sta_segment_mean(kg.data_ptr(), vg.data_ptr(), _native.DTYPE_CODES[kg.dtype], bh, n, dim, dv,
+                                        block_size, compress_stride, n_rep, rep_k.data_ptr(), rep_v.data_ptr(),
+                                        _native.stream_handle(kg.device))
+    _native.check(st, "sta_segment_mean")
+    return rep_k.to(device=home, dtype=k_bhn.dtype), rep_v.to(device=home, dtype=v_bhn.dtype), rpb
+
+
+@torch.no_grad()
+def triton_article_causal_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    degree: int = 2,
+    block_size: int = 128,
+    compress_stride: int = 2,
+    scale: Optional[float] = None,
+    block_m: int = 16,
+    block_n: int = 64,
+    block_r: int = 64,
+    value_block: Optional[int] = None,
+    denominator_eps: float = 1.0e-12,
+    output_dtype: Optional[torch.dtype] = torch.float32,
+    return_stats: bool = False,
+) -> Union[Tensor, Tuple[Tensor, TritonArticleStats]]:
+    """Same arguments, checks and result as triton_article_attention.py:447-577.  block_m, block_n,
+    block_r and value_block are tile hints of the Triton kernel; the HIP kernels use their own fixed
+    CDNA4 tiling, so they are accepted and ignored."""
+    _require_backend()
+    _require_device(q, k, v)
+    if degree not in (0, 1, 2):
+        raise NotImplementedError("Triton article kernel currently supports degree 0, 1, or 2")
+    if block_size <= 0 or compress_stride <= 0:
+        raise ValueError("block_size and compress_stride must be positive")
+    if block_size % compress_stride != 0:
+        raise ValueError("block_size must be divisible by compress_stride")
+    q3, k3, v3, original_shape, had_bh = _flatten_bh_qkv(q, k, v)
+    bh, n, dim = q3.shape
+    dv = v3.shape[-1]
+    if dim > 128:
+        raise ValueError("this compact kernel supports D <= 128; increase BLOCK_D logic for larger heads")
+    if dv > 256:
+        raise ValueError("this compact kernel supports Dv <= 256")
+    if q3.dtype not in _native.DTYPE_CODES:
+        q3, k3 = q3.float(), k3.float()
+    if v3.dtype not in _native.DTYPE_CODES:
+        v3 = v3.float()
+    if not (q3.dtype == k3.dtype == v3.dtype):
+        q3, k3, v3 = q3.float(), k3.float(), v3.float()
+    out_dtype = output_dtype or torch.float32
+    res = _engine.prefill(q3, k3, v3, degree=degree, block=block_size, scale=_attention_scale(scale, dim),
+                          semantics="segment", stride=compress_stride, exp_clamp=True, eps=denominator_eps,
+                          out_dtype=out_dtype)
+    out = _unflatten_output(res.out, original_shape, had_bh)
+    if not return_stats:
+        return out
+    r = max(0, (n - 1) // block_size) * (block_size // compress_stride)
+    ekv = q3.element_size()
+    eo = res.out.element_size()
+    stats = TritonArticleStats(degree, block_size, compress_stride, int(r), int(r * (dim + dv) * ekv),
+                               int(n * (dim + dv) * ekv), int(n * n * ekv), int(n * dv * eo))
+    return out, stats

@@ -1,0 +1,311 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle and the reference's golden
+vectors.  Tolerances: fp32 inputs rel-L2 <= 1e-4, bf16 inputs <= 5e-3 (against the fp32 oracle on the
+upcast inputs); coreset selections (kept token index and weight of every node) bit-exact."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import _engine
+import _native
+import _plan
+import fast_article_attention as faa
+import reference_cpu as orc
+import streaming_taylor_coreset_attention as stc
+import triton_article_attention as taa
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+FP32_TOL = 1e-4
+BF16_TOL = 5e-3
+
+
+def rel(a, b):
+    return orc.rel_l2(torch.as_tensor(a).cpu(), torch.as_tensor(b).cpu())
+
+
+def t(x):
+    return torch.from_numpy(np.ascontiguousarray(x))
+
+
+# --------------------------------------------------------------------------- matrix-core layout
+
+def test_mfma_operand_layout():
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(64, generator=g)
+    b = torch.randn(64, generator=g)
+    out = torch.empty(256, device=DEV)
+    st = _native.lib().sta_selftest_mfma(a.to(DEV).data_ptr(), b.to(DEV).data_ptr(), out.data_ptr())
+    _native.check(st, "sta_selftest_mfma")
+    A = torch.empty(16, 4)
+    B = torch.empty(4, 16)
+    for lane in range(64):
+        i, gq = lane % 16, lane // 16
+        A[i, gq] = a[lane]
+        B[gq, i] = b[lane]
+    expect = (A.double() @ B.double()).float()
+    assert torch.allclose(out.cpu().reshape(16, 16), expect, rtol=1e-5, atol=1e-5)
+
+
+# --------------------------------------------------------------------------- moments (K1 + closed form)
+
+@pytest.mark.parametrize("degree,d,dv,n", [(0, 8, 5, 77), (1, 16, 16, 200), (2, 32, 32, 1024), (2, 12, 5, 300),
+                                           (2, 64, 64, 700), (2, 128, 40, 257), (3, 16, 64, 333), (3, 6, 5, 64)])
+def test_low_degree_sums(degree, d, dv, n):
+    g = torch.Generator().manual_seed(degree * 100 + d)
+    q = torch.randn(n, d, generator=g) * 0.3
+    k = torch.randn(n, d, generator=g) * 0.3
+    v = torch.randn(n, dv, generator=g)
+    res = _engine.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=degree, block=1, scale=0.9,
+                          semantics="taylor")
+    num, den = orc.low_sums_direct(q, k, v, degree, 0.9)
+    assert rel(res.out[0], num) < 2e-6
+    assert rel(res.den[0], den) < 2e-6
+
+
+def test_low_degree_api_matches_reference(golden):
+    g = golden("flat_c1")
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    for mode in ("auto", "stream", "prefix"):
+        num, den, f = faa.low_degree_taylor_causal_sums(q, k, v, degree=2, scale=1.0, mode=mode)
+        assert f == 561
+        assert rel(num, g["low_num"]) < 1e-5 and rel(den, g["low_den"]) < 1e-5
+
+
+# --------------------------------------------------------------------------- compressor (K3)
+
+def _nodes(res):
+    return res.node_src.cpu().numpy(), res.node_w.cpu().numpy()
+
+
+@pytest.mark.parametrize("name,prefix", [("flat_c1", "sorted_pair_"), ("flat_c1", "random_"), ("flat_oddblock", "")])
+def test_flat_selection_bit_exact(golden, name, prefix):
+    g = golden(name)
+    comp = "random" if prefix == "random_" else "sorted_pair"
+    block = int(g.meta["block"])
+    seed = int(g.meta["seed"])
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    res = _engine.prefill(q[None], k[None], v[None], degree=2, block=block, scale=1.0, semantics="flat",
+                          compressor=comp, seed=seed)
+    src, w = _nodes(res)
+    sizes = res.plan.meta[:, 0]
+    idx = np.concatenate([src[0, b, : sizes[b]] for b in range(len(res.plan.batches[0]))])
+    ws = np.concatenate([w[0, b, : sizes[b]] for b in range(len(res.plan.batches[0]))])
+    assert np.array_equal(idx, g[f"{prefix}rep_idx"])
+    assert np.array_equal(ws, g[f"{prefix}rep_w"])
+
+
+LEVEL_CASES = ["levels_c1", "levels_random", "levels_deg3", "levels_oddblock", "levels_block2"]
+
+
+@pytest.mark.parametrize("name", LEVEL_CASES)
+def test_level_nodes_bit_exact(golden, name):
+    """Every node of the level tree (kept token and weight, in order) equals the reference's
+    compress call with the same position in its call sequence."""
+    g = golden(name)
+    m = g.meta
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    res = _engine.prefill(q[None], k[None], v[None], degree=m["degree"], block=m["block"],
+                          scale=1.0 if m["scale"] is None else m["scale"], semantics="levels",
+                          compressor=m["compressor"], seed=m["seed"])
+    src, w = _nodes(res)
+    plan = res.plan
+    n_calls = int(g["ncalls"])
+    assert len(plan.call_sizes) == n_calls
+    for node in range(plan.n_nodes):
+        slot = int(plan.desc[node, 6])
+        size = int(plan.meta[node, 0])
+        assert np.array_equal(src[0, node, :size], g[f"call{slot}_src_out"]), f"node {node} (call {slot})"
+        assert np.array_equal(w[0, node, :size], g[f"call{slot}_w_out"])
+
+
+# --------------------------------------------------------------------------- full forward vs reference
+
+def test_fast_none_reconstructs_classical(golden):
+    g = golden("flat_c1")
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    out = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=128, scale=1.0, compressor="none")
+    assert rel(out, g["exact"]) < FP32_TOL
+    assert rel(out, g["out_none"]) < FP32_TOL
+
+
+def test_reference_test_exact_residual_small():
+    # test_fast_article_attention.py:10-29 on the GPU
+    torch.manual_seed(0)
+    q = torch.randn(64, 8) * 0.1
+    k = torch.randn(64, 8) * 0.1
+    v = torch.randn(64, 7)
+    out = faa.fast_article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=16, scale=1.0,
+                                            compressor="none", low_mode="stream")
+    exact = orc.classical_attention(q, k, v, 1.0)
+    assert rel(out, exact) < 2e-6
+    assert (out.cpu().double() - exact).abs().max().item() < 3e-6
+
+
+@pytest.mark.parametrize("comp", ["sorted_pair", "random"])
+def test_fast_coreset_matches_reference(golden, comp):
+    g = golden("flat_c1")
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    out, stats = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=128, scale=1.0, compressor=comp,
+                                                   seed=0, return_stats=True)
+    assert out.dtype == torch.float32 and out.shape == (1024, 32)
+    assert rel(out, g[f"{comp}_out"]) < FP32_TOL
+    assert stats.feature_count == 561 and stats.coreset_items == 448
+
+
+def test_fast_oddblock(golden):
+    g = golden("flat_oddblock")
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    out = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=33, scale=1.0, seed=9)
+    assert rel(out, g["out"]) < FP32_TOL
+
+
+def test_fast_bh_seeds_and_stats(golden):
+    g = golden("flat_bh")
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    out, st = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=32, scale=None, seed=7,
+                                                return_stats=True)
+    assert rel(out, g["out"]) < FP32_TOL
+    ref_stats = g["stats"].tolist()
+    ours = [st.degree, st.block_size, st.feature_count, st.coreset_items, st.approx_streaming_state_bytes,
+            st.scratch_low_prefix_bytes, st.scratch_residual_matrix_bytes]
+    # the low-prefix scratch estimate depends on the tensors' device type (prefix on GPU, stream on CPU)
+    assert ours[:5] == ref_stats[:5] and ours[6] == ref_stats[6]
+
+
+@pytest.mark.parametrize("name", LEVEL_CASES)
+def test_levels_match_reference(golden, name):
+    g = golden(name)
+    m = g.meta
+    q, k, v = (t(g[x]).to(DEV) for x in "qkv")
+    out = stc.article_causal_attention(q, k, v, degree=m["degree"], block_size=m["block"], scale=m["scale"],
+                                       compressor=m["compressor"], seed=m["seed"])
+    assert rel(out, g["out"]) < FP32_TOL
+
+
+def test_levels_without_compression_is_exact():
+    torch.manual_seed(0)
+    q = torch.randn(24, 6)
+    k = torch.randn(24, 6)
+    v = torch.randn(24, 5)
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = k / k.norm(dim=-1, keepdim=True)
+    out = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=3, block_size=25, scale=1.0)
+    assert torch.allclose(out.cpu().double(), orc.classical_attention(q, k, v, 1.0), atol=3e-6, rtol=3e-6)
+
+
+# --------------------------------------------------------------------------- against the oracle, more shapes
+
+@pytest.mark.parametrize("n,d,dv,block,comp,scale", [
+    (1, 8, 4, 16, "sorted_pair", 1.0), (17, 8, 4, 16, "sorted_pair", 1.0), (130, 16, 16, 128, "sorted_pair", 1.0),
+    (513, 64, 64, 256, "sorted_pair", 0.125), (600, 12, 5, 16, "random", 1.0), (300, 32, 100, 2, "sorted_pair", 1.0),
+    (257, 128, 256, 64, "sorted_pair", None), (400, 20, 9, 50, "sorted_pair", 0.5),
+])
+def test_flat_vs_oracle(n, d, dv, block, comp, scale):
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=n)
+    out = faa.fast_article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=block,
+                                            scale=scale, compressor=comp, seed=3)
+    ref = orc.fast_path_forward(q, k, v, degree=2, block=block, scale=scale, compressor=comp, seed=3)
+    assert rel(out, ref) < FP32_TOL
+
+
+@pytest.mark.parametrize("n,d,dv,block,degree,comp,radius", [
+    (1000, 32, 32, 128, 2, "sorted_pair", 1.0), (513, 16, 64, 128, 3, "sorted_pair", 1.5),
+    (700, 64, 64, 256, 2, "sorted_pair", 1.0), (255, 8, 8, 16, 1, "sorted_pair", 1.0), (100, 8, 8, 16, 0, "random", 1.0),
+    (129, 8, 3, 64, 2, "none", 1.0),
+])
+def test_levels_vs_oracle(n, d, dv, block, degree, comp, radius):
+    q, k, v = orc.make_data((), n, d, dv, radius=radius, data="unit_ball", seed=n + 1)
+    out = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=degree, block_size=block, scale=1.0,
+                                       compressor=comp, seed=5)
+    ref = orc.levels_forward(q, k, v, degree=degree, block=block, scale=1.0, compressor=comp, seed=5)
+    assert rel(out, ref) < FP32_TOL
+
+
+def test_bf16_inputs_flat_and_levels():
+    """config c2's regime (q, k, v ~ N(0,1), scale 1/8, bf16 inputs, fp32 accumulation), reduced size."""
+    g = torch.Generator().manual_seed(21)
+    bsz, heads, n, d = 2, 2, 640, 64
+    q = torch.randn(bsz, heads, n, d, generator=g).bfloat16()
+    k = torch.randn(bsz, heads, n, d, generator=g).bfloat16()
+    v = torch.randn(bsz, heads, n, d, generator=g).bfloat16()
+    out = faa.fast_article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=256,
+                                            scale=0.125, seed=0)
+    assert out.dtype == torch.bfloat16
+    for b in range(bsz):
+        for h in range(heads):
+            ref = orc.fast_path_forward(q[b, h].float(), k[b, h].float(), v[b, h].float(), degree=2, block=256,
+                                        scale=0.125, seed=b * heads + h)
+            assert rel(out[b, h].float(), ref) < BF16_TOL
+    out_l = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=128, scale=0.125)
+    ref_l = orc.levels_forward(q[1, 1].float(), k[1, 1].float(), v[1, 1].float(), degree=2, block=128, scale=0.125,
+                               seed=3)
+    assert rel(out_l[1, 1].float(), ref_l) < BF16_TOL
+
+
+# --------------------------------------------------------------------------- Triton-API path
+
+def test_segment_mean_matches_reference(golden):
+    g = golden("segment_mean")
+    rk, rv, rpb = taa.build_segment_mean_coreset(t(g["k"]).to(DEV), t(g["v"]).to(DEV), block_size=8,
+                                                 compress_stride=2)
+    assert rpb == 4 and rk.shape == (2, 8, 4) and rv.shape == (2, 8, 5)
+    assert torch.allclose(rk.cpu(), t(g["rep_k"]), atol=1e-6)
+    assert torch.allclose(rv.cpu(), t(g["rep_v"]), atol=1e-6)
+
+
+@pytest.mark.parametrize("stride,dtype", [(1, torch.float32), (2, torch.float32), (4, torch.float16), (2, torch.bfloat16)])
+def test_triton_article_vs_oracle(stride, dtype):
+    g = torch.Generator().manual_seed(stride)
+    q = (torch.randn(2, 3, 300, 32, generator=g) / 32 ** 0.5).to(dtype)
+    k = (torch.randn(2, 3, 300, 32, generator=g) / 32 ** 0.5).to(dtype)
+    v = torch.randn(2, 3, 300, 24, generator=g).to(dtype)
+    out, st = taa.triton_article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=64,
+                                                  compress_stride=stride, scale=1.0, return_stats=True)
+    assert out.dtype == torch.float32
+    ref = orc.segment_forward(q.float().reshape(6, 300, 32), k.float().reshape(6, 300, 32),
+                              v.float().reshape(6, 300, 24), degree=2, block=64, stride=stride, scale=1.0)
+    assert rel(out.reshape(6, 300, 24), ref) < (FP32_TOL if dtype == torch.float32 else 1e-5 + FP32_TOL)
+    assert st.coreset_items_per_sequence == 4 * (64 // stride)
+    if stride == 1 and dtype == torch.float32:
+        assert rel(out.reshape(6, 300, 24), orc.classical_attention(q.reshape(6, 300, 32), k.reshape(6, 300, 32),
+                                                                    v.reshape(6, 300, 24), 1.0)) < FP32_TOL
+
+
+def test_triton_reference_numerics_test():
+    # test_triton_article_attention.py:42-65 (fp16, stride 1 == exact)
+    torch.manual_seed(0)
+    n, d, dv = 64, 16, 16
+    q = (torch.randn(n, d) / d ** 0.5).half()
+    k = (torch.randn(n, d) / d ** 0.5).half()
+    v = torch.randn(n, dv).half()
+    exact = orc.classical_attention(q.float(), k.float(), v.float(), 1.0)
+    art = taa.triton_article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=16,
+                                              compress_stride=1, scale=1.0, output_dtype=torch.float32)
+    assert rel(art, exact) < 2e-2
+    assert rel(art, exact) < 1e-3  # far inside the reference's bound
+
+
+def test_triton_cpu_guard():
+    with pytest.raises((ImportError, ValueError)):
+        taa.triton_article_causal_attention(torch.randn(8, 4), torch.randn(8, 4), torch.randn(8, 4))
+
+
+# --------------------------------------------------------------------------- properties
+
+def test_deterministic_reruns():
+    q, k, v = orc.make_data((2, 2), 1500, 64, 64, radius=1.0, data="unit_ball", seed=4)
+    args = dict(degree=2, block_size=256, scale=0.125, seed=1)
+    a = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), **args)
+    b = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), **args)
+    assert torch.equal(a, b)
+
+
+def test_cpu_inputs_round_trip():
+    q, k, v = orc.make_data((), 300, 16, 8, radius=1.0, data="unit_ball", seed=8)
+    out = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=64, scale=1.0)
+    assert out.device.type == "cpu"
+    assert rel(out, orc.fast_path_forward(q, k, v, degree=2, block=64, scale=1.0)) < FP32_TOL

@@ -1,0 +1,183 @@
+"""Host-side checks of the product that need no GPU: the C-ABI library loads and exports every symbol
+the header declares; the seed-derived draws the product replays equal the reference's; level-tree
+plans follow the reference's cascade; the Python API raises the reference's exceptions."""
+
+import pathlib
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import _native
+import _plan
+import fast_article_attention as faa
+import streaming_taylor_coreset_attention as stc
+import triton_article_attention as taa
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "streamattn.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(sta_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_header_symbols():
+    lib = _native.load_library()
+    syms = header_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(_native.EXPORTED_SYMBOLS)
+    assert lib.sta_version() >= 100
+    assert lib.sta_tile_rows() == _plan.TILE_ROWS
+    for d in (8, 64, 65, 128):
+        assert lib.sta_moment_chunk(d) == _plan.moment_chunk(d)
+    assert lib.sta_status_string(0) == b"ok"
+    lim = _native.limits()
+    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 3, "max_compress_in": 1024}
+
+
+def test_library_rejects_bad_arguments_without_touching_a_device():
+    lib = _native.load_library()
+    # null pointers / bad sizes are refused before any launch
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 1, 1, 2, 1.0, 64, 0, 1, 16, None, None, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
+
+
+def _norm(raw):
+    d = torch.from_numpy(raw)
+    return (d / torch.clamp(torch.linalg.vector_norm(d), min=1e-12)).numpy()
+
+
+@pytest.mark.parametrize("comp", ["sorted_pair", "random"])
+def test_flat_draw_replay_matches_reference(golden, comp):
+    g = golden("flat_c1")
+    plan = _plan.flat_plan(1024, 128, comp)
+    draws, desc = _plan.draws_for(plan, (0,), 32, comp)
+    assert draws.n_calls == int(g[f"{comp}_ncalls"]) == 7
+    for c in range(7):
+        if comp == "sorted_pair":
+            assert np.array_equal(draws.dirs[0, c], _norm(g[f"{comp}_call{c}_direction_raw"]))
+            assert np.array_equal(draws.unif[0, c, :64], g[f"{comp}_call{c}_uniforms"])
+            assert desc[c, 5] == _plan.METHOD_SORTED_PAIR
+        else:
+            assert np.array_equal(draws.perms[0, c, :128], g[f"{comp}_call{c}_perm"])
+            assert desc[c, 5] == _plan.METHOD_PERM
+
+
+@pytest.mark.parametrize("name", ["levels_c1", "levels_random", "levels_deg3", "levels_oddblock", "levels_block2"])
+def test_level_draw_replay_and_cascade_match_reference(golden, name):
+    g = golden(name)
+    m = g.meta
+    plan = _plan.levels_plan(m["n"], m["block"], m["compressor"])
+    draws, desc = _plan.draws_for(plan, (m["seed"],), m["d"], m["compressor"])
+    n_calls = int(g["ncalls"])
+    assert plan.call_sizes == [int(g[f"call{c}_src_in"].shape[0]) for c in range(n_calls)]
+    for c in range(n_calls):
+        if f"call{c}_direction_raw" in g:
+            assert np.array_equal(draws.dirs[0, c], _norm(g[f"call{c}_direction_raw"]))
+            assert np.array_equal(draws.unif[0, c, : g[f"call{c}_uniforms"].shape[0]], g[f"call{c}_uniforms"])
+        if f"call{c}_perm" in g:
+            assert np.array_equal(draws.perms[0, c, : g[f"call{c}_perm"].shape[0]], g[f"call{c}_perm"])
+    # merge inputs are cat(old, new) of the two children, in that order
+    slot_of = {int(plan.desc[i, 6]): i for i in range(plan.n_nodes)}
+    for c in range(n_calls):
+        node = slot_of[c]
+        kind, a, b, n_in = (int(x) for x in plan.desc[node, :4])
+        if kind == _plan.KIND_RAW:
+            assert np.array_equal(g[f"call{c}_src_in"], np.arange(a, a + n_in))
+        else:
+            ca, cb = int(plan.desc[a, 6]), int(plan.desc[b, 6])
+            assert np.array_equal(g[f"call{c}_src_in"], np.concatenate([g[f"call{ca}_src_out"], g[f"call{cb}_src_out"]]))
+
+
+def test_level_plan_intervals_follow_binary_counter():
+    n, B = 5000, 64
+    plan = _plan.levels_plan(n, B, "sorted_pair")
+    # for every row, the visible nodes are exactly those of the counter (i+1)//B
+    for i in range(0, n, 37):
+        c = (i + 1) // B
+        vis = {int(x) for x in np.nonzero((plan.meta[:, 1] <= i) & (plan.meta[:, 2] >= i) & (plan.meta[:, 0] > 0))[0]}
+        expect = set()
+        for lev in range(c.bit_length()):
+            if (c >> lev) & 1:
+                j = (c >> lev) - 1
+                expect.add(int(np.nonzero((plan.level_of == lev))[0][0]) + j)
+        assert vis == expect, i
+        t = (i + plan.shift) // _plan.TILE_ROWS
+        assert vis <= set(plan.tile_nodes[plan.tile_ptr[t]:plan.tile_ptr[t + 1]].tolist())
+
+
+def test_feature_plan_layout():
+    fp = _plan.feature_plan(5, 3, 2)
+    assert fp.count == 1 + 5 + 15 + 35
+    assert fp.per_split % 16 == 0 and fp.per_split * 2 >= fp.count
+    i0 = fp.idx & 255
+    i1 = (fp.idx >> 8) & 255
+    i2 = (fp.idx >> 16) & 255
+    assert (i0[0], i1[0], i2[0]) == (5, 5, 5) and fp.coef[0] == 1.0  # constant feature
+    assert (i0[1], i1[1], i2[1]) == (0, 5, 5)  # x_0
+    assert (i0[6], i1[6], i2[6]) == (0, 0, 5) and fp.coef[6] == 0.5  # x_0^2 / 2
+    assert (i0[21], i1[21], i2[21]) == (0, 0, 0) and fp.coef[21] == np.float32(1 / 6)
+    assert np.all(fp.coef[fp.count:] == 0)
+
+
+# --------------------------------------------------------------------------- reference error behaviour
+
+def _qkv(n=10, d=4, dv=3):
+    return torch.randn(n, d), torch.randn(n, d), torch.randn(n, dv)
+
+
+def test_fast_path_argument_errors():
+    q, k, v = _qkv()
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q[None], k, v)
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q, k[:, :3], v)
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q, k, v[:5])
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q, k, v, query_chunk_size=0)
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q, k, v, block_size=0)
+    with pytest.raises(NotImplementedError):
+        faa.fast_article_causal_attention(q, k, v, degree=3)
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q, k, v, low_mode="bogus")
+    with pytest.raises(ValueError):
+        faa.fast_article_causal_attention(q[None, None], k[None, None], v[None, None, :5])
+    with pytest.raises(ValueError):
+        faa.low_degree_taylor_causal_sums(q, k, v, mode="bogus")
+    with pytest.raises(NotImplementedError):
+        faa.num_taylor_features(4, 3)
+    with pytest.raises(ValueError):
+        faa.exp_taylor(torch.zeros(2), -1)
+
+
+def test_streaming_argument_errors():
+    q, k, v = _qkv()
+    with pytest.raises(ValueError):
+        stc.article_causal_attention(q, k, v, block_size=1)
+    with pytest.raises(ValueError):
+        stc.article_causal_attention(q, k, v, degree=4, max_monomials=10)
+    with pytest.raises(ValueError):
+        stc.article_causal_attention(q, k, v, block_size=4, compressor="bogus")
+
+
+def test_triton_api_argument_errors():
+    q, k, v = _qkv()
+    with pytest.raises((ImportError, ValueError)):
+        taa.triton_article_causal_attention(q, k, v)  # CPU tensors (test_triton_article_attention.py:17-26)
+    with pytest.raises(ValueError):
+        taa.build_segment_mean_coreset(k[None], v[None], block_size=8, compress_stride=3)
+
+
+def test_stats_formulas_match_reference(golden):
+    g = golden("flat_bh")
+    ref = g["stats"].tolist()
+    st = faa._stats(200, 16, 8, 4, 2, 32, "sorted_pair", 2048, "stream", "cpu")
+    assert [st.degree, st.block_size, st.feature_count, st.coreset_items, st.approx_streaming_state_bytes,
+            st.scratch_low_prefix_bytes, st.scratch_residual_matrix_bytes] == ref

@@ -1,0 +1,332 @@
+"""Pins the CPU oracle (oracle/reference_cpu.py) before it is trusted as the checker:
+known answers, closed forms, brute force, the reference's golden vectors, and planted mistakes."""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import reference_cpu as orc
+
+TOL_FP32 = dict(rel=2e-6)
+
+
+def rel(a, b):
+    return orc.rel_l2(torch.as_tensor(a), torch.as_tensor(b))
+
+
+# --------------------------------------------------------------------------- primitives
+
+def test_exp_taylor_known_values():
+    # test_streaming_attention.py:24-28
+    y = orc.exp_taylor(torch.tensor([0.0, 1.0, -1.0]), 3)
+    assert torch.allclose(y, torch.tensor([1.0, 8.0 / 3.0, 1.0 / 3.0]))
+
+
+def test_exp_taylor_matches_reference_values(golden):
+    g = golden("features")
+    assert np.array_equal(orc.exp_taylor(torch.from_numpy(g["x"]), 3).numpy(), g["taylor3"])
+
+
+@pytest.mark.parametrize("d,t,expect", [(64, 2, 2145), (32, 2, 561), (16, 3, 969), (8, 0, 1), (5, 1, 6)])
+def test_feature_counts(d, t, expect):
+    assert len(orc.monomials(d, t)) == expect
+    assert expect == sum(math.comb(d + l - 1, l) for l in range(t + 1))
+
+
+def test_feature_order_is_combinations_with_replacement():
+    combos = orc.monomials(6, 3)
+    expected = [()] + [c for l in (1, 2, 3) for c in itertools.combinations_with_replacement(range(6), l)]
+    assert combos == expected
+    # degree-2 block equals torch.triu_indices row-major order (fast_article_attention.py:173)
+    r, c = torch.triu_indices(6, 6)
+    assert [x for x in combos if len(x) == 2] == list(zip(r.tolist(), c.tolist()))
+
+
+def test_features_match_reference_fast_path(golden):
+    g = golden("features")
+    x = torch.from_numpy(g["x"])
+    assert np.array_equal(orc.features(x, 2, True).numpy(), g["key2"])
+    assert np.array_equal(orc.features(x, 2, False).numpy(), g["query2"])
+
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+def test_feature_inner_product_is_truncated_exp(degree):
+    g = torch.Generator().manual_seed(degree)
+    q = torch.randn(9, 5, generator=g, dtype=torch.float64)
+    k = torch.randn(7, 5, generator=g, dtype=torch.float64)
+    lhs = orc.features(q, degree, False) @ orc.features(k, degree, True).T
+    rhs = orc.exp_taylor(q @ k.T, degree)
+    assert torch.allclose(lhs, rhs, rtol=1e-12, atol=1e-12)
+
+
+def test_inv_multinomial_values():
+    assert orc.inv_multinomial(()) == 1.0
+    assert orc.inv_multinomial((2, 2)) == 0.5
+    assert orc.inv_multinomial((1, 1, 1)) == pytest.approx(1 / 6)
+    assert orc.inv_multinomial((0, 0, 3)) == 0.5
+    assert orc.inv_multinomial((0, 1, 2)) == 1.0
+
+
+# --------------------------------------------------------------------------- moments
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+def test_stream_moments_equal_closed_form(degree):
+    g = torch.Generator().manual_seed(10 + degree)
+    q = torch.randn(40, 6, generator=g, dtype=torch.float64) * 0.4
+    k = torch.randn(40, 6, generator=g, dtype=torch.float64) * 0.4
+    v = torch.randn(40, 3, generator=g, dtype=torch.float64)
+    num, den = orc.low_sums_stream(q, k, v, degree, 0.7)
+    num2, den2 = orc.low_sums_direct(q, k, v, degree, 0.7)
+    assert torch.allclose(num, num2, rtol=1e-10, atol=1e-10)
+    assert torch.allclose(den, den2, rtol=1e-10, atol=1e-10)
+
+
+def test_stream_moments_match_reference(golden):
+    g = golden("flat_c1")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    num, den = orc.low_sums_stream(q, k, v, 2, 1.0)
+    assert rel(num, g["low_num"]) < 1e-6
+    assert rel(den, g["low_den"]) < 1e-6
+
+
+def test_make_data_matches_reference(golden):
+    g = golden("flat_c1")
+    q, k, v = orc.make_data((), 1024, 32, 32, radius=1.0, data="unit_ball", seed=0)
+    assert np.array_equal(q.numpy(), g["q"]) and np.array_equal(k.numpy(), g["k"]) and np.array_equal(v.numpy(), g["v"])
+
+
+# --------------------------------------------------------------------------- exact residual
+
+def test_none_compressor_reconstructs_classical():
+    # test_fast_article_attention.py:10-29 with the reference tolerances
+    torch.manual_seed(0)
+    q = torch.randn(64, 8) * 0.1
+    k = torch.randn(64, 8) * 0.1
+    v = torch.randn(64, 7)
+    out = orc.fast_path_forward(q, k, v, degree=2, block=16, scale=1.0, compressor="none")
+    exact = orc.classical_attention(q, k, v, 1.0)
+    assert rel(out, exact) < 2e-6
+    assert (out.double() - exact).abs().max().item() < 3e-6
+
+
+def test_none_compressor_matches_reference_output(golden):
+    g = golden("flat_c1")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    out = orc.fast_path_forward(q, k, v, degree=2, block=128, scale=1.0, compressor="none")
+    assert rel(out, g["out_none"]) < 1e-6
+    assert rel(out, g["exact"]) < 1e-5
+
+
+# --------------------------------------------------------------------------- flat coreset
+
+def _golden_calls(g, prefix, count):
+    return [{k[len(f"{prefix}call{i}_"):]: g[k] for k in g if k.startswith(f"{prefix}call{i}_")} for i in range(count)]
+
+
+def _normalise(raw):
+    d = torch.from_numpy(raw)
+    return (d / torch.clamp(torch.linalg.vector_norm(d), min=1e-12)).numpy()
+
+
+@pytest.mark.parametrize("comp", ["sorted_pair", "random"])
+def test_flat_draws_and_selection_match_reference(golden, comp):
+    g = golden("flat_c1")
+    k = g["k"]
+    ref_calls = _golden_calls(g, f"{comp}_", int(g[f"{comp}_ncalls"]))
+    calls = orc.flat_coreset(k, 128, comp, 0, score_fn=orc.torch_scores)
+    assert len(calls) == len(ref_calls) == 7
+    for c, rc in zip(calls, ref_calls):
+        if comp == "sorted_pair":
+            assert np.array_equal(c.direction, _normalise(rc["direction_raw"]))
+            assert np.array_equal(c.uniforms, rc["uniforms"])
+            assert np.array_equal(orc.torch_scores(k[c.src_in], c.direction), rc["scores"])
+        else:
+            assert np.array_equal(c.perm, rc["perm"])
+    idx = np.concatenate([c.src_out for c in calls])
+    assert np.array_equal(idx, g[f"{comp}_rep_idx"])
+    assert np.array_equal(np.concatenate([c.w_out for c in calls]), g[f"{comp}_rep_w"])
+    act = np.concatenate([np.full(c.src_out.shape[0], c.src_in[-1] + 1) for c in calls])
+    assert np.array_equal(act, g[f"{comp}_rep_active"])
+
+
+def near_tie_flips(ref_scores, ref_order, our_order, ulps=8):
+    """Positions where two sorts differ; each must sit on a near-tie of the reference scores."""
+    bad = []
+    diff = np.nonzero(ref_order != our_order)[0]
+    s_sorted = ref_scores[ref_order]
+    for p in diff:
+        lo, hi = max(p - 1, 0), min(p + 1, len(s_sorted) - 1)
+        gap = min(abs(float(s_sorted[p]) - float(s_sorted[lo])) if lo != p else np.inf,
+                  abs(float(s_sorted[hi]) - float(s_sorted[p])) if hi != p else np.inf)
+        if gap > ulps * np.spacing(np.float32(abs(s_sorted[p]) + 1e-30)):
+            bad.append(int(p))
+    return diff, bad
+
+
+def test_fixed_order_scores_agree_with_reference_order(golden):
+    """The HIP compressor's fixed-order fp64 scores sort exactly like the reference's MKL fp32 scores,
+    except at near-ties (audited)."""
+    total_diff = 0
+    checked = 0
+    for name, prefix in (("flat_c1", "sorted_pair_"), ("flat_oddblock", ""), ("levels_c1", ""), ("levels_deg3", ""),
+                         ("levels_oddblock", "")):
+        g = golden(name)
+        k = g["k"]
+        block = int(g.meta["block"])
+        for ci, rc in enumerate(_golden_calls(g, prefix, int(g[f"{prefix}ncalls"]))):
+            if "scores" not in rc:
+                continue
+            ref_scores = rc["scores"]
+            ref_order = rc["order"]
+            if "src_in" in rc:  # level cascade: the compress input as token ids
+                rows = k[rc["src_in"]]
+            else:  # flat: call ci is block ci
+                rows = k[ci * block:(ci + 1) * block]
+            checked += 1
+            ours = orc.projection_scores(rows, _normalise(rc["direction_raw"]))
+            our_order = np.argsort(ours, kind="stable")
+            diff, bad = near_tie_flips(ref_scores, ref_order, our_order)
+            total_diff += diff.size
+            assert not bad, f"{name}: order differs away from a near-tie at {bad}"
+    assert checked > 40
+    assert total_diff == 0  # none expected at these sizes
+
+
+def test_flat_fixed_order_selection_equals_reference(golden):
+    for name, comp_prefix in (("flat_c1", "sorted_pair_"), ("flat_oddblock", "")):
+        g = golden(name)
+        block = int(g.meta["block"])
+        calls = orc.flat_coreset(g["k"], block, "sorted_pair", int(g.meta["seed"]))
+        idx = np.concatenate([c.src_out for c in calls])
+        assert np.array_equal(idx, g[f"{comp_prefix}rep_idx"])
+        assert np.array_equal(np.concatenate([c.w_out for c in calls]), g[f"{comp_prefix}rep_w"])
+
+
+@pytest.mark.parametrize("comp", ["sorted_pair", "random"])
+def test_flat_forward_matches_reference(golden, comp):
+    g = golden("flat_c1")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    out = orc.fast_path_forward(q, k, v, degree=2, block=128, scale=1.0, compressor=comp, seed=0)
+    assert rel(out, g[f"{comp}_out"]) < 1e-6
+
+
+def test_flat_oddblock_forward(golden):
+    g = golden("flat_oddblock")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    out = orc.fast_path_forward(q, k, v, degree=2, block=33, scale=1.0, compressor="sorted_pair", seed=9)
+    assert rel(out, g["out"]) < 1e-6
+    assert sorted(set(g["rep_w"].tolist())) == [1.0, 2.0]  # odd tail keeps weight 1
+
+
+def test_flat_bh_seeds(golden):
+    g = golden("flat_bh")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    bsz, heads = q.shape[:2]
+    for b in range(bsz):
+        for h in range(heads):
+            out = orc.fast_path_forward(q[b, h], k[b, h], v[b, h], degree=2, block=32, scale=None,
+                                        compressor="sorted_pair", seed=7 + b * heads + h)
+            assert rel(out, g["out"][b, h]) < 1e-6
+
+
+# --------------------------------------------------------------------------- merge-and-reduce levels
+
+LEVEL_CASES = ["levels_c1", "levels_random", "levels_deg3", "levels_oddblock", "levels_block2"]
+
+
+@pytest.mark.parametrize("name", LEVEL_CASES)
+def test_level_cascade_matches_reference(golden, name):
+    g = golden(name)
+    m = g.meta
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    state = orc.LevelState()
+    out = orc.levels_forward(q, k, v, degree=m["degree"], block=m["block"], scale=m["scale"],
+                             compressor=m["compressor"], seed=m["seed"], state_out=state)
+    ref_calls = [c for c in _golden_calls(g, "", int(g["ncalls"]))]
+    # every compress call: same inputs (order and weights), same kept items and weights
+    assert len(state.calls) == len(ref_calls)
+    for c, rc in zip(state.calls, ref_calls):
+        assert np.array_equal(c.src_in, rc["src_in"]) and np.array_equal(c.w_in, rc["w_in"])
+        assert np.array_equal(c.src_out, rc["src_out"]), f"{name}: selection differs"
+        assert np.array_equal(c.w_out, rc["w_out"])
+    assert rel(out, g["out"]) < 2e-6
+
+
+def test_level_invariants(golden):
+    g = golden("levels_c1")
+    m = g.meta
+    state = orc.LevelState()
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    orc.levels_forward(q, k, v, degree=2, block=m["block"], scale=1.0, seed=0, state_out=state)
+    nb = m["n"] // m["block"]
+    for lev, node in enumerate(state.levels):
+        present = node is not None
+        assert present == bool((nb >> lev) & 1)
+        if present:
+            assert node[0].shape[0] == m["block"] // 2
+            assert np.all(node[1] == 2.0 ** (lev + 1))
+    items_w = sum(float(n[1].sum()) for n in state.levels if n is not None)
+    assert items_w == nb * m["block"]  # weight is conserved
+
+
+def test_levels_without_compression_is_exact():
+    # test_streaming_attention.py:10-21: degree 3, block > n, unit-norm q, k
+    torch.manual_seed(0)
+    q = torch.randn(24, 6)
+    k = torch.randn(24, 6)
+    v = torch.randn(24, 5)
+    q = q / q.norm(dim=-1, keepdim=True)
+    k = k / k.norm(dim=-1, keepdim=True)
+    out = orc.levels_forward(q, k, v, degree=3, block=25, scale=1.0)
+    assert torch.allclose(out.double(), orc.classical_attention(q, k, v, 1.0), atol=3e-6, rtol=3e-6)
+
+
+# --------------------------------------------------------------------------- segment means
+
+def test_segment_mean_matches_reference(golden):
+    g = golden("segment_mean")
+    rk, rv, rpb = orc.segment_mean_coreset(torch.from_numpy(g["k"]), torch.from_numpy(g["v"]), 8, 2)
+    assert rpb == int(g["reps_per_block"]) == 4
+    assert rk.shape == (2, 8, 4) and rv.shape == (2, 8, 5)  # test_triton_article_attention.py:29-39
+    assert torch.allclose(rk, torch.from_numpy(g["rep_k"]), atol=1e-7)
+    assert torch.allclose(rv, torch.from_numpy(g["rep_v"]), atol=1e-7)
+
+
+def test_segment_forward_stride1_is_exact():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 40, 8, generator=g) * 0.3
+    k = torch.randn(2, 40, 8, generator=g) * 0.3
+    v = torch.randn(2, 40, 4, generator=g)
+    out = orc.segment_forward(q, k, v, degree=2, block=8, stride=1, scale=1.0)
+    assert rel(out, orc.classical_attention(q, k, v, 1.0)) < 1e-12
+
+
+# --------------------------------------------------------------------------- planted mistakes
+
+def test_planted_pair_rule_mistake_is_caught(golden, monkeypatch):
+    """Swapping the kept element of each pair must break the golden selections."""
+    g = golden("levels_c1")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    real = orc.sorted_pair_select
+
+    def flipped(src, w, scores, u):
+        return real(src, w, scores, 1.0 - u)
+
+    monkeypatch.setattr(orc, "sorted_pair_select", flipped)
+    state = orc.LevelState()
+    orc.levels_forward(q, k, v, degree=2, block=64, scale=1.0, seed=0, state_out=state)
+    ref0 = g["call0_src_out"]
+    assert not np.array_equal(state.calls[0].src_out, ref0)
+
+
+def test_planted_taylor_mistake_is_caught(golden, monkeypatch):
+    """Dropping the quadratic Taylor term must break the reference moment sums."""
+    g = golden("flat_c1")
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    real = orc.features
+    monkeypatch.setattr(orc, "features", lambda x, deg, ks: real(x, min(deg, 1), ks))
+    num, den = orc.low_sums_stream(q, k, v, 2, 1.0)
+    assert rel(den, g["low_den"]) > 1e-4
