@@ -62,7 +62,7 @@ def cpu_baseline(q, k, v, w):
 
     threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
-    rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "8192"))
+    rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "16384"))
     t = oracle.time_fast_path_sample(q[0, 0].contiguous(), k[0, 0].contiguous(), v[0, 0].contiguous(),
                                      degree=w["degree"], block=w["block"], scale=w["scale"], seed=w["seed"], rows=rows)
     n = w["seq_len"]

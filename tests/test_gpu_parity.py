@@ -38,7 +38,8 @@ def test_mfma_operand_layout():
     a = torch.randn(64, generator=g)
     b = torch.randn(64, generator=g)
     out = torch.empty(256, device=DEV)
-    st = _native.lib().sta_selftest_mfma(a.to(DEV).data_ptr(), b.to(DEV).data_ptr(), out.data_ptr())
+    a_d, b_d = a.to(DEV), b.to(DEV)  # keep the device copies alive across the launch
+    st = _native.lib().sta_selftest_mfma(a_d.data_ptr(), b_d.data_ptr(), out.data_ptr())
     _native.check(st, "sta_selftest_mfma")
     A = torch.empty(16, 4)
     B = torch.empty(4, 16)
