@@ -50,15 +50,33 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  * Exact low-degree Taylor moments over all keys *before* each row's chunk (K1).
  * Replaces low_degree_taylor_causal_sums / _stream / _prefix (fast_article_attention.py:184-285) and
  * TaylorMomentSketch.update/query (streaming_taylor_coreset_attention.py:265-296).
- *   chunk c covers rows [c*chunk - shift, (c+1)*chunk - shift); chunk is 64 (D <= 64) or 32 (D <= 128)
- *   feat_idx / feat_coef: the symmetric monomial table (fsplit * feat_per_split entries, feat_per_split
- *     a multiple of 16): packed indices i0 | i1<<8 | i2<<16 into [x_0..x_{D-1}, 1] and the key-side
- *     coefficient 1/prod(alpha!) (0 for padding features).
- *   outputs: low_num [BH][fsplit][N][Dv], low_den [BH][fsplit][N] (fp32, partial over feature splits).
+ *   chunk c covers rows [c*chunk - shift, (c+1)*chunk - shift); chunk must be sta_moment_chunk(d).
+ *   feat_quads [fsplit][4][wave_tiles][4], feat_coef [fsplit][4][wave_tiles][16]: the symmetric monomial
+ *     basis in tiles of 4 quads, wave_tiles tiles for each of the 4 waves of each feature split (padded
+ *     with coefficient-0 tiles).  A quad packs i0 | b<<8 | i2<<16 (b a multiple of 4, at most d) and
+ *     holds the features x[i0] x[b+s] x[i2], s = 0..3, of [x_0..x_{D-1}, 1, 0, 0, 0]; feat_coef is the
+ *     key-side coefficient 1/prod(alpha!) of each feature (0 for padding).  wave_tiles must be a count
+ *     the library is built for (sta_moment_wave_tiles).
+ *   ldq / ldv: row strides (elements) of q, k and of v; rows are read in 16-byte units, so ldq and ldv
+ *     times the element size must be multiples of 16 (pad the rows otherwise), ldq <= 64 for d <= 64
+ *     (128 above), and q, k, v must be 16-byte aligned.
+ *   grid: bh * fsplit * ceil(dv/32) workgroups of 256 threads.
+ *   outputs (fp32, partial over feature splits), in the layout sta_moment_partials_layout gives:
+ *     low_num [BH][fsplit][rows][ld], low_den [BH][fsplit][rows], row i stored at row_offset + i.
  */
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int degree, float scale, int chunk, int shift, int fsplit, int feat_per_split,
-                const uint32_t* feat_idx, const float* feat_coef, float* low_num, float* low_den, void* stream);
+                int ldq, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream);
+
+/* Smallest per-wave tile count >= want that sta_moments supports for (d, degree); -1 if none. */
+int sta_moment_wave_tiles(int d, int degree, int want);
+
+/* Layout of sta_moments' partial outputs for a sequence of n rows and dv value columns: rows per
+ * (head, split) including guard rows, row stride of low_num, and the storage row of sequence row 0. */
+int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* row_offset);
+
+/* Moment workgroups the kernel keeps resident per compute unit at (d, per-wave tile count): 1 or 2. */
+int sta_moment_occupancy(int d, int wave_tiles);
 
 /*
  * Block compressor for one batch of coreset nodes (K3), all heads at once.
@@ -96,6 +114,7 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *   tile_ptr[n_tiles+1] / tile_nodes: CSR list of the nodes each tile needs.
  *   node_meta[n_nodes][4]: item count, first and last active row, materialized flag (items index
  *     rep_k/rep_v instead of k/v).
+ *   low_num / low_den: sta_moments' partial outputs (sta_moment_partials_layout), fsplit splits.
  *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
  *   out: [BH][N][Dv] in out_dtype.
  *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator

@@ -48,6 +48,18 @@ def _f32(a: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
 
 
+def _unit_rows(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its rows are whole 16-byte units and 16-byte aligned, else a zero-padded copy."""
+    per_unit = 16 // t.element_size()
+    width = t.shape[-1]
+    if width % per_unit == 0 and t.data_ptr() % 16 == 0:
+        return t
+    padded = -(-width // per_unit) * per_unit
+    out = torch.zeros(t.shape[:-1] + (padded,), device=t.device, dtype=t.dtype)
+    out[..., :width] = t
+    return out
+
+
 class KernelTimer:
     """Records HIP events around each launch on the launch stream (for measured per-kernel times)."""
 
@@ -127,9 +139,10 @@ def prefill(
     stream = _native.stream_handle(dev)
     chunk = _plan.moment_chunk(d)
 
-    fsplit = int(os.environ.get("STA_FSPLIT", "0")) or _plan.choose_fsplit(d, degree, bh, dv)
-    fp = _plan.feature_plan(d, degree, fsplit)
-    fidx, fcoef = _on_device(("feat", d, degree, fsplit), dev, lambda: (_i32(fp.idx, dev), _f32(fp.coef, dev)))
+    ft = _plan.feature_tiles(d, degree)
+    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(d, degree))
+    fsplit = ms.fsplit
+    fidx, fcoef = _on_device(("mtable", d, degree, bh, dv), dev, lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
 
     raw = semantics == "taylor"
     if semantics in ("exact", "taylor"):
@@ -171,13 +184,18 @@ def prefill(
             dirs_d, unif_d, perms_d, desc_d = (_f32(dr.dirs, dev), _f32(dr.unif, dev), _i32(dr.perms, dev), _i32(desc, dev))
         batches_d = _on_device(("batches",) + pkey, dev, lambda: [_i32(b, dev) for b in plan.batches])
 
-    low_num = torch.empty((bh, fsplit, n, dv), device=dev, dtype=torch.float32)
-    low_den = torch.empty((bh, fsplit, n), device=dev, dtype=torch.float32)
+    lrows, lld, _ = _native.moment_partials_layout(n, dv)
+    low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
+    low_den = torch.empty((bh, fsplit, lrows), device=dev, dtype=torch.float32)
+
+    # the moment kernel reads rows in 16-byte units: pad rows whose byte length is not a whole unit
+    mq, mk, mv = _unit_rows(q3), _unit_rows(k3), _unit_rows(v3)
 
     def k1():
         st = lib.sta_moments(
-            q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), dt, bh, n, d, dv, degree, float(scale), chunk, shift,
-            fsplit, fp.per_split, fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+            mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, d, dv, mq.shape[-1], mv.shape[-1], degree,
+            float(scale), chunk, shift,
+            fsplit, ms.wave_tiles, fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")
 
     _run(timer, "moments", k1)
@@ -237,4 +255,4 @@ def prefill(
         _native.check(st, "sta_block_attention")
 
     _run(timer, "block_attention", k24)
-    return PrefillResult(out, node_src, node_w, plan, fp.count, fsplit, out_den)
+    return PrefillResult(out, node_src, node_w, plan, ft.count, fsplit, out_den)

@@ -40,8 +40,12 @@ _SIGNATURES = {
     "sta_moment_chunk": (_i32, [_i32]),
     "sta_moments": (
         _i32,
-        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p, _c_p],
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
+         _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),
+    "sta_moment_occupancy": (_i32, [_i32, _i32]),
+    "sta_moment_partials_layout": (_i32, [_i64, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "sta_compress_nodes": (
         _i32,
         [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],
@@ -114,6 +118,32 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_wave_tile_options: dict = {}
+
+
+def moment_wave_tile_options(d: int, degree: int) -> tuple:
+    """((per-wave tile count, workgroups resident per compute unit), ...) the moment kernel is built
+    for at (d, degree)."""
+    key = (d, degree)
+    if key not in _wave_tile_options:
+        l = lib()
+        opts = set()
+        for want in range(1, 65):
+            nt = l.sta_moment_wave_tiles(d, degree, want)
+            if nt > 0:
+                opts.add((nt, l.sta_moment_occupancy(d, nt)))
+        _wave_tile_options[key] = tuple(sorted(opts))
+    return _wave_tile_options[key]
+
+
+def moment_partials_layout(n: int, dv: int) -> tuple:
+    """(rows, ld, row_offset) of the moment kernel's partial outputs."""
+    rows, ld, off = _i64(), _i32(), _i32()
+    check(lib().sta_moment_partials_layout(n, dv, ctypes.byref(rows), ctypes.byref(ld), ctypes.byref(off)),
+          "sta_moment_partials_layout")
+    return rows.value, ld.value, off.value
 
 
 def limits() -> dict:

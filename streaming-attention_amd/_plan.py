@@ -50,7 +50,8 @@ def _cached(key, build):
 
 
 def moment_chunk(d: int) -> int:
-    return 64 if d <= 64 else 32
+    """Tokens per moment chunk (must equal sta_moment_chunk)."""
+    return 32
 
 
 def num_features(d: int, degree: int) -> int:
@@ -65,55 +66,149 @@ def _factorial_inverse(combo: Tuple[int, ...]) -> float:
     return inv
 
 
-# ----------------------------------------------------------------------------- feature table
+# ----------------------------------------------------------------------------- feature tiles
+
+MOM_WAVES = 4  # waves per moment workgroup (sta_moments)
+OCC2_SPEEDUP = 1.2  # per-tile throughput of two resident moment workgroups per CU vs one
+MOM_MAX_WAVE_TILES = 16  # largest per-wave tile count the kernel is instantiated for
+
 
 @dataclass(frozen=True)
-class FeaturePlan:
+class FeatureTiles:
+    """The monomial basis through `degree` laid out for the moment kernel: tiles of 16 features made of
+    4 quads; quad q of tile t is quads[4 t + q] (packed i0 | b << 8 | i2 << 16) and holds the features
+    x[i0] * x[b + s] * x[i2], s = 0..3, with b a multiple of 4 and x[d] = 1 (so i0 = i2 = d reduces the
+    degree).  coef[16 t + 4 q + s] is the key-side coefficient 1/prod(alpha!) of feature s of the quad,
+    0 where b + s is not a valid last factor (padding; x[b + s] is then 0 or the constant 1).
+
+    Same set of monomials as the reference's feature map (fast_article_attention.py:151-181,
+    streaming_taylor_coreset_attention.py:118-216); the order differs, which the moment sums do not
+    depend on.  Monomials sharing all factors but the last form a row (last factor >= the others); a
+    row is cut at multiples of 4, so every quad is one 16-byte LDS read in the kernel.  Padding costs
+    about 4% more tiles than a dense packing at d = 64, degree 2."""
+
     d: int
     degree: int
     count: int
-    fsplit: int
-    per_split: int
-    idx: np.ndarray  # uint32 [fsplit * per_split]
-    coef: np.ndarray  # float32
+    n_tiles: int
+    quads: np.ndarray  # uint32 [n_tiles * 4]
+    coef: np.ndarray  # float32 [n_tiles * 16]
 
 
-def choose_fsplit(d: int, degree: int, bh: int, dv: int, target_workgroups: int = 256) -> int:
-    ntile = -(-num_features(d, degree) // 16)
-    groups = -(-dv // 16)
-    fs_min = -(-ntile // (17 * 8))
-    fs_fill = -(-target_workgroups // max(1, bh * groups))
-    return max(fs_min, min(fs_fill, -(-ntile // 8)))
-
-
-def feature_plan(d: int, degree: int, fsplit: int) -> FeaturePlan:
-    """Monomial order [1, x_0..x_{d-1}, x_a x_b (a<=b, row-major), x_a x_b x_c (a<=b<=c, lexicographic)]:
-    the fast path's order for degree <= 2 (fast_article_attention.py:167-181) and
-    combinations_with_replacement for every degree (streaming_taylor_coreset_attention.py:170-178)."""
+def feature_tiles(d: int, degree: int) -> FeatureTiles:
+    if degree > 3 or d > 252:
+        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 252")
 
     def build():
-        one = d  # slot d of a staged row holds the constant 1
-        idx: List[int] = []
-        coef: List[float] = []
-        for l in range(degree + 1):
-            for combo in itertools.combinations_with_replacement(range(d), l):
-                ids = list(combo) + [one] * (3 - l)
-                idx.append(ids[0] | (ids[1] << 8) | (ids[2] << 16))
-                coef.append(_factorial_inverse(combo))
-        count = len(idx)
-        per = -(-count // fsplit)
-        per = -(-per // 16) * 16
-        total = per * fsplit
-        pad = one | (one << 8) | (one << 16)
-        idx_a = np.full(total, pad, dtype=np.uint32)
-        coef_a = np.zeros(total, dtype=np.float32)
-        idx_a[:count] = np.asarray(idx, dtype=np.uint32)
-        coef_a[:count] = np.asarray(coef, dtype=np.float32)
-        return FeaturePlan(d, degree, count, fsplit, per, idx_a, coef_a)
+        one = d
+        quads: List[int] = []
+        coefs: List[List[float]] = []
+        count = 0
 
-    if degree > 3 or d > 255:
-        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 255")
-    return _cached(("feat", d, degree, fsplit), build)
+        def add_row(prefix: Tuple[int, ...], lo: int, hi: int, with_const: bool) -> None:
+            """Features prefix + (c,) for lo <= c < hi (and the constant feature `prefix` when
+            with_const, stored at c = d), in quads of 4-aligned c."""
+            nonlocal count
+            last = d if with_const else hi - 1
+            if last < lo:
+                return
+            i0 = prefix[0] if len(prefix) >= 1 else one
+            i2 = prefix[1] if len(prefix) >= 2 else one
+            for b in range((lo // 4) * 4, last + 1, 4):
+                cs = []
+                for s in range(4):
+                    c = b + s
+                    if lo <= c < hi:
+                        cs.append(_factorial_inverse(tuple(sorted(prefix + (c,)))))
+                        count += 1
+                    elif with_const and c == d:
+                        cs.append(_factorial_inverse(prefix))
+                        count += 1
+                    else:
+                        cs.append(0.0)
+                quads.append(i0 | (b << 8) | (i2 << 16))
+                coefs.append(cs)
+
+        # degree 0 and 1: x_c for c < d plus the constant, all with prefix ()
+        add_row((), 0, d if degree >= 1 else 0, True)
+        if degree >= 2:
+            for a in range(d):
+                add_row((a,), a, d, False)
+        if degree >= 3:
+            for a in range(d):
+                for b2 in range(a, d):
+                    add_row((a, b2), b2, d, False)
+        n_tiles = -(-len(quads) // 4)
+        pad_quad = one | ((d // 4 * 4) << 8) | (one << 16)  # finite staged values; coefficient 0
+        q = np.full(n_tiles * 4, pad_quad, dtype=np.uint32)
+        c = np.zeros(n_tiles * 16, dtype=np.float32)
+        q[: len(quads)] = np.asarray(quads, dtype=np.uint32)
+        c[: 4 * len(coefs)] = np.asarray(coefs, dtype=np.float32).reshape(-1)
+        return FeatureTiles(d, degree, count, n_tiles, q, c)
+
+    return _cached(("ftiles", d, degree), build)
+
+
+@dataclass(frozen=True)
+class MomentSplit:
+    """Work split of the moment kernel: `fsplit` feature splits x `csplit` 32-column groups per head,
+    4 waves per workgroup, every wave holding exactly `wave_tiles` tiles.  quads/coef are the feature
+    table in the kernel's layout [fsplit][4][wave_tiles][4 quads | 16 coefficients]; wave j (= 4 fs + w)
+    holds the real tiles [tile_off[j], tile_off[j+1]) followed by padding tiles (coefficient 0)."""
+
+    fsplit: int
+    csplit: int
+    wave_tiles: int
+    tile_off: np.ndarray  # int32 [fsplit * 4 + 1]
+    quads: np.ndarray  # uint32 [fsplit * 4 * wave_tiles * 4]
+    coef: np.ndarray  # float32 [fsplit * 4 * wave_tiles * 16]
+
+
+def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int, int], ...],
+                 compute_units: int = 256) -> MomentSplit:
+    """Choose (fsplit, wave_tiles) minimising rounds-of-workgroups x tiles-per-wave on a GPU with
+    `compute_units` compute units; nt_options lists (per-wave tile count, workgroups resident per
+    compute unit) pairs the library supports.  Ties go to fewer feature splits (fewer partial sums)."""
+
+    def build():
+        t = ft.n_tiles
+        csplit = -(-dv // 32)
+        opts = sorted(nt_options)
+        best = None
+        for fsplit in range(1, t + 1):
+            need = -(-t // (MOM_WAVES * fsplit))
+            cand = next(((o, occ) for o, occ in opts if o >= need), None)
+            if cand is None:
+                continue
+            nt, occ = cand
+            rounds = -(-(bh * fsplit * csplit) // (compute_units * occ))
+            # a compute unit time-shares its resident workgroups; two waves per SIMD overlap one wave's
+            # VALU/LDS work with the other's matrix-core work (measured 1.2x per tile at d = 64)
+            cost = rounds * nt * occ / (OCC2_SPEEDUP if occ == 2 else 1.0)
+            if best is None or cost < best[0]:
+                best = (cost, fsplit, nt)
+            if need == 1:
+                break
+        if best is None:
+            raise ValueError(f"no supported per-wave tile count for {t} feature tiles (options {opts})")
+        _, fsplit, nt = best
+        parts = fsplit * MOM_WAVES
+        base, extra = divmod(t, parts)
+        sizes = [base + (1 if i < extra else 0) for i in range(parts)]
+        off = np.zeros(parts + 1, dtype=np.int32)
+        off[1:] = np.cumsum(sizes)
+        pad_quad = ft.d | ((ft.d // 4 * 4) << 8) | (ft.d << 16)
+        quads = np.full((parts, nt, 4), pad_quad, dtype=np.uint32)
+        coef = np.zeros((parts, nt, 16), dtype=np.float32)
+        tiles_q = ft.quads.reshape(t, 4)
+        tiles_c = ft.coef.reshape(t, 16)
+        for j in range(parts):
+            cnt = sizes[j]
+            quads[j, :cnt] = tiles_q[off[j]:off[j] + cnt]
+            coef[j, :cnt] = tiles_c[off[j]:off[j] + cnt]
+        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1))
+
+    return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units), build)
 
 
 # ----------------------------------------------------------------------------- draws

@@ -22,36 +22,65 @@ bool dtype_ok(int dt) { return dt == STA_F32 || dt == STA_BF16 || dt == STA_F16;
 constexpr int kMaxD = 128;
 constexpr int kMaxDv = 256;
 constexpr int kMaxDegree = 3;
-constexpr int kNW = 8;       // waves per moment workgroup
 constexpr int kTileRows = 128;
 
 // ---------------------------------------------------------------- moments dispatch
-template <bool DEG3, int NT, int CH>
+template <int NT, bool DEG3, bool DBIG>
 int launch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
-  const size_t smem = sta::moments_smem_bytes(CH, kNW, a.d, a.feat_per_split);
-  auto fn = sta::moments_kernel<DEG3, NT, kNW, CH>;
-  if (smem > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-    if (e != hipSuccess) return hip_status(e);
-  }
-  const int64_t grid = bh * a.ngroups * a.fsplit;
+  const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT)) * sizeof(float);
+  auto fn = sta::moments_kernel<NT, DEG3, DBIG>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+  if (e != hipSuccess) return hip_status(e);
+  const int64_t grid = bh * a.fsplit * a.csplit;
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(kNW * 64), smem, s, a);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOM_THREADS), smem, s, a);
   return check_launch();
 }
 
-template <bool DEG3, int CH>
-int dispatch_nt(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt) {
-  if (nt <= 1) return launch_moments<DEG3, 1, CH>(a, bh, s);
-  if (nt <= 2) return launch_moments<DEG3, 2, CH>(a, bh, s);
-  if (nt <= 3) return launch_moments<DEG3, 3, CH>(a, bh, s);
-  if (nt <= 5) return launch_moments<DEG3, 5, CH>(a, bh, s);
-  if (nt <= 9) return launch_moments<DEG3, 9, CH>(a, bh, s);
-  if (nt <= 13) return launch_moments<DEG3, 13, CH>(a, bh, s);
-  if (nt <= 17) return launch_moments<DEG3, 17, CH>(a, bh, s);
+// Per-wave tile counts the moment kernel is instantiated for, per (degree 3, d > 64).
+constexpr int kNtD2[] = {2, 4, 5, 9, 16};
+constexpr int kNtD3[] = {4, 8, 16};
+constexpr int kNtBigD2[] = {5, 16};
+constexpr int kNtBigD3[] = {4, 16};
+
+template <size_t L>
+int next_nt(const int (&tab)[L], int want) {
+  for (size_t i = 0; i < L; ++i)
+    if (tab[i] >= want) return tab[i];
+  return -1;
+}
+
+int moment_wave_tiles(int d, int degree, int want) {
+  if (want < 1) want = 1;
+  const bool deg3 = degree >= 3, big = d > 64;
+  if (!big) return deg3 ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
+  return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
+}
+
+#define STA_MOM_CASE(NT, D3, BIG) \
+  case NT: return launch_moments<NT, D3, BIG>(a, bh, s);
+
+int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
+  if (a.d <= 64) {
+    if (deg3) {
+      switch (nt) { STA_MOM_CASE(4, true, false) STA_MOM_CASE(8, true, false) STA_MOM_CASE(16, true, false) }
+    } else {
+      switch (nt) {
+        STA_MOM_CASE(2, false, false) STA_MOM_CASE(4, false, false) STA_MOM_CASE(5, false, false)
+        STA_MOM_CASE(9, false, false) STA_MOM_CASE(16, false, false)
+      }
+    }
+  } else {
+    if (deg3) {
+      switch (nt) { STA_MOM_CASE(4, true, true) STA_MOM_CASE(16, true, true) }
+    } else {
+      switch (nt) { STA_MOM_CASE(5, false, true) STA_MOM_CASE(16, false, true) }
+    }
+  }
   return STA_ERR_UNSUPPORTED;
 }
+#undef STA_MOM_CASE
 
 // ---------------------------------------------------------------- block-attention dispatch
 template <int DP, int DVT>
@@ -110,26 +139,45 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in) {
 
 int sta_tile_rows(void) { return kTileRows; }
 
-int sta_moment_chunk(int d) { return d <= 64 ? 64 : 32; }
+int sta_moment_chunk(int d) { return d > 0 ? sta::MOM_C : 0; }
+
+int sta_moment_wave_tiles(int d, int degree, int want) {
+  if (d <= 0 || d > kMaxD || degree < 0 || degree > kMaxDegree) return -1;
+  return moment_wave_tiles(d, degree, want);
+}
+
+int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* row_offset) {
+  if (n <= 0 || dv <= 0 || !rows || !ld || !row_offset) return STA_ERR_ARG;
+  *rows = n + 2 * sta::MOM_GUARD;
+  *ld = 32 * ((dv + 31) / 32);
+  *row_offset = sta::MOM_GUARD;
+  return STA_OK;
+}
+
+int sta_moment_occupancy(int d, int wave_tiles) {
+  return (wave_tiles > 0 && d > 0) ? sta::mom_wg_per_cu(wave_tiles, d > 64) : 0;
+}
 
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int degree, float scale, int chunk, int shift, int fsplit, int feat_per_split,
-                const uint32_t* feat_idx, const float* feat_coef, float* low_num, float* low_den, void* stream) {
-  if (!q || !k || !v || !feat_idx || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
+                int ldq, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream) {
+  if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
-  if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || feat_per_split <= 0) return STA_ERR_SHAPE;
-  if (feat_per_split % 16 != 0) return STA_ERR_SHAPE;
+  if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0) return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
+  if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
+  // rows are read in 16-byte units: strides must be whole units and the bases 16-byte aligned
+  const int esize = dtype == STA_F32 ? 4 : 2;
+  if (ldq < d || ldv < dv || (ldq * esize) % 16 != 0 || (ldv * esize) % 16 != 0) return STA_ERR_ARG;
+  if (ldq > (d <= 64 ? 64 : 128)) return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
+    return STA_ERR_ARG;
   sta::MomArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
-  a.ngroups = (dv + 15) / 16; a.fsplit = fsplit; a.feat_per_split = feat_per_split;
-  a.fidx = feat_idx; a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den;
-  const int nt = (feat_per_split / 16 + kNW - 1) / kNW;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool deg3 = degree >= 3;
-  if (chunk == 64) return deg3 ? dispatch_nt<true, 64>(a, bh, s, nt) : dispatch_nt<false, 64>(a, bh, s, nt);
-  return deg3 ? dispatch_nt<true, 32>(a, bh, s, nt) : dispatch_nt<false, 32>(a, bh, s, nt);
+  a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
+  a.low_num = low_num; a.low_den = low_den; a.ldq = ldq; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
+  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
 }
 
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
@@ -192,6 +240,7 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.degree = degree; a.scale = scale;
   a.eps = eps; a.mode = mode; a.block = block; a.chunk = chunk; a.shift = shift; a.exp_clamp = exp_clamp;
   a.low_num = low_num; a.low_den = low_den; a.fsplit = fsplit; a.tile_ptr = tile_ptr; a.tile_nodes = tile_nodes;
+  a.low_rows = n + 2 * sta::MOM_GUARD; a.low_ld = 32 * ((dv + 31) / 32); a.low_off = sta::MOM_GUARD;
   a.n_tiles = n_tiles; a.node_meta = node_meta; a.n_nodes = n_nodes; a.cap = cap; a.node_src = node_src;
   a.node_w = node_w; a.rep_k = rep_k; a.rep_v = rep_v; a.n_rep = n_rep; a.out = out; a.out_dtype = out_dtype; a.out_den = out_den;
   hipStream_t s = static_cast<hipStream_t>(stream);

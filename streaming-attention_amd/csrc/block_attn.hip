@@ -40,9 +40,12 @@ struct BlockArgs {
   int chunk;
   int shift;
   int exp_clamp;
-  const float* low_num;  // [BH][fsplit][n][dv]
-  const float* low_den;  // [BH][fsplit][n]
+  const float* low_num;  // [BH][fsplit][low_rows][low_ld], row i at low_off + i (sta_moments layout)
+  const float* low_den;  // [BH][fsplit][low_rows]
   int fsplit;
+  int64_t low_rows;
+  int low_ld;
+  int low_off;
   const int32_t* tile_ptr;    // [n_tiles + 1]
   const int32_t* tile_nodes;  // node ids
   int n_tiles;
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
     if (!rvalid[rs]) continue;
     const int64_t i = myrow[rs];
     float lowd = 0.f;
-    for (int f = 0; f < a.fsplit; ++f) lowd += a.low_den[(bh * a.fsplit + f) * a.n + i];
+    for (int f = 0; f < a.fsplit; ++f) lowd += a.low_den[(bh * a.fsplit + f) * a.low_rows + a.low_off + i];
     const bool raw = a.out_den != nullptr;
     if (raw && lg == 0) a.out_den[bh * a.n + i] = lowd + dsum;
     const float dn = fmaxf(lowd + dsum, a.eps);
@@ -294,7 +297,8 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
         const int col = 16 * ct + 4 * lg + r;
         if (col < a.dv) {
           float lown = 0.f;
-          for (int f = 0; f < a.fsplit; ++f) lown += a.low_num[((bh * a.fsplit + f) * a.n + i) * a.dv + col];
+          for (int f = 0; f < a.fsplit; ++f)
+            lown += a.low_num[((bh * a.fsplit + f) * a.low_rows + a.low_off + i) * a.low_ld + col];
           const float numv = num[rs][ct][r] + lown;
           if (raw)
             static_cast<float*>(a.out)[(bh * a.n + i) * a.dv + col] = numv;

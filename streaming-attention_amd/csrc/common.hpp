@@ -53,6 +53,10 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Empty register constraint: pins the computation of x at this point of the instruction stream (keeps
+// the scheduler from sinking an accumulation chain and holding all of its inputs live).
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
 // Taylor truncation sum_{r<=deg} x^r / r!, evaluated term by term (term = term * x / r) so that the
 // fp32 rounding sequence is the one of the reference's exp_taylor.
 __device__ __forceinline__ float taylor_poly(float x, int deg) {

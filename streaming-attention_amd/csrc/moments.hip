@@ -7,17 +7,54 @@
 // own chunk are added by the block kernel (closed-form Taylor polynomial), so the two kernels together
 // give sum_{j<=i} exp_{<=t}(s q_i.k_j) [v_j, 1] exactly (in exact arithmetic).
 //
-// Decomposition: one workgroup per (head, 16-wide value-column group g, feature split fs).  It walks the
-// sequence chunk by chunk, keeping its [features-in-split x 16] slice of S in MFMA accumulators for the
-// whole sequence (no state ever goes to HBM).  Per chunk:
-//   query : out[tok][col] += phi_q(tok)[f] * S[f][col]   (A = generated features, B = accumulators)
-//   update: S[f][col]     += phi_k(tok)[f] * V[tok][col] (A = generated features, B = V from LDS)
-// The denominator column (the "1" appended to v) is kept by VALU in LDS.  Partial outputs of the 8
-// waves are summed in LDS in a fixed order (deterministic), and the feature-split partials are summed
-// by the block kernel.
+// Feature layout.  The monomials are grouped in quads x[i0] x[b+s] x[i2], s = 0..3, b a multiple of 4
+// (x[d] = 1 lowers the degree; see feature_tiles in _plan.py), 4 quads per tile of 16 features.  The
+// tiles are split over `fsplit` workgroups and over the 4 waves of a workgroup, every wave holding
+// exactly NT tiles (the host pads with zero tiles, so the loops are branch-free and fully unrolled).
+// A workgroup also owns one 32-wide group of value columns (csplit = ceil(dv/32) per feature split).
+// Each wave keeps its [NT x 16 features] x [32 columns] slice of S in MFMA accumulators for the whole
+// sequence (no state ever goes to HBM) and walks the sequence in chunks of 32 tokens:
+//   query : out[tok][col] += phi_q(tok)[f] S[f][col]. A (16 tok x 4 f): lane (li, lg) holds token li,
+//           features of quad lg -- one 16-byte LDS read of the row-major queries gives all four
+//           x[b+s], one more read x[i0].  B = the accumulator itself (see common.hpp).
+//   update: S[f][col] += phi_k(tok)[f] V[tok][col].   A (16 f x 4 tok): lane (li, lg) holds feature li
+//           and, at step ks, token 8 lg + ks; B: V[8 lg + ks][col] with the same token mapping.  With
+//           keys and values stored token-contiguous, two 16-byte reads give a lane its 8 steps.
+// Every generated feature value feeds two MFMAs (two 16-column tiles).  The denominator column (the
+// "1" appended to v) is kept by VALU per feature, in registers.  The 4 waves' query partials are
+// summed in LDS in a fixed order (deterministic) and stored per feature split; the block kernel adds
+// the splits.
+//
+// Pipeline.  Two chunk buffers and two partial buffers in LDS, one barrier per chunk.  Iteration c:
+// issue the (unconditional, clamped) 16-byte loads of chunk c+1; query chunk c from buffer c&1; write
+// c's partials; stage chunk c+1 into the other buffer; reduce and store chunk c-1's partials; update
+// the state with chunk c; barrier.  A dependent MFMA waits ~3 issue slots for its accumulator, so both
+// phases keep >= 8 independent accumulator chains in flight: the query alternates two accumulator sets
+// by tile, the update walks token steps outermost over all NT tiles.  Operands of the next step are
+// read while the current step's MFMAs issue.  For NT <= 5 two workgroups share a compute unit (two
+// waves per SIMD), so one wave's VALU/LDS work runs under the other's matrix-core work.
+//
+// LDS layouts (fp32) per chunk buffer:
+//   Qs [32][LDQ]   row-major scaled queries; column d = 1 (0 on rows outside the sequence), columns
+//                  d+1..d+3 = 0; LDQ = 68 (d <= 64) or 132, = 4 (mod 64): the 16 rows of a 16-byte
+//                  read land in distinct bank quads.
+//   Kt [KR][36]    transposed keys (row = dimension), row d = constant, rows d+1..d+3 = 0.
+//   Vt [32][36]    transposed values of the workgroup's 32 columns.
+// Partials: red [4 waves][33][32]: column-major [column][token], column 32 = denominator.
+// Running denominators: den [4 waves][NT tiles x 16 features].
 #include "common.hpp"
 
 namespace sta {
+
+constexpr int MOM_C = 32;    // tokens per chunk
+constexpr int MOM_LDT = 36;  // token stride of the transposed Kt / Vt rows
+constexpr int MOM_LDR = 32;  // token stride of a partial column
+constexpr int MOM_WAVES = 4;
+constexpr int MOM_THREADS = 64 * MOM_WAVES;
+// Guard rows before and after the sequence in the partial outputs: every chunk's rows have a valid
+// address, so the partial stores are unconditional (conditional stores would make the compiler's
+// vmcnt accounting wait for them before the next chunk's prefetched loads).
+constexpr int MOM_GUARD = 32;
 
 struct MomArgs {
   const void* q;
@@ -28,184 +65,386 @@ struct MomArgs {
   int d;
   int dv;
   float scale;
-  int shift;           // chunk c covers rows [c*CH - shift, (c+1)*CH - shift)
-  int ngroups;         // ceil(dv / 16)
-  int fsplit;          // feature splits
-  int feat_per_split;  // multiple of 16
-  const uint32_t* fidx;  // [fsplit * feat_per_split] packed (i0 | i1 << 8 | i2 << 16), slot d == 1.0
-  const float* fcoef;    // key-side coefficient 1/prod(alpha!), 0 for padding features
-  float* low_num;        // [BH][fsplit][n][dv]
-  float* low_den;        // [BH][fsplit][n]
+  int shift;              // chunk c covers rows [c*32 - shift, (c+1)*32 - shift)
+  int fsplit;             // feature splits (workgroups per head and column group)
+  int csplit;             // 32-column groups
+  const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4] packed (i0 | b << 8 | i2 << 16)
+  const float* fcoef;     // [fsplit][4 waves][NT tiles][16] key-side coefficient, 0 for padding
+  float* low_num;         // [BH][fsplit][n + 2*MOM_GUARD][ldo], row r at r + MOM_GUARD
+  float* low_den;         // [BH][fsplit][n + 2*MOM_GUARD]
+  int ldo;                // low_num row stride: 32 * csplit
+  int ldq;                // row stride (elements) of q and k: ldq >= d, ldq * esize a multiple of 16
+  int ldv;                // row stride of v: ldv >= dv, ldv * esize a multiple of 16
+  int esize;              // bytes per input element (4 or 2)
 };
 
-template <bool DEG3, int NT, int NW, int CH>
-__global__ __launch_bounds__(NW * 64) void moments_kernel(const MomArgs a) {
-  extern __shared__ float smem[];
-  const int LD = a.d + 1;
-  const int FP = a.feat_per_split;
-  // Layout: [ftab | fcoef | den] persistent, then the chunk region, aliased by the reduction buffer.
-  uint32_t* ftab = reinterpret_cast<uint32_t*>(smem);
-  float* fcoef = smem + FP;
-  float* den_s = smem + 2 * FP;
-  float* region = smem + 3 * FP;
-  float* Qs = region;              // [CH][LD]
-  float* Ks = Qs + CH * LD;        // [CH][LD]
-  float* Vs = Ks + CH * LD;        // [CH][16]
-  float* red = region;             // [NW][CH][17]  (used after Qs/Ks/Vs are dead)
+__host__ __device__ constexpr int mom_ldq(bool dbig) { return dbig ? 132 : 68; }
+__host__ __device__ constexpr int mom_krows(bool dbig) { return dbig ? 132 : 68; }
+__host__ __device__ constexpr int mom_buf_floats(bool dbig) {
+  return MOM_C * mom_ldq(dbig) + mom_krows(dbig) * MOM_LDT + 32 * MOM_LDT;
+}
+__host__ __device__ constexpr int mom_red_floats() { return MOM_WAVES * 33 * MOM_LDR; }
+// Shared-memory floats of a launch (must match the carve-up in moments_kernel).
+__host__ __device__ constexpr int mom_smem_floats(bool dbig, int nt) {
+  return 2 * mom_buf_floats(dbig) + 2 * mom_red_floats() + MOM_WAVES * nt * 16;
+}
+// Workgroups per compute unit an instantiation is built for (registers <= 256 and LDS <= 80 KiB for 2).
+__host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig) { return (nt <= 5 && !dbig) ? 2 : 1; }
 
-  const int per_head = a.ngroups * a.fsplit;
-  const int wg = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t bh = wg / per_head;
-  const int rem = wg % per_head;
-  const int g = rem / a.fsplit;
-  const int fs = rem % a.fsplit;
+// Chunk staging in registers: 16-byte units.  The loads are unconditional (row index clamped into the
+// sequence, unit index clamped into the row), so none of them waits on another; validity and the dtype
+// conversion are applied when the units are written to LDS.
+template <bool DBIG>
+struct MomStage {
+  static constexpr int QV = MOM_C * (DBIG ? 128 : 64) * 4 / 16 / MOM_THREADS;  // 2 or 4 (fp32 rows)
+  uint4 q[QV];
+  uint4 k[QV];
+  uint4 v;
+};
 
+__device__ __forceinline__ int64_t clamp_row(int64_t row, int64_t n) { return row < 0 ? 0 : (row >= n ? n - 1 : row); }
+
+template <bool DBIG>
+__device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomArgs& a, int64_t bh, int64_t row0, int col0) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const int ntile = FP / 16;
-
-  for (int e = tid; e < FP; e += NW * 64) {
-    ftab[e] = a.fidx[(int64_t)fs * FP + e];
-    fcoef[e] = a.fcoef[(int64_t)fs * FP + e];
-    den_s[e] = 0.0f;
+  const int epu = 16 / a.esize;  // elements per 16-byte unit
+  const int uq = a.ldq / epu;    // units per q/k row
+  const char* qb = static_cast<const char*>(a.q) + bh * a.n * a.ldq * a.esize;
+  const char* kb = static_cast<const char*>(a.k) + bh * a.n * a.ldq * a.esize;
+  const char* vb = static_cast<const char*>(a.v) + bh * a.n * a.ldv * a.esize;
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+    const int e = tid + MOM_THREADS * j;
+    {  // q: row-major slots (coalesced)
+      const int t = e / uq;
+      const int u = e - t * uq;
+      const int64_t row = clamp_row(row0 + min(t, MOM_C - 1), a.n);
+      st.q[j] = *reinterpret_cast<const uint4*>(qb + (row * a.ldq + u * epu) * a.esize);
+    }
+    {  // k: token-fast slots (transposed LDS writes)
+      const int tok = e & (MOM_C - 1);
+      const int u = min(e >> 5, uq - 1);
+      const int64_t row = clamp_row(row0 + tok, a.n);
+      st.k[j] = *reinterpret_cast<const uint4*>(kb + (row * a.ldq + u * epu) * a.esize);
+    }
   }
+  {  // v: token-fast slots over the workgroup's 32 columns
+    const int tok = tid & (MOM_C - 1);
+    const int u = tid >> 5;  // < 8
+    const int col = min(col0 + u * epu, a.ldv - epu);
+    const int64_t row = clamp_row(row0 + tok, a.n);
+    st.v = *reinterpret_cast<const uint4*>(vb + (row * a.ldv + col) * a.esize);
+  }
+}
 
-  floatx4 st[NT];
+// The 16-byte unit u as 4 (fp32) or 8 (bf16 / fp16) floats; only f[0..16/esize) are meaningful.
+__device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f)[8]) {
+  if (dtype == F32) {
+    f[0] = __uint_as_float(u.x);
+    f[1] = __uint_as_float(u.y);
+    f[2] = __uint_as_float(u.z);
+    f[3] = __uint_as_float(u.w);
+    f[4] = f[5] = f[6] = f[7] = 0.f;
+  } else if (dtype == BF16) {
+    f[0] = __uint_as_float(u.x << 16);
+    f[1] = __uint_as_float(u.x & 0xffff0000u);
+    f[2] = __uint_as_float(u.y << 16);
+    f[3] = __uint_as_float(u.y & 0xffff0000u);
+    f[4] = __uint_as_float(u.z << 16);
+    f[5] = __uint_as_float(u.z & 0xffff0000u);
+    f[6] = __uint_as_float(u.w << 16);
+    f[7] = __uint_as_float(u.w & 0xffff0000u);
+  } else {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int kt = 0; kt < NT; ++kt) st[kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < 8; ++m)
+      f[m] = static_cast<float>(
+          __builtin_bit_cast(_Float16, static_cast<uint16_t>((m & 1) ? (w[m >> 1] >> 16) : (w[m >> 1] & 0xffffu))));
+  }
+}
 
-  const int64_t qkbase = bh * a.n * a.d;
-  const int64_t vbase = bh * a.n * a.dv;
-  const int nchunks = static_cast<int>((a.n + a.shift + CH - 1) / CH);
-  const int col0 = 16 * g;
-
-  for (int c = 0; c < nchunks; ++c) {
-    const int64_t row0 = static_cast<int64_t>(c) * CH - a.shift;
-    __syncthreads();  // previous chunk's reduction buffer reads are done
-    for (int e = tid; e < CH * LD; e += NW * 64) {
-      const int t = e / LD, col = e - t * LD;
+template <bool DBIG>
+__device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomArgs& a, float* buf, int64_t row0,
+                                          int col0) {
+  constexpr int LDQ = mom_ldq(DBIG);
+  float* Qs = buf;
+  float* Kt = Qs + MOM_C * LDQ;
+  float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
+  const int tid = threadIdx.x;
+  const int epu = 16 / a.esize;
+  const int uq = a.ldq / epu;
+  const bool fast = a.esize == 4 && (a.d & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+    const int e = tid + MOM_THREADS * j;
+    {
+      const int t = e / uq, u = e - t * uq;
       const int64_t row = row0 + t;
-      const bool valid = row >= 0 && row < a.n;
-      float qv = 0.f, kv = 0.f;
-      if (col < a.d) {
-        if (valid) {
-          qv = load_elem(a.q, qkbase + row * a.d + col, a.dtype) * a.scale;
-          kv = load_elem(a.k, qkbase + row * a.d + col, a.dtype);
-        }
-      } else {
-        // slot d carries the constant 1 of the monomial basis; 0 on invalid rows zeroes every feature
-        qv = valid ? 1.f : 0.f;
-        kv = valid ? 1.f : 0.f;
-      }
-      Qs[e] = qv;
-      Ks[e] = kv;
-    }
-    for (int e = tid; e < CH * 16; e += NW * 64) {
-      const int t = e >> 4, j = e & 15;
-      const int64_t row = row0 + t;
-      const int col = col0 + j;
-      Vs[e] = (row >= 0 && row < a.n && col < a.dv) ? load_elem(a.v, vbase + row * a.dv + col, a.dtype) : 0.f;
-    }
-    __syncthreads();
-
-    // ---- query with the exclusive state ----
-    floatx4 o[CH / 16];
-    float dq[CH / 16];
+      const float sc = (row >= 0 && row < a.n) ? a.scale : 0.f;
+      if (t < MOM_C) {
+        float f[8];
+        unit_floats(st.q[j], a.dtype, f);
+        if (fast) {
+          if (4 * u < a.d) *reinterpret_cast<floatx4*>(Qs + t * LDQ + 4 * u) = floatx4{f[0], f[1], f[2], f[3]} * sc;
+        } else {
 #pragma unroll
-    for (int tt = 0; tt < CH / 16; ++tt) {
-      o[tt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      dq[tt] = 0.f;
-    }
-#pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
-      const int tile = wave + kt * NW;
-      if (tile < ntile) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int f = 16 * tile + 4 * lg + s;
-          const uint32_t idx = ftab[f];
-          const int i0 = idx & 255, i1 = (idx >> 8) & 255, i2 = (idx >> 16) & 255;
-          const float dnf = den_s[f];
-#pragma unroll
-          for (int tt = 0; tt < CH / 16; ++tt) {
-            const float* qr = Qs + (16 * tt + li) * LD;
-            float x = qr[i0] * qr[i1];
-            if (DEG3) x = x * qr[i2];
-            o[tt] = mfma4(x, st[kt][s], o[tt]);
-            dq[tt] += x * dnf;
+          for (int m = 0; m < 8; ++m) {
+            const int dim = u * epu + m;
+            if (m < epu && dim < a.d) Qs[t * LDQ + dim] = f[m] * sc;
           }
         }
       }
     }
-
-    // ---- update the state with this chunk ----
-    float dacc[NT];
+    {
+      const int tok = e & (MOM_C - 1), u = e >> 5;
+      const int64_t row = row0 + tok;
+      const float ok = (row >= 0 && row < a.n) ? 1.f : 0.f;
+      if (u < uq) {
+        float f[8];
+        unit_floats(st.k[j], a.dtype, f);
 #pragma unroll
-    for (int kt = 0; kt < NT; ++kt) dacc[kt] = 0.f;
-    for (int ks = 0; ks < CH / 4; ++ks) {
-      const int tok = 4 * ks + lg;
-      const float b = Vs[tok * 16 + li];
-      const float* kr = Ks + tok * LD;
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        const int tile = wave + kt * NW;
-        if (tile < ntile) {
-          const int f = 16 * tile + li;
-          const uint32_t idx = ftab[f];
-          const int i0 = idx & 255, i1 = (idx >> 8) & 255, i2 = (idx >> 16) & 255;
-          float x = kr[i0] * kr[i1];
-          if (DEG3) x = x * kr[i2];
-          x = x * fcoef[f];
-          st[kt] = mfma4(x, b, st[kt]);
-          dacc[kt] += x;
+        for (int m = 0; m < 8; ++m) {
+          const int dim = u * epu + m;
+          if (m < epu && dim < a.d) Kt[dim * MOM_LDT + tok] = f[m] * ok;
         }
       }
     }
+  }
+  {
+    const int tok = tid & (MOM_C - 1), u = tid >> 5;
+    const int64_t row = row0 + tok;
+    const bool ok = row >= 0 && row < a.n;
+    if (u * epu < 32) {
+      float f[8];
+      unit_floats(st.v, a.dtype, f);
 #pragma unroll
-    for (int kt = 0; kt < NT; ++kt) {
-      const int tile = wave + kt * NW;
-      float dsum = dacc[kt];
-      dsum += __shfl_xor(dsum, 16);
-      dsum += __shfl_xor(dsum, 32);
-      if (tile < ntile && lg == 0) den_s[16 * tile + li] += dsum;
-    }
-    __syncthreads();  // Qs/Ks/Vs dead; den_s updated
-
-    // ---- deterministic cross-wave reduction of the query partials ----
-#pragma unroll
-    for (int tt = 0; tt < CH / 16; ++tt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[(wave * CH + 16 * tt + 4 * lg + r) * 17 + li] = o[tt][r];
-      float dsum = dq[tt];
-      dsum += __shfl_xor(dsum, 16);
-      dsum += __shfl_xor(dsum, 32);
-      if (lg == 0) red[(wave * CH + 16 * tt + li) * 17 + 16] = dsum;
-    }
-    __syncthreads();
-    for (int e = tid; e < CH * 17; e += NW * 64) {
-      const int t = e / 17, j = e - t * 17;
-      const int64_t row = row0 + t;
-      if (row < 0 || row >= a.n) continue;
-      float acc = 0.f;
-      for (int w = 0; w < NW; ++w) acc += red[(w * CH + t) * 17 + j];
-      const int64_t obase = (bh * a.fsplit + fs) * a.n + row;
-      if (j < 16) {
-        const int col = col0 + j;
-        if (col < a.dv) a.low_num[obase * a.dv + col] = acc;
-      } else if (g == 0) {
-        a.low_den[obase] = acc;
+      for (int m = 0; m < 8; ++m) {
+        const int c = u * epu + m;  // column within the group of 32
+        if (m < epu) Vt[c * MOM_LDT + tok] = (ok && col0 + c < a.dv) ? f[m] : 0.f;
       }
     }
   }
+  // the constant factor: 1 on rows inside the sequence, 0 outside (zeroes every feature of the row)
+  if (tid < MOM_C) {
+    const int64_t row = row0 + tid;
+    const float one = (row >= 0 && row < a.n) ? 1.f : 0.f;
+    Qs[tid * LDQ + a.d] = one;
+    Kt[a.d * MOM_LDT + tid] = one;
+  }
 }
 
-// Shared-memory bytes for a launch (must match the carve-up above).
-inline size_t moments_smem_bytes(int CH, int NW, int d, int feat_per_split) {
-  const size_t region_a = static_cast<size_t>(CH) * (d + 1) * 2 + static_cast<size_t>(CH) * 16;
-  const size_t region_b = static_cast<size_t>(NW) * CH * 17;
-  const size_t region = region_a > region_b ? region_a : region_b;
-  return (3 * static_cast<size_t>(feat_per_split) + region) * sizeof(float);
+// Fixed-order sum of the 4 waves' partials of the chunk starting at row0, stored unconditionally:
+// low_num rows of the workgroup's 32 columns and the low_den rows (the column-group workgroups of a
+// feature split compute bit-identical denominators, so all of them store it).
+__device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
+                                                 int col0) {
+  const int tid = threadIdx.x;
+  const int col = tid & 31, t4 = 4 * (tid >> 5);  // 8 groups of 4 tokens
+  floatx4 acc = *reinterpret_cast<const floatx4*>(red + col * MOM_LDR + t4);
+#pragma unroll
+  for (int ww = 1; ww < MOM_WAVES; ++ww) acc += *reinterpret_cast<const floatx4*>(red + (ww * 33 + col) * MOM_LDR + t4);
+  float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
+  const int tok = tid & (MOM_C - 1);
+  float den = red[32 * MOM_LDR + tok];
+#pragma unroll
+  for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[(ww * 33 + 32) * MOM_LDR + tok];
+  a.low_den[obase + row0 + tok] = den;
+}
+
+template <int NT, bool DEG3, bool DBIG>
+__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
+  constexpr int LDQ = mom_ldq(DBIG);
+  constexpr int BUF = mom_buf_floats(DBIG);
+  constexpr int CT = 2;           // 16-column tiles per wave
+  constexpr int TT = MOM_C / 16;  // 16-token tiles per chunk (query)
+  constexpr int KS = MOM_C / 4;   // update steps per chunk (token 8 lg + ks)
+  static_assert(KS == 8, "update token mapping assumes 32-token chunks");
+  extern __shared__ float smem[];
+  float* red_all = smem + 2 * BUF;
+  float* den_all = red_all + 2 * mom_red_floats();  // [4 waves][NT * 16]
+
+  const int per_head = a.fsplit * a.csplit;
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / per_head;
+  const int rem = wg - static_cast<int>(bh) * per_head;
+  const int fs = rem / a.csplit;
+  const int cs = rem - fs * a.csplit;
+  const int col0 = 32 * cs;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  float* den_s = den_all + w * NT * 16;  // running denominator of every feature of this wave's tiles
+
+  // ---- per-lane feature offsets (constant over the sequence) ----
+  const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NT;
+  int qa[NT], qb[NT], qc[DEG3 ? NT : 1];  // query: columns of x[i0], x[b..b+3], x[i2] of quad lg
+  int ka[NT], kb[NT], kc[DEG3 ? NT : 1];  // update: Kt rows of feature li, plus the token offset 8 lg
+  float kcoef[NT];
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+    const uint32_t pq = a.quads[(tile0 + kt) * 4 + lg];
+    qa[kt] = static_cast<int>(pq & 255u);
+    qb[kt] = static_cast<int>((pq >> 8) & 255u);
+    if (DEG3) qc[DEG3 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
+    const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
+    ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 8 * lg;
+    kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 8 * lg;
+    if (DEG3) kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 8 * lg;
+    kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
+  }
+
+  floatx4 st[NT][CT];
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nchunks = static_cast<int>((a.n + a.shift + MOM_C - 1) / MOM_C);
+  const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
+  const int64_t first = -static_cast<int64_t>(a.shift);
+
+  // zero both chunk buffers (their padding rows / columns are never written again) and the denominators
+  for (int e = tid; e < 2 * BUF; e += MOM_THREADS) smem[e] = 0.f;
+  for (int e = tid; e < MOM_WAVES * NT * 16; e += MOM_THREADS) den_all[e] = 0.f;
+  __syncthreads();
+  MomStage<DBIG> pre;
+  mom_load<DBIG>(pre, a, bh, first, col0);
+  mom_store<DBIG>(pre, a, smem, first, col0);
+  __syncthreads();
+
+  for (int c = 0; c < nchunks; ++c) {
+    const int cur = c & 1;
+    const int64_t row0 = first + static_cast<int64_t>(c) * MOM_C;
+    const float* Qs = smem + cur * BUF;
+    const float* Kt = Qs + MOM_C * LDQ;
+    const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
+
+    // prefetch chunk c+1 (unconditional, clamped); staged after the query phase
+    mom_load<DBIG>(pre, a, bh, row0 + MOM_C, col0);
+
+    // ---- query with the state of all previous chunks: two accumulator sets (tile parity), so 8
+    //      independent MFMA chains; tile kt+1's operands are read during tile kt ----
+    floatx4 o[2][TT][CT];
+    float dq[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      dq[tt] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) o[0][tt][ct] = o[1][tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    {
+      float x0[2][TT], x2[2][TT];
+      floatx4 x1[2][TT], dn[2];
+      const float* qrow = Qs + li * LDQ;
+      auto qload = [&](int kt, int buf) {
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+          x0[buf][tt] = qrow[16 * tt * LDQ + qa[kt]];
+          x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + qb[kt]);
+          if (DEG3) x2[buf][tt] = qrow[16 * tt * LDQ + qc[DEG3 ? kt : 0]];
+        }
+        dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
+      };
+      qload(0, 0);
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        const int cb = kt & 1;
+        if (kt + 1 < NT) qload(kt + 1, cb ^ 1);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) {
+            float x = x0[cb][tt] * x1[cb][tt][s];
+            if (DEG3) x *= x2[cb][tt];
+            dq[tt] = fmaf(x, dn[cb][s], dq[tt]);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) o[cb][tt][ct] = mfma4(x, st[kt][ct][s], o[cb][tt][ct]);
+          }
+        }
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) pin(dq[tt]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the one-tile-ahead pipeline shape
+      }
+    }
+
+    // ---- this wave's query partials -> red[cur] (column-major, 4 tokens per 16-byte write) ----
+    {
+      float* rw = red_all + cur * mom_red_floats() + w * 33 * MOM_LDR;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          *reinterpret_cast<floatx4*>(rw + (16 * ct + li) * MOM_LDR + 16 * tt + 4 * lg) = o[0][tt][ct] + o[1][tt][ct];
+        float s = dq[tt];
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        if (lg == 0) rw[32 * MOM_LDR + 16 * tt + li] = s;
+      }
+    }
+    // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
+    if (c + 1 < nchunks) mom_store<DBIG>(pre, a, smem + (cur ^ 1) * BUF, row0 + MOM_C, col0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- update: token steps outermost over all tiles (2 NT independent chains), in two halves of 4
+    //      steps; the keys of the second half are read while the first half's MFMAs issue ----
+    {
+      floatx4 vv[2][CT];  // values of tokens 8 lg + 0..3 and 8 lg + 4..7
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
+        vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
+      }
+      floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
+      auto uload = [&](int h) {
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+          fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + ka[kt] + 4 * h);
+          fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + kb[kt] + 4 * h);
+          if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + kc[DEG3 ? kt : 0] + 4 * h);
+        }
+      };
+      uload(0);
+      // partials of the previous chunk: fixed-order reduction and store, under the first loads
+      if (c > 0) mom_reduce_store(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
+      __builtin_amdgcn_sched_barrier(0);
+      float dacc[NT];
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) dacc[kt] = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 0) uload(1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int kt = 0; kt < NT; ++kt) {
+            float x = fa[h][kt][e] * fb[h][kt][e];
+            if (DEG3) x *= fc[h][DEG3 ? kt : 0][e];
+            x *= kcoef[kt];
+            dacc[kt] += x;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma4(x, vv[h][ct][e], st[kt][ct]);
+          }
+#pragma unroll
+          for (int kt = 0; kt < NT; ++kt) pin(dacc[kt]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        float s = dacc[kt];
+        s += __shfl_xor(s, 16);
+        s += __shfl_xor(s, 32);
+        if (lg == 0) den_s[16 * kt + li] += s;
+      }
+    }
+    __syncthreads();
+  }
+  mom_reduce_store(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase,
+                   first + static_cast<int64_t>(nchunks - 1) * MOM_C, col0);
 }
 
 }  // namespace sta

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import _native
+import reference_cpu as orc
 import _plan
 import fast_article_attention as faa
 import streaming_taylor_coreset_attention as stc
@@ -42,7 +43,7 @@ def test_library_exports_header_symbols():
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 1, 1, 2, 1.0, 64, 0, 1, 16, None, None, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 1, 1, 4, 4, 2, 1.0, 64, 0, 1, 9, None, None, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
 
@@ -111,18 +112,72 @@ def test_level_plan_intervals_follow_binary_counter():
         assert vis <= set(plan.tile_nodes[plan.tile_ptr[t]:plan.tile_ptr[t + 1]].tolist())
 
 
-def test_feature_plan_layout():
-    fp = _plan.feature_plan(5, 3, 2)
-    assert fp.count == 1 + 5 + 15 + 35
-    assert fp.per_split % 16 == 0 and fp.per_split * 2 >= fp.count
-    i0 = fp.idx & 255
-    i1 = (fp.idx >> 8) & 255
-    i2 = (fp.idx >> 16) & 255
-    assert (i0[0], i1[0], i2[0]) == (5, 5, 5) and fp.coef[0] == 1.0  # constant feature
-    assert (i0[1], i1[1], i2[1]) == (0, 5, 5)  # x_0
-    assert (i0[6], i1[6], i2[6]) == (0, 0, 5) and fp.coef[6] == 0.5  # x_0^2 / 2
-    assert (i0[21], i1[21], i2[21]) == (0, 0, 0) and fp.coef[21] == np.float32(1 / 6)
-    assert np.all(fp.coef[fp.count:] == 0)
+def _quad_features(ft):
+    """(monomial, coef) of every feature slot of a quad table: monomial = sorted factors without the
+    constant index d; slots beyond the constant (index > d) are reported as None."""
+    out = []
+    for q, packed in enumerate(ft.quads):
+        i0, b, i2 = int(packed) & 255, (int(packed) >> 8) & 255, (int(packed) >> 16) & 255
+        for s in range(4):
+            ids = (i0, b + s, i2)
+            coef = float(ft.coef[4 * q + s])
+            mono = None if max(ids) > ft.d else tuple(sorted(i for i in ids if i != ft.d))
+            out.append((mono, coef))
+    return out
+
+
+@pytest.mark.parametrize("d,degree", [(5, 3), (64, 2), (32, 2), (16, 3), (8, 0), (12, 1), (128, 2), (6, 2)])
+def test_feature_tiles_cover_the_monomial_basis(d, degree):
+    ft = _plan.feature_tiles(d, degree)
+    assert ft.count == _plan.num_features(d, degree)
+    assert ft.quads.shape == (4 * ft.n_tiles,) and ft.coef.shape == (16 * ft.n_tiles,)
+    feats = _quad_features(ft)
+    live = sorted((m, np.float32(c).item()) for m, c in feats if c != 0.0)
+    expect = sorted((m, np.float32(orc.inv_multinomial(m)).item()) for m in orc.monomials(d, degree))
+    assert live == expect
+    # every slot reads inside the staged row: factors up to d + 3 (the constant, then zero padding)
+    for packed in ft.quads:
+        b = (int(packed) >> 8) & 255
+        assert b % 4 == 0 and b + 3 <= ft.d + 3
+        assert max(int(packed) & 255, (int(packed) >> 16) & 255) <= ft.d
+
+
+def test_feature_tiles_padding_is_small():
+    ft = _plan.feature_tiles(64, 2)  # the long-context workload's basis
+    assert ft.n_tiles == 141  # 135 for a dense packing of 2145 features
+
+
+def test_moment_split_balances_waves():
+    opts = ((2, 2), (4, 2), (5, 2), (9, 2), (16, 1))
+    ft = _plan.feature_tiles(64, 2)
+    ms = _plan.moment_split(ft, 32, 64, opts)  # 32 heads, d = dv = 64, degree 2
+    assert (ms.fsplit, ms.csplit, ms.wave_tiles) == (8, 2, 5)
+    assert 32 * ms.fsplit * ms.csplit <= 512
+    for d, degree, bh, dv in [(64, 2, 128, 64), (16, 3, 128, 64), (32, 2, 1, 32), (4, 0, 1, 5), (40, 2, 1, 256)]:
+        ft = _plan.feature_tiles(d, degree)
+        ms = _plan.moment_split(ft, bh, dv, opts)
+        sizes = np.diff(ms.tile_off)
+        assert ms.tile_off[0] == 0 and ms.tile_off[-1] == ft.n_tiles
+        assert len(sizes) == 4 * ms.fsplit and sizes.min() >= 0 and sizes.max() <= ms.wave_tiles
+        assert ms.wave_tiles in [o for o, _ in opts] and ms.csplit == -(-dv // 32)
+        # the padded table holds every real tile exactly once, padding has coefficient 0
+        tab = ms.quads.reshape(4 * ms.fsplit, ms.wave_tiles, 4)
+        cf = ms.coef.reshape(4 * ms.fsplit, ms.wave_tiles, 16)
+        real = np.concatenate([tab[j, :sizes[j]] for j in range(len(sizes))]).reshape(-1)
+        assert np.array_equal(real, ft.quads)
+        assert all(np.all(cf[j, sizes[j]:] == 0) for j in range(len(sizes)))
+
+
+def test_library_moment_tile_options():
+    lib = _native.load_library()
+    for d, degree in [(64, 2), (16, 3), (128, 2), (100, 3)]:
+        opts = [lib.sta_moment_wave_tiles(d, degree, w) for w in range(1, 17)]
+        assert all(o >= w for o, w in zip(opts, range(1, 17)))
+        assert opts[-1] == 16
+    assert lib.sta_moment_wave_tiles(64, 2, 9) == 9
+    assert lib.sta_moment_wave_tiles(64, 2, 17) == -1
+    assert lib.sta_moment_occupancy(64, 5) == 2 and lib.sta_moment_occupancy(64, 16) == 1
+    assert lib.sta_moment_occupancy(128, 5) == 1
 
 
 # --------------------------------------------------------------------------- reference error behaviour
