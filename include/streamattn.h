@@ -57,15 +57,15 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *     holds the features x[i0] x[b+s] x[i2], s = 0..3, of [x_0..x_{D-1}, 1, 0, 0, 0]; feat_coef is the
  *     key-side coefficient 1/prod(alpha!) of each feature (0 for padding).  wave_tiles must be a count
  *     the library is built for (sta_moment_wave_tiles).
- *   ldq / ldv: row strides (elements) of q, k and of v; rows are read in 16-byte units, so ldq and ldv
- *     times the element size must be multiples of 16 (pad the rows otherwise), ldq <= 64 for d <= 64
- *     (128 above), and q, k, v must be 16-byte aligned.
+ *   q and k rows are d elements long and v rows ldv (a multiple of 32, >= dv); rows are read in
+ *     16-byte units, so d times the element size must be a multiple of 16 (pad rows with zero columns
+ *     otherwise: zero dimensions only add zero-valued features), and q, k, v must be 16-byte aligned.
  *   grid: bh * fsplit * ceil(dv/32) workgroups of 256 threads.
  *   outputs (fp32, partial over feature splits), in the layout sta_moment_partials_layout gives:
  *     low_num [BH][fsplit][rows][ld], low_den [BH][fsplit][rows], row i stored at row_offset + i.
  */
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldq, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
                 const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream);
 
 /* Smallest per-wave tile count >= want that sta_moments supports for (d, degree); -1 if none. */

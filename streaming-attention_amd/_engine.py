@@ -48,15 +48,19 @@ def _f32(a: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
 
 
-def _unit_rows(t: torch.Tensor) -> torch.Tensor:
-    """t itself when its rows are whole 16-byte units and 16-byte aligned, else a zero-padded copy."""
-    per_unit = 16 // t.element_size()
-    width = t.shape[-1]
-    if width % per_unit == 0 and t.data_ptr() % 16 == 0:
+def _unit_width(width: int, element_size: int) -> int:
+    """Smallest row length >= width that is a whole number of 16-byte units."""
+    per_unit = 16 // element_size
+    return -(-width // per_unit) * per_unit
+
+
+def _padded_rows(t: torch.Tensor, width: int) -> torch.Tensor:
+    """t itself when its rows already have `width` elements and it is 16-byte aligned, else a copy
+    zero-padded to `width` columns."""
+    if t.shape[-1] == width and t.data_ptr() % 16 == 0:
         return t
-    padded = -(-width // per_unit) * per_unit
-    out = torch.zeros(t.shape[:-1] + (padded,), device=t.device, dtype=t.dtype)
-    out[..., :width] = t
+    out = torch.zeros(t.shape[:-1] + (width,), device=t.device, dtype=t.dtype)
+    out[..., : t.shape[-1]] = t
     return out
 
 
@@ -139,10 +143,13 @@ def prefill(
     stream = _native.stream_handle(dev)
     chunk = _plan.moment_chunk(d)
 
-    ft = _plan.feature_tiles(d, degree)
-    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(d, degree))
+    # the moment kernel reads rows in 16-byte units: q/k padded with zero dimensions to a whole unit
+    # (zero dimensions only add zero-valued features), v to whole 32-column groups
+    dm = _unit_width(d, q3.element_size())
+    ft = _plan.feature_tiles(dm, degree)
+    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree))
     fsplit = ms.fsplit
-    fidx, fcoef = _on_device(("mtable", d, degree, bh, dv), dev, lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv), dev, lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
 
     raw = semantics == "taylor"
     if semantics in ("exact", "taylor"):
@@ -188,12 +195,11 @@ def prefill(
     low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
     low_den = torch.empty((bh, fsplit, lrows), device=dev, dtype=torch.float32)
 
-    # the moment kernel reads rows in 16-byte units: pad rows whose byte length is not a whole unit
-    mq, mk, mv = _unit_rows(q3), _unit_rows(k3), _unit_rows(v3)
+    mq, mk, mv = _padded_rows(q3, dm), _padded_rows(k3, dm), _padded_rows(v3, -(-dv // 32) * 32)
 
     def k1():
         st = lib.sta_moments(
-            mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, d, dv, mq.shape[-1], mv.shape[-1], degree,
+            mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
             float(scale), chunk, shift,
             fsplit, ms.wave_tiles, fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")

@@ -40,7 +40,7 @@ _SIGNATURES = {
     "sta_moment_chunk": (_i32, [_i32]),
     "sta_moments": (
         _i32,
-        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
          _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
     "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),

@@ -159,7 +159,7 @@ int sta_moment_occupancy(int d, int wave_tiles) {
 }
 
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldq, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
                 const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
@@ -167,16 +167,18 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
-  // rows are read in 16-byte units: strides must be whole units and the bases 16-byte aligned
+  // rows are read in 16-byte units: d must be a whole number of units, v rows whole 32-column groups,
+  // every base 16-byte aligned, and a head's rows addressable with 32-bit byte offsets
   const int esize = dtype == STA_F32 ? 4 : 2;
-  if (ldq < d || ldv < dv || (ldq * esize) % 16 != 0 || (ldv * esize) % 16 != 0) return STA_ERR_ARG;
-  if (ldq > (d <= 64 ? 64 : 128)) return STA_ERR_ARG;
+  if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0) return STA_ERR_ARG;
   if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
     return STA_ERR_ARG;
+  if (n * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+    return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
-  a.low_num = low_num; a.low_den = low_den; a.ldq = ldq; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
+  a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
 }
 

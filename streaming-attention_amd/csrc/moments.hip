@@ -73,8 +73,7 @@ struct MomArgs {
   float* low_num;         // [BH][fsplit][n + 2*MOM_GUARD][ldo], row r at r + MOM_GUARD
   float* low_den;         // [BH][fsplit][n + 2*MOM_GUARD]
   int ldo;                // low_num row stride: 32 * csplit
-  int ldq;                // row stride (elements) of q and k: ldq >= d, ldq * esize a multiple of 16
-  int ldv;                // row stride of v: ldv >= dv, ldv * esize a multiple of 16
+  int ldv;                // row stride of v (elements): a multiple of 32, >= dv; q and k rows are d long
   int esize;              // bytes per input element (4 or 2)
 };
 
@@ -86,14 +85,17 @@ __host__ __device__ constexpr int mom_buf_floats(bool dbig) {
 __host__ __device__ constexpr int mom_red_floats() { return MOM_WAVES * 33 * MOM_LDR; }
 // Shared-memory floats of a launch (must match the carve-up in moments_kernel).
 __host__ __device__ constexpr int mom_smem_floats(bool dbig, int nt) {
-  return 2 * mom_buf_floats(dbig) + 2 * mom_red_floats() + MOM_WAVES * nt * 16;
+  return 2 * mom_buf_floats(dbig) + 2 * mom_red_floats() + MOM_WAVES * nt * 16 + 8;
 }
 // Workgroups per compute unit an instantiation is built for (registers <= 256 and LDS <= 80 KiB for 2).
 __host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig) { return (nt <= 5 && !dbig) ? 2 : 1; }
 
-// Chunk staging in registers: 16-byte units.  The loads are unconditional (row index clamped into the
-// sequence, unit index clamped into the row), so none of them waits on another; validity and the dtype
-// conversion are applied when the units are written to LDS.
+// Chunk staging in registers: 16-byte units (4 fp32 or 8 bf16/fp16 elements).  The host guarantees
+// ldq == d with d a multiple of the unit and ldv a multiple of 32, so units never straddle the constant
+// column.  Every thread's slot geometry is fixed for the whole sequence (MomSlots); per chunk only the
+// row changes.  Loads are unconditional (rows clamped into the sequence), so none of them waits on
+// another; rows outside the sequence are zeroed when the units are written to LDS, and unused slots
+// write to a dummy LDS slot, so the staging has no branches.
 template <bool DBIG>
 struct MomStage {
   static constexpr int QV = MOM_C * (DBIG ? 128 : 64) * 4 / 16 / MOM_THREADS;  // 2 or 4 (fp32 rows)
@@ -102,39 +104,59 @@ struct MomStage {
   uint4 v;
 };
 
-__device__ __forceinline__ int64_t clamp_row(int64_t row, int64_t n) { return row < 0 ? 0 : (row >= n ? n - 1 : row); }
+template <bool DBIG>
+struct MomSlots {
+  static constexpr int QV = MomStage<DBIG>::QV;
+  int q_tok[QV];    // token of q slot j (row-major slots; clamped to the chunk)
+  uint32_t q_off[QV];  // byte offset of the unit within its row
+  int q_lds[QV];    // float offset of the unit in Qs, or the dummy slot
+  bool q_use[QV];
+  uint32_t k_off[QV];  // token = tid & 31 (token-fast slots)
+  int k_dim[QV];    // first dimension of the unit, or -1 when unused
+  uint32_t v_off;   // byte offset of the unit within its v row
+  int v_col;        // first column (within the group of 32) of the unit, or -1 when unused
+};
 
 template <bool DBIG>
-__device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomArgs& a, int64_t bh, int64_t row0, int col0) {
+__device__ __forceinline__ MomSlots<DBIG> mom_slots(const MomArgs& a, int col0, int dummy) {
+  constexpr int LDQ = mom_ldq(DBIG);
+  MomSlots<DBIG> sl;
   const int tid = threadIdx.x;
-  const int epu = 16 / a.esize;  // elements per 16-byte unit
-  const int uq = a.ldq / epu;    // units per q/k row
-  const char* qb = static_cast<const char*>(a.q) + bh * a.n * a.ldq * a.esize;
-  const char* kb = static_cast<const char*>(a.k) + bh * a.n * a.ldq * a.esize;
-  const char* vb = static_cast<const char*>(a.v) + bh * a.n * a.ldv * a.esize;
+  const int epu = 16 / a.esize;
+  const int uq = a.d / epu;  // units per q/k row
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
     const int e = tid + MOM_THREADS * j;
-    {  // q: row-major slots (coalesced)
-      const int t = e / uq;
-      const int u = e - t * uq;
-      const int64_t row = clamp_row(row0 + min(t, MOM_C - 1), a.n);
-      st.q[j] = *reinterpret_cast<const uint4*>(qb + (row * a.ldq + u * epu) * a.esize);
-    }
-    {  // k: token-fast slots (transposed LDS writes)
-      const int tok = e & (MOM_C - 1);
-      const int u = min(e >> 5, uq - 1);
-      const int64_t row = clamp_row(row0 + tok, a.n);
-      st.k[j] = *reinterpret_cast<const uint4*>(kb + (row * a.ldq + u * epu) * a.esize);
-    }
+    const int t = e / uq, u = e - t * uq;
+    sl.q_use[j] = t < MOM_C;
+    sl.q_tok[j] = min(t, MOM_C - 1);
+    sl.q_off[j] = static_cast<uint32_t>(u * 16);
+    sl.q_lds[j] = t < MOM_C ? t * LDQ + u * epu : dummy;
+    const int uk = e >> 5;
+    sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
+    sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
-  {  // v: token-fast slots over the workgroup's 32 columns
-    const int tok = tid & (MOM_C - 1);
-    const int u = tid >> 5;  // < 8
-    const int col = min(col0 + u * epu, a.ldv - epu);
-    const int64_t row = clamp_row(row0 + tok, a.n);
-    st.v = *reinterpret_cast<const uint4*>(vb + (row * a.ldv + col) * a.esize);
+  const int uv = tid >> 5;  // unit of the workgroup's 32 columns
+  sl.v_off = static_cast<uint32_t>((col0 + min(uv * epu, 32 - epu)) * a.esize);
+  sl.v_col = uv * epu < 32 ? uv * epu : -1;
+  return sl;
+}
+
+__device__ __forceinline__ int clamp_row(int row, int n) { return min(max(row, 0), n - 1); }
+
+template <bool DBIG>
+__device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
+                                         const char* qh, const char* kh, const char* vh, int row0) {
+  const uint32_t qrow = static_cast<uint32_t>(a.d * a.esize), vrow = static_cast<uint32_t>(a.ldv * a.esize);
+  const int ktok = row0 + (threadIdx.x & (MOM_C - 1));
+  const uint32_t krow = static_cast<uint32_t>(clamp_row(ktok, a.n));
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+    const uint32_t r = static_cast<uint32_t>(clamp_row(row0 + sl.q_tok[j], a.n));
+    st.q[j] = *reinterpret_cast<const uint4*>(qh + r * qrow + sl.q_off[j]);
+    st.k[j] = *reinterpret_cast<const uint4*>(kh + krow * qrow + sl.k_off[j]);
   }
+  st.v = *reinterpret_cast<const uint4*>(vh + krow * vrow + sl.v_off);
 }
 
 // The 16-byte unit u as 4 (fp32) or 8 (bf16 / fp16) floats; only f[0..16/esize) are meaningful.
@@ -164,72 +186,52 @@ __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f
 }
 
 template <bool DBIG>
-__device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomArgs& a, float* buf, int64_t row0,
-                                          int col0) {
+__device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
+                                          float* buf, int dummy_rel, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
   float* Qs = buf;
   float* Kt = Qs + MOM_C * LDQ;
   float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
+  float* dmy = buf + dummy_rel;  // 8 floats nobody reads
   const int tid = threadIdx.x;
-  const int epu = 16 / a.esize;
-  const int uq = a.ldq / epu;
-  const bool fast = a.esize == 4 && (a.d & 3) == 0;
+  const int tok = tid & (MOM_C - 1);
+  const bool tok_ok = row0 + tok >= 0 && row0 + tok < a.n;
+  const float kok = tok_ok ? 1.f : 0.f;
+  const bool wide = a.esize == 2;  // 8 elements per unit
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
-    const int e = tid + MOM_THREADS * j;
-    {
-      const int t = e / uq, u = e - t * uq;
-      const int64_t row = row0 + t;
-      const float sc = (row >= 0 && row < a.n) ? a.scale : 0.f;
-      if (t < MOM_C) {
-        float f[8];
-        unit_floats(st.q[j], a.dtype, f);
-        if (fast) {
-          if (4 * u < a.d) *reinterpret_cast<floatx4*>(Qs + t * LDQ + 4 * u) = floatx4{f[0], f[1], f[2], f[3]} * sc;
-        } else {
+    const int row = row0 + sl.q_tok[j];
+    const float sc = (sl.q_use[j] && row >= 0 && row < a.n) ? a.scale : 0.f;
+    float f[8];
+    unit_floats(st.q[j], a.dtype, f);
+    float* qd = sl.q_use[j] ? Qs + sl.q_lds[j] : dmy;
+    *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
+    if (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
+    unit_floats(st.k[j], a.dtype, f);
+    const int kd = sl.k_dim[j];
 #pragma unroll
-          for (int m = 0; m < 8; ++m) {
-            const int dim = u * epu + m;
-            if (m < epu && dim < a.d) Qs[t * LDQ + dim] = f[m] * sc;
-          }
-        }
-      }
-    }
-    {
-      const int tok = e & (MOM_C - 1), u = e >> 5;
-      const int64_t row = row0 + tok;
-      const float ok = (row >= 0 && row < a.n) ? 1.f : 0.f;
-      if (u < uq) {
-        float f[8];
-        unit_floats(st.k[j], a.dtype, f);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-          const int dim = u * epu + m;
-          if (m < epu && dim < a.d) Kt[dim * MOM_LDT + tok] = f[m] * ok;
-        }
+    for (int m = 0; m < 8; ++m) {
+      if (m < 4 || wide) {
+        float* p = kd >= 0 ? Kt + (kd + m) * MOM_LDT + tok : dmy + m;
+        *p = f[m] * kok;
       }
     }
   }
   {
-    const int tok = tid & (MOM_C - 1), u = tid >> 5;
-    const int64_t row = row0 + tok;
-    const bool ok = row >= 0 && row < a.n;
-    if (u * epu < 32) {
-      float f[8];
-      unit_floats(st.v, a.dtype, f);
+    float f[8];
+    unit_floats(st.v, a.dtype, f);
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const int c = u * epu + m;  // column within the group of 32
-        if (m < epu) Vt[c * MOM_LDT + tok] = (ok && col0 + c < a.dv) ? f[m] : 0.f;
+    for (int m = 0; m < 8; ++m) {
+      if (m < 4 || wide) {
+        float* p = sl.v_col >= 0 ? Vt + (sl.v_col + m) * MOM_LDT + tok : dmy + m;
+        *p = f[m] * kok;
       }
     }
   }
   // the constant factor: 1 on rows inside the sequence, 0 outside (zeroes every feature of the row)
   if (tid < MOM_C) {
-    const int64_t row = row0 + tid;
-    const float one = (row >= 0 && row < a.n) ? 1.f : 0.f;
-    Qs[tid * LDQ + a.d] = one;
-    Kt[a.d * MOM_LDT + tid] = one;
+    Qs[tid * LDQ + a.d] = kok;
+    Kt[a.d * MOM_LDT + tid] = kok;
   }
 }
 
@@ -264,6 +266,7 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
   extern __shared__ float smem[];
   float* red_all = smem + 2 * BUF;
   float* den_all = red_all + 2 * mom_red_floats();  // [4 waves][NT * 16]
+  const int dummy_abs = 2 * BUF + 2 * mom_red_floats() + MOM_WAVES * NT * 16;  // 8 floats, write-only
 
   const int per_head = a.fsplit * a.csplit;
   const int wg = xcd_remap(blockIdx.x, gridDim.x);
@@ -303,28 +306,33 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) st[kt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int nchunks = static_cast<int>((a.n + a.shift + MOM_C - 1) / MOM_C);
+  const int n = static_cast<int>(a.n);
+  const int nchunks = (n + a.shift + MOM_C - 1) / MOM_C;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
-  const int64_t first = -static_cast<int64_t>(a.shift);
+  const int first = -a.shift;
+  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * a.esize;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * a.esize;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * a.esize;
+  const MomSlots<DBIG> sl = mom_slots<DBIG>(a, col0, dummy_abs);
 
   // zero both chunk buffers (their padding rows / columns are never written again) and the denominators
   for (int e = tid; e < 2 * BUF; e += MOM_THREADS) smem[e] = 0.f;
   for (int e = tid; e < MOM_WAVES * NT * 16; e += MOM_THREADS) den_all[e] = 0.f;
   __syncthreads();
   MomStage<DBIG> pre;
-  mom_load<DBIG>(pre, a, bh, first, col0);
-  mom_store<DBIG>(pre, a, smem, first, col0);
+  mom_load<DBIG>(pre, sl, a, qh, kh, vh, first);
+  mom_store<DBIG>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
     const int cur = c & 1;
-    const int64_t row0 = first + static_cast<int64_t>(c) * MOM_C;
+    const int row0 = first + c * MOM_C;
     const float* Qs = smem + cur * BUF;
     const float* Kt = Qs + MOM_C * LDQ;
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
 
     // prefetch chunk c+1 (unconditional, clamped); staged after the query phase
-    mom_load<DBIG>(pre, a, bh, row0 + MOM_C, col0);
+    mom_load<DBIG>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
 
     // ---- query with the state of all previous chunks: two accumulator sets (tile parity), so 8
     //      independent MFMA chains; tile kt+1's operands are read during tile kt ----
@@ -386,7 +394,7 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
       }
     }
     // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
-    if (c + 1 < nchunks) mom_store<DBIG>(pre, a, smem + (cur ^ 1) * BUF, row0 + MOM_C, col0);
+    if (c + 1 < nchunks) mom_store<DBIG>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update: token steps outermost over all tiles (2 NT independent chains), in two halves of 4
@@ -443,8 +451,7 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
     }
     __syncthreads();
   }
-  mom_reduce_store(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase,
-                   first + static_cast<int64_t>(nchunks - 1) * MOM_C, col0);
+  mom_reduce_store(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C, col0);
 }
 
 }  // namespace sta

@@ -43,7 +43,7 @@ def test_library_exports_header_symbols():
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 1, 1, 4, 4, 2, 1.0, 64, 0, 1, 9, None, None, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, None, None, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
 
