@@ -78,16 +78,64 @@ __device__ __forceinline__ int64_t residual_start(int64_t i, int mode, int block
   return 0;
 }
 
+// Taylor truncation sum_{r<=deg} x^r / r! with the reference's term order (term = term * x / r; out =
+// out + term).  Division by 1 and 2 is exact, so degrees <= 2 need no division (bit-identical result).
+__device__ __forceinline__ float taylor_fast(float x, int deg) {
+  if (deg <= 0) return 1.0f;
+  float out = 1.0f + x;
+  if (deg == 1) return out;
+  float term = (x * x) * 0.5f;
+  out += term;
+  for (int r = 3; r <= deg; ++r) {
+    term = __fdiv_rn(term * x, static_cast<float>(r));
+    out += term;
+  }
+  return out;
+}
+
+// 4 consecutive row elements [col, col+4) as fp32 (zero beyond `width`); vector load when possible.
+__device__ __forceinline__ floatx4 load4_row(const void* base, int64_t row_off, int col, int width, int dtype,
+                                             bool vec) {
+  if (vec && col + 3 < width) {
+    if (dtype == F32) return *reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + row_off + col);
+    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + row_off + col);
+    if (dtype == BF16)
+      return floatx4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u), __uint_as_float(raw.y << 16),
+                     __uint_as_float(raw.y & 0xffff0000u)};
+    const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
+    return floatx4{static_cast<float>(h[0]), static_cast<float>(h[1]), static_cast<float>(h[2]), static_cast<float>(h[3])};
+  }
+  floatx4 r = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (col + m < width) r[m] = load_elem(base, row_off + col + m, dtype);
+  return r;
+}
+
+// Work layout: one workgroup per (head, tile of 64*RS query rows); wave w owns RS strips of 16 rows.
+// Keys are staged in LDS 64 (or 32) at a time: K row-major, V transposed ([column][key]).  For a staged
+// batch each wave computes X = K Q^T for all its (strip, 16-key subtile) pairs with interleaved MFMA
+// chains (k-step kk of lane group lg covers dimension (D/4) lg + kk, so a lane's key operands are
+// 16-byte LDS reads), evaluates the weights elementwise, and accumulates num^T += V^T P^T with the P^T
+// tile fed straight from the accumulator as the B operand.
+// Two waves per SIMD when the per-wave register arrays (queries, numerators, X and P tiles) leave room.
+__host__ __device__ constexpr int block_occupancy(int dp, int dvt, int rs) {
+  return (rs * dp / 4 + rs * dvt * 4 + 2 * rs * ((dp + dvt * 16 > 192) ? 2 : 4) * 4) <= 160 ? 2 : 1;
+}
+
 template <int DP, int DVT, int RS>
-__global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
+__global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_kernel(const BlockArgs a) {
   constexpr int KB = (DP + DVT * 16 > 192) ? 32 : 64;  // keys per LDS stage
-  constexpr int LDK = DP + 4;
-  constexpr int LDV = DVT * 16 + 4;
+  constexpr int NSUB = KB / 16;                         // 16-key subtiles per stage
+  constexpr int LDK = DP + 4;                           // = 4 (mod 64) for the 16-byte key reads
+  constexpr int DV = DVT * 16;
+  constexpr int LDVT = KB + 4;
+  constexpr int DQ = DP / 4;  // k-steps of X = K Q^T, dimensions per lane group
   constexpr int TM = 64 * RS;
   __shared__ float Kst[KB * LDK];
-  __shared__ float Vst[KB * LDV];
+  __shared__ float Vt[DV * LDVT];
   __shared__ float Wst[KB];
-  __shared__ int64_t Jst[KB];
+  __shared__ int Jst[KB];
 
   const int wg = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t bh = wg / a.n_tiles;
@@ -95,27 +143,34 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int64_t r0 = static_cast<int64_t>(t) * TM - a.shift;
+  const int n = static_cast<int>(a.n);
+  const int r0 = t * TM - a.shift;
 
   const int64_t qkbase = bh * a.n * a.d;
   const int64_t vbase = bh * a.n * a.dv;
+  const bool vec = (a.d % 4 == 0) && (a.dv % 4 == 0);
 
-  int64_t rbase[RS], myrow[RS], cs[RS], rsv[RS];
+  int rbase[RS], myrow[RS], csr[RS], rsr[RS];
   bool rvalid[RS];
-  float qB[RS][DP / 4];
+  float qB[RS][DQ];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     rbase[rs] = r0 + (wave * RS + rs) * 16;
     myrow[rs] = rbase[rs] + li;
-    rvalid[rs] = myrow[rs] >= 0 && myrow[rs] < a.n;
-    cs[rs] = chunk_start(myrow[rs], a.chunk, a.shift);
-    rsv[rs] = residual_start(myrow[rs], a.mode, a.block);
+    rvalid[rs] = myrow[rs] >= 0 && myrow[rs] < n;
+    csr[rs] = static_cast<int>(chunk_start(myrow[rs], a.chunk, a.shift));
+    const int64_t rsv = residual_start(myrow[rs], a.mode, a.block);
+    rsr[rs] = rsv > INT32_MAX ? INT32_MAX : static_cast<int>(rsv);
+    const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.d;
 #pragma unroll
-    for (int kk = 0; kk < DP / 4; ++kk) {
-      const int dim = 4 * kk + lg;
-      qB[rs][kk] = (rvalid[rs] && dim < a.d) ? load_elem(a.q, qkbase + myrow[rs] * a.d + dim, a.dtype) : 0.f;
+    for (int m = 0; m < DQ / 4; ++m) {
+      floatx4 v4 = load4_row(a.q, qoff, DQ * lg + 4 * m, a.d, a.dtype, vec);
+      if (!rvalid[rs]) v4 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e];
     }
   }
+  const int wrow_lo = r0 + wave * RS * 16, wrow_hi = wrow_lo + RS * 16 - 1;  // this wave's rows
 
   floatx4 num[RS][DVT];
   float den[RS];
@@ -126,117 +181,117 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
     for (int ct = 0; ct < DVT; ++ct) num[rs][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int64_t row_lo = r0 > 0 ? r0 : 0;
-  const int64_t row_hi = (r0 + TM < a.n ? r0 + TM : a.n) - 1;  // inclusive
+  const int row_lo = r0 > 0 ? r0 : 0;
+  const int row_hi = (r0 + TM < n ? r0 + TM : n) - 1;  // inclusive
   if (row_lo > row_hi) return;  // whole tile outside the sequence (uniform)
 
-  // One staged batch of keys: in-tile keys (is_node == false) or node items.
-  auto process = [&](bool is_node, int64_t lo, int64_t hi) {
+  // One staged batch: in-tile keys (is_node false) or the items of a node active on rows [lo, hi].
+  auto process = [&](bool is_node, int lo, int hi) {
+    floatx4 x[RS][NSUB];
 #pragma unroll
-    for (int kt = 0; kt < KB / 16; ++kt) {
-      bool act[RS];
-      const int64_t j0 = Jst[16 * kt];  // first key of the sub-tile (in-tile phase)
+    for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
-      for (int rs = 0; rs < RS; ++rs) {
-        const int64_t s_lo = rbase[rs], s_hi = rbase[rs] + 15;
-        bool on = s_hi >= 0 && s_lo < a.n;
-        if (is_node) {
-          on = on && s_hi >= lo && s_lo <= hi;
-        } else {
-          on = on && j0 >= 0 && j0 <= s_hi;
-        }
-        act[rs] = on;
-      }
-      bool any = false;
+      for (int kt = 0; kt < NSUB; ++kt) x[rs][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int rs = 0; rs < RS; ++rs) any = any || act[rs];
-      if (!any) continue;
-
-      float ka[DP / 4];
+    for (int m = 0; m < DQ / 4; ++m) {
+      floatx4 kv[NSUB];
 #pragma unroll
-      for (int kk = 0; kk < DP / 4; ++kk) ka[kk] = Kst[(16 * kt + li) * LDK + 4 * kk + lg];
-
-      float P[RS][4];
+      for (int kt = 0; kt < NSUB; ++kt)
+        kv[kt] = *reinterpret_cast<const floatx4*>(Kst + (16 * kt + li) * LDK + DQ * lg + 4 * m);
 #pragma unroll
-      for (int rs = 0; rs < RS; ++rs) {
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) P[rs][r] = 0.f;
-        if (!act[rs]) continue;
-        floatx4 x = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int kt = 0; kt < NSUB; ++kt)
 #pragma unroll
-        for (int kk = 0; kk < DP / 4; ++kk) x = mfma4(ka[kk], qB[rs][kk], x);
-        const int64_t i = myrow[rs];
+          for (int rs = 0; rs < RS; ++rs) x[rs][kt] = mfma4(kv[kt][e], qB[rs][4 * m + e], x[rs][kt]);
+    }
+    // weights, elementwise (key 16 kt + 4 lg + r, row myrow[rs])
+    floatx4 P[RS][NSUB];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int kidx = 16 * kt + 4 * lg + r;
-          const float xv = x[r] * a.scale;
-          float p = 0.f;
-          if (rvalid[rs]) {
-            if (is_node) {
-              const float w = Wst[kidx];
-              if (i >= lo && i <= hi && w != 0.f) {
-                const float e = expf(a.exp_clamp ? fminf(xv, 80.f) : xv);
-                p = (e - taylor_poly(xv, a.degree)) * w;
-              }
-            } else {
-              const int64_t j = Jst[kidx];
-              if (j >= 0 && j <= i) {
-                const bool inT = j >= cs[rs];
-                const bool inR = j >= rsv[rs];
-                if (inT || inR) {
-                  const float tp = taylor_poly(xv, a.degree);
-                  if (inR) {
-                    const float e = expf(a.exp_clamp ? fminf(xv, 80.f) : xv);
-                    p = inT ? e : e - tp;
-                  } else {
-                    p = tp;
-                  }
-                }
-              }
-            }
+    for (int kt = 0; kt < NSUB; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kidx = 16 * kt + 4 * lg + r;
+        const int j = Jst[kidx];
+        const float w = Wst[kidx];
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) {
+          const int i = myrow[rs];
+          const float xv = x[rs][kt][r] * a.scale;
+          const float ex = expf(a.exp_clamp ? fminf(xv, 80.f) : xv);
+          const float tp = taylor_fast(xv, a.degree);
+          float p;
+          if (is_node) {
+            const bool on = rvalid[rs] && i >= lo && i <= hi;
+            p = on ? (ex - tp) * w : 0.f;
+          } else {
+            const bool on = rvalid[rs] && j >= 0 && j <= i;
+            const bool inT = j >= csr[rs], inR = j >= rsr[rs];
+            const float pr = inT ? ex : ex - tp;
+            p = on ? (inR ? pr : (inT ? tp : 0.f)) : 0.f;
           }
-          P[rs][r] = p;
+          P[rs][kt][r] = p;
           den[rs] += p;
         }
       }
+    }
+    // num^T += V^T P^T
+#pragma unroll
+    for (int kt = 0; kt < NSUB; ++kt) {
 #pragma unroll
       for (int ct = 0; ct < DVT; ++ct) {
+        const floatx4 va = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * LDVT + 16 * kt + 4 * lg);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float va = Vst[(16 * kt + 4 * lg + s) * LDV + 16 * ct + li];
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs)
-            if (act[rs]) num[rs][ct] = mfma4(va, P[rs][s], num[rs][ct]);
-        }
+          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma4(va[s], P[rs][kt][s], num[rs][ct]);
       }
     }
   };
 
+  // Stage keys [first key j0 .. ) of the batch: k rows row-major, v rows transposed.  src(r) gives the
+  // source row of batch slot r (-1: empty slot, zero-filled).
+  auto stage = [&](auto src_of, bool mat) {
+    constexpr int KU = DP / 4, VU = DV / 4;
+    for (int e = tid; e < KB * KU; e += 256) {
+      const int r = e / KU, u = e - r * KU;
+      const int src = src_of(r);
+      floatx4 v4 = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (src >= 0) {
+        v4 = mat ? load4_row(a.rep_k, (bh * a.n_rep + src) * a.d, 4 * u, a.d, F32, vec)
+                 : load4_row(a.k, qkbase + static_cast<int64_t>(src) * a.d, 4 * u, a.d, a.dtype, vec);
+      }
+      *reinterpret_cast<floatx4*>(Kst + r * LDK + 4 * u) = v4;
+    }
+    for (int e = tid; e < KB * VU; e += 256) {
+      const int r = e % KB, u = e / KB;  // key-fast: conflict-light transposed writes
+      const int src = src_of(r);
+      floatx4 v4 = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (src >= 0) {
+        v4 = mat ? load4_row(a.rep_v, (bh * a.n_rep + src) * a.dv, 4 * u, a.dv, F32, vec)
+                 : load4_row(a.v, vbase + static_cast<int64_t>(src) * a.dv, 4 * u, a.dv, a.dtype, vec);
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) Vt[(4 * u + m) * LDVT + r] = v4[m];
+    }
+  };
+
   // ---- phase A: keys of the tile's own chunk / article block ----
-  int64_t kstart = chunk_start(row_lo, a.chunk, a.shift);
+  int kstart = static_cast<int>(chunk_start(row_lo, a.chunk, a.shift));
   const int64_t rs_lo = residual_start(row_lo, a.mode, a.block);
-  if (rs_lo < kstart) kstart = rs_lo;
+  if (rs_lo < kstart) kstart = static_cast<int>(rs_lo);
   if (kstart < 0) kstart = 0;
-  const int64_t kend = row_hi + 1;
-  for (int64_t kb0 = kstart; kb0 < kend; kb0 += KB) {
+  const int kend = row_hi + 1;
+  for (int kb0 = kstart; kb0 < kend; kb0 += KB) {
     __syncthreads();
-    for (int e = tid; e < KB * DP; e += 256) {
-      const int r = e / DP, col = e % DP;
-      const int64_t j = kb0 + r;
-      Kst[r * LDK + col] = (j < kend && col < a.d) ? load_elem(a.k, qkbase + j * a.d + col, a.dtype) : 0.f;
-    }
-    for (int e = tid; e < KB * DVT * 16; e += 256) {
-      const int r = e / (DVT * 16), col = e % (DVT * 16);
-      const int64_t j = kb0 + r;
-      Vst[r * LDV + col] = (j < kend && col < a.dv) ? load_elem(a.v, vbase + j * a.dv + col, a.dtype) : 0.f;
-    }
     if (tid < KB) {
-      const int64_t j = kb0 + tid;
+      const int j = kb0 + tid;
       Jst[tid] = j < kend ? j : -1;
       Wst[tid] = 1.f;
     }
+    stage([&](int r) { return kb0 + r < kend ? kb0 + r : -1; }, false);
     __syncthreads();
-    process(false, 0, 0);
+    if (kb0 <= wrow_hi) process(false, 0, 0);  // some key of the batch precedes some row of this wave
   }
 
   // ---- phase B: coreset nodes visible to some row of the tile ----
@@ -245,39 +300,25 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
     const int node = a.tile_nodes[p];
     const int32_t* meta = a.node_meta + static_cast<int64_t>(node) * NODE_META;
     const int size = meta[0];
-    const int64_t lo = meta[1], hi = meta[2];
+    const int lo = meta[1], hi = meta[2];
     const bool mat = meta[3] != 0;
     const int64_t ibase = (bh * a.n_nodes + node) * a.cap;
     for (int i0 = 0; i0 < size; i0 += KB) {
       __syncthreads();
       if (tid < KB) {
         const int it = i0 + tid;
-        Jst[tid] = it < size ? static_cast<int64_t>(a.node_src[ibase + it]) : -1;
+        Jst[tid] = it < size ? a.node_src[ibase + it] : -1;
         Wst[tid] = it < size ? a.node_w[ibase + it] : 0.f;
       }
       __syncthreads();
-      for (int e = tid; e < KB * DP; e += 256) {
-        const int r = e / DP, col = e % DP;
-        const int64_t src = Jst[r];
-        float val = 0.f;
-        if (src >= 0 && col < a.d)
-          val = mat ? a.rep_k[(bh * a.n_rep + src) * a.d + col] : load_elem(a.k, qkbase + src * a.d + col, a.dtype);
-        Kst[r * LDK + col] = val;
-      }
-      for (int e = tid; e < KB * DVT * 16; e += 256) {
-        const int r = e / (DVT * 16), col = e % (DVT * 16);
-        const int64_t src = Jst[r];
-        float val = 0.f;
-        if (src >= 0 && col < a.dv)
-          val = mat ? a.rep_v[(bh * a.n_rep + src) * a.dv + col] : load_elem(a.v, vbase + src * a.dv + col, a.dtype);
-        Vst[r * LDV + col] = val;
-      }
+      stage([&](int r) { return Jst[r]; }, mat);
       __syncthreads();
-      process(true, lo, hi);
+      if (hi >= wrow_lo && lo <= wrow_hi) process(true, lo, hi);
     }
   }
 
   // ---- epilogue: add the moment partials, normalise, store ----
+  const bool raw = a.out_den != nullptr;
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     float dsum = den[rs];
@@ -287,19 +328,21 @@ __global__ __launch_bounds__(256) void block_attn_kernel(const BlockArgs a) {
     const int64_t i = myrow[rs];
     float lowd = 0.f;
     for (int f = 0; f < a.fsplit; ++f) lowd += a.low_den[(bh * a.fsplit + f) * a.low_rows + a.low_off + i];
-    const bool raw = a.out_den != nullptr;
     if (raw && lg == 0) a.out_den[bh * a.n + i] = lowd + dsum;
     const float dn = fmaxf(lowd + dsum, a.eps);
 #pragma unroll
     for (int ct = 0; ct < DVT; ++ct) {
+      const int c0 = 16 * ct + 4 * lg;
+      if (c0 >= a.dv) continue;
+      floatx4 lown = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int f = 0; f < a.fsplit; ++f)
+        lown += *reinterpret_cast<const floatx4*>(
+            a.low_num + ((bh * a.fsplit + f) * a.low_rows + a.low_off + i) * a.low_ld + c0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int col = 16 * ct + 4 * lg + r;
+        const int col = c0 + r;
         if (col < a.dv) {
-          float lown = 0.f;
-          for (int f = 0; f < a.fsplit; ++f)
-            lown += a.low_num[((bh * a.fsplit + f) * a.low_rows + a.low_off + i) * a.low_ld + col];
-          const float numv = num[rs][ct][r] + lown;
+          const float numv = num[rs][ct][r] + lown[r];
           if (raw)
             static_cast<float*>(a.out)[(bh * a.n + i) * a.dv + col] = numv;
           else
