@@ -78,20 +78,25 @@ __device__ __forceinline__ int64_t residual_start(int64_t i, int mode, int block
   return 0;
 }
 
-// Taylor truncation sum_{r<=deg} x^r / r! with the reference's term order (term = term * x / r; out =
-// out + term).  Division by 1 and 2 is exact, so degrees <= 2 need no division (bit-identical result).
-__device__ __forceinline__ float taylor_fast(float x, int deg) {
-  if (deg <= 0) return 1.0f;
-  float out = 1.0f + x;
-  if (deg == 1) return out;
-  float term = (x * x) * 0.5f;
-  out += term;
-  for (int r = 3; r <= deg; ++r) {
-    term = __fdiv_rn(term * x, static_cast<float>(r));
-    out += term;
-  }
-  return out;
+// Taylor truncation sum_{r<=deg} x^r / r!, deg <= 3, without branches or selects: c1..c3 are 1 for the
+// terms the degree includes, else 0 (uniform).  Degrees <= 2 reproduce the reference's term order and
+// rounding exactly (1 + x, then + x*x/2 with exact division by 2; a zero coefficient adds exactly 0);
+// the cubic term multiplies by 1/3 instead of dividing (within 1 ulp of the division).
+struct TaylorCoef {
+  float c1, c2, c3;
+};
+__host__ __device__ inline TaylorCoef taylor_coef(int deg) {
+  return TaylorCoef{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 1.f : 0.f, deg >= 3 ? 1.f : 0.f};
 }
+__device__ __forceinline__ float taylor_fast(float x, const TaylorCoef& c) {
+  const float t2 = (x * x) * 0.5f;
+  const float t3 = (t2 * x) * 0.333333343f;
+  return fmaf(t3, c.c3, fmaf(t2, c.c2, fmaf(x, c.c1, 1.0f)));
+}
+
+// exp(x) as 2^(x log2 e) on the hardware exp2 (about 1 ulp; the fused residual needs the difference
+// exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding).
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
 
 // 4 consecutive row elements [col, col+4) as fp32 (zero beyond `width`); vector load when possible.
 __device__ __forceinline__ floatx4 load4_row(const void* base, int64_t row_off, int col, int width, int dtype,
@@ -162,12 +167,12 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     const int64_t rsv = residual_start(myrow[rs], a.mode, a.block);
     rsr[rs] = rsv > INT32_MAX ? INT32_MAX : static_cast<int>(rsv);
     const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.d;
+    const float qs = rvalid[rs] ? a.scale : 0.f;  // the logits come out scaled
 #pragma unroll
     for (int m = 0; m < DQ / 4; ++m) {
-      floatx4 v4 = load4_row(a.q, qoff, DQ * lg + 4 * m, a.d, a.dtype, vec);
-      if (!rvalid[rs]) v4 = floatx4{0.f, 0.f, 0.f, 0.f};
+      const floatx4 v4 = load4_row(a.q, qoff, DQ * lg + 4 * m, a.d, a.dtype, vec);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e];
+      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e] * qs;
     }
   }
   const int wrow_lo = r0 + wave * RS * 16, wrow_hi = wrow_lo + RS * 16 - 1;  // this wave's rows
@@ -181,6 +186,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     for (int ct = 0; ct < DVT; ++ct) num[rs][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
+  const TaylorCoef tc = taylor_coef(a.degree);
+  const float xmax = a.exp_clamp ? 80.f : __builtin_huge_valf();  // exp(min(x, 80)) in the Triton mode
   const int row_lo = r0 > 0 ? r0 : 0;
   const int row_hi = (r0 + TM < n ? r0 + TM : n) - 1;  // inclusive
   if (row_lo > row_hi) return;  // whole tile outside the sequence (uniform)
@@ -217,18 +224,18 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
           const int i = myrow[rs];
-          const float xv = x[rs][kt][r] * a.scale;
-          const float ex = expf(a.exp_clamp ? fminf(xv, 80.f) : xv);
-          const float tp = taylor_fast(xv, a.degree);
+          const float xv = x[rs][kt][r];
+          const float ex = exp_fast(fminf(xv, xmax));
+          const float tp = taylor_fast(xv, tc);
           float p;
           if (is_node) {
             const bool on = rvalid[rs] && i >= lo && i <= hi;
             p = on ? (ex - tp) * w : 0.f;
           } else {
+            // own chunk (j >= cs): Taylor part; article block (j >= rs): residual; both: exp
             const bool on = rvalid[rs] && j >= 0 && j <= i;
-            const bool inT = j >= csr[rs], inR = j >= rsr[rs];
-            const float pr = inT ? ex : ex - tp;
-            p = on ? (inR ? pr : (inT ? tp : 0.f)) : 0.f;
+            const float pr = (j >= rsr[rs] ? ex - tp : 0.f) + (j >= csr[rs] ? tp : 0.f);
+            p = on ? pr : 0.f;
           }
           P[rs][kt][r] = p;
           den[rs] += p;
