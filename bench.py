@@ -55,6 +55,18 @@ def make_inputs(batch, heads, n, d, dv, seed):
     return q / qn * rq, k / kn * rk, v
 
 
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of
+    this workload (calibrated against a copy of known size), or None when there is none."""
+    path = ROOT / "profiles" / f"{workload}_hbm_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith(f"{kernel} traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(q, k, v, w):
     """Reference CPU fast path on one head (bounded sample), via the oracle."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -86,6 +98,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seq-len", type=int, default=WORKLOAD["seq_len"])
     ap.add_argument("--heads", type=int, default=WORKLOAD["heads"])
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy a MIB-MiB fp32 tensor 3 times (calibration kernel for the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (heads shard with no "
@@ -94,6 +108,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe * (1 << 18), device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "copies": 3}))
+        return 0
 
     import _engine
     import _plan
@@ -168,7 +191,7 @@ def main() -> int:
             "peak": MFMA_FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic(w["workload"], "moments_kernel"),
             "algorithmic_flops_per_launch": mom_flops,
             "avg_launch_ms": mom_ms,
         },
