@@ -14,6 +14,13 @@ fused residual + normalisation K2/K4).  Prints one JSON line:
   a bounded sample of one head on this host's cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+`--workload decode_levels_c5` measures streaming decode instead: 64 x 32 = 2048 streams, each holding the
+state after a 32768-token prefix (moments plus merge-and-reduce levels, block 256), d = dv = 64,
+degree 2, scale 1/8, bf16 inputs q, k, v ~ N(0,1)/8 (generated on the GPU); one step = update(k, v) +
+query(q) for every stream, block completions (compress + merges) included.  value = stream-tokens/s;
+roofline of the moment-state read (HBM); CPU baseline = the reference's per-token streaming object
+restated in oracle/, one stream with the same state sizes.
 """
 
 from __future__ import annotations
@@ -36,6 +43,9 @@ import torch  # noqa: E402
 WORKLOAD = dict(workload="prefill_levels_c3", batch=1, heads=32, seq_len=65536, d=64, dv=64, degree=2, block=256,
                 scale=0.125, compressor="sorted_pair", semantics="merge-and-reduce levels", data="unit_ball r=1",
                 dtype="fp32", seed=0)
+
+DECODE = dict(workload="decode_levels_c5", batch=64, heads=32, prefix=32768, d=64, dv=64, degree=2, block=256,
+              scale=0.125, compressor="sorted_pair", data="N(0,1)/8", dtype="bf16", seed=0)
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
@@ -93,14 +103,22 @@ def cpu_baseline(q, k, v, w):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 10; decode 256)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps first (default 2; decode 8)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seq-len", type=int, default=WORKLOAD["seq_len"])
     ap.add_argument("--heads", type=int, default=WORKLOAD["heads"])
+    ap.add_argument("--workload", default=WORKLOAD["workload"], choices=[WORKLOAD["workload"], DECODE["workload"]])
+    ap.add_argument("--streams", type=int, default=DECODE["batch"] * DECODE["heads"], help="decode streams")
+    ap.add_argument("--prefix", type=int, default=DECODE["prefix"], help="decode prefix tokens")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB fp32 tensor 3 times (calibration kernel for the HBM byte counters)")
     args = ap.parse_args()
+    decode = args.workload == DECODE["workload"]
+    if args.steps is None:
+        args.steps = 256 if decode else 10
+    if args.warmup is None:
+        args.warmup = 8 if decode else 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (heads shard with no "
               f"communication across GPUs; see DESIGN.md)", file=sys.stderr)
@@ -117,6 +135,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "copies": 3}))
         return 0
+
+    if args.workload == DECODE["workload"]:
+        return run_decode(args)
 
     import _engine
     import _plan
@@ -202,6 +223,116 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print(f"[bench] timing CPU baseline", file=sys.stderr, flush=True)
         cb = cpu_baseline(q, k, v, w)
+        line["cpu_baseline"] = cb
+        line["speedup_vs_cpu_baseline"] = value / cb["value"]
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+def run_decode(args) -> int:
+    """Streaming decode throughput (see the module docstring)."""
+    import _engine
+    import _plan
+    import streaming_taylor_coreset_attention as stc
+
+    w = dict(DECODE, prefix=args.prefix)
+    s_total, d, dv = args.streams, w["d"], w["dv"]
+    w["streams"] = s_total
+    dev = torch.device("cuda:0")
+    st = stc.ArticleStreamingAttention(d, dv, degree=w["degree"], block_size=w["block"], scale=w["scale"],
+                                       compressor=w["compressor"], device=dev, dtype=torch.bfloat16, seed=w["seed"],
+                                       streams=s_total)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(w["seed"])
+
+    def draw(*shape):
+        return (torch.randn(*shape, generator=gen, device=dev) * 0.125).to(torch.bfloat16)
+
+    print(f"[bench] decode: building the state of {s_total} streams after {w['prefix']} tokens", file=sys.stderr,
+          flush=True)
+    t0 = time.perf_counter()
+    chunk = 4096
+    for lo in range(0, w["prefix"], chunk):
+        n = min(chunk, w["prefix"] - lo)
+        st.extend(draw(s_total, n, d), draw(s_total, n, dv))
+    torch.cuda.synchronize()
+    t_prefix = time.perf_counter() - t0
+    total = args.warmup + args.steps
+    xs = draw(total, 3, s_total, d)
+    t0 = time.perf_counter()
+    st._st.reserve_draws(total)
+    t_draws = time.perf_counter() - t0
+    print(f"[bench] decode: prefix {t_prefix:.1f}s, draws {t_draws:.1f}s; warmup", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        st.step(xs[i, 0], xs[i, 1], xs[i, 2])
+    torch.cuda.synchronize()
+    timer = _engine.KernelTimer()
+    st._st.timer = timer
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for i in range(args.warmup, total):
+        st.step(xs[i, 0], xs[i, 1], xs[i, 2])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    st._st.timer = None
+    ms_step = start.elapsed_time(end) / args.steps
+    per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_launch": round(tot / cnt, 5)}
+                  for name, (tot, cnt) in timer.totals_ms().items()}
+    f = _plan.num_features(d, w["degree"])
+    state_bytes = s_total * f * (dv + 1) * 4  # algorithmic: the moment state is read once per step
+    mom_ms = per_kernel["decode_moments"]["ms_total"] / per_kernel["decode_moments"]["launches"]
+    achieved = state_bytes / (mom_ms * 1e-3) / 1e9
+    value = s_total / (ms_step * 1e-3)  # every stream advances one token per step
+    line = {
+        "metric": "decode stream-tokens/sec (update + query per stream), prefix 32K, d=64 deg-2; % of HBM roofline",
+        "value": value,
+        "unit": "stream-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 inputs, fp32 state",
+        "data": "synthetic",
+        "config": w,
+        "roofline": {
+            "kernel": "decode_moments_kernel (moment-state read of every stream)",
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": measured_traffic(w["workload"], "decode_moments_kernel"),
+            "algorithmic_bytes_per_launch": state_bytes,
+            "avg_launch_ms": mom_ms,
+        },
+        "kernels": per_kernel,
+        "block_completions_timed": (w["prefix"] + total) // w["block"] - (w["prefix"] + args.warmup) // w["block"],
+        "host_prefix_build_s": round(t_prefix, 3),
+        "host_draws_s": round(t_draws, 3),
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import reference_cpu as oracle
+
+        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+        steps = int(os.environ.get("STA_CPU_DECODE_STEPS", "256"))
+        print(f"[bench] timing CPU baseline ({steps} steps of one stream)", file=sys.stderr, flush=True)
+        t = oracle.time_decode_sample(dim=d, value_dim=dv, degree=w["degree"], block=w["block"], scale=w["scale"],
+                                      prefix=w["prefix"], steps=steps, seed=w["seed"])
+        cb = {"value": 1.0 / t["s_per_step"], "unit": "stream-tokens/s", "cores": threads, "kind": "port",
+              "sample": (f"reference ArticleStreamingAttention update+query restated in oracle/ (per-token torch "
+                         f"ops), one stream with the state sizes after a {w['prefix']}-token prefix, {steps} steps "
+                         f"(block completions included); the reference runs streams one after another")}
         line["cpu_baseline"] = cb
         line["speedup_vs_cpu_baseline"] = value / cb["value"]
     else:

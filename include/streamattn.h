@@ -79,6 +79,76 @@ int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* r
 int sta_moment_occupancy(int d, int wave_tiles);
 
 /*
+ * Persistent moment state update (the decode state; K1's update without the query):
+ *   state_num[h][f][c] += sum_{j<n} phi_k(k_j)[f] v_j[c],  state_den[h][f] += sum_{j<n} phi_k(k_j)[f]
+ * for rows [0, n) of every head h (head h starts head_rows rows after head h-1 in k and v).
+ * Replaces TaylorMomentSketch.update (streaming_taylor_coreset_attention.py:265-280), applied to a whole
+ * block of tokens at once (the block completion of a decode step, or a prompt).
+ *   Feature table as for sta_moments (wave_tiles tiles of 4 quads per wave) plus feat_rows
+ *   [fsplit][4][wave_tiles][16]: the state row of every feature slot in the reference's feature order
+ *   (degree 0, 1, ..., each in combinations_with_replacement order), -1 for padding slots.
+ *   state_num [BH][n_feat][ld] with ld = 32*ceil(dv/32), state_den [BH][n_feat], fp32, accumulated in
+ *   place.  k / v row rules as for sta_moments (16-byte units, ldv a multiple of 32).
+ */
+int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
+                          int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
+                          const float* feat_coef, const int32_t* feat_rows, int n_feat, float* state_num,
+                          float* state_den, void* stream);
+
+/*
+ * Streaming decode (K5) for S streams in lockstep: ArticleStreamingAttention.update / query
+ * (streaming_taylor_coreset_attention.py:576-609).  The state of stream s (fp32, caller-owned):
+ *   moments of the tokens of completed blocks   state_num [S][F][ldv], state_den [S][F] (reference order)
+ *   the current block's tokens (the buffer)     buf_k [S][block][dk], buf_v [S][block][ldv]
+ *   level coresets                              lev_k [S][L][m][dk], lev_v [S][L][m][ldv], lev_w [S][L][m],
+ *                                               lev_pos [S][L][m] (sequence positions), m = ceil(block/2)
+ * with zero padding columns.  A query returns low + exp over the buffered tokens + weighted exp_{>t}
+ * over the occupied levels' items, the reference's low + tail regrouped (the buffered tokens' Taylor
+ * part lives in their exact exponential instead of the moments).
+ */
+
+/* Row lengths of the decode buffers: dk = 4*ceil(d/4), ldv = 32*ceil(dv/32). */
+int sta_decode_layout(int d, int dv, int* dk, int* ldv);
+
+/*
+ * Moment part of a decode query: part_num[s][p][c] = sum over features f of split p of
+ * phi_q(scale*q_s)[f] state_num[s][f][c] (part_den likewise), splits = feature splits per stream.
+ * feat_index [F]: factors of feature f packed i0 | i1 << 8 | i2 << 16 into x = [scale*q, 1] (index d is
+ * the constant 1).  Replaces TaylorMomentSketch.query (streaming_taylor_coreset_attention.py:282-296).
+ */
+int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv, float scale, const float* state_num,
+                       const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* part_num,
+                       float* part_den, void* stream);
+
+/*
+ * Buffer append and query of a decode step.  flags: 1 APPEND (write k, v [S][d|dv] into buffer slot
+ * buf_len), 2 CURRENT (the appended token also counts as a buffered token of this query), 4 QUERY
+ * (out[s] = (low + tail numerators) / max(den, eps) in out_dtype; low from sta_decode_moments'
+ * partials).  level_mask: bit l set = level l occupied (the completed-block counter).  stats [S][4]
+ * (optional): denominator, the reference's low and tail denominators, coreset item count.
+ * Replaces MergeReduceCoreset.append / items (streaming_taylor_coreset_attention.py:376-394, :469-490)
+ * and the query tail and normalisation of ArticleStreamingAttention.query (:581-609).
+ */
+int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
+                    int degree, float scale, float eps, int flags, float* buf_k, float* buf_v, int block, int buf_len,
+                    const float* lev_k, const float* lev_v, const float* lev_w, int n_levels, int level_size,
+                    uint64_t level_mask, const float* part_num, const float* part_den, int splits, void* out,
+                    int out_dtype, float* stats, void* stream);
+
+/*
+ * Block completion: compress the full buffer (call 0) and merge cat(level i-1, previous output) for
+ * calls i = 1 .. n_calls-1 (the occupied levels below the counter's lowest zero bit), writing the
+ * result as level n_calls-1.  methods [n_calls] (1 sorted_pair, 2 permutation) and the draws dirs
+ * [S][n_calls][d], unif [S][n_calls][max_in/2], perms [S][n_calls][max_in] as for sta_compress_nodes;
+ * pos0 = sequence position of buffer row 0.  Replaces MergeReduceCoreset.append's compression and
+ * _insert_level (streaming_taylor_coreset_attention.py:387-467).
+ */
+int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, const float* buf_v, int block, int pos0,
+                        float* lev_k, float* lev_v, float* lev_w, int32_t* lev_pos, int n_levels, int level_size,
+                        int n_calls, const int32_t* methods, const float* dirs, const float* unif,
+                        const int32_t* perms, int max_in, void* stream);
+
+/*
  * Block compressor for one batch of coreset nodes (K3), all heads at once.
  * Replaces _compress_one_completed_block (fast_article_attention.py:312-361) for the flat block coreset
  * and MergeReduceCoreset._compress* (streaming_taylor_coreset_attention.py:413-467) for level merges.

@@ -507,3 +507,139 @@ def make_data(shape_lead: Tuple[int, ...], n: int, d: int, dv: int, *, radius: f
 def rel_l2(a: Tensor, b: Tensor) -> float:
     a64, b64 = a.double().cpu(), b.double().cpu()
     return float(torch.linalg.vector_norm(a64 - b64) / torch.clamp(torch.linalg.vector_norm(b64), min=1e-300))
+
+
+# ----------------------------------------------------------------------------- streaming object
+
+class StreamingAttentionCPU:
+    """Per-token restatement of ArticleStreamingAttention (streaming_taylor_coreset_attention.py:523-616)
+    on the CPU in the reference's op order: TaylorMomentSketch.update / query (:265-296) with per-degree
+    gathered monomials, MergeReduceCoreset.append / _insert_level / _compress (:376-467) with torch's
+    `keys @ direction` and argsort, and the query tail over items() (:581-609).  It is the decode CPU
+    baseline (one stream, one token per call, as the reference runs) and a token-by-token checker."""
+
+    def __init__(self, dim: int, value_dim: int, *, degree: int, block: int, scale: float,
+                 compressor: str = "sorted_pair", seed: int = 0, eps: float = 1e-12) -> None:
+        self.dim, self.value_dim, self.degree, self.block = dim, value_dim, degree, block
+        self.scale, self.compressor, self.eps = float(scale), compressor, eps
+        self.idx: List[Optional[Tensor]] = [None]
+        self.coef: List[Tensor] = [torch.ones(1)]
+        for l in range(1, degree + 1):
+            combos = list(itertools.combinations_with_replacement(range(dim), l))
+            self.idx.append(torch.tensor(combos, dtype=torch.long))
+            self.coef.append(torch.tensor([inv_multinomial(c) for c in combos], dtype=torch.float32))
+        self.den = [torch.zeros(c.shape[0]) for c in self.coef]
+        self.num = [torch.zeros(c.shape[0], value_dim) for c in self.coef]
+        self.g = torch.Generator(device="cpu")
+        self.g.manual_seed(int(seed))
+        self.buf_k: List[Tensor] = []
+        self.buf_v: List[Tensor] = []
+        self.levels: List[Optional[Tuple[Tensor, Tensor, Tensor]]] = []
+        self.length = 0
+
+    def _feats(self, x: Tensor, key_side: bool) -> List[Tensor]:
+        out = [torch.ones(1)]
+        for l in range(1, self.degree + 1):
+            m = x[self.idx[l]].prod(dim=-1)
+            out.append(m * self.coef[l] if key_side else m)
+        return out
+
+    def _compress(self, keys: Tensor, values: Tensor, weights: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+        n = weights.numel()
+        if self.compressor == "none" or n <= 1:
+            return keys, values, weights
+        method, dvec, u, perm = draw_for_call(self.g, n, self.dim, self.compressor)
+        if method == "perm":
+            m = (n + 1) // 2
+            p = torch.from_numpy(perm[:m]).long()
+            return keys[p], values[p], weights[p] * (float(n) / float(m))
+        order = torch.argsort(keys @ torch.from_numpy(dvec))
+        keys, values, weights = keys[order], values[order], weights[order]
+        pc = n // 2
+        wa, wb = weights[0: 2 * pc: 2], weights[1: 2 * pc: 2]
+        wsum = wa + wb
+        choose_a = torch.from_numpy(u) < wa / torch.clamp(wsum, min=1e-30)
+        nk = torch.where(choose_a[:, None], keys[0: 2 * pc: 2], keys[1: 2 * pc: 2])
+        nv = torch.where(choose_a[:, None], values[0: 2 * pc: 2], values[1: 2 * pc: 2])
+        nw = wsum
+        if n % 2 == 1:
+            nk, nv, nw = torch.cat([nk, keys[-1:]]), torch.cat([nv, values[-1:]]), torch.cat([nw, weights[-1:]])
+        return nk, nv, nw
+
+    def update(self, k: Tensor, v: Tensor) -> None:
+        for l, f in enumerate(self._feats(k, True)):
+            self.den[l].add_(f)
+            self.num[l].add_(f[:, None] * v[None, :])
+        self.buf_k.append(k.clone())
+        self.buf_v.append(v.clone())
+        self.length += 1
+        if len(self.buf_k) >= self.block:
+            keys, values = torch.stack(self.buf_k), torch.stack(self.buf_v)
+            self.buf_k.clear()
+            self.buf_v.clear()
+            blk = self._compress(keys, values, torch.ones(keys.shape[0]))
+            level = 0
+            while True:
+                while len(self.levels) <= level:
+                    self.levels.append(None)
+                if self.levels[level] is None:
+                    self.levels[level] = blk
+                    break
+                old = self.levels[level]
+                self.levels[level] = None
+                blk = self._compress(torch.cat([old[0], blk[0]]), torch.cat([old[1], blk[1]]), torch.cat([old[2], blk[2]]))
+                level += 1
+
+    def query(self, q: Tensor) -> Tensor:
+        den = torch.zeros(())
+        num = torch.zeros(self.value_dim)
+        for l, f in enumerate(self._feats(q * self.scale, False)):
+            den = den + torch.dot(self.den[l], f)
+            num = num + f @ self.num[l]
+        blocks = []
+        if self.buf_k:
+            blocks.append((torch.stack(self.buf_k), torch.stack(self.buf_v), torch.ones(len(self.buf_k))))
+        blocks += [b for b in self.levels if b is not None and b[2].numel() > 0]
+        if blocks:
+            keys = torch.cat([b[0] for b in blocks])
+            vals = torch.cat([b[1] for b in blocks])
+            w = torch.cat([b[2] for b in blocks])
+            logits = self.scale * (keys @ q)
+            r = w * _residual(logits, self.degree)
+            den = den + r.sum()
+            num = num + r @ vals
+        return num / torch.clamp(den, min=self.eps)
+
+
+def time_decode_sample(*, dim: int, value_dim: int, degree: int, block: int, scale: float, prefix: int, steps: int,
+                       seed: int = 0) -> Dict[str, float]:
+    """Seconds per update + query step of the reference's streaming object (StreamingAttentionCPU) for
+    ONE stream whose state has the sizes it has after `prefix` tokens: moments filled, the levels of
+    the counter prefix // block occupied with block/2-item coresets, prefix % block buffered tokens
+    (the per-step cost depends on these sizes, not on the values).  The timed steps include every
+    block completion (compress + merges) they reach."""
+    import time as _time
+
+    g = torch.Generator().manual_seed(seed)
+    st = StreamingAttentionCPU(dim, value_dim, degree=degree, block=block, scale=scale, seed=seed)
+    for l in range(len(st.den)):
+        st.den[l] = torch.randn(st.den[l].shape, generator=g)
+        st.num[l] = torch.randn(st.num[l].shape, generator=g)
+    c = prefix // block
+    m = (block + 1) // 2
+    for lev in range(c.bit_length()):
+        st.levels.append(None)
+        if (c >> lev) & 1:
+            st.levels[lev] = (torch.randn(m, dim, generator=g) * 0.125, torch.randn(m, value_dim, generator=g),
+                              torch.full((m,), float(2 ** (lev + 1))))
+    for _ in range(prefix % block):
+        st.buf_k.append(torch.randn(dim, generator=g) * 0.125)
+        st.buf_v.append(torch.randn(value_dim, generator=g))
+    st.length = prefix
+    xs = torch.randn(steps, 3, max(dim, value_dim), generator=g) * 0.125
+    t0 = _time.perf_counter()
+    for i in range(steps):
+        st.update(xs[i, 1, :dim], xs[i, 2, :value_dim])
+        st.query(xs[i, 0, :dim])
+    dt = _time.perf_counter() - t0
+    return {"s_per_step": dt / steps, "steps": steps, "prefix": prefix}

@@ -1,0 +1,429 @@
+"""Batched streaming decode state on one ROCm device: S independent streams (stream s seeded seed + s)
+advancing in lockstep, the state of the reference's ArticleStreamingAttention
+(streaming_taylor_coreset_attention.py:523-616) for each of them.
+
+Device state (fp32, see csrc/decode.hip):
+  state_num [S, F, ldv], state_den [S, F]   moments of the tokens of completed blocks, reference order
+  buf_k [S, cap, dk], buf_v [S, cap, ldv]   the tokens of the current block (cap = block; for
+                                            compressor "none" every token, cap grows)
+  lev_k [S, L, m, dk], lev_v [S, L, m, ldv], lev_w [S, L, m], lev_pos [S, L, m]   level coresets
+Host state: length (tokens per stream), blocks (completed blocks = the level-occupancy counter),
+buf_len, and one torch CPU generator per stream that the compress calls draw from in the reference's
+order (randn(d) + rand(n//2) per sorted_pair call, randperm(n) for n <= 2 or "random").
+
+Per decode step (update then query of one token per stream): sta_decode_moments (state read) and
+sta_decode_tail (append + buffer / level items + combine).  When the token completes a block:
+sta_moment_accumulate (buffer -> state) and sta_decode_compress (buffer -> level 0 and the merge
+cascade), then the query.
+"""
+
+from __future__ import annotations
+
+from collections import deque
+from dataclasses import dataclass
+from typing import Deque, Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+import _native
+import _plan
+
+M_SORTED_PAIR, M_PERM = _plan.METHOD_SORTED_PAIR, _plan.METHOD_PERM
+
+
+@dataclass
+class _CompletionDraws:
+    blocks_before: int
+    n_calls: int
+    methods: torch.Tensor  # int32 [n_calls]
+    dirs: torch.Tensor  # float32 [S, n_calls, d]
+    unif: torch.Tensor  # float32 [S, n_calls, max_in // 2]
+    perms: torch.Tensor  # int32 [S, n_calls, max_in]
+
+
+class DecodeState:
+    def __init__(self, streams: int, dim: int, value_dim: int, *, degree: int, block: int, scale: float,
+                 compressor: str, seed: int, device: torch.device, eps: float = 1e-12) -> None:
+        if streams <= 0:
+            raise ValueError("streams must be positive")
+        if dim <= 0 or value_dim <= 0:
+            raise ValueError("dim and value_dim must be positive")
+        if block < 2:
+            raise ValueError("block_size must be at least 2")
+        lim = _native.limits()
+        if dim > lim["max_d"] or value_dim > lim["max_dv"]:
+            raise ValueError(f"the HIP kernels support D <= {lim['max_d']} and Dv <= {lim['max_dv']}")
+        if degree < 0:
+            raise ValueError("degree must be non-negative")
+        if degree > lim["max_degree"]:
+            raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+        if device.type != "cuda":
+            raise ValueError("the HIP decode state lives on a ROCm GPU device")
+        self.S, self.d, self.dv = int(streams), int(dim), int(value_dim)
+        self.degree, self.block, self.scale = int(degree), int(block), float(scale)
+        self.compressor, self.seed, self.eps = str(compressor), int(seed), float(eps)
+        self.device = device
+        self.exact = self.compressor == "none"
+        self.m = (self.block + 1) // 2
+        if not self.exact and max(self.block, 2 * self.m) > lim["max_compress_in"]:
+            raise ValueError(f"block_size {block} exceeds the HIP compressor's {lim['max_compress_in']} items")
+        self.dk, self.ldv = _native.decode_layout(self.d, self.dv)
+        self.F = _plan.num_features(self.d, self.degree)
+        self.lib = _native.lib()
+
+        dev, S = device, self.S
+        f32 = dict(device=dev, dtype=torch.float32)
+        self.state_num = torch.zeros((S, self.F, self.ldv), **f32)
+        self.state_den = torch.zeros((S, self.F), **f32)
+        self.cap = self.block
+        self.buf_k = torch.zeros((S, self.cap, self.dk), **f32)
+        self.buf_v = torch.zeros((S, self.cap, self.ldv), **f32)
+        self.L = 0
+        self.lev_k = torch.zeros((S, 1, 1, self.dk), **f32)
+        self.lev_v = torch.zeros((S, 1, 1, self.ldv), **f32)
+        self.lev_w = torch.zeros((S, 1, 1), **f32)
+        self.lev_pos = torch.zeros((S, 1, 1), device=dev, dtype=torch.int32)
+        self.length = 0
+        self.blocks = 0
+        self.buf_len = 0
+        self.num_compressions = 0
+        self._gens = [torch.Generator(device="cpu") for _ in range(S)]
+        for s, g in enumerate(self._gens):
+            g.manual_seed(self.seed + s)
+        self._draws: Deque[_CompletionDraws] = deque()
+
+        # moment query: feature factors in reference order, splits to fill the GPU
+        self.findex = torch.from_numpy(_plan.feature_index(self.d, self.degree).view(np.int32)).to(dev)
+        self.splits = max(1, min(-(-2048 // S), self.F // 64 if self.F >= 64 else 1))
+        self.part_num = torch.zeros((S, self.splits, self.ldv), **f32)
+        self.part_den = torch.zeros((S, self.splits), **f32)
+        self._acc_tables: Dict[int, tuple] = {}
+        self.timer = None  # optional _engine.KernelTimer: HIP events around every launch
+
+    def _launch(self, name: str, fn) -> None:
+        if self.timer is None:
+            fn()
+        else:
+            self.timer.wrap(name, fn)
+
+    # ------------------------------------------------------------------ helpers
+    def _stream(self) -> int:
+        return _native.stream_handle(self.device)
+
+    def _acc_table(self, width: int):
+        """Moment-accumulate tables for rows `width` elements long: (split, quads, coef, rows)."""
+        if width not in self._acc_tables:
+            ft = _plan.feature_tiles(width, self.degree)
+            ms = _plan.moment_split(ft, self.S, self.dv, _native.moment_wave_tile_options(width, self.degree))
+            rows = _plan.split_state_rows(ft, ms, self.d)
+            dev = self.device
+            self._acc_tables[width] = (
+                ms,
+                torch.from_numpy(ms.quads.view(np.int32)).to(dev),
+                torch.from_numpy(ms.coef).to(dev),
+                torch.from_numpy(rows).to(dev),
+            )
+        return self._acc_tables[width]
+
+    def _accumulate(self, k: torch.Tensor, v: torch.Tensor, n: int, head_rows: int, state_num: torch.Tensor,
+                    state_den: torch.Tensor, row_off: int = 0) -> None:
+        """state += moments of rows [row_off, row_off + n) of k [S, head_rows, width] / v [S, head_rows, ldv]
+        (contiguous, width a whole number of 16-byte units, ldv a multiple of 32)."""
+        if n <= 0:
+            return
+        width = k.shape[-1]
+        assert k.is_contiguous() and v.is_contiguous() and k.shape[1] == head_rows == v.shape[1]
+        ms, quads, coef, rows = self._acc_table(width)
+        kp = k.data_ptr() + row_off * width * k.element_size()
+        vp = v.data_ptr() + row_off * v.shape[-1] * v.element_size()
+
+        def run():
+            st = self.lib.sta_moment_accumulate(
+                kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, width, self.dv,
+                v.shape[-1], self.degree, ms.fsplit, ms.wave_tiles, quads.data_ptr(), coef.data_ptr(), rows.data_ptr(),
+                self.F, state_num.data_ptr(), state_den.data_ptr(), self._stream())
+            _native.check(st, "sta_moment_accumulate")
+
+        self._launch("moment_accumulate", run)
+
+    def _ensure_levels(self, need: int) -> None:
+        if need <= self.L:
+            return
+        new_l = max(need, 2 * self.L, 4)
+        S, m = self.S, self.m
+        f32 = dict(device=self.device, dtype=torch.float32)
+        lk = torch.zeros((S, new_l, m, self.dk), **f32)
+        lv = torch.zeros((S, new_l, m, self.ldv), **f32)
+        lw = torch.zeros((S, new_l, m), **f32)
+        lp = torch.zeros((S, new_l, m), device=self.device, dtype=torch.int32)
+        if self.L:
+            lk[:, : self.L] = self.lev_k
+            lv[:, : self.L] = self.lev_v
+            lw[:, : self.L] = self.lev_w
+            lp[:, : self.L] = self.lev_pos
+        self.lev_k, self.lev_v, self.lev_w, self.lev_pos, self.L = lk, lv, lw, lp, new_l
+
+    def _grow_buffer(self) -> None:
+        new_cap = 2 * self.cap
+        f32 = dict(device=self.device, dtype=torch.float32)
+        bk = torch.zeros((self.S, new_cap, self.dk), **f32)
+        bv = torch.zeros((self.S, new_cap, self.ldv), **f32)
+        bk[:, : self.cap] = self.buf_k
+        bv[:, : self.cap] = self.buf_v
+        self.buf_k, self.buf_v, self.cap = bk, bv, new_cap
+
+    # ------------------------------------------------------------------ draws
+    def _draw_completion(self, blocks_before: int) -> _CompletionDraws:
+        sizes = _plan.completion_call_sizes(blocks_before, self.block, self.compressor)
+        n_calls = len(sizes)
+        max_in = max(self.block, 2 * self.m)
+        S, d = self.S, self.d
+        dirs = np.zeros((S, n_calls, d), dtype=np.float32)
+        unif = np.zeros((S, n_calls, max_in // 2), dtype=np.float32)
+        perms = np.zeros((S, n_calls, max_in), dtype=np.int32)
+        methods: List[int] = []
+        for s, g in enumerate(self._gens):
+            for c, n_in in enumerate(sizes):
+                method, dvec, u, perm = _plan._draw_one_call(g, n_in, d, self.compressor)
+                if s == 0:
+                    methods.append(method)
+                if dvec is not None:
+                    dirs[s, c] = dvec
+                    unif[s, c, : u.shape[0]] = u
+                if perm is not None:
+                    perms[s, c, : perm.shape[0]] = perm
+        dev = self.device
+        return _CompletionDraws(
+            blocks_before, n_calls, torch.tensor(methods, dtype=torch.int32).to(dev), torch.from_numpy(dirs).to(dev),
+            torch.from_numpy(unif).to(dev), torch.from_numpy(perms).to(dev))
+
+    def reserve_draws(self, tokens: int) -> int:
+        """Draw ahead, on the host, the compress calls of every block completion within the next
+        `tokens` tokens (they depend only on the seeds); returns the number of completions queued."""
+        if self.exact:
+            return 0
+        queued_to = self.blocks + len(self._draws)
+        last = (self.length + tokens) // self.block
+        for c in range(queued_to, last):
+            self._draws.append(self._draw_completion(c))
+        return len(self._draws)
+
+    def _take_draws(self) -> _CompletionDraws:
+        if self._draws:
+            dr = self._draws.popleft()
+            assert dr.blocks_before == self.blocks
+            return dr
+        return self._draw_completion(self.blocks)
+
+    # ------------------------------------------------------------------ block completion
+    def _complete_block(self, accumulate: bool = True) -> None:
+        """The buffer holds a full block: moments += buffer, then compress + cascade into the levels."""
+        if accumulate:
+            self._accumulate(self.buf_k, self.buf_v, self.block, self.cap, self.state_num, self.state_den)
+        dr = self._take_draws()
+        self._ensure_levels(dr.n_calls)
+
+        def run():
+            st = self.lib.sta_decode_compress(
+                self.S, self.d, self.dv, self.buf_k.data_ptr(), self.buf_v.data_ptr(), self.block,
+                self.length - self.block, self.lev_k.data_ptr(), self.lev_v.data_ptr(), self.lev_w.data_ptr(),
+                self.lev_pos.data_ptr(), self.L, self.m, dr.n_calls, dr.methods.data_ptr(), dr.dirs.data_ptr(),
+                dr.unif.data_ptr(), dr.perms.data_ptr(), dr.perms.shape[-1], self._stream())
+            _native.check(st, "sta_decode_compress")
+
+        self._launch("decode_compress", run)
+        self.num_compressions += dr.n_calls
+        self.blocks += 1
+        self.buf_len = 0
+
+    # ------------------------------------------------------------------ kernels
+    def _check_rows(self, x: torch.Tensor, width: int, what: str) -> torch.Tensor:
+        if x.shape != (self.S, width):
+            raise ValueError(f"{what} must have shape [{self.S}, {width}], got {tuple(x.shape)}")
+        if x.device != self.device:
+            x = x.to(self.device)
+        if x.dtype not in _native.DTYPE_CODES:
+            x = x.float()
+        return x.contiguous()
+
+    def _tail(self, q, k, v, flags: int, out_dtype: torch.dtype, stats: Optional[torch.Tensor]):
+        dt_src = q if q is not None else k
+        dt = _native.DTYPE_CODES[dt_src.dtype]
+        out = None
+        if flags & _native.DEC_QUERY:
+            out = torch.empty((self.S, self.dv), device=self.device, dtype=out_dtype)
+
+        def run():
+            st = self.lib.sta_decode_tail(
+                _native.ptr(q), _native.ptr(k), _native.ptr(v), dt, self.S, self.d, self.dv, self.degree, self.scale,
+                self.eps, flags, self.buf_k.data_ptr(), self.buf_v.data_ptr(), self.cap, self.buf_len,
+                self.lev_k.data_ptr(), self.lev_v.data_ptr(), self.lev_w.data_ptr(), self.L, self.m,
+                self.blocks if not self.exact else 0, self.part_num.data_ptr(), self.part_den.data_ptr(), self.splits,
+                _native.ptr(out), _native.DTYPE_CODES[out_dtype], _native.ptr(stats), self._stream())
+            _native.check(st, "sta_decode_tail")
+
+        self._launch("decode_tail", run)
+        return out
+
+    def _moments(self, q: torch.Tensor) -> None:
+        if self.exact:
+            return  # the state stays zero: every token is answered exactly from the buffer
+
+        def run():
+            st = self.lib.sta_decode_moments(
+                q.data_ptr(), _native.DTYPE_CODES[q.dtype], self.S, self.d, self.dv, self.scale,
+                self.state_num.data_ptr(), self.state_den.data_ptr(), self.F, self.findex.data_ptr(), self.splits,
+                self.part_num.data_ptr(), self.part_den.data_ptr(), self._stream())
+            _native.check(st, "sta_decode_moments")
+
+        self._launch("decode_moments", run)
+
+    # ------------------------------------------------------------------ public operations
+    def update(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append one token per stream (MergeReduceCoreset.append + TaylorMomentSketch.update)."""
+        k = self._check_rows(k, self.d, "key")
+        v = self._check_rows(v, self.dv, "value").to(k.dtype)
+        if self.exact and self.buf_len == self.cap:
+            self._grow_buffer()
+        self._tail(None, k, v, _native.DEC_APPEND, torch.float32, None)
+        self.buf_len += 1
+        self.length += 1
+        if not self.exact and self.buf_len == self.block:
+            self._complete_block()
+
+    def query(self, q: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+              stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+        q = self._check_rows(q, self.d, "query")
+        self._moments(q)
+        return self._tail(q, None, None, _native.DEC_QUERY, out_dtype, stats)
+
+    def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+             stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """update(k, v) then query(q) for every stream, fused into two launches unless the token
+        completes a block."""
+        completes = (not self.exact and self.buf_len + 1 == self.block) or (self.exact and self.buf_len == self.cap)
+        if completes:
+            self.update(k, v)
+            return self.query(q, out_dtype, stats)
+        q = self._check_rows(q, self.d, "query")
+        k = self._check_rows(k, self.d, "key").to(q.dtype)
+        v = self._check_rows(v, self.dv, "value").to(q.dtype)
+        self._moments(q)
+        out = self._tail(q, k, v, _native.DEC_APPEND | _native.DEC_CURRENT | _native.DEC_QUERY, out_dtype, stats)
+        self.buf_len += 1
+        self.length += 1
+        return out
+
+    def extend(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """update() for every token of k [S, P, d] / v [S, P, dv], in bulk: whole blocks go to the state
+        in one moment-accumulate launch and are compressed block by block."""
+        if k.ndim != 3 or k.shape[0] != self.S or k.shape[2] != self.d:
+            raise ValueError(f"keys must have shape [{self.S}, P, {self.d}], got {tuple(k.shape)}")
+        if v.shape != (self.S, k.shape[1], self.dv):
+            raise ValueError(f"values must have shape [{self.S}, {k.shape[1]}, {self.dv}], got {tuple(v.shape)}")
+        k = k.to(self.device)
+        v = v.to(self.device)
+        if k.dtype not in _native.DTYPE_CODES:
+            k = k.float()
+        v = v.to(k.dtype)
+        p_total = k.shape[1]
+        i = 0
+
+        def to_buffer(lo: int, hi: int) -> None:
+            n = hi - lo
+            while self.exact and self.buf_len + n > self.cap:
+                self._grow_buffer()
+            self.buf_k[:, self.buf_len: self.buf_len + n, : self.d] = k[:, lo:hi].float()
+            self.buf_v[:, self.buf_len: self.buf_len + n, : self.dv] = v[:, lo:hi].float()
+            self.buf_len += n
+            self.length += n
+
+        if self.exact:
+            to_buffer(0, p_total)
+            return
+        # 1. top up a partly filled buffer
+        if self.buf_len > 0:
+            n = min(p_total, self.block - self.buf_len)
+            to_buffer(0, n)
+            i = n
+            if self.buf_len == self.block:
+                self._complete_block()
+        # 2. whole blocks: one moment-accumulate launch, then block-by-block compression
+        nb = (p_total - i) // self.block
+        if nb > 0:
+            esize = k.element_size()
+            width = -(-self.d // (16 // esize)) * (16 // esize)
+            lo, hi = i, i + nb * self.block
+            if width == self.d and k.is_contiguous() and k.data_ptr() % 16 == 0:
+                kp, koff = k, lo  # read in place
+            else:
+                kp, koff = torch.zeros((self.S, hi - lo, width), device=self.device, dtype=k.dtype), 0
+                kp[..., : self.d] = k[:, lo:hi]
+            if self.ldv == self.dv and v.is_contiguous() and v.data_ptr() % 16 == 0 and koff == lo:
+                vp = v
+            else:
+                vp = torch.zeros((self.S, kp.shape[1], self.ldv), device=self.device, dtype=k.dtype)
+                vp[:, koff: koff + hi - lo, : self.dv] = v[:, lo:hi]
+            self._accumulate(kp, vp, hi - lo, kp.shape[1], self.state_num, self.state_den, row_off=koff)
+            for b in range(nb):
+                to_buffer(lo + b * self.block, lo + (b + 1) * self.block)
+                self._complete_block(accumulate=False)
+            i = hi
+        # 3. the rest starts a new buffer
+        if i < p_total:
+            to_buffer(i, p_total)
+
+    # ------------------------------------------------------------------ inspection
+    def full_moments(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(den [S, F], num [S, F, dv]) over every token so far, reference feature order (the
+        reference's sketch state: completed blocks plus the buffer)."""
+        num = self.state_num.clone()
+        den = self.state_den.clone()
+        self._accumulate(self.buf_k, self.buf_v, self.buf_len, self.cap, num, den)
+        return den, num[..., : self.dv]
+
+    def level_items(self) -> List[Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]]]:
+        """Per level: (keys [S, m, d], values [S, m, dv], weights [S, m], positions [S, m]) or None."""
+        out = []
+        top = self.blocks.bit_length()
+        for l in range(top):
+            if self.exact or not (self.blocks >> l) & 1:
+                out.append(None)
+            else:
+                out.append((self.lev_k[:, l, :, : self.d], self.lev_v[:, l, :, : self.dv], self.lev_w[:, l],
+                            self.lev_pos[:, l]))
+        return out
+
+    def buffer_items(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(keys [S, n, d], values [S, n, dv], positions [n]) of the uncompressed buffer."""
+        n = self.buf_len
+        pos = torch.arange(self.length - n, self.length, device=self.device, dtype=torch.int32)
+        return self.buf_k[:, :n, : self.d], self.buf_v[:, :n, : self.dv], pos
+
+    def num_items(self) -> int:
+        if self.exact:
+            return self.length
+        return self.buf_len + self.m * bin(self.blocks).count("1")
+
+    def reference_state_bytes(self, elem: int, include_feature_map: bool = False) -> int:
+        """ArticleStreamingAttention.state_size_bytes of one stream for element size `elem`
+        (streaming_taylor_coreset_attention.py:298-306, :495-506, :611-612)."""
+        d, dv = self.d, self.dv
+        total = self.F * (1 + dv) * elem
+        if include_feature_map:
+            for l in range(1, self.degree + 1):
+                total += (_plan.num_features(d, l) - _plan.num_features(d, l - 1)) * l * 8
+            total += self.F * elem
+        buffered = self.length - (self.length // self.block) * self.block
+        total += buffered * (d + dv) * elem
+        completed = self.length // self.block
+        items = completed * self.block if self.exact else self.m * bin(completed).count("1")
+        total += items * (d + dv + 1) * elem
+        return int(total)
+
+    def device_bytes(self) -> int:
+        """Bytes of device memory this state holds."""
+        ts = [self.state_num, self.state_den, self.buf_k, self.buf_v, self.lev_k, self.lev_v, self.lev_w,
+              self.lev_pos, self.part_num, self.part_den, self.findex]
+        return int(sum(t.numel() * t.element_size() for t in ts))

@@ -62,6 +62,32 @@ _SIGNATURES = {
             _c_p, _i32, _c_p, _c_p,  # out out_dtype out_den stream
         ],
     ),
+    "sta_moment_accumulate": (
+        _i32,
+        [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dtype bh n rows d dv ldv deg fs nt
+         _c_p, _c_p, _c_p, _i32, _c_p, _c_p, _c_p],  # quads coef rows n_feat state_num state_den stream
+    ),
+    "sta_decode_layout": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+    "sta_decode_moments": (
+        _i32, [_c_p, _i32, _i64, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _i32, _c_p, _c_p, _c_p],
+    ),
+    "sta_decode_tail": (
+        _i32,
+        [
+            _c_p, _c_p, _c_p, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _i32,  # q k v dtype S d dv deg scale eps flags
+            _c_p, _c_p, _i32, _i32,  # buf_k buf_v block buf_len
+            _c_p, _c_p, _c_p, _i32, _i32, ctypes.c_uint64,  # lev_k lev_v lev_w n_levels level_size mask
+            _c_p, _c_p, _i32, _c_p, _i32, _c_p, _c_p,  # part_num part_den splits out out_dtype stats stream
+        ],
+    ),
+    "sta_decode_compress": (
+        _i32,
+        [
+            _i64, _i32, _i32, _c_p, _c_p, _i32, _i32,  # S d dv buf_k buf_v block pos0
+            _c_p, _c_p, _c_p, _c_p, _i32, _i32,  # lev_k lev_v lev_w lev_pos n_levels level_size
+            _i32, _c_p, _c_p, _c_p, _c_p, _i32, _c_p,  # n_calls methods dirs unif perms max_in stream
+        ],
+    ),
     "sta_selftest_mfma": (_i32, [_c_p, _c_p, _c_p]),
 }
 
@@ -144,6 +170,16 @@ def moment_partials_layout(n: int, dv: int) -> tuple:
     check(lib().sta_moment_partials_layout(n, dv, ctypes.byref(rows), ctypes.byref(ld), ctypes.byref(off)),
           "sta_moment_partials_layout")
     return rows.value, ld.value, off.value
+
+
+def decode_layout(d: int, dv: int) -> tuple:
+    """(dk, ldv): row lengths of the decode buffers for keys and values (zero-padded columns)."""
+    dk, ldv = _i32(), _i32()
+    check(lib().sta_decode_layout(d, dv, ctypes.byref(dk), ctypes.byref(ldv)), "sta_decode_layout")
+    return dk.value, ldv.value
+
+
+DEC_APPEND, DEC_CURRENT, DEC_QUERY = 1, 2, 4
 
 
 def limits() -> dict:

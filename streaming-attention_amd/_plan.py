@@ -93,6 +93,7 @@ class FeatureTiles:
     n_tiles: int
     quads: np.ndarray  # uint32 [n_tiles * 4]
     coef: np.ndarray  # float32 [n_tiles * 16]
+    combos: Tuple[Optional[Tuple[int, ...]], ...] = ()  # sorted multi-index of each slot, None for padding
 
 
 def feature_tiles(d: int, degree: int) -> FeatureTiles:
@@ -103,6 +104,7 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
         one = d
         quads: List[int] = []
         coefs: List[List[float]] = []
+        slot_combos: List[Optional[Tuple[int, ...]]] = []
         count = 0
 
         def add_row(prefix: Tuple[int, ...], lo: int, hi: int, with_const: bool) -> None:
@@ -120,12 +122,15 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
                     c = b + s
                     if lo <= c < hi:
                         cs.append(_factorial_inverse(tuple(sorted(prefix + (c,)))))
+                        slot_combos.append(tuple(sorted(prefix + (c,))))
                         count += 1
                     elif with_const and c == d:
                         cs.append(_factorial_inverse(prefix))
+                        slot_combos.append(tuple(prefix))
                         count += 1
                     else:
                         cs.append(0.0)
+                        slot_combos.append(None)
                 quads.append(i0 | (b << 8) | (i2 << 16))
                 coefs.append(cs)
 
@@ -144,9 +149,42 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
         c = np.zeros(n_tiles * 16, dtype=np.float32)
         q[: len(quads)] = np.asarray(quads, dtype=np.uint32)
         c[: 4 * len(coefs)] = np.asarray(coefs, dtype=np.float32).reshape(-1)
-        return FeatureTiles(d, degree, count, n_tiles, q, c)
+        combos = tuple(slot_combos) + (None,) * (n_tiles * 16 - len(slot_combos))
+        return FeatureTiles(d, degree, count, n_tiles, q, c, combos)
 
     return _cached(("ftiles", d, degree), build)
+
+
+def reference_feature_order(d: int, degree: int) -> Dict[Tuple[int, ...], int]:
+    """Index of every sorted multi-index in the reference's feature order: degree 0, 1, ..., t, each
+    degree in itertools.combinations_with_replacement(range(d), l) order
+    (streaming_taylor_coreset_attention.py:160-176, fast_article_attention.py:151-181)."""
+
+    def build():
+        order: Dict[Tuple[int, ...], int] = {(): 0}
+        for l in range(1, degree + 1):
+            for combo in itertools.combinations_with_replacement(range(d), l):
+                order[combo] = len(order)
+        return order
+
+    return _cached(("reforder", d, degree), build)
+
+
+def feature_index(d: int, degree: int) -> np.ndarray:
+    """uint32 [F]: the factors of reference feature f packed i0 | i1 << 8 | i2 << 16, indices into
+    x = [x_0 .. x_{d-1}, 1] (index d is the constant 1 filling the unused factors)."""
+
+    def build():
+        order = reference_feature_order(d, degree)
+        out = np.zeros(len(order), dtype=np.uint32)
+        for combo, f in order.items():
+            idx = list(combo) + [d] * (3 - len(combo))
+            out[f] = idx[0] | (idx[1] << 8) | (idx[2] << 16)
+        return out
+
+    if degree > 3 or d > 255:
+        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 255")
+    return _cached(("findex", d, degree), build)
 
 
 @dataclass(frozen=True)
@@ -211,6 +249,28 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
     return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units), build)
 
 
+def split_state_rows(ft: FeatureTiles, ms: MomentSplit, d: int) -> np.ndarray:
+    """int32 [fsplit * 4 * wave_tiles * 16]: the reference-order feature row (for the true dimension d
+    <= ft.d) of every feature slot of the split's table, -1 for padding slots and for monomials that
+    involve a padding dimension >= d (their keys are zero there)."""
+
+    def build():
+        order = reference_feature_order(d, ft.degree)
+        slot_row = np.full(ft.n_tiles * 16, -1, dtype=np.int32)
+        for i, combo in enumerate(ft.combos):
+            if combo is not None and all(c < d for c in combo):
+                slot_row[i] = order[combo]
+        parts = ms.tile_off.shape[0] - 1
+        rows = np.full((parts, ms.wave_tiles, 16), -1, dtype=np.int32)
+        for j in range(parts):
+            a, b = int(ms.tile_off[j]), int(ms.tile_off[j + 1])
+            rows[j, : b - a] = slot_row[16 * a: 16 * b].reshape(b - a, 16)
+        assert sorted(r for r in rows.reshape(-1) if r >= 0) == list(range(len(order)))
+        return rows.reshape(-1)
+
+    return _cached(("srows", ft.d, ft.degree, d, ms.fsplit, ms.wave_tiles, ms.tile_off.tobytes()), build)
+
+
 # ----------------------------------------------------------------------------- draws
 
 def _compressed_size(n_in: int, compressor: str) -> int:
@@ -234,11 +294,11 @@ def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str):
     """Consume the generator exactly as one reference compress call on n_in items does."""
     if compressor == "none" or n_in <= 1:
         return METHOD_COPY, None, None, None
+    if compressor not in ("random", "sorted_pair"):
+        raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
     if compressor == "random" or n_in <= 2:
         perm = torch.randperm(n_in, generator=g)
         return METHOD_PERM, None, None, perm.numpy().astype(np.int32)
-    if compressor != "sorted_pair":
-        raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
     direction = torch.randn(d, generator=g, dtype=torch.float32)
     direction = direction / torch.clamp(torch.linalg.vector_norm(direction), min=1e-12)
     u = torch.rand(n_in // 2, generator=g, dtype=torch.float32)
@@ -455,6 +515,19 @@ def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str) -
         return draws, desc
 
     return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor), build)
+
+
+def completion_call_sizes(blocks_before: int, block: int, compressor: str) -> List[int]:
+    """Input sizes of the compress calls made when block number blocks_before + 1 completes: the
+    block itself, then one merge per occupied level below the counter's lowest zero bit
+    (streaming_taylor_coreset_attention.py:387-411); every level holds compressed_size(block) items."""
+    m = _compressed_size(block, compressor)
+    carries = 0
+    c = blocks_before
+    while c & 1:
+        carries += 1
+        c >>= 1
+    return [block] + [2 * m] * carries
 
 
 def sequence_seeds(seed: int, bh: int) -> Tuple[int, ...]:

@@ -3,6 +3,7 @@
 #include "../../include/streamattn.h"
 #include "block_attn.hip"
 #include "compress.hip"
+#include "decode.hip"
 #include "moments.hip"
 
 namespace {
@@ -38,6 +39,19 @@ int launch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   return check_launch();
 }
 
+template <int NT, bool DEG3, bool DBIG>
+int launch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
+  const size_t smem = static_cast<size_t>(sta::mom_acc_smem_floats(DBIG, NT)) * sizeof(float);
+  auto fn = sta::moment_accumulate_kernel<NT, DEG3, DBIG>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+  if (e != hipSuccess) return hip_status(e);
+  const int64_t grid = bh * a.fsplit * a.csplit;
+  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOM_THREADS), smem, s, a);
+  return check_launch();
+}
+
 // Per-wave tile counts the moment kernel is instantiated for, per (degree 3, d > 64).
 constexpr int kNtD2[] = {2, 4, 5, 9, 16};
 constexpr int kNtD3[] = {4, 8, 16};
@@ -59,9 +73,9 @@ int moment_wave_tiles(int d, int degree, int want) {
 }
 
 #define STA_MOM_CASE(NT, D3, BIG) \
-  case NT: return launch_moments<NT, D3, BIG>(a, bh, s);
+  case NT: return accumulate ? launch_accumulate<NT, D3, BIG>(a, bh, s) : launch_moments<NT, D3, BIG>(a, bh, s);
 
-int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
+int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3, bool accumulate) {
   if (a.d <= 64) {
     if (deg3) {
       switch (nt) { STA_MOM_CASE(4, true, false) STA_MOM_CASE(8, true, false) STA_MOM_CASE(16, true, false) }
@@ -179,7 +193,128 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
-  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
+  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, false);
+}
+
+int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
+                          int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
+                          const float* feat_coef, const int32_t* feat_rows, int n_feat, float* state_num,
+                          float* state_den, void* stream) {
+  if (!k || !v || !feat_quads || !feat_coef || !feat_rows || !state_num || !state_den) return STA_ERR_ARG;
+  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  if (bh <= 0 || n < 0 || head_rows < n || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0 || n_feat <= 0)
+    return STA_ERR_SHAPE;
+  if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
+  if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
+  if (n == 0) return STA_OK;
+  const int esize = dtype == STA_F32 ? 4 : 2;
+  if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0) return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0) return STA_ERR_ARG;
+  if (head_rows * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+    return STA_ERR_UNSUPPORTED;
+  sta::MomArgs a;
+  a.q = k; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = 1.0f; a.shift = 0;
+  a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
+  a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
+  a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
+  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, true);
+}
+
+int sta_decode_layout(int d, int dv, int* dk, int* ldv) {
+  if (d <= 0 || dv <= 0 || !dk || !ldv) return STA_ERR_ARG;
+  if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
+  *dk = 4 * ((d + 3) / 4);
+  *ldv = 32 * ((dv + 31) / 32);
+  return STA_OK;
+}
+
+int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv, float scale, const float* state_num,
+                       const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* part_num,
+                       float* part_den, void* stream) {
+  if (!q || !state_num || !state_den || !feat_index || !part_num || !part_den) return STA_ERR_ARG;
+  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  if (streams <= 0 || d <= 0 || dv <= 0 || n_feat <= 0 || splits <= 0 || splits > n_feat) return STA_ERR_SHAPE;
+  if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
+  if (((reinterpret_cast<uintptr_t>(state_num) | reinterpret_cast<uintptr_t>(part_num)) & 15u) != 0) return STA_ERR_ARG;
+  const int64_t grid = streams * splits;
+  if (grid > 0x7fffffff) return STA_ERR_UNSUPPORTED;
+  sta::DecMomArgs a;
+  a.q = q; a.dtype = dtype; a.d = d; a.scale = scale; a.state_num = state_num; a.state_den = state_den;
+  a.n_feat = n_feat; a.ldm = 32 * ((dv + 31) / 32); a.rowfeat = feat_index; a.splits = splits;
+  a.rows_per_split = (n_feat + splits - 1) / splits; a.part_num = part_num; a.part_den = part_den;
+  hipLaunchKernelGGL(sta::decode_moments_kernel, dim3(static_cast<unsigned>(grid)), dim3(sta::DEC_THREADS), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch();
+}
+
+int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
+                    int degree, float scale, float eps, int flags, float* buf_k, float* buf_v, int block, int buf_len,
+                    const float* lev_k, const float* lev_v, const float* lev_w, int n_levels, int level_size,
+                    uint64_t level_mask, const float* part_num, const float* part_den, int splits, void* out,
+                    int out_dtype, float* stats, void* stream) {
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return STA_ERR_DTYPE;
+  if (streams <= 0 || d <= 0 || dv <= 0 || block <= 0 || buf_len < 0 || n_levels < 0 || level_size < 0)
+    return STA_ERR_SHAPE;
+  if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
+  if (flags & ~(sta::DEC_APPEND | sta::DEC_CURRENT | sta::DEC_QUERY)) return STA_ERR_ARG;
+  if ((flags & sta::DEC_CURRENT) && !(flags & sta::DEC_APPEND)) return STA_ERR_ARG;
+  if (!buf_k || !buf_v) return STA_ERR_ARG;
+  if ((flags & sta::DEC_APPEND) && (!k || !v || buf_len >= block)) return STA_ERR_ARG;
+  if (buf_len > block) return STA_ERR_SHAPE;
+  if (flags & sta::DEC_QUERY) {
+    if (!q || !out || !part_num || !part_den || splits <= 0) return STA_ERR_ARG;
+    if (n_levels > 64 || (n_levels < 64 && (level_mask >> n_levels) != 0)) return STA_ERR_SHAPE;
+    if (level_mask && (!lev_k || !lev_v || !lev_w || level_size <= 0)) return STA_ERR_ARG;
+  }
+  if (streams > 0x7fffffff) return STA_ERR_UNSUPPORTED;
+  int dk = 0, ldv = 0;
+  sta_decode_layout(d, dv, &dk, &ldv);
+  if (((reinterpret_cast<uintptr_t>(buf_k) | reinterpret_cast<uintptr_t>(buf_v) | reinterpret_cast<uintptr_t>(lev_k) |
+        reinterpret_cast<uintptr_t>(lev_v)) & 15u) != 0)
+    return STA_ERR_ARG;
+  sta::DecTailArgs a;
+  a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.d = d; a.dv = dv; a.degree = degree; a.scale = scale; a.eps = eps;
+  a.buf_k = buf_k; a.buf_v = buf_v; a.B = block; a.dk = dk; a.ldv = ldv; a.buf_len = buf_len;
+  a.lev_k = lev_k; a.lev_v = lev_v; a.lev_w = lev_w; a.L = n_levels; a.m = level_size; a.level_mask = level_mask;
+  a.flags = flags; a.part_num = part_num; a.part_den = part_den; a.splits = splits; a.out = out;
+  a.out_dtype = out_dtype; a.stats = stats;
+  const dim3 grid(static_cast<unsigned>(streams));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int kc = d <= 64 ? 1 : 2;
+  const int vc = dv <= 64 ? 1 : (dv <= 128 ? 2 : 4);
+  if (kc == 1 && vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 1>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  else if (kc == 1 && vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 2>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  else if (kc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 4>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  else if (vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 1>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  else if (vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 2>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  else hipLaunchKernelGGL((sta::decode_tail_kernel<2, 4>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  return check_launch();
+}
+
+int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, const float* buf_v, int block, int pos0,
+                        float* lev_k, float* lev_v, float* lev_w, int32_t* lev_pos, int n_levels, int level_size,
+                        int n_calls, const int32_t* methods, const float* dirs, const float* unif,
+                        const int32_t* perms, int max_in, void* stream) {
+  if (!buf_k || !buf_v || !lev_k || !lev_v || !lev_w || !lev_pos || !methods || !dirs || !unif || !perms)
+    return STA_ERR_ARG;
+  if (streams <= 0 || d <= 0 || dv <= 0 || block < 2 || pos0 < 0 || n_levels <= 0 || level_size <= 0)
+    return STA_ERR_SHAPE;
+  if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
+  if (n_calls <= 0 || n_calls > n_levels) return STA_ERR_SHAPE;
+  // every level holds ceil(block / 2) items and every call's input fits the LDS lists
+  if (level_size != (block + 1) / 2) return STA_ERR_SHAPE;
+  if (block > sta::CMP_MAX_IN || 2 * level_size > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
+  if (max_in < block || max_in < 2 * level_size) return STA_ERR_ARG;
+  if (streams > 0x7fffffff) return STA_ERR_UNSUPPORTED;
+  int dk = 0, ldv = 0;
+  sta_decode_layout(d, dv, &dk, &ldv);
+  sta::DecCmpArgs a;
+  a.buf_k = buf_k; a.buf_v = buf_v; a.B = block; a.d = d; a.dk = dk; a.ldv = ldv; a.pos0 = pos0;
+  a.lev_k = lev_k; a.lev_v = lev_v; a.lev_w = lev_w; a.lev_pos = lev_pos; a.L = n_levels; a.m = level_size;
+  a.n_calls = n_calls; a.methods = methods; a.dirs = dirs; a.unif = unif; a.perms = perms; a.max_in = max_in;
+  hipLaunchKernelGGL(sta::decode_compress_kernel, dim3(static_cast<unsigned>(streams)), dim3(sta::CMP_THREADS), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch();
 }
 
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,

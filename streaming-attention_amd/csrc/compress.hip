@@ -47,6 +47,45 @@ __device__ __forceinline__ bool key_greater(float sa, int pa, float sb, int pb) 
   return sa > sb || (sa == sb && pa > pb);
 }
 
+// Projection score <row, dir>: fp64 accumulation in dimension order, rounded to fp32 once (every fp32 x
+// fp32 product is exact in fp64, so the score is a fixed function of the inputs).
+__device__ __forceinline__ float projection_score(const float* row, int row_stride, const float* dir, int d) {
+  double acc = 0.0;
+  for (int col = 0; col < d; ++col)
+    acc = fma(static_cast<double>(row[col * row_stride]), static_cast<double>(dir[col]), acc);
+  return static_cast<float>(acc);
+}
+
+// Ascending bitonic sort of (key, pos) pairs in LDS, np a power of two, ties broken by position (a
+// stable order); all `nthreads` threads of the workgroup take part.
+__device__ __forceinline__ void bitonic_sort_pairs(float* key_s, int* pos_s, int np, int tid, int nthreads) {
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (np >> 1); t += nthreads) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int j = i + stride;
+        const bool up = (i & size) == 0;
+        const float si = key_s[i], sj = key_s[j];
+        const int pi = pos_s[i], pj = pos_s[j];
+        if (key_greater(si, pi, sj, pj) == up) {
+          key_s[i] = sj;
+          key_s[j] = si;
+          pos_s[i] = pj;
+          pos_s[j] = pi;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Keep-first decision of the weighted pair rule: u < w_a / max(w_a + w_b, 1e-30)
+// (streaming_taylor_coreset_attention.py:452-457; with unit weights the flat rule rand < 0.5,
+// fast_article_attention.py:348).
+__device__ __forceinline__ bool pair_keeps_first(float u, float wa, float wb) {
+  return u < __fdiv_rn(wa, fmaxf(wa + wb, 1e-30f));
+}
+
 __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
   __shared__ int src_s[CMP_MAX_IN];
   __shared__ float w_s[CMP_MAX_IN];
@@ -116,10 +155,7 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
     }
     __syncthreads();
     if (tid < cnt) {
-      double acc = 0.0;
-      for (int col = 0; col < a.d; ++col)
-        acc = fma(static_cast<double>(rows[tid * LD + col]), static_cast<double>(dir_s[col]), acc);
-      key_s[base + tid] = static_cast<float>(acc);
+      key_s[base + tid] = projection_score(rows + tid * LD, 1, dir_s, a.d);
       pos_s[base + tid] = base + tid;
     }
   }
@@ -132,24 +168,7 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   __syncthreads();
 
   // ---- bitonic sort of (score, position), ascending ----
-  for (int size = 2; size <= np; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < (np >> 1); t += CMP_THREADS) {
-        const int i = 2 * t - (t & (stride - 1));
-        const int j = i + stride;
-        const bool up = (i & size) == 0;
-        const float si = key_s[i], sj = key_s[j];
-        const int pi = pos_s[i], pj = pos_s[j];
-        if (key_greater(si, pi, sj, pj) == up) {
-          key_s[i] = sj;
-          key_s[j] = si;
-          pos_s[i] = pj;
-          pos_s[j] = pi;
-        }
-      }
-      __syncthreads();
-    }
-  }
+  bitonic_sort_pairs(key_s, pos_s, np, tid, CMP_THREADS);
 
   // ---- pair selection with weight transfer ----
   const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);
@@ -157,11 +176,9 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   for (int p = tid; p < pc; p += CMP_THREADS) {
     const int ia2 = pos_s[2 * p], ib2 = pos_s[2 * p + 1];
     const float wa = w_s[ia2], wb = w_s[ib2];
-    const float wsum = wa + wb;
-    const float prob = __fdiv_rn(wa, fmaxf(wsum, 1e-30f));
-    const bool choose_a = u[p] < prob;
+    const bool choose_a = pair_keeps_first(u[p], wa, wb);
     a.node_src[obase + p] = choose_a ? src_s[ia2] : src_s[ib2];
-    a.node_w[obase + p] = wsum;
+    a.node_w[obase + p] = wa + wb;
   }
   if ((n_in & 1) && tid == 0) {
     const int il = pos_s[n_in - 1];

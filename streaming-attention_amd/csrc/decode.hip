@@ -1,0 +1,446 @@
+// K5: batched streaming decode (ArticleStreamingAttention.update / query,
+// streaming_taylor_coreset_attention.py:576-609) for S independent streams advancing in lockstep.
+//
+// Decode state of stream s (all fp32, caller-owned):
+//   state_num [S][F][ldm], state_den [S][F]  moments sum phi_k(k_j) [v_j, 1] over the tokens of the
+//       completed blocks only, features in the reference's order (degree 0, 1, ..., each in
+//       combinations_with_replacement order, streaming_taylor_coreset_attention.py:180-216);
+//   buf_k [S][B][dk], buf_v [S][B][ldv]  the uncompressed buffer: the tokens of the current block;
+//   lev_k [S][L][m][dk], lev_v [S][L][m][ldv], lev_w [S][L][m], lev_pos [S][L][m]  the level coresets
+//       (level l occupied iff bit l of the completed-block counter is set; every level holds m items).
+// Padding columns of dk / ldv are zero.  A query is answered as
+//   low (phi_q . state: keys of completed blocks, exactly the reference's Taylor part for them)
+//   + sum over buffered tokens of exp(s q.k) [v, 1]          (their Taylor part plus their exp_{>t}
+//                                                             tail: together the exact exponential)
+//   + sum over level items of w (exp(s q.k) - exp_{<=t}(s q.k)) [v, 1]
+// which is, term by term, the reference's low + tail (:583-597) regrouped: the reference's sketch holds
+// the buffered tokens too, and its coreset items() lists them with weight 1.  Keeping the buffered
+// tokens out of the state makes a decode step read the state once and write nothing; the block's
+// rank-B state update is applied when the block completes (moment_accumulate_kernel over the buffer).
+//
+// Kernels per step: decode_moments_kernel (state read, HBM-bound) and decode_tail_kernel (buffer and
+// level items, HBM-bound; also appends the token).  On a block completion the host adds
+// moment_accumulate_kernel (buffer -> state) and decode_compress_kernel (buffer -> level 0, then the
+// cascade of merges cat(old level, new) while levels are occupied, :387-411).
+#include "common.hpp"
+
+namespace sta {
+
+constexpr int DEC_THREADS = 256;
+constexpr int DEC_GROUPS = DEC_THREADS / 16;  // items in flight per workgroup pass (16 lanes per item)
+constexpr int DEC_MAX_X = 136;                // staged query features x[0..d] (d <= 128) plus zeros
+
+enum DecFlags : int { DEC_APPEND = 1, DEC_CURRENT = 2, DEC_QUERY = 4 };
+
+// ------------------------------------------------------------------------------------------------
+// decode_moments_kernel: part_num[s][split][col] = sum_{f in split} phi_q(s q)[f] state_num[s][f][col],
+// part_den[s][split] likewise with state_den.  Thread (row slot rp, column quad c4) walks the rows
+// f = f0 + rp + j * rpp, 4 rows per trip with unconditional (clamped) 16-byte loads.
+struct DecMomArgs {
+  const void* q;  // [S][d] current queries (dtype)
+  int dtype;
+  int d;
+  float scale;
+  const float* state_num;  // [S][n_feat][ldm]
+  const float* state_den;  // [S][n_feat]
+  int n_feat;
+  int ldm;                  // a multiple of 32
+  const uint32_t* rowfeat;  // [n_feat] factors i0 | i1 << 8 | i2 << 16 of x = [s q, 1] (index d = 1)
+  int splits;
+  int rows_per_split;
+  float* part_num;  // [S][splits][ldm]
+  float* part_den;  // [S][splits]
+};
+
+__global__ __launch_bounds__(DEC_THREADS) void decode_moments_kernel(const DecMomArgs a) {
+  __shared__ float xs[DEC_MAX_X];
+  __shared__ floatx4 red[DEC_THREADS];
+  __shared__ float dred[DEC_THREADS];
+  const int wg = blockIdx.x;
+  const int64_t s = wg / a.splits;
+  const int sp = wg - static_cast<int>(s) * a.splits;
+  const int tid = threadIdx.x;
+  for (int j = tid; j < DEC_MAX_X; j += DEC_THREADS)
+    xs[j] = j < a.d ? a.scale * load_elem(a.q, s * a.d + j, a.dtype) : (j == a.d ? 1.f : 0.f);
+  __syncthreads();
+
+  const int c4n = a.ldm >> 2;
+  const int rpp = DEC_THREADS / c4n;
+  const int rp = tid / c4n, c4 = tid - rp * c4n;
+  const int f0 = sp * a.rows_per_split;
+  const int f1 = min(a.n_feat, f0 + a.rows_per_split);
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  float dacc = 0.f;
+  if (rp < rpp && f0 < f1) {
+    const float* sn = a.state_num + s * a.n_feat * a.ldm + 4 * c4;
+    const float* sd = a.state_den + s * a.n_feat;
+    constexpr int U = 4;
+    for (int r = f0 + rp; r < f1; r += U * rpp) {
+      floatx4 S[U];
+      float D[U], phi[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int row = r + u * rpp;
+        const int rr = min(row, f1 - 1);
+        S[u] = *reinterpret_cast<const floatx4*>(sn + static_cast<int64_t>(rr) * a.ldm);
+        D[u] = sd[rr];
+        const uint32_t pf = a.rowfeat[rr];
+        const float ph = xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u];
+        phi[u] = row < f1 ? ph : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc += phi[u] * S[u];
+        dacc = fmaf(phi[u], D[u], dacc);
+      }
+    }
+  }
+  red[tid] = acc;
+  dred[tid] = dacc;
+  __syncthreads();
+  const int64_t ob = s * a.splits + sp;
+  if (tid < c4n) {
+    floatx4 t = red[tid];
+    for (int j = 1; j < rpp; ++j) t += red[j * c4n + tid];
+    *reinterpret_cast<floatx4*>(a.part_num + ob * a.ldm + 4 * tid) = t;
+  }
+  if (tid == 0) {
+    float t = dred[0];
+    for (int j = 1; j < rpp; ++j) t += dred[j * c4n];
+    a.part_den[ob] = t;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// decode_tail_kernel: one workgroup per stream.  APPEND writes the current (k, v) into buffer slot
+// buf_len; QUERY answers the current query from the moment partials, the buf_len buffered tokens (plus
+// the current token when CURRENT: the append of this same launch) and the occupied levels, and writes
+// out = num / max(den, eps).  Items are spread over 16-lane groups: lane c of a group holds 16-byte
+// column units c, c + 16, ... of the key and the value, the score is a 16-lane xor reduction.
+struct DecTailArgs {
+  const void* q;  // [S][d]
+  const void* k;  // [S][d]
+  const void* v;  // [S][dv]
+  int dtype;
+  int d, dv, degree;
+  float scale, eps;
+  float* buf_k;  // [S][B][dk]
+  float* buf_v;  // [S][B][ldv]
+  int B, dk, ldv;
+  int buf_len;
+  const float* lev_k;  // [S][L][m][dk]
+  const float* lev_v;  // [S][L][m][ldv]
+  const float* lev_w;  // [S][L][m]
+  int L, m;
+  uint64_t level_mask;
+  int flags;
+  const float* part_num;  // [S][splits][ldv]
+  const float* part_den;  // [S][splits]
+  int splits;
+  void* out;  // [S][dv]
+  int out_dtype;
+  float* stats;  // [S][4] or null: denominator, reference low / tail denominators, items
+};
+
+template <int KC, int VC>
+struct DecItem {
+  floatx4 k[KC];
+  floatx4 v[VC];
+};
+
+template <int KC, int VC>
+__device__ __forceinline__ void dec_load_item(DecItem<KC, VC>& it, const float* krow, const float* vrow, int c, int dk4,
+                                              int dv4) {
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const int u = c + 16 * j;
+    it.k[j] = u < dk4 ? *reinterpret_cast<const floatx4*>(krow + 4 * u) : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < VC; ++j) {
+    const int u = c + 16 * j;
+    it.v[j] = u < dv4 ? *reinterpret_cast<const floatx4*>(vrow + 4 * u) : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+template <int KC>
+__device__ __forceinline__ float dec_dot(const floatx4 (&x)[KC], const floatx4 (&k)[KC]) {
+  float t = 0.f;
+#pragma unroll
+  for (int j = 0; j < KC; ++j) t += x[j][0] * k[j][0] + x[j][1] * k[j][1] + x[j][2] * k[j][2] + x[j][3] * k[j][3];
+  t += __shfl_xor(t, 8, 16);
+  t += __shfl_xor(t, 4, 16);
+  t += __shfl_xor(t, 2, 16);
+  t += __shfl_xor(t, 1, 16);
+  return t;
+}
+
+template <int KC, int VC>
+__global__ __launch_bounds__(DEC_THREADS) void decode_tail_kernel(const DecTailArgs a) {
+  __shared__ float xs[DEC_MAX_X];
+  __shared__ float cur_k[DEC_MAX_X];
+  __shared__ float cur_v[4 * 16 * VC];
+  __shared__ float redv[DEC_GROUPS][4 * 16 * VC];
+  __shared__ float redd[DEC_GROUPS][2];
+  const int64_t s = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int dk4 = a.dk >> 2, dv4 = a.ldv >> 2;
+
+  if (a.flags & (DEC_APPEND | DEC_CURRENT)) {
+    for (int j = tid; j < a.dk + a.ldv; j += DEC_THREADS) {
+      if (j < a.dk) {
+        const float x = j < a.d ? load_elem(a.k, s * a.d + j, a.dtype) : 0.f;
+        cur_k[j] = x;
+        if (a.flags & DEC_APPEND) a.buf_k[(s * a.B + a.buf_len) * a.dk + j] = x;
+      } else {
+        const int c = j - a.dk;
+        const float x = c < a.dv ? load_elem(a.v, s * a.dv + c, a.dtype) : 0.f;
+        if (c < 4 * 16 * VC) cur_v[c] = x;
+        if (a.flags & DEC_APPEND) a.buf_v[(s * a.B + a.buf_len) * a.ldv + c] = x;
+      }
+    }
+  }
+  if (!(a.flags & DEC_QUERY)) return;
+  for (int j = tid; j < DEC_MAX_X; j += DEC_THREADS)
+    xs[j] = j < a.d ? a.scale * load_elem(a.q, s * a.d + j, a.dtype) : 0.f;
+  __syncthreads();
+
+  const int c = tid & 15, g = tid >> 4;
+  floatx4 x[KC];
+#pragma unroll
+  for (int j = 0; j < KC; ++j) {
+    const int u = c + 16 * j;
+    x[j] = u < dk4 ? *reinterpret_cast<const floatx4*>(xs + 4 * u) : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  floatx4 acc[VC];
+#pragma unroll
+  for (int j = 0; j < VC; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float den = 0.f, tay = 0.f;  // tay: Taylor part of the buffered tokens (reference low denominator)
+
+  // buffered tokens: exact exponential, weight 1 (two items per group in flight)
+  const float* bk = a.buf_k + s * a.B * a.dk;
+  const float* bv = a.buf_v + s * a.B * a.ldv;
+  for (int j0 = g; j0 < a.buf_len; j0 += 2 * DEC_GROUPS) {
+    DecItem<KC, VC> it[2];
+    const int j1 = min(j0 + DEC_GROUPS, a.buf_len - 1);
+    dec_load_item<KC, VC>(it[0], bk + j0 * a.dk, bv + j0 * a.ldv, c, dk4, dv4);
+    dec_load_item<KC, VC>(it[1], bk + j1 * a.dk, bv + j1 * a.ldv, c, dk4, dv4);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float z = dec_dot<KC>(x, it[h].k);
+      const bool on = h == 0 || j0 + DEC_GROUPS < a.buf_len;
+      const float p = on ? expf(z) : 0.f;
+      den += p;
+      tay += on ? taylor_poly(z, a.degree) : 0.f;
+#pragma unroll
+      for (int j = 0; j < VC; ++j) acc[j] += p * it[h].v[j];
+    }
+  }
+  // the current token of this launch (group 0)
+  if ((a.flags & DEC_CURRENT) && g == 0) {
+    DecItem<KC, VC> it;
+    dec_load_item<KC, VC>(it, cur_k, cur_v, c, dk4, dv4);
+    const float z = dec_dot<KC>(x, it.k);
+    const float p = expf(z);
+    den += p;
+    tay += taylor_poly(z, a.degree);
+#pragma unroll
+    for (int j = 0; j < VC; ++j) acc[j] += p * it.v[j];
+  }
+  // level items: weighted exp_{>t} residual
+  int n_items = a.buf_len + ((a.flags & DEC_CURRENT) ? 1 : 0);
+  for (int l = 0; l < a.L; ++l) {
+    if (!((a.level_mask >> l) & 1u)) continue;
+    n_items += a.m;
+    const int64_t base = (s * a.L + l) * a.m;
+    const float* lk = a.lev_k + base * a.dk;
+    const float* lv = a.lev_v + base * a.ldv;
+    const float* lw = a.lev_w + base;
+    for (int j0 = g; j0 < a.m; j0 += 2 * DEC_GROUPS) {
+      DecItem<KC, VC> it[2];
+      const int j1 = min(j0 + DEC_GROUPS, a.m - 1);
+      dec_load_item<KC, VC>(it[0], lk + j0 * a.dk, lv + j0 * a.ldv, c, dk4, dv4);
+      dec_load_item<KC, VC>(it[1], lk + j1 * a.dk, lv + j1 * a.ldv, c, dk4, dv4);
+      const float w0 = lw[j0], w1 = lw[j1];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float z = dec_dot<KC>(x, it[h].k);
+        const bool on = h == 0 || j0 + DEC_GROUPS < a.m;
+        const float r = on ? (h == 0 ? w0 : w1) * (expf(z) - taylor_poly(z, a.degree)) : 0.f;
+        den += r;
+#pragma unroll
+        for (int j = 0; j < VC; ++j) acc[j] += r * it[h].v[j];
+      }
+    }
+  }
+
+  // ---- fixed-order combination: groups, then moment partials ----
+#pragma unroll
+  for (int j = 0; j < VC; ++j) *reinterpret_cast<floatx4*>(&redv[g][4 * (c + 16 * j)]) = acc[j];
+  if (c == 0) {
+    redd[g][0] = den;
+    redd[g][1] = tay;
+  }
+  __syncthreads();
+  float tail_den = 0.f, buf_tay = 0.f;
+  for (int j = 0; j < DEC_GROUPS; ++j) {
+    tail_den += redd[j][0];
+    buf_tay += redd[j][1];
+  }
+  float low_den = 0.f;
+  for (int j = 0; j < a.splits; ++j) low_den += a.part_den[s * a.splits + j];
+  const float total = low_den + tail_den;
+  const float safe = fmaxf(total, a.eps);
+  for (int col = tid; col < a.dv; col += DEC_THREADS) {
+    float num = 0.f;
+    for (int j = 0; j < a.splits; ++j) num += a.part_num[(s * a.splits + j) * a.ldv + col];
+    for (int j = 0; j < DEC_GROUPS; ++j) num += redv[j][col];
+    store_elem(a.out, s * a.dv + col, a.out_dtype, __fdiv_rn(num, safe));
+  }
+  if (a.stats && tid == 0) {
+    a.stats[s * 4 + 0] = total;
+    a.stats[s * 4 + 1] = low_den + buf_tay;
+    a.stats[s * 4 + 2] = total - (low_den + buf_tay);
+    a.stats[s * 4 + 3] = static_cast<float>(n_items);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// decode_compress_kernel: one workgroup per stream, run when the buffer is full.  Call 0 compresses the
+// B buffered tokens (weight 1); call i >= 1 merges cat(level i-1, output of call i-1) (old then new,
+// streaming_taylor_coreset_attention.py:404-408); the output of the last call becomes level
+// n_calls - 1, which is free (the counter's lowest zero bit).  An item is a handle: buffer row h < B or
+// level row h - B; only handles, weights and positions move between calls, and the selected rows are
+// copied once at the end, so nothing the kernel reads is written by it.
+struct DecCmpArgs {
+  const float* buf_k;  // [S][B][dk]
+  const float* buf_v;  // [S][B][ldv]
+  int B, d, dk, ldv;
+  int pos0;  // sequence position of buffer row 0
+  float* lev_k;
+  float* lev_v;
+  float* lev_w;
+  int32_t* lev_pos;
+  int L, m;
+  int n_calls;
+  const int32_t* methods;  // [n_calls] M_SORTED_PAIR or M_PERM
+  const float* dirs;       // [S][n_calls][d]
+  const float* unif;       // [S][n_calls][max_in / 2]
+  const int32_t* perms;    // [S][n_calls][max_in]
+  int max_in;
+};
+
+__global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecCmpArgs a) {
+  __shared__ int in_h[CMP_MAX_IN];
+  __shared__ float in_w[CMP_MAX_IN];
+  __shared__ int in_p[CMP_MAX_IN];
+  __shared__ float key_s[CMP_MAX_IN];
+  __shared__ int pos_s[CMP_MAX_IN];
+  __shared__ int cur_h[CMP_MAX_IN / 2 + 1];
+  __shared__ float cur_w[CMP_MAX_IN / 2 + 1];
+  __shared__ int cur_p[CMP_MAX_IN / 2 + 1];
+  __shared__ float dir_s[128];
+  const int64_t s = blockIdx.x;
+  const int tid = threadIdx.x;
+  auto key_row = [&](int h) -> const float* {
+    return h < a.B ? a.buf_k + (s * a.B + h) * a.dk : a.lev_k + (s * a.L * a.m + (h - a.B)) * a.dk;
+  };
+  auto val_row = [&](int h) -> const float* {
+    return h < a.B ? a.buf_v + (s * a.B + h) * a.ldv : a.lev_v + (s * a.L * a.m + (h - a.B)) * a.ldv;
+  };
+
+  int m_cur = 0;
+  for (int call = 0; call < a.n_calls; ++call) {
+    // ---- input list ----
+    int n;
+    if (call == 0) {
+      n = a.B;
+      for (int j = tid; j < n; j += CMP_THREADS) {
+        in_h[j] = j;
+        in_w[j] = 1.0f;
+        in_p[j] = a.pos0 + j;
+      }
+    } else {
+      n = a.m + m_cur;
+      const int64_t lb = (s * a.L + (call - 1)) * a.m;
+      for (int j = tid; j < n; j += CMP_THREADS) {
+        if (j < a.m) {
+          in_h[j] = a.B + (call - 1) * a.m + j;
+          in_w[j] = a.lev_w[lb + j];
+          in_p[j] = a.lev_pos[lb + j];
+        } else {
+          in_h[j] = cur_h[j - a.m];
+          in_w[j] = cur_w[j - a.m];
+          in_p[j] = cur_p[j - a.m];
+        }
+      }
+    }
+    __syncthreads();
+    const int method = a.methods[call];
+    const int64_t slot = s * a.n_calls + call;
+    if (method == M_PERM) {
+      const int mo = (n + 1) / 2;
+      const int32_t* perm = a.perms + slot * a.max_in;
+      const float factor = static_cast<float>(static_cast<double>(n) / static_cast<double>(mo));
+      for (int j = tid; j < mo; j += CMP_THREADS) {
+        const int p = perm[j];
+        cur_h[j] = in_h[p];
+        cur_w[j] = in_w[p] * factor;
+        cur_p[j] = in_p[p];
+      }
+      m_cur = mo;
+    } else {
+      // sorted_pair: fp64 projection scores of the input rows, stable ascending sort, pair selection
+      for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = a.dirs[slot * a.d + e];
+      __syncthreads();
+      for (int j = tid; j < n; j += CMP_THREADS) {
+        key_s[j] = projection_score(key_row(in_h[j]), 1, dir_s, a.d);
+        pos_s[j] = j;
+      }
+      int np = 1;
+      while (np < n) np <<= 1;
+      for (int j = n + tid; j < np; j += CMP_THREADS) {
+        key_s[j] = __builtin_huge_valf();
+        pos_s[j] = j;
+      }
+      __syncthreads();
+      bitonic_sort_pairs(key_s, pos_s, np, tid, CMP_THREADS);
+      const float* u = a.unif + slot * (a.max_in / 2);
+      const int pc = n / 2;
+      for (int p = tid; p < pc; p += CMP_THREADS) {
+        const int ia = pos_s[2 * p], ib = pos_s[2 * p + 1];
+        const float wa = in_w[ia], wb = in_w[ib];
+        const int keep = pair_keeps_first(u[p], wa, wb) ? ia : ib;
+        cur_h[p] = in_h[keep];
+        cur_w[p] = wa + wb;
+        cur_p[p] = in_p[keep];
+      }
+      if ((n & 1) && tid == 0) {
+        const int il = pos_s[n - 1];
+        cur_h[pc] = in_h[il];
+        cur_w[pc] = in_w[il];
+        cur_p[pc] = in_p[il];
+      }
+      m_cur = pc + (n & 1);
+    }
+    __syncthreads();
+  }
+
+  // ---- the result becomes level n_calls - 1 ----
+  const int dest = a.n_calls - 1;
+  const int64_t ob = (s * a.L + dest) * a.m;
+  for (int e = tid; e < m_cur * a.dk; e += CMP_THREADS) {
+    const int j = e / a.dk, col = e - j * a.dk;
+    a.lev_k[(ob + j) * a.dk + col] = key_row(cur_h[j])[col];
+  }
+  for (int e = tid; e < m_cur * a.ldv; e += CMP_THREADS) {
+    const int j = e / a.ldv, col = e - j * a.ldv;
+    a.lev_v[(ob + j) * a.ldv + col] = val_row(cur_h[j])[col];
+  }
+  for (int j = tid; j < m_cur; j += CMP_THREADS) {
+    a.lev_w[ob + j] = cur_w[j];
+    a.lev_pos[ob + j] = cur_p[j];
+  }
+}
+
+}  // namespace sta

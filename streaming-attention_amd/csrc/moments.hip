@@ -75,6 +75,12 @@ struct MomArgs {
   int ldo;                // low_num row stride: 32 * csplit
   int ldv;                // row stride of v (elements): a multiple of 32, >= dv; q and k rows are d long
   int esize;              // bytes per input element (4 or 2)
+  // moment_accumulate_kernel only: persistent state in the reference's feature order
+  int64_t head_rows;      // rows between consecutive heads of k / v (>= n)
+  const int32_t* rowmap;  // [fsplit][4 waves][NT tiles][16] state row of each feature slot, -1 for padding
+  float* state_num;       // [BH][n_feat][ldo]
+  float* state_den;       // [BH][n_feat]
+  int n_feat;
 };
 
 __host__ __device__ constexpr int mom_ldq(bool dbig) { return dbig ? 132 : 68; }
@@ -255,6 +261,91 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
   a.low_den[obase + row0 + tok] = den;
 }
 
+// Per-lane feature offsets of a wave's NT tiles (constant over the sequence).  Query side: columns of
+// x[i0], x[b..b+3], x[i2] of quad lg in the row-major queries.  Update side: Kt rows of feature li plus
+// the token offset 8 lg, and the key-side coefficient of feature li.
+template <int NT, bool DEG3>
+struct MomLane {
+  int qa[NT], qb[NT], qc[DEG3 ? NT : 1];
+  int ka[NT], kb[NT], kc[DEG3 ? NT : 1];
+  float kcoef[NT];
+};
+
+template <int NT, bool DEG3>
+__device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t tile0, int li, int lg) {
+  MomLane<NT, DEG3> m;
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+    const uint32_t pq = a.quads[(tile0 + kt) * 4 + lg];
+    m.qa[kt] = static_cast<int>(pq & 255u);
+    m.qb[kt] = static_cast<int>((pq >> 8) & 255u);
+    if (DEG3) m.qc[DEG3 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
+    const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
+    m.ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 8 * lg;
+    m.kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 8 * lg;
+    if (DEG3) m.kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 8 * lg;
+    m.kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
+  }
+  return m;
+}
+
+// State update with one staged chunk: S[f][col] += phi_k(tok)[f] V[tok][col] for the wave's NT tiles and
+// its 32 columns, den_s[f] += phi_k(tok)[f].  Token steps outermost over all tiles (2 NT independent
+// chains), in two halves of 4 steps; the keys of the second half are read while the first half's
+// MFMAs issue.  `mid()` runs after the first key reads are issued (work to hide under them).
+template <int NT, bool DEG3, class Mid>
+__device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, const float* Kt, const float* Vt,
+                                           const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
+  constexpr int CT = 2;
+  floatx4 vv[2][CT];  // values of tokens 8 lg + 0..3 and 8 lg + 4..7
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
+    vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
+  }
+  floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
+  auto uload = [&](int h) {
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 4 * h);
+      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 4 * h);
+      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 4 * h);
+    }
+  };
+  uload(0);
+  mid();
+  __builtin_amdgcn_sched_barrier(0);
+  float dacc[NT];
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) dacc[kt] = 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 0) uload(1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+        float x = fa[h][kt][e] * fb[h][kt][e];
+        if (DEG3) x *= fc[h][DEG3 ? kt : 0][e];
+        x *= m.kcoef[kt];
+        dacc[kt] += x;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma4(x, vv[h][ct][e], st[kt][ct]);
+      }
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) pin(dacc[kt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+    float s = dacc[kt];
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    if (lg == 0) den_s[16 * kt + li] += s;
+  }
+}
+
 template <int NT, bool DEG3, bool DBIG>
 __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
   constexpr int LDQ = mom_ldq(DBIG);
@@ -282,23 +373,8 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
   const int li = lane & 15, lg = lane >> 4;
   float* den_s = den_all + w * NT * 16;  // running denominator of every feature of this wave's tiles
 
-  // ---- per-lane feature offsets (constant over the sequence) ----
   const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NT;
-  int qa[NT], qb[NT], qc[DEG3 ? NT : 1];  // query: columns of x[i0], x[b..b+3], x[i2] of quad lg
-  int ka[NT], kb[NT], kc[DEG3 ? NT : 1];  // update: Kt rows of feature li, plus the token offset 8 lg
-  float kcoef[NT];
-#pragma unroll
-  for (int kt = 0; kt < NT; ++kt) {
-    const uint32_t pq = a.quads[(tile0 + kt) * 4 + lg];
-    qa[kt] = static_cast<int>(pq & 255u);
-    qb[kt] = static_cast<int>((pq >> 8) & 255u);
-    if (DEG3) qc[DEG3 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
-    const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
-    ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 8 * lg;
-    kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 8 * lg;
-    if (DEG3) kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 8 * lg;
-    kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
-  }
+  const MomLane<NT, DEG3> m = mom_lane<NT, DEG3>(a, tile0, li, lg);
 
   floatx4 st[NT][CT];
 #pragma unroll
@@ -351,9 +427,9 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
       auto qload = [&](int kt, int buf) {
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
-          x0[buf][tt] = qrow[16 * tt * LDQ + qa[kt]];
-          x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + qb[kt]);
-          if (DEG3) x2[buf][tt] = qrow[16 * tt * LDQ + qc[DEG3 ? kt : 0]];
+          x0[buf][tt] = qrow[16 * tt * LDQ + m.qa[kt]];
+          x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[kt]);
+          if (DEG3) x2[buf][tt] = qrow[16 * tt * LDQ + m.qc[DEG3 ? kt : 0]];
         }
         dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
       };
@@ -397,61 +473,104 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
     if (c + 1 < nchunks) mom_store<DBIG>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- update: token steps outermost over all tiles (2 NT independent chains), in two halves of 4
-    //      steps; the keys of the second half are read while the first half's MFMAs issue ----
-    {
-      floatx4 vv[2][CT];  // values of tokens 8 lg + 0..3 and 8 lg + 4..7
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
-        vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
-      }
-      floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
-      auto uload = [&](int h) {
-#pragma unroll
-        for (int kt = 0; kt < NT; ++kt) {
-          fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + ka[kt] + 4 * h);
-          fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + kb[kt] + 4 * h);
-          if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + kc[DEG3 ? kt : 0] + 4 * h);
-        }
-      };
-      uload(0);
-      // partials of the previous chunk: fixed-order reduction and store, under the first loads
+    // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
+    //      key reads ----
+    mom_update<NT, DEG3>(st, den_s, Kt, Vt, m, li, lg, [&]() {
       if (c > 0) mom_reduce_store(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
-      __builtin_amdgcn_sched_barrier(0);
-      float dacc[NT];
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) dacc[kt] = 0.f;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (h == 0) uload(1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-#pragma unroll
-          for (int kt = 0; kt < NT; ++kt) {
-            float x = fa[h][kt][e] * fb[h][kt][e];
-            if (DEG3) x *= fc[h][DEG3 ? kt : 0][e];
-            x *= kcoef[kt];
-            dacc[kt] += x;
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma4(x, vv[h][ct][e], st[kt][ct]);
-          }
-#pragma unroll
-          for (int kt = 0; kt < NT; ++kt) pin(dacc[kt]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        float s = dacc[kt];
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
-        if (lg == 0) den_s[16 * kt + li] += s;
-      }
-    }
+    });
     __syncthreads();
   }
   mom_reduce_store(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C, col0);
+}
+
+// Shared-memory floats of moment_accumulate_kernel: one chunk buffer, the running denominators, a dummy.
+__host__ __device__ constexpr int mom_acc_smem_floats(bool dbig, int nt) {
+  return mom_buf_floats(dbig) + MOM_WAVES * nt * 16 + 8;
+}
+
+// Persistent-state form of the moment update (the decode state of a stream):
+//   state_num[f][col] += sum_{j < n} phi_k(k_j)[f] v_j[col],  state_den[f] += sum_{j < n} phi_k(k_j)[f]
+// over the n rows of each head, the state kept in the reference's feature order
+// (streaming_taylor_coreset_attention.py:180-216, TaylorMomentSketch.update :265-280).  Same feature
+// tiles, chunk staging and MFMA update as moments_kernel; the wave's slice of the state is loaded into
+// the accumulators at the start and written back at the end (each (head, feature, column) belongs to
+// exactly one wave of the grid, so the read-modify-write has no race).  Rows [0, n) of every head are
+// read at k + bh * head_rows * d (v: ldv).
+template <int NT, bool DEG3, bool DBIG>
+__global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const MomArgs a) {
+  constexpr int BUF = mom_buf_floats(DBIG);
+  constexpr int CT = 2;
+  extern __shared__ float smem[];
+  float* den_all = smem + BUF;
+  const int dummy_abs = BUF + MOM_WAVES * NT * 16;
+
+  const int per_head = a.fsplit * a.csplit;
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / per_head;
+  const int rem = wg - static_cast<int>(bh) * per_head;
+  const int fs = rem / a.csplit;
+  const int cs = rem - fs * a.csplit;
+  const int col0 = 32 * cs;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  float* den_s = den_all + w * NT * 16;
+  const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NT;
+  const MomLane<NT, DEG3> m = mom_lane<NT, DEG3>(a, tile0, li, lg);
+
+  // ---- the wave's slice of the state -> accumulators and running denominators ----
+  float* snum = a.state_num + bh * a.n_feat * a.ldo;
+  float* sden = a.state_den + bh * a.n_feat;
+  floatx4 st[NT][CT];
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        st[kt][ct][r] = row >= 0 ? snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] : 0.f;
+    }
+    if (lg == 0) {
+      const int row = a.rowmap[(tile0 + kt) * 16 + li];
+      den_s[16 * kt + li] = row >= 0 ? sden[row] : 0.f;
+    }
+  }
+
+  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.d * a.esize;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * a.esize;
+  const MomSlots<DBIG> sl = mom_slots<DBIG>(a, col0, dummy_abs);
+  const int nchunks = static_cast<int>((a.n + MOM_C - 1) / MOM_C);
+  for (int e = tid; e < BUF; e += MOM_THREADS) smem[e] = 0.f;  // padding rows / columns stay 0
+  for (int c = 0; c < nchunks; ++c) {
+    MomStage<DBIG> stg;
+    mom_load<DBIG>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
+    __syncthreads();  // the previous chunk's update is done with the buffer
+    mom_store<DBIG>(stg, sl, a, smem, dummy_abs, c * MOM_C);
+    __syncthreads();
+    const float* Kt = smem + MOM_C * mom_ldq(DBIG);
+    const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
+    mom_update<NT, DEG3>(st, den_s, Kt, Vt, m, li, lg, []() {});
+  }
+
+  // ---- write the slice back (the denominators once per feature split) ----
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+      if (row >= 0) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] = st[kt][ct][r];
+      }
+    }
+    if (lg == 0 && cs == 0) {
+      const int row = a.rowmap[(tile0 + kt) * 16 + li];
+      if (row >= 0) sden[row] = den_s[16 * kt + li];
+    }
+  }
 }
 
 }  // namespace sta

@@ -10,23 +10,32 @@ returns (streaming_taylor_coreset_attention.py:641-754), computed as one prefill
   * for token i: the uncompressed buffer (tokens of the current block up to i, weight 1) plus the
     level coresets present after update(k_i) -- so the last token of a block is answered from the
     freshly compressed levels, exactly as in the reference.
+
+`ArticleStreamingAttention` is the mutable streaming state itself (streaming_taylor_coreset_attention.py
+:523-616) with `update(k, v)`, `query(q)`, `state_size_bytes()` and `length`, kept on the GPU (decode
+kernels K5).  Beyond the reference it takes `streams=S` for S independent streams advanced in lockstep
+(stream s seeded seed + s, the per-sequence seeding of article_causal_attention), and offers `step`
+(update + query fused), `extend` (bulk update) and `prefill` (outputs for a prompt plus the state).
 """
 
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 from typing import List, Optional, Tuple, Union
 
 import torch
 
+import _decode
 import _engine
 import _plan
-from fast_article_attention import _compute_dtype, _to_gpu
+from fast_article_attention import _compute_dtype, _resolve_dtype, _to_gpu
 
 Tensor = torch.Tensor
 
-__all__ = ["article_causal_attention", "article_causal_attention_single", "classical_causal_attention",
-           "exp_taylor", "safe_relative_l2", "state_size_trace"]
+__all__ = ["ArticleStreamingAttention", "AttentionQueryStats", "CoresetBlock", "article_causal_attention",
+           "article_causal_attention_single", "classical_causal_attention", "exp_taylor", "safe_relative_l2",
+           "state_size_trace"]
 
 
 def exp_taylor(logits: Tensor, degree: int) -> Tensor:
@@ -181,3 +190,295 @@ def article_causal_attention(
         return out
     one = state_size_trace(n, dim, dv, degree, block_size, compressor, q.element_size())
     return out, one * (bsz * heads)
+
+
+# -----------------------------------------------------------------------------------------------
+# Streaming state (streaming_taylor_coreset_attention.py:229-616)
+# -----------------------------------------------------------------------------------------------
+
+
+@dataclass
+class CoresetBlock:
+    """Keys, values and weights of a set of coreset items (streaming_taylor_coreset_attention.py:313-329).
+    In batched mode every tensor has a leading stream dimension."""
+
+    keys: Tensor
+    values: Tensor
+    weights: Tensor
+
+    @property
+    def size(self) -> int:
+        return int(self.weights.shape[-1])
+
+
+@dataclass
+class AttentionQueryStats:
+    """streaming_taylor_coreset_attention.py:514-520.  In batched mode the three denominators are
+    tensors [S]; coreset_items and state_bytes are per stream (every stream has the same counts)."""
+
+    denominator: Union[float, Tensor]
+    low_denominator: Union[float, Tensor]
+    tail_denominator: Union[float, Tensor]
+    coreset_items: int
+    state_bytes: int
+
+
+def _resolve_gpu(device: Optional[Union[str, torch.device]]) -> torch.device:
+    if device is None or str(device) == "auto":
+        if not torch.cuda.is_available():
+            raise RuntimeError("streaming-attention HIP kernels need a ROCm GPU; none is visible")
+        return torch.device("cuda", torch.cuda.current_device())
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError("ArticleStreamingAttention keeps its state on a ROCm GPU; pass a cuda device")
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    return dev
+
+
+def _elem(dtype: torch.dtype) -> int:
+    return torch.tensor([], dtype=dtype).element_size()
+
+
+class _SketchView:
+    """The moment sketch of the state (TaylorMomentSketch, streaming_taylor_coreset_attention.py:229-306):
+    den_moments / num_moments per degree, in the reference's feature order."""
+
+    def __init__(self, owner: "ArticleStreamingAttention") -> None:
+        self._o = owner
+
+    @property
+    def length(self) -> int:
+        return self._o._st.length
+
+    @property
+    def sizes(self) -> List[int]:
+        d = self._o.dim
+        return [math.comb(d + l - 1, l) if l else 1 for l in range(self._o.degree + 1)]
+
+    def _parts(self, x: Tensor) -> List[Tensor]:
+        out, at = [], 0
+        for m in self.sizes:
+            part = x[:, at: at + m].to(self._o.dtype)
+            out.append(part[0] if self._o._single else part)
+            at += m
+        return out
+
+    @property
+    def den_moments(self) -> List[Tensor]:
+        return self._parts(self._o._st.full_moments()[0])
+
+    @property
+    def num_moments(self) -> List[Tensor]:
+        return self._parts(self._o._st.full_moments()[1])
+
+    def state_size_bytes(self, include_feature_map: bool = False) -> int:
+        o = self._o
+        elem = _elem(o.dtype)
+        total = o._st.F * (1 + o.value_dim) * elem
+        if include_feature_map:
+            for l in range(1, o.degree + 1):
+                total += math.comb(o.dim + l - 1, l) * l * 8
+            total += o._st.F * elem
+        return int(total)
+
+
+class _CoresetView:
+    """The merge-and-reduce coreset of the state (MergeReduceCoreset, streaming_taylor_coreset_attention.py
+    :332-506)."""
+
+    def __init__(self, owner: "ArticleStreamingAttention") -> None:
+        self._o = owner
+
+    @property
+    def length(self) -> int:
+        return self._o._st.length
+
+    @property
+    def block_size(self) -> int:
+        return self._o.block_size
+
+    @property
+    def num_compressions(self) -> int:
+        return self._o._st.num_compressions
+
+    def _pack(self, keys: Tensor, values: Tensor, weights: Tensor) -> CoresetBlock:
+        dt = self._o.dtype
+        if self._o._single:
+            keys, values, weights = keys[0], values[0], weights[0]
+        return CoresetBlock(keys.to(dt), values.to(dt), weights.to(dt))
+
+    @property
+    def levels(self) -> List[Optional[CoresetBlock]]:
+        st = self._o._st
+        if st.exact:
+            raise NotImplementedError("compressor='none' keeps every token in one exact buffer; use items()")
+        return [None if lv is None else self._pack(lv[0], lv[1], lv[2]) for lv in st.level_items()]
+
+    def level_positions(self) -> List[Optional[Tensor]]:
+        """Sequence positions of the items of every level (which tokens were selected)."""
+        out = []
+        for lv in self._o._st.level_items():
+            out.append(None if lv is None else (lv[3][0] if self._o._single else lv[3]))
+        return out
+
+    def items(self) -> CoresetBlock:
+        """Buffer (weight 1), then levels 0, 1, ... (streaming_taylor_coreset_attention.py:469-490)."""
+        st = self._o._st
+        bk, bv, _ = st.buffer_items()
+        ks, vs, ws = [bk], [bv], [torch.ones(bk.shape[:2], device=bk.device, dtype=torch.float32)]
+        if not st.exact:
+            for lv in st.level_items():
+                if lv is not None:
+                    ks.append(lv[0])
+                    vs.append(lv[1])
+                    ws.append(lv[2])
+        return self._pack(torch.cat(ks, 1), torch.cat(vs, 1), torch.cat(ws, 1))
+
+    def num_items(self) -> int:
+        return self._o._st.num_items()
+
+    def state_size_bytes(self) -> int:
+        o = self._o
+        elem = _elem(o.dtype)
+        return o._st.reference_state_bytes(elem) - o._st.F * (1 + o.value_dim) * elem
+
+
+class ArticleStreamingAttention:
+    """Streaming causal attention via Taylor moments + residual coreset, state on the GPU
+    (streaming_taylor_coreset_attention.py:523-616).
+
+    `update(k, v)` then `query(q)` answers causal self-attention including the current token.  With
+    `streams=None` keys are [dim] and outputs [value_dim], as in the reference; with `streams=S` keys
+    are [S, dim], queries [S, dim] and outputs [S, value_dim], stream s seeded `seed + s`.
+
+    The state is fp32 whatever `dtype` is: inputs are rounded to `dtype` first (the reference casts
+    them to its state dtype) and outputs are returned in `dtype`."""
+
+    def __init__(
+        self,
+        dim: int,
+        value_dim: int,
+        *,
+        degree: int = 2,
+        block_size: int = 128,
+        scale: Optional[float] = None,
+        compressor: str = "sorted_pair",
+        device: Optional[Union[str, torch.device]] = None,
+        dtype: Union[str, torch.dtype] = torch.float32,
+        seed: int = 0,
+        max_monomials: int = 5_000_000,
+        denominator_eps: float = 1e-12,
+        streams: Optional[int] = None,
+    ) -> None:
+        if dim <= 0:
+            raise ValueError("dim must be positive")
+        if degree < 0:
+            raise ValueError("degree must be non-negative")
+        _feature_count(int(dim), int(degree), int(max_monomials))
+        if block_size < 2:
+            raise ValueError("block_size must be at least 2")
+        self.dim = int(dim)
+        self.value_dim = int(value_dim)
+        self.degree = int(degree)
+        self.block_size = int(block_size)
+        self.scale = float(1.0 / math.sqrt(dim) if scale is None else scale)
+        self.compressor = str(compressor)
+        self.device = _resolve_gpu(device)
+        self.dtype = _resolve_dtype(dtype)
+        if self.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError(f"dtype {self.dtype} is not supported by the HIP kernels (float32, bfloat16, float16)")
+        self.seed = int(seed)
+        self.denominator_eps = float(denominator_eps)
+        self._single = streams is None
+        self.streams = 1 if streams is None else int(streams)
+        self._st = _decode.DecodeState(self.streams, self.dim, self.value_dim, degree=self.degree,
+                                       block=self.block_size, scale=self.scale, compressor=self.compressor,
+                                       seed=self.seed, device=self.device, eps=self.denominator_eps)
+        self.sketch = _SketchView(self)
+        self.coreset = _CoresetView(self)
+
+    # ---- input handling ----
+    def _rows(self, x: Tensor, width: int, what: str) -> Tensor:
+        want = (width,) if self._single else (self.streams, width)
+        if tuple(x.shape) != want:
+            shape = f"[{width}]" if self._single else f"[{self.streams}, {width}]"
+            raise ValueError(f"{what} must have shape {shape}, got {tuple(x.shape)}")
+        return x.to(device=self.device, dtype=self.dtype).reshape(self.streams, width)
+
+    def _stats_buffer(self, return_stats: bool) -> Optional[Tensor]:
+        return torch.empty((self.streams, 4), device=self.device, dtype=torch.float32) if return_stats else None
+
+    def _finish(self, out: Tensor, stats: Optional[Tensor]):
+        out = out[0] if self._single else out
+        if stats is None:
+            return out
+        st = stats.cpu()
+        nbytes = self.state_size_bytes(include_feature_map=False)
+        if self._single:
+            s = AttentionQueryStats(float(st[0, 0]), float(st[0, 1]), float(st[0, 2]), self._st.num_items(), nbytes)
+        else:
+            s = AttentionQueryStats(st[:, 0], st[:, 1], st[:, 2], self._st.num_items(), nbytes)
+        return out, s
+
+    # ---- the reference API ----
+    @torch.no_grad()
+    def update(self, key: Tensor, value: Tensor) -> None:
+        """sketch.update(k, v); coreset.append(k, v) (streaming_taylor_coreset_attention.py:576-579)."""
+        self._st.update(self._rows(key, self.dim, "key"), self._rows(value, self.value_dim, "value"))
+
+    @torch.no_grad()
+    def query(self, query: Tensor, *, return_stats: bool = False) -> Union[Tensor, Tuple[Tensor, AttentionQueryStats]]:
+        """low + weighted exp_{>t} tail over items(), divided by clamp(den, eps)
+        (streaming_taylor_coreset_attention.py:581-609)."""
+        stats = self._stats_buffer(return_stats)
+        out = self._st.query(self._rows(query, self.dim, "query"), out_dtype=self.dtype, stats=stats)
+        return self._finish(out, stats)
+
+    def state_size_bytes(self, *, include_feature_map: bool = False) -> int:
+        """Bytes of the reference's state of one stream at the reference's dtype
+        (streaming_taylor_coreset_attention.py:611-612)."""
+        return self._st.reference_state_bytes(_elem(self.dtype), include_feature_map)
+
+    @property
+    def length(self) -> int:
+        return self._st.length
+
+    # ---- extensions ----
+    @torch.no_grad()
+    def step(self, query: Tensor, key: Tensor, value: Tensor, *, return_stats: bool = False):
+        """update(key, value) then query(query), in two kernel launches (plus the block compression
+        when the token completes a block)."""
+        stats = self._stats_buffer(return_stats)
+        out = self._st.step(self._rows(query, self.dim, "query"), self._rows(key, self.dim, "key"),
+                            self._rows(value, self.value_dim, "value"), out_dtype=self.dtype, stats=stats)
+        return self._finish(out, stats)
+
+    @torch.no_grad()
+    def extend(self, keys: Tensor, values: Tensor) -> None:
+        """update() with every row of keys [P, dim] ([S, P, dim] batched) and values, in bulk."""
+        if self._single:
+            if keys.ndim != 2 or keys.shape[-1] != self.dim or tuple(values.shape) != (keys.shape[0], self.value_dim):
+                raise ValueError("keys / values must have shapes [P, dim] / [P, value_dim]")
+            keys, values = keys[None], values[None]
+        self._st.extend(keys.to(device=self.device, dtype=self.dtype), values.to(device=self.device, dtype=self.dtype))
+
+    @torch.no_grad()
+    def prefill(self, q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+        """Outputs of update(k_i, v_i); query(q_i) for every row of a prompt ([P, dim], or [S, P, dim]
+        batched), leaving the state after the prompt.  Only on a fresh state."""
+        if self._st.length != 0:
+            raise ValueError("prefill starts from an empty state; use step() / extend() afterwards")
+        one = self._single
+        q3 = (q[None] if one else q).to(device=self.device, dtype=self.dtype).contiguous()
+        k3 = (k[None] if one else k).to(device=self.device, dtype=self.dtype).contiguous()
+        v3 = (v[None] if one else v).to(device=self.device, dtype=self.dtype).contiguous()
+        if (q3.ndim != 3 or q3.shape[0] != self.streams or q3.shape[-1] != self.dim or q3.shape != k3.shape
+                or tuple(v3.shape) != (self.streams, q3.shape[1], self.value_dim)):
+            raise ValueError("q, k, v must be [P, dim] / [P, value_dim] ([S, P, ...] batched)")
+        semantics = "exact" if self.compressor == "none" else "levels"
+        res = _engine.prefill(q3, k3, v3, degree=self.degree, block=self.block_size, scale=self.scale,
+                              semantics=semantics, compressor=self.compressor, seed=self.seed,
+                              eps=self.denominator_eps, out_dtype=self.dtype)
+        self._st.extend(k3, v3)
+        return res.out[0] if one else res.out

@@ -1,0 +1,245 @@
+"""GPU parity of the streaming decode path (ArticleStreamingAttention on the HIP decode kernels K5,
+through the C ABI): per-token update / query outputs against the reference's own outputs (golden
+fixtures) and the oracle, the level coresets bit-exact (kept token and weight of every item), the
+batched step / extend / prefill forms against the prefill kernels, the moment sketch against the
+closed-form feature sums, and the query statistics against the reference's low / tail split.
+Tolerances: fp32 rel-L2 <= 1e-4, bf16 inputs <= 5e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+import _engine
+import _native
+import reference_cpu as orc
+import streaming_taylor_coreset_attention as stc
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+FP32_TOL = 1e-4
+BF16_TOL = 5e-3
+LEVEL_CASES = ["levels_c1", "levels_random", "levels_deg3", "levels_oddblock", "levels_block2"]
+
+
+def rel(a, b):
+    return orc.rel_l2(torch.as_tensor(a).float().cpu(), torch.as_tensor(b).float().cpu())
+
+
+def t(x):
+    return torch.from_numpy(np.ascontiguousarray(x))
+
+
+def level_node(plan, lev, j):
+    ids = np.nonzero(plan.level_of[: plan.n_nodes] == lev)[0]
+    return int(ids[j])
+
+
+def final_level_nodes(plan, n, block):
+    """{level: node id} of the levels occupied after n tokens (counter c = n // block)."""
+    c = n // block
+    return {lev: level_node(plan, lev, (c >> lev) - 1) for lev in range(c.bit_length()) if (c >> lev) & 1}
+
+
+@pytest.mark.parametrize("name", LEVEL_CASES)
+def test_decode_matches_reference_goldens(golden, name):
+    """update(k_i, v_i); query(q_i) token by token == the reference's outputs; the final levels are
+    the reference's compress outputs (positions and weights, bit-exact)."""
+    g = golden(name)
+    m = g.meta
+    q, k, v = (t(g[x]) for x in "qkv")
+    n = q.shape[0]
+    st = stc.ArticleStreamingAttention(m["d"], m["dv"], degree=m["degree"], block_size=m["block"], scale=m["scale"],
+                                       compressor=m["compressor"], device=DEV, seed=m["seed"])
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = []
+    for i in range(n):
+        st.update(kd[i], vd[i])
+        outs.append(st.query(qd[i]))
+    out = torch.stack(outs)
+    assert rel(out, g["out"]) < FP32_TOL
+    assert st.length == n
+
+    plan = _engine._plan.levels_plan(n, m["block"], m["compressor"])
+    pos = st.coreset.level_positions()
+    levels = st.coreset.levels
+    for lev, node in final_level_nodes(plan, n, m["block"]).items():
+        slot = int(plan.desc[node, 6])
+        assert np.array_equal(pos[lev].cpu().numpy(), g[f"call{slot}_src_out"]), f"level {lev}"
+        assert np.array_equal(levels[lev].weights.cpu().numpy(), g[f"call{slot}_w_out"])
+        assert torch.equal(levels[lev].keys.cpu(), k[pos[lev].cpu().long()])
+    occupied = [lev for lev, lv in enumerate(levels) if lv is not None]
+    assert occupied == sorted(final_level_nodes(plan, n, m["block"]))
+
+
+def _data(streams, n, d, dv, seed, dtype=torch.float32, scale_in=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(streams, n, d, generator=g) * scale_in).to(dtype)
+    k = (torch.randn(streams, n, d, generator=g) * scale_in).to(dtype)
+    v = torch.randn(streams, n, dv, generator=g).to(dtype)
+    return q, k, v
+
+
+BATCH_CASES = [
+    # streams, n, d, dv, block, degree, compressor, scale, dtype, input scale
+    (5, 700, 32, 48, 64, 2, "sorted_pair", 0.3, torch.float32, 1.0),
+    (3, 400, 16, 64, 33, 3, "sorted_pair", 0.5, torch.float32, 1.0),
+    (4, 300, 8, 8, 16, 2, "random", 1.0, torch.float32, 0.5),
+    (2, 130, 12, 5, 2, 1, "sorted_pair", 1.0, torch.float32, 0.5),
+    (3, 200, 64, 64, 32, 2, "none", 0.125, torch.float32, 1.0),
+    (6, 600, 64, 64, 128, 2, "sorted_pair", 0.125, torch.bfloat16, 1.0),
+    (2, 300, 128, 130, 64, 2, "sorted_pair", None, torch.float32, 1.0),
+]
+
+
+@pytest.mark.parametrize("streams,n,d,dv,block,degree,comp,scale,dtype,xs", BATCH_CASES)
+def test_batched_step_matches_prefill(streams, n, d, dv, block, degree, comp, scale, dtype, xs):
+    """step() per token over S streams == the prefill kernels on the same [1, S, N, D] input (stream s
+    seeded seed + s); the final levels hold the prefill's selected tokens, bit-exact."""
+    q, k, v = _data(streams, n, d, dv, seed=n + d, dtype=dtype, scale_in=xs)
+    seed = 7
+    ref = stc.article_causal_attention(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=degree,
+                                       block_size=block, scale=scale, compressor=comp, seed=seed)[0]
+    st = stc.ArticleStreamingAttention(d, dv, degree=degree, block_size=block, scale=scale, compressor=comp,
+                                       device=DEV, dtype=dtype, seed=seed, streams=streams)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(n)], dim=1)
+    assert outs.dtype == dtype
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    assert rel(outs, ref) < tol
+    if comp != "none":
+        s = float(1.0 / np.sqrt(d)) if scale is None else scale
+        res = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=degree, block=block, scale=s,
+                              semantics="levels", compressor=comp, seed=seed)
+        src = res.node_src.cpu().numpy()
+        w = res.node_w.cpu().numpy()
+        pos = st.coreset.level_positions()
+        lw = st.coreset.levels
+        for lev, node in final_level_nodes(res.plan, n, block).items():
+            size = int(res.plan.meta[node, 0])
+            assert np.array_equal(pos[lev].cpu().numpy(), src[:, node, :size]), f"level {lev}"
+            assert np.array_equal(lw[lev].weights.float().cpu().numpy(), w[:, node, :size])
+
+
+@pytest.mark.parametrize("prefix", [0, 1, 64, 333])
+def test_extend_then_step(prefix):
+    """extend() over a prefix (any length, partial blocks included) then step() == prefill rows."""
+    streams, n, d, dv, block = 3, 520, 16, 16, 64
+    q, k, v = _data(streams, n, d, dv, seed=prefix)
+    ref = stc.article_causal_attention(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=2,
+                                       block_size=block, scale=0.5, seed=11)[0]
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=0.5, device=DEV, seed=11,
+                                       streams=streams)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    lo = 0
+    if prefix == 333:  # a partly filled buffer first
+        st.extend(kd[:, :40], vd[:, :40])
+        lo = 40
+    st.extend(kd[:, lo:prefix], vd[:, lo:prefix])
+    assert st.length == prefix
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(prefix, n)], dim=1)
+    assert rel(outs, ref[:, prefix:]) < FP32_TOL
+
+
+def test_prefill_then_step_bf16():
+    """prefill() of a prompt returns the prompt's outputs and leaves the state for decoding
+    (the decode workload's regime: q, k, v ~ N(0,1)/8, bf16, scale 1/8, block 256)."""
+    streams, n, p, d = 4, 900, 600, 64
+    q, k, v = _data(streams, n, d, d, seed=5, dtype=torch.bfloat16, scale_in=0.125)
+    ref = stc.article_causal_attention(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=2,
+                                       block_size=256, seed=0)[0]
+    st = stc.ArticleStreamingAttention(d, d, degree=2, block_size=256, device=DEV, dtype=torch.bfloat16,
+                                       streams=streams)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    head = st.prefill(qd[:, :p], kd[:, :p], vd[:, :p])
+    assert rel(head, ref[:, :p]) < BF16_TOL
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(p, n)], dim=1)
+    assert rel(outs, ref[:, p:]) < BF16_TOL
+
+
+def test_decode_vs_oracle_single_stream():
+    n, d, dv, block = 300, 8, 8, 16
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=9)
+    ref = orc.levels_forward(q, k, v, degree=2, block=block, scale=1.0, seed=4)
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=1.0, device=DEV, seed=4)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = torch.stack([st.step(qd[i], kd[i], vd[i]) for i in range(n)])
+    assert rel(out, ref) < FP32_TOL
+    # the oracle's literal level state after the same tokens
+    state = orc.LevelState()
+    orc.levels_forward(q, k, v, degree=2, block=block, scale=1.0, seed=4, state_out=state)
+    pos = st.coreset.level_positions()
+    for lev, lv in enumerate(state.levels):
+        if lv is None:
+            assert lev >= len(pos) or pos[lev] is None
+        else:
+            assert np.array_equal(pos[lev].cpu().numpy(), lv[0]) and np.array_equal(
+                st.coreset.levels[lev].weights.cpu().numpy(), lv[1])
+
+
+def test_sketch_moments_closed_form():
+    """den_moments / num_moments (reference order, per degree) == sum_j phi_k(k_j) [1, v_j] in fp64."""
+    n, d, dv = 150, 6, 5
+    g = torch.Generator().manual_seed(2)
+    k = torch.randn(n, d, generator=g) * 0.5
+    v = torch.randn(n, dv, generator=g)
+    st = stc.ArticleStreamingAttention(d, dv, degree=3, block_size=32, device=DEV)
+    st.extend(k[:100].to(DEV), v[:100].to(DEV))
+    for i in range(100, n):
+        st.update(k[i].to(DEV), v[i].to(DEV))
+    phi = orc.features(k.double(), 3, key_side=True)
+    den = torch.cat([x.cpu().double() for x in st.sketch.den_moments])
+    num = torch.cat([x.cpu().double() for x in st.sketch.num_moments])
+    assert [x.shape[0] for x in st.sketch.den_moments] == [1, 6, 21, 56]
+    assert rel(den, phi.sum(0)) < 1e-6
+    assert rel(num, phi.T @ v.double()) < 1e-6
+
+
+def test_query_stats_split():
+    """return_stats: denominator = low + tail, with the reference's split: low over every token (the
+    sketch holds the buffered tokens too), tail over items() = buffer (weight 1) + levels."""
+    n, d, dv, block, s = 77, 8, 4, 16, 0.7
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=3)
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=s, device=DEV, seed=1)
+    st.extend(k[: n - 1].to(DEV), v[: n - 1].to(DEV))
+    st.update(k[n - 1].to(DEV), v[n - 1].to(DEV))
+    out, stats = st.query(q[n - 1].to(DEV), return_stats=True)
+    x = (k.double() @ q[n - 1].double()) * s
+    low = orc.exp_taylor(x, 2).sum().item()
+    items = st.coreset.items()
+    xi = (items.keys.cpu().double() @ q[n - 1].double()) * s
+    tail = (items.weights.cpu().double() * (torch.exp(xi) - orc.exp_taylor(xi, 2))).sum().item()
+    assert abs(stats.low_denominator - low) < 1e-5 * abs(low)
+    assert abs(stats.tail_denominator - tail) < 2e-5 * abs(low + tail)
+    assert abs(stats.denominator - (low + tail)) < 1e-5 * abs(low + tail)
+    assert stats.coreset_items == items.size == (n % block) + (block // 2) * bin(n // block).count("1")
+    assert stats.state_bytes == st.state_size_bytes()
+
+
+def test_state_size_matches_trace():
+    """state_size_bytes() after every token == the reference's state-size formula."""
+    n, d, dv, block = 100, 4, 3, 8
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=1)
+    trace = stc.state_size_trace(n, d, dv, 2, block, "sorted_pair", 4)
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=1.0, device=DEV)
+    for i in range(n):
+        st.update(k[i].to(DEV), v[i].to(DEV))
+        assert st.state_size_bytes() == trace[i]
+        assert st.coreset.num_items() == (i + 1) % block + (block // 2) * bin((i + 1) // block).count("1")
+
+
+def test_decode_errors():
+    st = stc.ArticleStreamingAttention(8, 4, device=DEV)
+    with pytest.raises(ValueError):
+        st.update(torch.zeros(7, device=DEV), torch.zeros(4, device=DEV))
+    with pytest.raises(ValueError):
+        st.query(torch.zeros(2, 8, device=DEV))
+    with pytest.raises(ValueError):
+        stc.ArticleStreamingAttention(8, 4, block_size=1, device=DEV)
+    bad = stc.ArticleStreamingAttention(4, 2, block_size=2, compressor="bogus", device=DEV)
+    bad.update(torch.zeros(4, device=DEV), torch.zeros(2, device=DEV))
+    with pytest.raises(ValueError):
+        bad.update(torch.zeros(4, device=DEV), torch.zeros(2, device=DEV))
+    lib = _native.lib()
+    assert lib.sta_decode_compress(1, 4, 2, None, None, 2, 0, None, None, None, None, 1, 1, 1, None, None, None,
+                                   None, 2, None) == _native.STA_ERR_ARG

@@ -236,3 +236,62 @@ def test_stats_formulas_match_reference(golden):
     st = faa._stats(200, 16, 8, 4, 2, 32, "sorted_pair", 2048, "stream", "cpu")
     assert [st.degree, st.block_size, st.feature_count, st.coreset_items, st.approx_streaming_state_bytes,
             st.scratch_low_prefix_bytes, st.scratch_residual_matrix_bytes] == ref
+
+
+# --------------------------------------------------------------------------- decode host logic
+
+def test_library_decode_entries_reject_bad_arguments():
+    lib = _native.load_library()
+    assert lib.sta_moment_accumulate(None, None, 0, 1, 1, 1, 4, 1, 32, 2, 1, 9, None, None, None, 15, None, None,
+                                     None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_moments(None, 0, 1, 4, 4, 1.0, None, None, 15, None, 1, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_tail(None, None, None, 0, 1, 4, 4, 2, 1.0, 1e-12, 8, None, None, 16, 0, None, None, None, 0,
+                               8, 0, None, None, 1, None, 0, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_compress(1, 4, 2, None, None, 2, 0, None, None, None, None, 1, 1, 1, None, None, None,
+                                   None, 2, None) == _native.STA_ERR_ARG
+    assert _native.decode_layout(6, 5) == (8, 32)
+    assert _native.decode_layout(64, 130) == (64, 160)
+
+
+@pytest.mark.parametrize("d,degree", [(4, 2), (5, 3), (64, 2), (16, 3), (3, 0), (7, 1)])
+def test_feature_index_is_reference_order(d, degree):
+    idx = _plan.feature_index(d, degree)
+    combos = orc.monomials(d, degree)
+    assert idx.shape == (len(combos),)
+    for f, c in enumerate(combos):
+        full = list(c) + [d] * (3 - len(c))
+        assert int(idx[f]) == full[0] | (full[1] << 8) | (full[2] << 16)
+
+
+@pytest.mark.parametrize("width,d,degree,bh,dv", [(64, 64, 2, 2048, 64), (8, 6, 3, 1, 5), (16, 16, 3, 96, 64),
+                                                  (8, 5, 2, 3, 16), (128, 128, 2, 2, 130), (4, 4, 1, 7, 3)])
+def test_split_state_rows_cover_reference_features(width, d, degree, bh, dv):
+    """Every reference feature of dimension d has exactly one slot in the accumulate table; each slot's
+    monomial (the quad's factors) is that feature's monomial."""
+    ft = _plan.feature_tiles(width, degree)
+    opts = ((2, 2), (4, 2), (5, 2), (9, 2), (16, 1)) if degree < 3 else ((4, 2), (8, 1), (16, 1))
+    ms = _plan.moment_split(ft, bh, dv, opts)
+    rows = _plan.split_state_rows(ft, ms, d)
+    order = _plan.reference_feature_order(d, degree)
+    inv = {f: c for c, f in order.items()}
+    assert sorted(r for r in rows if r >= 0) == list(range(_plan.num_features(d, degree)))
+    quads = ms.quads.reshape(-1, 4)  # [parts * wave_tiles, 4]
+    coef = ms.coef.reshape(-1, 16)
+    for slot, r in enumerate(rows):
+        if r < 0:
+            continue
+        tile, q, s = slot // 16, (slot % 16) // 4, slot % 4
+        pq = int(quads[tile, q])
+        fac = sorted(f for f in (pq & 255, ((pq >> 8) & 255) + s, (pq >> 16) & 255) if f < width)
+        assert tuple(fac) == inv[r]
+        assert coef[tile, slot % 16] == np.float32(orc.inv_multinomial(inv[r]))
+
+
+@pytest.mark.parametrize("block,comp", [(16, "sorted_pair"), (33, "sorted_pair"), (2, "sorted_pair"), (32, "random")])
+def test_completion_calls_follow_the_level_plan(block, comp):
+    """Concatenating the per-completion call sizes of blocks 1..C gives the level plan's call order."""
+    c = 37
+    sizes = []
+    for b in range(c):
+        sizes += _plan.completion_call_sizes(b, block, comp)
+    assert sizes == _plan.levels_plan(c * block, block, comp).call_sizes

@@ -330,3 +330,22 @@ def test_planted_taylor_mistake_is_caught(golden, monkeypatch):
     monkeypatch.setattr(orc, "features", lambda x, deg, ks: real(x, min(deg, 1), ks))
     num, den = orc.low_sums_stream(q, k, v, 2, 1.0)
     assert rel(den, g["low_den"]) > 1e-4
+
+
+def test_streaming_object_matches_levels_forward():
+    """The per-token restatement of the reference's streaming object (reference-style torch projection
+    and argsort) gives the vectorised level semantics' outputs."""
+    n, d, dv, block = 200, 6, 4, 16
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=2)
+    ref = orc.levels_forward(q, k, v, degree=2, block=block, scale=0.8, seed=5, reference_scores=True)
+    st = orc.StreamingAttentionCPU(d, dv, degree=2, block=block, scale=0.8, seed=5)
+    outs = []
+    for i in range(n):
+        st.update(k[i], v[i])
+        outs.append(st.query(q[i]))
+    assert orc.rel_l2(torch.stack(outs), ref) < 1e-5
+
+
+def test_decode_timing_sample_runs():
+    t = orc.time_decode_sample(dim=8, value_dim=8, degree=2, block=16, scale=0.5, prefix=100, steps=40)
+    assert t["s_per_step"] > 0 and t["steps"] == 40
