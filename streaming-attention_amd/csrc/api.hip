@@ -26,10 +26,10 @@ constexpr int kMaxDegree = 3;
 constexpr int kTileRows = 128;
 
 // ---------------------------------------------------------------- moments dispatch
-template <int NT, bool DEG3, bool DBIG>
+template <int NT, bool DEG3, bool DBIG, int ES>
 int launch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG>;
+  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -39,10 +39,10 @@ int launch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   return check_launch();
 }
 
-template <int NT, bool DEG3, bool DBIG>
+template <int NT, bool DEG3, bool DBIG, int ES>
 int launch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_acc_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moment_accumulate_kernel<NT, DEG3, DBIG>;
+  auto fn = sta::moment_accumulate_kernel<NT, DEG3, DBIG, ES>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -72,8 +72,16 @@ int moment_wave_tiles(int d, int degree, int want) {
   return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
 }
 
+// Instantiated per element size (4: fp32, 2: bf16 / fp16) so the chunk staging is straight-line code.
+template <int NT, bool D3, bool BIG>
+int launch_mom_es(const sta::MomArgs& a, int64_t bh, hipStream_t s, bool accumulate) {
+  if (a.esize == 4)
+    return accumulate ? launch_accumulate<NT, D3, BIG, 4>(a, bh, s) : launch_moments<NT, D3, BIG, 4>(a, bh, s);
+  return accumulate ? launch_accumulate<NT, D3, BIG, 2>(a, bh, s) : launch_moments<NT, D3, BIG, 2>(a, bh, s);
+}
+
 #define STA_MOM_CASE(NT, D3, BIG) \
-  case NT: return accumulate ? launch_accumulate<NT, D3, BIG>(a, bh, s) : launch_moments<NT, D3, BIG>(a, bh, s);
+  case NT: return launch_mom_es<NT, D3, BIG>(a, bh, s, accumulate);
 
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3, bool accumulate) {
   if (a.d <= 64) {

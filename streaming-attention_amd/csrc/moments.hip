@@ -123,12 +123,12 @@ struct MomSlots {
   int v_col;        // first column (within the group of 32) of the unit, or -1 when unused
 };
 
-template <bool DBIG>
+template <bool DBIG, int ES>
 __device__ __forceinline__ MomSlots<DBIG> mom_slots(const MomArgs& a, int col0, int dummy) {
   constexpr int LDQ = mom_ldq(DBIG);
   MomSlots<DBIG> sl;
   const int tid = threadIdx.x;
-  const int epu = 16 / a.esize;
+  constexpr int epu = 16 / ES;
   const int uq = a.d / epu;  // units per q/k row
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
@@ -143,17 +143,17 @@ __device__ __forceinline__ MomSlots<DBIG> mom_slots(const MomArgs& a, int col0, 
     sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
   const int uv = tid >> 5;  // unit of the workgroup's 32 columns
-  sl.v_off = static_cast<uint32_t>((col0 + min(uv * epu, 32 - epu)) * a.esize);
+  sl.v_off = static_cast<uint32_t>((col0 + min(uv * epu, 32 - epu)) * ES);
   sl.v_col = uv * epu < 32 ? uv * epu : -1;
   return sl;
 }
 
 __device__ __forceinline__ int clamp_row(int row, int n) { return min(max(row, 0), n - 1); }
 
-template <bool DBIG>
+template <bool DBIG, int ES>
 __device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
                                          const char* qh, const char* kh, const char* vh, int row0) {
-  const uint32_t qrow = static_cast<uint32_t>(a.d * a.esize), vrow = static_cast<uint32_t>(a.ldv * a.esize);
+  const uint32_t qrow = static_cast<uint32_t>(a.d * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
   const int ktok = row0 + (threadIdx.x & (MOM_C - 1));
   const uint32_t krow = static_cast<uint32_t>(clamp_row(ktok, a.n));
 #pragma unroll
@@ -165,9 +165,11 @@ __device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomSlots<DBIG
   st.v = *reinterpret_cast<const uint4*>(vh + krow * vrow + sl.v_off);
 }
 
-// The 16-byte unit u as 4 (fp32) or 8 (bf16 / fp16) floats; only f[0..16/esize) are meaningful.
+// The 16-byte unit u as 4 (fp32, ES = 4) or 8 (bf16 / fp16, ES = 2) floats; only f[0..16/ES) are
+// meaningful.
+template <int ES>
 __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f)[8]) {
-  if (dtype == F32) {
+  if constexpr (ES == 4) {
     f[0] = __uint_as_float(u.x);
     f[1] = __uint_as_float(u.y);
     f[2] = __uint_as_float(u.z);
@@ -191,7 +193,7 @@ __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f
   }
 }
 
-template <bool DBIG>
+template <bool DBIG, int ES>
 __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
                                           float* buf, int dummy_rel, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
@@ -203,17 +205,17 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
   const int tok = tid & (MOM_C - 1);
   const bool tok_ok = row0 + tok >= 0 && row0 + tok < a.n;
   const float kok = tok_ok ? 1.f : 0.f;
-  const bool wide = a.esize == 2;  // 8 elements per unit
+  constexpr bool wide = ES == 2;  // 8 elements per unit
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
     const int row = row0 + sl.q_tok[j];
     const float sc = (sl.q_use[j] && row >= 0 && row < a.n) ? a.scale : 0.f;
     float f[8];
-    unit_floats(st.q[j], a.dtype, f);
+    unit_floats<ES>(st.q[j], a.dtype, f);
     float* qd = sl.q_use[j] ? Qs + sl.q_lds[j] : dmy;
     *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
-    if (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
-    unit_floats(st.k[j], a.dtype, f);
+    if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
+    unit_floats<ES>(st.k[j], a.dtype, f);
     const int kd = sl.k_dim[j];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
@@ -225,7 +227,7 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
   }
   {
     float f[8];
-    unit_floats(st.v, a.dtype, f);
+    unit_floats<ES>(st.v, a.dtype, f);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       if (m < 4 || wide) {
@@ -242,8 +244,9 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
 }
 
 // Fixed-order sum of the 4 waves' partials of the chunk starting at row0, stored unconditionally:
-// low_num rows of the workgroup's 32 columns and the low_den rows (the column-group workgroups of a
-// feature split compute bit-identical denominators, so all of them store it).
+// low_num rows of the workgroup's 32 columns and, for the workgroup that keeps the denominator column
+// (DEN), the low_den rows.
+template <bool DEN>
 __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
                                                  int col0) {
   const int tid = threadIdx.x;
@@ -254,11 +257,13 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
   float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
 #pragma unroll
   for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
-  const int tok = tid & (MOM_C - 1);
-  float den = red[32 * MOM_LDR + tok];
+  if constexpr (DEN) {
+    const int tok = tid & (MOM_C - 1);
+    float den = red[32 * MOM_LDR + tok];
 #pragma unroll
-  for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[(ww * 33 + 32) * MOM_LDR + tok];
-  a.low_den[obase + row0 + tok] = den;
+    for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[(ww * 33 + 32) * MOM_LDR + tok];
+    a.low_den[obase + row0 + tok] = den;
+  }
 }
 
 // Per-lane feature offsets of a wave's NT tiles (constant over the sequence).  Query side: columns of
@@ -293,7 +298,7 @@ __device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t 
 // its 32 columns, den_s[f] += phi_k(tok)[f].  Token steps outermost over all tiles (2 NT independent
 // chains), in two halves of 4 steps; the keys of the second half are read while the first half's
 // MFMAs issue.  `mid()` runs after the first key reads are issued (work to hide under them).
-template <int NT, bool DEG3, class Mid>
+template <int NT, bool DEG3, bool DEN, class Mid>
 __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, const float* Kt, const float* Vt,
                                            const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
   constexpr int CT = 2;
@@ -328,26 +333,33 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, c
         float x = fa[h][kt][e] * fb[h][kt][e];
         if (DEG3) x *= fc[h][DEG3 ? kt : 0][e];
         x *= m.kcoef[kt];
-        dacc[kt] += x;
+        if constexpr (DEN) dacc[kt] += x;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma4(x, vv[h][ct][e], st[kt][ct]);
       }
+      if constexpr (DEN) {
 #pragma unroll
-      for (int kt = 0; kt < NT; ++kt) pin(dacc[kt]);
+        for (int kt = 0; kt < NT; ++kt) pin(dacc[kt]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if constexpr (DEN) {
 #pragma unroll
-  for (int kt = 0; kt < NT; ++kt) {
-    float s = dacc[kt];
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
-    if (lg == 0) den_s[16 * kt + li] += s;
+    for (int kt = 0; kt < NT; ++kt) {
+      float s = dacc[kt];
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      if (lg == 0) den_s[16 * kt + li] += s;
+    }
   }
 }
 
-template <int NT, bool DEG3, bool DBIG>
-__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
+// The kernel body for one workgroup (head bh, feature split fs, column group cs).  DEN: this
+// workgroup also keeps the denominator column (only column group 0 does; the others would compute
+// bit-identical values).
+template <int NT, bool DEG3, bool DBIG, int ES, bool DEN>
+__device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int BUF = mom_buf_floats(DBIG);
   constexpr int CT = 2;           // 16-column tiles per wave
@@ -359,12 +371,6 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
   float* den_all = red_all + 2 * mom_red_floats();  // [4 waves][NT * 16]
   const int dummy_abs = 2 * BUF + 2 * mom_red_floats() + MOM_WAVES * NT * 16;  // 8 floats, write-only
 
-  const int per_head = a.fsplit * a.csplit;
-  const int wg = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t bh = wg / per_head;
-  const int rem = wg - static_cast<int>(bh) * per_head;
-  const int fs = rem / a.csplit;
-  const int cs = rem - fs * a.csplit;
   const int col0 = 32 * cs;
 
   const int tid = threadIdx.x;
@@ -386,18 +392,18 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
   const int nchunks = (n + a.shift + MOM_C - 1) / MOM_C;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
   const int first = -a.shift;
-  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * a.esize;
-  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * a.esize;
-  const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * a.esize;
-  const MomSlots<DBIG> sl = mom_slots<DBIG>(a, col0, dummy_abs);
+  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
+  const MomSlots<DBIG> sl = mom_slots<DBIG, ES>(a, col0, dummy_abs);
 
   // zero both chunk buffers (their padding rows / columns are never written again) and the denominators
   for (int e = tid; e < 2 * BUF; e += MOM_THREADS) smem[e] = 0.f;
   for (int e = tid; e < MOM_WAVES * NT * 16; e += MOM_THREADS) den_all[e] = 0.f;
   __syncthreads();
   MomStage<DBIG> pre;
-  mom_load<DBIG>(pre, sl, a, qh, kh, vh, first);
-  mom_store<DBIG>(pre, sl, a, smem, dummy_abs, first);
+  mom_load<DBIG, ES>(pre, sl, a, qh, kh, vh, first);
+  mom_store<DBIG, ES>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
@@ -408,7 +414,7 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
 
     // prefetch chunk c+1 (unconditional, clamped); staged after the query phase
-    mom_load<DBIG>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
+    mom_load<DBIG, ES>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
 
     // ---- query with the state of all previous chunks: two accumulator sets (tile parity), so 8
     //      independent MFMA chains; tile kt+1's operands are read during tile kt ----
@@ -431,7 +437,7 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
           x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[kt]);
           if (DEG3) x2[buf][tt] = qrow[16 * tt * LDQ + m.qc[DEG3 ? kt : 0]];
         }
-        dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
+        if constexpr (DEN) dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
       };
       qload(0, 0);
 #pragma unroll
@@ -444,13 +450,15 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
           for (int tt = 0; tt < TT; ++tt) {
             float x = x0[cb][tt] * x1[cb][tt][s];
             if (DEG3) x *= x2[cb][tt];
-            dq[tt] = fmaf(x, dn[cb][s], dq[tt]);
+            if constexpr (DEN) dq[tt] = fmaf(x, dn[cb][s], dq[tt]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) o[cb][tt][ct] = mfma4(x, st[kt][ct][s], o[cb][tt][ct]);
           }
         }
+        if constexpr (DEN) {
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt) pin(dq[tt]);
+          for (int tt = 0; tt < TT; ++tt) pin(dq[tt]);
+        }
         __builtin_amdgcn_sched_barrier(0);  // keep the one-tile-ahead pipeline shape
       }
     }
@@ -463,24 +471,64 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
           *reinterpret_cast<floatx4*>(rw + (16 * ct + li) * MOM_LDR + 16 * tt + 4 * lg) = o[0][tt][ct] + o[1][tt][ct];
-        float s = dq[tt];
-        s += __shfl_xor(s, 16);
-        s += __shfl_xor(s, 32);
-        if (lg == 0) rw[32 * MOM_LDR + 16 * tt + li] = s;
+        if constexpr (DEN) {
+          float s = dq[tt];
+          s += __shfl_xor(s, 16);
+          s += __shfl_xor(s, 32);
+          if (lg == 0) rw[32 * MOM_LDR + 16 * tt + li] = s;
+        }
       }
     }
     // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
-    if (c + 1 < nchunks) mom_store<DBIG>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
+    if (c + 1 < nchunks) mom_store<DBIG, ES>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
     //      key reads ----
-    mom_update<NT, DEG3>(st, den_s, Kt, Vt, m, li, lg, [&]() {
-      if (c > 0) mom_reduce_store(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
+    mom_update<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, [&]() {
+      if (c > 0) mom_reduce_store<DEN>(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
     });
     __syncthreads();
   }
-  mom_reduce_store(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C, col0);
+  mom_reduce_store<DEN>(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C,
+                        col0);
+}
+
+// Workgroup -> (head, feature split, column group).  Workgroups are dispatched round-robin over the 8
+// XCDs and, within an XCD, one per compute unit before a compute unit gets its second one.  When the
+// grid divides evenly, the first wave of an XCD's workgroups takes column group 0 and the next column
+// group 1, ..., over the (head, feature split) pairs of that XCD: every compute unit then holds one
+// workgroup that keeps the denominator column and one that does not, and a head's workgroups share
+// one L2.  Otherwise the plain XCD-contiguous order.
+__device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int& fs, int& cs) {
+  const int total = gridDim.x;
+  const int nper = total >> 3;
+  if ((total & 7) == 0 && nper % a.csplit == 0) {
+    const int per_cs = nper / a.csplit;
+    const int x = blockIdx.x & 7, p = blockIdx.x >> 3;
+    cs = p / per_cs;
+    const int hf = x * per_cs + (p - cs * per_cs);
+    bh = hf / a.fsplit;
+    fs = hf - static_cast<int>(bh) * a.fsplit;
+    return;
+  }
+  const int per_head = a.fsplit * a.csplit;
+  const int wg = xcd_remap(blockIdx.x, total);
+  bh = wg / per_head;
+  const int rem = wg - static_cast<int>(bh) * per_head;
+  fs = rem / a.csplit;
+  cs = rem - fs * a.csplit;
+}
+
+template <int NT, bool DEG3, bool DBIG, int ES>
+__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
+  int64_t bh;
+  int fs, cs;
+  mom_workgroup(a, bh, fs, cs);
+  if (cs == 0)
+    moments_body<NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
+  else
+    moments_body<NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
 }
 
 // Shared-memory floats of moment_accumulate_kernel: one chunk buffer, the running denominators, a dummy.
@@ -496,7 +544,7 @@ __host__ __device__ constexpr int mom_acc_smem_floats(bool dbig, int nt) {
 // the accumulators at the start and written back at the end (each (head, feature, column) belongs to
 // exactly one wave of the grid, so the read-modify-write has no race).  Rows [0, n) of every head are
 // read at k + bh * head_rows * d (v: ldv).
-template <int NT, bool DEG3, bool DBIG>
+template <int NT, bool DEG3, bool DBIG, int ES>
 __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const MomArgs a) {
   constexpr int BUF = mom_buf_floats(DBIG);
   constexpr int CT = 2;
@@ -539,20 +587,20 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
     }
   }
 
-  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.d * a.esize;
-  const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * a.esize;
-  const MomSlots<DBIG> sl = mom_slots<DBIG>(a, col0, dummy_abs);
+  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.d * ES;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * ES;
+  const MomSlots<DBIG> sl = mom_slots<DBIG, ES>(a, col0, dummy_abs);
   const int nchunks = static_cast<int>((a.n + MOM_C - 1) / MOM_C);
   for (int e = tid; e < BUF; e += MOM_THREADS) smem[e] = 0.f;  // padding rows / columns stay 0
   for (int c = 0; c < nchunks; ++c) {
     MomStage<DBIG> stg;
-    mom_load<DBIG>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
+    mom_load<DBIG, ES>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
     __syncthreads();  // the previous chunk's update is done with the buffer
-    mom_store<DBIG>(stg, sl, a, smem, dummy_abs, c * MOM_C);
+    mom_store<DBIG, ES>(stg, sl, a, smem, dummy_abs, c * MOM_C);
     __syncthreads();
     const float* Kt = smem + MOM_C * mom_ldq(DBIG);
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
-    mom_update<NT, DEG3>(st, den_s, Kt, Vt, m, li, lg, []() {});
+    mom_update<NT, DEG3, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
   }
 
   // ---- write the slice back (the denominators once per feature split) ----
