@@ -14,6 +14,11 @@
 // fp32; stable ascending sort of (score, position); pair p = sorted positions (2p, 2p+1); keep the
 // first with probability w_a / max(w_a + w_b, 1e-30) (u_p < prob); the kept item carries w_a + w_b;
 // an odd last item is kept with its own weight.
+//
+// A node is latency-bound work for one workgroup: every thread scores its own items straight from
+// the key rows (16-byte loads, fp64 chain in dimension order), then the sorted order comes from one
+// rank computation per item (count of smaller keys plus equal keys at lower positions), so the whole
+// call needs three barriers.
 #include "common.hpp"
 
 namespace sta {
@@ -23,7 +28,6 @@ enum NodeMethod : int { M_COPY = 0, M_SORTED_PAIR = 1, M_PERM = 2 };
 constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, unused
 constexpr int CMP_MAX_IN = 1024;
 constexpr int CMP_THREADS = 256;
-constexpr int CMP_STAGE = 32;  // key rows staged in LDS at a time for the scores
 
 struct CompressArgs {
   const void* k;
@@ -43,40 +47,71 @@ struct CompressArgs {
   float* node_w;      // [BH][n_nodes][cap]
 };
 
-__device__ __forceinline__ bool key_greater(float sa, int pa, float sb, int pb) {
-  return sa > sb || (sa == sb && pa > pb);
-}
-
-// Projection score <row, dir>: fp64 accumulation in dimension order, rounded to fp32 once (every fp32 x
-// fp32 product is exact in fp64, so the score is a fixed function of the inputs).
-__device__ __forceinline__ float projection_score(const float* row, int row_stride, const float* dir, int d) {
+// Projection score <row, dir> of one key row: fp64 accumulation in dimension order, rounded to fp32
+// once (every fp32 x fp32 product is exact in fp64, so the score is a fixed function of the inputs).  The
+// row starts at element offset `off` of k (fp32 / bf16 / fp16) and is read in 16-byte units when `vec`
+// (row start 16-byte aligned and d a whole number of units).
+__device__ __forceinline__ float projection_score_row(const void* k, int64_t off, int d, int dtype, bool vec,
+                                                      const float* dir) {
   double acc = 0.0;
-  for (int col = 0; col < d; ++col)
-    acc = fma(static_cast<double>(row[col * row_stride]), static_cast<double>(dir[col]), acc);
+  if (vec && dtype == F32) {
+    const floatx4* r = reinterpret_cast<const floatx4*>(static_cast<const float*>(k) + off);
+    for (int u = 0; u < d / 4; ++u) {
+      const floatx4 x = r[u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fma(static_cast<double>(x[e]), static_cast<double>(dir[4 * u + e]), acc);
+    }
+  } else if (vec) {
+    const uint4* r = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(k) + off);
+    for (int u = 0; u < d / 8; ++u) {
+      const uint4 x = r[u];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t h = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+        const float f = dtype == BF16 ? __uint_as_float(static_cast<uint32_t>(h) << 16)
+                                      : static_cast<float>(__builtin_bit_cast(_Float16, h));
+        acc = fma(static_cast<double>(f), static_cast<double>(dir[8 * u + e]), acc);
+      }
+    }
+  } else {
+    for (int col = 0; col < d; ++col)
+      acc = fma(static_cast<double>(load_elem(k, off + col, dtype)), static_cast<double>(dir[col]), acc);
+  }
   return static_cast<float>(acc);
 }
 
-// Ascending bitonic sort of (key, pos) pairs in LDS, np a power of two, ties broken by position (a
-// stable order); all `nthreads` threads of the workgroup take part.
-__device__ __forceinline__ void bitonic_sort_pairs(float* key_s, int* pos_s, int np, int tid, int nthreads) {
-  for (int size = 2; size <= np; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < (np >> 1); t += nthreads) {
-        const int i = 2 * t - (t & (stride - 1));
-        const int j = i + stride;
-        const bool up = (i & size) == 0;
-        const float si = key_s[i], sj = key_s[j];
-        const int pi = pos_s[i], pj = pos_s[j];
-        if (key_greater(si, pi, sj, pj) == up) {
-          key_s[i] = sj;
-          key_s[j] = si;
-          pos_s[i] = pj;
-          pos_s[j] = pi;
-        }
-      }
-      __syncthreads();
+// Unsigned key whose order is the float order (-0 = +0; NaN above everything), so that (key, position)
+// is a strict total order and the ranks below are a permutation whatever the scores are.
+__device__ __forceinline__ uint32_t sort_key(float f) {
+  if (f == 0.f) return 0x80000000u;
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Stable ascending order of n keys (ties by position): pos_s[rank(i)] = i with rank(i) = #{j: key_j <
+// key_i} + #{j < i: key_j == key_i}.  key_s holds the scores on entry (overwritten with sort keys);
+// n <= CMP_MAX_IN; two barriers.
+__device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int tid, int nthreads) {
+  uint32_t* uk = reinterpret_cast<uint32_t*>(key_s);
+  for (int i = tid; i < n; i += nthreads) uk[i] = sort_key(key_s[i]);
+  for (int i = n + tid; i < ((n + 3) & ~3); i += nthreads) uk[i] = 0xffffffffu;  // padding of the 4-wide reads
+  __syncthreads();
+  for (int i = tid; i < n; i += nthreads) {
+    const uint32_t me = uk[i];
+    int rank = 0;
+    const int n4 = (n + 3) & ~3;
+    for (int j = 0; j < n4; j += 4) {
+      const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
+      rank += (o.x < me || (o.x == me && j + 0 < i)) ? 1 : 0;
+      rank += (o.y < me || (o.y == me && j + 1 < i)) ? 1 : 0;
+      rank += (o.z < me || (o.z == me && j + 2 < i)) ? 1 : 0;
+      rank += (o.w < me || (o.w == me && j + 3 < i)) ? 1 : 0;
     }
+    pos_s[rank] = i;
   }
+  __syncthreads();
 }
 
 // Keep-first decision of the weighted pair rule: u < w_a / max(w_a + w_b, 1e-30)
@@ -89,9 +124,8 @@ __device__ __forceinline__ bool pair_keeps_first(float u, float wa, float wb) {
 __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
   __shared__ int src_s[CMP_MAX_IN];
   __shared__ float w_s[CMP_MAX_IN];
-  __shared__ float key_s[CMP_MAX_IN];
+  __shared__ __align__(16) float key_s[CMP_MAX_IN];
   __shared__ int pos_s[CMP_MAX_IN];
-  __shared__ float rows[CMP_STAGE * 129];
   __shared__ float dir_s[128];
 
   const int node = a.batch[blockIdx.x];
@@ -141,34 +175,17 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
     return;
   }
 
-  // ---- sorted_pair: projection scores (fp64 accumulation, fixed index order) ----
+  // ---- sorted_pair: projection scores (fp64 accumulation, fixed index order), one item per thread ----
   const float* dir = a.dirs + (bh * a.n_draws + slot) * a.d;
   for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = dir[e];
-  const int LD = a.d + 1;
-  for (int base = 0; base < n_in; base += CMP_STAGE) {
-    const int cnt = min(CMP_STAGE, n_in - base);
-    __syncthreads();
-    for (int e = tid; e < cnt * a.d; e += CMP_THREADS) {
-      const int r = e / a.d, col = e - r * a.d;
-      const int64_t tok = src_s[base + r];
-      rows[r * LD + col] = load_elem(a.k, (bh * a.n + tok) * a.d + col, a.dtype);
-    }
-    __syncthreads();
-    if (tid < cnt) {
-      key_s[base + tid] = projection_score(rows + tid * LD, 1, dir_s, a.d);
-      pos_s[base + tid] = base + tid;
-    }
-  }
-  int np = 1;
-  while (np < n_in) np <<= 1;
-  for (int i = n_in + tid; i < np; i += CMP_THREADS) {
-    key_s[i] = __builtin_huge_valf();
-    pos_s[i] = i;
-  }
   __syncthreads();
+  const int epu = a.dtype == F32 ? 4 : 8;
+  const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
+  for (int i = tid; i < n_in; i += CMP_THREADS)
+    key_s[i] = projection_score_row(a.k, (bh * a.n + src_s[i]) * a.d, a.d, a.dtype, vec, dir_s);
 
-  // ---- bitonic sort of (score, position), ascending ----
-  bitonic_sort_pairs(key_s, pos_s, np, tid, CMP_THREADS);
+  // ---- stable ascending order of (score, position) ----
+  rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
 
   // ---- pair selection with weight transfer ----
   const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);

@@ -334,7 +334,7 @@ __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecC
   __shared__ int in_h[CMP_MAX_IN];
   __shared__ float in_w[CMP_MAX_IN];
   __shared__ int in_p[CMP_MAX_IN];
-  __shared__ float key_s[CMP_MAX_IN];
+  __shared__ __align__(16) float key_s[CMP_MAX_IN];
   __shared__ int pos_s[CMP_MAX_IN];
   __shared__ int cur_h[CMP_MAX_IN / 2 + 1];
   __shared__ float cur_w[CMP_MAX_IN / 2 + 1];
@@ -393,18 +393,9 @@ __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecC
       // sorted_pair: fp64 projection scores of the input rows, stable ascending sort, pair selection
       for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = a.dirs[slot * a.d + e];
       __syncthreads();
-      for (int j = tid; j < n; j += CMP_THREADS) {
-        key_s[j] = projection_score(key_row(in_h[j]), 1, dir_s, a.d);
-        pos_s[j] = j;
-      }
-      int np = 1;
-      while (np < n) np <<= 1;
-      for (int j = n + tid; j < np; j += CMP_THREADS) {
-        key_s[j] = __builtin_huge_valf();
-        pos_s[j] = j;
-      }
-      __syncthreads();
-      bitonic_sort_pairs(key_s, pos_s, np, tid, CMP_THREADS);
+      for (int j = tid; j < n; j += CMP_THREADS)
+        key_s[j] = projection_score_row(key_row(in_h[j]), 0, a.d, F32, (a.d & 3) == 0, dir_s);
+      rank_sort(key_s, pos_s, n, tid, CMP_THREADS);
       const float* u = a.unif + slot * (a.max_in / 2);
       const int pc = n / 2;
       for (int p = tid; p < pc; p += CMP_THREADS) {
