@@ -185,6 +185,10 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *   node_meta[n_nodes][4]: item count, first and last active row, materialized flag (items index
  *     rep_k/rep_v instead of k/v).
  *   low_num / low_den: sta_moments' partial outputs (sta_moment_partials_layout), fsplit splits.
+ *   ld_qk / ld_v: row strides (elements) of q, k and of v, multiples of 4 (rows are read in units of
+ *     4 elements; pad them with zero columns), bases 16-byte aligned.
+ *   rep_k / rep_v (fp32, row strides ld_rep_k / ld_rep_v, multiples of 4): materialized items
+ *     (segment means; fp32 inputs only), NULL otherwise.
  *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
  *   out: [BH][N][Dv] in out_dtype.
  *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator
@@ -192,12 +196,12 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *     low_degree_taylor_causal_sums, fast_article_attention.py:262-285, when mode is 3).
  */
 int sta_block_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
-                        int dv, int degree, float scale, float eps, int mode, int block, int chunk, int shift,
-                        int exp_clamp, const float* low_num, const float* low_den, int fsplit,
+                        int dv, int ld_qk, int ld_v, int degree, float scale, float eps, int mode, int block, int chunk,
+                        int shift, int exp_clamp, const float* low_num, const float* low_den, int fsplit,
                         const int32_t* tile_ptr, const int32_t* tile_nodes, int n_tiles, const int32_t* node_meta,
                         int n_nodes, int cap, const int32_t* node_src, const float* node_w, const float* rep_k,
-                        const float* rep_v, int64_t n_rep, void* out, int out_dtype, float* out_den,
-                        void* stream);
+                        const float* rep_v, int ld_rep_k, int ld_rep_v, int64_t n_rep, void* out, int out_dtype,
+                        float* out_den, void* stream);
 
 /* Rows per block-attention tile and the moment chunk the library uses for a head dimension D. */
 int sta_tile_rows(void);

@@ -138,6 +138,9 @@ def prefill(
         raise ValueError(f"the HIP kernels support D <= {lim['max_d']} and Dv <= {lim['max_dv']}")
     if degree > lim["max_degree"]:
         raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+    if semantics == "segment" and q3.dtype != torch.float32:
+        # segment means are fp32 and the residual kernel reads them with the inputs in one format
+        q3, k3, v3 = q3.float(), k3.float(), v3.float()
     dt = _native.DTYPE_CODES[q3.dtype]
     odt = _native.DTYPE_CODES[out_dtype]
     stream = _native.stream_handle(dev)
@@ -221,6 +224,7 @@ def prefill(
                 _native.check(st, "sta_segment_mean")
 
             _run(timer, "segment_mean", k_seg)
+            rep_k, rep_v = _padded_rows(rep_k, -(-d // 4) * 4), _padded_rows(rep_v, -(-dv // 4) * 4)
             rpb = block // stride
             src_np = np.arange(plan.n_nodes * plan.cap, dtype=np.int32).reshape(plan.n_nodes, plan.cap)
             src_np = np.where(src_np < n_rep, src_np, 0).astype(np.int32)
@@ -253,10 +257,11 @@ def prefill(
 
     def k24():
         st = lib.sta_block_attention(
-            q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), dt, bh, n, d, dv, degree, float(scale), float(eps), mode,
-            block, chunk, shift, 1 if exp_clamp else 0, low_num.data_ptr(), low_den.data_ptr(), fsplit,
-            tptr_d.data_ptr(), tnodes_d.data_ptr(), plan.n_tiles, meta_d.data_ptr(), n_nodes_arg, plan.cap,
-            _native.ptr(node_src), _native.ptr(node_w), _native.ptr(rep_k), _native.ptr(rep_v), n_rep_arg,
+            mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, d, dv, dm, mv.shape[-1], degree, float(scale),
+            float(eps), mode, block, chunk, shift, 1 if exp_clamp else 0, low_num.data_ptr(), low_den.data_ptr(),
+            fsplit, tptr_d.data_ptr(), tnodes_d.data_ptr(), plan.n_tiles, meta_d.data_ptr(), n_nodes_arg, plan.cap,
+            _native.ptr(node_src), _native.ptr(node_w), _native.ptr(rep_k), _native.ptr(rep_v),
+            rep_k.shape[-1] if rep_k is not None else 0, rep_v.shape[-1] if rep_v is not None else 0, n_rep_arg,
             out.data_ptr(), odt, _native.ptr(out_den), stream)
         _native.check(st, "sta_block_attention")
 

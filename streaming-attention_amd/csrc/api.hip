@@ -109,7 +109,10 @@ template <int DP, int DVT>
 int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
   const int64_t grid = bh * a.n_tiles;
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  if (a.dtype == STA_F32)
+    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, 4>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, 2>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
   return check_launch();
 }
 
@@ -366,12 +369,12 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
 }
 
 int sta_block_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
-                        int dv, int degree, float scale, float eps, int mode, int block, int chunk, int shift,
-                        int exp_clamp, const float* low_num, const float* low_den, int fsplit,
+                        int dv, int ld_qk, int ld_v, int degree, float scale, float eps, int mode, int block, int chunk,
+                        int shift, int exp_clamp, const float* low_num, const float* low_den, int fsplit,
                         const int32_t* tile_ptr, const int32_t* tile_nodes, int n_tiles, const int32_t* node_meta,
                         int n_nodes, int cap, const int32_t* node_src, const float* node_w, const float* rep_k,
-                        const float* rep_v, int64_t n_rep, void* out, int out_dtype, float* out_den,
-                        void* stream) {
+                        const float* rep_v, int ld_rep_k, int ld_rep_v, int64_t n_rep, void* out, int out_dtype,
+                        float* out_den, void* stream) {
   if (!q || !k || !v || !low_num || !low_den || !tile_ptr || !out) return STA_ERR_ARG;
   if (out_den && out_dtype != STA_F32) return STA_ERR_DTYPE;
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return STA_ERR_DTYPE;
@@ -381,6 +384,17 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   if (kTileRows % chunk != 0) return STA_ERR_ARG;
   if (n_tiles != static_cast<int>((n + shift + kTileRows - 1) / kTileRows)) return STA_ERR_SHAPE;
   if (n_nodes > 0 && (!node_meta || !node_src || !node_w || !tile_nodes || cap <= 0)) return STA_ERR_ARG;
+  // rows are read in units of 4 elements: strides multiples of 4, bases 16-byte aligned; materialized
+  // representatives (segment means) are fp32 and only combine with fp32 inputs
+  if (ld_qk < d || ld_qk % 4 != 0 || ld_v < dv || ld_v % 4 != 0) return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
+    return STA_ERR_ARG;
+  if (rep_k || rep_v) {
+    if (!rep_k || !rep_v || n_rep <= 0 || ld_rep_k < d || ld_rep_k % 4 != 0 || ld_rep_v < dv || ld_rep_v % 4 != 0)
+      return STA_ERR_ARG;
+    if (((reinterpret_cast<uintptr_t>(rep_k) | reinterpret_cast<uintptr_t>(rep_v)) & 15u) != 0) return STA_ERR_ARG;
+    if (dtype != STA_F32) return STA_ERR_DTYPE;
+  }
   sta::BlockArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.degree = degree; a.scale = scale;
   a.eps = eps; a.mode = mode; a.block = block; a.chunk = chunk; a.shift = shift; a.exp_clamp = exp_clamp;
@@ -388,6 +402,7 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   a.low_rows = n + 2 * sta::MOM_GUARD; a.low_ld = 32 * ((dv + 31) / 32); a.low_off = sta::MOM_GUARD;
   a.n_tiles = n_tiles; a.node_meta = node_meta; a.n_nodes = n_nodes; a.cap = cap; a.node_src = node_src;
   a.node_w = node_w; a.rep_k = rep_k; a.rep_v = rep_v; a.n_rep = n_rep; a.out = out; a.out_dtype = out_dtype; a.out_den = out_den;
+  a.ldqk = ld_qk; a.ldvr = ld_v; a.ldrk = ld_rep_k; a.ldrv = ld_rep_v;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (d <= 16) return dispatch_dvt<16>(a, bh, s);
   if (d <= 32) return dispatch_dvt<32>(a, bh, s);

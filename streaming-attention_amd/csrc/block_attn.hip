@@ -57,6 +57,10 @@ struct BlockArgs {
   const float* rep_k;       // [BH][n_rep][d]   (materialized items)
   const float* rep_v;       // [BH][n_rep][dv]
   int64_t n_rep;
+  int ldqk;  // row stride (elements) of q and k: a multiple of 4, >= d
+  int ldvr;  // row stride of v: a multiple of 4, >= dv
+  int ldrk;  // row stride of rep_k / rep_v (fp32; multiples of 4)
+  int ldrv;
   void* out;  // [BH][n][dv]
   int out_dtype;
   float* out_den;  // optional [BH][n]: when set, out (fp32) receives num and out_den receives den, unnormalised
@@ -98,23 +102,34 @@ __device__ __forceinline__ float taylor_fast(float x, const TaylorCoef& c) {
 // exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding).
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
 
-// 4 consecutive row elements [col, col+4) as fp32 (zero beyond `width`); vector load when possible.
-__device__ __forceinline__ floatx4 load4_row(const void* base, int64_t row_off, int col, int width, int dtype,
-                                             bool vec) {
-  if (vec && col + 3 < width) {
-    if (dtype == F32) return *reinterpret_cast<const floatx4*>(static_cast<const float*>(base) + row_off + col);
-    const uint2 raw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + row_off + col);
-    if (dtype == BF16)
-      return floatx4{__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u), __uint_as_float(raw.y << 16),
-                     __uint_as_float(raw.y & 0xffff0000u)};
-    const _Float16* h = reinterpret_cast<const _Float16*>(&raw);
-    return floatx4{static_cast<float>(h[0]), static_cast<float>(h[1]), static_cast<float>(h[2]), static_cast<float>(h[3])};
+// Elements [off, off+4) of a row as raw bits: 16 bytes (ES = 4) or 8 bytes (ES = 2, in .x/.y).  Rows are
+// read in units of 4 elements; the caller guarantees alignment and that the unit lies in the row.
+template <int ES>
+__device__ __forceinline__ uint4 load_unit(const void* base, int64_t off) {
+  if constexpr (ES == 4) {
+    return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+  } else {
+    const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+    return uint4{r.x, r.y, 0u, 0u};
   }
-  floatx4 r = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int m = 0; m < 4; ++m)
-    if (col + m < width) r[m] = load_elem(base, row_off + col + m, dtype);
-  return r;
+}
+
+// A raw unit as 4 floats (fp32 bits when ES = 4, else bf16 / fp16 by dtype), times `scale`.
+template <int ES>
+__device__ __forceinline__ floatx4 unit_to_f4(const uint4& r, int dtype, float scale) {
+  floatx4 f;
+  if constexpr (ES == 4) {
+    f = floatx4{__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w)};
+  } else if (dtype == BF16) {
+    f = floatx4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                __uint_as_float(r.y & 0xffff0000u)};
+  } else {
+    f = floatx4{static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x & 0xffffu))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x >> 16))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y & 0xffffu))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y >> 16)))};
+  }
+  return f * scale;
 }
 
 // Work layout: one workgroup per (head, tile of 64*RS query rows); wave w owns RS strips of 16 rows.
@@ -123,14 +138,28 @@ __device__ __forceinline__ floatx4 load4_row(const void* base, int64_t row_off, 
 // chains (k-step kk of lane group lg covers dimension (D/4) lg + kk, so a lane's key operands are
 // 16-byte LDS reads), evaluates the weights elementwise, and accumulates num^T += V^T P^T with the P^T
 // tile fed straight from the accumulator as the B operand.
-// Two waves per SIMD when the per-wave register arrays (queries, numerators, X and P tiles) leave room.
+//
+// Batches: first the keys of the tile's own chunk / article block (contiguous rows), then the coreset
+// items of the tile's nodes, flattened into an LDS list (token, weight, first and last active row per
+// item) filled up to BA_LIST items at a time, so a batch may span two nodes.  The rows of batch b+1 are
+// loaded into registers while batch b computes (one batch of software pipelining), so the global
+// latency of the gathers is hidden behind the matrix-core work.
+// Two waves per SIMD when the per-wave register arrays (queries, numerators, X and P tiles, prefetched
+// rows) leave room.
+constexpr int BA_LIST = 1024;
+__host__ __device__ constexpr int block_kb(int dp, int dvt) { return (dp + dvt * 16 > 192) ? 32 : 64; }
+__host__ __device__ constexpr int block_kpt(int dp, int dvt) { return (block_kb(dp, dvt) * dp / 4 + 255) / 256; }
+__host__ __device__ constexpr int block_vpt(int dp, int dvt) { return (block_kb(dp, dvt) * dvt * 4 + 255) / 256; }
 __host__ __device__ constexpr int block_occupancy(int dp, int dvt, int rs) {
-  return (rs * dp / 4 + rs * dvt * 4 + 2 * rs * ((dp + dvt * 16 > 192) ? 2 : 4) * 4) <= 160 ? 2 : 1;
+  return (rs * dp / 4 + rs * dvt * 4 + 2 * rs * (block_kb(dp, dvt) / 16) * 4 +
+          4 * (block_kpt(dp, dvt) + block_vpt(dp, dvt))) <= 160
+             ? 2
+             : 1;
 }
 
-template <int DP, int DVT, int RS>
+template <int DP, int DVT, int RS, int ES>
 __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_kernel(const BlockArgs a) {
-  constexpr int KB = (DP + DVT * 16 > 192) ? 32 : 64;  // keys per LDS stage
+  constexpr int KB = block_kb(DP, DVT);  // keys per LDS stage
   constexpr int NSUB = KB / 16;                         // 16-key subtiles per stage
   constexpr int LDK = DP + 4;                           // = 4 (mod 64) for the 16-byte key reads
   constexpr int DV = DVT * 16;
@@ -141,6 +170,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   __shared__ float Vt[DV * LDVT];
   __shared__ float Wst[KB];
   __shared__ int Jst[KB];
+  __shared__ int Lost[KB], Hist[KB];  // active rows of the staged items (node batches)
+  __shared__ int Lj[BA_LIST], Llo[BA_LIST], Lhi[BA_LIST];
+  __shared__ float Lw[BA_LIST];
 
   const int wg = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t bh = wg / a.n_tiles;
@@ -151,9 +183,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   const int n = static_cast<int>(a.n);
   const int r0 = t * TM - a.shift;
 
-  const int64_t qkbase = bh * a.n * a.d;
-  const int64_t vbase = bh * a.n * a.dv;
-  const bool vec = (a.d % 4 == 0) && (a.dv % 4 == 0);
+  const int64_t qkbase = bh * a.n * a.ldqk;
+  const int64_t vbase = bh * a.n * a.ldvr;
 
   int rbase[RS], myrow[RS], csr[RS], rsr[RS];
   bool rvalid[RS];
@@ -166,13 +197,15 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     csr[rs] = static_cast<int>(chunk_start(myrow[rs], a.chunk, a.shift));
     const int64_t rsv = residual_start(myrow[rs], a.mode, a.block);
     rsr[rs] = rsv > INT32_MAX ? INT32_MAX : static_cast<int>(rsv);
-    const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.d;
+    const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.ldqk;
     const float qs = rvalid[rs] ? a.scale : 0.f;  // the logits come out scaled
 #pragma unroll
     for (int m = 0; m < DQ / 4; ++m) {
-      const floatx4 v4 = load4_row(a.q, qoff, DQ * lg + 4 * m, a.d, a.dtype, vec);
+      const int col = DQ * lg + 4 * m;  // columns beyond the row (DP > ldqk) are zero
+      const floatx4 v4 = unit_to_f4<ES>(load_unit<ES>(a.q, qoff + min(col, a.ldqk - 4)), a.dtype,
+                                         col < a.ldqk ? qs : 0.f);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e] * qs;
+      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e];
     }
   }
   const int wrow_lo = r0 + wave * RS * 16, wrow_hi = wrow_lo + RS * 16 - 1;  // this wave's rows
@@ -193,7 +226,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   if (row_lo > row_hi) return;  // whole tile outside the sequence (uniform)
 
   // One staged batch: in-tile keys (is_node false) or the items of a node active on rows [lo, hi].
-  auto process = [&](bool is_node, int lo, int hi) {
+  auto process = [&](bool is_node) {
     floatx4 x[RS][NSUB];
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs)
@@ -229,7 +262,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           const float tp = taylor_fast(xv, tc);
           float p;
           if (is_node) {
-            const bool on = rvalid[rs] && i >= lo && i <= hi;
+            const bool on = rvalid[rs] && i >= Lost[kidx] && i <= Hist[kidx];
             p = on ? (ex - tp) * w : 0.f;
           } else {
             // own chunk (j >= cs): Taylor part; article block (j >= rs): residual; both: exp
@@ -256,72 +289,161 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     }
   };
 
-  // Stage keys [first key j0 .. ) of the batch: k rows row-major, v rows transposed.  src(r) gives the
-  // source row of batch slot r (-1: empty slot, zero-filled).
-  auto stage = [&](auto src_of, bool mat) {
-    constexpr int KU = DP / 4, VU = DV / 4;
-    for (int e = tid; e < KB * KU; e += 256) {
-      const int r = e / KU, u = e - r * KU;
-      const int src = src_of(r);
-      floatx4 v4 = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (src >= 0) {
-        v4 = mat ? load4_row(a.rep_k, (bh * a.n_rep + src) * a.d, 4 * u, a.d, F32, vec)
-                 : load4_row(a.k, qkbase + static_cast<int64_t>(src) * a.d, 4 * u, a.d, a.dtype, vec);
-      }
-      *reinterpret_cast<floatx4*>(Kst + r * LDK + 4 * u) = v4;
-    }
-    for (int e = tid; e < KB * VU; e += 256) {
-      const int r = e % KB, u = e / KB;  // key-fast: conflict-light transposed writes
-      const int src = src_of(r);
-      floatx4 v4 = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (src >= 0) {
-        v4 = mat ? load4_row(a.rep_v, (bh * a.n_rep + src) * a.dv, 4 * u, a.dv, F32, vec)
-                 : load4_row(a.v, vbase + static_cast<int64_t>(src) * a.dv, 4 * u, a.dv, a.dtype, vec);
-      }
-#pragma unroll
-      for (int m = 0; m < 4; ++m) Vt[(4 * u + m) * LDVT + r] = v4[m];
-    }
-  };
-
-  // ---- phase A: keys of the tile's own chunk / article block ----
+  // ---- batch sequence: phase A = contiguous keys [kstart, kend), phase B = the node item list ----
   int kstart = static_cast<int>(chunk_start(row_lo, a.chunk, a.shift));
   const int64_t rs_lo = residual_start(row_lo, a.mode, a.block);
   if (rs_lo < kstart) kstart = static_cast<int>(rs_lo);
   if (kstart < 0) kstart = 0;
   const int kend = row_hi + 1;
-  for (int kb0 = kstart; kb0 < kend; kb0 += KB) {
-    __syncthreads();
-    if (tid < KB) {
-      const int j = kb0 + tid;
-      Jst[tid] = j < kend ? j : -1;
-      Wst[tid] = 1.f;
-    }
-    stage([&](int r) { return kb0 + r < kend ? kb0 + r : -1; }, false);
-    __syncthreads();
-    if (kb0 <= wrow_hi) process(false, 0, 0);  // some key of the batch precedes some row of this wave
-  }
+  const int n_a = kend > kstart ? (kend - kstart + KB - 1) / KB : 0;
+  const bool mat = a.rep_k != nullptr;  // segment-mean items index rep_k / rep_v (every node or none)
 
-  // ---- phase B: coreset nodes visible to some row of the tile ----
+  // node item list, filled BA_LIST items at a time in tile-list order (uniform control flow)
+  int p_cur = a.tile_ptr[t], i_cur = 0;
   const int p_end = a.tile_ptr[t + 1];
-  for (int p = a.tile_ptr[t]; p < p_end; ++p) {
-    const int node = a.tile_nodes[p];
-    const int32_t* meta = a.node_meta + static_cast<int64_t>(node) * NODE_META;
-    const int size = meta[0];
-    const int lo = meta[1], hi = meta[2];
-    const bool mat = meta[3] != 0;
-    const int64_t ibase = (bh * a.n_nodes + node) * a.cap;
-    for (int i0 = 0; i0 < size; i0 += KB) {
-      __syncthreads();
-      if (tid < KB) {
-        const int it = i0 + tid;
-        Jst[tid] = it < size ? a.node_src[ibase + it] : -1;
-        Wst[tid] = it < size ? a.node_w[ibase + it] : 0.f;
+  int llen = 0;
+  auto fill = [&]() {
+    llen = 0;
+    while (p_cur < p_end && llen < BA_LIST) {
+      const int node = a.tile_nodes[p_cur];
+      const int32_t* meta = a.node_meta + static_cast<int64_t>(node) * NODE_META;
+      const int size = meta[0], lo = meta[1], hi = meta[2];
+      const int take = min(size - i_cur, BA_LIST - llen);
+      const int64_t ibase = (bh * a.n_nodes + node) * a.cap + i_cur;
+      for (int e = tid; e < take; e += 256) {
+        Lj[llen + e] = a.node_src[ibase + e];
+        Lw[llen + e] = a.node_w[ibase + e];
+        Llo[llen + e] = lo;
+        Lhi[llen + e] = hi;
       }
-      __syncthreads();
-      stage([&](int r) { return Jst[r]; }, mat);
-      __syncthreads();
-      if (hi >= wrow_lo && lo <= wrow_hi) process(true, lo, hi);
+      llen += take > 0 ? take : 0;
+      i_cur += take > 0 ? take : 0;
+      if (i_cur >= size) {
+        ++p_cur;
+        i_cur = 0;
+      }
     }
+  };
+
+  // prefetch registers: this thread's 4-element units of the next batch's key and value rows, raw (they
+  // are converted when written to LDS, so no instruction waits on the loads before the next commit),
+  // and which of them are real (row of the batch, column inside the row)
+  constexpr int KU = DP / 4, VU = DV / 4;
+  constexpr int KPT = block_kpt(DP, DVT), VPT = block_vpt(DP, DVT);
+  uint4 pk[KPT], pv[VPT];
+  uint32_t pk_ok = 0, pv_ok = 0;
+  int pj = -1, plo = 0, phi = -1;
+  float pw = 0.f;
+  auto src_of = [&](bool node, int off, int r) -> int {
+    if (!node) return off + r < kend ? off + r : -1;
+    return off + r < llen ? Lj[off + r] : -1;
+  };
+  auto prefetch = [&](bool node, int off) {
+    // in-block keys come from k / v; node items from rep_k / rep_v in segment mode (fp32, ES == 4 there)
+    const bool from_rep = mat && node;
+    const void* kb = a.k;
+    const void* vb = a.v;
+    int64_t kbase = qkbase, vbase2 = vbase;
+    int ldk = a.ldqk, ldv = a.ldvr;
+    if constexpr (ES == 4) {
+      if (from_rep) {
+        kb = a.rep_k;
+        vb = a.rep_v;
+        kbase = bh * a.n_rep * a.ldrk;
+        vbase2 = bh * a.n_rep * a.ldrv;
+        ldk = a.ldrk;
+        ldv = a.ldrv;
+      }
+    }
+    pk_ok = pv_ok = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / KU, u = e - r * KU;
+      const int src = (e < KB * KU) ? src_of(node, off, r) : -1;
+      const bool ok = src >= 0 && 4 * u < ldk;
+      pk_ok |= ok ? (1u << i) : 0u;
+      pk[i] = load_unit<ES>(kb, kbase + static_cast<int64_t>(src >= 0 ? src : 0) * ldk + min(4 * u, ldk - 4));
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e % KB, u = e / KB;  // key-fast: conflict-light transposed writes
+      const int src = (e < KB * VU) ? src_of(node, off, r) : -1;
+      const bool ok = src >= 0 && 4 * u < ldv;
+      pv_ok |= ok ? (1u << i) : 0u;
+      pv[i] = load_unit<ES>(vb, vbase2 + static_cast<int64_t>(src >= 0 ? src : 0) * ldv + min(4 * u, ldv - 4));
+    }
+    if (tid < KB) {
+      pj = src_of(node, off, tid);
+      const bool in = node && off + tid < llen;
+      pw = in ? Lw[off + tid] : (node ? 0.f : 1.f);
+      plo = in ? Llo[off + tid] : 0;
+      phi = in ? Lhi[off + tid] : -1;
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int e = tid + 256 * i;
+      if (e < KB * KU) {
+        const int r = e / KU, u = e - r * KU;
+        *reinterpret_cast<floatx4*>(Kst + r * LDK + 4 * u) =
+            unit_to_f4<ES>(pk[i], a.dtype, ((pk_ok >> i) & 1u) ? 1.f : 0.f);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = tid + 256 * i;
+      if (e < KB * VU) {
+        const int r = e % KB, u = e / KB;
+        const floatx4 f = unit_to_f4<ES>(pv[i], a.dtype, ((pv_ok >> i) & 1u) ? 1.f : 0.f);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Vt[(4 * u + m) * LDVT + r] = f[m];
+      }
+    }
+    if (tid < KB) {
+      Jst[tid] = pj;
+      Wst[tid] = pw;
+      Lost[tid] = plo;
+      Hist[tid] = phi;
+    }
+  };
+
+  // batch b: phase A for b < n_a (offset kstart + b KB), then phase B (offset into the list chunk).  The
+  // list is read only by prefetch(); once a batch is committed its items live in Jst/Wst/Lost/Hist, so
+  // the list can be refilled right after the commit of its last batch.
+  if (p_cur < p_end) fill();  // the first list chunk
+  __syncthreads();
+  bool cur_node = n_a == 0;
+  int cur_off = cur_node ? 0 : kstart;
+  bool have = n_a > 0 || llen > 0;
+  if (have) prefetch(cur_node, cur_off);
+  for (int b = 0; have; ++b) {
+    __syncthreads();  // every wave is done with the staging buffers of the previous batch
+    commit();
+    bool nxt_node = true;
+    int nxt_off = cur_node ? cur_off + KB : 0;
+    if (!cur_node && b + 1 < n_a) {
+      nxt_node = false;
+      nxt_off = cur_off + KB;
+    } else if (nxt_off >= llen) {  // the list chunk is used up: refill it (uniform)
+      nxt_off = 0;
+      if (cur_node && p_cur < p_end)
+        fill();
+      else if (cur_node)
+        llen = 0;
+    }
+    const bool nxt_have = !nxt_node || nxt_off < llen;
+    __syncthreads();  // staged batch and list visible
+    if (nxt_have) prefetch(nxt_node, nxt_off);
+    if (cur_node)
+      process(true);
+    else if (cur_off <= wrow_hi)
+      process(false);  // some key of the batch precedes some row of this wave
+    cur_node = nxt_node;
+    cur_off = nxt_off;
+    have = nxt_have;
   }
 
   // ---- epilogue: add the moment partials, normalise, store ----
