@@ -40,7 +40,8 @@
 //                  read land in distinct bank quads.
 //   Kt [KR][36]    transposed keys (row = dimension), row d = constant, rows d+1..d+3 = 0.
 //   Vt [32][36]    transposed values of the workgroup's 32 columns.
-// Partials: red [4 waves][33][32]: column-major [column][token], column 32 = denominator.
+// Partials: red [4 waves][33][32]: column-major [column][token], column 32 = denominator, token groups
+//           of 4 permuted per column (red_off).
 // Running denominators: den [4 waves][NT tiles x 16 features].
 #include "common.hpp"
 
@@ -49,6 +50,13 @@ namespace sta {
 constexpr int MOM_C = 32;    // tokens per chunk
 constexpr int MOM_LDT = 36;  // token stride of the transposed Kt / Vt rows
 constexpr int MOM_LDR = 32;  // token stride of a partial column
+
+// Offset of token t of partial column col.  The 4-token groups of a column are permuted by
+// (col / 2) mod 8, so the 16 columns a 16-byte access touches at one token group fall on 16 distinct
+// bank quads (with the plain stride of 32 floats they would fall on two).
+__device__ __forceinline__ int red_off(int col, int t) {
+  return col * MOM_LDR + 4 * ((t >> 2) ^ ((col >> 1) & 7)) + (t & 3);
+}
 constexpr int MOM_WAVES = 4;
 constexpr int MOM_THREADS = 64 * MOM_WAVES;
 // Guard rows before and after the sequence in the partial outputs: every chunk's rows have a valid
@@ -251,17 +259,17 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
                                                  int col0) {
   const int tid = threadIdx.x;
   const int col = tid & 31, t4 = 4 * (tid >> 5);  // 8 groups of 4 tokens
-  floatx4 acc = *reinterpret_cast<const floatx4*>(red + col * MOM_LDR + t4);
+  floatx4 acc = *reinterpret_cast<const floatx4*>(red + red_off(col, t4));
 #pragma unroll
-  for (int ww = 1; ww < MOM_WAVES; ++ww) acc += *reinterpret_cast<const floatx4*>(red + (ww * 33 + col) * MOM_LDR + t4);
+  for (int ww = 1; ww < MOM_WAVES; ++ww) acc += *reinterpret_cast<const floatx4*>(red + ww * 33 * MOM_LDR + red_off(col, t4));
   float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
 #pragma unroll
   for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
   if constexpr (DEN) {
     const int tok = tid & (MOM_C - 1);
-    float den = red[32 * MOM_LDR + tok];
+    float den = red[red_off(32, tok)];
 #pragma unroll
-    for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[(ww * 33 + 32) * MOM_LDR + tok];
+    for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[ww * 33 * MOM_LDR + red_off(32, tok)];
     a.low_den[obase + row0 + tok] = den;
   }
 }
@@ -470,12 +478,12 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
       for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
-          *reinterpret_cast<floatx4*>(rw + (16 * ct + li) * MOM_LDR + 16 * tt + 4 * lg) = o[0][tt][ct] + o[1][tt][ct];
+          *reinterpret_cast<floatx4*>(rw + red_off(16 * ct + li, 16 * tt + 4 * lg)) = o[0][tt][ct] + o[1][tt][ct];
         if constexpr (DEN) {
           float s = dq[tt];
           s += __shfl_xor(s, 16);
           s += __shfl_xor(s, 32);
-          if (lg == 0) rw[32 * MOM_LDR + 16 * tt + li] = s;
+          if (lg == 0) rw[red_off(32, 16 * tt + li)] = s;
         }
       }
     }
