@@ -17,6 +17,8 @@
 //
 // Matrix-core layout: X^T = K Q^T with A = key rows (LDS), B = q rows (registers, per wave); the P^T
 // tile in the accumulator is fed straight back as the B operand of num^T += V^T P^T.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace sta {
@@ -226,43 +228,44 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   if (row_lo > row_hi) return;  // whole tile outside the sequence (uniform)
 
   // One staged batch: in-tile keys (is_node false) or the items of a node active on rows [lo, hi].
-  auto process = [&](bool is_node) {
-    floatx4 x[RS][NSUB];
+  // One staged batch, pipelined by 16-key subtile: the X = K Q^T products of subtile kt+1 are issued
+  // while the weights of subtile kt are evaluated (VALU in the matrix cores' shadow), then subtile kt's
+  // num^T += V^T P^T.  X is accumulated in two halves of the dimensions (4 independent chains).
+  // NODE: coreset items (weight, active rows) instead of the tile's own keys.
+  auto process = [&](auto node_tag) {
+    constexpr bool NODE = decltype(node_tag)::value;
+    constexpr int QKM = DQ * RS;  // matrix-core ops of one subtile's X
+    auto qk = [&](int kt, floatx4 (&xq)[2][RS]) {
 #pragma unroll
-    for (int rs = 0; rs < RS; ++rs)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int kt = 0; kt < NSUB; ++kt) x[rs][kt] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int rs = 0; rs < RS; ++rs) xq[h][rs] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int m = 0; m < DQ / 4; ++m) {
-      floatx4 kv[NSUB];
+      for (int m = 0; m < DQ / 4; ++m) {
+        const floatx4 kv = *reinterpret_cast<const floatx4*>(Kst + (16 * kt + li) * LDK + DQ * lg + 4 * m);
 #pragma unroll
-      for (int kt = 0; kt < NSUB; ++kt)
-        kv[kt] = *reinterpret_cast<const floatx4*>(Kst + (16 * kt + li) * LDK + DQ * lg + 4 * m);
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int kt = 0; kt < NSUB; ++kt)
-#pragma unroll
-          for (int rs = 0; rs < RS; ++rs) x[rs][kt] = mfma4(kv[kt][e], qB[rs][4 * m + e], x[rs][kt]);
-    }
-    // weights, elementwise (key 16 kt + 4 lg + r, row myrow[rs])
-    floatx4 P[RS][NSUB];
-#pragma unroll
-    for (int kt = 0; kt < NSUB; ++kt) {
+          for (int rs = 0; rs < RS; ++rs) xq[m & 1][rs] = mfma4(kv[e], qB[rs][4 * m + e], xq[m & 1][rs]);
+      }
+    };
+    // weights of subtile kt, elementwise (key 16 kt + 4 lg + r, row myrow[rs])
+    auto weights = [&](int kt, const floatx4 (&xq)[2][RS], floatx4 (&P)[RS]) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kidx = 16 * kt + 4 * lg + r;
         const int j = Jst[kidx];
         const float w = Wst[kidx];
+        const int lo = NODE ? Lost[kidx] : 0, hi = NODE ? Hist[kidx] : 0;
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
           const int i = myrow[rs];
-          const float xv = x[rs][kt][r];
+          const float xv = xq[0][rs][r] + xq[1][rs][r];
           const float ex = exp_fast(fminf(xv, xmax));
           const float tp = taylor_fast(xv, tc);
           float p;
-          if (is_node) {
-            const bool on = rvalid[rs] && i >= Lost[kidx] && i <= Hist[kidx];
+          if constexpr (NODE) {
+            const bool on = rvalid[rs] && i >= lo && i <= hi;
             p = on ? (ex - tp) * w : 0.f;
           } else {
             // own chunk (j >= cs): Taylor part; article block (j >= rs): residual; both: exp
@@ -270,24 +273,42 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
             const float pr = (j >= rsr[rs] ? ex - tp : 0.f) + (j >= csr[rs] ? tp : 0.f);
             p = on ? pr : 0.f;
           }
-          P[rs][kt][r] = p;
+          P[rs][r] = p;
           den[rs] += p;
         }
       }
-    }
-    // num^T += V^T P^T
-#pragma unroll
-    for (int kt = 0; kt < NSUB; ++kt) {
+    };
+    auto pv = [&](int kt, const floatx4 (&P)[RS]) {
 #pragma unroll
       for (int ct = 0; ct < DVT; ++ct) {
         const floatx4 va = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * LDVT + 16 * kt + 4 * lg);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma4(va[s], P[rs][kt][s], num[rs][ct]);
+          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma4(va[s], P[rs][s], num[rs][ct]);
       }
+    };
+    floatx4 xa[2][RS], xb[2][RS];
+    qk(0, xa);
+#pragma unroll
+    for (int kt = 0; kt < NSUB; ++kt) {
+      floatx4(&xc)[2][RS] = (kt & 1) ? xb : xa;
+      floatx4(&xn)[2][RS] = (kt & 1) ? xa : xb;
+      if (kt + 1 < NSUB) qk(kt + 1, xn);
+      floatx4 P[RS];
+      weights(kt, xc, P);
+      if (kt + 1 < NSUB) {
+#pragma unroll
+        for (int g = 0; g < QKM; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix-core op of X(kt+1)
+          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the weights of kt
+        }
+      }
+      pv(kt, P);
     }
   };
+  using node_batch = std::integral_constant<bool, true>;
+  using block_batch = std::integral_constant<bool, false>;
 
   // ---- batch sequence: phase A = contiguous keys [kstart, kend), phase B = the node item list ----
   int kstart = static_cast<int>(chunk_start(row_lo, a.chunk, a.shift));
@@ -438,9 +459,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     __syncthreads();  // staged batch and list visible
     if (nxt_have) prefetch(nxt_node, nxt_off);
     if (cur_node)
-      process(true);
+      process(node_batch{});
     else if (cur_off <= wrow_hi)
-      process(false);  // some key of the batch precedes some row of this wave
+      process(block_batch{});  // some key of the batch precedes some row of this wave
     cur_node = nxt_node;
     cur_off = nxt_off;
     have = nxt_have;
