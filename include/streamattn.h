@@ -65,8 +65,12 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *     low_num [BH][fsplit][rows][ld], low_den [BH][fsplit][rows], row i stored at row_offset + i.
  */
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
                 const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream);
+
+/* 1 when sta_moments runs (d, degree, wave_tiles) with mixed = 1: the feature splits fs >= fsplit/2
+ * (fsplit even) then use wave_tiles - 1 tiles per wave (slot wave_tiles of their waves is padding). */
+int sta_moment_mixed_ok(int d, int degree, int wave_tiles);
 
 /* Smallest per-wave tile count >= want that sta_moments supports for (d, degree); -1 if none. */
 int sta_moment_wave_tiles(int d, int degree, int want);

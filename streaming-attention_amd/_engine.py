@@ -150,9 +150,11 @@ def prefill(
     # (zero dimensions only add zero-valued features), v to whole 32-column groups
     dm = _unit_width(d, q3.element_size())
     ft = _plan.feature_tiles(dm, degree)
-    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree))
+    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
+                            mixed_nts=_native.moment_mixed_tiles(dm, degree))
     fsplit = ms.fsplit
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv), dev, lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed), dev,
+                             lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
 
     raw = semantics == "taylor"
     if semantics in ("exact", "taylor"):
@@ -204,7 +206,8 @@ def prefill(
         st = lib.sta_moments(
             mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
             float(scale), chunk, shift,
-            fsplit, ms.wave_tiles, fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+            fsplit, ms.wave_tiles, int(ms.mixed), fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(),
+            low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")
 
     _run(timer, "moments", k1)

@@ -40,9 +40,10 @@ _SIGNATURES = {
     "sta_moment_chunk": (_i32, [_i32]),
     "sta_moments": (
         _i32,
-        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32,
          _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sta_moment_mixed_ok": (_i32, [_i32, _i32, _i32]),
     "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),
     "sta_moment_occupancy": (_i32, [_i32, _i32]),
     "sta_moment_partials_layout": (_i32, [_i64, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
@@ -162,6 +163,12 @@ def moment_wave_tile_options(d: int, degree: int) -> tuple:
                 opts.add((nt, l.sta_moment_occupancy(d, nt)))
         _wave_tile_options[key] = tuple(sorted(opts))
     return _wave_tile_options[key]
+
+
+def moment_mixed_tiles(d: int, degree: int) -> tuple:
+    """Per-wave tile counts the moment kernel also runs with mixed tile counts at (d, degree)."""
+    l = lib()
+    return tuple(nt for nt, _ in moment_wave_tile_options(d, degree) if l.sta_moment_mixed_ok(d, degree, nt))
 
 
 def moment_partials_layout(n: int, dv: int) -> tuple:

@@ -200,13 +200,16 @@ class MomentSplit:
     tile_off: np.ndarray  # int32 [fsplit * 4 + 1]
     quads: np.ndarray  # uint32 [fsplit * 4 * wave_tiles * 4]
     coef: np.ndarray  # float32 [fsplit * 4 * wave_tiles * 16]
+    mixed: bool = False  # splits fs >= fsplit / 2 run wave_tiles - 1 tiles per wave
 
 
 def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int, int], ...],
-                 compute_units: int = 256) -> MomentSplit:
-    """Choose (fsplit, wave_tiles) minimising rounds-of-workgroups x tiles-per-wave on a GPU with
+                 compute_units: int = 256, mixed_nts: Tuple[int, ...] = ()) -> MomentSplit:
+    """Choose (fsplit, wave_tiles, mixed) minimising rounds-of-workgroups x tiles-per-wave on a GPU with
     `compute_units` compute units; nt_options lists (per-wave tile count, workgroups resident per
-    compute unit) pairs the library supports.  Ties go to fewer feature splits (fewer partial sums)."""
+    compute unit) pairs the library supports, mixed_nts the tile counts it also runs mixed (the feature
+    splits fs >= fsplit / 2 hold one tile less per wave; every compute unit then pairs a full and a
+    short workgroup).  Ties go to fewer feature splits (fewer partial sums)."""
 
     def build():
         t = ft.n_tiles
@@ -222,17 +225,33 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
             rounds = -(-(bh * fsplit * csplit) // (compute_units * occ))
             # a compute unit time-shares its resident workgroups; two waves per SIMD overlap one wave's
             # VALU/LDS work with the other's matrix-core work (measured 1.2x per tile at d = 64)
-            cost = rounds * nt * occ / (OCC2_SPEEDUP if occ == 2 else 1.0)
-            if best is None or cost < best[0]:
-                best = (cost, fsplit, nt)
+            speed = OCC2_SPEEDUP if occ == 2 else 1.0
+            for mixed in (False, True):
+                if mixed and (nt not in mixed_nts or fsplit % 2 or csplit != 2 or occ != 2
+                              or 2 * fsplit * (2 * nt - 1) < t):
+                    continue
+                cost = rounds * (nt - 0.5 if mixed else nt) * occ / speed
+                if best is None or cost < best[0] - 1e-9:
+                    best = (cost, fsplit, nt, mixed)
             if need == 1:
                 break
         if best is None:
             raise ValueError(f"no supported per-wave tile count for {t} feature tiles (options {opts})")
-        _, fsplit, nt = best
+        _, fsplit, nt, mixed = best
         parts = fsplit * MOM_WAVES
-        base, extra = divmod(t, parts)
-        sizes = [base + (1 if i < extra else 0) for i in range(parts)]
+        if mixed:
+            caps = [nt if j < parts // 2 else nt - 1 for j in range(parts)]
+            sizes = list(caps)
+            excess = sum(caps) - t
+            j = parts - 1
+            while excess > 0:
+                if sizes[j] > 0:
+                    sizes[j] -= 1
+                    excess -= 1
+                j = j - 1 if j > 0 else parts - 1
+        else:
+            base, extra = divmod(t, parts)
+            sizes = [base + (1 if i < extra else 0) for i in range(parts)]
         off = np.zeros(parts + 1, dtype=np.int32)
         off[1:] = np.cumsum(sizes)
         pad_quad = ft.d | ((ft.d // 4 * 4) << 8) | (ft.d << 16)
@@ -244,9 +263,9 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
             cnt = sizes[j]
             quads[j, :cnt] = tiles_q[off[j]:off[j] + cnt]
             coef[j, :cnt] = tiles_c[off[j]:off[j] + cnt]
-        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1))
+        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1), mixed)
 
-    return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units), build)
+    return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units, tuple(mixed_nts)), build)
 
 
 def split_state_rows(ft: FeatureTiles, ms: MomentSplit, d: int) -> np.ndarray:

@@ -179,12 +179,19 @@ int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* r
   return STA_OK;
 }
 
+int sta_moment_mixed_ok(int d, int degree, int wave_tiles) {
+  return (d > 0 && d <= 64 && degree >= 0 && degree <= kMaxDegree && (wave_tiles == 4 || wave_tiles == 5) &&
+          moment_wave_tiles(d, degree, wave_tiles) == wave_tiles)
+             ? 1
+             : 0;
+}
+
 int sta_moment_occupancy(int d, int wave_tiles) {
   return (wave_tiles > 0 && d > 0) ? sta::mom_wg_per_cu(wave_tiles, d > 64) : 0;
 }
 
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles,
+                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
                 const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
@@ -192,6 +199,7 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
+  if (mixed != 0 && (mixed != 1 || fsplit % 2 != 0 || !sta_moment_mixed_ok(d, degree, wave_tiles))) return STA_ERR_ARG;
   // rows are read in 16-byte units: d must be a whole number of units, v rows whole 32-column groups,
   // every base 16-byte aligned, and a head's rows addressable with 32-bit byte offsets
   const int esize = dtype == STA_F32 ? 4 : 2;
@@ -202,7 +210,7 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
     return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
-  a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
+  a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, false);
 }
@@ -225,7 +233,7 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
     return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = k; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = 1.0f; a.shift = 0;
-  a.fsplit = fsplit; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
+  a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
   return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, true);

@@ -75,6 +75,7 @@ struct MomArgs {
   float scale;
   int shift;              // chunk c covers rows [c*32 - shift, (c+1)*32 - shift)
   int fsplit;             // feature splits (workgroups per head and column group)
+  int mixed;              // 1: feature splits fs >= fsplit / 2 hold one tile less per wave (see moments_kernel)
   int csplit;             // 32-column groups
   const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4] packed (i0 | b << 8 | i2 << 16)
   const float* fcoef;     // [fsplit][4 waves][NT tiles][16] key-side coefficient, 0 for padding
@@ -363,10 +364,10 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, c
   }
 }
 
-// The kernel body for one workgroup (head bh, feature split fs, column group cs).  DEN: this
-// workgroup also keeps the denominator column (only column group 0 does; the others would compute
-// bit-identical values).
-template <int NT, bool DEG3, bool DBIG, int ES, bool DEN>
+// The kernel body for one workgroup (head bh, feature split fs, column group cs) with NT tiles per wave
+// out of the NTS the split table holds per wave.  DEN: this workgroup also keeps the denominator column
+// (only column group 0 does; the others would compute bit-identical values).
+template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN>
 __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int BUF = mom_buf_floats(DBIG);
@@ -387,7 +388,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   const int li = lane & 15, lg = lane >> 4;
   float* den_s = den_all + w * NT * 16;  // running denominator of every feature of this wave's tiles
 
-  const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NT;
+  const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NTS;  // NTS: table tiles per wave
   const MomLane<NT, DEG3> m = mom_lane<NT, DEG3>(a, tile0, li, lg);
 
   floatx4 st[NT][CT];
@@ -518,6 +519,8 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
     const int hf = x * per_cs + (p - cs * per_cs);
     bh = hf / a.fsplit;
     fs = hf - static_cast<int>(bh) * a.fsplit;
+    // mixed tile counts: the partner of a full split is a short one (fs + fsplit / 2)
+    if (a.mixed && cs == 1) fs = (fs + a.fsplit / 2) % a.fsplit;
     return;
   }
   const int per_head = a.fsplit * a.csplit;
@@ -528,15 +531,27 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
   cs = rem - fs * a.csplit;
 }
 
+// Mixed tile counts (a.mixed, instantiated for NT = 4 and 5): the feature splits fs >= fsplit / 2 run
+// NT - 1 tiles per wave (their table slot NT is padding), so the tiles need fsplit * 4 * (NT - 1/2)
+// slots instead of fsplit * 4 * NT, and every compute unit holds one full and one short workgroup.
 template <int NT, bool DEG3, bool DBIG, int ES>
 __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
   mom_workgroup(a, bh, fs, cs);
-  if (cs == 0)
-    moments_body<NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
-  else
-    moments_body<NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
+  constexpr bool MIX = (NT == 4 || NT == 5) && !DBIG;
+  if (MIX && a.mixed && fs >= a.fsplit / 2) {
+    constexpr int NTL = MIX ? NT - 1 : NT;
+    if (cs == 0)
+      moments_body<NTL, NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
+    else
+      moments_body<NTL, NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
+  } else {
+    if (cs == 0)
+      moments_body<NT, NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
+    else
+      moments_body<NT, NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
+  }
 }
 
 // Shared-memory floats of moment_accumulate_kernel: one chunk buffer, the running denominators, a dummy.

@@ -43,7 +43,8 @@ def test_library_exports_header_symbols():
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, None, None, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, None, None, None, None,
+                           None) == _native.STA_ERR_ARG
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
 
@@ -166,6 +167,19 @@ def test_moment_split_balances_waves():
         real = np.concatenate([tab[j, :sizes[j]] for j in range(len(sizes))]).reshape(-1)
         assert np.array_equal(real, ft.quads)
         assert all(np.all(cf[j, sizes[j]:] == 0) for j in range(len(sizes)))
+    # mixed tile counts: half the feature splits run one tile less per wave
+    ft = _plan.feature_tiles(64, 2)
+    ms = _plan.moment_split(ft, 32, 64, ((2, 2), (4, 2), (5, 2), (9, 1), (16, 1)), mixed_nts=(4, 5))
+    assert (ms.fsplit, ms.csplit, ms.wave_tiles, ms.mixed) == (8, 2, 5, True)
+    sizes = np.diff(ms.tile_off)
+    half = 2 * ms.fsplit
+    assert sizes[:half].max() <= 5 and sizes[half:].max() <= 4 and sizes.sum() == ft.n_tiles == 141
+    # every real tile sits inside the slots its wave runs
+    q = ms.quads.reshape(4 * ms.fsplit, ms.wave_tiles, 4)
+    c = ms.coef.reshape(4 * ms.fsplit, ms.wave_tiles, 16)
+    assert np.all(c[half:, ms.wave_tiles - 1] == 0)
+    got = sorted(tuple(q[j, i]) for j in range(4 * ms.fsplit) for i in range(sizes[j]))
+    assert got == sorted(tuple(x) for x in ft.quads.reshape(-1, 4))
 
 
 def test_library_moment_tile_options():
