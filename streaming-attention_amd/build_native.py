@@ -2,6 +2,11 @@
 
     python streaming-attention_amd/build_native.py
 
+The library is 43 objects compiled in parallel and linked into one shared object: api.hip (entry
+points, compressor and decode kernels), launch_moments.hip, launch_accumulate.hip and launch_block.hip
+once per residual-kernel configuration (padded key width, value-column tiles, element size).  Objects
+go to streaming-attention_amd/_build/.
+
 Packed-fp32 VALU instructions are disabled (-packed-fp32-ops): the kernels are written for the
 scalar fp32 and MFMA paths.
 """
@@ -13,11 +18,23 @@ import pathlib
 import shutil
 import subprocess
 import sys
+import time
 
 HERE = pathlib.Path(__file__).resolve().parent
-SRC = HERE / "csrc" / "api.hip"
+CSRC = HERE / "csrc"
+# (source, object stem, defines), slowest first
+UNITS = (
+    ("launch_moments.hip", "launch_moments", ()),
+    ("launch_accumulate.hip", "launch_accumulate", ()),
+) + tuple(("launch_block.hip", f"launch_block_{dp}_{dvt}_{es}",
+           (f"-DSTA_BLOCK_DP={dp}", f"-DSTA_BLOCK_DVT={dvt}", f"-DSTA_BLOCK_ES={es}"))
+          for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + (
+    ("api.hip", "api", ()),
+)
+OBJDIR = HERE / "_build"
 OUT = HERE / "libstreamattn.so"
 ARCH = os.environ.get("STA_OFFLOAD_ARCH", "gfx950")
+NOISE = "'-packed-fp32-ops' is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -27,23 +44,56 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+def _flags() -> list[str]:
+    return [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-Wall", "-Wno-unused-function"]
+
+
+def _messages(res_out: str) -> list[str]:
+    return [ln for ln in res_out.splitlines() if NOISE not in ln]
+
+
 def build(verbose: bool = False) -> pathlib.Path:
+    OBJDIR.mkdir(exist_ok=True)
+    cc = hipcc()
+    jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    pending = list(UNITS)
+    running, failed, objs = [], [], []
+    t0 = time.time()
+    while pending or running:
+        while pending and len(running) < jobs:
+            src, stem, defs = pending.pop(0)
+            obj = OBJDIR / f"{stem}.o"
+            cmd = [cc, *_flags(), *defs, "-c", str(CSRC / src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            log = open(OBJDIR / f"{stem}.log", "w+")  # a file, not a pipe: long diagnostics cannot block
+            running.append((stem, log, subprocess.Popen(cmd, stdout=log, stderr=subprocess.STDOUT)))
+            objs.append(str(obj))
+        time.sleep(0.2)
+        for item in [r for r in running if r[2].poll() is not None]:
+            running.remove(item)
+            stem, log, p = item
+            log.seek(0)
+            msgs = _messages(log.read())
+            log.close()
+            if p.returncode != 0:
+                failed.append(f"{stem}:\n" + "\n".join(msgs))
+            elif verbose and msgs:
+                print("\n".join(msgs))
+            if verbose:
+                print(f"  {stem}: done at {time.time() - t0:.0f} s", flush=True)
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-Wall", "-Wno-unused-function",
-        str(SRC), "-o", str(tmp),
-    ]
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "'-packed-fp32-ops' is not a recognized feature for this target"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]
+    msgs = _messages(res.stdout + res.stderr)
     if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
-    if verbose and msgs:
-        print("\n".join(msgs))
+        raise RuntimeError("link failed:\n" + "\n".join(msgs))
     os.replace(tmp, OUT)
     return OUT
 

@@ -1,130 +1,20 @@
-// extern "C" entry points of libstreamattn.so (declared in include/streamattn.h): argument checks,
-// template dispatch and kernel launches.  The library allocates nothing; every buffer is the caller's.
-#include "../../include/streamattn.h"
+// extern "C" entry points of libstreamattn.so (declared in include/streamattn.h): argument checks and
+// kernel launches.  The moment and block-attention kernels are instantiated and launched from their own
+// units (launch_moments.hip, launch_accumulate.hip, launch_block.hip); this unit includes their sources
+// for the argument structs only.  The library allocates nothing; every buffer is the caller's.
+#include "api_common.hpp"
 #include "block_attn.hip"
 #include "compress.hip"
 #include "decode.hip"
 #include "moments.hip"
 
-namespace {
-
+namespace sta_api {
 thread_local int g_last_hip_error = 0;
+}  // namespace sta_api
 
-int hip_status(hipError_t e) {
-  if (e == hipSuccess) return STA_OK;
-  g_last_hip_error = static_cast<int>(e);
-  return STA_ERR_HIP;
-}
+using namespace sta_api;
 
-int check_launch() { return hip_status(hipGetLastError()); }
-
-bool dtype_ok(int dt) { return dt == STA_F32 || dt == STA_BF16 || dt == STA_F16; }
-
-constexpr int kMaxD = 128;
-constexpr int kMaxDv = 256;
-constexpr int kMaxDegree = 3;
-constexpr int kTileRows = 128;
-
-// ---------------------------------------------------------------- moments dispatch
-template <int NT, bool DEG3, bool DBIG, int ES>
-int launch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
-  const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-  if (e != hipSuccess) return hip_status(e);
-  const int64_t grid = bh * a.fsplit * a.csplit;
-  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOM_THREADS), smem, s, a);
-  return check_launch();
-}
-
-template <int NT, bool DEG3, bool DBIG, int ES>
-int launch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
-  const size_t smem = static_cast<size_t>(sta::mom_acc_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moment_accumulate_kernel<NT, DEG3, DBIG, ES>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
-  if (e != hipSuccess) return hip_status(e);
-  const int64_t grid = bh * a.fsplit * a.csplit;
-  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOM_THREADS), smem, s, a);
-  return check_launch();
-}
-
-// Per-wave tile counts the moment kernel is instantiated for, per (degree 3, d > 64).
-constexpr int kNtD2[] = {2, 4, 5, 9, 16};
-constexpr int kNtD3[] = {4, 8, 16};
-constexpr int kNtBigD2[] = {5, 16};
-constexpr int kNtBigD3[] = {4, 16};
-
-template <size_t L>
-int next_nt(const int (&tab)[L], int want) {
-  for (size_t i = 0; i < L; ++i)
-    if (tab[i] >= want) return tab[i];
-  return -1;
-}
-
-int moment_wave_tiles(int d, int degree, int want) {
-  if (want < 1) want = 1;
-  const bool deg3 = degree >= 3, big = d > 64;
-  if (!big) return deg3 ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
-  return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
-}
-
-// Instantiated per element size (4: fp32, 2: bf16 / fp16) so the chunk staging is straight-line code.
-template <int NT, bool D3, bool BIG>
-int launch_mom_es(const sta::MomArgs& a, int64_t bh, hipStream_t s, bool accumulate) {
-  if (a.esize == 4)
-    return accumulate ? launch_accumulate<NT, D3, BIG, 4>(a, bh, s) : launch_moments<NT, D3, BIG, 4>(a, bh, s);
-  return accumulate ? launch_accumulate<NT, D3, BIG, 2>(a, bh, s) : launch_moments<NT, D3, BIG, 2>(a, bh, s);
-}
-
-#define STA_MOM_CASE(NT, D3, BIG) \
-  case NT: return launch_mom_es<NT, D3, BIG>(a, bh, s, accumulate);
-
-int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3, bool accumulate) {
-  if (a.d <= 64) {
-    if (deg3) {
-      switch (nt) { STA_MOM_CASE(4, true, false) STA_MOM_CASE(8, true, false) STA_MOM_CASE(16, true, false) }
-    } else {
-      switch (nt) {
-        STA_MOM_CASE(2, false, false) STA_MOM_CASE(4, false, false) STA_MOM_CASE(5, false, false)
-        STA_MOM_CASE(9, false, false) STA_MOM_CASE(16, false, false)
-      }
-    }
-  } else {
-    if (deg3) {
-      switch (nt) { STA_MOM_CASE(4, true, true) STA_MOM_CASE(16, true, true) }
-    } else {
-      switch (nt) { STA_MOM_CASE(5, false, true) STA_MOM_CASE(16, false, true) }
-    }
-  }
-  return STA_ERR_UNSUPPORTED;
-}
-#undef STA_MOM_CASE
-
-// ---------------------------------------------------------------- block-attention dispatch
-template <int DP, int DVT>
-int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
-  const int64_t grid = bh * a.n_tiles;
-  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  if (a.dtype == STA_F32)
-    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, 4>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, 2>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
-  return check_launch();
-}
-
-template <int DP>
-int dispatch_dvt(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
-  if (a.dv <= 16) return launch_block<DP, 1>(a, bh, s);
-  if (a.dv <= 32) return launch_block<DP, 2>(a, bh, s);
-  if (a.dv <= 64) return launch_block<DP, 4>(a, bh, s);
-  if (a.dv <= 128) return launch_block<DP, 8>(a, bh, s);
-  if (a.dv <= 256) return launch_block<DP, 16>(a, bh, s);
-  return STA_ERR_UNSUPPORTED;
-}
+namespace {
 
 __global__ void selftest_mfma_kernel(const float* a, const float* b, float* d) {
   const int l = threadIdx.x;
@@ -132,6 +22,17 @@ __global__ void selftest_mfma_kernel(const float* a, const float* b, float* d) {
   c = sta::mfma4(a[l], b[l], c);
   const int i = l & 15, g = l >> 4;
   for (int r = 0; r < 4; ++r) d[(4 * g + r) * 16 + i] = c[r];
+}
+
+// Residual kernel configuration by value width (value-column tiles of 16).
+template <int DP, int ES>
+int dispatch_dvt(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
+  if (a.dv <= 16) return launch_block<DP, 1, ES>(a, bh, s);
+  if (a.dv <= 32) return launch_block<DP, 2, ES>(a, bh, s);
+  if (a.dv <= 64) return launch_block<DP, 4, ES>(a, bh, s);
+  if (a.dv <= 128) return launch_block<DP, 8, ES>(a, bh, s);
+  if (a.dv <= 256) return launch_block<DP, 16, ES>(a, bh, s);
+  return STA_ERR_UNSUPPORTED;
 }
 
 }  // namespace
@@ -212,7 +113,7 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
-  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, false);
+  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
@@ -236,7 +137,7 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
   a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
-  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3, true);
+  return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
 }
 
 int sta_decode_layout(int d, int dv, int* dk, int* ldv) {
@@ -412,10 +313,11 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   a.node_w = node_w; a.rep_k = rep_k; a.rep_v = rep_v; a.n_rep = n_rep; a.out = out; a.out_dtype = out_dtype; a.out_den = out_den;
   a.ldqk = ld_qk; a.ldvr = ld_v; a.ldrk = ld_rep_k; a.ldrv = ld_rep_v;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (d <= 16) return dispatch_dvt<16>(a, bh, s);
-  if (d <= 32) return dispatch_dvt<32>(a, bh, s);
-  if (d <= 64) return dispatch_dvt<64>(a, bh, s);
-  return dispatch_dvt<128>(a, bh, s);
+  const bool f32 = dtype == STA_F32;
+  if (d <= 16) return f32 ? dispatch_dvt<16, 4>(a, bh, s) : dispatch_dvt<16, 2>(a, bh, s);
+  if (d <= 32) return f32 ? dispatch_dvt<32, 4>(a, bh, s) : dispatch_dvt<32, 2>(a, bh, s);
+  if (d <= 64) return f32 ? dispatch_dvt<64, 4>(a, bh, s) : dispatch_dvt<64, 2>(a, bh, s);
+  return f32 ? dispatch_dvt<128, 4>(a, bh, s) : dispatch_dvt<128, 2>(a, bh, s);
 }
 
 int sta_selftest_mfma(const float* a, const float* b, float* d_out) {

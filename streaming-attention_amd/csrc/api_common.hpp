@@ -1,0 +1,74 @@
+// Shared by the translation units of libstreamattn.so: status helpers, argument limits, the moment
+// kernel configurations and the dispatch functions one unit provides to another.  The kernels are
+// compiled in separate units (moments, moment accumulation, block attention per configuration, the
+// rest) so the build runs them in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/streamattn.h"
+
+namespace sta {
+struct MomArgs;
+struct BlockArgs;
+}  // namespace sta
+
+namespace sta_api {
+
+extern thread_local int g_last_hip_error;  // defined in api.hip
+
+inline int hip_status(hipError_t e) {
+  if (e == hipSuccess) return STA_OK;
+  g_last_hip_error = static_cast<int>(e);
+  return STA_ERR_HIP;
+}
+
+inline int check_launch() { return hip_status(hipGetLastError()); }
+
+inline bool dtype_ok(int dt) { return dt == STA_F32 || dt == STA_BF16 || dt == STA_F16; }
+
+constexpr int kMaxD = 128;
+constexpr int kMaxDv = 256;
+constexpr int kMaxDegree = 3;
+constexpr int kTileRows = 128;
+
+// Per-wave tile counts the moment kernels are instantiated for, per (degree 3, d > 64).  Every entry
+// must appear in STA_MOMENT_CONFIGS.
+constexpr int kNtD2[] = {2, 4, 5, 9, 16};
+constexpr int kNtD3[] = {4, 8, 16};
+constexpr int kNtBigD2[] = {5, 16};
+constexpr int kNtBigD3[] = {4, 16};
+
+// X(NT, DEG3, DBIG) for every instantiated moment configuration.
+#define STA_MOMENT_CONFIGS(X)                                                                       \
+  X(2, false, false) X(4, false, false) X(5, false, false) X(9, false, false) X(16, false, false)   \
+  X(4, true, false) X(8, true, false) X(16, true, false) X(5, false, true) X(16, false, true)       \
+  X(4, true, true) X(16, true, true)
+
+template <size_t L>
+int next_nt(const int (&tab)[L], int want) {
+  for (size_t i = 0; i < L; ++i)
+    if (tab[i] >= want) return tab[i];
+  return -1;
+}
+
+inline int moment_wave_tiles(int d, int degree, int want) {
+  if (want < 1) want = 1;
+  const bool deg3 = degree >= 3, big = d > 64;
+  if (!big) return deg3 ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
+  return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
+}
+
+// launch_moments.hip: the prefill moment scan (moments_kernel) for wave-tile count nt.
+int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
+// launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
+int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
+// launch_block.hip, one object per (DP, DVT, ES): the residual / combine kernel (block_attn_kernel) for
+// padded key width DP, value-column tile count DVT and element size ES.
+template <int DP, int DVT, int ES>
+int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s);
+
+}  // namespace sta_api

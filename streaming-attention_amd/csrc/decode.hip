@@ -35,7 +35,7 @@ enum DecFlags : int { DEC_APPEND = 1, DEC_CURRENT = 2, DEC_QUERY = 4 };
 // ------------------------------------------------------------------------------------------------
 // decode_moments_kernel: part_num[s][split][col] = sum_{f in split} phi_q(s q)[f] state_num[s][f][col],
 // part_den[s][split] likewise with state_den.  Thread (row slot rp, column quad c4) walks the rows
-// f = f0 + rp + j * rpp, 4 rows per trip with unconditional (clamped) 16-byte loads.
+// f = f0 + rp + j * rpp, 4 rows per trip with unconditional (clamped), non-temporal 16-byte loads.
 struct DecMomArgs {
   const void* q;  // [S][d] current queries (dtype)
   int dtype;
@@ -82,8 +82,9 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_moments_kernel(const DecMo
       for (int u = 0; u < U; ++u) {
         const int row = r + u * rpp;
         const int rr = min(row, f1 - 1);
-        S[u] = *reinterpret_cast<const floatx4*>(sn + static_cast<int64_t>(rr) * a.ldm);
-        D[u] = sd[rr];
+        // the state is streamed once per step: non-temporal loads keep it from displacing cached data
+        S[u] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(sn + static_cast<int64_t>(rr) * a.ldm));
+        D[u] = __builtin_nontemporal_load(sd + rr);
         const uint32_t pf = a.rowfeat[rr];
         const float ph = xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u];
         phi[u] = row < f1 ? ph : 0.f;

@@ -1,0 +1,24 @@
+// Launch of the residual / combine kernel (block_attn_kernel) for one configuration.  The build compiles
+// this unit once per padded key width DP (16, 32, 64, 128), value-column tile count DVT (1, 2, 4, 8,
+// 16) and element size ES (4: fp32, 2: bf16 / fp16), given as -DSTA_BLOCK_DP=, -DSTA_BLOCK_DVT= and
+// -DSTA_BLOCK_ES=, so the forty instantiations compile in parallel.
+#include "api_common.hpp"
+#include "block_attn.hip"
+
+#if !defined(STA_BLOCK_DP) || !defined(STA_BLOCK_DVT) || !defined(STA_BLOCK_ES)
+#error "launch_block.hip is compiled with -DSTA_BLOCK_DP= -DSTA_BLOCK_DVT= -DSTA_BLOCK_ES="
+#endif
+
+namespace sta_api {
+
+template <int DP, int DVT, int ES>
+int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
+  const int64_t grid = bh * a.n_tiles;
+  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
+  hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  return check_launch();
+}
+
+template int launch_block<STA_BLOCK_DP, STA_BLOCK_DVT, STA_BLOCK_ES>(const sta::BlockArgs&, int64_t, hipStream_t);
+
+}  // namespace sta_api
