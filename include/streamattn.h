@@ -207,6 +207,17 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
                         const float* rep_v, int ld_rep_k, int ld_rep_v, int64_t n_rep, void* out, int out_dtype,
                         float* out_den, void* stream);
 
+/*
+ * Exact causal softmax attention, FlashAttention-style (online row maximum, no N x N scores).
+ * Replaces _flash_causal_kernel / triton_flash_causal_attention (triton_article_attention.py:372-435,
+ * :580-637):  out_i = sum_{j<=i} exp(s q_i.k_j - m_i) v_j / max(sum_{j<=i} exp(s q_i.k_j - m_i), 1e-20).
+ *   q, k rows are ld_qk elements apart (a multiple of 4, >= d; columns [d, ld_qk) are ignored), v rows
+ *   ld_v (a multiple of 4, >= dv); q, k, v 16-byte aligned.  out [BH][N][Dv] dense, dtype out_dtype.
+ *   d <= 128, dv <= 256.  fp32 accumulation; products of the inputs are exact (fp32 matrix cores).
+ */
+int sta_flash_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
+                        int dv, int ld_qk, int ld_v, float scale, void* out, int out_dtype, void* stream);
+
 /* Rows per block-attention tile and the moment chunk the library uses for a head dimension D. */
 int sta_tile_rows(void);
 int sta_moment_chunk(int d);

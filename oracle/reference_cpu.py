@@ -13,7 +13,9 @@ Pinning (see tests/test_oracle.py): exp_taylor known answers; feature counts C(d
 itertools.combinations_with_replacement; phi_k . phi_q == exp_{<=t} by brute force; moment sums ==
 quadratic closed form; compressor="none" == fp64 softmax attention; sorted_pair / random selections,
 flat and level-merge outputs == golden vectors written from the reference (tests/golden/); level
-invariants (occupancy == binary counter, weight 2^(l+1), weights sum to the tokens compressed).
+invariants (occupancy == binary counter, weight 2^(l+1), weights sum to the tokens compressed); the
+blocked online-softmax recursion of the flash baseline == torch.softmax attention for every block size,
+and its special cases (one key: out = v_0; equal keys: running mean of v).
 """
 
 from __future__ import annotations
@@ -53,6 +55,33 @@ def classical_attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor
     logits = (q64 @ k64.transpose(-1, -2)) * scale
     mask = torch.ones(n, n, dtype=torch.bool).tril()
     return torch.softmax(logits.masked_fill(~mask, float("-inf")), dim=-1) @ v64
+
+
+def flash_attention_blocked(q: Tensor, k: Tensor, v: Tensor, scale: float, block_n: int = 64) -> Tensor:
+    """The online-softmax recursion of _flash_causal_kernel (triton_article_attention.py:397-428) in
+    float64 for one [N, D] sequence: keys in blocks of block_n; per block the row maximum
+    m_new = max(m, max_j s_ij), p_ij = exp(s_ij - m_new), alpha = exp(m - m_new),
+    acc = alpha acc + p v, l = alpha l + sum_j p_ij; out = acc / max(l, 1e-20)."""
+    q64, k64, v64 = q.double(), k.double(), v.double()
+    n = q.shape[0]
+    m = torch.full((n,), -math.inf, dtype=torch.float64)
+    l = torch.zeros(n, dtype=torch.float64)
+    acc = torch.zeros(n, v.shape[-1], dtype=torch.float64)
+    rows = torch.arange(n)
+    for start in range(0, n, block_n):
+        cols = torch.arange(start, min(start + block_n, n))
+        s = (q64 @ k64[cols].T) * scale
+        s = s.masked_fill(cols[None, :] > rows[:, None], -math.inf)
+        m_new = torch.maximum(m, s.max(dim=1).values)
+        # rows with every key so far masked keep m = -inf; exp(-inf - -inf) would be NaN, their terms are 0
+        finite = torch.isfinite(m_new)
+        p = torch.where(finite[:, None], torch.exp(s - torch.where(finite, m_new, 0.0)[:, None]), 0.0)
+        alpha = torch.where(finite, torch.exp(torch.where(torch.isfinite(m), m, -math.inf) -
+                                              torch.where(finite, m_new, 0.0)), 1.0)
+        acc = acc * alpha[:, None] + p @ v64[cols]
+        l = l * alpha + p.sum(dim=1)
+        m = m_new
+    return acc / torch.clamp(l, min=1e-20)[:, None]
 
 
 def monomials(dim: int, degree: int) -> List[Tuple[int, ...]]:

@@ -270,3 +270,31 @@ def prefill(
 
     _run(timer, "block_attention", k24)
     return PrefillResult(out, node_src, node_w, plan, ft.count, fsplit, out_den)
+
+
+def flash(q3: torch.Tensor, k3: torch.Tensor, v3: torch.Tensor, *, scale: float,
+          out_dtype: torch.dtype = torch.float32, timer: Optional[KernelTimer] = None) -> torch.Tensor:
+    """Exact causal softmax attention of contiguous [BH, N, D] device tensors of one dtype
+    (sta_flash_attention); rows are zero-padded to whole 4-element units when D or Dv is not."""
+    for t in (q3, k3, v3):
+        _native.require_device(t)
+    if not (q3.dtype == k3.dtype == v3.dtype) or q3.dtype not in _native.DTYPE_CODES:
+        raise ValueError("q, k, v must share one of the dtypes float32, bfloat16, float16")
+    bh, n, d = q3.shape
+    dv = v3.shape[-1]
+    odt = out_dtype if out_dtype in _native.DTYPE_CODES else torch.float32
+    out = torch.empty((bh, n, dv), device=q3.device, dtype=odt)
+    if bh == 0 or n == 0:
+        return out.to(out_dtype)
+    dq, dvp = -(-d // 4) * 4, -(-dv // 4) * 4
+    mq, mk, mv = _padded_rows(q3, dq), _padded_rows(k3, dq), _padded_rows(v3, dvp)
+    lib = _native.lib()
+
+    def launch():
+        st = lib.sta_flash_attention(mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), _native.DTYPE_CODES[q3.dtype],
+                                     bh, n, d, dv, dq, dvp, float(scale), out.data_ptr(), _native.DTYPE_CODES[odt],
+                                     _native.stream_handle(q3.device))
+        _native.check(st, "sta_flash_attention")
+
+    _run(timer, "flash", launch)
+    return out if odt == out_dtype else out.to(out_dtype)

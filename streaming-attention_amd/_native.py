@@ -63,6 +63,9 @@ _SIGNATURES = {
             _c_p, _i32, _c_p, _c_p,  # out out_dtype out_den stream
         ],
     ),
+    "sta_flash_attention": (
+        _i32, [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _c_p, _i32, _c_p],
+    ),
     "sta_moment_accumulate": (
         _i32,
         [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dtype bh n rows d dv ldv deg fs nt

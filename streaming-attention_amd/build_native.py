@@ -2,10 +2,10 @@
 
     python streaming-attention_amd/build_native.py
 
-The library is 43 objects compiled in parallel and linked into one shared object: api.hip (entry
-points, compressor and decode kernels), launch_moments.hip, launch_accumulate.hip and launch_block.hip
-once per residual-kernel configuration (padded key width, value-column tiles, element size).  Objects
-go to streaming-attention_amd/_build/.
+The library is 83 objects compiled in parallel and linked into one shared object: api.hip (entry
+points, compressor and decode kernels), launch_moments.hip, launch_accumulate.hip, and
+launch_block.hip and launch_flash.hip once per residual / flash kernel configuration (padded key
+width, value-column tiles, element size).  Objects go to streaming-attention_amd/_build/.
 
 Packed-fp32 VALU instructions are disabled (-packed-fp32-ops): the kernels are written for the
 scalar fp32 and MFMA paths.
@@ -28,7 +28,10 @@ UNITS = (
     ("launch_accumulate.hip", "launch_accumulate", ()),
 ) + tuple(("launch_block.hip", f"launch_block_{dp}_{dvt}_{es}",
            (f"-DSTA_BLOCK_DP={dp}", f"-DSTA_BLOCK_DVT={dvt}", f"-DSTA_BLOCK_ES={es}"))
-          for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + (
+          for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + tuple(
+    ("launch_flash.hip", f"launch_flash_{dp}_{dvt}_{es}",
+     (f"-DSTA_FLASH_DP={dp}", f"-DSTA_FLASH_DVT={dvt}", f"-DSTA_FLASH_ES={es}"))
+    for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + (
     ("api.hip", "api", ()),
 )
 OBJDIR = HERE / "_build"

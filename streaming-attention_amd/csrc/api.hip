@@ -6,6 +6,7 @@
 #include "block_attn.hip"
 #include "compress.hip"
 #include "decode.hip"
+#include "flash_attn.hip"
 #include "moments.hip"
 
 namespace sta_api {
@@ -24,7 +25,7 @@ __global__ void selftest_mfma_kernel(const float* a, const float* b, float* d) {
   for (int r = 0; r < 4; ++r) d[(4 * g + r) * 16 + i] = c[r];
 }
 
-// Residual kernel configuration by value width (value-column tiles of 16).
+// Residual and flash kernel configurations by value width (value-column tiles of 16).
 template <int DP, int ES>
 int dispatch_dvt(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
   if (a.dv <= 16) return launch_block<DP, 1, ES>(a, bh, s);
@@ -32,6 +33,16 @@ int dispatch_dvt(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
   if (a.dv <= 64) return launch_block<DP, 4, ES>(a, bh, s);
   if (a.dv <= 128) return launch_block<DP, 8, ES>(a, bh, s);
   if (a.dv <= 256) return launch_block<DP, 16, ES>(a, bh, s);
+  return STA_ERR_UNSUPPORTED;
+}
+
+template <int DP, int ES>
+int dispatch_flash_dvt(const sta::FlashArgs& a, int64_t bh, hipStream_t s) {
+  if (a.dv <= 16) return launch_flash<DP, 1, ES>(a, bh, s);
+  if (a.dv <= 32) return launch_flash<DP, 2, ES>(a, bh, s);
+  if (a.dv <= 64) return launch_flash<DP, 4, ES>(a, bh, s);
+  if (a.dv <= 128) return launch_flash<DP, 8, ES>(a, bh, s);
+  if (a.dv <= 256) return launch_flash<DP, 16, ES>(a, bh, s);
   return STA_ERR_UNSUPPORTED;
 }
 
@@ -61,6 +72,31 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in) {
   if (max_degree) *max_degree = kMaxDegree;
   if (max_compress_in) *max_compress_in = sta::CMP_MAX_IN;
   return STA_OK;
+}
+
+int sta_flash_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
+                        int dv, int ld_qk, int ld_v, float scale, void* out, int out_dtype, void* stream) {
+  if (!q || !k || !v || !out) return STA_ERR_ARG;
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return STA_ERR_DTYPE;
+  if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0) return STA_ERR_SHAPE;
+  if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
+  if (ld_qk < d || ld_qk % 4 != 0 || ld_v < dv || ld_v % 4 != 0) return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
+    return STA_ERR_ARG;
+  if (n >= (int64_t(1) << 31) - 128) return STA_ERR_UNSUPPORTED;
+  constexpr int kFlashRows = 128;  // 64 RS query rows per workgroup, RS = 2
+  sta::FlashArgs a;
+  a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.ldqk = ld_qk; a.ldv = ld_v;
+  a.scale2 = scale * 1.4426950408889634f;
+  a.n_tiles = static_cast<int>((n + kFlashRows - 1) / kFlashRows);
+  a.out = out; a.out_dtype = out_dtype;
+  a.vec_out = (out_dtype == STA_F32 && dv % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f32 = dtype == STA_F32;
+  if (d <= 16) return f32 ? dispatch_flash_dvt<16, 4>(a, bh, s) : dispatch_flash_dvt<16, 2>(a, bh, s);
+  if (d <= 32) return f32 ? dispatch_flash_dvt<32, 4>(a, bh, s) : dispatch_flash_dvt<32, 2>(a, bh, s);
+  if (d <= 64) return f32 ? dispatch_flash_dvt<64, 4>(a, bh, s) : dispatch_flash_dvt<64, 2>(a, bh, s);
+  return f32 ? dispatch_flash_dvt<128, 4>(a, bh, s) : dispatch_flash_dvt<128, 2>(a, bh, s);
 }
 
 int sta_tile_rows(void) { return kTileRows; }

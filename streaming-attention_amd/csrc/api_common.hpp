@@ -14,6 +14,7 @@
 namespace sta {
 struct MomArgs;
 struct BlockArgs;
+struct FlashArgs;
 }  // namespace sta
 
 namespace sta_api {
@@ -70,5 +71,8 @@ int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt
 // padded key width DP, value-column tile count DVT and element size ES.
 template <int DP, int DVT, int ES>
 int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s);
+// launch_flash.hip, one object per (DP, DVT, ES): exact causal softmax attention (flash_attn_kernel).
+template <int DP, int DVT, int ES>
+int launch_flash(const sta::FlashArgs& a, int64_t bh, hipStream_t s);
 
 }  // namespace sta_api

@@ -104,36 +104,6 @@ __device__ __forceinline__ float taylor_fast(float x, const TaylorCoef& c) {
 // exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding).
 __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
 
-// Elements [off, off+4) of a row as raw bits: 16 bytes (ES = 4) or 8 bytes (ES = 2, in .x/.y).  Rows are
-// read in units of 4 elements; the caller guarantees alignment and that the unit lies in the row.
-template <int ES>
-__device__ __forceinline__ uint4 load_unit(const void* base, int64_t off) {
-  if constexpr (ES == 4) {
-    return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
-  } else {
-    const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
-    return uint4{r.x, r.y, 0u, 0u};
-  }
-}
-
-// A raw unit as 4 floats (fp32 bits when ES = 4, else bf16 / fp16 by dtype), times `scale`.
-template <int ES>
-__device__ __forceinline__ floatx4 unit_to_f4(const uint4& r, int dtype, float scale) {
-  floatx4 f;
-  if constexpr (ES == 4) {
-    f = floatx4{__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w)};
-  } else if (dtype == BF16) {
-    f = floatx4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
-                __uint_as_float(r.y & 0xffff0000u)};
-  } else {
-    f = floatx4{static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x & 0xffffu))),
-                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x >> 16))),
-                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y & 0xffffu))),
-                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y >> 16)))};
-  }
-  return f * scale;
-}
-
 // Work layout: one workgroup per (head, tile of 64*RS query rows); wave w owns RS strips of 16 rows.
 // Keys are staged in LDS 64 (or 32) at a time: K row-major, V transposed ([column][key]).  For a staged
 // batch each wave computes X = K Q^T for all its (strip, 16-key subtile) pairs with interleaved MFMA

@@ -69,6 +69,36 @@ __device__ __forceinline__ float taylor_poly(float x, int deg) {
   return out;
 }
 
+// Elements [off, off+4) of a row as raw bits: 16 bytes (ES = 4) or 8 bytes (ES = 2, in .x/.y).  Rows are
+// read in units of 4 elements; the caller guarantees alignment and that the unit lies in the row.
+template <int ES>
+__device__ __forceinline__ uint4 load_unit(const void* base, int64_t off) {
+  if constexpr (ES == 4) {
+    return *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+  } else {
+    const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+    return uint4{r.x, r.y, 0u, 0u};
+  }
+}
+
+// A raw unit as 4 floats (fp32 bits when ES = 4, else bf16 / fp16 by dtype), times `scale`.
+template <int ES>
+__device__ __forceinline__ floatx4 unit_to_f4(const uint4& r, int dtype, float scale) {
+  floatx4 f;
+  if constexpr (ES == 4) {
+    f = floatx4{__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z), __uint_as_float(r.w)};
+  } else if (dtype == BF16) {
+    f = floatx4{__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                __uint_as_float(r.y & 0xffff0000u)};
+  } else {
+    f = floatx4{static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x & 0xffffu))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.x >> 16))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y & 0xffffu))),
+                static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.y >> 16)))};
+  }
+  return f * scale;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on XCD w % 8).  This maps
 // the hardware workgroup id to a logical id such that consecutive logical ids share an XCD, so the
 // workgroups that read the same head's rows share one L2.

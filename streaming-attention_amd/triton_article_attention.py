@@ -26,7 +26,7 @@ from fast_article_attention import safe_relative_l2  # noqa: F401  (re-exported 
 Tensor = torch.Tensor
 
 __all__ = ["TritonArticleStats", "build_segment_mean_coreset", "torch_classical_causal_attention",
-           "triton_article_causal_attention", "exp_taylor", "safe_relative_l2"]
+           "triton_article_causal_attention", "triton_flash_causal_attention", "exp_taylor", "safe_relative_l2"]
 
 
 def _require_backend() -> None:
@@ -220,3 +220,34 @@ def triton_article_causal_attention(
     stats = TritonArticleStats(degree, block_size, compress_stride, int(r), int(r * (dim + dv) * ekv),
                                int(n * (dim + dv) * ekv), int(n * n * ekv), int(n * dv * eo))
     return out, stats
+
+
+@torch.no_grad()
+def triton_flash_causal_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    *,
+    scale: Optional[float] = None,
+    block_m: int = 16,
+    block_n: int = 64,
+    value_block: Optional[int] = None,
+    output_dtype: Optional[torch.dtype] = torch.float32,
+) -> Tensor:
+    """Exact causal attention baseline (triton_article_attention.py:580-637): online row maximum, fp32
+    accumulation, no N x N score matrix, for [N,D] and [B,H,N,D] tensors; computed by the HIP flash
+    kernel.  block_m, block_n and value_block are tile hints of the Triton kernel, accepted and ignored
+    (the HIP kernel uses its own CDNA4 tiling)."""
+    _require_backend()
+    _require_device(q, k, v)
+    q3, k3, v3, original_shape, had_bh = _flatten_bh_qkv(q, k, v)
+    dim = q3.shape[-1]
+    dv = v3.shape[-1]
+    if dim > 128:
+        raise ValueError("this compact kernel supports D <= 128")
+    if dv > 256:
+        raise ValueError("this compact kernel supports Dv <= 256")
+    if not (q3.dtype == k3.dtype == v3.dtype) or q3.dtype not in _native.DTYPE_CODES:
+        q3, k3, v3 = q3.float(), k3.float(), v3.float()
+    out3 = _engine.flash(q3, k3, v3, scale=_attention_scale(scale, dim), out_dtype=output_dtype or torch.float32)
+    return _unflatten_output(out3, original_shape, had_bh)

@@ -47,6 +47,14 @@ def test_library_rejects_bad_arguments_without_touching_a_device():
                            None) == _native.STA_ERR_ARG
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
+    # flash: null pointers, D beyond the limit, strides not whole 4-element units, misaligned rows
+    assert lib.sta_flash_attention(None, 16, 16, 0, 1, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_ARG
+    assert lib.sta_flash_attention(16, 16, 16, 0, 1, 8, 129, 4, 132, 4, 1.0, 16, 0, None) == _native.STA_ERR_UNSUPPORTED
+    assert lib.sta_flash_attention(16, 16, 16, 0, 1, 8, 4, 300, 4, 300, 1.0, 16, 0, None) == _native.STA_ERR_UNSUPPORTED
+    assert lib.sta_flash_attention(16, 16, 16, 0, 1, 8, 6, 4, 6, 4, 1.0, 16, 0, None) == _native.STA_ERR_ARG
+    assert lib.sta_flash_attention(8, 16, 16, 0, 1, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_ARG
+    assert lib.sta_flash_attention(16, 16, 16, 7, 1, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_DTYPE
+    assert lib.sta_flash_attention(16, 16, 16, 0, 0, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_SHAPE
 
 
 def _norm(raw):
@@ -242,6 +250,8 @@ def test_triton_api_argument_errors():
         taa.triton_article_causal_attention(q, k, v)  # CPU tensors (test_triton_article_attention.py:17-26)
     with pytest.raises(ValueError):
         taa.build_segment_mean_coreset(k[None], v[None], block_size=8, compress_stride=3)
+    with pytest.raises((ImportError, ValueError)):
+        taa.triton_flash_causal_attention(q, k, v)  # CPU tensors
 
 
 def test_stats_formulas_match_reference(golden):

@@ -98,6 +98,35 @@ def test_make_data_matches_reference(golden):
     assert np.array_equal(q.numpy(), g["q"]) and np.array_equal(k.numpy(), g["k"]) and np.array_equal(v.numpy(), g["v"])
 
 
+# --------------------------------------------------------------------------- flash baseline recursion
+
+@pytest.mark.parametrize("block_n", [1, 7, 16, 64, 1000])
+def test_flash_recursion_equals_softmax_attention(block_n):
+    # the blocked online-softmax recursion (triton_article_attention.py:397-428) against torch.softmax
+    g = torch.Generator().manual_seed(block_n)
+    q = torch.randn(150, 12, generator=g) * 2.0  # logits of tens: the running maximum moves
+    k = torch.randn(150, 12, generator=g) * 2.0
+    v = torch.randn(150, 5, generator=g)
+    out = orc.flash_attention_blocked(q, k, v, 1.5, block_n)
+    assert rel(out, orc.classical_attention(q, k, v, 1.5)) < 1e-12
+
+
+def test_flash_recursion_special_cases():
+    g = torch.Generator().manual_seed(1)
+    v = torch.randn(40, 3, generator=g)
+    q = torch.randn(40, 4, generator=g)
+    k = torch.ones(40, 4)  # equal keys: uniform weights over each prefix
+    out = orc.flash_attention_blocked(q, k, v, 1.0, 16)
+    expect = torch.cumsum(v.double(), 0) / torch.arange(1, 41, dtype=torch.float64)[:, None]
+    assert torch.allclose(out, expect, rtol=1e-12, atol=1e-12)
+    assert torch.equal(out[0], v[0].double())  # row 0 sees key 0 only
+    # logits of 1000 and 2000: no overflow, each row takes its largest visible key
+    qb = torch.tensor([[1.0, 0.0]] * 3)
+    kb = torch.tensor([[0.0, 0.0], [1000.0, 0.0], [2000.0, 0.0]])
+    out = orc.flash_attention_blocked(qb, kb, v[:3], 1.0, 2)
+    assert torch.allclose(out, v[:3].double())
+
+
 # --------------------------------------------------------------------------- exact residual
 
 def test_none_compressor_reconstructs_classical():
