@@ -21,6 +21,11 @@ degree 2, scale 1/8, bf16 inputs q, k, v ~ N(0,1)/8 (generated on the GPU); one 
 query(q) for every stream, block completions (compress + merges) included.  value = stream-tokens/s;
 roofline of the moment-state read (HBM); CPU baseline = the reference's per-token streaming object
 restated in oracle/, one stream with the same state sizes.
+
+`--workload flash_c3` measures the exact causal softmax baseline (triton_flash_causal_attention) on the
+default workload's inputs (1 x 32 heads, N = 65536, d = dv = 64, scale 1/8, fp32): value =
+head-tokens/s, roofline of the flash kernel against the fp32 MFMA peak (algorithmic (d + dv) N (N + 1)
+flop per head); CPU baseline = torch's fp32 softmax attention on the host over a bounded row sample.
 """
 
 from __future__ import annotations
@@ -46,6 +51,10 @@ WORKLOAD = dict(workload="prefill_levels_c3", batch=1, heads=32, seq_len=65536, 
 
 DECODE = dict(workload="decode_levels_c5", batch=64, heads=32, prefix=32768, d=64, dv=64, degree=2, block=256,
               scale=0.125, compressor="sorted_pair", data="N(0,1)/8", dtype="bf16", seed=0)
+
+FLASH = dict(WORKLOAD, workload="flash_c3", semantics="exact causal softmax attention")
+for _k in ("degree", "block", "compressor"):
+    del FLASH[_k]
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
@@ -108,17 +117,19 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seq-len", type=int, default=WORKLOAD["seq_len"])
     ap.add_argument("--heads", type=int, default=WORKLOAD["heads"])
-    ap.add_argument("--workload", default=WORKLOAD["workload"], choices=[WORKLOAD["workload"], DECODE["workload"]])
+    ap.add_argument("--workload", default=WORKLOAD["workload"],
+                    choices=[WORKLOAD["workload"], DECODE["workload"], FLASH["workload"]])
     ap.add_argument("--streams", type=int, default=DECODE["batch"] * DECODE["heads"], help="decode streams")
     ap.add_argument("--prefix", type=int, default=DECODE["prefix"], help="decode prefix tokens")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB fp32 tensor 3 times (calibration kernel for the HBM byte counters)")
     args = ap.parse_args()
     decode = args.workload == DECODE["workload"]
+    flash = args.workload == FLASH["workload"]
     if args.steps is None:
-        args.steps = 256 if decode else 10
+        args.steps = 256 if decode else (3 if flash else 10)
     if args.warmup is None:
-        args.warmup = 8 if decode else 2
+        args.warmup = 8 if decode else (1 if flash else 2)
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (heads shard with no "
               f"communication across GPUs; see DESIGN.md)", file=sys.stderr)
@@ -136,8 +147,10 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4, "copies": 3}))
         return 0
 
-    if args.workload == DECODE["workload"]:
+    if decode:
         return run_decode(args)
+    if flash:
+        return run_flash(args)
 
     import _engine
     import _plan
@@ -225,6 +238,106 @@ def main() -> int:
         cb = cpu_baseline(q, k, v, w)
         line["cpu_baseline"] = cb
         line["speedup_vs_cpu_baseline"] = value / cb["value"]
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+def run_flash(args) -> int:
+    """Exact causal softmax attention throughput (see the module docstring)."""
+    import _engine
+    import triton_article_attention as taa
+
+    w = dict(FLASH, seq_len=args.seq_len, heads=args.heads)
+    bh, n, d, dv = w["batch"] * w["heads"], w["seq_len"], w["d"], w["dv"]
+    print(f"[bench] flash: generating inputs {w['batch']}x{w['heads']}x{n}x{d}", file=sys.stderr, flush=True)
+    q, k, v = make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"])
+    dev = torch.device("cuda:0")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    q3, k3, v3 = qd.reshape(bh, n, d), kd.reshape(bh, n, d), vd.reshape(bh, n, dv)
+
+    def step(timer=None):
+        return _engine.flash(q3, k3, v3, scale=w["scale"], timer=timer)
+
+    api_out = taa.triton_flash_causal_attention(qd, kd, vd, scale=w["scale"])
+    out = step()
+    for _ in range(args.warmup - 1):
+        step()
+    torch.cuda.synchronize()
+    assert torch.equal(out.reshape(api_out.shape), api_out)
+    print(f"[bench] flash: warmup done", file=sys.stderr, flush=True)
+
+    timer = _engine.KernelTimer()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        step(timer)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = start.elapsed_time(end) / args.steps
+    tot, cnt = timer.totals_ms()["flash"]
+    k_ms = tot / cnt
+    flops = float(d + dv) * n * (n + 1) * bh  # QK^T and PV over the n (n + 1) / 2 causal pairs
+    achieved = flops / (k_ms * 1e-3) / 1e12
+    value = bh * n / (ms_step * 1e-3)
+    line = {
+        "metric": "head-tokens/sec, exact causal softmax attention, N=64K d=64; % of MFMA roofline",
+        "value": value,
+        "unit": "head-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": w,
+        "roofline": {
+            "kernel": "flash_attn_kernel (online-softmax exact attention, fp32 matrix cores)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": MFMA_FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+            "traffic": measured_traffic(w["workload"], "flash_attn_kernel"),
+            "algorithmic_flops_per_launch": flops,
+            "avg_launch_ms": k_ms,
+        },
+        "kernels": {"flash": {"ms_total": round(tot, 4), "launches": cnt}},
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu_baseline:
+        print(f"[bench] flash: timing CPU baseline", file=sys.stderr, flush=True)
+        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+        chunk = 2048  # query rows per host product (the whole N x N logits of a head would be 17 GB)
+        qh, kh, vh = q[0, 0], k[0, 0], v[0, 0]
+        kt = kh.T.contiguous()
+        t0 = time.perf_counter()
+        for lo in range(0, n, chunk):
+            hi = min(lo + chunk, n)
+            logits = (qh[lo:hi] @ kt[:, :hi]) * w["scale"]
+            mask = torch.arange(hi)[None, :] > torch.arange(lo, hi)[:, None]
+            o = torch.softmax(logits.masked_fill(mask, float("-inf")), dim=-1) @ vh[:hi]
+            assert bool(torch.isfinite(o).all())
+        secs_head = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": n / secs_head,
+            "unit": "head-tokens/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"torch fp32 causal softmax attention on the host (the reference's "
+                       f"torch_classical_causal_attention, triton_article_attention.py:123-143) over one whole "
+                       f"head (N={n}) in blocks of {chunk} query rows against their prefix: {secs_head:.2f} s"),
+        }
+        line["speedup_vs_cpu_baseline"] = value / line["cpu_baseline"]["value"]
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line))

@@ -20,6 +20,7 @@ kernels K5).  Beyond the reference it takes `streams=S` for S independent stream
 
 from __future__ import annotations
 
+import argparse
 import math
 from dataclasses import dataclass
 from typing import List, Optional, Tuple, Union
@@ -482,3 +483,45 @@ class ArticleStreamingAttention:
                               eps=self.denominator_eps, out_dtype=self.dtype)
         self._st.extend(k3, v3)
         return res.out[0] if one else res.out
+
+
+# ----------------------------------------------------------------------------- small CLI sanity check
+# Same flags and printed lines as the reference's (streaming_taylor_coreset_attention.py:762-805).
+
+def _demo(args: argparse.Namespace) -> None:
+    device = _resolve_gpu(args.device)
+    dtype = _resolve_dtype(args.dtype)
+    torch.manual_seed(args.seed)
+    q = torch.randn(args.n, args.d, device=device, dtype=dtype)
+    k = torch.randn(args.n, args.d, device=device, dtype=dtype)
+    v = torch.randn(args.n, args.dv, device=device, dtype=dtype)
+    # unit directions scaled to the radius: moderate logits for the low-degree split
+    q = q / torch.clamp(torch.linalg.vector_norm(q, dim=-1, keepdim=True), min=1e-12) * args.radius
+    k = k / torch.clamp(torch.linalg.vector_norm(k, dim=-1, keepdim=True), min=1e-12) * args.radius
+    scale = args.scale if args.scale is not None else 1.0
+    exact = classical_causal_attention(q, k, v, scale=scale)
+    approx, sizes = article_causal_attention(q, k, v, degree=args.degree, block_size=args.block_size, scale=scale,
+                                             compressor=args.compressor, seed=args.seed, return_state_sizes=True)
+    print(f"relative_l2={safe_relative_l2(approx, exact):.6g}")
+    print(f"max_abs={(approx - exact).abs().max().item():.6g}")
+    print(f"final_state_bytes={sizes[-1] if sizes else 0:,}")
+
+
+def _parser() -> argparse.ArgumentParser:
+    p = argparse.ArgumentParser(description="Demo for streaming Taylor+coreset attention (HIP/MI355X)")
+    p.add_argument("--n", type=int, default=128)
+    p.add_argument("--d", type=int, default=16)
+    p.add_argument("--dv", type=int, default=16)
+    p.add_argument("--degree", type=int, default=2)
+    p.add_argument("--block-size", type=int, default=64)
+    p.add_argument("--radius", type=float, default=1.0)
+    p.add_argument("--scale", type=float, default=None)
+    p.add_argument("--compressor", choices=["sorted_pair", "random", "none"], default="sorted_pair")
+    p.add_argument("--device", default=None)
+    p.add_argument("--dtype", default="float32")
+    p.add_argument("--seed", type=int, default=0)
+    return p
+
+
+if __name__ == "__main__":
+    _demo(_parser().parse_args())

@@ -251,3 +251,123 @@ def triton_flash_causal_attention(
         q3, k3, v3 = q3.float(), k3.float(), v3.float()
     out3 = _engine.flash(q3, k3, v3, scale=_attention_scale(scale, dim), out_dtype=output_dtype or torch.float32)
     return _unflatten_output(out3, original_shape, had_bh)
+
+
+# ----------------------------------------------------------------------------- demo / benchmark CLI
+# Same flags and table columns as the reference's CLI (triton_article_attention.py:640-855); the
+# "triton_*" columns time this module's HIP kernels.
+
+def _make_data(n: int, d: int, dv: int, *, batch: int, heads: int, radius: float, data: str,
+               device: torch.device, dtype: torch.dtype, seed: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """Inputs in the reference's draw order on `device` (triton_article_attention.py:645-680): randn q, k,
+    v of `dtype`; for unit_ball the radii rand^(1/d) r of q then k; unit_sphere scales to radius r."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    lead = (batch, heads) if batch * heads > 1 else ()
+    q = torch.randn(*lead, n, d, device=device, dtype=dtype, generator=g)
+    k = torch.randn(*lead, n, d, device=device, dtype=dtype, generator=g)
+    v = torch.randn(*lead, n, dv, device=device, dtype=dtype, generator=g)
+
+    def unit(x):
+        return x / torch.clamp(torch.linalg.vector_norm(x, dim=-1, keepdim=True), min=1e-12)
+
+    if data == "unit_ball":
+        rq = torch.rand((*q.shape[:-1], 1), device=device, dtype=dtype, generator=g).pow(1.0 / d) * radius
+        rk = torch.rand((*k.shape[:-1], 1), device=device, dtype=dtype, generator=g).pow(1.0 / d) * radius
+        q, k = unit(q) * rq, unit(k) * rk
+    elif data == "unit_sphere":
+        q, k = unit(q) * radius, unit(k) * radius
+    elif data != "normal":
+        raise ValueError("data must be one of {'unit_ball', 'unit_sphere', 'normal'}")
+    return q, k, v
+
+
+_DTYPES = {"float32": torch.float32, "fp32": torch.float32, "float16": torch.float16, "fp16": torch.float16,
+           "half": torch.float16, "bfloat16": torch.bfloat16, "bf16": torch.bfloat16}
+
+
+def _resolve_dtype(name: str) -> torch.dtype:
+    if name.lower() not in _DTYPES:
+        raise ValueError(f"unsupported dtype {name!r}; choose one of {sorted(_DTYPES)}")
+    return _DTYPES[name.lower()]
+
+
+def _bench_gpu_ms(fn, repeats: int) -> float:
+    """Median of `repeats` HIP-event timings after 3 warm-up calls."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    times: List[float] = []
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(float(start.elapsed_time(end)))
+    return statistics.median(times)
+
+
+def _demo(args: argparse.Namespace) -> None:
+    _require_backend()
+    if not torch.cuda.is_available():
+        raise RuntimeError("a ROCm GPU is required for this benchmark")
+    device = torch.device(args.device)
+    dtype = _resolve_dtype(args.dtype)
+    scale = args.scale if args.scale is not None else (1.0 / math.sqrt(args.d) if args.standard_scale else 1.0)
+    headers = ["n", "rel_l2_article", "max_abs_article", "rel_l2_flash", "torch_classical_ms", "triton_flash_ms",
+               "triton_article_ms", "coreset_items", "coreset_bytes", "kv_bytes", "score_matrix"]
+    print("\n" + " | ".join(headers))
+    print(" | ".join(["---"] * len(headers)))
+    for n in args.sweep_n:
+        q, k, v = _make_data(n, args.d, args.dv, batch=args.batch, heads=args.heads, radius=args.radius,
+                             data=args.data, device=device, dtype=dtype, seed=args.seed)
+        tiles = dict(block_m=args.block_m, block_n=args.block_n, value_block=args.value_block,
+                     output_dtype=torch.float32)
+        article_kw = dict(tiles, degree=args.degree, block_size=args.block_size, compress_stride=args.compress_stride,
+                          scale=scale, block_r=args.block_r)
+        exact = torch_classical_causal_attention(q.float(), k.float(), v.float(), scale=scale)
+        flash = triton_flash_causal_attention(q, k, v, scale=scale, **tiles)
+        article, stats = triton_article_causal_attention(q, k, v, return_stats=True, **article_kw)
+        torch_ms = _bench_gpu_ms(lambda: torch_classical_causal_attention(q.float(), k.float(), v.float(), scale=scale),
+                                 args.repeats)
+        flash_ms = _bench_gpu_ms(lambda: triton_flash_causal_attention(q, k, v, scale=scale, **tiles), args.repeats)
+        article_ms = _bench_gpu_ms(lambda: triton_article_causal_attention(q, k, v, **article_kw), args.repeats)
+        print(" | ".join([
+            str(n), f"{safe_relative_l2(article, exact):.4g}", f"{(article - exact).abs().max().item():.4g}",
+            f"{safe_relative_l2(flash, exact):.4g}", f"{torch_ms:.3f}", f"{flash_ms:.3f}", f"{article_ms:.3f}",
+            str(stats.coreset_items_per_sequence), _human_bytes(stats.coreset_bytes_per_sequence),
+            _human_bytes(stats.kv_bytes_per_sequence), _human_bytes(stats.score_matrix_bytes_per_sequence),
+        ]))
+
+
+def _parse_args(argv: Optional[Sequence[str]] = None) -> argparse.Namespace:
+    p = argparse.ArgumentParser(description="HIP (MI355X) kernels for article-style Taylor + residual-coreset "
+                                            "attention, with the exact flash baseline")
+    p.add_argument("--sweep-n", type=int, nargs="+", default=[256, 512, 1024, 2048])
+    p.add_argument("--d", type=int, default=32)
+    p.add_argument("--dv", type=int, default=32)
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--heads", type=int, default=1)
+    p.add_argument("--degree", type=int, default=2, choices=[0, 1, 2])
+    p.add_argument("--block-size", type=int, default=128)
+    p.add_argument("--compress-stride", type=int, default=2,
+                   help="1 disables residual compression and should match exact attention")
+    p.add_argument("--block-m", type=int, default=16)
+    p.add_argument("--block-n", type=int, default=64)
+    p.add_argument("--block-r", type=int, default=64)
+    p.add_argument("--value-block", type=int, default=None)
+    p.add_argument("--data", choices=["unit_ball", "unit_sphere", "normal"], default="unit_ball")
+    p.add_argument("--radius", type=float, default=1.0)
+    p.add_argument("--scale", type=float, default=None)
+    p.add_argument("--standard-scale", action="store_true", help="Use 1/sqrt(d) when --scale is omitted")
+    p.add_argument("--device", default="cuda")
+    p.add_argument("--dtype", default="float16", choices=sorted(_DTYPES))
+    p.add_argument("--repeats", type=int, default=10)
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args(argv)
+
+
+if __name__ == "__main__":
+    _demo(_parse_args())
