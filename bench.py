@@ -8,9 +8,10 @@ the reference's draw order and copied to HBM before timing).
 
 One step = one full forward through the public API path (moment scan K1, level-tree compressor K3,
 fused residual + normalisation K2/K4).  Prints one JSON line:
-  value = head-tokens/s (B*H*N / step time), roofline of the dominant kernel (the moment scan, fp32
-  MFMA) from HIP events recorded around its launches inside the timed region, and the CPU baseline:
-  the reference CPU fast path (oracle restatement, flat sorted_pair coreset, stream moments) timed on
+  value = head-tokens/s (B*H*N / step time), roofline of the dominant kernel (the moment scan; its
+  split-bf16 matrix-core products bound fp32-equivalent flops at a third of the bf16 peak) from HIP
+  events recorded around its launches inside the timed region, and the CPU baseline: the reference
+  CPU fast path (oracle restatement, flat sorted_pair coreset, stream moments) timed on
   a bounded sample of one head on this host's cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
@@ -57,6 +58,10 @@ for _k in ("degree", "block", "compressor"):
     del FLASH[_k]
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
+# split-bf16 products: each fp32 product is three bf16 matrix-core products, so the matrix-core bound on
+# fp32-equivalent flops is a third of the bf16 peak
+SPLIT_BF16_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 3.0
 HBM_PEAK_GBS = 8000.0
 
 
@@ -203,6 +208,8 @@ def main() -> int:
     mom_ms = per_kernel["moments"]["ms_total"] / per_kernel["moments"]["launches"]
     achieved = mom_flops / (mom_ms * 1e-3) / 1e12
     value = bh * n / (ms_step * 1e-3)
+    split = _engine.MOMENT_PRODUCTS == _engine._native.PRODUCTS_SPLIT_BF16
+    peak = SPLIT_BF16_PEAK_TFLOPS if split else MFMA_FP32_PEAK_TFLOPS
 
     line = {
         "metric": "head-tokens/sec, N=64K d=64 deg-2; % of HBM/MFMA roofline",
@@ -222,9 +229,12 @@ def main() -> int:
             "kernel": "moments_kernel (K1, exact Taylor moment scan)",
             "bound": "mfma",
             "achieved": achieved,
-            "peak": MFMA_FP32_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+            "frac": achieved / peak,
+            "products": "split-bf16" if split else "fp32",
+            "peak_basis": ("fp32-equivalent flops of split-bf16 products: bf16 dense peak / 3 (three bf16 "
+                           "matrix-core products per fp32 product)" if split else "fp32 matrix-core peak"),
             "traffic": measured_traffic(w["workload"], "moments_kernel"),
             "algorithmic_flops_per_launch": mom_flops,
             "avg_launch_ms": mom_ms,

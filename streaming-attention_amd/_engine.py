@@ -22,6 +22,11 @@ import _plan
 
 SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 
+# Matrix-core products of the moment scan (sta_moments): fp32 operands carried as bf16 hi + lo with three
+# bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
+# products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
+MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+
 _dev_lock = threading.Lock()
 _dev_cache: Dict[tuple, object] = {}
 
@@ -121,6 +126,7 @@ def prefill(
     exp_clamp: bool = False,
     draws: Optional[_plan.Draws] = None,
     timer: Optional[KernelTimer] = None,
+    products: Optional[int] = None,
 ) -> PrefillResult:
     """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype."""
     if semantics not in SEMANTICS:
@@ -206,8 +212,8 @@ def prefill(
         st = lib.sta_moments(
             mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
             float(scale), chunk, shift,
-            fsplit, ms.wave_tiles, int(ms.mixed), fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(),
-            low_den.data_ptr(), stream)
+            fsplit, ms.wave_tiles, int(ms.mixed), MOMENT_PRODUCTS if products is None else int(products),
+            fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")
 
     _run(timer, "moments", k1)

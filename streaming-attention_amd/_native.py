@@ -24,6 +24,8 @@ STA_ERR_HIP = 4
 STA_ERR_ARG = 5
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+PRODUCTS_FP32 = 0
+PRODUCTS_SPLIT_BF16 = 1
 
 _c_p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -40,7 +42,7 @@ _SIGNATURES = {
     "sta_moment_chunk": (_i32, [_i32]),
     "sta_moments": (
         _i32,
-        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
          _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
     "sta_moment_mixed_ok": (_i32, [_i32, _i32, _i32]),

@@ -2,8 +2,9 @@
 
     python streaming-attention_amd/build_native.py
 
-The library is 83 objects compiled in parallel and linked into one shared object: api.hip (entry
-points, compressor and decode kernels), launch_moments.hip, launch_accumulate.hip, and
+The library is 84 objects compiled in parallel and linked into one shared object: api.hip (entry
+points, compressor and decode kernels), launch_moments.hip (fp32 and split-bf16 products),
+launch_accumulate.hip, and
 launch_block.hip and launch_flash.hip once per residual / flash kernel configuration (padded key
 width, value-column tiles, element size).  Objects go to streaming-attention_amd/_build/.
 
@@ -24,7 +25,8 @@ HERE = pathlib.Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 # (source, object stem, defines), slowest first
 UNITS = (
-    ("launch_moments.hip", "launch_moments", ()),
+    ("launch_moments.hip", "launch_moments_split", ("-DSTA_MOM_SPLIT=1",)),
+    ("launch_moments.hip", "launch_moments", ("-DSTA_MOM_SPLIT=0",)),
     ("launch_accumulate.hip", "launch_accumulate", ()),
 ) + tuple(("launch_block.hip", f"launch_block_{dp}_{dvt}_{es}",
            (f"-DSTA_BLOCK_DP={dp}", f"-DSTA_BLOCK_DVT={dvt}", f"-DSTA_BLOCK_ES={es}"))

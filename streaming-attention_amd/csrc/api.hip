@@ -129,7 +129,8 @@ int sta_moment_occupancy(int d, int wave_tiles) {
 
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
                 int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
-                const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den, void* stream) {
+                int products, const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den,
+                void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0) return STA_ERR_SHAPE;
@@ -137,6 +138,7 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
   if (mixed != 0 && (mixed != 1 || fsplit % 2 != 0 || !sta_moment_mixed_ok(d, degree, wave_tiles))) return STA_ERR_ARG;
+  if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
   // rows are read in 16-byte units: d must be a whole number of units, v rows whole 32-column groups,
   // every base 16-byte aligned, and a head's rows addressable with 32-bit byte offsets
   const int esize = dtype == STA_F32 ? 4 : 2;
@@ -149,7 +151,9 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
-  return dispatch_moments(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
+  return products == STA_PRODUCTS_SPLIT_BF16
+             ? dispatch_moments<true>(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3)
+             : dispatch_moments<false>(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,

@@ -63,7 +63,9 @@ inline int moment_wave_tiles(int d, int degree, int want) {
   return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
 }
 
-// launch_moments.hip: the prefill moment scan (moments_kernel) for wave-tile count nt.
+// launch_moments.hip, one object per SPLIT: the prefill moment scan (moments_kernel) for wave-tile count
+// nt, with fp32 (SPLIT false) or split-bf16 (SPLIT true) matrix-core products.
+template <bool SPLIT>
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
 int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);

@@ -53,6 +53,47 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Split-bf16 products (bf16 matrix cores at 16x the fp32 rate).  An fp32 value x is carried as
+// hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even: x - hi is exact in fp32 and
+// |x - hi - lo| <= 2^-9 |x - hi| <= 2^-18 |x|.  A product is taken as hi.hi' + hi.lo' + lo.hi' (bf16
+// products are exact, sums fp32), which drops lo.lo' (<= 2^-18 |x x'|): about 2^-16 relative error
+// per product, against 2^-11 for the tf32 operands of the reference's Triton dots.
+// v_mfma_f32_16x16x32_bf16, lane l = 16 g + i:  A[i][8 g + j] = a[j],  B[8 g + j][i] = b[j],
+// D[4 g + r][i] = d[r]  (the layout of mfma4 with 8 contraction elements per lane instead of one).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ floatx4 mfma_bf16(bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// two floats to packed bf16 (one v_cvt_pk_bf16_f32, round to nearest even)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
+}
+
+// 3 VALU per value: packed hi, hi back to fp32 from the packed bits (shift / mask), x - hi, packed lo
+__device__ __forceinline__ void split_bf16(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = pk_bf16(x[2 * p], x[2 * p + 1]);
+    const float h0 = __uint_as_float(h[p] << 16), h1 = __uint_as_float(h[p] & 0xffff0000u);
+    l[p] = pk_bf16(x[2 * p] - h0, x[2 * p + 1] - h1);
+  }
+  hi = __builtin_bit_cast(bf16x8, uint4{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8, uint4{l[0], l[1], l[2], l[3]});
+}
+
+// c += a.b for split operands (three bf16 matrix-core products)
+__device__ __forceinline__ floatx4 mfma_split(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                              const bf16x8& bl, floatx4 c) {
+  c = mfma_bf16(ah, bl, c);
+  c = mfma_bf16(al, bh, c);
+  return mfma_bf16(ah, bh, c);
+}
+
 // Empty register constraint: pins the computation of x at this point of the instruction stream (keeps
 // the scheduler from sinking an accumulation chain and holding all of its inputs live).
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }

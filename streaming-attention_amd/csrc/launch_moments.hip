@@ -1,15 +1,21 @@
 // Launches of the prefill moment scan (moments_kernel), one instantiation per wave-tile count, degree-3
 // flag, d > 64 flag and element size (4: fp32, 2: bf16 / fp16, so the chunk staging is straight-line).
+// The build compiles this unit twice, with -DSTA_MOM_SPLIT=0 (fp32 matrix-core products) and
+// -DSTA_MOM_SPLIT=1 (split-bf16 products).
 #include "api_common.hpp"
 #include "moments.hip"
+
+#if !defined(STA_MOM_SPLIT)
+#error "launch_moments.hip is compiled with -DSTA_MOM_SPLIT=<0|1>"
+#endif
 
 namespace sta_api {
 namespace {
 
-template <int NT, bool DEG3, bool DBIG, int ES>
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT>
 int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES>;
+  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -21,14 +27,17 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
 
 }  // namespace
 
+template <bool SPLIT>
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
   const bool big = a.d > 64;
 #define STA_CASE(NT, D3, BIG)                                                                       \
   if (nt == NT && deg3 == D3 && big == BIG)                                                         \
-    return a.esize == 4 ? launch<NT, D3, BIG, 4>(a, bh, s) : launch<NT, D3, BIG, 2>(a, bh, s);
+    return a.esize == 4 ? launch<NT, D3, BIG, 4, SPLIT>(a, bh, s) : launch<NT, D3, BIG, 2, SPLIT>(a, bh, s);
   STA_MOMENT_CONFIGS(STA_CASE)
 #undef STA_CASE
   return STA_ERR_UNSUPPORTED;
 }
+
+template int dispatch_moments<STA_MOM_SPLIT != 0>(const sta::MomArgs&, int64_t, hipStream_t, int, bool);
 
 }  // namespace sta_api

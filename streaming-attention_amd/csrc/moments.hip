@@ -364,10 +364,157 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, c
   }
 }
 
+// Split-bf16 form of mom_update: one 16x16x32 bf16 product covers the 32 tokens of the chunk.  A (16 f x
+// 32 tok): lane (li, lg) holds feature li of the tile for tokens 8 lg + j, j = 0..7 (the fp32 update's
+// A values of its 8 steps); B: V[8 lg + j][col].  The feature values and the values are split into
+// bf16 hi + lo, and S += A_hi B_lo + A_lo B_hi + A_hi B_hi (terms outermost, so the 2 NT accumulators
+// are independent chains).  The denominator sums the fp32 feature values as before.
+template <int NT, bool DEG3, bool DEN, class Mid>
+__device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][2], float* den_s, const float* Kt, const float* Vt,
+                                                 const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
+  constexpr int CT = 2;
+  floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 4 * h);
+      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 4 * h);
+      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 4 * h);
+    }
+  bf16x8 vh[CT], vl[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const floatx4 v0 = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
+    const floatx4 v1 = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
+    const float t[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    split_bf16(t, vh[ct], vl[ct]);
+  }
+  mid();
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x8 ah[NT], al[NT];
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+    float x[8];
+    float dacc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = fa[j >> 2][kt][j & 3] * fb[j >> 2][kt][j & 3];
+      if (DEG3) y *= fc[j >> 2][DEG3 ? kt : 0][j & 3];
+      y *= m.kcoef[kt];
+      x[j] = y;
+      if constexpr (DEN) dacc += y;
+    }
+    split_bf16(x, ah[kt], al[kt]);
+    if constexpr (DEN) {
+      dacc += __shfl_xor(dacc, 16);
+      dacc += __shfl_xor(dacc, 32);
+      if (lg == 0) den_s[16 * kt + li] += dacc;
+    }
+  }
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah[kt], vl[ct], st[kt][ct]);
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(al[kt], vh[ct], st[kt][ct]);
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah[kt], vh[ct], st[kt][ct]);
+}
+
+// Split-bf16 form of the query: out[tok][col] += sum_f phi_q(tok)[f] S[f][col] over the wave's tiles,
+// two tiles per 16x16x32 bf16 product.  For tile pair (t0, t1) the contraction index 8 lg + j is
+// feature 4 lg + j of t0 (j < 4) or 4 lg + j - 4 of t1: lane (li, lg) supplies phi_q of token li for
+// quad lg of both tiles (A) and its own accumulator elements S[t0|t1][4 lg + r][col li] (B), so the
+// state is used in place, split into bf16 hi + lo once per chunk.  An odd last tile pairs with zeros.
+// o[tt][ct] accumulates rows 16 tt + 4 lg + r, column 16 ct + li; dq the denominator (fp32 VALU, the
+// fp32 path's order).
+template <int NT, bool DEG3, bool DEN, int LDQ>
+__device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][2], float (&dq)[2], const floatx4 (&st)[NT][2],
+                                                const float* Qs, const float* den_s, const MomLane<NT, DEG3>& m,
+                                                int li, int lg) {
+  constexpr int CT = 2, TT = 2;
+  constexpr int NP = (NT + 1) / 2;
+  const float* qrow = Qs + li * LDQ;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int t0 = 2 * p, t1 = 2 * p + 1;
+    const bool has1 = t1 < NT;
+    bf16x8 sh[CT], sl[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      float t[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        t[r] = st[t0][ct][r];
+        t[4 + r] = has1 ? st[has1 ? t1 : t0][ct][r] : 0.f;
+      }
+      split_bf16(t, sh[ct], sl[ct]);
+    }
+    floatx4 dn0, dn1;
+    if constexpr (DEN) {
+      dn0 = *reinterpret_cast<const floatx4*>(den_s + 16 * t0 + 4 * lg);
+      dn1 = has1 ? *reinterpret_cast<const floatx4*>(den_s + 16 * (has1 ? t1 : t0) + 4 * lg) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    bf16x8 ah[TT], al[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      float x[8];
+      {
+        const float a0 = qrow[16 * tt * LDQ + m.qa[t0]];
+        const floatx4 b0 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[t0]);
+        const float c0 = DEG3 ? qrow[16 * tt * LDQ + m.qc[DEG3 ? t0 : 0]] : 1.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float y = a0 * b0[s];
+          if (DEG3) y *= c0;
+          x[s] = y;
+          if constexpr (DEN) dq[tt] = fmaf(y, dn0[s], dq[tt]);
+        }
+      }
+      if (has1) {
+        const int u = has1 ? t1 : t0;
+        const float a1 = qrow[16 * tt * LDQ + m.qa[u]];
+        const floatx4 b1 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[u]);
+        const float c1 = DEG3 ? qrow[16 * tt * LDQ + m.qc[DEG3 ? u : 0]] : 1.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float y = a1 * b1[s];
+          if (DEG3) y *= c1;
+          x[4 + s] = y;
+          if constexpr (DEN) dq[tt] = fmaf(y, dn1[s], dq[tt]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) x[4 + s] = 0.f;
+      }
+      if constexpr (DEN) pin(dq[tt]);
+      split_bf16(x, ah[tt], al[tt]);
+    }
+    floatx4(&oc)[TT][CT] = o[p & 1];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) oc[tt][ct] = mfma_bf16(ah[tt], sl[ct], oc[tt][ct]);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) oc[tt][ct] = mfma_bf16(al[tt], sh[ct], oc[tt][ct]);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) oc[tt][ct] = mfma_bf16(ah[tt], sh[ct], oc[tt][ct]);
+  }
+}
+
 // The kernel body for one workgroup (head bh, feature split fs, column group cs) with NT tiles per wave
 // out of the NTS the split table holds per wave.  DEN: this workgroup also keeps the denominator column
 // (only column group 0 does; the others would compute bit-identical values).
-template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN>
+template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT>
 __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int BUF = mom_buf_floats(DBIG);
@@ -435,7 +582,9 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) o[0][tt][ct] = o[1][tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    {
+    if constexpr (SPLIT) {
+      mom_query_split<NT, DEG3, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
+    } else {
       float x0[2][TT], x2[2][TT];
       floatx4 x1[2][TT], dn[2];
       const float* qrow = Qs + li * LDQ;
@@ -494,9 +643,13 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
     //      key reads ----
-    mom_update<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, [&]() {
+    auto mid = [&]() {
       if (c > 0) mom_reduce_store<DEN>(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
-    });
+    };
+    if constexpr (SPLIT)
+      mom_update_split<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
+    else
+      mom_update<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
     __syncthreads();
   }
   mom_reduce_store<DEN>(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C,
@@ -534,7 +687,8 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
 // Mixed tile counts (a.mixed, instantiated for NT = 4 and 5): the feature splits fs >= fsplit / 2 run
 // NT - 1 tiles per wave (their table slot NT is padding), so the tiles need fsplit * 4 * (NT - 1/2)
 // slots instead of fsplit * 4 * NT, and every compute unit holds one full and one short workgroup.
-template <int NT, bool DEG3, bool DBIG, int ES>
+// SPLIT: split-bf16 matrix-core products (mom_query_split / mom_update_split) instead of fp32 ones.
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT>
 __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
@@ -543,14 +697,14 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_
   if (MIX && a.mixed && fs >= a.fsplit / 2) {
     constexpr int NTL = MIX ? NT - 1 : NT;
     if (cs == 0)
-      moments_body<NTL, NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT>(a, bh, fs, cs);
     else
-      moments_body<NTL, NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT>(a, bh, fs, cs);
   } else {
     if (cs == 0)
-      moments_body<NT, NT, DEG3, DBIG, ES, true>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT>(a, bh, fs, cs);
     else
-      moments_body<NT, NT, DEG3, DBIG, ES, false>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT>(a, bh, fs, cs);
   }
 }
 

@@ -53,17 +53,21 @@ def test_mfma_operand_layout():
 
 # --------------------------------------------------------------------------- moments (K1 + closed form)
 
+# fp32 matrix-core products: 2e-6; split-bf16 products (about 2^-16 relative per product): 2e-5.  The
+# denominator column is fp32 VALU in both.
+@pytest.mark.parametrize("products,tol", [(_native.PRODUCTS_FP32, 2e-6), (_native.PRODUCTS_SPLIT_BF16, 2e-5)])
 @pytest.mark.parametrize("degree,d,dv,n", [(0, 8, 5, 77), (1, 16, 16, 200), (2, 32, 32, 1024), (2, 12, 5, 300),
-                                           (2, 64, 64, 700), (2, 128, 40, 257), (3, 16, 64, 333), (3, 6, 5, 64)])
-def test_low_degree_sums(degree, d, dv, n):
+                                           (2, 64, 64, 700), (2, 128, 40, 257), (3, 16, 64, 333), (3, 6, 5, 64),
+                                           (2, 64, 64, 8192)])
+def test_low_degree_sums(degree, d, dv, n, products, tol):
     g = torch.Generator().manual_seed(degree * 100 + d)
     q = torch.randn(n, d, generator=g) * 0.3
     k = torch.randn(n, d, generator=g) * 0.3
     v = torch.randn(n, dv, generator=g)
     res = _engine.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=degree, block=1, scale=0.9,
-                          semantics="taylor")
+                          semantics="taylor", products=products)
     num, den = orc.low_sums_direct(q, k, v, degree, 0.9)
-    assert rel(res.out[0], num) < 2e-6
+    assert rel(res.out[0], num) < tol
     assert rel(res.den[0], den) < 2e-6
 
 

@@ -43,8 +43,10 @@ def test_library_exports_header_symbols():
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, None, None, None, None,
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, 0, None, None, None, None,
                            None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, 64, 2, 1.0, 32, 0, 8, 5, 0, 2, 16, 16, 16, 16,
+                           None) == _native.STA_ERR_ARG  # unknown products mode
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
     # flash: null pointers, D beyond the limit, strides not whole 4-element units, misaligned rows
