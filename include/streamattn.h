@@ -202,6 +202,8 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *   rep_k / rep_v (fp32, row strides ld_rep_k / ld_rep_v, multiples of 4): materialized items
  *     (segment means; fp32 inputs only), NULL otherwise.
  *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
+ *   products: STA_PRODUCTS_FP32 or STA_PRODUCTS_SPLIT_BF16 for the logits q.k and the weighted value
+ *     sums (see sta_moments); weights, exponentials and all sums stay fp32.
  *   out: [BH][N][Dv] in out_dtype.
  *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator
  *     and out_den [BH][N] the denominator, unnormalised (the low_num/low_den pair of
@@ -209,7 +211,7 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  */
 int sta_block_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
                         int dv, int ld_qk, int ld_v, int degree, float scale, float eps, int mode, int block, int chunk,
-                        int shift, int exp_clamp, const float* low_num, const float* low_den, int fsplit,
+                        int shift, int exp_clamp, int products, const float* low_num, const float* low_den, int fsplit,
                         const int32_t* tile_ptr, const int32_t* tile_nodes, int n_tiles, const int32_t* node_meta,
                         int n_nodes, int cap, const int32_t* node_src, const float* node_w, const float* rep_k,
                         const float* rep_v, int ld_rep_k, int ld_rep_v, int64_t n_rep, void* out, int out_dtype,

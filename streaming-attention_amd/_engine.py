@@ -26,6 +26,13 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 # bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
 # products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+# The same choice for the residual / combine kernel (sta_block_attention): logits and weighted value sums,
+# when coreset items take part.  Without them (compressor "none", the raw Taylor sums, or sequences no
+# longer than a block) the result is exact attention and keeps fp32 products: the reference holds those
+# cases to 2e-6 / 3e-6 of softmax attention (test_fast_article_attention.py:10-29,
+# test_streaming_attention.py:10-21), which split products in this kernel exceed (about 5e-6).
+RESIDUAL_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+EXACT_SEMANTICS = ("exact", "taylor")
 
 _dev_lock = threading.Lock()
 _dev_cache: Dict[tuple, object] = {}
@@ -127,6 +134,7 @@ def prefill(
     draws: Optional[_plan.Draws] = None,
     timer: Optional[KernelTimer] = None,
     products: Optional[int] = None,
+    residual_products: Optional[int] = None,
 ) -> PrefillResult:
     """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype."""
     if semantics not in SEMANTICS:
@@ -264,10 +272,18 @@ def prefill(
         out_den = None
     n_nodes_arg = plan.n_nodes if (node_src is not None) else 0
 
+    if residual_products is not None:
+        k2_products = int(residual_products)
+    elif semantics in EXACT_SEMANTICS or (n_nodes_arg == 0 and n_rep_arg == 0):
+        k2_products = _native.PRODUCTS_FP32  # no coreset item: the result is exact attention
+    else:
+        k2_products = RESIDUAL_PRODUCTS
+
     def k24():
         st = lib.sta_block_attention(
             mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, d, dv, dm, mv.shape[-1], degree, float(scale),
-            float(eps), mode, block, chunk, shift, 1 if exp_clamp else 0, low_num.data_ptr(), low_den.data_ptr(),
+            float(eps), mode, block, chunk, shift, 1 if exp_clamp else 0,
+            k2_products, low_num.data_ptr(), low_den.data_ptr(),
             fsplit, tptr_d.data_ptr(), tnodes_d.data_ptr(), plan.n_tiles, meta_d.data_ptr(), n_nodes_arg, plan.cap,
             _native.ptr(node_src), _native.ptr(node_w), _native.ptr(rep_k), _native.ptr(rep_v),
             rep_k.shape[-1] if rep_k is not None else 0, rep_v.shape[-1] if rep_v is not None else 0, n_rep_arg,

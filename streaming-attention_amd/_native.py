@@ -58,7 +58,7 @@ _SIGNATURES = {
         _i32,
         [
             _c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32,  # q k v dtype bh n d dv ld_qk ld_v
-            _i32, _f32, _f32, _i32, _i32, _i32, _i32, _i32,  # degree scale eps mode block chunk shift clamp
+            _i32, _f32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,  # degree scale eps mode block chunk shift clamp products
             _c_p, _c_p, _i32,  # low_num low_den fsplit
             _c_p, _c_p, _i32, _c_p, _i32, _i32,  # tile_ptr tile_nodes n_tiles node_meta n_nodes cap
             _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i64,  # node_src node_w rep_k rep_v ld_rep_k ld_rep_v n_rep

@@ -319,7 +319,7 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
 
 int sta_block_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
                         int dv, int ld_qk, int ld_v, int degree, float scale, float eps, int mode, int block, int chunk,
-                        int shift, int exp_clamp, const float* low_num, const float* low_den, int fsplit,
+                        int shift, int exp_clamp, int products, const float* low_num, const float* low_den, int fsplit,
                         const int32_t* tile_ptr, const int32_t* tile_nodes, int n_tiles, const int32_t* node_meta,
                         int n_nodes, int cap, const int32_t* node_src, const float* node_w, const float* rep_k,
                         const float* rep_v, int ld_rep_k, int ld_rep_v, int64_t n_rep, void* out, int out_dtype,
@@ -330,6 +330,7 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || block <= 0 || fsplit <= 0) return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (mode < 0 || mode > 3 || chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
+  if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
   if (kTileRows % chunk != 0) return STA_ERR_ARG;
   if (n_tiles != static_cast<int>((n + shift + kTileRows - 1) / kTileRows)) return STA_ERR_SHAPE;
   if (n_nodes > 0 && (!node_meta || !node_src || !node_w || !tile_nodes || cap <= 0)) return STA_ERR_ARG;
@@ -352,6 +353,7 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   a.n_tiles = n_tiles; a.node_meta = node_meta; a.n_nodes = n_nodes; a.cap = cap; a.node_src = node_src;
   a.node_w = node_w; a.rep_k = rep_k; a.rep_v = rep_v; a.n_rep = n_rep; a.out = out; a.out_dtype = out_dtype; a.out_den = out_den;
   a.ldqk = ld_qk; a.ldvr = ld_v; a.ldrk = ld_rep_k; a.ldrv = ld_rep_v;
+  a.split = products == STA_PRODUCTS_SPLIT_BF16 ? 1 : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f32 = dtype == STA_F32;
   if (d <= 16) return f32 ? dispatch_dvt<16, 4>(a, bh, s) : dispatch_dvt<16, 2>(a, bh, s);

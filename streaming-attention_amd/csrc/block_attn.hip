@@ -66,6 +66,7 @@ struct BlockArgs {
   void* out;  // [BH][n][dv]
   int out_dtype;
   float* out_den;  // optional [BH][n]: when set, out (fp32) receives num and out_den receives den, unnormalised
+  int split;       // 1: split-bf16 matrix-core products (block_attn_kernel<..., true>)
 };
 
 __device__ __forceinline__ int64_t floordiv(int64_t a, int64_t b) {
@@ -129,7 +130,19 @@ __host__ __device__ constexpr int block_occupancy(int dp, int dvt, int rs) {
              : 1;
 }
 
-template <int DP, int DVT, int RS, int ES>
+// SPLIT: split-bf16 matrix-core products (the fp32 operands as bf16 hi + lo, three 16x16x32 bf16 products
+// per product; common.hpp).  The staged key and value rows are split once per workgroup when written
+// to LDS (bf16 hi and lo planes), the wave's query rows once per kernel, the probabilities per pair of
+// 16-key subtiles.  X = K Q^T: k-step m of lane group lg covers dimensions 32 m + 8 lg + j, j = 0..7
+// (16-byte LDS reads of 8 bf16).  num^T += V^T P^T over a subtile pair (2 s, 2 s + 1): contraction
+// index 8 lg + j is key 16 (2 s) + 4 lg + j (j < 4) or 16 (2 s + 1) + 4 lg + j - 4, i.e. element j & 3 of
+// the lane's own P tile of that subtile; the value planes store each pair's 32 keys in that order
+// (split_key_pos), so the A operand is again one 16-byte read.
+__host__ __device__ constexpr int split_key_pos(int r) {
+  return 32 * (r >> 5) + 8 * ((r >> 2) & 3) + 4 * ((r >> 4) & 1) + (r & 3);
+}
+
+template <int DP, int DVT, int RS, int ES, bool SPLIT>
 __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_kernel(const BlockArgs a) {
   constexpr int KB = block_kb(DP, DVT);  // keys per LDS stage
   constexpr int NSUB = KB / 16;                         // 16-key subtiles per stage
@@ -138,8 +151,23 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   constexpr int LDVT = KB + 4;
   constexpr int DQ = DP / 4;  // k-steps of X = K Q^T, dimensions per lane group
   constexpr int TM = 64 * RS;
-  __shared__ float Kst[KB * LDK];
-  __shared__ float Vt[DV * LDVT];
+  // split layout: dimensions padded to whole 32-dimension steps; bf16 row strides of 16 (2m + 1) bytes,
+  // so the 16 rows of a 16-byte read fall on distinct bank groups
+  constexpr int DPS = DP < 32 ? 32 : DP;
+  constexpr int MS = DPS / 32;
+  constexpr int LDKB = DPS + 8;
+  constexpr int LDVB = KB + 8;
+  static_assert(!SPLIT || NSUB % 2 == 0, "split products pair the 16-key subtiles");
+  constexpr int F32_WORDS = KB * LDK + DV * LDVT;
+  constexpr int SPLIT_WORDS = KB * LDKB + DV * LDVB;  // two bf16 planes each
+  constexpr int STAGE_WORDS = SPLIT ? SPLIT_WORDS : F32_WORDS;
+  __shared__ floatx4 stage4[(STAGE_WORDS + 3) / 4];
+  float* const Kst = reinterpret_cast<float*>(stage4);
+  float* const Vt = Kst + KB * LDK;
+  __bf16* const Kh = reinterpret_cast<__bf16*>(stage4);
+  __bf16* const Kl = Kh + KB * LDKB;
+  __bf16* const Vh = Kl + KB * LDKB;
+  __bf16* const Vl = Vh + DV * LDVB;
   __shared__ float Wst[KB];
   __shared__ int Jst[KB];
   __shared__ int Lost[KB], Hist[KB];  // active rows of the staged items (node batches)
@@ -160,7 +188,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
 
   int rbase[RS], myrow[RS], csr[RS], rsr[RS];
   bool rvalid[RS];
-  float qB[RS][DQ];
+  float qB[RS][SPLIT ? 1 : DQ];
+  bf16x8 qh[RS][SPLIT ? MS : 1], ql[RS][SPLIT ? MS : 1];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     rbase[rs] = r0 + (wave * RS + rs) * 16;
@@ -171,13 +200,29 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     rsr[rs] = rsv > INT32_MAX ? INT32_MAX : static_cast<int>(rsv);
     const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.ldqk;
     const float qs = rvalid[rs] ? a.scale : 0.f;  // the logits come out scaled
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int m = 0; m < DQ / 4; ++m) {
-      const int col = DQ * lg + 4 * m;  // columns beyond the row (DP > ldqk) are zero
-      const floatx4 v4 = unit_to_f4<ES>(load_unit<ES>(a.q, qoff + min(col, a.ldqk - 4)), a.dtype,
-                                         col < a.ldqk ? qs : 0.f);
+      for (int m = 0; m < MS; ++m) {
+        float x[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qB[rs][4 * m + e] = v4[e];
+        for (int h = 0; h < 2; ++h) {
+          const int col = 32 * m + 8 * lg + 4 * h;  // columns beyond the row (DPS > ldqk) are zero
+          const floatx4 v4 = unit_to_f4<ES>(load_unit<ES>(a.q, qoff + min(col, a.ldqk - 4)), a.dtype,
+                                             col < a.ldqk ? qs : 0.f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[4 * h + e] = v4[e];
+        }
+        split_bf16(x, qh[rs][m], ql[rs][m]);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < DQ / 4; ++m) {
+        const int col = DQ * lg + 4 * m;  // columns beyond the row (DP > ldqk) are zero
+        const floatx4 v4 = unit_to_f4<ES>(load_unit<ES>(a.q, qoff + min(col, a.ldqk - 4)), a.dtype,
+                                           col < a.ldqk ? qs : 0.f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qB[rs][SPLIT ? 0 : 4 * m + e] = v4[e];
+      }
     }
   }
   const int wrow_lo = r0 + wave * RS * 16, wrow_hi = wrow_lo + RS * 16 - 1;  // this wave's rows
@@ -204,23 +249,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // NODE: coreset items (weight, active rows) instead of the tile's own keys.
   auto process = [&](auto node_tag) {
     constexpr bool NODE = decltype(node_tag)::value;
-    constexpr int QKM = DQ * RS;  // matrix-core ops of one subtile's X
-    auto qk = [&](int kt, floatx4 (&xq)[2][RS]) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int rs = 0; rs < RS; ++rs) xq[h][rs] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int m = 0; m < DQ / 4; ++m) {
-        const floatx4 kv = *reinterpret_cast<const floatx4*>(Kst + (16 * kt + li) * LDK + DQ * lg + 4 * m);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int rs = 0; rs < RS; ++rs) xq[m & 1][rs] = mfma4(kv[e], qB[rs][4 * m + e], xq[m & 1][rs]);
-      }
-    };
-    // weights of subtile kt, elementwise (key 16 kt + 4 lg + r, row myrow[rs])
-    auto weights = [&](int kt, const floatx4 (&xq)[2][RS], floatx4 (&P)[RS]) {
+    // weights of subtile kt from its logits X (key 16 kt + 4 lg + r, row myrow[rs]), elementwise
+    auto weights = [&](int kt, const floatx4 (&X)[RS], floatx4 (&P)[RS]) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int kidx = 16 * kt + 4 * lg + r;
@@ -230,7 +260,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
           const int i = myrow[rs];
-          const float xv = xq[0][rs][r] + xq[1][rs][r];
+          const float xv = X[rs][r];
           const float ex = exp_fast(fminf(xv, xmax));
           const float tp = taylor_fast(xv, tc);
           float p;
@@ -248,33 +278,117 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         }
       }
     };
-    auto pv = [&](int kt, const floatx4 (&P)[RS]) {
+    if constexpr (SPLIT) {
+      // X of subtiles 2 s and 2 s + 1 (2 RS independent chains of 3 MS products)
+      auto qk2 = [&](int sp, floatx4 (&xq)[2][RS]) {
 #pragma unroll
-      for (int ct = 0; ct < DVT; ++ct) {
-        const floatx4 va = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * LDVT + 16 * kt + 4 * lg);
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+          for (int rs = 0; rs < RS; ++rs) xq[h][rs] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma4(va[s], P[rs][s], num[rs][ct]);
-      }
-    };
-    floatx4 xa[2][RS], xb[2][RS];
-    qk(0, xa);
+        for (int m = 0; m < MS; ++m) {
+          bf16x8 kh[2], kl[2];
 #pragma unroll
-    for (int kt = 0; kt < NSUB; ++kt) {
-      floatx4(&xc)[2][RS] = (kt & 1) ? xb : xa;
-      floatx4(&xn)[2][RS] = (kt & 1) ? xa : xb;
-      if (kt + 1 < NSUB) qk(kt + 1, xn);
-      floatx4 P[RS];
-      weights(kt, xc, P);
-      if (kt + 1 < NSUB) {
+          for (int h = 0; h < 2; ++h) {
+            const int off = (16 * (2 * sp + h) + li) * LDKB + 32 * m + 8 * lg;
+            kh[h] = *reinterpret_cast<const bf16x8*>(Kh + off);
+            kl[h] = *reinterpret_cast<const bf16x8*>(Kl + off);
+          }
 #pragma unroll
-        for (int g = 0; g < QKM; ++g) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix-core op of X(kt+1)
-          __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the weights of kt
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kh[h], ql[rs][m], xq[h][rs]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kl[h], qh[rs][m], xq[h][rs]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kh[h], qh[rs][m], xq[h][rs]);
         }
+      };
+      // num^T += V^T P^T over subtiles 2 s, 2 s + 1
+      auto pv2 = [&](int sp, const floatx4 (&P)[2][RS]) {
+        bf16x8 ph[RS], pl[RS];
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) {
+          const float x[8] = {P[0][rs][0], P[0][rs][1], P[0][rs][2], P[0][rs][3],
+                              P[1][rs][0], P[1][rs][1], P[1][rs][2], P[1][rs][3]};
+          split_bf16(x, ph[rs], pl[rs]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < DVT; ++ct) {
+          const int off = (16 * ct + li) * LDVB + 32 * sp + 8 * lg;
+          const bf16x8 vh = *reinterpret_cast<const bf16x8*>(Vh + off);
+          const bf16x8 vl = *reinterpret_cast<const bf16x8*>(Vl + off);
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vh, pl[rs], num[rs][ct]);
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vl, ph[rs], num[rs][ct]);
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vh, ph[rs], num[rs][ct]);
+        }
+      };
+      floatx4 xa[2][RS], xb[2][RS];
+      qk2(0, xa);
+#pragma unroll
+      for (int sp = 0; sp < NSUB / 2; ++sp) {
+        floatx4(&xc)[2][RS] = (sp & 1) ? xb : xa;
+        floatx4(&xn)[2][RS] = (sp & 1) ? xa : xb;
+        if (sp + 1 < NSUB / 2) qk2(sp + 1, xn);
+        floatx4 P[2][RS];
+        weights(2 * sp, xc[0], P[0]);
+        weights(2 * sp + 1, xc[1], P[1]);
+        pv2(sp, P);
       }
-      pv(kt, P);
+    } else {
+      constexpr int QKM = DQ * RS;  // matrix-core ops of one subtile's X
+      auto qk = [&](int kt, floatx4 (&xq)[2][RS]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) xq[h][rs] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < DQ / 4; ++m) {
+          const floatx4 kv = *reinterpret_cast<const floatx4*>(Kst + (16 * kt + li) * LDK + DQ * lg + 4 * m);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs)
+              xq[m & 1][rs] = mfma4(kv[e], qB[rs][SPLIT ? 0 : 4 * m + e], xq[m & 1][rs]);
+        }
+      };
+      auto pv = [&](int kt, const floatx4 (&P)[RS]) {
+#pragma unroll
+        for (int ct = 0; ct < DVT; ++ct) {
+          const floatx4 va = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * LDVT + 16 * kt + 4 * lg);
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma4(va[s], P[rs][s], num[rs][ct]);
+        }
+      };
+      floatx4 xa[2][RS], xb[2][RS];
+      qk(0, xa);
+#pragma unroll
+      for (int kt = 0; kt < NSUB; ++kt) {
+        floatx4(&xc)[2][RS] = (kt & 1) ? xb : xa;
+        floatx4(&xn)[2][RS] = (kt & 1) ? xa : xb;
+        if (kt + 1 < NSUB) qk(kt + 1, xn);
+        floatx4 X[RS], P[RS];
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) X[rs] = xc[0][rs] + xc[1][rs];
+        weights(kt, X, P);
+        if (kt + 1 < NSUB) {
+#pragma unroll
+          for (int g = 0; g < QKM; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix-core op of X(kt+1)
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // then VALU of the weights of kt
+          }
+        }
+        pv(kt, P);
+      }
     }
   };
   using node_batch = std::integral_constant<bool, true>;
@@ -374,6 +488,38 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     }
   };
   auto commit = [&]() {
+    if constexpr (SPLIT) {
+      // bf16 hi / lo planes; keys row-major (dimension 4 u..4 u+3 of key r: 8 bytes per plane), values
+      // transposed with each subtile pair's keys in contraction order (split_key_pos)
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int e = tid + 256 * i;
+        if (e < KB * KU) {
+          const int r = e / KU, u = e - r * KU;
+          const floatx4 f = unit_to_f4<ES>(pk[i], a.dtype, ((pk_ok >> i) & 1u) ? 1.f : 0.f);
+          const uint32_t h0 = pk_bf16(f[0], f[1]), h1 = pk_bf16(f[2], f[3]);
+          const uint32_t l0 = pk_bf16(f[0] - __uint_as_float(h0 << 16), f[1] - __uint_as_float(h0 & 0xffff0000u));
+          const uint32_t l1 = pk_bf16(f[2] - __uint_as_float(h1 << 16), f[3] - __uint_as_float(h1 & 0xffff0000u));
+          *reinterpret_cast<uint2*>(Kh + r * LDKB + 4 * u) = uint2{h0, h1};
+          *reinterpret_cast<uint2*>(Kl + r * LDKB + 4 * u) = uint2{l0, l1};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int e = tid + 256 * i;
+        if (e < KB * VU) {
+          const int r = e % KB, u = e / KB;
+          const floatx4 f = unit_to_f4<ES>(pv[i], a.dtype, ((pv_ok >> i) & 1u) ? 1.f : 0.f);
+          const int pos = split_key_pos(r);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            const __bf16 h = static_cast<__bf16>(f[m]);
+            Vh[(4 * u + m) * LDVB + pos] = h;
+            Vl[(4 * u + m) * LDVB + pos] = static_cast<__bf16>(f[m] - static_cast<float>(h));
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int e = tid + 256 * i;
@@ -393,6 +539,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         for (int m = 0; m < 4; ++m) Vt[(4 * u + m) * LDVT + r] = f[m];
       }
     }
+    }
     if (tid < KB) {
       Jst[tid] = pj;
       Wst[tid] = pw;
@@ -404,6 +551,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // batch b: phase A for b < n_a (offset kstart + b KB), then phase B (offset into the list chunk).  The
   // list is read only by prefetch(); once a batch is committed its items live in Jst/Wst/Lost/Hist, so
   // the list can be refilled right after the commit of its last batch.
+  if constexpr (SPLIT && DPS != DP) {  // dimensions [DP, DPS) of the key planes are never written: zero
+    for (int e = tid; e < KB * LDKB; e += 256) Kh[e] = Kl[e] = static_cast<__bf16>(0.f);
+  }
   if (p_cur < p_end) fill();  // the first list chunk
   __syncthreads();
   bool cur_node = n_a == 0;

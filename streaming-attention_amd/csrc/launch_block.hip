@@ -1,7 +1,8 @@
 // Launch of the residual / combine kernel (block_attn_kernel) for one configuration.  The build compiles
 // this unit once per padded key width DP (16, 32, 64, 128), value-column tile count DVT (1, 2, 4, 8,
 // 16) and element size ES (4: fp32, 2: bf16 / fp16), given as -DSTA_BLOCK_DP=, -DSTA_BLOCK_DVT= and
-// -DSTA_BLOCK_ES=, so the forty instantiations compile in parallel.
+// -DSTA_BLOCK_ES=, so the forty configurations compile in parallel; each object holds the fp32-product
+// and the split-bf16-product kernel of its configuration.
 #include "api_common.hpp"
 #include "block_attn.hip"
 
@@ -15,7 +16,12 @@ template <int DP, int DVT, int ES>
 int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
   const int64_t grid = bh * a.n_tiles;
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  if (a.split)
+    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES, true>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       s, a);
+  else
+    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES, false>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       s, a);
   return check_launch();
 }
 
