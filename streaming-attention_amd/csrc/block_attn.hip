@@ -85,25 +85,23 @@ __device__ __forceinline__ int64_t residual_start(int64_t i, int mode, int block
   return 0;
 }
 
-// Taylor truncation sum_{r<=deg} x^r / r!, deg <= 3, without branches or selects: c1..c3 are 1 for the
-// terms the degree includes, else 0 (uniform).  Degrees <= 2 reproduce the reference's term order and
-// rounding exactly (1 + x, then + x*x/2 with exact division by 2; a zero coefficient adds exactly 0);
-// the cubic term multiplies by 1/3 instead of dividing (within 1 ulp of the division).
-struct TaylorCoef {
-  float c1, c2, c3;
+// The logits come out in base 2: the staged queries carry scale * log2(e), so y = x log2(e) for the
+// natural logit x, exp(x) = exp2(y) on the hardware exp2 (about 1 ulp; the fused residual needs the
+// difference exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding)
+// and the Taylor truncation sum_{r<=deg} x^r / r! (deg <= 3) is the Horner form in y,
+// 1 + y (k1 + y (k2 + y k3)) with k_r = (ln 2)^r / r! for r <= deg and 0 above: three fused
+// multiply-adds for every degree, within a few ulp of the reference's term-by-term sum.
+struct TaylorCoef2 {
+  float k1, k2, k3;
 };
-__host__ __device__ inline TaylorCoef taylor_coef(int deg) {
-  return TaylorCoef{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 1.f : 0.f, deg >= 3 ? 1.f : 0.f};
+__host__ __device__ inline TaylorCoef2 taylor_coef2(int deg) {
+  return TaylorCoef2{deg >= 1 ? 0.693147180560f : 0.f, deg >= 2 ? 0.240226506959f : 0.f,
+                     deg >= 3 ? 0.0555041086648f : 0.f};
 }
-__device__ __forceinline__ float taylor_fast(float x, const TaylorCoef& c) {
-  const float t2 = (x * x) * 0.5f;
-  const float t3 = (t2 * x) * 0.333333343f;
-  return fmaf(t3, c.c3, fmaf(t2, c.c2, fmaf(x, c.c1, 1.0f)));
+__device__ __forceinline__ float taylor2(float y, const TaylorCoef2& c) {
+  return fmaf(y, fmaf(y, fmaf(y, c.k3, c.k2), c.k1), 1.0f);
 }
-
-// exp(x) as 2^(x log2 e) on the hardware exp2 (about 1 ulp; the fused residual needs the difference
-// exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding).
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+constexpr float LOG2E = 1.44269504f;
 
 // Work layout: one workgroup per (head, tile of 64*RS query rows); wave w owns RS strips of 16 rows.
 // Keys are staged in LDS 64 (or 32) at a time: K row-major, V transposed ([column][key]).  For a staged
@@ -199,7 +197,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     const int64_t rsv = residual_start(myrow[rs], a.mode, a.block);
     rsr[rs] = rsv > INT32_MAX ? INT32_MAX : static_cast<int>(rsv);
     const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.ldqk;
-    const float qs = rvalid[rs] ? a.scale : 0.f;  // the logits come out scaled
+    const float qs = rvalid[rs] ? a.scale * LOG2E : 0.f;  // the logits come out scaled, in base 2
     if constexpr (SPLIT) {
 #pragma unroll
       for (int m = 0; m < MS; ++m) {
@@ -236,8 +234,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     for (int ct = 0; ct < DVT; ++ct) num[rs][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const TaylorCoef tc = taylor_coef(a.degree);
-  const float xmax = a.exp_clamp ? 80.f : __builtin_huge_valf();  // exp(min(x, 80)) in the Triton mode
+  const TaylorCoef2 tc = taylor_coef2(a.degree);
+  const float ymax = a.exp_clamp ? 80.f * LOG2E : __builtin_huge_valf();  // exp(min(x, 80)) in the Triton mode
   const int row_lo = r0 > 0 ? r0 : 0;
   const int row_hi = (r0 + TM < n ? r0 + TM : n) - 1;  // inclusive
   if (row_lo > row_hi) return;  // whole tile outside the sequence (uniform)
@@ -260,9 +258,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
 #pragma unroll
         for (int rs = 0; rs < RS; ++rs) {
           const int i = myrow[rs];
-          const float xv = X[rs][r];
-          const float ex = exp_fast(fminf(xv, xmax));
-          const float tp = taylor_fast(xv, tc);
+          const float yv = X[rs][r];
+          const float ex = __builtin_amdgcn_exp2f(fminf(yv, ymax));
+          const float tp = taylor2(yv, tc);
           float p;
           if constexpr (NODE) {
             const bool on = rvalid[rs] && i >= lo && i <= hi;
