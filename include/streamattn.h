@@ -63,18 +63,25 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *   q and k rows are d elements long and v rows ldv (a multiple of 32, >= dv); rows are read in
  *     16-byte units, so d times the element size must be a multiple of 16 (pad rows with zero columns
  *     otherwise: zero dimensions only add zero-valued features), and q, k, v must be 16-byte aligned.
- *   grid: bh * fsplit * ceil(dv/32) workgroups of 256 threads.
+ *   grid: bh * fsplit * ceil(dv/columns) workgroups of 256 threads.
  *   products: STA_PRODUCTS_FP32 (fp32 matrix cores; products of the fp32 features exact) or
  *     STA_PRODUCTS_SPLIT_BF16 (each fp32 operand as bf16 hi + lo, three bf16 matrix-core products per
  *     product: about 2^-16 relative error per product, 16x the fp32 matrix-core rate).  Feature values,
  *     the denominator column and all sums stay fp32 either way.
+ *   columns: value columns per workgroup, 32 (grid bh * fsplit * ceil(dv/32)) or 64
+ *     (sta_moment_columns_ok; grid bh * fsplit).
  *   outputs (fp32, partial over feature splits), in the layout sta_moment_partials_layout gives:
  *     low_num [BH][fsplit][rows][ld], low_den [BH][fsplit][rows], row i stored at row_offset + i.
  */
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
                 int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
-                int products, const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den,
-                void* stream);
+                int products, int columns, const uint32_t* feat_quads, const float* feat_coef, float* low_num,
+                float* low_den, void* stream);
+
+/* 1 when sta_moments runs (d, degree, dv, wave_tiles, products) with columns = 64: one workgroup per
+ * (head, feature split) covering all value columns (split-bf16 products, 32 < dv <= 64, mixed = 0;
+ * one workgroup per compute unit). */
+int sta_moment_columns_ok(int d, int degree, int dv, int wave_tiles, int products);
 
 /* 1 when sta_moments runs (d, degree, wave_tiles) with mixed = 1: the feature splits fs >= fsplit/2
  * (fsplit even) then use wave_tiles - 1 tiles per wave (slot wave_tiles of their waves is padding). */

@@ -26,6 +26,11 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 # bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
 # products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+# Offer the planner the 64-column moment workgroups (split products, 32 < dv <= 64).  Off: on 32 heads x
+# 65536 tokens (d = dv = 64) they take 9.6 ms against 8.4 ms for two 32-column workgroups per compute
+# unit; the feature work they save (17 % of the VALU) is less than one wave per SIMD loses in latency.
+MOMENT_WIDE = False
+
 # The same choice for the residual / combine kernel (sta_block_attention): logits and weighted value sums,
 # when coreset items take part.  Without them (compressor "none", the raw Taylor sums, or sequences no
 # longer than a block) the result is exact attention and keeps fp32 products: the reference holds those
@@ -164,10 +169,12 @@ def prefill(
     # (zero dimensions only add zero-valued features), v to whole 32-column groups
     dm = _unit_width(d, q3.element_size())
     ft = _plan.feature_tiles(dm, degree)
+    k1_products = MOMENT_PRODUCTS if products is None else int(products)
     ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
-                            mixed_nts=_native.moment_mixed_tiles(dm, degree))
+                            mixed_nts=_native.moment_mixed_tiles(dm, degree),
+                            wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
     fsplit = ms.fsplit
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed), dev,
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit), dev,
                              lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
 
     raw = semantics == "taylor"
@@ -220,7 +227,7 @@ def prefill(
         st = lib.sta_moments(
             mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
             float(scale), chunk, shift,
-            fsplit, ms.wave_tiles, int(ms.mixed), MOMENT_PRODUCTS if products is None else int(products),
+            fsplit, ms.wave_tiles, int(ms.mixed), k1_products, ms.columns,
             fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")
 

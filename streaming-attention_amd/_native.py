@@ -43,8 +43,9 @@ _SIGNATURES = {
     "sta_moments": (
         _i32,
         [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _c_p, _c_p, _c_p, _c_p, _c_p],
+         _i32, _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sta_moment_columns_ok": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "sta_moment_mixed_ok": (_i32, [_i32, _i32, _i32]),
     "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),
     "sta_moment_occupancy": (_i32, [_i32, _i32]),
@@ -198,3 +199,9 @@ def limits() -> dict:
     vals = [_i32() for _ in range(4)]
     lib().sta_limits(*[ctypes.byref(x) for x in vals])
     return {"max_d": vals[0].value, "max_dv": vals[1].value, "max_degree": vals[2].value, "max_compress_in": vals[3].value}
+
+
+def moment_wide_tiles(d: int, degree: int, dv: int, products: int) -> tuple:
+    """Per-wave tile counts the 64-column moment kernels run for (d, degree, dv, products)."""
+    lib_ = lib()
+    return tuple(nt for nt in (5,) if lib_.sta_moment_columns_ok(d, degree, dv, nt, products))

@@ -70,6 +70,7 @@ def _factorial_inverse(combo: Tuple[int, ...]) -> float:
 
 MOM_WAVES = 4  # waves per moment workgroup (sta_moments)
 OCC2_SPEEDUP = 1.2  # per-tile throughput of two resident moment workgroups per CU vs one
+WIDE_COST = 1.2  # time per tile of a 64-column workgroup (split products) vs a 32-column one alone
 MOM_MAX_WAVE_TILES = 16  # largest per-wave tile count the kernel is instantiated for
 
 
@@ -189,7 +190,8 @@ def feature_index(d: int, degree: int) -> np.ndarray:
 
 @dataclass(frozen=True)
 class MomentSplit:
-    """Work split of the moment kernel: `fsplit` feature splits x `csplit` 32-column groups per head,
+    """Work split of the moment kernel: `fsplit` feature splits x `csplit` column groups of `columns`
+    (32 or 64) value columns per head,
     4 waves per workgroup, every wave holding exactly `wave_tiles` tiles.  quads/coef are the feature
     table in the kernel's layout [fsplit][4][wave_tiles][4 quads | 16 coefficients]; wave j (= 4 fs + w)
     holds the real tiles [tile_off[j], tile_off[j+1]) followed by padding tiles (coefficient 0)."""
@@ -201,15 +203,20 @@ class MomentSplit:
     quads: np.ndarray  # uint32 [fsplit * 4 * wave_tiles * 4]
     coef: np.ndarray  # float32 [fsplit * 4 * wave_tiles * 16]
     mixed: bool = False  # splits fs >= fsplit / 2 run wave_tiles - 1 tiles per wave
+    columns: int = 32  # value columns per workgroup
 
 
 def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int, int], ...],
-                 compute_units: int = 256, mixed_nts: Tuple[int, ...] = ()) -> MomentSplit:
+                 compute_units: int = 256, mixed_nts: Tuple[int, ...] = (),
+                 wide_nts: Tuple[int, ...] = ()) -> MomentSplit:
     """Choose (fsplit, wave_tiles, mixed) minimising rounds-of-workgroups x tiles-per-wave on a GPU with
     `compute_units` compute units; nt_options lists (per-wave tile count, workgroups resident per
     compute unit) pairs the library supports, mixed_nts the tile counts it also runs mixed (the feature
     splits fs >= fsplit / 2 hold one tile less per wave; every compute unit then pairs a full and a
-    short workgroup).  Ties go to fewer feature splits (fewer partial sums)."""
+    short workgroup), wide_nts the tile counts it runs with 64 value columns per workgroup (one
+    workgroup per compute unit, every feature value generated once for all 64 columns: WIDE_COST per
+    tile against one 32-column tile alone on a compute unit).  Ties go to fewer feature splits (fewer
+    partial sums)."""
 
     def build():
         t = ft.n_tiles
@@ -232,12 +239,18 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
                     continue
                 cost = rounds * (nt - 0.5 if mixed else nt) * occ / speed
                 if best is None or cost < best[0] - 1e-9:
-                    best = (cost, fsplit, nt, mixed)
+                    best = (cost, fsplit, nt, mixed, 32)
+            wide = next((o for o in sorted(wide_nts) if o >= need), None)
+            if wide is not None:
+                cost = -(-(bh * fsplit) // compute_units) * wide * WIDE_COST
+                if best is None or cost < best[0] - 1e-9:
+                    best = (cost, fsplit, wide, False, 64)
             if need == 1:
                 break
         if best is None:
             raise ValueError(f"no supported per-wave tile count for {t} feature tiles (options {opts})")
-        _, fsplit, nt, mixed = best
+        _, fsplit, nt, mixed, columns = best
+        csplit = -(-dv // columns)
         parts = fsplit * MOM_WAVES
         if mixed:
             caps = [nt if j < parts // 2 else nt - 1 for j in range(parts)]
@@ -263,9 +276,10 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
             cnt = sizes[j]
             quads[j, :cnt] = tiles_q[off[j]:off[j] + cnt]
             coef[j, :cnt] = tiles_c[off[j]:off[j] + cnt]
-        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1), mixed)
+        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1), mixed, columns)
 
-    return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units, tuple(mixed_nts)), build)
+    return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units, tuple(mixed_nts),
+                    tuple(wide_nts)), build)
 
 
 def split_state_rows(ft: FeatureTiles, ms: MomentSplit, d: int) -> np.ndarray:

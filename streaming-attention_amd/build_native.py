@@ -2,8 +2,8 @@
 
     python streaming-attention_amd/build_native.py
 
-The library is 84 objects compiled in parallel and linked into one shared object: api.hip (entry
-points, compressor and decode kernels), launch_moments.hip (fp32 and split-bf16 products),
+The library is 85 objects compiled in parallel and linked into one shared object: api.hip (entry
+points, compressor and decode kernels), launch_moments.hip (fp32 and split-bf16 products, 32 or 64 columns),
 launch_accumulate.hip, and
 launch_block.hip and launch_flash.hip once per residual / flash kernel configuration (padded key
 width, value-column tiles, element size).  Objects go to streaming-attention_amd/_build/.
@@ -26,6 +26,7 @@ CSRC = HERE / "csrc"
 # (source, object stem, defines), slowest first
 UNITS = (
     ("launch_moments.hip", "launch_moments_split", ("-DSTA_MOM_SPLIT=1",)),
+    ("launch_moments.hip", "launch_moments_split64", ("-DSTA_MOM_SPLIT=1", "-DSTA_MOM_CG=64")),
     ("launch_moments.hip", "launch_moments", ("-DSTA_MOM_SPLIT=0",)),
     ("launch_accumulate.hip", "launch_accumulate", ()),
 ) + tuple(("launch_block.hip", f"launch_block_{dp}_{dvt}_{es}",

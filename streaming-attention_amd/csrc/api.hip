@@ -123,14 +123,18 @@ int sta_moment_mixed_ok(int d, int degree, int wave_tiles) {
              : 0;
 }
 
+int sta_moment_columns_ok(int d, int degree, int dv, int wave_tiles, int products) {
+  return moment_columns64_ok(d, degree, dv, wave_tiles, products) ? 1 : 0;
+}
+
 int sta_moment_occupancy(int d, int wave_tiles) {
   return (wave_tiles > 0 && d > 0) ? sta::mom_wg_per_cu(wave_tiles, d > 64) : 0;
 }
 
 int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
                 int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
-                int products, const uint32_t* feat_quads, const float* feat_coef, float* low_num, float* low_den,
-                void* stream) {
+                int products, int columns, const uint32_t* feat_quads, const float* feat_coef, float* low_num,
+                float* low_den, void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0) return STA_ERR_SHAPE;
@@ -139,6 +143,8 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
   if (mixed != 0 && (mixed != 1 || fsplit % 2 != 0 || !sta_moment_mixed_ok(d, degree, wave_tiles))) return STA_ERR_ARG;
   if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
+  if (columns != 32 && (columns != 64 || mixed != 0 || !moment_columns64_ok(d, degree, dv, wave_tiles, products)))
+    return STA_ERR_ARG;
   // rows are read in 16-byte units: d must be a whole number of units, v rows whole 32-column groups,
   // every base 16-byte aligned, and a head's rows addressable with 32-bit byte offsets
   const int esize = dtype == STA_F32 ? 4 : 2;
@@ -149,11 +155,13 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
     return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
-  a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
-  a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
-  return products == STA_PRODUCTS_SPLIT_BF16
-             ? dispatch_moments<true>(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3)
-             : dispatch_moments<false>(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
+  a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + columns - 1) / columns; a.quads = feat_quads;
+  a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
+  a.ldo = 32 * ((dv + 31) / 32);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (columns == 64) return dispatch_moments<true, 64>(a, bh, s, wave_tiles, degree >= 3);
+  return products == STA_PRODUCTS_SPLIT_BF16 ? dispatch_moments<true, 32>(a, bh, s, wave_tiles, degree >= 3)
+                                             : dispatch_moments<false, 32>(a, bh, s, wave_tiles, degree >= 3);
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,

@@ -49,11 +49,20 @@ constexpr int kNtBigD3[] = {4, 16};
   X(4, true, false) X(8, true, false) X(16, true, false) X(5, false, true) X(16, false, true)       \
   X(4, true, true) X(16, true, true)
 
+// X(NT, DEG3, DBIG) of the 64-column (split-product) moment kernels.
+#define STA_MOMENT_CONFIGS_64(X) X(5, false, false)
+
 template <size_t L>
 int next_nt(const int (&tab)[L], int want) {
   for (size_t i = 0; i < L; ++i)
     if (tab[i] >= want) return tab[i];
   return -1;
+}
+
+// 64 value columns per workgroup: split products, a configuration in STA_MOMENT_CONFIGS_64, and
+// 32 < dv <= 64 (so the workgroup's columns are the whole row of the partials).
+inline bool moment_columns64_ok(int d, int degree, int dv, int wave_tiles, int products) {
+  return products == STA_PRODUCTS_SPLIT_BF16 && d <= 64 && degree <= 2 && dv > 32 && dv <= 64 && wave_tiles == 5;
 }
 
 inline int moment_wave_tiles(int d, int degree, int want) {
@@ -63,9 +72,10 @@ inline int moment_wave_tiles(int d, int degree, int want) {
   return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
 }
 
-// launch_moments.hip, one object per SPLIT: the prefill moment scan (moments_kernel) for wave-tile count
-// nt, with fp32 (SPLIT false) or split-bf16 (SPLIT true) matrix-core products.
-template <bool SPLIT>
+// launch_moments.hip, one object per (SPLIT, CG): the prefill moment scan (moments_kernel) for wave-tile
+// count nt, with fp32 (SPLIT false) or split-bf16 (SPLIT true) matrix-core products and CG value columns
+// per workgroup (64: split products, STA_MOMENT_CONFIGS_64 only).
+template <bool SPLIT, int CG>
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
 int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);

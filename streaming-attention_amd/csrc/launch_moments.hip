@@ -1,21 +1,25 @@
 // Launches of the prefill moment scan (moments_kernel), one instantiation per wave-tile count, degree-3
 // flag, d > 64 flag and element size (4: fp32, 2: bf16 / fp16, so the chunk staging is straight-line).
-// The build compiles this unit twice, with -DSTA_MOM_SPLIT=0 (fp32 matrix-core products) and
-// -DSTA_MOM_SPLIT=1 (split-bf16 products).
+// The build compiles this unit three times: -DSTA_MOM_SPLIT=0 (fp32 matrix-core products),
+// -DSTA_MOM_SPLIT=1 (split-bf16 products) and -DSTA_MOM_SPLIT=1 -DSTA_MOM_CG=64 (split-bf16 products,
+// 64 value columns per workgroup, for the configurations in STA_MOMENT_CONFIGS_64).
 #include "api_common.hpp"
 #include "moments.hip"
 
 #if !defined(STA_MOM_SPLIT)
 #error "launch_moments.hip is compiled with -DSTA_MOM_SPLIT=<0|1>"
 #endif
+#if !defined(STA_MOM_CG)
+#define STA_MOM_CG 32
+#endif
 
 namespace sta_api {
 namespace {
 
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT>
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
 int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
-  const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT>;
+  const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT, CG)) * sizeof(float);
+  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT, CG>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -27,17 +31,21 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
 
 }  // namespace
 
-template <bool SPLIT>
+template <bool SPLIT, int CG>
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
   const bool big = a.d > 64;
 #define STA_CASE(NT, D3, BIG)                                                                       \
   if (nt == NT && deg3 == D3 && big == BIG)                                                         \
-    return a.esize == 4 ? launch<NT, D3, BIG, 4, SPLIT>(a, bh, s) : launch<NT, D3, BIG, 2, SPLIT>(a, bh, s);
+    return a.esize == 4 ? launch<NT, D3, BIG, 4, SPLIT, CG>(a, bh, s) : launch<NT, D3, BIG, 2, SPLIT, CG>(a, bh, s);
+#if STA_MOM_CG == 64
+  STA_MOMENT_CONFIGS_64(STA_CASE)
+#else
   STA_MOMENT_CONFIGS(STA_CASE)
+#endif
 #undef STA_CASE
   return STA_ERR_UNSUPPORTED;
 }
 
-template int dispatch_moments<STA_MOM_SPLIT != 0>(const sta::MomArgs&, int64_t, hipStream_t, int, bool);
+template int dispatch_moments<STA_MOM_SPLIT != 0, STA_MOM_CG>(const sta::MomArgs&, int64_t, hipStream_t, int, bool);
 
 }  // namespace sta_api

@@ -94,16 +94,20 @@ struct MomArgs {
 
 __host__ __device__ constexpr int mom_ldq(bool dbig) { return dbig ? 132 : 68; }
 __host__ __device__ constexpr int mom_krows(bool dbig) { return dbig ? 132 : 68; }
-__host__ __device__ constexpr int mom_buf_floats(bool dbig) {
-  return MOM_C * mom_ldq(dbig) + mom_krows(dbig) * MOM_LDT + 32 * MOM_LDT;
+// cg: value columns per workgroup (32, or 64 for the 64-column kernels)
+__host__ __device__ constexpr int mom_buf_floats(bool dbig, int cg = 32) {
+  return MOM_C * mom_ldq(dbig) + mom_krows(dbig) * MOM_LDT + cg * MOM_LDT;
 }
-__host__ __device__ constexpr int mom_red_floats() { return MOM_WAVES * 33 * MOM_LDR; }
+__host__ __device__ constexpr int mom_red_floats(int cg = 32) { return MOM_WAVES * (cg + 1) * MOM_LDR; }
 // Shared-memory floats of a launch (must match the carve-up in moments_kernel).
-__host__ __device__ constexpr int mom_smem_floats(bool dbig, int nt) {
-  return 2 * mom_buf_floats(dbig) + 2 * mom_red_floats() + MOM_WAVES * nt * 16 + 8;
+__host__ __device__ constexpr int mom_smem_floats(bool dbig, int nt, int cg = 32) {
+  return 2 * mom_buf_floats(dbig, cg) + 2 * mom_red_floats(cg) + MOM_WAVES * nt * 16 + 8;
 }
-// Workgroups per compute unit an instantiation is built for (registers <= 256 and LDS <= 80 KiB for 2).
-__host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig) { return (nt <= 5 && !dbig) ? 2 : 1; }
+// Workgroups per compute unit an instantiation is built for (registers <= 256 and LDS <= 80 KiB for 2;
+// the 64-column kernels need 124 KiB of LDS).
+__host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig, int cg = 32) {
+  return (nt <= 5 && !dbig && cg == 32) ? 2 : 1;
+}
 
 // Chunk staging in registers: 16-byte units (4 fp32 or 8 bf16/fp16 elements).  The host guarantees
 // ldq == d with d a multiple of the unit and ldv a multiple of 32, so units never straddle the constant
@@ -111,36 +115,38 @@ __host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig) { return (nt 
 // row changes.  Loads are unconditional (rows clamped into the sequence), so none of them waits on
 // another; rows outside the sequence are zeroed when the units are written to LDS, and unused slots
 // write to a dummy LDS slot, so the staging has no branches.
-template <bool DBIG>
+template <bool DBIG, int CG>
 struct MomStage {
   static constexpr int QV = MOM_C * (DBIG ? 128 : 64) * 4 / 16 / MOM_THREADS;  // 2 or 4 (fp32 rows)
+  static constexpr int VV = MOM_C * CG * 4 / 16 / MOM_THREADS;                 // 1 or 2 (fp32 rows)
   uint4 q[QV];
   uint4 k[QV];
-  uint4 v;
+  uint4 v[VV];
 };
 
-template <bool DBIG>
+template <bool DBIG, int CG>
 struct MomSlots {
-  static constexpr int QV = MomStage<DBIG>::QV;
+  static constexpr int QV = MomStage<DBIG, CG>::QV;
+  static constexpr int VV = MomStage<DBIG, CG>::VV;
   int q_tok[QV];    // token of q slot j (row-major slots; clamped to the chunk)
   uint32_t q_off[QV];  // byte offset of the unit within its row
   int q_lds[QV];    // float offset of the unit in Qs, or the dummy slot
   bool q_use[QV];
   uint32_t k_off[QV];  // token = tid & 31 (token-fast slots)
   int k_dim[QV];    // first dimension of the unit, or -1 when unused
-  uint32_t v_off;   // byte offset of the unit within its v row
-  int v_col;        // first column (within the group of 32) of the unit, or -1 when unused
+  uint32_t v_off[VV];  // byte offset of the unit within its v row
+  int v_col[VV];       // first column (within the workgroup's CG) of the unit, or -1 when unused
 };
 
-template <bool DBIG, int ES>
-__device__ __forceinline__ MomSlots<DBIG> mom_slots(const MomArgs& a, int col0, int dummy) {
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ MomSlots<DBIG, CG> mom_slots(const MomArgs& a, int col0, int dummy) {
   constexpr int LDQ = mom_ldq(DBIG);
-  MomSlots<DBIG> sl;
+  MomSlots<DBIG, CG> sl;
   const int tid = threadIdx.x;
   constexpr int epu = 16 / ES;
   const int uq = a.d / epu;  // units per q/k row
 #pragma unroll
-  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+  for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
     const int e = tid + MOM_THREADS * j;
     const int t = e / uq, u = e - t * uq;
     sl.q_use[j] = t < MOM_C;
@@ -151,27 +157,32 @@ __device__ __forceinline__ MomSlots<DBIG> mom_slots(const MomArgs& a, int col0, 
     sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
     sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
-  const int uv = tid >> 5;  // unit of the workgroup's 32 columns
-  sl.v_off = static_cast<uint32_t>((col0 + min(uv * epu, 32 - epu)) * ES);
-  sl.v_col = uv * epu < 32 ? uv * epu : -1;
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG, CG>::VV; ++j) {
+    const int uv = (tid >> 5) + (MOM_THREADS / 32) * j;  // unit of the workgroup's CG columns
+    sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
+    sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
+  }
   return sl;
 }
 
 __device__ __forceinline__ int clamp_row(int row, int n) { return min(max(row, 0), n - 1); }
 
-template <bool DBIG, int ES>
-__device__ __forceinline__ void mom_load(MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ void mom_load(MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                          const char* qh, const char* kh, const char* vh, int row0) {
   const uint32_t qrow = static_cast<uint32_t>(a.d * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
   const int ktok = row0 + (threadIdx.x & (MOM_C - 1));
   const uint32_t krow = static_cast<uint32_t>(clamp_row(ktok, a.n));
 #pragma unroll
-  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+  for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
     const uint32_t r = static_cast<uint32_t>(clamp_row(row0 + sl.q_tok[j], a.n));
     st.q[j] = *reinterpret_cast<const uint4*>(qh + r * qrow + sl.q_off[j]);
     st.k[j] = *reinterpret_cast<const uint4*>(kh + krow * qrow + sl.k_off[j]);
   }
-  st.v = *reinterpret_cast<const uint4*>(vh + krow * vrow + sl.v_off);
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG, CG>::VV; ++j)
+    st.v[j] = *reinterpret_cast<const uint4*>(vh + krow * vrow + sl.v_off[j]);
 }
 
 // The 16-byte unit u as 4 (fp32, ES = 4) or 8 (bf16 / fp16, ES = 2) floats; only f[0..16/ES) are
@@ -202,8 +213,8 @@ __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f
   }
 }
 
-template <bool DBIG, int ES>
-__device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlots<DBIG>& sl, const MomArgs& a,
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                           float* buf, int dummy_rel, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
   float* Qs = buf;
@@ -216,7 +227,7 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
   const float kok = tok_ok ? 1.f : 0.f;
   constexpr bool wide = ES == 2;  // 8 elements per unit
 #pragma unroll
-  for (int j = 0; j < MomStage<DBIG>::QV; ++j) {
+  for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
     const int row = row0 + sl.q_tok[j];
     const float sc = (sl.q_use[j] && row >= 0 && row < a.n) ? a.scale : 0.f;
     float f[8];
@@ -234,13 +245,14 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
       }
     }
   }
-  {
+#pragma unroll
+  for (int j = 0; j < MomStage<DBIG, CG>::VV; ++j) {
     float f[8];
-    unit_floats<ES>(st.v, a.dtype, f);
+    unit_floats<ES>(st.v[j], a.dtype, f);
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       if (m < 4 || wide) {
-        float* p = sl.v_col >= 0 ? Vt + (sl.v_col + m) * MOM_LDT + tok : dmy + m;
+        float* p = sl.v_col[j] >= 0 ? Vt + (sl.v_col[j] + m) * MOM_LDT + tok : dmy + m;
         *p = f[m] * kok;
       }
     }
@@ -253,24 +265,30 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG>& st, const MomSlo
 }
 
 // Fixed-order sum of the 4 waves' partials of the chunk starting at row0, stored unconditionally:
-// low_num rows of the workgroup's 32 columns and, for the workgroup that keeps the denominator column
-// (DEN), the low_den rows.
-template <bool DEN>
+// low_num rows of the workgroup's CG columns and, for the workgroup that keeps the denominator column
+// (DEN), the low_den rows.  A wave's partials are CG + 1 columns of MOM_LDR tokens (column CG: the
+// denominator).
+template <bool DEN, int CG>
 __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
                                                  int col0) {
+  constexpr int WS = (CG + 1) * MOM_LDR;  // one wave's partials
   const int tid = threadIdx.x;
-  const int col = tid & 31, t4 = 4 * (tid >> 5);  // 8 groups of 4 tokens
-  floatx4 acc = *reinterpret_cast<const floatx4*>(red + red_off(col, t4));
+  const int t4 = 4 * (tid >> 5);  // 8 groups of 4 tokens
 #pragma unroll
-  for (int ww = 1; ww < MOM_WAVES; ++ww) acc += *reinterpret_cast<const floatx4*>(red + ww * 33 * MOM_LDR + red_off(col, t4));
-  float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
+  for (int h = 0; h < CG / 32; ++h) {
+    const int col = (tid & 31) + 32 * h;
+    floatx4 acc = *reinterpret_cast<const floatx4*>(red + red_off(col, t4));
 #pragma unroll
-  for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
+    for (int ww = 1; ww < MOM_WAVES; ++ww) acc += *reinterpret_cast<const floatx4*>(red + ww * WS + red_off(col, t4));
+    float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
+  }
   if constexpr (DEN) {
     const int tok = tid & (MOM_C - 1);
-    float den = red[red_off(32, tok)];
+    float den = red[red_off(CG, tok)];
 #pragma unroll
-    for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[ww * 33 * MOM_LDR + red_off(32, tok)];
+    for (int ww = 1; ww < MOM_WAVES; ++ww) den += red[ww * WS + red_off(CG, tok)];
     a.low_den[obase + row0 + tok] = den;
   }
 }
@@ -307,10 +325,9 @@ __device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t 
 // its 32 columns, den_s[f] += phi_k(tok)[f].  Token steps outermost over all tiles (2 NT independent
 // chains), in two halves of 4 steps; the keys of the second half are read while the first half's
 // MFMAs issue.  `mid()` runs after the first key reads are issued (work to hide under them).
-template <int NT, bool DEG3, bool DEN, class Mid>
-__device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, const float* Kt, const float* Vt,
+template <int NT, int CT, bool DEG3, bool DEN, class Mid>
+__device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, const float* Kt, const float* Vt,
                                            const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
-  constexpr int CT = 2;
   floatx4 vv[2][CT];  // values of tokens 8 lg + 0..3 and 8 lg + 4..7
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -369,10 +386,10 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][2], float* den_s, c
 // A values of its 8 steps); B: V[8 lg + j][col].  The feature values and the values are split into
 // bf16 hi + lo, and S += A_hi B_lo + A_lo B_hi + A_hi B_hi (terms outermost, so the 2 NT accumulators
 // are independent chains).  The denominator sums the fp32 feature values as before.
-template <int NT, bool DEG3, bool DEN, class Mid>
-__device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][2], float* den_s, const float* Kt, const float* Vt,
-                                                 const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
-  constexpr int CT = 2;
+template <int NT, int CT, bool DEG3, bool DEN, class Mid>
+__device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* den_s, const float* Kt,
+                                                 const float* Vt, const MomLane<NT, DEG3>& m, int li, int lg,
+                                                 Mid mid) {
   floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -392,7 +409,8 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][2], float* de
   }
   mid();
   __builtin_amdgcn_sched_barrier(0);
-  bf16x8 ah[NT], al[NT];
+  // tile kt's products are issued as soon as its operands are split, so the next tile's VALU work runs
+  // while the matrix cores work through them
 #pragma unroll
   for (int kt = 0; kt < NT; ++kt) {
     float x[8];
@@ -405,25 +423,20 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][2], float* de
       x[j] = y;
       if constexpr (DEN) dacc += y;
     }
-    split_bf16(x, ah[kt], al[kt]);
+    bf16x8 ah, al;
+    split_bf16(x, ah, al);
     if constexpr (DEN) {
       dacc += __shfl_xor(dacc, 16);
       dacc += __shfl_xor(dacc, 32);
       if (lg == 0) den_s[16 * kt + li] += dacc;
     }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vl[ct], st[kt][ct]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(al, vh[ct], st[kt][ct]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vh[ct], st[kt][ct]);
   }
-#pragma unroll
-  for (int kt = 0; kt < NT; ++kt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah[kt], vl[ct], st[kt][ct]);
-#pragma unroll
-  for (int kt = 0; kt < NT; ++kt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(al[kt], vh[ct], st[kt][ct]);
-#pragma unroll
-  for (int kt = 0; kt < NT; ++kt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah[kt], vh[ct], st[kt][ct]);
 }
 
 // Split-bf16 form of the query: out[tok][col] += sum_f phi_q(tok)[f] S[f][col] over the wave's tiles,
@@ -433,11 +446,11 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][2], float* de
 // state is used in place, split into bf16 hi + lo once per chunk.  An odd last tile pairs with zeros.
 // o[tt][ct] accumulates rows 16 tt + 4 lg + r, column 16 ct + li; dq the denominator (fp32 VALU, the
 // fp32 path's order).
-template <int NT, bool DEG3, bool DEN, int LDQ>
-__device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][2], float (&dq)[2], const floatx4 (&st)[NT][2],
+template <int NT, int CT, bool DEG3, bool DEN, int LDQ>
+__device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&dq)[2], const floatx4 (&st)[NT][CT],
                                                 const float* Qs, const float* den_s, const MomLane<NT, DEG3>& m,
                                                 int li, int lg) {
-  constexpr int CT = 2, TT = 2;
+  constexpr int TT = 2;
   constexpr int NP = (NT + 1) / 2;
   const float* qrow = Qs + li * LDQ;
 #pragma unroll
@@ -514,20 +527,21 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][2], float (&d
 // The kernel body for one workgroup (head bh, feature split fs, column group cs) with NT tiles per wave
 // out of the NTS the split table holds per wave.  DEN: this workgroup also keeps the denominator column
 // (only column group 0 does; the others would compute bit-identical values).
-template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT>
+template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT, int CG>
 __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
-  constexpr int BUF = mom_buf_floats(DBIG);
-  constexpr int CT = 2;           // 16-column tiles per wave
+  constexpr int BUF = mom_buf_floats(DBIG, CG);
+  constexpr int RED = mom_red_floats(CG);
+  constexpr int CT = CG / 16;     // 16-column tiles per wave
   constexpr int TT = MOM_C / 16;  // 16-token tiles per chunk (query)
   constexpr int KS = MOM_C / 4;   // update steps per chunk (token 8 lg + ks)
   static_assert(KS == 8, "update token mapping assumes 32-token chunks");
   extern __shared__ float smem[];
   float* red_all = smem + 2 * BUF;
-  float* den_all = red_all + 2 * mom_red_floats();  // [4 waves][NT * 16]
-  const int dummy_abs = 2 * BUF + 2 * mom_red_floats() + MOM_WAVES * NT * 16;  // 8 floats, write-only
+  float* den_all = red_all + 2 * RED;  // [4 waves][NT * 16]
+  const int dummy_abs = 2 * BUF + 2 * RED + MOM_WAVES * NT * 16;  // 8 floats, write-only
 
-  const int col0 = 32 * cs;
+  const int col0 = CG * cs;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -551,15 +565,15 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
   const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
-  const MomSlots<DBIG> sl = mom_slots<DBIG, ES>(a, col0, dummy_abs);
+  const MomSlots<DBIG, CG> sl = mom_slots<DBIG, ES, CG>(a, col0, dummy_abs);
 
   // zero both chunk buffers (their padding rows / columns are never written again) and the denominators
   for (int e = tid; e < 2 * BUF; e += MOM_THREADS) smem[e] = 0.f;
   for (int e = tid; e < MOM_WAVES * NT * 16; e += MOM_THREADS) den_all[e] = 0.f;
   __syncthreads();
-  MomStage<DBIG> pre;
-  mom_load<DBIG, ES>(pre, sl, a, qh, kh, vh, first);
-  mom_store<DBIG, ES>(pre, sl, a, smem, dummy_abs, first);
+  MomStage<DBIG, CG> pre;
+  mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first);
+  mom_store<DBIG, ES, CG>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
@@ -570,7 +584,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
 
     // prefetch chunk c+1 (unconditional, clamped); staged after the query phase
-    mom_load<DBIG, ES>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
+    mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
 
     // ---- query with the state of all previous chunks: two accumulator sets (tile parity), so 8
     //      independent MFMA chains; tile kt+1's operands are read during tile kt ----
@@ -583,7 +597,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
       for (int ct = 0; ct < CT; ++ct) o[0][tt][ct] = o[1][tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     if constexpr (SPLIT) {
-      mom_query_split<NT, DEG3, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
+      mom_query_split<NT, CT, DEG3, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
     } else {
       float x0[2][TT], x2[2][TT];
       floatx4 x1[2][TT], dn[2];
@@ -623,7 +637,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
 
     // ---- this wave's query partials -> red[cur] (column-major, 4 tokens per 16-byte write) ----
     {
-      float* rw = red_all + cur * mom_red_floats() + w * 33 * MOM_LDR;
+      float* rw = red_all + cur * RED + w * (CG + 1) * MOM_LDR;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
@@ -633,27 +647,27 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
           float s = dq[tt];
           s += __shfl_xor(s, 16);
           s += __shfl_xor(s, 32);
-          if (lg == 0) rw[red_off(32, 16 * tt + li)] = s;
+          if (lg == 0) rw[red_off(CG, 16 * tt + li)] = s;
         }
       }
     }
     // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
-    if (c + 1 < nchunks) mom_store<DBIG, ES>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
+    if (c + 1 < nchunks)
+      mom_store<DBIG, ES, CG>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
     //      key reads ----
     auto mid = [&]() {
-      if (c > 0) mom_reduce_store<DEN>(a, red_all + (cur ^ 1) * mom_red_floats(), obase, row0 - MOM_C, col0);
+      if (c > 0) mom_reduce_store<DEN, CG>(a, red_all + (cur ^ 1) * RED, obase, row0 - MOM_C, col0);
     };
     if constexpr (SPLIT)
-      mom_update_split<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
+      mom_update_split<NT, CT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
     else
-      mom_update<NT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
+      mom_update<NT, CT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
     __syncthreads();
   }
-  mom_reduce_store<DEN>(a, red_all + ((nchunks - 1) & 1) * mom_red_floats(), obase, first + (nchunks - 1) * MOM_C,
-                        col0);
+  mom_reduce_store<DEN, CG>(a, red_all + ((nchunks - 1) & 1) * RED, obase, first + (nchunks - 1) * MOM_C, col0);
 }
 
 // Workgroup -> (head, feature split, column group).  Workgroups are dispatched round-robin over the 8
@@ -688,23 +702,26 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
 // NT - 1 tiles per wave (their table slot NT is padding), so the tiles need fsplit * 4 * (NT - 1/2)
 // slots instead of fsplit * 4 * NT, and every compute unit holds one full and one short workgroup.
 // SPLIT: split-bf16 matrix-core products (mom_query_split / mom_update_split) instead of fp32 ones.
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT>
-__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG)) void moments_kernel(const MomArgs a) {
+// CG: value columns per workgroup, 32 or 64.  With 64 the feature values of a token are generated and
+// split once for 4 column tiles instead of twice for 2 (the 32-column workgroups of a head each do
+// their own), at one workgroup per compute unit (124 KiB of LDS).
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
+__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
   mom_workgroup(a, bh, fs, cs);
-  constexpr bool MIX = (NT == 4 || NT == 5) && !DBIG;
+  constexpr bool MIX = (NT == 4 || NT == 5) && !DBIG && CG == 32;
   if (MIX && a.mixed && fs >= a.fsplit / 2) {
     constexpr int NTL = MIX ? NT - 1 : NT;
     if (cs == 0)
-      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT, CG>(a, bh, fs, cs);
     else
-      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT, CG>(a, bh, fs, cs);
   } else {
     if (cs == 0)
-      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT, CG>(a, bh, fs, cs);
     else
-      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT, CG>(a, bh, fs, cs);
   }
 }
 
@@ -766,18 +783,18 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
 
   const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.d * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * ES;
-  const MomSlots<DBIG> sl = mom_slots<DBIG, ES>(a, col0, dummy_abs);
+  const MomSlots<DBIG, 32> sl = mom_slots<DBIG, ES, 32>(a, col0, dummy_abs);
   const int nchunks = static_cast<int>((a.n + MOM_C - 1) / MOM_C);
   for (int e = tid; e < BUF; e += MOM_THREADS) smem[e] = 0.f;  // padding rows / columns stay 0
   for (int c = 0; c < nchunks; ++c) {
-    MomStage<DBIG> stg;
-    mom_load<DBIG, ES>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
+    MomStage<DBIG, 32> stg;
+    mom_load<DBIG, ES, 32>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
     __syncthreads();  // the previous chunk's update is done with the buffer
-    mom_store<DBIG, ES>(stg, sl, a, smem, dummy_abs, c * MOM_C);
+    mom_store<DBIG, ES, 32>(stg, sl, a, smem, dummy_abs, c * MOM_C);
     __syncthreads();
     const float* Kt = smem + MOM_C * mom_ldq(DBIG);
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
-    mom_update<NT, DEG3, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
+    mom_update<NT, CT, DEG3, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
   }
 
   // ---- write the slice back (the denominators once per feature split) ----

@@ -72,6 +72,27 @@ def test_low_degree_sums(degree, d, dv, n, products, tol):
     assert rel(res.den[0], den) < tol
 
 
+@pytest.mark.parametrize("dv,dtype", [(64, torch.float32), (40, torch.float32), (64, torch.bfloat16)])
+def test_low_degree_sums_64_column_workgroups(monkeypatch, dv, dtype):
+    """The 64-column moment kernel (split products; the planner picks it when the heads fill the GPU):
+    forced here by offering the planner only 5 tiles per wave."""
+    monkeypatch.setattr(_native, "moment_wave_tile_options", lambda d, degree: ((5, 2),))
+    monkeypatch.setattr(_native, "moment_mixed_tiles", lambda d, degree: ())
+    ft = _plan.feature_tiles(64, 2)
+    ms = _plan.moment_split(ft, 3, dv, ((5, 2),), wide_nts=_native.moment_wide_tiles(64, 2, dv, 1))
+    assert ms.columns == 64 and ms.csplit == 1
+    g = torch.Generator().manual_seed(dv)
+    q = (torch.randn(3, 1000, 64, generator=g) * 0.15).to(dtype)
+    k = (torch.randn(3, 1000, 64, generator=g) * 0.15).to(dtype)
+    v = torch.randn(3, 1000, dv, generator=g).to(dtype)
+    res = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block=1, scale=0.9, semantics="taylor",
+                          products=_native.PRODUCTS_SPLIT_BF16, residual_products=_native.PRODUCTS_SPLIT_BF16)
+    for h in range(3):
+        num, den = orc.low_sums_direct(q[h].float(), k[h].float(), v[h].float(), 2, 0.9)
+        assert rel(res.out[h], num) < 2e-5
+        assert rel(res.den[h], den) < 2e-5
+
+
 def test_low_degree_api_matches_reference(golden):
     g = golden("flat_c1")
     q, k, v = (t(g[x]).to(DEV) for x in "qkv")

@@ -43,10 +43,16 @@ def test_library_exports_header_symbols():
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, 0, None, None, None, None,
-                           None) == _native.STA_ERR_ARG
-    assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, 64, 2, 1.0, 32, 0, 8, 5, 0, 2, 16, 16, 16, 16,
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, 0, 32, None, None, None,
+                           None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, 64, 2, 1.0, 32, 0, 8, 5, 0, 2, 32, 16, 16, 16, 16,
                            None) == _native.STA_ERR_ARG  # unknown products mode
+    for mixed, products, columns, dv in [(1, 1, 64, 64), (0, 0, 64, 64), (0, 1, 64, 32), (0, 1, 48, 64)]:
+        assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, dv, 64, 2, 1.0, 32, 0, 8, 5, mixed, products, columns, 16,
+                               16, 16, 16, None) == _native.STA_ERR_ARG  # 64 columns: split, unmixed, 32 < dv <= 64
+    assert lib.sta_moment_columns_ok(64, 2, 64, 5, 1) == 1
+    assert lib.sta_moment_columns_ok(64, 2, 64, 5, 0) == 0 and lib.sta_moment_columns_ok(64, 3, 64, 5, 1) == 0
+    assert lib.sta_moment_columns_ok(64, 2, 32, 5, 1) == 0 and lib.sta_moment_columns_ok(64, 2, 64, 4, 1) == 0
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
     # flash: null pointers, D beyond the limit, strides not whole 4-element units, misaligned rows
@@ -190,6 +196,10 @@ def test_moment_split_balances_waves():
     assert np.all(c[half:, ms.wave_tiles - 1] == 0)
     got = sorted(tuple(q[j, i]) for j in range(4 * ms.fsplit) for i in range(sizes[j]))
     assert got == sorted(tuple(x) for x in ft.quads.reshape(-1, 4))
+    # 64-column workgroups (split products): one per compute unit, 8 feature splits of 5 tiles per wave
+    ms = _plan.moment_split(ft, 32, 64, ((2, 2), (4, 2), (5, 2), (9, 1), (16, 1)), mixed_nts=(4, 5), wide_nts=(5,))
+    assert (ms.fsplit, ms.csplit, ms.wave_tiles, ms.mixed, ms.columns) == (8, 1, 5, False, 64)
+    assert np.diff(ms.tile_off).sum() == 141 and np.diff(ms.tile_off).max() <= 5
 
 
 def test_library_moment_tile_options():
