@@ -26,6 +26,22 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 # bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
 # products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+# Run the level / block compressor on a second stream, overlapping the moment scan's tail.
+OVERLAP_COMPRESS = True
+
+_side_streams: Dict[str, "torch.cuda.Stream"] = {}
+
+
+def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
+    key = str(dev)
+    with _dev_lock:
+        st = _side_streams.get(key)
+        if st is None:
+            st = torch.cuda.Stream(device=dev)  # default priority
+            _side_streams[key] = st
+    return st
+
+
 # Offer the planner the 64-column moment workgroups (split products, 32 < dv <= 64).  Off: on 32 heads x
 # 65536 tokens (d = dv = 64) they take 9.6 ms against 8.4 ms for two 32-column workgroups per compute
 # unit; the feature work they save (17 % of the VALU) is less than one wave per SIMD loses in latency.
@@ -231,6 +247,14 @@ def prefill(
             fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
         _native.check(st, "sta_moments")
 
+    # The compressor needs only the keys and the draws: on a second stream (default priority), released
+    # before the moment scan is queued, it runs in the compute units the scan leaves idle (its shorter
+    # workgroups finish first).
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev) if (OVERLAP_COMPRESS and semantics != "segment" and plan.batches) else main
+    if side is not main:
+        side.wait_stream(main)
+
     _run(timer, "moments", k1)
 
     node_src = node_w = None
@@ -261,15 +285,22 @@ def prefill(
     elif plan.batches:
         node_src = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.int32)
         node_w = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.float32)
-        for bd in batches_d:
-            def k3_launch(bd=bd):
-                st = lib.sta_compress_nodes(
-                    k3.data_ptr(), dt, bh, n, d, bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(), plan.n_nodes,
-                    plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(), dr.dirs.shape[1],
-                    dr.max_in, node_src.data_ptr(), node_w.data_ptr(), stream)
-                _native.check(st, "sta_compress_nodes")
+        if side is not main:
+            node_src.record_stream(side)
+            node_w.record_stream(side)
+        with torch.cuda.stream(side):
+            k3_stream = _native.stream_handle(dev)
+            for bd in batches_d:
+                def k3_launch(bd=bd):
+                    st = lib.sta_compress_nodes(
+                        k3.data_ptr(), dt, bh, n, d, bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(),
+                        plan.n_nodes, plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(),
+                        dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(), k3_stream)
+                    _native.check(st, "sta_compress_nodes")
 
-            _run(timer, "compress", k3_launch)
+                _run(timer, "compress", k3_launch)
+        if side is not main:
+            main.wait_stream(side)
 
     if raw:
         out = torch.empty((bh, n, dv), device=dev, dtype=torch.float32)

@@ -245,8 +245,11 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // while the weights of subtile kt are evaluated (VALU in the matrix cores' shadow), then subtile kt's
   // num^T += V^T P^T.  X is accumulated in two halves of the dimensions (4 independent chains).
   // NODE: coreset items (weight, active rows) instead of the tile's own keys.
+  // node_tag: 0 the tile's own keys, 1 coreset items with their active-row test, 2 coreset items active
+  // on every row of the tile (the test is skipped)
   auto process = [&](auto node_tag) {
-    constexpr bool NODE = decltype(node_tag)::value;
+    constexpr bool NODE = decltype(node_tag)::value != 0;
+    constexpr bool FULL = decltype(node_tag)::value == 2;
     // weights of subtile kt from its logits X (key 16 kt + 4 lg + r, row myrow[rs]), elementwise
     auto weights = [&](int kt, const floatx4 (&X)[RS], floatx4 (&P)[RS]) {
 #pragma unroll
@@ -262,7 +265,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           const float ex = __builtin_amdgcn_exp2f(fminf(yv, ymax));
           const float tp = taylor2(yv, tc);
           float p;
-          if constexpr (NODE) {
+          if constexpr (FULL) {
+            p = (ex - tp) * w;  // rows outside the sequence have zero queries and are never stored
+          } else if constexpr (NODE) {
             const bool on = rvalid[rs] && i >= lo && i <= hi;
             p = on ? (ex - tp) * w : 0.f;
           } else {
@@ -389,8 +394,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
       }
     }
   };
-  using node_batch = std::integral_constant<bool, true>;
-  using block_batch = std::integral_constant<bool, false>;
+  using block_batch = std::integral_constant<int, 0>;
+  using node_batch = std::integral_constant<int, 1>;
+  using node_batch_full = std::integral_constant<int, 2>;
 
   // ---- batch sequence: phase A = contiguous keys [kstart, kend), phase B = the node item list ----
   int kstart = static_cast<int>(chunk_start(row_lo, a.chunk, a.shift));
@@ -485,6 +491,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
       phi = in ? Lhi[off + tid] : -1;
     }
   };
+  bool item_full = true;
   auto commit = [&]() {
     if constexpr (SPLIT) {
       // bf16 hi / lo planes; keys row-major (dimension 4 u..4 u+3 of key r: 8 bytes per plane), values
@@ -544,6 +551,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
       Lost[tid] = plo;
       Hist[tid] = phi;
     }
+    // this thread's staged item is padding or active on every row of the tile
+    item_full = tid >= KB || pj < 0 || (plo <= row_lo && phi >= row_hi);
   };
 
   // batch b: phase A for b < n_a (offset kstart + b KB), then phase B (offset into the list chunk).  The
@@ -574,9 +583,12 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         llen = 0;
     }
     const bool nxt_have = !nxt_node || nxt_off < llen;
-    __syncthreads();  // staged batch and list visible
+    // staged batch and list visible; whether every staged item is active on all rows of the tile
+    const bool full = __syncthreads_and(item_full ? 1 : 0) != 0;
     if (nxt_have) prefetch(nxt_node, nxt_off);
-    if (cur_node)
+    if (cur_node && full)
+      process(node_batch_full{});
+    else if (cur_node)
       process(node_batch{});
     else if (cur_off <= wrow_hi)
       process(block_batch{});  // some key of the batch precedes some row of this wave
