@@ -422,6 +422,69 @@ class DecodeState:
         total += items * (d + dv + 1) * elem
         return int(total)
 
+    # ------------------------------------------------------------------ save / resume
+    def _config(self) -> Dict[str, object]:
+        return {"streams": self.S, "dim": self.d, "value_dim": self.dv, "degree": self.degree, "block": self.block,
+                "scale": self.scale, "compressor": self.compressor, "seed": self.seed, "eps": self.eps}
+
+    def state_dict(self) -> Dict[str, object]:
+        """The streams' whole state on the host: configuration, counters, moments, buffered tokens, level
+        coresets, each stream's generator state and any reserved completion draws.  Plain tensors, ints,
+        floats and strings, so torch.save / torch.load(weights_only=True) round-trip it."""
+        torch.cuda.synchronize(self.device)
+        levels = {}
+        if self.L:
+            levels = {"lev_k": self.lev_k.cpu(), "lev_v": self.lev_v.cpu(), "lev_w": self.lev_w.cpu(),
+                      "lev_pos": self.lev_pos.cpu()}
+        draws = [{"blocks_before": dr.blocks_before, "n_calls": dr.n_calls, "methods": dr.methods.cpu(),
+                  "dirs": dr.dirs.cpu(), "unif": dr.unif.cpu(), "perms": dr.perms.cpu()} for dr in self._draws]
+        return {
+            "format": 1,
+            "config": self._config(),
+            "length": self.length, "blocks": self.blocks, "buf_len": self.buf_len,
+            "num_compressions": self.num_compressions, "levels_allocated": self.L,
+            "state_num": self.state_num.cpu(), "state_den": self.state_den.cpu(),
+            "buf_k": self.buf_k[:, : self.buf_len].cpu(), "buf_v": self.buf_v[:, : self.buf_len].cpu(),
+            **levels,
+            "generators": torch.stack([g.get_state() for g in self._gens]),
+            "draws": draws,
+        }
+
+    def load_state_dict(self, sd: Dict[str, object]) -> None:
+        """Resume from state_dict(): the configuration must match this object's."""
+        if sd.get("format") != 1:
+            raise ValueError("unknown decode state format")
+        if sd["config"] != self._config():
+            raise ValueError(f"decode state configuration {sd['config']} does not match {self._config()}")
+        dev = self.device
+        buf_len = int(sd["buf_len"])
+        while self.cap < buf_len:
+            self._grow_buffer()
+        self.state_num.copy_(sd["state_num"].to(dev))
+        self.state_den.copy_(sd["state_den"].to(dev))
+        self.buf_k.zero_()
+        self.buf_v.zero_()
+        self.buf_k[:, :buf_len] = sd["buf_k"].to(dev)
+        self.buf_v[:, :buf_len] = sd["buf_v"].to(dev)
+        n_lev = int(sd["levels_allocated"])
+        if n_lev:
+            self._ensure_levels(n_lev)
+            self.lev_k.zero_()
+            self.lev_v.zero_()
+            self.lev_w.zero_()
+            self.lev_pos.zero_()
+            self.lev_k[:, :n_lev] = sd["lev_k"].to(dev)
+            self.lev_v[:, :n_lev] = sd["lev_v"].to(dev)
+            self.lev_w[:, :n_lev] = sd["lev_w"].to(dev)
+            self.lev_pos[:, :n_lev] = sd["lev_pos"].to(dev)
+        self.length, self.blocks, self.buf_len = int(sd["length"]), int(sd["blocks"]), buf_len
+        self.num_compressions = int(sd["num_compressions"])
+        for g, st in zip(self._gens, sd["generators"]):
+            g.set_state(st.clone())
+        self._draws = deque(_CompletionDraws(int(d["blocks_before"]), int(d["n_calls"]), d["methods"].to(dev),
+                                             d["dirs"].to(dev), d["unif"].to(dev), d["perms"].to(dev))
+                            for d in sd["draws"])
+
     def device_bytes(self) -> int:
         """Bytes of device memory this state holds."""
         ts = [self.state_num, self.state_den, self.buf_k, self.buf_v, self.lev_k, self.lev_v, self.lev_w,

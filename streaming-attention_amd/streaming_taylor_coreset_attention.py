@@ -484,6 +484,24 @@ class ArticleStreamingAttention:
         self._st.extend(k3, v3)
         return res.out[0] if one else res.out
 
+    def state_dict(self) -> dict:
+        """The streams' state for a later resume (no counterpart in the reference): the decode state's
+        tensors on the host, counters and generator states, plus this object's settings.  Plain tensors
+        and Python scalars, so torch.save / torch.load(weights_only=True) round-trip it."""
+        return {"attention": self.state_dict_settings(), "decode": self._st.state_dict()}
+
+    def load_state_dict(self, state: dict) -> None:
+        """Resume from state_dict() of an object built with the same settings (the device may differ)."""
+        mine = self.state_dict_settings()
+        if state["attention"] != mine:
+            raise ValueError(f"state settings {state['attention']} do not match this object's {mine}")
+        self._st.load_state_dict(state["decode"])
+
+    def state_dict_settings(self) -> dict:
+        return {"dim": self.dim, "value_dim": self.value_dim, "degree": self.degree, "block_size": self.block_size,
+                "scale": self.scale, "compressor": self.compressor, "dtype": str(self.dtype), "seed": self.seed,
+                "denominator_eps": self.denominator_eps, "streams": None if self._single else self.streams}
+
 
 # ----------------------------------------------------------------------------- small CLI sanity check
 # Same flags and printed lines as the reference's (streaming_taylor_coreset_attention.py:762-805).

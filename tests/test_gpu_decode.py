@@ -243,3 +243,36 @@ def test_decode_errors():
     lib = _native.lib()
     assert lib.sta_decode_compress(1, 4, 2, None, None, 2, 0, None, None, None, None, 1, 1, 1, None, None, None,
                                    None, 2, None) == _native.STA_ERR_ARG
+
+
+@pytest.mark.parametrize("comp,dtype", [("sorted_pair", torch.float32), ("random", torch.bfloat16),
+                                        ("none", torch.float32)])
+def test_state_dict_resume_is_bit_exact(comp, dtype):
+    """state_dict() after 300 tokens (with draws reserved ahead), torch.save / torch.load(weights_only=True),
+    load_state_dict() into a fresh object: the next 400 steps (block completions and merges included)
+    equal those of the original object bit for bit, and so do the final levels."""
+    import io
+    S, d, dv, block = 5, 24, 20, 32
+    g = torch.Generator().manual_seed(3)
+    q, k, v = ((torch.randn(S, 700, w, generator=g) * 0.3).to(dtype) for w in (d, d, dv))
+    kw = dict(degree=2, block_size=block, scale=0.5, compressor=comp, device=DEV, dtype=dtype, seed=11, streams=S)
+    a = stc.ArticleStreamingAttention(d, dv, **kw)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    a.extend(kd[:, :290], vd[:, :290])
+    for i in range(290, 300):
+        a.step(qd[:, i], kd[:, i], vd[:, i])
+    a._st.reserve_draws(100)
+    buf = io.BytesIO()
+    torch.save(a.state_dict(), buf)
+    buf.seek(0)
+    b = stc.ArticleStreamingAttention(d, dv, **kw)
+    b.load_state_dict(torch.load(buf, weights_only=True))
+    assert b.length == a.length == 300
+    out_a = torch.stack([a.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(300, 700)], dim=1)
+    out_b = torch.stack([b.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(300, 700)], dim=1)
+    assert torch.equal(out_a, out_b)
+    if comp != "none":
+        for la, lb in zip(a.coreset.level_positions(), b.coreset.level_positions()):
+            assert (la is None and lb is None) or torch.equal(la, lb)
+    with pytest.raises(ValueError):
+        stc.ArticleStreamingAttention(d, dv, **dict(kw, seed=12)).load_state_dict(a.state_dict())
