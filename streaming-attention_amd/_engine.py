@@ -26,11 +26,11 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 # bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
 # products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
-# Run the level / block compressor on a second stream, overlapping the moment scan's tail.  Off: on
-# 32 heads x 65536 tokens the step takes the same time either way (12.15-12.25 ms against 12.17 ms on
-# one box); the moment scan's workgroups hold the compute units' LDS until it ends, so the
-# compressor's workgroups start only at its tail.
-OVERLAP_COMPRESS = False
+# Run the level / block compressor on a second stream, overlapping the moment scan's tail (the scan's
+# workgroups hold the compute units' LDS, so the compressor's start as the scan's shorter workgroups
+# finish).  On 32 heads x 65536 tokens: 11.47-11.49 ms per step against 11.81-11.88 ms without on one
+# box, no difference (12.15-12.25 against 12.17-12.18 ms) on another.
+OVERLAP_COMPRESS = True
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 

@@ -50,6 +50,7 @@ namespace sta {
 constexpr int MOM_C = 32;    // tokens per chunk
 constexpr int MOM_LDT = 36;  // token stride of the transposed Kt / Vt rows
 constexpr int MOM_LDR = 32;  // token stride of a partial column
+static_assert(MOM_C <= MOM_LDT, "the bf16 value planes [2][CG][MOM_C] fit in the fp32 rows [CG][MOM_LDT]");
 
 // Offset of token t of partial column col.  The 4-token groups of a column are permuted by
 // (col / 2) mod 8, so the 16 columns a 16-byte access touches at one token group fall on 16 distinct
@@ -213,7 +214,9 @@ __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f
   }
 }
 
-template <bool DBIG, int ES, int CG>
+// SPLIT: the values go to LDS as bf16 hi / lo planes [CG][32 tokens] (split once per workgroup for the
+// split-product update) in place of the fp32 Vt rows; they fit in Vt's space.
+template <bool DBIG, int ES, int CG, bool SPLIT = false>
 __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                           float* buf, int dummy_rel, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
@@ -252,8 +255,22 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const Mo
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       if (m < 4 || wide) {
-        float* p = sl.v_col[j] >= 0 ? Vt + (sl.v_col[j] + m) * MOM_LDT + tok : dmy + m;
-        *p = f[m] * kok;
+        if constexpr (SPLIT) {
+          __bf16* vh = reinterpret_cast<__bf16*>(Vt);
+          const float x = f[m] * kok;
+          const __bf16 h = static_cast<__bf16>(x);
+          const __bf16 l = static_cast<__bf16>(x - static_cast<float>(h));
+          if (sl.v_col[j] >= 0) {
+            vh[(sl.v_col[j] + m) * MOM_C + tok] = h;
+            vh[(CG + sl.v_col[j] + m) * MOM_C + tok] = l;
+          } else {
+            reinterpret_cast<__bf16*>(dmy + m)[0] = h;
+            reinterpret_cast<__bf16*>(dmy + m)[1] = l;
+          }
+        } else {
+          float* p = sl.v_col[j] >= 0 ? Vt + (sl.v_col[j] + m) * MOM_LDT + tok : dmy + m;
+          *p = f[m] * kok;
+        }
       }
     }
   }
@@ -399,13 +416,15 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
       fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 4 * h);
       if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 4 * h);
     }
+  // the staged bf16 planes (mom_store<..., true>): row 16 ct + li, tokens 8 lg .. 8 lg + 7; the 64 lanes'
+  // 16-byte reads tile one contiguous 1 KiB block per plane
+  constexpr int CG = 16 * CT;
+  const __bf16* vplane = reinterpret_cast<const __bf16*>(Vt);
   bf16x8 vh[CT], vl[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const floatx4 v0 = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
-    const floatx4 v1 = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
-    const float t[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-    split_bf16(t, vh[ct], vl[ct]);
+    vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + (16 * ct + li) * MOM_C + 8 * lg);
+    vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + (CG + 16 * ct + li) * MOM_C + 8 * lg);
   }
   mid();
   __builtin_amdgcn_sched_barrier(0);
@@ -573,7 +592,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   __syncthreads();
   MomStage<DBIG, CG> pre;
   mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first);
-  mom_store<DBIG, ES, CG>(pre, sl, a, smem, dummy_abs, first);
+  mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
 
   for (int c = 0; c < nchunks; ++c) {
@@ -653,7 +672,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
     }
     // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
     if (c + 1 < nchunks)
-      mom_store<DBIG, ES, CG>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
+      mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
