@@ -240,6 +240,8 @@ def main() -> int:
             "avg_launch_ms": mom_ms,
         },
         "kernels": per_kernel,
+        "kernels_note": ("compress runs on a second stream overlapping moments; its HIP-event interval "
+                         "includes the wait for compute units" if _engine.OVERLAP_COMPRESS else ""),
         "host_plan_and_draws_s": round(t_plan, 3),
         "wall_s_timed_region": round(wall, 4),
     }
