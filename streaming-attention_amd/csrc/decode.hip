@@ -149,19 +149,27 @@ struct DecItem {
   floatx4 v[VC];
 };
 
+// Loads are unconditional (units past the row clamped to its last one, zeroed by a select afterwards):
+// a load under a branch makes the compiler wait for it at the join, serialising the items in flight.
 template <int KC, int VC>
 __device__ __forceinline__ void dec_load_item(DecItem<KC, VC>& it, const float* krow, const float* vrow, int c, int dk4,
                                               int dv4) {
 #pragma unroll
   for (int j = 0; j < KC; ++j) {
     const int u = c + 16 * j;
-    it.k[j] = u < dk4 ? *reinterpret_cast<const floatx4*>(krow + 4 * u) : floatx4{0.f, 0.f, 0.f, 0.f};
+    it.k[j] = *reinterpret_cast<const floatx4*>(krow + 4 * min(u, dk4 - 1));
   }
 #pragma unroll
   for (int j = 0; j < VC; ++j) {
     const int u = c + 16 * j;
-    it.v[j] = u < dv4 ? *reinterpret_cast<const floatx4*>(vrow + 4 * u) : floatx4{0.f, 0.f, 0.f, 0.f};
+    it.v[j] = *reinterpret_cast<const floatx4*>(vrow + 4 * min(u, dv4 - 1));
   }
+#pragma unroll
+  for (int j = 0; j < KC; ++j)
+    if (c + 16 * j >= dk4) it.k[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < VC; ++j)
+    if (c + 16 * j >= dv4) it.v[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 }
 
 template <int KC>
@@ -175,6 +183,23 @@ __device__ __forceinline__ float dec_dot(const floatx4 (&x)[KC], const floatx4 (
   t += __shfl_xor(t, 1, 16);
   return t;
 }
+
+// exp(z) on the hardware exp2 (about 1 ulp) and the Taylor truncation sum_{r<=deg} z^r / r! by Horner
+// (c1..c3 = [deg >= r] / r!): the residual exp - exp_{<=t} and the buffered tokens' exp need 1e-5
+// relative, not the reference's term-by-term rounding.
+struct DecTaylor {
+  float c1, c2, c3;
+};
+__device__ __forceinline__ DecTaylor dec_taylor(int deg) {
+  return DecTaylor{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 0.5f : 0.f, deg >= 3 ? 0.166666672f : 0.f};
+}
+__device__ __forceinline__ float dec_tp(float z, const DecTaylor& t) {
+  return fmaf(z, fmaf(z, fmaf(z, t.c3, t.c2), t.c1), 1.f);
+}
+__device__ __forceinline__ float dec_exp(float z) { return __builtin_amdgcn_exp2f(z * 1.44269504f); }
+
+// Items per 16-lane group in flight: NB rows are loaded before any of them is used.
+constexpr int DEC_NB = 4;
 
 template <int KC, int VC>
 __global__ __launch_bounds__(DEC_THREADS) void decode_tail_kernel(const DecTailArgs a) {
@@ -218,23 +243,26 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_tail_kernel(const DecTailA
   for (int j = 0; j < VC; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
   float den = 0.f, tay = 0.f;  // tay: Taylor part of the buffered tokens (reference low denominator)
 
-  // buffered tokens: exact exponential, weight 1 (two items per group in flight)
+  const DecTaylor tc = dec_taylor(a.degree);
+  // buffered tokens: exact exponential, weight 1 (DEC_NB items per group in flight)
   const float* bk = a.buf_k + s * a.B * a.dk;
   const float* bv = a.buf_v + s * a.B * a.ldv;
-  for (int j0 = g; j0 < a.buf_len; j0 += 2 * DEC_GROUPS) {
-    DecItem<KC, VC> it[2];
-    const int j1 = min(j0 + DEC_GROUPS, a.buf_len - 1);
-    dec_load_item<KC, VC>(it[0], bk + j0 * a.dk, bv + j0 * a.ldv, c, dk4, dv4);
-    dec_load_item<KC, VC>(it[1], bk + j1 * a.dk, bv + j1 * a.ldv, c, dk4, dv4);
+  for (int j0 = g; j0 < a.buf_len; j0 += DEC_NB * DEC_GROUPS) {
+    DecItem<KC, VC> it[DEC_NB];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float z = dec_dot<KC>(x, it[h].k);
-      const bool on = h == 0 || j0 + DEC_GROUPS < a.buf_len;
-      const float p = on ? expf(z) : 0.f;
+    for (int b = 0; b < DEC_NB; ++b) {
+      const int jb = min(j0 + b * DEC_GROUPS, a.buf_len - 1);
+      dec_load_item<KC, VC>(it[b], bk + jb * a.dk, bv + jb * a.ldv, c, dk4, dv4);
+    }
+#pragma unroll
+    for (int b = 0; b < DEC_NB; ++b) {
+      const float z = dec_dot<KC>(x, it[b].k);
+      const bool on = j0 + b * DEC_GROUPS < a.buf_len;
+      const float p = on ? dec_exp(z) : 0.f;
       den += p;
-      tay += on ? taylor_poly(z, a.degree) : 0.f;
+      tay += on ? dec_tp(z, tc) : 0.f;
 #pragma unroll
-      for (int j = 0; j < VC; ++j) acc[j] += p * it[h].v[j];
+      for (int j = 0; j < VC; ++j) acc[j] += p * it[b].v[j];
     }
   }
   // the current token of this launch (group 0)
@@ -242,9 +270,9 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_tail_kernel(const DecTailA
     DecItem<KC, VC> it;
     dec_load_item<KC, VC>(it, cur_k, cur_v, c, dk4, dv4);
     const float z = dec_dot<KC>(x, it.k);
-    const float p = expf(z);
+    const float p = dec_exp(z);
     den += p;
-    tay += taylor_poly(z, a.degree);
+    tay += dec_tp(z, tc);
 #pragma unroll
     for (int j = 0; j < VC; ++j) acc[j] += p * it.v[j];
   }
@@ -257,20 +285,23 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_tail_kernel(const DecTailA
     const float* lk = a.lev_k + base * a.dk;
     const float* lv = a.lev_v + base * a.ldv;
     const float* lw = a.lev_w + base;
-    for (int j0 = g; j0 < a.m; j0 += 2 * DEC_GROUPS) {
-      DecItem<KC, VC> it[2];
-      const int j1 = min(j0 + DEC_GROUPS, a.m - 1);
-      dec_load_item<KC, VC>(it[0], lk + j0 * a.dk, lv + j0 * a.ldv, c, dk4, dv4);
-      dec_load_item<KC, VC>(it[1], lk + j1 * a.dk, lv + j1 * a.ldv, c, dk4, dv4);
-      const float w0 = lw[j0], w1 = lw[j1];
+    for (int j0 = g; j0 < a.m; j0 += DEC_NB * DEC_GROUPS) {
+      DecItem<KC, VC> it[DEC_NB];
+      float w[DEC_NB];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float z = dec_dot<KC>(x, it[h].k);
-        const bool on = h == 0 || j0 + DEC_GROUPS < a.m;
-        const float r = on ? (h == 0 ? w0 : w1) * (expf(z) - taylor_poly(z, a.degree)) : 0.f;
+      for (int b = 0; b < DEC_NB; ++b) {
+        const int jb = min(j0 + b * DEC_GROUPS, a.m - 1);
+        dec_load_item<KC, VC>(it[b], lk + jb * a.dk, lv + jb * a.ldv, c, dk4, dv4);
+        w[b] = lw[jb];
+      }
+#pragma unroll
+      for (int b = 0; b < DEC_NB; ++b) {
+        const float z = dec_dot<KC>(x, it[b].k);
+        const bool on = j0 + b * DEC_GROUPS < a.m;
+        const float r = on ? w[b] * (dec_exp(z) - dec_tp(z, tc)) : 0.f;
         den += r;
 #pragma unroll
-        for (int j = 0; j < VC; ++j) acc[j] += r * it[h].v[j];
+        for (int j = 0; j < VC; ++j) acc[j] += r * it[b].v[j];
       }
     }
   }
