@@ -126,6 +126,8 @@ def main() -> int:
                     choices=[WORKLOAD["workload"], DECODE["workload"], FLASH["workload"]])
     ap.add_argument("--streams", type=int, default=DECODE["batch"] * DECODE["heads"], help="decode streams")
     ap.add_argument("--prefix", type=int, default=DECODE["prefix"], help="decode prefix tokens")
+    ap.add_argument("--flash-dtype", default="fp32", choices=["fp32", "bf16", "fp16"],
+                    help="input dtype of the flash workload (16-bit inputs run on the 16-bit matrix cores)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB fp32 tensor 3 times (calibration kernel for the HBM byte counters)")
     args = ap.parse_args()
@@ -261,10 +263,13 @@ def run_flash(args) -> int:
     import _engine
     import triton_article_attention as taa
 
-    w = dict(FLASH, seq_len=args.seq_len, heads=args.heads)
+    in_dtype = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.flash_dtype]
+    w = dict(FLASH, seq_len=args.seq_len, heads=args.heads, dtype=args.flash_dtype)
+    if args.flash_dtype != "fp32":
+        w["workload"] = f"flash_c3_{args.flash_dtype}"
     bh, n, d, dv = w["batch"] * w["heads"], w["seq_len"], w["d"], w["dv"]
     print(f"[bench] flash: generating inputs {w['batch']}x{w['heads']}x{n}x{d}", file=sys.stderr, flush=True)
-    q, k, v = make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"])
+    q, k, v = (x.to(in_dtype) for x in make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"]))
     dev = torch.device("cuda:0")
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     q3, k3, v3 = qd.reshape(bh, n, d), kd.reshape(bh, n, d), vd.reshape(bh, n, dv)
@@ -297,6 +302,7 @@ def run_flash(args) -> int:
     flops = float(d + dv) * n * (n + 1) * bh  # QK^T and PV over the n (n + 1) / 2 causal pairs
     achieved = flops / (k_ms * 1e-3) / 1e12
     value = bh * n / (ms_step * 1e-3)
+    peak = MFMA_FP32_PEAK_TFLOPS if args.flash_dtype == "fp32" else MFMA_BF16_PEAK_TFLOPS
     line = {
         "metric": "head-tokens/sec, exact causal softmax attention, N=64K d=64; % of MFMA roofline",
         "value": value,
@@ -308,16 +314,18 @@ def run_flash(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": args.flash_dtype,
         "data": "synthetic",
         "config": w,
         "roofline": {
-            "kernel": "flash_attn_kernel (online-softmax exact attention, fp32 matrix cores)",
+            "kernel": ("flash_attn_kernel (online-softmax exact attention, fp32 matrix cores)" if args.flash_dtype == "fp32"
+                       else "flash_attn16_kernel (online-softmax exact attention, 16-bit matrix cores: one product "
+                            "for QK^T, two (P as hi + lo) for PV)"),
             "bound": "mfma",
             "achieved": achieved,
-            "peak": MFMA_FP32_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": achieved / MFMA_FP32_PEAK_TFLOPS,
+            "frac": achieved / peak,
             "traffic": measured_traffic(w["workload"], "flash_attn_kernel"),
             "algorithmic_flops_per_launch": flops,
             "avg_launch_ms": k_ms,
@@ -330,7 +338,7 @@ def run_flash(args) -> int:
         threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
         torch.set_num_threads(threads)
         chunk = 2048  # query rows per host product (the whole N x N logits of a head would be 17 GB)
-        qh, kh, vh = q[0, 0], k[0, 0], v[0, 0]
+        qh, kh, vh = q[0, 0].float(), k[0, 0].float(), v[0, 0].float()
         kt = kh.T.contiguous()
         t0 = time.perf_counter()
         for lo in range(0, n, chunk):

@@ -11,8 +11,9 @@
 // (lanes li, li + 16, li + 32, li + 48) and the rescale exp2(m_old - m_new) applies to the lane's own
 // accumulators.
 //
-// Products are fp32 matrix-core ops for every input dtype: exact products of the inputs (the
-// reference's tf32 dots round fp32 operands to 10 mantissa bits).
+// Products for fp32 inputs are fp32 matrix-core ops: exact products of the inputs (the reference's tf32
+// dots round fp32 operands to 10 mantissa bits); 16-bit inputs use the 16-bit matrix cores
+// (flash_attn16_kernel below).
 #include <type_traits>
 
 #include "common.hpp"
@@ -244,6 +245,296 @@ __global__ __launch_bounds__(256, flash_occupancy(DP, DVT, RS)) void flash_attn_
   }
 
   // ---- epilogue: row sums over the four lane groups, normalise, store ----
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
+    float dsum = den[rs];
+    dsum += __shfl_xor(dsum, 16);
+    dsum += __shfl_xor(dsum, 32);
+    if (!rvalid[rs]) continue;
+    const float dn = fmaxf(dsum, 1e-20f);
+    const int64_t obase = (bh * a.n + myrow[rs]) * a.dv;
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) {
+      const int c0 = 16 * ct + 4 * lg;
+      if (c0 >= a.dv) continue;
+      floatx4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = num[rs][ct][r] / dn;
+      if (a.vec_out) {
+        *reinterpret_cast<floatx4*>(static_cast<float*>(a.out) + obase + c0) = o;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (c0 + r < a.dv) store_elem(a.out, obase + c0 + r, a.out_dtype, o[r]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// 16-bit inputs (bf16 / fp16): the matrix cores take the inputs as they are.  X^T = K Q^T with
+// v_mfma_f32_16x16x32_{bf16,f16} is exact (16-bit products, fp32 sums) and scaled to base-2 logits
+// afterwards; num^T += V^T P^T takes the fp32 probabilities as 16-bit hi + lo (P = hi + lo + e,
+// |e| <= 2^-17 P for bf16, 2^-21 P for fp16) against the exact values: two products.  Lane layout as
+// in the split-product residual kernel: k-step m of lane group lg covers dimensions 32 m + 8 lg + j;
+// the V^T rows hold each pair of 16-key subtiles in contraction order (flash_key_pos), so every
+// operand is one 16-byte LDS read.
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+__host__ __device__ constexpr int flash_key_pos(int r) {
+  return 32 * (r >> 5) + 8 * ((r >> 2) & 3) + 4 * ((r >> 4) & 1) + (r & 3);
+}
+
+template <bool F16>
+__device__ __forceinline__ floatx4 mfma16(const uint4& a, const uint4& b, floatx4 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// two fp32 values as packed 16-bit (bf16: round to nearest even; fp16: round toward zero, so the low
+// part x - hi keeps the sign of x) and back
+template <bool F16>
+__device__ __forceinline__ uint32_t pack16(float a, float b) {
+  if constexpr (F16)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+  else
+    return pk_bf16(a, b);
+}
+template <bool F16>
+__device__ __forceinline__ float lo16(uint32_t p) {
+  if constexpr (F16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(p & 0xffffu)));
+  else
+    return __uint_as_float(p << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float hi16(uint32_t p) {
+  if constexpr (F16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(p >> 16)));
+  else
+    return __uint_as_float(p & 0xffff0000u);
+}
+
+// the first `valid` of the 4 16-bit elements of a raw unit (x: elements 0, 1; y: 2, 3), the rest zero
+__device__ __forceinline__ uint2 mask16(uint2 u, int valid) {
+  const uint32_t m0 = valid >= 2 ? 0xffffffffu : (valid == 1 ? 0x0000ffffu : 0u);
+  const uint32_t m1 = valid >= 4 ? 0xffffffffu : (valid == 3 ? 0x0000ffffu : 0u);
+  return uint2{u.x & m0, u.y & m1};
+}
+
+// two workgroups per compute unit while the accumulators and staging registers fit in 256 VGPRs
+__host__ __device__ constexpr int flash16_occupancy(int dp, int dvt) { return dp + 16 * dvt <= 128 ? 2 : 1; }
+
+template <int DP, int DVT, int RS, bool F16>
+__global__ __launch_bounds__(256, flash16_occupancy(DP, DVT)) void flash_attn16_kernel(const FlashArgs a) {
+  constexpr int KB = 64;  // keys per LDS stage
+  constexpr int NSUB = KB / 16;
+  constexpr int DPS = DP < 32 ? 32 : DP;  // dimensions in whole 32-element steps
+  constexpr int MS = DPS / 32;
+  constexpr int LDK = DPS + 8;  // 16-bit elements per key row: 16 (2 j + 1) bytes
+  constexpr int DV = DVT * 16;
+  constexpr int LDV = KB + 8;
+  constexpr int TM = 64 * RS;
+  constexpr int KU = DP / 4, VU = DV / 4;
+  constexpr int KPT = (KB * KU + 255) / 256, VPT = (KB * VU + 255) / 256;
+  __shared__ uint4 kst4[(KB * LDK + 7) / 8];
+  __shared__ uint4 vst4[(DV * LDV + 7) / 8];
+  uint16_t* const Kst = reinterpret_cast<uint16_t*>(kst4);
+  uint16_t* const Vst = reinterpret_cast<uint16_t*>(vst4);
+
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / a.n_tiles;
+  const int t = a.n_tiles - 1 - (wg - static_cast<int>(bh) * a.n_tiles);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int n = static_cast<int>(a.n);
+  const int r0 = t * TM;
+  const int64_t qkbase = bh * a.n * a.ldqk;
+  const int64_t vbase = bh * a.n * a.ldv;
+
+  // the wave's query rows as B operands (8 dimensions per lane and k-step), columns >= d zero
+  int myrow[RS];
+  bool rvalid[RS];
+  uint4 qB[RS][MS];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
+    myrow[rs] = r0 + (wave * RS + rs) * 16 + li;
+    rvalid[rs] = myrow[rs] < n;
+    const int64_t qoff = qkbase + static_cast<int64_t>(rvalid[rs] ? myrow[rs] : 0) * a.ldqk;
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+      uint2 h[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int col = 32 * m + 8 * lg + 4 * hh;
+        const uint4 raw = load_unit<2>(a.q, qoff + min(col, a.ldqk - 4));
+        h[hh] = mask16(uint2{raw.x, raw.y}, rvalid[rs] ? a.d - col : 0);
+      }
+      qB[rs][m] = uint4{h[0].x, h[0].y, h[1].x, h[1].y};
+    }
+  }
+  const int wrow_lo = r0 + wave * RS * 16, wrow_hi = wrow_lo + RS * 16 - 1;
+
+  floatx4 num[RS][DVT];
+  float den[RS], mrow[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
+    den[rs] = 0.f;
+    mrow[rs] = -1e30f;
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) num[rs][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto process = [&](auto diag_tag, int off) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    floatx4 X[NSUB][RS];
+#pragma unroll
+    for (int kt = 0; kt < NSUB; ++kt)
+#pragma unroll
+      for (int rs = 0; rs < RS; ++rs) X[kt][rs] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+#pragma unroll
+      for (int kt = 0; kt < NSUB; ++kt) {
+        const uint4 kv = *reinterpret_cast<const uint4*>(Kst + (16 * kt + li) * LDK + 32 * m + 8 * lg);
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) X[kt][rs] = mfma16<F16>(kv, qB[rs][m], X[kt][rs]);
+      }
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+      float mx = -__builtin_huge_valf();
+#pragma unroll
+      for (int kt = 0; kt < NSUB; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float y = X[kt][rs][r] * a.scale2;
+          if constexpr (DIAG) {
+            if (off + 16 * kt + 4 * lg + r > myrow[rs]) y = -__builtin_huge_valf();
+          }
+          X[kt][rs][r] = y;
+          mx = fmaxf(mx, y);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(mrow[rs], mx);
+      const float alpha = __builtin_amdgcn_exp2f(mrow[rs] - mnew);
+      mrow[rs] = mnew;
+      den[rs] *= alpha;
+#pragma unroll
+      for (int ct = 0; ct < DVT; ++ct) num[rs][ct] *= alpha;
+#pragma unroll
+      for (int kt = 0; kt < NSUB; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(X[kt][rs][r] - mnew);
+          X[kt][rs][r] = p;
+          den[rs] += p;
+        }
+    }
+#pragma unroll
+    for (int sp = 0; sp < NSUB / 2; ++sp) {
+      uint4 ph[RS], pl[RS];
+#pragma unroll
+      for (int rs = 0; rs < RS; ++rs) {
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const floatx4& P = X[2 * sp + (e >> 1)][rs];
+          const float p0 = P[2 * (e & 1)], p1 = P[2 * (e & 1) + 1];
+          h[e] = pack16<F16>(p0, p1);
+          l[e] = pack16<F16>(p0 - lo16<F16>(h[e]), p1 - hi16<F16>(h[e]));
+        }
+        ph[rs] = uint4{h[0], h[1], h[2], h[3]};
+        pl[rs] = uint4{l[0], l[1], l[2], l[3]};
+      }
+#pragma unroll
+      for (int ct = 0; ct < DVT; ++ct) {
+        const uint4 vv = *reinterpret_cast<const uint4*>(Vst + (16 * ct + li) * LDV + 32 * sp + 8 * lg);
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma16<F16>(vv, pl[rs], num[rs][ct]);
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma16<F16>(vv, ph[rs], num[rs][ct]);
+      }
+    }
+  };
+
+  const int row_hi = (r0 + TM < n ? r0 + TM : n) - 1;
+  const int kend = row_hi + 1;
+  const int nb = (kend + KB - 1) / KB;
+
+  uint2 pk[KPT], pv[VPT];
+  uint32_t pk_ok = 0, pv_ok = 0;
+  auto prefetch = [&](int off) {
+    pk_ok = pv_ok = 0;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / KU, u = e - r * KU;
+      const bool ok = e < KB * KU && off + r < kend && 4 * u < a.d;
+      pk_ok |= ok ? (1u << i) : 0u;
+      const int src = ok ? off + r : 0;
+      const uint4 raw = load_unit<2>(a.k, qkbase + static_cast<int64_t>(src) * a.ldqk + min(4 * u, a.ldqk - 4));
+      pk[i] = uint2{raw.x, raw.y};
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e % KB, u = e / KB;
+      const bool ok = e < KB * VU && off + r < kend && 4 * u < a.dv;
+      pv_ok |= ok ? (1u << i) : 0u;
+      const int src = ok ? off + r : 0;
+      const uint4 raw = load_unit<2>(a.v, vbase + static_cast<int64_t>(src) * a.ldv + min(4 * u, a.ldv - 4));
+      pv[i] = uint2{raw.x, raw.y};
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int e = tid + 256 * i;
+      if (e < KB * KU) {
+        const int r = e / KU, u = e - r * KU;
+        const int valid = ((pk_ok >> i) & 1u) ? a.d - 4 * u : 0;
+        *reinterpret_cast<uint2*>(Kst + r * LDK + 4 * u) = mask16(pk[i], valid);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = tid + 256 * i;
+      if (e < KB * VU) {
+        const int r = e % KB, u = e / KB;
+        const uint2 w = mask16(pv[i], ((pv_ok >> i) & 1u) ? a.dv - 4 * u : 0);
+        const int pos = flash_key_pos(r);
+        Vst[(4 * u + 0) * LDV + pos] = static_cast<uint16_t>(w.x & 0xffffu);
+        Vst[(4 * u + 1) * LDV + pos] = static_cast<uint16_t>(w.x >> 16);
+        Vst[(4 * u + 2) * LDV + pos] = static_cast<uint16_t>(w.y & 0xffffu);
+        Vst[(4 * u + 3) * LDV + pos] = static_cast<uint16_t>(w.y >> 16);
+      }
+    }
+  };
+
+  if constexpr (DPS != DP) {  // dimensions [DP, DPS) of the key rows are never written: zero them
+    for (int e = tid; e < KB * LDK; e += 256) Kst[e] = 0;
+  }
+  prefetch(0);
+  for (int b = 0; b < nb; ++b) {
+    __syncthreads();
+    commit();
+    __syncthreads();
+    if (b + 1 < nb) prefetch((b + 1) * KB);
+    const int off = b * KB;
+    if (off <= wrow_hi) {
+      if (off + KB - 1 > wrow_lo)
+        process(std::true_type{}, off);
+      else
+        process(std::false_type{}, off);
+    }
+  }
+
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     float dsum = den[rs];

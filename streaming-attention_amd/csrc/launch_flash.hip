@@ -15,7 +15,15 @@ template <int DP, int DVT, int ES>
 int launch_flash(const sta::FlashArgs& a, int64_t bh, hipStream_t s) {
   const int64_t grid = bh * a.n_tiles;
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
-  hipLaunchKernelGGL((sta::flash_attn_kernel<DP, DVT, 2, ES>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  if constexpr (ES == 4) {
+    hipLaunchKernelGGL((sta::flash_attn_kernel<DP, DVT, 2, 4>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  } else if (a.dtype == STA_F16) {
+    hipLaunchKernelGGL((sta::flash_attn16_kernel<DP, DVT, 2, true>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       s, a);
+  } else {
+    hipLaunchKernelGGL((sta::flash_attn16_kernel<DP, DVT, 2, false>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       s, a);
+  }
   return check_launch();
 }
 
