@@ -502,9 +502,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         if (e < KB * KU) {
           const int r = e / KU, u = e - r * KU;
           const floatx4 f = unit_to_f4<ES>(pk[i], a.dtype, ((pk_ok >> i) & 1u) ? 1.f : 0.f);
-          const uint32_t h0 = pk_bf16(f[0], f[1]), h1 = pk_bf16(f[2], f[3]);
-          const uint32_t l0 = pk_bf16(f[0] - __uint_as_float(h0 << 16), f[1] - __uint_as_float(h0 & 0xffff0000u));
-          const uint32_t l1 = pk_bf16(f[2] - __uint_as_float(h1 << 16), f[3] - __uint_as_float(h1 & 0xffff0000u));
+          uint32_t h0, h1, l0, l1;
+          split_pair(f[0], f[1], h0, l0);
+          split_pair(f[2], f[3], h1, l1);
           *reinterpret_cast<uint2*>(Kh + r * LDKB + 4 * u) = uint2{h0, h1};
           *reinterpret_cast<uint2*>(Kl + r * LDKB + 4 * u) = uint2{l0, l1};
         }
@@ -598,7 +598,13 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   }
 
   // ---- epilogue: add the moment partials, normalise, store ----
+  // The fsplit partials of a row are summed in the order f = 0, 1, ...  Every load of a group of
+  // EPI_GROUP partials is issued before the first sum (a partial past fsplit re-reads the last one and
+  // is dropped; a column past dv reads column 0 and is not stored), so a group costs one round trip.
+  constexpr int EPI_GROUP = DVT <= 4 ? 8 : 32 / DVT;  // at most 128 registers of loads in flight
   const bool raw = a.out_den != nullptr;
+  const int fs = a.fsplit;
+  const int64_t pden_stride = a.low_rows, pnum_stride = a.low_rows * a.low_ld;
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     float dsum = den[rs];
@@ -606,23 +612,46 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     dsum += __shfl_xor(dsum, 32);
     if (!rvalid[rs]) continue;
     const int64_t i = myrow[rs];
+    const float* pd = a.low_den + bh * fs * pden_stride + a.low_off + i;
+    const float* pn = a.low_num + (bh * fs * a.low_rows + a.low_off + i) * a.low_ld;
     float lowd = 0.f;
-    for (int f = 0; f < a.fsplit; ++f) lowd += a.low_den[(bh * a.fsplit + f) * a.low_rows + a.low_off + i];
+    floatx4 lown[DVT];
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) lown[ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int f0 = 0; f0 < fs; f0 += EPI_GROUP) {
+      float gd[EPI_GROUP];
+      floatx4 gn[EPI_GROUP][DVT];
+#pragma unroll
+      for (int j = 0; j < EPI_GROUP; ++j) {
+        const int64_t f = min(f0 + j, fs - 1);
+        gd[j] = __builtin_nontemporal_load(pd + f * pden_stride);
+#pragma unroll
+        for (int ct = 0; ct < DVT; ++ct) {
+          const int c0 = 16 * ct + 4 * lg;
+          gn[j][ct] = __builtin_nontemporal_load(
+              reinterpret_cast<const floatx4*>(pn + f * pnum_stride + (c0 < a.dv ? c0 : 0)));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < EPI_GROUP; ++j) {
+        if (f0 + j < fs) {
+          lowd += gd[j];
+#pragma unroll
+          for (int ct = 0; ct < DVT; ++ct) lown[ct] += gn[j][ct];
+        }
+      }
+    }
     if (raw && lg == 0) a.out_den[bh * a.n + i] = lowd + dsum;
     const float dn = fmaxf(lowd + dsum, a.eps);
 #pragma unroll
     for (int ct = 0; ct < DVT; ++ct) {
       const int c0 = 16 * ct + 4 * lg;
       if (c0 >= a.dv) continue;
-      floatx4 lown = floatx4{0.f, 0.f, 0.f, 0.f};
-      for (int f = 0; f < a.fsplit; ++f)
-        lown += *reinterpret_cast<const floatx4*>(
-            a.low_num + ((bh * a.fsplit + f) * a.low_rows + a.low_off + i) * a.low_ld + c0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int col = c0 + r;
         if (col < a.dv) {
-          const float numv = num[rs][ct][r] + lown[r];
+          const float numv = num[rs][ct][r] + lown[ct][r];
           if (raw)
             static_cast<float*>(a.out)[(bh * a.n + i) * a.dv + col] = numv;
           else

@@ -73,15 +73,26 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2){a, b}, bf16x2));
 }
 
-// 3 VALU per value: packed hi, hi back to fp32 from the packed bits (shift / mask), x - hi, packed lo
+// hi and lo of two values as packed bf16 pairs in 4 VALU: packed hi (v_cvt_pk_bf16_f32), x - hi with
+// one v_dot2_f32_bf16 per value, packed lo.  The dot product of the packed hi pair with the bf16 pair
+// (-1, 0) (or (0, -1)) plus x is x - hi exactly: bf16 products are exact in fp32 and x - hi is
+// representable.  The two pairs are held in scalar registers behind an empty asm: the compiler would
+// otherwise encode (-1, 0) as the inline constant -1.0, which the hardware reads as the 32-bit float
+// (the pair (0, -1)).
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& h, uint32_t& l) {
+  uint32_t c0 = 0x0000BF80u, c1 = 0xBF800000u;
+  asm("" : "+s"(c0));
+  asm("" : "+s"(c1));
+  const bf16x2 hp = __builtin_convertvector((floatx2){a, b}, bf16x2);
+  h = __builtin_bit_cast(uint32_t, hp);
+  l = pk_bf16(__builtin_amdgcn_fdot2_f32_bf16(hp, __builtin_bit_cast(bf16x2, c0), a, false),
+              __builtin_amdgcn_fdot2_f32_bf16(hp, __builtin_bit_cast(bf16x2, c1), b, false));
+}
+
 __device__ __forceinline__ void split_bf16(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
   uint32_t h[4], l[4];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    h[p] = pk_bf16(x[2 * p], x[2 * p + 1]);
-    const float h0 = __uint_as_float(h[p] << 16), h1 = __uint_as_float(h[p] & 0xffff0000u);
-    l[p] = pk_bf16(x[2 * p] - h0, x[2 * p + 1] - h1);
-  }
+  for (int p = 0; p < 4; ++p) split_pair(x[2 * p], x[2 * p + 1], h[p], l[p]);
   hi = __builtin_bit_cast(bf16x8, uint4{h[0], h[1], h[2], h[3]});
   lo = __builtin_bit_cast(bf16x8, uint4{l[0], l[1], l[2], l[3]});
 }

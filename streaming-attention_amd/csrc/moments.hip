@@ -26,9 +26,10 @@
 // the splits.
 //
 // Pipeline.  Two chunk buffers and two partial buffers in LDS, one barrier per chunk.  Iteration c:
-// issue the (unconditional, clamped) 16-byte loads of chunk c+1; query chunk c from buffer c&1; write
-// c's partials; stage chunk c+1 into the other buffer; reduce and store chunk c-1's partials; update
-// the state with chunk c; barrier.  A dependent MFMA waits ~3 issue slots for its accumulator, so both
+// query chunk c from buffer c&1; write c's partials; stage chunk c+1 (in registers since iteration
+// c-1) into the other buffer; issue the (unconditional, clamped) 16-byte loads of chunk c+2 into the
+// same registers, so they have a whole iteration to land; reduce and store chunk c-1's partials;
+// update the state with chunk c; barrier.  A dependent MFMA waits ~3 issue slots for its accumulator, so both
 // phases keep >= 8 independent accumulator chains in flight: the query alternates two accumulator sets
 // by tile, the update walks token steps outermost over all NT tiles.  Operands of the next step are
 // read while the current step's MFMAs issue.  For NT <= 5 two workgroups share a compute unit (two
@@ -594,6 +595,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first);
   mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
+  mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first + MOM_C);
 
   for (int c = 0; c < nchunks; ++c) {
     const int cur = c & 1;
@@ -601,9 +603,6 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
     const float* Qs = smem + cur * BUF;
     const float* Kt = Qs + MOM_C * LDQ;
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
-
-    // prefetch chunk c+1 (unconditional, clamped); staged after the query phase
-    mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, row0 + MOM_C);
 
     // ---- query with the state of all previous chunks: two accumulator sets (tile parity), so 8
     //      independent MFMA chains; tile kt+1's operands are read during tile kt ----
@@ -670,9 +669,11 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
         }
       }
     }
-    // ---- stage chunk c+1 into the other buffer (its loads had the query phase to land) ----
+    // ---- stage chunk c+1 into the other buffer (loaded a whole iteration earlier), then prefetch chunk
+    //      c+2 into the same registers (unconditional, clamped rows) ----
     if (c + 1 < nchunks)
       mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
+    mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, row0 + 2 * MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
