@@ -144,6 +144,25 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
             for a in range(d):
                 for b2 in range(a, d):
                     add_row((a, b2), b2, d, False)
+        # Tiles: first every run of 4 quads that share (b, i2) and take 4 consecutive first factors
+        # i0 = 4k .. 4k+3, then the remaining quads in row order.  In the kernel's update a tile's 16
+        # lanes then read 4 distinct key rows per factor (x[i0] by quad, x[b + s] by slot), the pattern
+        # the swizzled key rows serve without LDS bank conflicts, and the query reads one 16-byte block
+        # x[b..b+3] per token for all 4 quads.
+        runs: Dict[Tuple[int, int, int], List[int]] = {}
+        for idx, qd in enumerate(quads):
+            i0, b, i2 = qd & 255, (qd >> 8) & 255, qd >> 16
+            if i0 != one:
+                runs.setdefault((i2, b, i0 >> 2), []).append(idx)
+        order: List[int] = []
+        for (_, _, k4), idxs in runs.items():
+            if sorted(quads[i] & 255 for i in idxs) == [4 * k4 + t for t in range(4)]:
+                order += sorted(idxs, key=lambda i: quads[i] & 255)
+        taken = set(order)
+        order += [i for i in range(len(quads)) if i not in taken]
+        quads = [quads[i] for i in order]
+        coefs = [coefs[i] for i in order]
+        slot_combos = [c for i in order for c in slot_combos[4 * i: 4 * i + 4]]
         n_tiles = -(-len(quads) // 4)
         pad_quad = one | ((d // 4 * 4) << 8) | (one << 16)  # finite staged values; coefficient 0
         q = np.full(n_tiles * 4, pad_quad, dtype=np.uint32)

@@ -16,10 +16,10 @@
 namespace sta_api {
 namespace {
 
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
-int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
+int launch_full(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT, CG)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT, CG>;
+  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT, CG, FULL>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -27,6 +27,15 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOM_THREADS), smem, s, a);
   return check_launch();
+}
+
+// fp32 rows of exactly the kernel's row width take the instantiation without dummy staging slots
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
+int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
+  if constexpr (ES == 4) {
+    if (sta::mom_full_slots(DBIG, ES, a.d)) return launch_full<NT, DEG3, DBIG, ES, SPLIT, CG, true>(a, bh, s);
+  }
+  return launch_full<NT, DEG3, DBIG, ES, SPLIT, CG, false>(a, bh, s);
 }
 
 }  // namespace

@@ -18,8 +18,12 @@
 //           features of quad lg -- one 16-byte LDS read of the row-major queries gives all four
 //           x[b+s], one more read x[i0].  B = the accumulator itself (see common.hpp).
 //   update: S[f][col] += phi_k(tok)[f] V[tok][col].   A (16 f x 4 tok): lane (li, lg) holds feature li
-//           and, at step ks, token 8 lg + ks; B: V[8 lg + ks][col] with the same token mapping.  With
-//           keys and values stored token-contiguous, two 16-byte reads give a lane its 8 steps.
+//           and, at step ks, token tok(lg, ks) = 4 lg + (ks & 3) + 16 (ks >> 2); B: V[tok(lg, ks)][col]
+//           with the same token mapping.  With keys and values stored token-contiguous, two 16-byte
+//           reads (token blocks lg and lg + 4) give a lane its 8 steps.  A tile's quads share b and take
+//           4 consecutive i0 (feature_tiles), so the 16 lanes of a key read touch 4 rows x 4 token
+//           blocks; with blocks lg and lg + 4 (rather than 2 lg and 2 lg + 1) these reads and the
+//           transposed staging writes run without LDS bank conflicts (measured).
 // Every generated feature value feeds two MFMAs (two 16-column tiles).  The denominator column (the
 // "1" appended to v) is kept by VALU per feature, in registers.  The 4 waves' query partials are
 // summed in LDS in a fixed order (deterministic) and stored per feature split; the block kernel adds
@@ -52,6 +56,11 @@ constexpr int MOM_C = 32;    // tokens per chunk
 constexpr int MOM_LDT = 36;  // token stride of the transposed Kt / Vt rows
 constexpr int MOM_LDR = 32;  // token stride of a partial column
 static_assert(MOM_C <= MOM_LDT, "the bf16 value planes [2][CG][MOM_C] fit in the fp32 rows [CG][MOM_LDT]");
+
+// bf16 offset of (column c, token t) in a value plane of the split-product update (see mom_store).
+__host__ __device__ constexpr int vps_off(int c, int t) {
+  return c * MOM_C + 8 * (((t >> 2) & 3) ^ ((c >> 1) & 3)) + (t & 3) + 4 * (t >> 4);
+}
 
 // Offset of token t of partial column col.  The 4-token groups of a column are permuted by
 // (col / 2) mod 8, so the 16 columns a 16-byte access touches at one token group fall on 16 distinct
@@ -170,15 +179,20 @@ __device__ __forceinline__ MomSlots<DBIG, CG> mom_slots(const MomArgs& a, int co
 
 __device__ __forceinline__ int clamp_row(int row, int n) { return min(max(row, 0), n - 1); }
 
-template <bool DBIG, int ES, int CG>
+// Whether every staging slot of every thread is in use (mom_slots): fp32 rows of exactly 64 (or 128)
+// elements; the value units always fill the CG columns for fp32.
+__host__ __device__ constexpr bool mom_full_slots(bool dbig, int es, int d) { return es == 4 && d == (dbig ? 128 : 64); }
+
+// MASK = false: the caller guarantees every row of the chunk lies in the sequence (no clamping).
+template <bool DBIG, int ES, int CG, bool MASK = true>
 __device__ __forceinline__ void mom_load(MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                          const char* qh, const char* kh, const char* vh, int row0) {
   const uint32_t qrow = static_cast<uint32_t>(a.d * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
   const int ktok = row0 + (threadIdx.x & (MOM_C - 1));
-  const uint32_t krow = static_cast<uint32_t>(clamp_row(ktok, a.n));
+  const uint32_t krow = static_cast<uint32_t>(MASK ? clamp_row(ktok, a.n) : ktok);
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
-    const uint32_t r = static_cast<uint32_t>(clamp_row(row0 + sl.q_tok[j], a.n));
+    const uint32_t r = static_cast<uint32_t>(MASK ? clamp_row(row0 + sl.q_tok[j], a.n) : row0 + sl.q_tok[j]);
     st.q[j] = *reinterpret_cast<const uint4*>(qh + r * qrow + sl.q_off[j]);
     st.k[j] = *reinterpret_cast<const uint4*>(kh + krow * qrow + sl.k_off[j]);
   }
@@ -215,9 +229,15 @@ __device__ __forceinline__ void unit_floats(const uint4& u, int dtype, float (&f
   }
 }
 
-// SPLIT: the values go to LDS as bf16 hi / lo planes [CG][32 tokens] (split once per workgroup for the
-// split-product update) in place of the fp32 Vt rows; they fit in Vt's space.
-template <bool DBIG, int ES, int CG, bool SPLIT = false>
+// SPLIT: the values go to LDS as bf16 hi / lo planes (split once per workgroup for the split-product
+// update) in place of the fp32 Vt rows; they fit in Vt's space.  Plane layout (vps_off): column c is a
+// row of 32 bf16 in 4 blocks of 8; block g ^ ((c >> 1) & 3) holds the tokens 4 g + (j & 3) + 16 (j >> 2),
+// j = 0..7, in the token order of the update's contraction, so a lane's 8 tokens are one 16-byte read.
+// The XOR spreads the update's reads (16 columns x 4 blocks) over all banks, and the staging writes
+// (32 tokens of one column per half-wave) stay within one row: both measured free of bank conflicts.
+// FULL: every staging slot of the thread is in use (mom_full_slots), so no slot is routed to the dummy.
+// MASK = false: every row of the chunk lies in the sequence (no zeroing of outside rows).
+template <bool DBIG, int ES, int CG, bool SPLIT = false, bool FULL = false, bool MASK = true>
 __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                           float* buf, int dummy_rel, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
@@ -227,16 +247,16 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const Mo
   float* dmy = buf + dummy_rel;  // 8 floats nobody reads
   const int tid = threadIdx.x;
   const int tok = tid & (MOM_C - 1);
-  const bool tok_ok = row0 + tok >= 0 && row0 + tok < a.n;
+  const bool tok_ok = !MASK || (row0 + tok >= 0 && row0 + tok < a.n);
   const float kok = tok_ok ? 1.f : 0.f;
   constexpr bool wide = ES == 2;  // 8 elements per unit
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
     const int row = row0 + sl.q_tok[j];
-    const float sc = (sl.q_use[j] && row >= 0 && row < a.n) ? a.scale : 0.f;
+    const float sc = ((FULL || sl.q_use[j]) && (!MASK || (row >= 0 && row < a.n))) ? a.scale : 0.f;
     float f[8];
     unit_floats<ES>(st.q[j], a.dtype, f);
-    float* qd = sl.q_use[j] ? Qs + sl.q_lds[j] : dmy;
+    float* qd = (FULL || sl.q_use[j]) ? Qs + sl.q_lds[j] : dmy;
     *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
     if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
     unit_floats<ES>(st.k[j], a.dtype, f);
@@ -244,7 +264,7 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const Mo
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       if (m < 4 || wide) {
-        float* p = kd >= 0 ? Kt + (kd + m) * MOM_LDT + tok : dmy + m;
+        float* p = (FULL || kd >= 0) ? Kt + (kd + m) * MOM_LDT + tok : dmy + m;
         *p = f[m] * kok;
       }
     }
@@ -261,15 +281,15 @@ __device__ __forceinline__ void mom_store(const MomStage<DBIG, CG>& st, const Mo
           const float x = f[m] * kok;
           const __bf16 h = static_cast<__bf16>(x);
           const __bf16 l = static_cast<__bf16>(x - static_cast<float>(h));
-          if (sl.v_col[j] >= 0) {
-            vh[(sl.v_col[j] + m) * MOM_C + tok] = h;
-            vh[(CG + sl.v_col[j] + m) * MOM_C + tok] = l;
+          if (FULL || sl.v_col[j] >= 0) {
+            vh[vps_off(sl.v_col[j] + m, tok)] = h;
+            vh[CG * MOM_C + vps_off(sl.v_col[j] + m, tok)] = l;
           } else {
             reinterpret_cast<__bf16*>(dmy + m)[0] = h;
             reinterpret_cast<__bf16*>(dmy + m)[1] = l;
           }
         } else {
-          float* p = sl.v_col[j] >= 0 ? Vt + (sl.v_col[j] + m) * MOM_LDT + tok : dmy + m;
+          float* p = (FULL || sl.v_col[j] >= 0) ? Vt + (sl.v_col[j] + m) * MOM_LDT + tok : dmy + m;
           *p = f[m] * kok;
         }
       }
@@ -313,7 +333,7 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
 
 // Per-lane feature offsets of a wave's NT tiles (constant over the sequence).  Query side: columns of
 // x[i0], x[b..b+3], x[i2] of quad lg in the row-major queries.  Update side: Kt rows of feature li plus
-// the token offset 8 lg, and the key-side coefficient of feature li.
+// the token offset 4 lg (token blocks lg and lg + 4), and the key-side coefficient of feature li.
 template <int NT, bool DEG3>
 struct MomLane {
   int qa[NT], qb[NT], qc[DEG3 ? NT : 1];
@@ -331,9 +351,9 @@ __device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t 
     m.qb[kt] = static_cast<int>((pq >> 8) & 255u);
     if (DEG3) m.qc[DEG3 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
     const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
-    m.ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 8 * lg;
-    m.kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 8 * lg;
-    if (DEG3) m.kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 8 * lg;
+    m.ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 4 * lg;
+    m.kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 4 * lg;
+    if (DEG3) m.kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 4 * lg;
     m.kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
   }
   return m;
@@ -346,19 +366,19 @@ __device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t 
 template <int NT, int CT, bool DEG3, bool DEN, class Mid>
 __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, const float* Kt, const float* Vt,
                                            const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
-  floatx4 vv[2][CT];  // values of tokens 8 lg + 0..3 and 8 lg + 4..7
+  floatx4 vv[2][CT];  // values of tokens 4 lg + 0..3 and 16 + 4 lg + 0..3
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg);
-    vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 8 * lg + 4);
+    vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg);
+    vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg + 16);
   }
   floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
   auto uload = [&](int h) {
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
-      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 4 * h);
-      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 4 * h);
-      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 4 * h);
+      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
+      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
+      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 16 * h);
     }
   };
   uload(0);
@@ -400,8 +420,8 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 }
 
 // Split-bf16 form of mom_update: one 16x16x32 bf16 product covers the 32 tokens of the chunk.  A (16 f x
-// 32 tok): lane (li, lg) holds feature li of the tile for tokens 8 lg + j, j = 0..7 (the fp32 update's
-// A values of its 8 steps); B: V[8 lg + j][col].  The feature values and the values are split into
+// 32 tok): lane (li, lg) holds feature li of the tile for tokens tok(lg, j), j = 0..7 (the fp32 update's
+// A values of its 8 steps); B: V[tok(lg, j)][col].  The feature values and the values are split into
 // bf16 hi + lo, and S += A_hi B_lo + A_lo B_hi + A_hi B_hi (terms outermost, so the 2 NT accumulators
 // are independent chains).  The denominator sums the fp32 feature values as before.
 template <int NT, int CT, bool DEG3, bool DEN, class Mid>
@@ -413,19 +433,18 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
-      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 4 * h);
-      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 4 * h);
-      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 4 * h);
+      fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
+      fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
+      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 16 * h);
     }
-  // the staged bf16 planes (mom_store<..., true>): row 16 ct + li, tokens 8 lg .. 8 lg + 7; the 64 lanes'
-  // 16-byte reads tile one contiguous 1 KiB block per plane
+  // the staged bf16 planes (mom_store<..., true>, vps_off): column 16 ct + li, tokens tok(lg, 0..7)
   constexpr int CG = 16 * CT;
   const __bf16* vplane = reinterpret_cast<const __bf16*>(Vt);
   bf16x8 vh[CT], vl[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + (16 * ct + li) * MOM_C + 8 * lg);
-    vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + (CG + 16 * ct + li) * MOM_C + 8 * lg);
+    vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + vps_off(16 * ct + li, 4 * lg));
+    vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + CG * MOM_C + vps_off(16 * ct + li, 4 * lg));
   }
   mid();
   __builtin_amdgcn_sched_barrier(0);
@@ -547,14 +566,14 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
 // The kernel body for one workgroup (head bh, feature split fs, column group cs) with NT tiles per wave
 // out of the NTS the split table holds per wave.  DEN: this workgroup also keeps the denominator column
 // (only column group 0 does; the others would compute bit-identical values).
-template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT, int CG>
+template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT, int CG, bool FULL>
 __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int BUF = mom_buf_floats(DBIG, CG);
   constexpr int RED = mom_red_floats(CG);
   constexpr int CT = CG / 16;     // 16-column tiles per wave
   constexpr int TT = MOM_C / 16;  // 16-token tiles per chunk (query)
-  constexpr int KS = MOM_C / 4;   // update steps per chunk (token 8 lg + ks)
+  constexpr int KS = MOM_C / 4;   // update steps per chunk (token tok(lg, ks))
   static_assert(KS == 8, "update token mapping assumes 32-token chunks");
   extern __shared__ float smem[];
   float* red_all = smem + 2 * BUF;
@@ -593,7 +612,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   __syncthreads();
   MomStage<DBIG, CG> pre;
   mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first);
-  mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem, dummy_abs, first);
+  mom_store<DBIG, ES, CG, SPLIT, FULL>(pre, sl, a, smem, dummy_abs, first);
   __syncthreads();
   mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, first + MOM_C);
 
@@ -671,9 +690,19 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
     }
     // ---- stage chunk c+1 into the other buffer (loaded a whole iteration earlier), then prefetch chunk
     //      c+2 into the same registers (unconditional, clamped rows) ----
-    if (c + 1 < nchunks)
-      mom_store<DBIG, ES, CG, SPLIT>(pre, sl, a, smem + (cur ^ 1) * BUF, dummy_abs - (cur ^ 1) * BUF, row0 + MOM_C);
-    mom_load<DBIG, ES, CG>(pre, sl, a, qh, kh, vh, row0 + 2 * MOM_C);
+    // (interior chunks, every row inside the sequence, skip the clamping and zeroing: a uniform branch)
+    if (c + 1 < nchunks) {
+      float* nb = smem + (cur ^ 1) * BUF;
+      const int nd = dummy_abs - (cur ^ 1) * BUF;
+      if (row0 + MOM_C >= 0 && row0 + 2 * MOM_C <= n)
+        mom_store<DBIG, ES, CG, SPLIT, FULL, false>(pre, sl, a, nb, nd, row0 + MOM_C);
+      else
+        mom_store<DBIG, ES, CG, SPLIT, FULL, true>(pre, sl, a, nb, nd, row0 + MOM_C);
+    }
+    if (row0 + 2 * MOM_C >= 0 && row0 + 3 * MOM_C <= n)
+      mom_load<DBIG, ES, CG, false>(pre, sl, a, qh, kh, vh, row0 + 2 * MOM_C);
+    else
+      mom_load<DBIG, ES, CG, true>(pre, sl, a, qh, kh, vh, row0 + 2 * MOM_C);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- update with chunk c; the previous chunk's partials are reduced and stored under the first
@@ -725,7 +754,8 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
 // CG: value columns per workgroup, 32 or 64.  With 64 the feature values of a token are generated and
 // split once for 4 column tiles instead of twice for 2 (the 32-column workgroups of a head each do
 // their own), at one workgroup per compute unit (124 KiB of LDS).
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
+// FULL: mom_full_slots(DBIG, ES, a.d) (the host picks the instantiation).
+template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
 __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
@@ -734,14 +764,14 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void mome
   if (MIX && a.mixed && fs >= a.fsplit / 2) {
     constexpr int NTL = MIX ? NT - 1 : NT;
     if (cs == 0)
-      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT, CG>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
     else
-      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT, CG>(a, bh, fs, cs);
+      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
   } else {
     if (cs == 0)
-      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT, CG>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
     else
-      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT, CG>(a, bh, fs, cs);
+      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
   }
 }
 
