@@ -56,8 +56,9 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *   chunk c covers rows [c*chunk - shift, (c+1)*chunk - shift); chunk must be sta_moment_chunk(d).
  *   feat_quads [fsplit][4][wave_tiles][4], feat_coef [fsplit][4][wave_tiles][16]: the symmetric monomial
  *     basis in tiles of 4 quads, wave_tiles tiles for each of the 4 waves of each feature split (padded
- *     with coefficient-0 tiles).  A quad packs i0 | b<<8 | i2<<16 (b a multiple of 4, at most d) and
- *     holds the features x[i0] x[b+s] x[i2], s = 0..3, of [x_0..x_{D-1}, 1, 0, 0, 0]; feat_coef is the
+ *     with coefficient-0 tiles).  A quad packs i0 | b<<8 | i2<<16 | i3<<24 (b a multiple of 4, at most d;
+ *     unused factors = d) and holds the features x[i0] x[b+s] x[i2] x[i3], s = 0..3, of
+ *     [x_0..x_{D-1}, 1, 0, 0, 0] (degree 4 needs d <= 64); feat_coef is the
  *     key-side coefficient 1/prod(alpha!) of each feature (0 for padding).  wave_tiles must be a count
  *     the library is built for (sta_moment_wave_tiles).
  *   q and k rows are d elements long and v rows ldv (a multiple of 32, >= dv); rows are read in
@@ -132,8 +133,8 @@ int sta_decode_layout(int d, int dv, int* dk, int* ldv);
 /*
  * Moment part of a decode query: part_num[s][p][c] = sum over features f of split p of
  * phi_q(scale*q_s)[f] state_num[s][f][c] (part_den likewise), splits = feature splits per stream.
- * feat_index [F]: factors of feature f packed i0 | i1 << 8 | i2 << 16 into x = [scale*q, 1] (index d is
- * the constant 1).  Replaces TaylorMomentSketch.query (streaming_taylor_coreset_attention.py:282-296).
+ * feat_index [F]: factors of feature f packed i0 | i1 << 8 | i2 << 16 | i3 << 24 into x = [scale*q, 1]
+ * (index d is the constant 1 and fills the unused factors).  Replaces TaylorMomentSketch.query (streaming_taylor_coreset_attention.py:282-296).
  */
 int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv, float scale, const float* state_num,
                        const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* part_num,
@@ -210,7 +211,8 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *     (segment means; fp32 inputs only), NULL otherwise.
  *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
  *   products: STA_PRODUCTS_FP32 or STA_PRODUCTS_SPLIT_BF16 for the logits q.k and the weighted value
- *     sums (see sta_moments); weights, exponentials and all sums stay fp32.
+ *     sums (see sta_moments); weights, exponentials and all sums stay fp32.  Degree 4 needs
+ *     STA_PRODUCTS_FP32 (STA_ERR_UNSUPPORTED otherwise).
  *   out: [BH][N][Dv] in out_dtype.
  *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator
  *     and out_den [BH][N] the denominator, unnormalised (the low_num/low_den pair of

@@ -315,8 +315,9 @@ def prefill(
 
     if residual_products is not None:
         k2_products = int(residual_products)
-    elif semantics in EXACT_SEMANTICS or (n_nodes_arg == 0 and n_rep_arg == 0):
-        k2_products = _native.PRODUCTS_FP32  # no coreset item: the result is exact attention
+    elif semantics in EXACT_SEMANTICS or (n_nodes_arg == 0 and n_rep_arg == 0) or degree > 3:
+        # no coreset item (the result is exact attention), or degree 4 (the fp32-product kernel's Taylor)
+        k2_products = _native.PRODUCTS_FP32
     else:
         k2_products = RESIDUAL_PRODUCTS
 

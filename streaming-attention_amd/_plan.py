@@ -77,9 +77,9 @@ MOM_MAX_WAVE_TILES = 16  # largest per-wave tile count the kernel is instantiate
 @dataclass(frozen=True)
 class FeatureTiles:
     """The monomial basis through `degree` laid out for the moment kernel: tiles of 16 features made of
-    4 quads; quad q of tile t is quads[4 t + q] (packed i0 | b << 8 | i2 << 16) and holds the features
-    x[i0] * x[b + s] * x[i2], s = 0..3, with b a multiple of 4 and x[d] = 1 (so i0 = i2 = d reduces the
-    degree).  coef[16 t + 4 q + s] is the key-side coefficient 1/prod(alpha!) of feature s of the quad,
+    4 quads; quad q of tile t is quads[4 t + q] (packed i0 | b << 8 | i2 << 16 | i3 << 24) and holds the
+    features x[i0] * x[b + s] * x[i2] * x[i3], s = 0..3, with b a multiple of 4 and x[d] = 1 (so
+    i0 = i2 = i3 = d reduces the degree).  coef[16 t + 4 q + s] is the key-side coefficient 1/prod(alpha!) of feature s of the quad,
     0 where b + s is not a valid last factor (padding; x[b + s] is then 0 or the constant 1).
 
     Same set of monomials as the reference's feature map (fast_article_attention.py:151-181,
@@ -98,8 +98,9 @@ class FeatureTiles:
 
 
 def feature_tiles(d: int, degree: int) -> FeatureTiles:
-    if degree > 3 or d > 252:
-        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 252")
+    if degree > 4 or d > 252 or (degree == 4 and d > 64):
+        raise NotImplementedError("the HIP feature map supports degree <= 3 with D <= 252 and degree 4 with "
+                                  "D <= 64")
 
     def build():
         one = d
@@ -117,6 +118,7 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
                 return
             i0 = prefix[0] if len(prefix) >= 1 else one
             i2 = prefix[1] if len(prefix) >= 2 else one
+            i3 = prefix[2] if len(prefix) >= 3 else one
             for b in range((lo // 4) * 4, last + 1, 4):
                 cs = []
                 for s in range(4):
@@ -132,7 +134,7 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
                     else:
                         cs.append(0.0)
                         slot_combos.append(None)
-                quads.append(i0 | (b << 8) | (i2 << 16))
+                quads.append(i0 | (b << 8) | (i2 << 16) | (i3 << 24))
                 coefs.append(cs)
 
         # degree 0 and 1: x_c for c < d plus the constant, all with prefix ()
@@ -144,18 +146,23 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
             for a in range(d):
                 for b2 in range(a, d):
                     add_row((a, b2), b2, d, False)
-        # Tiles: first every run of 4 quads that share (b, i2) and take 4 consecutive first factors
+        if degree >= 4:
+            for a in range(d):
+                for b2 in range(a, d):
+                    for b3 in range(b2, d):
+                        add_row((a, b2, b3), b3, d, False)
+        # Tiles: first every run of 4 quads that share (b, i2, i3) and take 4 consecutive first factors
         # i0 = 4k .. 4k+3, then the remaining quads in row order.  In the kernel's update a tile's 16
-        # lanes then read 4 distinct key rows per factor (x[i0] by quad, x[b + s] by slot), the pattern
-        # the swizzled key rows serve without LDS bank conflicts, and the query reads one 16-byte block
+        # lanes then read 4 distinct key rows per factor (x[i0] by quad, x[b + s] by slot), a pattern the
+        # transposed key rows serve without LDS bank conflicts, and the query reads one 16-byte block
         # x[b..b+3] per token for all 4 quads.
-        runs: Dict[Tuple[int, int, int], List[int]] = {}
+        runs: Dict[Tuple[int, int, int, int], List[int]] = {}
         for idx, qd in enumerate(quads):
-            i0, b, i2 = qd & 255, (qd >> 8) & 255, qd >> 16
+            i0, b, i2, i3 = qd & 255, (qd >> 8) & 255, (qd >> 16) & 255, qd >> 24
             if i0 != one:
-                runs.setdefault((i2, b, i0 >> 2), []).append(idx)
+                runs.setdefault((i3, i2, b, i0 >> 2), []).append(idx)
         order: List[int] = []
-        for (_, _, k4), idxs in runs.items():
+        for (_, _, _, k4), idxs in runs.items():
             if sorted(quads[i] & 255 for i in idxs) == [4 * k4 + t for t in range(4)]:
                 order += sorted(idxs, key=lambda i: quads[i] & 255)
         taken = set(order)
@@ -164,7 +171,7 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
         coefs = [coefs[i] for i in order]
         slot_combos = [c for i in order for c in slot_combos[4 * i: 4 * i + 4]]
         n_tiles = -(-len(quads) // 4)
-        pad_quad = one | ((d // 4 * 4) << 8) | (one << 16)  # finite staged values; coefficient 0
+        pad_quad = one | ((d // 4 * 4) << 8) | (one << 16) | (one << 24)  # finite staged values; coefficient 0
         q = np.full(n_tiles * 4, pad_quad, dtype=np.uint32)
         c = np.zeros(n_tiles * 16, dtype=np.float32)
         q[: len(quads)] = np.asarray(quads, dtype=np.uint32)
@@ -191,19 +198,19 @@ def reference_feature_order(d: int, degree: int) -> Dict[Tuple[int, ...], int]:
 
 
 def feature_index(d: int, degree: int) -> np.ndarray:
-    """uint32 [F]: the factors of reference feature f packed i0 | i1 << 8 | i2 << 16, indices into
+    """uint32 [F]: the factors of reference feature f packed i0 | i1 << 8 | i2 << 16 | i3 << 24, indices into
     x = [x_0 .. x_{d-1}, 1] (index d is the constant 1 filling the unused factors)."""
 
     def build():
         order = reference_feature_order(d, degree)
         out = np.zeros(len(order), dtype=np.uint32)
         for combo, f in order.items():
-            idx = list(combo) + [d] * (3 - len(combo))
-            out[f] = idx[0] | (idx[1] << 8) | (idx[2] << 16)
+            idx = list(combo) + [d] * (4 - len(combo))
+            out[f] = idx[0] | (idx[1] << 8) | (idx[2] << 16) | (idx[3] << 24)
         return out
 
-    if degree > 3 or d > 255:
-        raise NotImplementedError("the HIP feature map supports degree <= 3 and D <= 255")
+    if degree > 4 or d > 255:
+        raise NotImplementedError("the HIP feature map supports degree <= 4 and D <= 255")
     return _cached(("findex", d, degree), build)
 
 

@@ -159,9 +159,9 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
   a.ldo = 32 * ((dv + 31) / 32);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (columns == 64) return dispatch_moments<true, 64>(a, bh, s, wave_tiles, degree >= 3);
-  return products == STA_PRODUCTS_SPLIT_BF16 ? dispatch_moments<true, 32>(a, bh, s, wave_tiles, degree >= 3)
-                                             : dispatch_moments<false, 32>(a, bh, s, wave_tiles, degree >= 3);
+  if (columns == 64) return dispatch_moments<true, 64>(a, bh, s, wave_tiles, moment_extra_factors(degree));
+  return products == STA_PRODUCTS_SPLIT_BF16 ? dispatch_moments<true, 32>(a, bh, s, wave_tiles, moment_extra_factors(degree))
+                                             : dispatch_moments<false, 32>(a, bh, s, wave_tiles, moment_extra_factors(degree));
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
@@ -185,7 +185,7 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
   a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
-  return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, degree >= 3);
+  return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, moment_extra_factors(degree));
 }
 
 int sta_decode_layout(int d, int dv, int* dk, int* ldv) {
@@ -362,6 +362,7 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   a.node_w = node_w; a.rep_k = rep_k; a.rep_v = rep_v; a.n_rep = n_rep; a.out = out; a.out_dtype = out_dtype; a.out_den = out_den;
   a.ldqk = ld_qk; a.ldvr = ld_v; a.ldrk = ld_rep_k; a.ldrv = ld_rep_v;
   a.split = products == STA_PRODUCTS_SPLIT_BF16 ? 1 : 0;
+  if (a.split && degree > 3) return STA_ERR_UNSUPPORTED;  // the split-product kernel's Taylor stops at 3
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f32 = dtype == STA_F32;
   if (d <= 16) return f32 ? dispatch_dvt<16, 4>(a, bh, s) : dispatch_dvt<16, 2>(a, bh, s);

@@ -33,7 +33,7 @@ inline bool dtype_ok(int dt) { return dt == STA_F32 || dt == STA_BF16 || dt == S
 
 constexpr int kMaxD = 128;
 constexpr int kMaxDv = 256;
-constexpr int kMaxDegree = 3;
+constexpr int kMaxDegree = 4;
 constexpr int kTileRows = 128;
 
 // Per-wave tile counts the moment kernels are instantiated for, per (degree 3, d > 64).  Every entry
@@ -42,15 +42,17 @@ constexpr int kNtD2[] = {2, 4, 5, 9, 16};
 constexpr int kNtD3[] = {4, 8, 16};
 constexpr int kNtBigD2[] = {5, 16};
 constexpr int kNtBigD3[] = {4, 16};
+constexpr int kNtD4[] = {4, 8, 16};  // degree 4: d <= 64 only
 
-// X(NT, DEG3, DBIG) for every instantiated moment configuration.
+// X(NT, NX, DBIG) for every instantiated moment configuration; NX = extra factors per feature quad
+// (0: degree <= 2, 1: degree 3, 2: degree 4).
 #define STA_MOMENT_CONFIGS(X)                                                                       \
-  X(2, false, false) X(4, false, false) X(5, false, false) X(9, false, false) X(16, false, false)   \
-  X(4, true, false) X(8, true, false) X(16, true, false) X(5, false, true) X(16, false, true)       \
-  X(4, true, true) X(16, true, true)
+  X(2, 0, false) X(4, 0, false) X(5, 0, false) X(9, 0, false) X(16, 0, false)                       \
+  X(4, 1, false) X(8, 1, false) X(16, 1, false) X(5, 0, true) X(16, 0, true)                        \
+  X(4, 1, true) X(16, 1, true) X(4, 2, false) X(8, 2, false) X(16, 2, false)
 
-// X(NT, DEG3, DBIG) of the 64-column (split-product) moment kernels.
-#define STA_MOMENT_CONFIGS_64(X) X(5, false, false)
+// X(NT, NX, DBIG) of the 64-column (split-product) moment kernels.
+#define STA_MOMENT_CONFIGS_64(X) X(5, 0, false)
 
 template <size_t L>
 int next_nt(const int (&tab)[L], int want) {
@@ -65,20 +67,25 @@ inline bool moment_columns64_ok(int d, int degree, int dv, int wave_tiles, int p
   return products == STA_PRODUCTS_SPLIT_BF16 && d <= 64 && degree <= 2 && dv > 32 && dv <= 64 && wave_tiles == 5;
 }
 
+// extra factors per feature quad of a degree (the NX of the moment kernels)
+inline int moment_extra_factors(int degree) { return degree <= 2 ? 0 : degree - 2; }
+
 inline int moment_wave_tiles(int d, int degree, int want) {
   if (want < 1) want = 1;
-  const bool deg3 = degree >= 3, big = d > 64;
-  if (!big) return deg3 ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
-  return deg3 ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
+  const int nx = moment_extra_factors(degree);
+  const bool big = d > 64;
+  if (nx >= 2) return big ? -1 : next_nt(kNtD4, want);
+  if (!big) return nx ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
+  return nx ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
 }
 
 // launch_moments.hip, one object per (SPLIT, CG): the prefill moment scan (moments_kernel) for wave-tile
 // count nt, with fp32 (SPLIT false) or split-bf16 (SPLIT true) matrix-core products and CG value columns
 // per workgroup (64: split products, STA_MOMENT_CONFIGS_64 only).
 template <bool SPLIT, int CG>
-int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
+int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
-int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3);
+int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx);
 // launch_block.hip, one object per (DP, DVT, ES): the residual / combine kernel (block_attn_kernel) for
 // padded key width DP, value-column tile count DVT and element size ES.
 template <int DP, int DVT, int ES>

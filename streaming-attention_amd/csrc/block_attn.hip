@@ -88,18 +88,22 @@ __device__ __forceinline__ int64_t residual_start(int64_t i, int mode, int block
 // The logits come out in base 2: the staged queries carry scale * log2(e), so y = x log2(e) for the
 // natural logit x, exp(x) = exp2(y) on the hardware exp2 (about 1 ulp; the fused residual needs the
 // difference exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding)
-// and the Taylor truncation sum_{r<=deg} x^r / r! (deg <= 3) is the Horner form in y,
-// 1 + y (k1 + y (k2 + y k3)) with k_r = (ln 2)^r / r! for r <= deg and 0 above: three fused
-// multiply-adds for every degree, within a few ulp of the reference's term-by-term sum.
+// and the Taylor truncation sum_{r<=deg} x^r / r! (deg <= 4) is the Horner form in y,
+// 1 + y (k1 + y (k2 + y (k3 + y k4))) with k_r = (ln 2)^r / r! for r <= deg and 0 above, within a few
+// ulp of the reference's term-by-term sum.  D4: the fp32-product kernel, which serves degree 4, takes
+// the fourth fused multiply-add; the split-product kernel stops at degree 3 (three for every degree;
+// sta_block_attention rejects split products with degree 4).
 struct TaylorCoef2 {
-  float k1, k2, k3;
+  float k1, k2, k3, k4;
 };
 __host__ __device__ inline TaylorCoef2 taylor_coef2(int deg) {
   return TaylorCoef2{deg >= 1 ? 0.693147180560f : 0.f, deg >= 2 ? 0.240226506959f : 0.f,
-                     deg >= 3 ? 0.0555041086648f : 0.f};
+                     deg >= 3 ? 0.0555041086648f : 0.f, deg >= 4 ? 0.00961812910763f : 0.f};
 }
+template <bool D4>
 __device__ __forceinline__ float taylor2(float y, const TaylorCoef2& c) {
-  return fmaf(y, fmaf(y, fmaf(y, c.k3, c.k2), c.k1), 1.0f);
+  const float t3 = D4 ? fmaf(y, c.k4, c.k3) : c.k3;
+  return fmaf(y, fmaf(y, fmaf(y, t3, c.k2), c.k1), 1.0f);
 }
 constexpr float LOG2E = 1.44269504f;
 
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           const int i = myrow[rs];
           const float yv = X[rs][r];
           const float ex = __builtin_amdgcn_exp2f(fminf(yv, ymax));
-          const float tp = taylor2(yv, tc);
+          const float tp = taylor2<!SPLIT>(yv, tc);
           float p;
           if constexpr (FULL) {
             p = (ex - tp) * w;  // rows outside the sequence have zero queries and are never stored

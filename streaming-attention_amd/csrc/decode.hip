@@ -45,7 +45,7 @@ struct DecMomArgs {
   const float* state_den;  // [S][n_feat]
   int n_feat;
   int ldm;                  // a multiple of 32
-  const uint32_t* rowfeat;  // [n_feat] factors i0 | i1 << 8 | i2 << 16 of x = [s q, 1] (index d = 1)
+  const uint32_t* rowfeat;  // [n_feat] factors i0 | i1 << 8 | i2 << 16 | i3 << 24 of x = [s q, 1] (index d = 1)
   int splits;
   int rows_per_split;
   float* part_num;  // [S][splits][ldm]
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_moments_kernel(const DecMo
         S[u] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(sn + static_cast<int64_t>(rr) * a.ldm));
         D[u] = __builtin_nontemporal_load(sd + rr);
         const uint32_t pf = a.rowfeat[rr];
-        const float ph = xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u];
+        const float ph = xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u] * xs[pf >> 24];
         phi[u] = row < f1 ? ph : 0.f;
       }
 #pragma unroll
@@ -188,13 +188,14 @@ __device__ __forceinline__ float dec_dot(const floatx4 (&x)[KC], const floatx4 (
 // (c1..c3 = [deg >= r] / r!): the residual exp - exp_{<=t} and the buffered tokens' exp need 1e-5
 // relative, not the reference's term-by-term rounding.
 struct DecTaylor {
-  float c1, c2, c3;
+  float c1, c2, c3, c4;
 };
 __device__ __forceinline__ DecTaylor dec_taylor(int deg) {
-  return DecTaylor{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 0.5f : 0.f, deg >= 3 ? 0.166666672f : 0.f};
+  return DecTaylor{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 0.5f : 0.f, deg >= 3 ? 0.166666672f : 0.f,
+                   deg >= 4 ? 0.0416666679f : 0.f};
 }
 __device__ __forceinline__ float dec_tp(float z, const DecTaylor& t) {
-  return fmaf(z, fmaf(z, fmaf(z, t.c3, t.c2), t.c1), 1.f);
+  return fmaf(z, fmaf(z, fmaf(z, fmaf(z, t.c4, t.c3), t.c2), t.c1), 1.f);
 }
 __device__ __forceinline__ float dec_exp(float z) { return __builtin_amdgcn_exp2f(z * 1.44269504f); }
 

@@ -1,15 +1,15 @@
 // Launches of the in-place moment accumulation into a decode state (moment_accumulate_kernel), one
-// instantiation per wave-tile count, degree-3 flag, d > 64 flag and element size.
+// instantiation per wave-tile count, extra-factor count (NX), d > 64 flag and element size.
 #include "api_common.hpp"
 #include "moments.hip"
 
 namespace sta_api {
 namespace {
 
-template <int NT, bool DEG3, bool DBIG, int ES>
+template <int NT, int NX, bool DBIG, int ES>
 int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_acc_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moment_accumulate_kernel<NT, DEG3, DBIG, ES>;
+  auto fn = sta::moment_accumulate_kernel<NT, NX, DBIG, ES>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -21,10 +21,10 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
 
 }  // namespace
 
-int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
+int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx) {
   const bool big = a.d > 64;
 #define STA_CASE(NT, D3, BIG)                                                                       \
-  if (nt == NT && deg3 == D3 && big == BIG)                                                         \
+  if (nt == NT && nx == D3 && big == BIG)                                                         \
     return a.esize == 4 ? launch<NT, D3, BIG, 4>(a, bh, s) : launch<NT, D3, BIG, 2>(a, bh, s);
   STA_MOMENT_CONFIGS(STA_CASE)
 #undef STA_CASE

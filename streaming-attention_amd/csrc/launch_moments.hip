@@ -16,10 +16,10 @@
 namespace sta_api {
 namespace {
 
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
+template <int NT, int NX, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
 int launch_full(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_smem_floats(DBIG, NT, CG)) * sizeof(float);
-  auto fn = sta::moments_kernel<NT, DEG3, DBIG, ES, SPLIT, CG, FULL>;
+  auto fn = sta::moments_kernel<NT, NX, DBIG, ES, SPLIT, CG, FULL>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -30,21 +30,21 @@ int launch_full(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
 }
 
 // fp32 rows of exactly the kernel's row width take the instantiation without dummy staging slots
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG>
+template <int NT, int NX, bool DBIG, int ES, bool SPLIT, int CG>
 int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   if constexpr (ES == 4) {
-    if (sta::mom_full_slots(DBIG, ES, a.d)) return launch_full<NT, DEG3, DBIG, ES, SPLIT, CG, true>(a, bh, s);
+    if (sta::mom_full_slots(DBIG, ES, a.d)) return launch_full<NT, NX, DBIG, ES, SPLIT, CG, true>(a, bh, s);
   }
-  return launch_full<NT, DEG3, DBIG, ES, SPLIT, CG, false>(a, bh, s);
+  return launch_full<NT, NX, DBIG, ES, SPLIT, CG, false>(a, bh, s);
 }
 
 }  // namespace
 
 template <bool SPLIT, int CG>
-int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, bool deg3) {
+int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx) {
   const bool big = a.d > 64;
 #define STA_CASE(NT, D3, BIG)                                                                       \
-  if (nt == NT && deg3 == D3 && big == BIG)                                                         \
+  if (nt == NT && nx == D3 && big == BIG)                                                         \
     return a.esize == 4 ? launch<NT, D3, BIG, 4, SPLIT, CG>(a, bh, s) : launch<NT, D3, BIG, 2, SPLIT, CG>(a, bh, s);
 #if STA_MOM_CG == 64
   STA_MOMENT_CONFIGS_64(STA_CASE)
@@ -55,6 +55,6 @@ int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, b
   return STA_ERR_UNSUPPORTED;
 }
 
-template int dispatch_moments<STA_MOM_SPLIT != 0, STA_MOM_CG>(const sta::MomArgs&, int64_t, hipStream_t, int, bool);
+template int dispatch_moments<STA_MOM_SPLIT != 0, STA_MOM_CG>(const sta::MomArgs&, int64_t, hipStream_t, int, int);
 
 }  // namespace sta_api

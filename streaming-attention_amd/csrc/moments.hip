@@ -7,8 +7,10 @@
 // own chunk are added by the block kernel (closed-form Taylor polynomial), so the two kernels together
 // give sum_{j<=i} exp_{<=t}(s q_i.k_j) [v_j, 1] exactly (in exact arithmetic).
 //
-// Feature layout.  The monomials are grouped in quads x[i0] x[b+s] x[i2], s = 0..3, b a multiple of 4
-// (x[d] = 1 lowers the degree; see feature_tiles in _plan.py), 4 quads per tile of 16 features.  The
+// Feature layout.  The monomials are grouped in quads x[i0] x[b+s] x[i2] x[i3], s = 0..3, b a multiple of
+// 4 (x[d] = 1 lowers the degree; see feature_tiles in _plan.py), 4 quads per tile of 16 features.  NX:
+// the number of factors besides x[i0] and x[b+s] the instantiation multiplies in (0: degree <= 2,
+// 1: degree 3, 2: degree 4).  The
 // tiles are split over `fsplit` workgroups and over the 4 waves of a workgroup, every wave holding
 // exactly NT tiles (the host pads with zero tiles, so the loops are branch-free and fully unrolled).
 // A workgroup also owns one 32-wide group of value columns (csplit = ceil(dv/32) per feature split).
@@ -88,7 +90,7 @@ struct MomArgs {
   int fsplit;             // feature splits (workgroups per head and column group)
   int mixed;              // 1: feature splits fs >= fsplit / 2 hold one tile less per wave (see moments_kernel)
   int csplit;             // 32-column groups
-  const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4] packed (i0 | b << 8 | i2 << 16)
+  const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4] packed (i0 | b << 8 | i2 << 16 | i3 << 24)
   const float* fcoef;     // [fsplit][4 waves][NT tiles][16] key-side coefficient, 0 for padding
   float* low_num;         // [BH][fsplit][n + 2*MOM_GUARD][ldo], row r at r + MOM_GUARD
   float* low_den;         // [BH][fsplit][n + 2*MOM_GUARD]
@@ -334,26 +336,28 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
 // Per-lane feature offsets of a wave's NT tiles (constant over the sequence).  Query side: columns of
 // x[i0], x[b..b+3], x[i2] of quad lg in the row-major queries.  Update side: Kt rows of feature li plus
 // the token offset 4 lg (token blocks lg and lg + 4), and the key-side coefficient of feature li.
-template <int NT, bool DEG3>
+template <int NT, int NX>
 struct MomLane {
-  int qa[NT], qb[NT], qc[DEG3 ? NT : 1];
-  int ka[NT], kb[NT], kc[DEG3 ? NT : 1];
+  int qa[NT], qb[NT], qc[NX >= 1 ? NT : 1], qe[NX >= 2 ? NT : 1];
+  int ka[NT], kb[NT], kc[NX >= 1 ? NT : 1], ke[NX >= 2 ? NT : 1];
   float kcoef[NT];
 };
 
-template <int NT, bool DEG3>
-__device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t tile0, int li, int lg) {
-  MomLane<NT, DEG3> m;
+template <int NT, int NX>
+__device__ __forceinline__ MomLane<NT, NX> mom_lane(const MomArgs& a, int64_t tile0, int li, int lg) {
+  MomLane<NT, NX> m;
 #pragma unroll
   for (int kt = 0; kt < NT; ++kt) {
     const uint32_t pq = a.quads[(tile0 + kt) * 4 + lg];
     m.qa[kt] = static_cast<int>(pq & 255u);
     m.qb[kt] = static_cast<int>((pq >> 8) & 255u);
-    if (DEG3) m.qc[DEG3 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
+    if (NX >= 1) m.qc[NX >= 1 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
+    if (NX >= 2) m.qe[NX >= 2 ? kt : 0] = static_cast<int>((pq >> 24) & 255u);
     const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
     m.ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 4 * lg;
     m.kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 4 * lg;
-    if (DEG3) m.kc[DEG3 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 4 * lg;
+    if (NX >= 1) m.kc[NX >= 1 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 4 * lg;
+    if (NX >= 2) m.ke[NX >= 2 ? kt : 0] = static_cast<int>((pk >> 24) & 255u) * MOM_LDT + 4 * lg;
     m.kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
   }
   return m;
@@ -363,22 +367,23 @@ __device__ __forceinline__ MomLane<NT, DEG3> mom_lane(const MomArgs& a, int64_t 
 // its 32 columns, den_s[f] += phi_k(tok)[f].  Token steps outermost over all tiles (2 NT independent
 // chains), in two halves of 4 steps; the keys of the second half are read while the first half's
 // MFMAs issue.  `mid()` runs after the first key reads are issued (work to hide under them).
-template <int NT, int CT, bool DEG3, bool DEN, class Mid>
+template <int NT, int CT, int NX, bool DEN, class Mid>
 __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, const float* Kt, const float* Vt,
-                                           const MomLane<NT, DEG3>& m, int li, int lg, Mid mid) {
+                                           const MomLane<NT, NX>& m, int li, int lg, Mid mid) {
   floatx4 vv[2][CT];  // values of tokens 4 lg + 0..3 and 16 + 4 lg + 0..3
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg);
     vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg + 16);
   }
-  floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
+  floatx4 fa[2][NT], fb[2][NT], fc[2][NX >= 1 ? NT : 1], fe[2][NX >= 2 ? NT : 1];
   auto uload = [&](int h) {
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
       fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 16 * h);
+      if (NX >= 1) fc[h][NX >= 1 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
+      if (NX >= 2) fe[h][NX >= 2 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
     }
   };
   uload(0);
@@ -395,7 +400,8 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
         float x = fa[h][kt][e] * fb[h][kt][e];
-        if (DEG3) x *= fc[h][DEG3 ? kt : 0][e];
+        if (NX >= 1) x *= fc[h][NX >= 1 ? kt : 0][e];
+        if (NX >= 2) x *= fe[h][NX >= 2 ? kt : 0][e];
         x *= m.kcoef[kt];
         if constexpr (DEN) dacc[kt] += x;
 #pragma unroll
@@ -424,18 +430,19 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 // A values of its 8 steps); B: V[tok(lg, j)][col].  The feature values and the values are split into
 // bf16 hi + lo, and S += A_hi B_lo + A_lo B_hi + A_hi B_hi (terms outermost, so the 2 NT accumulators
 // are independent chains).  The denominator sums the fp32 feature values as before.
-template <int NT, int CT, bool DEG3, bool DEN, class Mid>
+template <int NT, int CT, int NX, bool DEN, class Mid>
 __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* den_s, const float* Kt,
-                                                 const float* Vt, const MomLane<NT, DEG3>& m, int li, int lg,
+                                                 const float* Vt, const MomLane<NT, NX>& m, int li, int lg,
                                                  Mid mid) {
-  floatx4 fa[2][NT], fb[2][NT], fc[2][DEG3 ? NT : 1];
+  floatx4 fa[2][NT], fb[2][NT], fc[2][NX >= 1 ? NT : 1], fe[2][NX >= 2 ? NT : 1];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
       fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (DEG3) fc[h][DEG3 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[DEG3 ? kt : 0] + 16 * h);
+      if (NX >= 1) fc[h][NX >= 1 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
+      if (NX >= 2) fe[h][NX >= 2 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
     }
   // the staged bf16 planes (mom_store<..., true>, vps_off): column 16 ct + li, tokens tok(lg, 0..7)
   constexpr int CG = 16 * CT;
@@ -457,7 +464,8 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float y = fa[j >> 2][kt][j & 3] * fb[j >> 2][kt][j & 3];
-      if (DEG3) y *= fc[j >> 2][DEG3 ? kt : 0][j & 3];
+      if (NX >= 1) y *= fc[j >> 2][NX >= 1 ? kt : 0][j & 3];
+      if (NX >= 2) y *= fe[j >> 2][NX >= 2 ? kt : 0][j & 3];
       y *= m.kcoef[kt];
       x[j] = y;
       if constexpr (DEN) dacc += y;
@@ -485,9 +493,9 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
 // state is used in place, split into bf16 hi + lo once per chunk.  An odd last tile pairs with zeros.
 // o[tt][ct] accumulates rows 16 tt + 4 lg + r, column 16 ct + li; dq the denominator (fp32 VALU, the
 // fp32 path's order).
-template <int NT, int CT, bool DEG3, bool DEN, int LDQ>
+template <int NT, int CT, int NX, bool DEN, int LDQ>
 __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&dq)[2], const floatx4 (&st)[NT][CT],
-                                                const float* Qs, const float* den_s, const MomLane<NT, DEG3>& m,
+                                                const float* Qs, const float* den_s, const MomLane<NT, NX>& m,
                                                 int li, int lg) {
   constexpr int TT = 2;
   constexpr int NP = (NT + 1) / 2;
@@ -519,11 +527,13 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
       {
         const float a0 = qrow[16 * tt * LDQ + m.qa[t0]];
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[t0]);
-        const float c0 = DEG3 ? qrow[16 * tt * LDQ + m.qc[DEG3 ? t0 : 0]] : 1.f;
+        const float c0 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? t0 : 0]] : 1.f;
+        const float e0 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? t0 : 0]] : 1.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           float y = a0 * b0[s];
-          if (DEG3) y *= c0;
+          if (NX >= 1) y *= c0;
+          if (NX >= 2) y *= e0;
           x[s] = y;
           if constexpr (DEN) dq[tt] = fmaf(y, dn0[s], dq[tt]);
         }
@@ -532,11 +542,13 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
         const int u = has1 ? t1 : t0;
         const float a1 = qrow[16 * tt * LDQ + m.qa[u]];
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[u]);
-        const float c1 = DEG3 ? qrow[16 * tt * LDQ + m.qc[DEG3 ? u : 0]] : 1.f;
+        const float c1 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? u : 0]] : 1.f;
+        const float e1 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? u : 0]] : 1.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           float y = a1 * b1[s];
-          if (DEG3) y *= c1;
+          if (NX >= 1) y *= c1;
+          if (NX >= 2) y *= e1;
           x[4 + s] = y;
           if constexpr (DEN) dq[tt] = fmaf(y, dn1[s], dq[tt]);
         }
@@ -566,7 +578,7 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
 // The kernel body for one workgroup (head bh, feature split fs, column group cs) with NT tiles per wave
 // out of the NTS the split table holds per wave.  DEN: this workgroup also keeps the denominator column
 // (only column group 0 does; the others would compute bit-identical values).
-template <int NT, int NTS, bool DEG3, bool DBIG, int ES, bool DEN, bool SPLIT, int CG, bool FULL>
+template <int NT, int NTS, int NX, bool DBIG, int ES, bool DEN, bool SPLIT, int CG, bool FULL>
 __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int fs, int cs) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int BUF = mom_buf_floats(DBIG, CG);
@@ -589,7 +601,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   float* den_s = den_all + w * NT * 16;  // running denominator of every feature of this wave's tiles
 
   const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NTS;  // NTS: table tiles per wave
-  const MomLane<NT, DEG3> m = mom_lane<NT, DEG3>(a, tile0, li, lg);
+  const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
 
   floatx4 st[NT][CT];
 #pragma unroll
@@ -634,9 +646,9 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
       for (int ct = 0; ct < CT; ++ct) o[0][tt][ct] = o[1][tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     if constexpr (SPLIT) {
-      mom_query_split<NT, CT, DEG3, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
+      mom_query_split<NT, CT, NX, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
     } else {
-      float x0[2][TT], x2[2][TT];
+      float x0[2][TT], x2[2][TT], x3[2][TT];
       floatx4 x1[2][TT], dn[2];
       const float* qrow = Qs + li * LDQ;
       auto qload = [&](int kt, int buf) {
@@ -644,7 +656,8 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
         for (int tt = 0; tt < TT; ++tt) {
           x0[buf][tt] = qrow[16 * tt * LDQ + m.qa[kt]];
           x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[kt]);
-          if (DEG3) x2[buf][tt] = qrow[16 * tt * LDQ + m.qc[DEG3 ? kt : 0]];
+          if (NX >= 1) x2[buf][tt] = qrow[16 * tt * LDQ + m.qc[NX >= 1 ? kt : 0]];
+          if (NX >= 2) x3[buf][tt] = qrow[16 * tt * LDQ + m.qe[NX >= 2 ? kt : 0]];
         }
         if constexpr (DEN) dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
       };
@@ -658,7 +671,8 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
 #pragma unroll
           for (int tt = 0; tt < TT; ++tt) {
             float x = x0[cb][tt] * x1[cb][tt][s];
-            if (DEG3) x *= x2[cb][tt];
+            if (NX >= 1) x *= x2[cb][tt];
+            if (NX >= 2) x *= x3[cb][tt];
             if constexpr (DEN) dq[tt] = fmaf(x, dn[cb][s], dq[tt]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) o[cb][tt][ct] = mfma4(x, st[kt][ct][s], o[cb][tt][ct]);
@@ -711,9 +725,9 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
       if (c > 0) mom_reduce_store<DEN, CG>(a, red_all + (cur ^ 1) * RED, obase, row0 - MOM_C, col0);
     };
     if constexpr (SPLIT)
-      mom_update_split<NT, CT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
+      mom_update_split<NT, CT, NX, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
     else
-      mom_update<NT, CT, DEG3, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
+      mom_update<NT, CT, NX, DEN>(st, den_s, Kt, Vt, m, li, lg, mid);
     __syncthreads();
   }
   mom_reduce_store<DEN, CG>(a, red_all + ((nchunks - 1) & 1) * RED, obase, first + (nchunks - 1) * MOM_C, col0);
@@ -755,7 +769,7 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
 // split once for 4 column tiles instead of twice for 2 (the 32-column workgroups of a head each do
 // their own), at one workgroup per compute unit (124 KiB of LDS).
 // FULL: mom_full_slots(DBIG, ES, a.d) (the host picks the instantiation).
-template <int NT, bool DEG3, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
+template <int NT, int NX, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
 __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
@@ -764,14 +778,14 @@ __global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void mome
   if (MIX && a.mixed && fs >= a.fsplit / 2) {
     constexpr int NTL = MIX ? NT - 1 : NT;
     if (cs == 0)
-      moments_body<NTL, NT, DEG3, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
+      moments_body<NTL, NT, NX, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
     else
-      moments_body<NTL, NT, DEG3, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
+      moments_body<NTL, NT, NX, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
   } else {
     if (cs == 0)
-      moments_body<NT, NT, DEG3, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
+      moments_body<NT, NT, NX, DBIG, ES, true, SPLIT, CG, FULL>(a, bh, fs, cs);
     else
-      moments_body<NT, NT, DEG3, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
+      moments_body<NT, NT, NX, DBIG, ES, false, SPLIT, CG, FULL>(a, bh, fs, cs);
   }
 }
 
@@ -788,7 +802,7 @@ __host__ __device__ constexpr int mom_acc_smem_floats(bool dbig, int nt) {
 // the accumulators at the start and written back at the end (each (head, feature, column) belongs to
 // exactly one wave of the grid, so the read-modify-write has no race).  Rows [0, n) of every head are
 // read at k + bh * head_rows * d (v: ldv).
-template <int NT, bool DEG3, bool DBIG, int ES>
+template <int NT, int NX, bool DBIG, int ES>
 __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const MomArgs a) {
   constexpr int BUF = mom_buf_floats(DBIG);
   constexpr int CT = 2;
@@ -810,7 +824,7 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
   const int li = lane & 15, lg = lane >> 4;
   float* den_s = den_all + w * NT * 16;
   const int64_t tile0 = (static_cast<int64_t>(fs) * MOM_WAVES + w) * NT;
-  const MomLane<NT, DEG3> m = mom_lane<NT, DEG3>(a, tile0, li, lg);
+  const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
 
   // ---- the wave's slice of the state -> accumulators and running denominators ----
   float* snum = a.state_num + bh * a.n_feat * a.ldo;
@@ -844,7 +858,7 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
     __syncthreads();
     const float* Kt = smem + MOM_C * mom_ldq(DBIG);
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
-    mom_update<NT, CT, DEG3, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
+    mom_update<NT, CT, NX, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
   }
 
   // ---- write the slice back (the denominators once per feature split) ----

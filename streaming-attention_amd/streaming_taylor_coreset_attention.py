@@ -3,7 +3,8 @@
 
 `article_causal_attention` returns what the reference's per-token loop `update(k_i, v_i); query(q_i)`
 returns (streaming_taylor_coreset_attention.py:641-754), computed as one prefill:
-  * exact Taylor moments of any degree <= 3 (symmetric monomial basis, key coefficient 1/prod(alpha!));
+  * exact Taylor moments of any degree <= 4 (degree 4 for D <= 64; symmetric monomial basis, key
+    coefficient 1/prod(alpha!));
   * the merge-and-reduce level tree built level-parallel from the same seed-derived draws the
     reference's generator produces, in its call order (one compress per completed block, one per
     cascade merge, merge input = cat(old, new));

@@ -177,6 +177,25 @@ def test_decode_vs_oracle_single_stream():
                 st.coreset.levels[lev].weights.cpu().numpy(), lv[1])
 
 
+def test_decode_degree4_vs_oracle():
+    """Degree-4 decode: per-token outputs and the sketch moments (reference feature order) against the
+    oracle; the 4-factor decode feature table and 4-term Taylor tail."""
+    n, d, dv, block = 150, 6, 8, 16
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=21)
+    ref = orc.levels_forward(q, k, v, degree=4, block=block, scale=1.0, seed=5)
+    st = stc.ArticleStreamingAttention(d, dv, degree=4, block_size=block, scale=1.0, device=DEV, seed=5)
+    st.extend(k[:40].to(DEV), v[:40].to(DEV))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = torch.stack([st.step(qd[i], kd[i], vd[i]) for i in range(40, n)])
+    assert rel(out, ref[40:]) < FP32_TOL
+    phi = orc.features(k.double(), 4, key_side=True)
+    den = torch.cat([x.cpu().double() for x in st.sketch.den_moments])
+    num = torch.cat([x.cpu().double() for x in st.sketch.num_moments])
+    assert [x.shape[0] for x in st.sketch.den_moments] == [1, 6, 21, 56, 126]
+    assert rel(den, phi.sum(0)) < 1e-6
+    assert rel(num, phi.T @ v.double()) < 1e-6
+
+
 def test_sketch_moments_closed_form():
     """den_moments / num_moments (reference order, per degree) == sum_j phi_k(k_j) [1, v_j] in fp64."""
     n, d, dv = 150, 6, 5

@@ -224,6 +224,36 @@ def test_levels_without_compression_is_exact():
     assert torch.allclose(out.cpu().double(), orc.classical_attention(q, k, v, 1.0), atol=3e-6, rtol=3e-6)
 
 
+@pytest.mark.parametrize("n,d,dv,block,comp,scale", [
+    (300, 8, 16, 32, "sorted_pair", 1.0), (200, 6, 5, 16, "random", 1.0), (129, 16, 64, 64, "sorted_pair", 0.25),
+])
+def test_degree4_levels_vs_oracle(n, d, dv, block, comp, scale):
+    """Degree-4 feature maps (x[i0] x[i2] x[i3] x[b + s] quads; 4-term Horner Taylor in the residual)
+    against the oracle's general-degree restatement of the reference (streaming_taylor_coreset_attention.py:
+    118-216)."""
+    print(f"degree 4 n={n} d={d} dv={dv} block={block} {comp}", flush=True)
+    q, k, v = orc.make_data((), n, d, dv, radius=1.0, data="unit_ball", seed=n + d)
+    out = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=4, block_size=block, scale=scale,
+                                       compressor=comp, seed=3)
+    ref = orc.levels_forward(q, k, v, degree=4, block=block, scale=scale, compressor=comp, seed=3)
+    assert rel(out, ref) < 1e-4
+
+
+def test_degree4_without_compression_is_exact_taylor_and_limits():
+    # one block covers the sequence: exact softmax attention (the Taylor part and the residual add up)
+    torch.manual_seed(1)
+    q = torch.nn.functional.normalize(torch.randn(40, 6), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(40, 6), dim=-1)
+    v = torch.randn(40, 5)
+    out = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=4, block_size=41, scale=1.0)
+    assert torch.allclose(out.cpu().double(), orc.classical_attention(q, k, v, 1.0), atol=3e-6, rtol=3e-6)
+    with pytest.raises(NotImplementedError):
+        stc.article_causal_attention(torch.randn(8, 72, device=DEV), torch.randn(8, 72, device=DEV),
+                                     torch.randn(8, 4, device=DEV), degree=4, block_size=4)
+    with pytest.raises(NotImplementedError):
+        stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=5, block_size=8)
+
+
 # --------------------------------------------------------------------------- against the oracle, more shapes
 
 @pytest.mark.parametrize("n,d,dv,block,comp,scale", [

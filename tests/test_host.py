@@ -37,7 +37,7 @@ def test_library_exports_header_symbols():
         assert lib.sta_moment_chunk(d) == _plan.moment_chunk(d)
     assert lib.sta_status_string(0) == b"ok"
     lim = _native.limits()
-    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 3, "max_compress_in": 1024}
+    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 4, "max_compress_in": 1024}
 
 
 def test_library_rejects_bad_arguments_without_touching_a_device():
@@ -134,16 +134,18 @@ def _quad_features(ft):
     constant index d; slots beyond the constant (index > d) are reported as None."""
     out = []
     for q, packed in enumerate(ft.quads):
-        i0, b, i2 = int(packed) & 255, (int(packed) >> 8) & 255, (int(packed) >> 16) & 255
+        i0, b, i2, i3 = (int(packed) & 255, (int(packed) >> 8) & 255, (int(packed) >> 16) & 255,
+                         int(packed) >> 24)
         for s in range(4):
-            ids = (i0, b + s, i2)
+            ids = (i0, b + s, i2, i3)
             coef = float(ft.coef[4 * q + s])
             mono = None if max(ids) > ft.d else tuple(sorted(i for i in ids if i != ft.d))
             out.append((mono, coef))
     return out
 
 
-@pytest.mark.parametrize("d,degree", [(5, 3), (64, 2), (32, 2), (16, 3), (8, 0), (12, 1), (128, 2), (6, 2)])
+@pytest.mark.parametrize("d,degree", [(5, 3), (64, 2), (32, 2), (16, 3), (8, 0), (12, 1), (128, 2), (6, 2), (6, 4),
+                                      (16, 4)])
 def test_feature_tiles_cover_the_monomial_basis(d, degree):
     ft = _plan.feature_tiles(d, degree)
     assert ft.count == _plan.num_features(d, degree)
@@ -156,7 +158,16 @@ def test_feature_tiles_cover_the_monomial_basis(d, degree):
     for packed in ft.quads:
         b = (int(packed) >> 8) & 255
         assert b % 4 == 0 and b + 3 <= ft.d + 3
-        assert max(int(packed) & 255, (int(packed) >> 16) & 255) <= ft.d
+        assert max(int(packed) & 255, (int(packed) >> 16) & 255, int(packed) >> 24) <= ft.d
+
+
+def test_feature_tiles_limits():
+    with pytest.raises(NotImplementedError):
+        _plan.feature_tiles(72, 4)  # degree 4 only for d <= 64
+    with pytest.raises(NotImplementedError):
+        _plan.feature_tiles(8, 5)
+    ft = _plan.feature_tiles(16, 4)
+    assert ft.count == 4845 and 16 * ft.n_tiles >= 4845
 
 
 def test_feature_tiles_padding_is_small():
@@ -289,14 +300,14 @@ def test_library_decode_entries_reject_bad_arguments():
     assert _native.decode_layout(64, 130) == (64, 160)
 
 
-@pytest.mark.parametrize("d,degree", [(4, 2), (5, 3), (64, 2), (16, 3), (3, 0), (7, 1)])
+@pytest.mark.parametrize("d,degree", [(4, 2), (5, 3), (64, 2), (16, 3), (3, 0), (7, 1), (6, 4), (16, 4)])
 def test_feature_index_is_reference_order(d, degree):
     idx = _plan.feature_index(d, degree)
     combos = orc.monomials(d, degree)
     assert idx.shape == (len(combos),)
     for f, c in enumerate(combos):
-        full = list(c) + [d] * (3 - len(c))
-        assert int(idx[f]) == full[0] | (full[1] << 8) | (full[2] << 16)
+        full = list(c) + [d] * (4 - len(c))
+        assert int(idx[f]) == full[0] | (full[1] << 8) | (full[2] << 16) | (full[3] << 24)
 
 
 @pytest.mark.parametrize("width,d,degree,bh,dv", [(64, 64, 2, 2048, 64), (8, 6, 3, 1, 5), (16, 16, 3, 96, 64),
