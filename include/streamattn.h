@@ -58,9 +58,14 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *     basis in tiles of 4 quads, wave_tiles tiles for each of the 4 waves of each feature split (padded
  *     with coefficient-0 tiles).  A quad packs i0 | b<<8 | i2<<16 | i3<<24 (b a multiple of 4, at most d;
  *     unused factors = d) and holds the features x[i0] x[b+s] x[i2] x[i3], s = 0..3, of
- *     [x_0..x_{D-1}, 1, 0, 0, 0] (degree 4 needs d <= 64); feat_coef is the
- *     key-side coefficient 1/prod(alpha!) of each feature (0 for padding).  wave_tiles must be a count
- *     the library is built for (sta_moment_wave_tiles).
+ *     [x_0..x_{D-1}, 1, 0, 0, 0] (degree 4 needs d <= 64; index d+1 selects a 0, for zero-valued
+ *     padding); feat_coef is the key-side coefficient 1/prod(alpha!) of each feature (0 for padding).
+ *     Exception: with STA_PRODUCTS_SPLIT_BF16 and degree <= 2 the kernel sums plain monomials and
+ *     applies feat_coef[16 t] to tile t's query-side monomials, so each tile's 16 entries must be one
+ *     value c_t with c_t * (sum of the tile's slot monomials) equal to the tile's coefficient-weighted
+ *     sum (e.g. 1/2 on every slot of a diagonal tile x[4k+r] x[4k+s]; the planner's
+ *     tile_coefficients).  wave_tiles must be a count the library is built for
+ *     (sta_moment_wave_tiles).
  *   q and k rows are d elements long and v rows ldv (a multiple of 32, >= dv); rows are read in
  *     16-byte units, so d times the element size must be a multiple of 16 (pad rows with zero columns
  *     otherwise: zero dimensions only add zero-valued features), and q, k, v must be 16-byte aligned.

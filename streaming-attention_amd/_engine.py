@@ -193,8 +193,12 @@ def prefill(
                             mixed_nts=_native.moment_mixed_tiles(dm, degree),
                             wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
     fsplit = ms.fsplit
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit), dev,
-                             lambda: (_i32(ms.quads, dev), _f32(ms.coef, dev)))
+    # split products at degree <= 2 apply one coefficient per tile on the query side
+    tile_coef = k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 2
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef), dev,
+                             lambda: (_i32(ms.quads, dev),
+                                      _f32(_plan.tile_coefficients(ms.quads, ms.coef, dm) if tile_coef else ms.coef,
+                                           dev)))
 
     raw = semantics == "taylor"
     if semantics in ("exact", "taylor"):

@@ -120,6 +120,8 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
             i2 = prefix[1] if len(prefix) >= 2 else one
             i3 = prefix[2] if len(prefix) >= 3 else one
             for b in range((lo // 4) * 4, last + 1, 4):
+                if not any(lo <= c < hi or (with_const and c == d) for c in range(b, b + 4)):
+                    continue  # no feature in this quad (degree 0: only the constant's quad is kept)
                 cs = []
                 for s in range(4):
                     c = b + s
@@ -171,7 +173,8 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
         coefs = [coefs[i] for i in order]
         slot_combos = [c for i in order for c in slot_combos[4 * i: 4 * i + 4]]
         n_tiles = -(-len(quads) // 4)
-        pad_quad = one | ((d // 4 * 4) << 8) | (one << 16) | (one << 24)  # finite staged values; coefficient 0
+        # padding: first factor x[d + 1] = 0, so every padding slot is a zero-valued monomial
+        pad_quad = (one + 1) | ((d // 4 * 4) << 8) | (one << 16) | (one << 24)
         q = np.full(n_tiles * 4, pad_quad, dtype=np.uint32)
         c = np.zeros(n_tiles * 16, dtype=np.float32)
         q[: len(quads)] = np.asarray(quads, dtype=np.uint32)
@@ -293,7 +296,7 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
             sizes = [base + (1 if i < extra else 0) for i in range(parts)]
         off = np.zeros(parts + 1, dtype=np.int32)
         off[1:] = np.cumsum(sizes)
-        pad_quad = ft.d | ((ft.d // 4 * 4) << 8) | (ft.d << 16)
+        pad_quad = (ft.d + 1) | ((ft.d // 4 * 4) << 8) | (ft.d << 16) | (ft.d << 24)  # zero-valued slots
         quads = np.full((parts, nt, 4), pad_quad, dtype=np.uint32)
         coef = np.zeros((parts, nt, 16), dtype=np.float32)
         tiles_q = ft.quads.reshape(t, 4)
@@ -306,6 +309,41 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
 
     return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units, tuple(mixed_nts),
                     tuple(wide_nts)), build)
+
+
+def tile_coefficients(quads: np.ndarray, coef: np.ndarray, d: int) -> np.ndarray:
+    """The coefficient table of the split-product moment scan at degree <= 2 (moments.hip,
+    mom_query_split): every tile's 16 entries set to one value c_t with
+
+        c_t * sum over the tile's 16 slots of monomial(slot) == sum over slots of coef(slot) * monomial(slot)
+
+    as polynomials in x (x[d] = 1, x[d + 1 ..] = 0).  The kernel then accumulates plain monomials and
+    applies c_t once per tile and query token.  Degree <= 2 tiles are of three kinds: 16 distinct
+    monomials of coefficient 1 (c_t = 1); a diagonal tile x[4k + r] x[4k + s], whose slot pairs (r, s),
+    (s, r) both hold the monomial of coefficient 1 and whose diagonal holds coefficient 1/2 (c_t = 1/2);
+    zero-valued padding (c_t = 0).  Raises ValueError for a table without such a c_t per tile (degree
+    >= 3, or d not a multiple of 4)."""
+    q = np.asarray(quads, dtype=np.int64).reshape(-1, 4)
+    c = np.asarray(coef, dtype=np.float64).reshape(-1, 16)
+    out = np.zeros(c.shape, dtype=np.float32)
+    for t in range(q.shape[0]):
+        want: Dict[Tuple[int, ...], float] = {}
+        cnt: Dict[Tuple[int, ...], int] = {}
+        for qi in range(4):
+            pq = int(q[t, qi])
+            i0, b, i2, i3 = pq & 255, (pq >> 8) & 255, (pq >> 16) & 255, (pq >> 24) & 255
+            for s_ in range(4):
+                ids = (i0, b + s_, i2, i3)
+                if max(ids) > d:
+                    continue  # a factor x[d + 1 ..] = 0
+                mono = tuple(sorted(i for i in ids if i != d))
+                want[mono] = want.get(mono, 0.0) + float(c[t, 4 * qi + s_])
+                cnt[mono] = cnt.get(mono, 0) + 1
+        vals = {want[m] / cnt[m] for m in cnt}
+        if len(vals) > 1:
+            raise ValueError(f"tile {t} has no uniform coefficient: {sorted(vals)}")
+        out[t] = vals.pop() if vals else 0.0
+    return out.reshape(np.asarray(coef).shape)
 
 
 def split_state_rows(ft: FeatureTiles, ms: MomentSplit, d: int) -> np.ndarray:

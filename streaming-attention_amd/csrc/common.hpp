@@ -78,8 +78,15 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
 // (-1, 0) (or (0, -1)) plus x is x - hi exactly: bf16 products are exact in fp32 and x - hi is
 // representable.  The two pairs are held in scalar registers behind an empty asm: the compiler would
 // otherwise encode (-1, 0) as the inline constant -1.0, which the hardware reads as the 32-bit float
-// (the pair (0, -1)).
+// (the pair (0, -1)).  The dot stays the compiler's builtin (selected as v_dot2c_f32_bf16, which costs
+// a v_mov where x stays live): a VALU instruction written as inline asm is invisible to the compiler's
+// MFMA hazard padding, and such a form gave wrong moments next to the matrix-core products.
 __device__ __forceinline__ void split_pair(float a, float b, uint32_t& h, uint32_t& l) {
+  // a pair the optimiser knows to be zero (the padding half of an odd tile pair) costs nothing
+  if (__builtin_constant_p(a) && __builtin_constant_p(b) && a == 0.f && b == 0.f) {
+    h = l = 0u;
+    return;
+  }
   uint32_t c0 = 0x0000BF80u, c1 = 0xBF800000u;
   asm("" : "+s"(c0));
   asm("" : "+s"(c1));

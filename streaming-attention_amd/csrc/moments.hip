@@ -430,6 +430,12 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 // A values of its 8 steps); B: V[tok(lg, j)][col].  The feature values and the values are split into
 // bf16 hi + lo, and S += A_hi B_lo + A_lo B_hi + A_hi B_hi (terms outermost, so the 2 NT accumulators
 // are independent chains).  The denominator sums the fp32 feature values as before.
+// NX = 0 (degree <= 2): the state holds the plain monomial sums and the coefficient table holds one
+// coefficient per tile (repeated over its 16 slots), which mom_query_split applies to the query
+// side's first factor: 1 multiply per tile and token instead of one per feature and token.  The
+// planner makes every degree <= 2 tile uniform (tile_coefficients in _plan.py): the diagonal tiles
+// x[4k + r] x[4k + s] take 1/2 on all 16 slots (the slot pairs (r, s), (s, r) add up to the
+// off-diagonal monomial), padding slots are zero-valued monomials.
 template <int NT, int CT, int NX, bool DEN, class Mid>
 __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* den_s, const float* Kt,
                                                  const float* Vt, const MomLane<NT, NX>& m, int li, int lg,
@@ -466,7 +472,7 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
       float y = fa[j >> 2][kt][j & 3] * fb[j >> 2][kt][j & 3];
       if (NX >= 1) y *= fc[j >> 2][NX >= 1 ? kt : 0][j & 3];
       if (NX >= 2) y *= fe[j >> 2][NX >= 2 ? kt : 0][j & 3];
-      y *= m.kcoef[kt];
+      if (NX >= 1) y *= m.kcoef[kt];  // NX = 0: the tile's coefficient is applied by the query
       x[j] = y;
       if constexpr (DEN) dacc += y;
     }
@@ -525,7 +531,7 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
     for (int tt = 0; tt < TT; ++tt) {
       float x[8];
       {
-        const float a0 = qrow[16 * tt * LDQ + m.qa[t0]];
+        const float a0 = (NX == 0) ? qrow[16 * tt * LDQ + m.qa[t0]] * m.kcoef[t0] : qrow[16 * tt * LDQ + m.qa[t0]];
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[t0]);
         const float c0 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? t0 : 0]] : 1.f;
         const float e0 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? t0 : 0]] : 1.f;
@@ -540,7 +546,7 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
       }
       if (has1) {
         const int u = has1 ? t1 : t0;
-        const float a1 = qrow[16 * tt * LDQ + m.qa[u]];
+        const float a1 = (NX == 0) ? qrow[16 * tt * LDQ + m.qa[u]] * m.kcoef[u] : qrow[16 * tt * LDQ + m.qa[u]];
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[u]);
         const float c1 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? u : 0]] : 1.f;
         const float e1 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? u : 0]] : 1.f;

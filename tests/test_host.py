@@ -154,11 +154,50 @@ def test_feature_tiles_cover_the_monomial_basis(d, degree):
     live = sorted((m, np.float32(c).item()) for m, c in feats if c != 0.0)
     expect = sorted((m, np.float32(orc.inv_multinomial(m)).item()) for m in orc.monomials(d, degree))
     assert live == expect
-    # every slot reads inside the staged row: factors up to d + 3 (the constant, then zero padding)
+    # every slot reads inside the staged row: factors up to d + 3 (the constant, then zero padding);
+    # padding quads take the zero x[d + 1] as first factor
     for packed in ft.quads:
         b = (int(packed) >> 8) & 255
         assert b % 4 == 0 and b + 3 <= ft.d + 3
-        assert max(int(packed) & 255, (int(packed) >> 16) & 255, int(packed) >> 24) <= ft.d
+        assert max((int(packed) >> 16) & 255, int(packed) >> 24) <= ft.d and int(packed) & 255 <= ft.d + 1
+
+
+@pytest.mark.parametrize("d,degree", [(64, 2), (32, 2), (128, 2), (8, 0), (12, 1), (16, 2), (4, 2)])
+def test_tile_coefficients_preserve_every_tile_polynomial(d, degree):
+    """The per-tile coefficient table of the split-product moment scan (degree <= 2) gives every tile
+    the same polynomial as the per-feature table: checked by evaluating both on random x (x[d] = 1,
+    x[d+1..d+3] = 0), over the padded work split too."""
+    ft = _plan.feature_tiles(d, degree)
+    opts = ((2, 2), (4, 2), (5, 2), (9, 2), (16, 1))
+    ms = _plan.moment_split(ft, 3, 64, opts)
+    rng = np.random.default_rng(d + degree)
+    for quads, coef in ((ft.quads, ft.coef), (ms.quads, ms.coef)):
+        tc = _plan.tile_coefficients(quads, coef, d)
+        q = quads.reshape(-1, 4).astype(np.int64)
+        per_tile = tc.reshape(-1, 16)
+        assert np.all(per_tile == per_tile[:, :1])  # uniform over a tile
+        assert set(np.unique(per_tile).tolist()) <= {0.0, 0.5, 1.0}
+        for _ in range(3):
+            x = np.concatenate([rng.standard_normal(d), [1.0, 0.0, 0.0, 0.0]])
+            i0, b, i2, i3 = q & 255, (q >> 8) & 255, (q >> 16) & 255, (q >> 24) & 255
+            mono = np.stack([x[i0] * x[b + s] * x[i2] * x[i3] for s in range(4)], axis=-1).reshape(-1, 16)
+            want = (mono * coef.reshape(-1, 16)).sum(1)
+            got = per_tile[:, 0] * mono.sum(1)
+            np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # planted mistakes: a diagonal coefficient of 1 instead of 1/2 has no uniform tile coefficient, and
+    # degree 3 tiles are rejected
+    if degree == 2:
+        bad = ft.coef.copy().reshape(-1, 4, 4)
+        q = ft.quads.reshape(-1, 4)
+        diag = [t for t in range(q.shape[0]) if all((int(q[t, r]) & 255) == ((int(q[t, 0]) >> 8) & 255) + r
+                                                    for r in range(4))]
+        assert len(diag) == d // 4
+        bad[diag[0], 1, 1] = 1.0
+        with pytest.raises(ValueError):
+            _plan.tile_coefficients(ft.quads, bad.reshape(-1), d)
+    with pytest.raises(ValueError):
+        ft3 = _plan.feature_tiles(16, 3)
+        _plan.tile_coefficients(ft3.quads, ft3.coef, 16)
 
 
 def test_feature_tiles_limits():
