@@ -250,10 +250,14 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // num^T += V^T P^T.  X is accumulated in two halves of the dimensions (4 independent chains).
   // NODE: coreset items (weight, active rows) instead of the tile's own keys.
   // node_tag: 0 the tile's own keys, 1 coreset items with their active-row test, 2 coreset items active
-  // on every row of the tile (the test is skipped)
+  // on every row of the tile (the test is skipped), 3 as 2 for degree <= 2 without the exp clamp: the
+  // Horner form stops at y^2 and the logit is not clamped (the same values for every finite logit:
+  // with k3 = 0 the third fused multiply-add returns k2 exactly, and min(y, inf) = y), two VALU
+  // instructions fewer per (row, item) pair on the most frequent batch kind
   auto process = [&](auto node_tag) {
     constexpr bool NODE = decltype(node_tag)::value != 0;
-    constexpr bool FULL = decltype(node_tag)::value == 2;
+    constexpr bool FULL = decltype(node_tag)::value >= 2;
+    constexpr bool FAST = decltype(node_tag)::value == 3;
     // weights of subtile kt from its logits X (key 16 kt + 4 lg + r, row myrow[rs]), elementwise
     auto weights = [&](int kt, const floatx4 (&X)[RS], floatx4 (&P)[RS]) {
 #pragma unroll
@@ -266,8 +270,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         for (int rs = 0; rs < RS; ++rs) {
           const int i = myrow[rs];
           const float yv = X[rs][r];
-          const float ex = __builtin_amdgcn_exp2f(fminf(yv, ymax));
-          const float tp = taylor2<!SPLIT>(yv, tc);
+          const float ex = __builtin_amdgcn_exp2f(FAST ? yv : fminf(yv, ymax));
+          const float tp = FAST ? fmaf(yv, fmaf(yv, tc.k2, tc.k1), 1.0f) : taylor2<!SPLIT>(yv, tc);
           float p;
           if constexpr (FULL) {
             p = (ex - tp) * w;  // rows outside the sequence have zero queries and are never stored
@@ -401,6 +405,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   using block_batch = std::integral_constant<int, 0>;
   using node_batch = std::integral_constant<int, 1>;
   using node_batch_full = std::integral_constant<int, 2>;
+  using node_batch_full_fast = std::integral_constant<int, 3>;
+  const bool fast = !a.exp_clamp && a.degree <= 2;
 
   // ---- batch sequence: phase A = contiguous keys [kstart, kend), phase B = the node item list ----
   int kstart = static_cast<int>(chunk_start(row_lo, a.chunk, a.shift));
@@ -590,7 +596,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     // staged batch and list visible; whether every staged item is active on all rows of the tile
     const bool full = __syncthreads_and(item_full ? 1 : 0) != 0;
     if (nxt_have) prefetch(nxt_node, nxt_off);
-    if (cur_node && full)
+    if (cur_node && full && fast)
+      process(node_batch_full_fast{});
+    else if (cur_node && full)
       process(node_batch_full{});
     else if (cur_node)
       process(node_batch{});
