@@ -23,6 +23,12 @@ query(q) for every stream, block completions (compress + merges) included.  valu
 roofline of the moment-state read (HBM); CPU baseline = the reference's per-token streaming object
 restated in oracle/, one stream with the same state sizes.
 
+`--workload prefill_flat_c2` (8 x 16 heads, N = 4096, d = dv = 64, degree 2, block 256, scale 1/8, bf16
+inputs ~ N(0, 1), the drop-in fast path with the flat sorted_pair coreset) and `--workload
+prefill_levels_c4` (4 x 32 heads, N = 16384, d = 16, dv = 64, degree 3 (969 features), block 128, scale 1,
+fp32, q and k in the radius-1.5 ball, levels) are the same measurement on the other prefill
+configurations.
+
 `--workload flash_c3` measures the exact causal softmax baseline (triton_flash_causal_attention) on the
 default workload's inputs (1 x 32 heads, N = 65536, d = dv = 64, scale 1/8, fp32): value =
 head-tokens/s, roofline of the flash kernel against the fp32 MFMA peak (algorithmic (d + dv) N (N + 1)
@@ -53,6 +59,16 @@ WORKLOAD = dict(workload="prefill_levels_c3", batch=1, heads=32, seq_len=65536, 
 DECODE = dict(workload="decode_levels_c5", batch=64, heads=32, prefix=32768, d=64, dv=64, degree=2, block=256,
               scale=0.125, compressor="sorted_pair", data="N(0,1)/8", dtype="bf16", seed=0)
 
+# the other prefill configurations, as secondary bench lines (`--workload`): the batched bf16 prefill
+# through the drop-in fast path (flat coreset) and the degree-3 long-sequence prefill (levels)
+PREFILL_C2 = dict(workload="prefill_flat_c2", batch=8, heads=16, seq_len=4096, d=64, dv=64, degree=2, block=256,
+                  scale=0.125, compressor="sorted_pair", semantics="flat (fast_article_causal_attention)",
+                  data="N(0,1)", dtype="bf16", seed=0)
+PREFILL_C4 = dict(workload="prefill_levels_c4", batch=4, heads=32, seq_len=16384, d=16, dv=64, degree=3, block=128,
+                  scale=1.0, compressor="sorted_pair", semantics="merge-and-reduce levels", data="unit_ball r=1.5",
+                  dtype="fp32", seed=0)
+PREFILL = {w["workload"]: w for w in (WORKLOAD, PREFILL_C2, PREFILL_C4)}
+
 FLASH = dict(WORKLOAD, workload="flash_c3", semantics="exact causal softmax attention")
 for _k in ("degree", "block", "compressor"):
     del FLASH[_k]
@@ -65,17 +81,20 @@ SPLIT_BF16_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 3.0
 HBM_PEAK_GBS = 8000.0
 
 
-def make_inputs(batch, heads, n, d, dv, seed):
-    """randn q, k, v then ball radii rand^(1/d) for q then k (the reference's draw order)."""
+def make_inputs(batch, heads, n, d, dv, seed, radius=1.0, ball=True):
+    """randn q, k, v then ball radii radius * rand^(1/d) for q then k (the reference's draw order,
+    fast_article_attention.py:738-750); ball=False: q, k, v ~ N(0, 1)."""
     g = torch.Generator(device="cpu")
     g.manual_seed(seed)
     q = torch.randn(batch, heads, n, d, generator=g)
     k = torch.randn(batch, heads, n, d, generator=g)
     v = torch.randn(batch, heads, n, dv, generator=g)
+    if not ball:
+        return q, k, v
     qn = torch.clamp(torch.linalg.vector_norm(q, dim=-1, keepdim=True), min=1e-12)
     kn = torch.clamp(torch.linalg.vector_norm(k, dim=-1, keepdim=True), min=1e-12)
-    rq = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d)
-    rk = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d)
+    rq = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d) * radius
+    rk = torch.rand(batch, heads, n, 1, generator=g).pow(1.0 / d) * radius
     return q / qn * rq, k / kn * rk, v
 
 
@@ -99,15 +118,19 @@ def cpu_baseline(q, k, v, w):
     threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "16384"))
-    t = oracle.time_fast_path_sample(q[0, 0].contiguous(), k[0, 0].contiguous(), v[0, 0].contiguous(),
+    # 16-bit inputs: the oracle runs on their values upcast to fp32 (the GPU computes in fp32 too)
+    t = oracle.time_fast_path_sample(q[0, 0].float().contiguous(), k[0, 0].float().contiguous(),
+                                     v[0, 0].float().contiguous(),
                                      degree=w["degree"], block=w["block"], scale=w["scale"], seed=w["seed"], rows=rows)
     n = w["seq_len"]
+    rows = min(rows, n)
+    general = " with the general feature map (the reference fast path raises for degree 3)" if w["degree"] > 2 else ""
     return {
         "value": n / t["total_s"],
         "unit": "head-tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"reference CPU fast path restated in oracle/ (stream moments, flat sorted_pair coreset, "
+        "sample": (f"reference CPU fast path restated in oracle/{general} (stream moments, flat sorted_pair coreset, "
                    f"query chunks of 2048), 1 head of the workload (N={n}); token loop, q x reps residual and "
                    f"in-block residual timed over the first {rows} rows and scaled by N/{rows}, reps built "
                    f"for all N; per-part seconds/head {json.dumps({k2: round(v2, 3) for k2, v2 in t.items()})}"),
@@ -120,10 +143,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 10; decode 256)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps first (default 2; decode 8)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--seq-len", type=int, default=WORKLOAD["seq_len"])
-    ap.add_argument("--heads", type=int, default=WORKLOAD["heads"])
+    ap.add_argument("--seq-len", type=int, default=None, help="override the prefill workload's N")
+    ap.add_argument("--heads", type=int, default=None, help="override the prefill workload's heads")
     ap.add_argument("--workload", default=WORKLOAD["workload"],
-                    choices=[WORKLOAD["workload"], DECODE["workload"], FLASH["workload"]])
+                    choices=list(PREFILL) + [DECODE["workload"], FLASH["workload"]])
     ap.add_argument("--streams", type=int, default=DECODE["batch"] * DECODE["heads"], help="decode streams")
     ap.add_argument("--prefix", type=int, default=DECODE["prefix"], help="decode prefix tokens")
     ap.add_argument("--flash-dtype", default="fp32", choices=["fp32", "bf16", "fp16"],
@@ -163,26 +186,39 @@ def main() -> int:
     import _plan
     import streaming_taylor_coreset_attention as stc
 
-    w = dict(WORKLOAD, seq_len=args.seq_len, heads=args.heads)
+    import fast_article_attention as faa
+
+    w = dict(PREFILL[args.workload])
+    if args.seq_len is not None:
+        w["seq_len"] = args.seq_len
+    if args.heads is not None:
+        w["heads"] = args.heads
     bh, n, d, dv = w["batch"] * w["heads"], w["seq_len"], w["d"], w["dv"]
+    flat = w["semantics"].startswith("flat")
+    ball = w["data"].startswith("unit_ball")
+    in_dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[w["dtype"]]
     print(f"[bench] generating inputs {w['batch']}x{w['heads']}x{n}x{d}", file=sys.stderr, flush=True)
-    q, k, v = make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"])
+    q, k, v = make_inputs(w["batch"], w["heads"], n, d, dv, w["seed"],
+                          radius=float(w["data"].split("r=")[1]) if ball else 1.0, ball=ball)
+    q, k, v = q.to(in_dtype), k.to(in_dtype), v.to(in_dtype)  # bf16 inputs: generated in fp32, then cast
     dev = torch.device("cuda:0")
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     q3, k3, v3 = qd.reshape(bh, n, d), kd.reshape(bh, n, d), vd.reshape(bh, n, dv)
 
     t_plan = time.perf_counter()
-    plan = _plan.levels_plan(n, w["block"], w["compressor"])
+    plan = (_plan.flat_plan if flat else _plan.levels_plan)(n, w["block"], w["compressor"])
     _plan.draws_for(plan, _plan.sequence_seeds(w["seed"], bh), d, w["compressor"])
     t_plan = time.perf_counter() - t_plan
 
     def step(timer=None):
         return _engine.prefill(q3, k3, v3, degree=w["degree"], block=w["block"], scale=w["scale"],
-                               semantics="levels", compressor=w["compressor"], seed=w["seed"], timer=timer)
+                               semantics="flat" if flat else "levels", compressor=w["compressor"], seed=w["seed"],
+                               out_dtype=in_dtype, timer=timer)
 
     # the public API path once, checked against the engine call the timing uses
-    api_out = stc.article_causal_attention(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"],
-                                           compressor=w["compressor"], seed=w["seed"])
+    api = faa.fast_article_causal_attention if flat else stc.article_causal_attention
+    api_out = api(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"],
+                  compressor=w["compressor"], seed=w["seed"])
     res = step()
     for _ in range(args.warmup - 1):
         step()
