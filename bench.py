@@ -274,6 +274,8 @@ def main() -> int:
             "peak_basis": ("fp32-equivalent flops of split-bf16 products: bf16 dense peak / 3 (three bf16 "
                            "matrix-core products per fp32 product)" if split else "fp32 matrix-core peak"),
             "traffic": measured_traffic(w["workload"], "moments_kernel"),
+            # the same fp32-equivalent rate against the bound fp32 matrix-core products would have
+            "achieved_vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS,
             "algorithmic_flops_per_launch": mom_flops,
             "avg_launch_ms": mom_ms,
         },
