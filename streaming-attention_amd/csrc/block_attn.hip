@@ -351,6 +351,14 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         floatx4 P[2][RS];
         weights(2 * sp, xc[0], P[0]);
         weights(2 * sp + 1, xc[1], P[1]);
+        if (sp + 1 < NSUB / 2) {
+          // the 6 RS MS products of X(sp + 1) spread over the weights' VALU of subtiles 2 sp, 2 sp + 1
+#pragma unroll
+          for (int g = 0; g < 6 * RS * MS; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          }
+        }
         pv2(sp, P);
       }
     } else {
