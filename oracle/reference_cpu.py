@@ -483,6 +483,23 @@ def segment_mean_coreset(k: Tensor, v: Tensor, block: int, stride: int) -> Tuple
     return rk, rv, rpb
 
 
+def segment_rep_weight(stride: int) -> float:
+    """A segment-mean representative stands for `stride` tokens: its residual term is multiplied by the
+    stride (triton_article_attention.py:357, `* compress_stride`)."""
+    return float(stride)
+
+
+def segment_rep_active_from(rep_block: Tensor, block: int) -> Tensor:
+    """First query row that sees the representatives of block rep_block: the row after the block ends
+    (triton_article_attention.py:353-355, `offs_m >= (rep_block + 1) * BLOCK_SIZE`)."""
+    return (rep_block + 1) * block
+
+
+def clamped_exp(x: Tensor) -> Tensor:
+    """exp(min(x, 80)), the Triton kernel's guard against overflow (triton_article_attention.py:333, :356)."""
+    return torch.exp(torch.clamp(x, max=80.0))
+
+
 def segment_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int, block: int, stride: int, scale: Optional[float] = None,
                     eps: float = 1e-12) -> Tensor:
     """Semantics of the fused Triton article kernel for [BH, N, D] in fp64: exp_{<=t} over the whole
@@ -497,14 +514,14 @@ def segment_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int, block: int,
     causal = pos[None, :] <= pos[:, None]
     same = (pos[None, :] // block) == (pos[:, None] // block)
     tay = exp_taylor(x, degree)
-    p = torch.where(causal, tay, torch.zeros_like(tay)) + torch.where(causal & same, torch.exp(torch.clamp(x, max=80.0)) - tay, torch.zeros_like(tay))
+    p = torch.where(causal, tay, torch.zeros_like(tay)) + torch.where(causal & same, clamped_exp(x) - tay, torch.zeros_like(tay))
     num = p @ v64
     den = p.sum(-1)
     if rk.shape[1]:
         xr = (q64 @ rk.transpose(-1, -2)) * s
         rep_block = torch.arange(rk.shape[1]) // rpb
-        active = pos[:, None] >= ((rep_block + 1) * block)[None, :]
-        r = torch.where(active, torch.exp(torch.clamp(xr, max=80.0)) - exp_taylor(xr, degree), torch.zeros_like(xr)) * stride
+        active = pos[:, None] >= segment_rep_active_from(rep_block, block)[None, :]
+        r = torch.where(active, clamped_exp(xr) - exp_taylor(xr, degree), torch.zeros_like(xr)) * segment_rep_weight(stride)
         num = num + r @ rv
         den = den + r.sum(-1)
     return num / torch.clamp(den[..., None], min=eps)

@@ -360,7 +360,8 @@ class DecodeState:
             else:
                 kp, koff = torch.zeros((self.S, hi - lo, width), device=self.device, dtype=k.dtype), 0
                 kp[..., : self.d] = k[:, lo:hi]
-            if self.ldv == self.dv and v.is_contiguous() and v.data_ptr() % 16 == 0 and koff == lo:
+            # v in place only next to k in place: both are then read at row lo of [S, p_total, .] rows
+            if kp is k and self.ldv == self.dv and v.is_contiguous() and v.data_ptr() % 16 == 0:
                 vp = v
             else:
                 vp = torch.zeros((self.S, kp.shape[1], self.ldv), device=self.device, dtype=k.dtype)

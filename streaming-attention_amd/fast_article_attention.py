@@ -195,6 +195,8 @@ def low_degree_taylor_causal_sums(
     f = num_taylor_features(q.shape[-1], degree)
     s = _attention_scale(scale, q.shape[-1])
     home = q.device
+    if q.shape[0] == 0:  # the reference's token loop and cumsum return empty sums
+        return q.new_empty((0, v.shape[-1])), q.new_empty((0,)), f
     (qg, kg, vg), _ = _to_gpu(q, k, v)
     dt = _compute_dtype(qg)
     res = _engine.prefill(qg.to(dt)[None], kg.to(dt)[None], vg.to(dt)[None], degree=degree, block=1, scale=s,
@@ -312,6 +314,12 @@ def fast_article_causal_attention_single(
     dv = v.shape[-1]
     _check_compressor(compressor, n, block_size)
     home = q.device
+    if n == 0:  # nothing to attend: the reference returns an empty [0, Dv] output
+        out = q.new_empty((0, dv))
+        if not return_stats:
+            return out
+        return out, _stats(n, dim, dv, q.element_size(), degree, block_size, compressor, query_chunk_size, low_mode,
+                           home.type)
     (qg, kg, vg), _ = _to_gpu(q, k, v)
     dt = _compute_dtype(qg)
     res = _run_bh(qg.to(dt)[None], kg.to(dt)[None], vg.to(dt)[None], degree=degree, block_size=block_size,

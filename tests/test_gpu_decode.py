@@ -141,6 +141,32 @@ def test_extend_then_step(prefix):
     assert rel(outs, ref[:, prefix:]) < FP32_TOL
 
 
+@pytest.mark.parametrize("how", ["extend", "prefill"])
+def test_extend_padded_keys_with_values_in_place(how):
+    """d = 6 needs a zero-padded copy of the keys (16-byte rows) while dv = 32 rows could be read in
+    place: the values must then be copied next to the key copy (rows [0, nb B) of the whole blocks), for
+    a prompt that ends in a partial block.  The following steps == the prefill rows."""
+    streams, n, p, d, dv, block = 3, 120, 40, 6, 32, 16
+    q, k, v = _data(streams, n, d, dv, seed=17, scale_in=0.5)
+    ref = stc.article_causal_attention(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=2,
+                                       block_size=block, scale=0.5, seed=3)[0]
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=0.5, device=DEV, seed=3,
+                                       streams=streams)
+    qd, kd, vd = q.to(DEV).contiguous(), k.to(DEV).contiguous(), v.to(DEV).contiguous()
+    if how == "extend":
+        st.extend(kd[:, :p].contiguous(), vd[:, :p].contiguous())
+    else:
+        head = st.prefill(qd[:, :p].contiguous(), kd[:, :p].contiguous(), vd[:, :p].contiguous())
+        assert rel(head, ref[:, :p]) < FP32_TOL
+    assert st.length == p
+    den, num = st._st.full_moments()
+    phi = orc.features(k[:, :p].double(), 2, key_side=True)  # [S, p, F]
+    assert rel(den.cpu(), phi.sum(1)) < 1e-6
+    assert rel(num.cpu(), phi.transpose(1, 2) @ v[:, :p].double()) < 1e-6
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(p, n)], dim=1)
+    assert rel(outs, ref[:, p:]) < FP32_TOL
+
+
 def test_prefill_then_step_bf16():
     """prefill() of a prompt returns the prompt's outputs and leaves the state for decoding
     (the decode workload's regime: q, k, v ~ N(0,1)/8, bf16, scale 1/8, block 256)."""

@@ -296,6 +296,20 @@ def test_fast_path_argument_errors():
         faa.exp_taylor(torch.zeros(2), -1)
 
 
+def test_empty_sequences_return_empty_outputs_on_the_host():
+    """N = 0: the reference returns empty outputs (its token loop and chunk loops do not run); nothing
+    is launched, so this holds without a GPU."""
+    q, k, v = torch.zeros(0, 6), torch.zeros(0, 6), torch.zeros(0, 3)
+    out = faa.fast_article_causal_attention(q, k, v)
+    assert out.shape == (0, 3) and out.dtype == torch.float32
+    out, st = faa.fast_article_causal_attention_single(q, k, v, return_stats=True)
+    assert out.shape == (0, 3) and st.coreset_items == 0 and st.feature_count == 28
+    num, den, f = faa.low_degree_taylor_causal_sums(q, k, v)
+    assert num.shape == (0, 3) and den.shape == (0,) and f == 28
+    out4 = faa.fast_article_causal_attention(q[None, None], k[None, None], v[None, None])
+    assert out4.shape == (1, 1, 0, 3)
+
+
 def test_streaming_argument_errors():
     q, k, v = _qkv()
     with pytest.raises(ValueError):

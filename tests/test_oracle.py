@@ -52,7 +52,7 @@ def test_features_match_reference_fast_path(golden):
     assert np.array_equal(orc.features(x, 2, False).numpy(), g["query2"])
 
 
-@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+@pytest.mark.parametrize("degree", [0, 1, 2, 3, 4])
 def test_feature_inner_product_is_truncated_exp(degree):
     g = torch.Generator().manual_seed(degree)
     q = torch.randn(9, 5, generator=g, dtype=torch.float64)
@@ -331,6 +331,78 @@ def test_segment_forward_stride1_is_exact():
     v = torch.randn(2, 40, 4, generator=g)
     out = orc.segment_forward(q, k, v, degree=2, block=8, stride=1, scale=1.0)
     assert rel(out, orc.classical_attention(q, k, v, 1.0)) < 1e-12
+
+
+def _segment_constant(n, d, dv, stride, seed, amp=0.8):
+    """q random; k and v constant inside every stride segment [s*stride, (s+1)*stride), so a segment's
+    mean is each of its tokens."""
+    g = torch.Generator().manual_seed(seed)
+    nseg = -(-n // stride)
+    q = torch.randn(2, n, d, generator=g, dtype=torch.float64) * amp
+    k = (torch.randn(2, nseg, d, generator=g, dtype=torch.float64) * amp).repeat_interleave(stride, dim=1)[:, :n]
+    v = torch.randn(2, nseg, dv, generator=g, dtype=torch.float64).repeat_interleave(stride, dim=1)[:, :n]
+    return q, k, v
+
+
+@pytest.mark.parametrize("block,stride,n,degree", [(8, 2, 45, 2), (16, 4, 70, 2), (16, 8, 64, 1), (12, 3, 50, 0),
+                                                   (8, 8, 33, 2)])
+def test_segment_forward_segment_constant_is_exact(block, stride, n, degree):
+    """With keys and values constant inside every stride segment, a segment-mean representative
+    weighted by the stride stands in exactly for the stride tokens it averages, and the completed
+    blocks' representatives cover exactly the keys before the row's block: the Triton semantics at any
+    stride then equal causal softmax attention (logits far below the clamp at 80)."""
+    q, k, v = _segment_constant(n, 8, 5, stride, seed=block + stride + n)
+    out = orc.segment_forward(q, k, v, degree=degree, block=block, stride=stride, scale=1.0)
+    assert rel(out, orc.classical_attention(q, k, v, 1.0)) < 1e-12
+
+
+def test_segment_forward_clamp_closed_form():
+    """exp(min(x, 80)) on both residual terms, checked against a hand evaluation (d = dv = 1, scale 1,
+    block 2, stride 2, degree 2, n = 3):
+      keys 9, 11, 10; values 1, 3, -1; queries 0.5, 9, 9.
+      row 0: only key 0 -> v0.
+      row 1 (logits 81, 99, both clamped): Taylor over keys 0, 1 plus the exact in-block residual ->
+             (e^80 v0 + e^80 v1) / (2 e^80).
+      row 2 (logits 81, 99, 90): Taylor over keys 0..2, in-block residual of key 2 (clamped to 80), and
+             block 0's one representative (key 10, value 2, logit 90 clamped, weight 2):
+             (T(81) v0 + T(99) v1 + e^80 v2 + 2 (e^80 - T(90)) 2) / (T(81) + T(99) + e^80 + 2 (e^80 - T(90))),
+             T(x) = 1 + x + x^2 / 2."""
+    T = lambda x: 1.0 + x + x * x / 2.0
+    e80 = math.exp(80.0)
+    k = torch.tensor([[[9.0], [11.0], [10.0]]], dtype=torch.float64)
+    v = torch.tensor([[[1.0], [3.0], [-1.0]]], dtype=torch.float64)
+    q = torch.tensor([[[0.5], [9.0], [9.0]]], dtype=torch.float64)
+    out = orc.segment_forward(q, k, v, degree=2, block=2, stride=2, scale=1.0)[0, :, 0]
+    row0 = 1.0
+    row1 = (e80 * 1.0 + e80 * 3.0) / (2 * e80)
+    num2 = T(81) * 1.0 + T(99) * 3.0 + e80 * -1.0 + 2 * (e80 - T(90)) * 2.0
+    den2 = T(81) + T(99) + e80 + 2 * (e80 - T(90))
+    expect = torch.tensor([row0, row1, num2 / den2], dtype=torch.float64)
+    assert torch.allclose(out, expect, rtol=1e-12, atol=0)
+    assert abs(float(out[1]) - 2.0) < 1e-12 and abs(float(out[2]) - 1.0) < 1e-9  # the clamp equalises
+
+
+@pytest.mark.parametrize("mistake", ["weight_one", "active_one_block_early", "active_one_block_late", "no_clamp"])
+def test_planted_segment_mistakes_are_caught(monkeypatch, mistake):
+    """Each plausible slip in the Triton semantics fails one of the two pins above."""
+    if mistake == "weight_one":
+        monkeypatch.setattr(orc, "segment_rep_weight", lambda stride: 1.0)
+    elif mistake == "active_one_block_early":
+        monkeypatch.setattr(orc, "segment_rep_active_from", lambda rb, block: rb * block)
+    elif mistake == "active_one_block_late":
+        monkeypatch.setattr(orc, "segment_rep_active_from", lambda rb, block: (rb + 2) * block)
+    else:
+        monkeypatch.setattr(orc, "clamped_exp", torch.exp)
+    failed = []
+    try:
+        test_segment_forward_segment_constant_is_exact(8, 2, 45, 2)
+    except AssertionError:
+        failed.append("segment_constant")
+    try:
+        test_segment_forward_clamp_closed_form()
+    except AssertionError:
+        failed.append("clamp")
+    assert failed, f"planted mistake {mistake} passed both pins"
 
 
 # --------------------------------------------------------------------------- planted mistakes
