@@ -84,6 +84,35 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
                 int products, int columns, const uint32_t* feat_quads, const float* feat_coef, float* low_num,
                 float* low_den, void* stream);
 
+/*
+ * Wave-specialised form of sta_moments (split-bf16 products, degree <= 3): moments over all keys before
+ * each row's *query block* of query_block rows (a multiple of 32, at least 64; blocks offset by shift
+ * like the chunks, block b covers rows [b*query_block - shift, (b+1)*query_block - shift)).  Same
+ * reference functions as sta_moments; with query_block equal to the article block the residual
+ * kernel's in-block keys carry exp(x) whole (sta_block_attention with chunk = query_block).
+ *   One workgroup of 512 threads per (head, feature split, group of 16*column_tiles value columns):
+ *   4 update waves keep the fp32 state, 4 query waves a frozen split copy refreshed once per block.
+ *   feat_quads [fsplit][4][slot_tiles][4] / feat_coef [fsplit][4][slot_tiles][16]: 4 slots of
+ *     slot_tiles tiles per feature split (layout and coefficient rules of sta_moments, per-tile query
+ *     coefficients at degree <= 2); mixed = 1: slots 2 and 3 hold slot_tiles - 1 real tiles (their
+ *     last table tile is padding).  slot_tiles must satisfy sta_moments_ws_ok.
+ *   column_tiles: 4 (64 columns per workgroup; ceil(dv/32) must be even) or 2 (32 columns).
+ *   handoff: caller-allocated scratch of sta_moments_ws_handoff_bytes(...) bytes, 16-byte aligned (the
+ *     per-workgroup copy of the state between the update and the query waves; contents undefined
+ *     before and after the call).
+ *   q / k / v row rules, outputs and their layout as for sta_moments.
+ */
+int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                   int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles, int mixed,
+                   int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
+                   float* low_num, float* low_den, void* stream);
+
+/* 1 when sta_moments_ws runs (d, degree, slot_tiles, column_tiles, dv), else 0. */
+int sta_moments_ws_ok(int d, int degree, int slot_tiles, int column_tiles, int dv);
+
+/* Bytes of sta_moments_ws' handoff scratch for bh heads, fsplit splits, slot_tiles, column_tiles, dv. */
+int64_t sta_moments_ws_handoff_bytes(int64_t bh, int fsplit, int slot_tiles, int column_tiles, int dv);
+
 /* 1 when sta_moments runs (d, degree, dv, wave_tiles, products) with columns = 64: one workgroup per
  * (head, feature split) covering all value columns (split-bf16 products, 32 < dv <= 64, mixed = 0;
  * one workgroup per compute unit). */
@@ -209,7 +238,9 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *   tile_ptr[n_tiles+1] / tile_nodes: CSR list of the nodes each tile needs.
  *   node_meta[n_nodes][4]: item count, first and last active row, materialized flag (items index
  *     rep_k/rep_v instead of k/v).
- *   low_num / low_den: sta_moments' partial outputs (sta_moment_partials_layout), fsplit splits.
+ *   low_num / low_den: sta_moments' (or sta_moments_ws') partial outputs (sta_moment_partials_layout),
+ *     fsplit splits; chunk: their chunk (sta_moment_chunk) or query block, a multiple of the moment
+ *     chunk that divides or is a multiple of the tile rows.
  *   ld_qk / ld_v: row strides (elements) of q, k and of v, multiples of 4 (rows are read in units of
  *     4 elements; pad them with zero columns), bases 16-byte aligned.
  *   rep_k / rep_v (fp32, row strides ld_rep_k / ld_rep_v, multiples of 4): materialized items
@@ -242,7 +273,9 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
 int sta_flash_attention(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d,
                         int dv, int ld_qk, int ld_v, float scale, void* out, int out_dtype, void* stream);
 
-/* Rows per block-attention tile and the moment chunk the library uses for a head dimension D. */
+/* Rows per block-attention tile and the moment chunk the library uses for a head dimension D (the
+ * chunk argument of sta_block_attention is that chunk for sta_moments' partials, the query block for
+ * sta_moments_ws' partials). */
 int sta_tile_rows(void);
 int sta_moment_chunk(int d);
 

@@ -45,6 +45,38 @@ def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
     return st
 
 
+# The wave-specialised moment kernel (sta_moments_ws: update and query waves, 64 value columns per
+# workgroup, the queries answered against the state before their article block) for split products at
+# degree <= 3 whenever the article block is a whole number (>= 2) of moment chunks.  Chosen where it
+# measured faster (one MI355X, A/B in one session, K1 / whole step):
+#   8 x 16 heads x 4096, bf16, degree 2, block 256:     2.33 -> 1.88 ms / 3.47 -> 3.04 ms
+#   4 x 32 heads x 16384, fp32, degree 3, block 128:    6.21 -> 5.07 ms / 7.97 -> 6.98 ms
+#   1 x 32 heads x 65536, fp32, degree 2, block 256:    7.34 -> 7.32 ms / 10.31 -> 10.58 ms
+# The last is a tie in the scan and a loss in the step: sta_moments' mixed tile counts free half the
+# compute units early, where the side-stream compressor runs; sta_moments_ws' workgroups all end
+# together.  So: 16-bit inputs or degree 3 (MOMENT_WS_POLICY "auto"); "always" / "never" override.
+MOMENT_WS_POLICY = os.environ.get("STA_MOMENT_WS", "auto")  # "auto" | "always" | "never"
+
+
+def use_moments_ws(element_size: int, degree: int) -> bool:
+    if MOMENT_WS_POLICY in ("always", "1"):
+        return True
+    if MOMENT_WS_POLICY in ("never", "0"):
+        return False
+    return element_size == 2 or degree == 3
+
+
+def ws_query_block(semantics: str, block: int) -> Optional[int]:
+    """Query block of sta_moments_ws for a prefill, or None for sta_moments: the article block where the
+    residual kernel's in-block keys start at the block (flat, levels, segment), any block where every
+    key is in the residual (exact)."""
+    if semantics in ("flat", "levels", "segment"):
+        return block if block % 32 == 0 and block >= 64 else None
+    if semantics == "exact":
+        return 256
+    return None  # raw Taylor sums: the residual kernel adds the polynomial over the query block's keys
+
+
 # Offer the planner the 64-column moment workgroups (split products, 32 < dv <= 64).  Off: on 32 heads x
 # 65536 tokens (d = dv = 64) they take 9.6 ms against 8.4 ms for two 32-column workgroups per compute
 # unit; the feature work they save (17 % of the VALU) is less than one wave per SIMD loses in latency.
@@ -159,8 +191,10 @@ def prefill(
     timer: Optional[KernelTimer] = None,
     products: Optional[int] = None,
     residual_products: Optional[int] = None,
+    moment_kernel: Optional[str] = None,
 ) -> PrefillResult:
-    """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype."""
+    """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype.  moment_kernel:
+    "ws" (sta_moments_ws where it applies), "chunked" (sta_moments) or None (use_moments_ws)."""
     if semantics not in SEMANTICS:
         raise ValueError(f"semantics must be one of {SEMANTICS}")
     for t in (q3, k3, v3):
@@ -189,13 +223,24 @@ def prefill(
     dm = _unit_width(d, q3.element_size())
     ft = _plan.feature_tiles(dm, degree)
     k1_products = MOMENT_PRODUCTS if products is None else int(products)
-    ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
-                            mixed_nts=_native.moment_mixed_tiles(dm, degree),
-                            wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
+    qblock = ws_query_block(semantics, block) if (k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 3 and
+                                                  (use_moments_ws(q3.element_size(), degree) if moment_kernel is None
+                                                   else moment_kernel == "ws")) else None
+    ws_ct = 4 if (-(-dv // 32)) % 2 == 0 else 2
+    ws_opts = _native.moment_ws_slot_tiles(dm, degree, ws_ct, dv) if qblock else ()
+    if ws_opts:
+        ms = _plan.moment_split_ws(ft, bh, dv, ws_opts, ws_ct)
+        chunk = qblock
+    else:
+        qblock = None
+        ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
+                                mixed_nts=_native.moment_mixed_tiles(dm, degree),
+                                wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
     fsplit = ms.fsplit
     # split products at degree <= 2 apply one coefficient per tile on the query side
     tile_coef = k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 2
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef), dev,
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef, ms.columns,
+                              qblock is not None), dev,
                              lambda: (_i32(ms.quads, dev),
                                       _f32(_plan.tile_coefficients(ms.quads, ms.coef, dm) if tile_coef else ms.coef,
                                            dev)))
@@ -246,13 +291,24 @@ def prefill(
 
     mq, mk, mv = _padded_rows(q3, dm), _padded_rows(k3, dm), _padded_rows(v3, -(-dv // 32) * 32)
 
-    def k1():
-        st = lib.sta_moments(
-            mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
-            float(scale), chunk, shift,
-            fsplit, ms.wave_tiles, int(ms.mixed), k1_products, ms.columns,
-            fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
-        _native.check(st, "sta_moments")
+    if qblock is not None:
+        hbytes = lib.sta_moments_ws_handoff_bytes(bh, fsplit, ms.wave_tiles, ws_ct, dv)
+        handoff = torch.empty((max(hbytes, 16) // 4,), device=dev, dtype=torch.float32)
+
+        def k1():
+            st = lib.sta_moments_ws(
+                mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
+                float(scale), qblock, shift, fsplit, ms.wave_tiles, int(ms.mixed), ws_ct,
+                fidx.data_ptr(), fcoef.data_ptr(), handoff.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+            _native.check(st, "sta_moments_ws")
+    else:
+        def k1():
+            st = lib.sta_moments(
+                mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
+                float(scale), chunk, shift,
+                fsplit, ms.wave_tiles, int(ms.mixed), k1_products, ms.columns,
+                fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+            _native.check(st, "sta_moments")
 
     # The compressor needs only the keys and the draws: on a second stream (default priority), released
     # before the moment scan is queued, it runs in the compute units the scan leaves idle (its shorter

@@ -45,6 +45,13 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
          _i32, _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sta_moments_ws": (
+        _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
+    ),
+    "sta_moments_ws_ok": (_i32, [_i32, _i32, _i32, _i32, _i32]),
+    "sta_moments_ws_handoff_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32]),
     "sta_moment_columns_ok": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "sta_moment_mixed_ok": (_i32, [_i32, _i32, _i32]),
     "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),
@@ -205,3 +212,12 @@ def moment_wide_tiles(d: int, degree: int, dv: int, products: int) -> tuple:
     """Per-wave tile counts the 64-column moment kernels run for (d, degree, dv, products)."""
     lib_ = lib()
     return tuple(nt for nt in (5,) if lib_.sta_moment_columns_ok(d, degree, dv, nt, products))
+
+
+WS_SLOT_TILES = (2, 3, 4, 5)  # candidates the planner offers sta_moments_ws_ok
+
+
+def moment_ws_slot_tiles(d: int, degree: int, column_tiles: int, dv: int) -> tuple:
+    """Tiles per slot the wave-specialised moment kernel runs for (d, degree, column_tiles, dv)."""
+    lib_ = lib()
+    return tuple(nt for nt in WS_SLOT_TILES if lib_.sta_moments_ws_ok(d, degree, nt, column_tiles, dv))

@@ -311,6 +311,66 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
                     tuple(wide_nts)), build)
 
 
+def moment_split_ws(ft: FeatureTiles, bh: int, dv: int, slot_options: Tuple[int, ...], column_tiles: int,
+                    compute_units: int = 256, allow_mixed: bool = True) -> MomentSplit:
+    """Work split of the wave-specialised moment kernel (sta_moments_ws): `fsplit` feature splits x
+    `csplit` groups of 16 * column_tiles value columns per head, one workgroup of 4 update and 4 query
+    waves per compute unit; a feature split holds 4 slots of `wave_tiles` tiles (mixed: slots 2 and 3
+    one tile less).  A SIMD runs the update wave of slot w and the query wave of slot (w + 2) & 3, so a
+    workgroup's time is proportional to 2 * wave_tiles - mixed; the choice minimises rounds of
+    workgroups times that, ties to fewer feature splits.  Same table layout as moment_split, with the
+    4 slots in place of the 4 waves."""
+
+    def build():
+        t = ft.n_tiles
+        csplit = -(-dv // (16 * column_tiles))
+        best = None
+        for nts in sorted(slot_options):
+            for mixed in (False, True):
+                if mixed and (nts < 2 or not allow_mixed):
+                    continue
+                per = 4 * nts - (2 if mixed else 0)
+                fsplit = -(-t // per)
+                rounds = -(-(bh * fsplit * csplit) // compute_units)
+                cost = rounds * (2 * nts - (1 if mixed else 0))
+                key = (cost, fsplit, mixed)
+                if best is None or key < best[0]:
+                    best = (key, fsplit, nts, mixed)
+        if best is None:
+            raise ValueError("no tile count for the wave-specialised moment kernel")
+        _, fsplit, nts, mixed = best
+        parts = fsplit * 4
+        caps = [nts - (1 if mixed and (j % 4) >= 2 else 0) for j in range(parts)]
+        # fill the slots in order, the last ones short when the tiles run out (padding tiles: coefficient 0)
+        sizes, left = [], t
+        per_fs = sum(caps[:4])
+        base_fs, extra = divmod(t, fsplit)
+        for fs in range(fsplit):
+            want = base_fs + (1 if fs < extra else 0)  # balance the real tiles over the feature splits
+            for j in range(4):
+                cap = caps[4 * fs + j]
+                take = min(cap, want, left)
+                sizes.append(take)
+                want -= take
+                left -= take
+        assert left == 0 and per_fs >= base_fs + (1 if extra else 0)
+        off = np.zeros(parts + 1, dtype=np.int32)
+        off[1:] = np.cumsum(sizes)
+        pad_quad = (ft.d + 1) | ((ft.d // 4 * 4) << 8) | (ft.d << 16) | (ft.d << 24)
+        quads = np.full((parts, nts, 4), pad_quad, dtype=np.uint32)
+        coef = np.zeros((parts, nts, 16), dtype=np.float32)
+        tiles_q = ft.quads.reshape(t, 4)
+        tiles_c = ft.coef.reshape(t, 16)
+        for j in range(parts):
+            cnt = sizes[j]
+            quads[j, :cnt] = tiles_q[off[j]:off[j] + cnt]
+            coef[j, :cnt] = tiles_c[off[j]:off[j] + cnt]
+        return MomentSplit(fsplit, csplit, nts, off, quads.reshape(-1), coef.reshape(-1), mixed, 16 * column_tiles)
+
+    return _cached(("msplit_ws", ft.d, ft.degree, bh, dv, tuple(slot_options), column_tiles, compute_units,
+                    allow_mixed), build)
+
+
 def tile_coefficients(quads: np.ndarray, coef: np.ndarray, d: int) -> np.ndarray:
     """The coefficient table of the split-product moment scan at degree <= 2 (moments.hip,
     mom_query_split): every tile's 16 entries set to one value c_t with

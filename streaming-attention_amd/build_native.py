@@ -2,9 +2,10 @@
 
     python streaming-attention_amd/build_native.py
 
-The library is 85 objects compiled in parallel and linked into one shared object: api.hip (entry
-points, compressor and decode kernels), launch_moments.hip (fp32 and split-bf16 products, 32 or 64 columns),
-launch_accumulate.hip, and
+The library is 89 objects compiled in parallel and linked into one shared object: api.hip (entry
+points, compressor and decode kernels), launch_moments_ws.hip (the wave-specialised moment scan, per
+element size and column-tile count), launch_moments.hip (fp32 and split-bf16 products, 32 or 64
+columns), launch_accumulate.hip, and
 launch_block.hip and launch_flash.hip once per residual / flash kernel configuration (padded key
 width, value-column tiles, element size).  Objects go to streaming-attention_amd/_build/.
 
@@ -24,7 +25,8 @@ import time
 HERE = pathlib.Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 # (source, object stem, defines), slowest first
-UNITS = (
+UNITS = tuple(("launch_moments_ws.hip", f"launch_moments_ws_{es}_{ct}", (f"-DSTA_WS_ES={es}", f"-DSTA_WS_CT={ct}"))
+              for es in (4, 2) for ct in (4, 2)) + (
     ("launch_moments.hip", "launch_moments_split", ("-DSTA_MOM_SPLIT=1",)),
     ("launch_moments.hip", "launch_moments_split64", ("-DSTA_MOM_SPLIT=1", "-DSTA_MOM_CG=64")),
     ("launch_moments.hip", "launch_moments", ("-DSTA_MOM_SPLIT=0",)),
@@ -60,12 +62,18 @@ def _messages(res_out: str) -> list[str]:
     return [ln for ln in res_out.splitlines() if NOISE not in ln]
 
 
-def build(verbose: bool = False) -> pathlib.Path:
+def build(verbose: bool = False, only: str = "") -> pathlib.Path:
+    """Compile every unit (or, with `only`, the units whose object stem starts with it, reusing the
+    other objects from an earlier build) and link the library."""
     OBJDIR.mkdir(exist_ok=True)
     cc = hipcc()
     jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
-    pending = list(UNITS)
-    running, failed, objs = [], [], []
+    pending = [u for u in UNITS if u[1].startswith(only)]
+    running, failed = [], []
+    objs = [str(OBJDIR / f"{stem}.o") for _, stem, _ in UNITS if not stem.startswith(only)]
+    missing = [o for o in objs if not pathlib.Path(o).exists()]
+    if missing:
+        raise RuntimeError(f"objects of an earlier build are missing: {missing[:3]}; build without `only`")
     t0 = time.time()
     while pending or running:
         while pending and len(running) < jobs:
@@ -105,5 +113,5 @@ def build(verbose: bool = False) -> pathlib.Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, only=sys.argv[1] if len(sys.argv) > 1 else ""))
     sys.exit(0)

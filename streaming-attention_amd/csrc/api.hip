@@ -7,7 +7,7 @@
 #include "compress.hip"
 #include "decode.hip"
 #include "flash_attn.hip"
-#include "moments.hip"
+#include "moments_ws.hip"
 
 namespace sta_api {
 thread_local int g_last_hip_error = 0;
@@ -162,6 +162,62 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if (columns == 64) return dispatch_moments<true, 64>(a, bh, s, wave_tiles, moment_extra_factors(degree));
   return products == STA_PRODUCTS_SPLIT_BF16 ? dispatch_moments<true, 32>(a, bh, s, wave_tiles, moment_extra_factors(degree))
                                              : dispatch_moments<false, 32>(a, bh, s, wave_tiles, moment_extra_factors(degree));
+}
+
+int sta_moments_ws_ok(int d, int degree, int slot_tiles, int column_tiles, int dv) {
+  if (d <= 0 || d > kMaxD || degree < 0 || degree > 3 || dv <= 0 || dv > kMaxDv) return 0;
+  if (column_tiles != 4 && column_tiles != 2) return 0;
+  if (column_tiles == 4 && ((dv + 31) / 32) % 2 != 0) return 0;
+  const int nx = moment_extra_factors(degree);
+  const bool big = d > 64;
+#define STA_CASE(NTS, NX, BIG) \
+  if (slot_tiles == NTS && nx == NX && big == BIG) return 1;
+  STA_MOMENT_WS_CONFIGS(STA_CASE)
+#undef STA_CASE
+  return 0;
+}
+
+int64_t sta_moments_ws_handoff_bytes(int64_t bh, int fsplit, int slot_tiles, int column_tiles, int dv) {
+  if (bh <= 0 || fsplit <= 0 || slot_tiles <= 0 || (column_tiles != 2 && column_tiles != 4) || dv <= 0) return -1;
+  const int64_t csplit = (dv + 16 * column_tiles - 1) / (16 * column_tiles);
+  const int64_t pairs = (slot_tiles + 1) / 2;
+  // [grid][2 parities][4 slots][pairs][column tiles][hi, lo][64 lanes] of 16 bytes
+  return bh * fsplit * csplit * 2 * 4 * pairs * column_tiles * 2 * 64 * 16;
+}
+
+int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                   int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles, int mixed,
+                   int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
+                   float* low_num, float* low_den, void* stream) {
+  if (!q || !k || !v || !feat_quads || !feat_coef || !handoff || !low_num || !low_den) return STA_ERR_ARG;
+  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || slot_tiles <= 0) return STA_ERR_SHAPE;
+  if (!sta_moments_ws_ok(d, degree, slot_tiles, column_tiles, dv)) return STA_ERR_UNSUPPORTED;
+  if (query_block < 2 * sta::MOM_C || query_block % sta::MOM_C != 0 || shift < 0 || shift >= sta::MOM_C)
+    return STA_ERR_ARG;
+  if (mixed != 0 && (mixed != 1 || slot_tiles < 2)) return STA_ERR_ARG;
+  const int esize = dtype == STA_F32 ? 4 : 2;
+  if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0 || ldv % (16 * column_tiles) != 0) return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+        reinterpret_cast<uintptr_t>(handoff)) & 15u) != 0)
+    return STA_ERR_ARG;
+  if (n * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+    return STA_ERR_UNSUPPORTED;
+  sta::WsArgs w;
+  sta::MomArgs& a = w.m;
+  a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
+  a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 16 * column_tiles - 1) / (16 * column_tiles);
+  a.quads = feat_quads; a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
+  a.ldo = 32 * ((dv + 31) / 32);
+  a.head_rows = n; a.rowmap = nullptr; a.state_num = nullptr; a.state_den = nullptr; a.n_feat = 0;
+  w.cpb = query_block / sta::MOM_C;
+  w.mixed = mixed;
+  w.hand = static_cast<uint4*>(handoff);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nx = moment_extra_factors(degree);
+  if (column_tiles == 4)
+    return esize == 4 ? dispatch_moments_ws<4, 4>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 4>(w, bh, s, slot_tiles, nx);
+  return esize == 4 ? dispatch_moments_ws<4, 2>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 2>(w, bh, s, slot_tiles, nx);
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
@@ -337,9 +393,9 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || block <= 0 || fsplit <= 0) return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
-  if (mode < 0 || mode > 3 || chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
+  if (mode < 0 || mode > 3 || chunk <= 0 || chunk % sta_moment_chunk(d) != 0 || shift < 0 || shift >= sta_moment_chunk(d))
+    return STA_ERR_ARG;
   if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
-  if (kTileRows % chunk != 0) return STA_ERR_ARG;
   if (n_tiles != static_cast<int>((n + shift + kTileRows - 1) / kTileRows)) return STA_ERR_SHAPE;
   if (n_nodes > 0 && (!node_meta || !node_src || !node_w || !tile_nodes || cap <= 0)) return STA_ERR_ARG;
   // rows are read in units of 4 elements: strides multiples of 4, bases 16-byte aligned; materialized

@@ -13,6 +13,7 @@
 
 namespace sta {
 struct MomArgs;
+struct WsArgs;
 struct BlockArgs;
 struct FlashArgs;
 }  // namespace sta
@@ -51,6 +52,14 @@ constexpr int kNtD4[] = {4, 8, 16};  // degree 4: d <= 64 only
   X(4, 1, false) X(8, 1, false) X(16, 1, false) X(5, 0, true) X(16, 0, true)                        \
   X(4, 1, true) X(16, 1, true) X(4, 2, false) X(8, 2, false) X(16, 2, false)
 
+// X(NTS, NX, DBIG) of the wave-specialised moment kernels (moments_ws_kernel; split-bf16 products,
+// degree <= 3): tiles per slot, extra factors per quad, d > 64.
+#define STA_MOMENT_WS_CONFIGS(X)                                                                    \
+  X(2, 0, false) X(3, 0, false) X(4, 0, false) X(5, 0, false)                                      \
+  X(2, 1, false) X(3, 1, false) X(4, 1, false) X(5, 1, false)                                      \
+  X(3, 0, true) X(5, 0, true)
+constexpr int kWsNts[] = {2, 3, 4, 5};
+
 // X(NT, NX, DBIG) of the 64-column (split-product) moment kernels.
 #define STA_MOMENT_CONFIGS_64(X) X(5, 0, false)
 
@@ -84,6 +93,10 @@ inline int moment_wave_tiles(int d, int degree, int want) {
 // per workgroup (64: split products, STA_MOMENT_CONFIGS_64 only).
 template <bool SPLIT, int CG>
 int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx);
+// launch_moments_ws.hip, one object per (ES, CT): the wave-specialised moment scan for nts tiles per
+// slot (moments_ws_kernel, 16 CT value columns per workgroup).
+template <int ES, int CT>
+int dispatch_moments_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s, int nts, int nx);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
 int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx);
 // launch_block.hip, one object per (DP, DVT, ES): the residual / combine kernel (block_attn_kernel) for

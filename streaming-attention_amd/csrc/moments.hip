@@ -50,6 +50,7 @@
 // Partials: red [4 waves][33][32]: column-major [column][token], column 32 = denominator, token groups
 //           of 4 permuted per column (red_off).
 // Running denominators: den [4 waves][NT tiles x 16 features].
+#pragma once
 #include "common.hpp"
 
 namespace sta {

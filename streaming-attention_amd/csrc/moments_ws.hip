@@ -1,0 +1,626 @@
+// K1, wave-specialised form (split-bf16 products): the exact low-degree Taylor moment scan
+//   low_num[i] = phi_q(s q_i) . S_{<b(i)}[:, :dv],   low_den[i] = phi_q(s q_i) . S_{<b(i)}[:, dv]
+// where b(i) is the query block of row i (blocks of QB = cpb * 32 rows, offset by `shift` like the
+// chunks) and S_{<b} = sum over the keys before the block of phi_k(k_j) [v_j, 1].  The residual kernel
+// adds every key of the row's own query block (the Taylor polynomial, or exp where the key is also in
+// the row's article block); with QB equal to the article block the two sets coincide and the residual
+// kernel's in-block keys carry exp(x) whole.  Reference semantics as moments_kernel:
+// low_degree_taylor_causal_sums_stream (fast_article_attention.py:217-259).
+//
+// Work split.  A workgroup of 512 threads = (head, feature split, 64-column group) holds 4 slots of
+// tiles (16 features each, the feature_tiles layout of moments.hip).  Waves 0-3 ("update waves") keep
+// the fp32 state of slot w in MFMA accumulators for the whole sequence and add every 32-token chunk:
+// S += phi_k^T [V, 1].  Waves 4-7 ("query waves") keep a frozen copy of the state of slot (w + 2) & 3
+// as split bf16 hi / lo operands, refreshed once per query block, and answer the chunk's queries:
+// out += phi_q S_frozen, 3 bf16 products per fp32 product.  Each wave generates one kind of feature
+// value only, every value feeds 4 column tiles (64 columns), and no state is re-split per chunk.  With
+// mixed tile counts slots 2 and 3 hold one tile less: a SIMD runs one update and one query wave
+// (waves w and w + 4) of slots w and (w + 2) & 3, so every SIMD carries the same number of tiles.
+//
+// Pipeline (one barrier per chunk).  Iteration c: update waves add chunk c; query waves answer chunk
+// c - 1 (one chunk behind, so the state of a new block is in flight for a whole iteration) and write
+// their partials to red[(c - 1) & 1]; all threads stage the keys / values of chunk c + 1 and the
+// queries of chunk c into the other LDS buffers, issue the global loads of the next slot, and reduce
+// red[(c - 2) & 1] over the 4 query waves in a fixed order (deterministic) into the partial outputs.
+// At the last chunk of a block the update waves split their state and write it (and the running
+// denominators) to a per-workgroup handoff buffer in global memory, double-buffered by block parity;
+// the query waves load it in the next iteration, right after their last use of the old copy.  The
+// handoff stays within the workgroup (stores, barrier, loads on one compute unit).
+#pragma once
+#include "moments.hip"
+
+namespace sta {
+
+constexpr int WS_WAVES = 8;
+constexpr int WS_THREADS = 64 * WS_WAVES;
+constexpr int WS_STAGERS = 512;  // every thread stages a share of each chunk
+constexpr int WS_REDUCERS = 256;  // the update waves reduce the partials
+
+struct WsArgs {
+  MomArgs m;        // inputs, feature table [fsplit][4 slots][NTS][..], partial outputs (moments_kernel layout)
+  int cpb;          // chunks per query block (>= 2)
+  int mixed;        // slots 2 and 3 hold NTS - 1 tiles
+  uint4* hand;      // [grid][2][4][NPS][CT][2][64]: split state as query operands (see ws_body)
+};
+
+__host__ __device__ constexpr int ws_kv_floats(bool dbig, int cg) { return mom_krows(dbig) * MOM_LDT + cg * MOM_C; }
+__host__ __device__ constexpr int ws_q_floats(bool dbig) { return MOM_C * mom_ldq(dbig); }
+__host__ __device__ constexpr int ws_red_floats(int cg) { return 4 * (cg + 4) * MOM_LDR; }
+// frozen running denominators of the query waves: [2 block parities][4 slots][nts * 16]
+__host__ __device__ constexpr int ws_den_floats(int nts) { return 2 * 4 * nts * 16; }
+__host__ __device__ constexpr int ws_smem_floats(bool dbig, int cg, int nts) {
+  return 2 * ws_kv_floats(dbig, cg) + 2 * ws_q_floats(dbig) + 2 * ws_red_floats(cg) + ws_den_floats(nts);
+}
+
+// Chunk staging in registers by all 512 threads: unit e = tid + 512 j of 16 bytes (4 fp32 or 8 bf16 /
+// fp16).
+// q: row-major units (token e / uq); k and v: token-fast units (token tid & 31) for the transposed LDS
+// rows.  Geometry per thread is fixed for the whole sequence.
+template <bool DBIG, int ES, int CG>
+struct WsStage {
+  static constexpr int QU = MOM_C * (DBIG ? 128 : 64) * ES / 16;
+  static constexpr int QV = (QU + WS_STAGERS - 1) / WS_STAGERS;
+  static constexpr int VU = MOM_C * CG * ES / 16;
+  static constexpr int VV = (VU + WS_STAGERS - 1) / WS_STAGERS;
+  uint4 q[QV];
+  uint4 k[QV];
+  uint4 v[VV];
+};
+
+template <bool DBIG, int ES, int CG>
+struct WsSlots {
+  static constexpr int QV = WsStage<DBIG, ES, CG>::QV;
+  static constexpr int VV = WsStage<DBIG, ES, CG>::VV;
+  int q_tok[QV];
+  uint32_t q_off[QV];
+  int q_lds[QV];
+  bool q_use[QV];
+  uint32_t k_off[QV];
+  int k_dim[QV];  // -1: unused
+  uint32_t v_off[VV];
+  int v_col[VV];  // -1: unused
+};
+
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ WsSlots<DBIG, ES, CG> ws_slots(const MomArgs& a, int col0) {
+  constexpr int LDQ = mom_ldq(DBIG);
+  constexpr int epu = 16 / ES;
+  WsSlots<DBIG, ES, CG> sl;
+  const int tid = threadIdx.x;
+  const int uq = a.d / epu;
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+    const int e = tid + WS_STAGERS * j;
+    const int t = e / uq, u = e - t * uq;
+    sl.q_use[j] = t < MOM_C;
+    sl.q_tok[j] = min(t, MOM_C - 1);
+    sl.q_off[j] = static_cast<uint32_t>(u * 16);
+    sl.q_lds[j] = t * LDQ + u * epu;
+    const int uk = e >> 5;
+    sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
+    sl.k_dim[j] = uk < uq ? uk * epu : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j) {
+    const int uv = (tid + WS_STAGERS * j) >> 5;
+    sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
+    sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
+  }
+  return sl;
+}
+
+// MASK = false: every row of the chunk lies in the sequence (no clamping)
+template <bool DBIG, int ES, int CG, bool MASK>
+__device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+                                          const MomArgs& a, const char* qh, int row0) {
+  const uint32_t qrow = static_cast<uint32_t>(a.d * ES);
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+    const int r = MASK ? clamp_row(row0 + sl.q_tok[j], static_cast<int>(a.n)) : row0 + sl.q_tok[j];
+    st.q[j] = *reinterpret_cast<const uint4*>(qh + static_cast<uint32_t>(r) * qrow + sl.q_off[j]);
+  }
+}
+
+template <bool DBIG, int ES, int CG, bool MASK>
+__device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+                                           const MomArgs& a, const char* kh, const char* vh, int row0) {
+  const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
+  const int t = row0 + (threadIdx.x & (MOM_C - 1));
+  const uint32_t r = static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j)
+    st.k[j] = *reinterpret_cast<const uint4*>(kh + r * krow_b + sl.k_off[j]);
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j)
+    st.v[j] = *reinterpret_cast<const uint4*>(vh + r * vrow_b + sl.v_off[j]);
+}
+
+// queries of the chunk at row0 -> Qs (scaled; column d = 1, or 0 on rows outside the sequence)
+template <bool DBIG, int ES, int CG, bool MASK>
+__device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+                                           const MomArgs& a, float* Qs, int row0) {
+  constexpr int LDQ = mom_ldq(DBIG);
+  constexpr bool wide = ES == 2;
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+    if (!sl.q_use[j]) continue;
+    const int row = row0 + sl.q_tok[j];
+    const float sc = (!MASK || (row >= 0 && row < a.n)) ? a.scale : 0.f;
+    float f[8];
+    unit_floats<ES>(st.q[j], a.dtype, f);
+    float* qd = Qs + sl.q_lds[j];
+    *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
+    if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
+  }
+  const int tid = threadIdx.x;
+  if (tid < MOM_C) Qs[tid * LDQ + a.d] = (!MASK || (row0 + tid >= 0 && row0 + tid < a.n)) ? 1.f : 0.f;
+}
+
+// keys (transposed, row d = constant) and values (bf16 hi / lo planes, vps_off) of the chunk at row0
+template <bool DBIG, int ES, int CG, bool MASK>
+__device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+                                            const MomArgs& a, float* Kt, __bf16* vplane, int row0) {
+  constexpr bool wide = ES == 2;
+  const int tok = threadIdx.x & (MOM_C - 1);
+  const float kok = (!MASK || (row0 + tok >= 0 && row0 + tok < a.n)) ? 1.f : 0.f;
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+    const int kd = sl.k_dim[j];
+    if (kd < 0) continue;
+    float f[8];
+    unit_floats<ES>(st.k[j], a.dtype, f);
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      if (m < 4 || wide) Kt[(kd + m) * MOM_LDT + tok] = f[m] * kok;
+  }
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j) {
+    const int c0 = sl.v_col[j];
+    if (c0 < 0) continue;
+    float f[8];
+    unit_floats<ES>(st.v[j], a.dtype, f);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (m < 4 || wide) {
+        const float x = f[m] * kok;
+        const __bf16 h = static_cast<__bf16>(x);
+        vplane[vps_off(c0 + m, tok)] = h;
+        vplane[CG * MOM_C + vps_off(c0 + m, tok)] = static_cast<__bf16>(x - static_cast<float>(h));
+      }
+    }
+  }
+  if (threadIdx.x < MOM_C) Kt[a.d * MOM_LDT + threadIdx.x] = kok;
+}
+
+// Update wave: S[f][col] += phi_k(tok)[f] V[tok][col] over the chunk for the slot's NT tiles and the
+// 16 CT columns; den_p[kt] += this lane's 8 tokens of phi_k (feature li of tile kt; the lanes' partials
+// are summed over lg when the state is handed to the query waves).  One 16x16x32 bf16 product covers
+// the 32 tokens (the token mapping of mom_update_split).  The next tile's key reads are issued as soon
+// as the current tile's feature values are formed (into the same registers), so they land while the
+// current tile's operands are split and its products issue.
+template <int NT, int CT, int NX>
+__device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[NT], const float* Kt,
+                                          const __bf16* vplane, const MomLane<NT, NX>& m, int li, int lg) {
+  constexpr int CG = 16 * CT;
+  bf16x8 vh[CT], vl[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + vps_off(16 * ct + li, 4 * lg));
+    vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + CG * MOM_C + vps_off(16 * ct + li, 4 * lg));
+  }
+  floatx4 fa[2], fb[2], fc[2], fe[2];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      fa[h] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
+      fb[h] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
+      if (NX >= 1) fc[h] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
+      if (NX >= 2) fe[h] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
+    }
+  };
+  load(0);
+#pragma unroll
+  for (int kt = 0; kt < NT; ++kt) {
+    float x[8];
+    float dacc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = fa[j >> 2][j & 3] * fb[j >> 2][j & 3];
+      if (NX >= 1) y *= fc[j >> 2][j & 3];
+      if (NX >= 2) y *= fe[j >> 2][j & 3];
+      if (NX >= 1) y *= m.kcoef[kt];  // NX = 0: the tile coefficient is applied by the query waves
+      x[j] = y;
+      dacc += y;
+    }
+    if (kt + 1 < NT) load(kt + 1);
+    den_p[kt] += dacc;
+    bf16x8 ah, al;
+    split_bf16(x, ah, al);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vl[ct], st[kt][ct]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(al, vh[ct], st[kt][ct]);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vh[ct], st[kt][ct]);
+  }
+}
+
+// Query-side operands of one tile for the lane's two tokens (li and 16 + li): x[i0] (times the tile
+// coefficient at NX = 0), x[b .. b + 3] and the extra factors.
+struct WsQOps {
+  float a[2];
+  floatx4 b[2];
+  float c[2], e[2];
+};
+
+template <int NT, int NX, int LDQ>
+__device__ __forceinline__ void ws_qload(WsQOps& o, int u, const float* Qs, const MomLane<NT, NX>& m, int li) {
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const float* qr = Qs + (li + 16 * tt) * LDQ;
+    o.a[tt] = (NX == 0) ? qr[m.qa[u]] * m.kcoef[u] : qr[m.qa[u]];
+    o.b[tt] = *reinterpret_cast<const floatx4*>(qr + m.qb[u]);
+    if (NX >= 1) o.c[tt] = qr[m.qc[NX >= 1 ? u : 0]];
+    if (NX >= 2) o.e[tt] = qr[m.qe[NX >= 2 ? u : 0]];
+  }
+}
+
+// phi_q of token tt (4 features of the lane's quad) from loaded operands; dq += phi_q . den
+template <int NX>
+__device__ __forceinline__ void ws_qfeat(float (&x)[4], float& dq, const WsQOps& o, int tt, const floatx4& dn, bool den) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    float y = o.a[tt] * o.b[tt][s];
+    if (NX >= 1) y *= o.c[tt];
+    if (NX >= 2) y *= o.e[tt];
+    x[s] = y;
+    if (den) dq = fmaf(y, dn[s], dq);
+  }
+}
+
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// Products of a tile pair: o[tt][ct] (rows 16 tt + 4 lg + r, column 16 ct + li) += phi_q . S_frozen with
+// the pair's 32 features as the contraction (mom_query_split's layout), 3 bf16 products per term.
+template <int CT>
+__device__ __forceinline__ void ws_qpair_mma(floatx4 (&o)[2][CT], const bf16x8 (&ah)[2], const bf16x8 (&al)[2],
+                                             const bf16x8 (&sh)[CT], const bf16x8 (&sl)[CT]) {
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mfma_bf16(ah[tt], sl[ct], o[tt][ct]);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mfma_bf16(al[tt], sh[ct], o[tt][ct]);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mfma_bf16(ah[tt], sh[ct], o[tt][ct]);
+}
+
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// Products of a single (odd last) tile: one 16x16x16 bf16 product per term, the tile's 16 features as the
+// contraction (lane (li, lg): features 4 lg + j).
+template <int CT>
+__device__ __forceinline__ void ws_qsingle_mma(floatx4 (&o)[2][CT], const uint2 (&ah)[2], const uint2 (&al)[2],
+                                               const uint2 (&sh)[CT], const uint2 (&sl)[CT]) {
+  auto mf = [](uint2 a, uint2 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(shortx4, a), __builtin_bit_cast(shortx4, b), c, 0,
+                                                    0, 0);
+  };
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mf(ah[tt], sl[ct], o[tt][ct]);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mf(al[tt], sh[ct], o[tt][ct]);
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[tt][ct] = mf(ah[tt], sh[ct], o[tt][ct]);
+}
+
+// Fixed-order sum of the 4 query waves' partials of the chunk at row0 -> low_num rows of the CG columns
+// (CG * 8 threads, 4 tokens each) and, with den, low_den (columns CG .. CG + 3 of a wave's partials: the
+// denominator sums of its 4 lane groups).
+constexpr int WS_RCOLS_EXTRA = 4;
+template <int CG>
+__device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
+                                                int col0, bool den) {
+  constexpr int WS = (CG + WS_RCOLS_EXTRA) * MOM_LDR;
+  const int tid = threadIdx.x;  // < WS_REDUCERS
+#pragma unroll
+  for (int e0 = 0; e0 < CG * 8; e0 += WS_REDUCERS) {
+    const int e = e0 + tid;
+    const int col = e % CG;
+    const int t4 = 4 * (e / CG);
+    floatx4 acc = *reinterpret_cast<const floatx4*>(red + red_off(col, t4));
+#pragma unroll
+    for (int q = 1; q < 4; ++q) acc += *reinterpret_cast<const floatx4*>(red + q * WS + red_off(col, t4));
+    float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
+  }
+  if (den && tid >= WS_REDUCERS - MOM_C) {
+    const int tok = tid - (WS_REDUCERS - MOM_C);
+    float dsum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) dsum += red[q * WS + red_off(CG + g, tok)];
+    a.low_den[obase + row0 + tok] = dsum;
+  }
+}
+
+// The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
+// out of the NTS the table holds per slot.  Every instantiation runs the same iterations and barriers.
+//
+// Handoff layout (global, per workgroup and block parity): for slot s, tile pair p = kt / 2 and column
+// tile ct, two uint4 per lane, the query operands hi and lo of the pair: bf16 of the 4 state values
+// the lane holds for tile 2 p (.xy) and tile 2 p + 1 (.zw); an odd last tile fills .xy only.  The
+// update wave writes its uint2 halves, the query wave loads whole operands.  The running denominators
+// go to LDS (den_lds[parity][slot][tile * 16 + feature]).
+template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT>
+__device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, int fs, int cs, int slot, int qw) {
+  const MomArgs& a = wa.m;
+  constexpr int CG = 16 * CT;
+  constexpr int LDQ = mom_ldq(DBIG);
+  constexpr int KVF = ws_kv_floats(DBIG, CG);
+  constexpr int QF = ws_q_floats(DBIG);
+  constexpr int REDF = ws_red_floats(CG);
+  constexpr int NPS = (NTS + 1) / 2;  // operand pairs per slot in the handoff
+  constexpr int NP = NT / 2;          // full tile pairs of this wave
+  constexpr bool ODD = (NT & 1) != 0;
+  extern __shared__ float smem[];
+  float* const kvb = smem;              // [2][KVF]: Kt [KR][36], then the bf16 value planes
+  float* const qb = smem + 2 * KVF;     // [2][QF]
+  float* const redb = qb + 2 * QF;      // [2][REDF]
+  float* const denb = redb + 2 * REDF;  // [2][4][NTS * 16]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int col0 = CG * cs;
+  const bool den = cs == 0;
+  const int n = static_cast<int>(a.n);
+  const int nch = (n + a.shift + MOM_C - 1) / MOM_C;
+  const int first = -a.shift;
+  const int cpb = wa.cpb;
+  const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
+  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
+  const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
+  const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
+  const WsSlots<DBIG, ES, CG> sl = ws_slots<DBIG, ES, CG>(a, col0);  // used by the update waves only
+  // operand (pair p, column tile ct, hi / lo) of this slot and block parity par
+  auto hand_at = [&](int par, int p, int ct, int hl) -> uint4* {
+    return wa.hand + ((((static_cast<int64_t>(wg) * 2 + par) * 4 + slot) * NPS + p) * CT + ct) * 128 + hl * 64 + lane;
+  };
+
+  floatx4 st[UPD ? NT : 1][CT];
+  float den_p[UPD ? NT : 1];  // per-lane partial denominators (this lane's tokens)
+  bf16x8 sh[UPD || NP == 0 ? 1 : NP][CT], sv[UPD || NP == 0 ? 1 : NP][CT];
+  uint2 oh[CT], ov[CT];  // the odd last tile's operands
+  if constexpr (UPD) {
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+      den_p[kt] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) st[kt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  } else {
+    const bf16x8 z = __builtin_bit_cast(bf16x8, uint4{0u, 0u, 0u, 0u});
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) sh[p][ct] = sv[p][ct] = z;
+      oh[ct] = ov[ct] = uint2{0u, 0u};
+    }
+  }
+
+  // zero every staging buffer (padding rows / columns are never written again) and the denominators of
+  // block 0 (parity 0: the state before the first block is empty)
+  for (int e = tid; e < 2 * (KVF + QF); e += WS_THREADS) smem[e] = 0.f;
+  for (int e = tid; e < ws_den_floats(NTS); e += WS_THREADS) denb[e] = 0.f;
+  __syncthreads();
+  // two register sets of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is held
+  // in set x & 1 from its load (iteration x - 3) to its store into LDS (iteration x - 1), so a load has
+  // two iterations to land
+  WsStage<DBIG, ES, CG> pre0, pre1;
+  ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first);
+  ws_store_kv<DBIG, ES, CG, true>(pre0, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
+  __syncthreads();
+  if (nch > 1) ws_load_kv<DBIG, ES, CG, true>(pre1, sl, a, kh, vh, first + MOM_C);  // slot 1
+  ws_load_q<DBIG, ES, CG, true>(pre1, sl, a, qh, first);
+  if (nch > 2) ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first + 2 * MOM_C);  // slot 2
+  if (nch > 1) ws_load_q<DBIG, ES, CG, true>(pre0, sl, a, qh, first + MOM_C);
+
+  for (int c = 0; c <= nch; ++c) {
+    if constexpr (UPD) {
+      if (c < nch) {
+        const float* Kt = kvb + (c & 1) * KVF;
+        ws_update<NT, CT, NX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li, lg);
+        if ((c + 1) % cpb == 0 && c + 1 < nch) {
+          // the state the queries of block (c + 1) / cpb see -> handoff (parity of that block)
+          const int par = ((c + 1) / cpb) & 1;
+#pragma unroll
+          for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              uint32_t h0, h1, l0, l1;
+              split_pair(st[kt][ct][0], st[kt][ct][1], h0, l0);
+              split_pair(st[kt][ct][2], st[kt][ct][3], h1, l1);
+              reinterpret_cast<uint2*>(hand_at(par, kt >> 1, ct, 0))[kt & 1] = uint2{h0, h1};
+              reinterpret_cast<uint2*>(hand_at(par, kt >> 1, ct, 1))[kt & 1] = uint2{l0, l1};
+            }
+            if (den) {
+              float t = den_p[kt];
+              t += __shfl_xor(t, 16);
+              t += __shfl_xor(t, 32);
+              if (lg == 0) denb[(par * 4 + slot) * NTS * 16 + kt * 16 + li] = t;
+            }
+          }
+        }
+      }
+    } else {
+      if (c >= 1) {
+        const float* Qs = qb + ((c - 1) & 1) * QF;
+        const float* dnb = denb + ((((c - 1) / cpb) & 1) * 4 + slot) * NTS * 16 + 4 * lg;
+        floatx4 o[2][CT];
+        float dq[2] = {0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) o[tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const bool reload = c % cpb == 0 && c < nch;
+        const int par = (c / cpb) & 1;
+        // operands of the first two tiles; each pair's successor is loaded once its features are formed
+        WsQOps op0, op1;
+        ws_qload<NT, NX, LDQ>(op0, 0, Qs, m, li);
+        if (NT > 1) ws_qload<NT, NX, LDQ>(op1, NT > 1 ? 1 : 0, Qs, m, li);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const floatx4 dn0 = *reinterpret_cast<const floatx4*>(dnb + 2 * p * 16);
+          const floatx4 dn1 = *reinterpret_cast<const floatx4*>(dnb + (2 * p + 1) * 16);
+          bf16x8 ah[2], al[2];
+          float x[2][8];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            float x0[4], x1[4];
+            ws_qfeat<NX>(x0, dq[tt], op0, tt, dn0, den);
+            ws_qfeat<NX>(x1, dq[tt], op1, tt, dn1, den);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              x[tt][j] = x0[j];
+              x[tt][4 + j] = x1[j];
+            }
+          }
+          if (2 * p + 2 < NT) ws_qload<NT, NX, LDQ>(op0, 2 * p + 2 < NT ? 2 * p + 2 : 0, Qs, m, li);
+          if (2 * p + 3 < NT) ws_qload<NT, NX, LDQ>(op1, 2 * p + 3 < NT ? 2 * p + 3 : 0, Qs, m, li);
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) split_bf16(x[tt], ah[tt], al[tt]);
+          ws_qpair_mma<CT>(o, ah, al, sh[p], sv[p]);
+          if (reload) {  // the next block's state, into the registers this pair no longer needs
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              sh[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 0));
+              sv[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 1));
+            }
+          }
+        }
+        if constexpr (ODD) {
+          const floatx4 dn = *reinterpret_cast<const floatx4*>(dnb + (NT - 1) * 16);
+          uint2 ah[2], al[2];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            float x0[4];
+            ws_qfeat<NX>(x0, dq[tt], op0, tt, dn, den);
+            split_pair(x0[0], x0[1], ah[tt].x, al[tt].x);
+            split_pair(x0[2], x0[3], ah[tt].y, al[tt].y);
+          }
+          ws_qsingle_mma<CT>(o, ah, al, oh, ov);
+          if (reload) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              oh[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 0));
+              ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
+            }
+          }
+        }
+        // this wave's partials of chunk c - 1 -> red[(c - 1) & 1], column-major (red_off); columns
+        // CG + lg: the denominator sums of lane group lg
+        float* rw = redb + ((c - 1) & 1) * REDF + qw * (CG + WS_RCOLS_EXTRA) * MOM_LDR;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+            *reinterpret_cast<floatx4*>(rw + red_off(16 * ct + li, 16 * tt + 4 * lg)) = o[tt][ct];
+          if (den) rw[red_off(CG + lg, 16 * tt + li)] = dq[tt];
+        }
+      }
+    }
+
+    // ---- after the role work, all threads: staging of slot c + 1 (keys / values of chunk c + 1, queries of
+    //      chunk c) from its register set and loads of slot c + 3 into it; update waves: the reduction of
+    //      chunk c - 2's partials ----
+    {
+      auto stage = [&](WsStage<DBIG, ES, CG>& pre) {
+        const int kv_row = first + (c + 1) * MOM_C;
+        const int q_row = first + c * MOM_C;
+        if (c + 1 < nch) {
+          float* Kt = kvb + ((c + 1) & 1) * KVF;
+          __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
+          if (kv_row >= 0 && kv_row + MOM_C <= n)
+            ws_store_kv<DBIG, ES, CG, false>(pre, sl, a, Kt, vp, kv_row);
+          else
+            ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, vp, kv_row);
+        }
+        if (c < nch) {
+          float* Qs = qb + (c & 1) * QF;
+          if (q_row >= 0 && q_row + MOM_C <= n)
+            ws_store_q<DBIG, ES, CG, false>(pre, sl, a, Qs, q_row);
+          else
+            ws_store_q<DBIG, ES, CG, true>(pre, sl, a, Qs, q_row);
+        }
+        const int kv3 = kv_row + 2 * MOM_C, q3 = q_row + 2 * MOM_C;
+        if (c + 3 < nch) {
+          if (kv3 >= 0 && kv3 + MOM_C <= n)
+            ws_load_kv<DBIG, ES, CG, false>(pre, sl, a, kh, vh, kv3);
+          else
+            ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv3);
+        }
+        if (c + 2 < nch) {
+          if (q3 >= 0 && q3 + MOM_C <= n)
+            ws_load_q<DBIG, ES, CG, false>(pre, sl, a, qh, q3);
+          else
+            ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q3);
+        }
+      };
+      if (c & 1)
+        stage(pre0);
+      else
+        stage(pre1);
+      if constexpr (UPD) {
+        if (c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
+      }
+    }
+    __syncthreads();
+  }
+  // partials of the last chunk (written by the query waves in iteration nch)
+  if constexpr (UPD) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
+}
+
+// Workgroup -> (head, feature split, column group): consecutive logical ids share an XCD, so a head's
+// workgroups share one L2 for its q / k / v rows.  Waves 0-3 update, 4-7 query.
+template <int NTS, int NX, bool DBIG, int ES, int CT>
+__global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs wa) {
+  const MomArgs& a = wa.m;
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_head = a.fsplit * a.csplit;
+  const int64_t bh = wg / per_head;
+  const int rem = wg - static_cast<int>(bh) * per_head;
+  const int fs = rem / a.csplit;
+  const int cs = rem - fs * a.csplit;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int NTL = NTS > 1 ? NTS - 1 : NTS;
+  if (w < 4) {
+    const int slot = w;
+    if (NTS > 1 && wa.mixed && slot >= 2)
+      ws_body<true, NTL, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, 0);
+    else
+      ws_body<true, NTS, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, 0);
+  } else {
+    const int slot = (w - 4 + 2) & 3;
+    if (NTS > 1 && wa.mixed && slot >= 2)
+      ws_body<false, NTL, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, w - 4);
+    else
+      ws_body<false, NTS, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, w - 4);
+  }
+}
+
+}  // namespace sta

@@ -21,7 +21,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 def header_symbols():
     text = (ROOT / "include" / "streamattn.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(sta_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|const char\*)\s+(sta_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_exports_header_symbols():
@@ -294,6 +294,27 @@ def test_fast_path_argument_errors():
         faa.num_taylor_features(4, 3)
     with pytest.raises(ValueError):
         faa.exp_taylor(torch.zeros(2), -1)
+
+
+@pytest.mark.parametrize("d,degree,bh,dv,ct", [(64, 2, 32, 64, 4), (64, 2, 128, 64, 4), (16, 3, 128, 64, 4), (32, 2, 1, 32, 2),
+                                                (64, 2, 3, 100, 4), (128, 2, 8, 96, 2)])
+def test_moment_split_ws_covers_every_tile_once(d, degree, bh, dv, ct):
+    """The wave-specialised kernel's table: 4 slots per feature split, slots within their tile budget
+    (slot_tiles, one less in slots 2 and 3 when mixed), every feature tile exactly once, padding slots
+    with coefficient 0."""
+    ft = _plan.feature_tiles(d, degree)
+    ms = _plan.moment_split_ws(ft, bh, dv, (2, 3, 4, 5), ct)
+    sizes = np.diff(ms.tile_off)
+    assert sizes.size == 4 * ms.fsplit and sizes.sum() == ft.n_tiles
+    caps = np.array([ms.wave_tiles - (1 if ms.mixed and j % 4 >= 2 else 0) for j in range(sizes.size)])
+    assert (sizes <= caps).all() and (sizes >= 0).all()
+    q = ms.quads.reshape(-1, ms.wave_tiles, 4)
+    c = ms.coef.reshape(-1, ms.wave_tiles, 16)
+    got = np.concatenate([q[j, : sizes[j]] for j in range(sizes.size)]).reshape(-1)
+    assert np.array_equal(got, ft.quads)
+    for j in range(sizes.size):
+        assert not c[j, sizes[j]:].any()
+    assert ms.csplit == -(-dv // (16 * ct)) and ms.columns == 16 * ct
 
 
 def test_empty_sequences_return_empty_outputs_on_the_host():
