@@ -47,23 +47,17 @@ def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
 
 # The wave-specialised moment kernel (sta_moments_ws: update and query waves, 64 value columns per
 # workgroup, the queries answered against the state before their article block) for split products at
-# degree <= 3 whenever the article block is a whole number (>= 2) of moment chunks.  Chosen where it
-# measured faster (one MI355X, A/B in one session, K1 / whole step):
-#   8 x 16 heads x 4096, bf16, degree 2, block 256:     2.33 -> 1.88 ms / 3.47 -> 3.04 ms
-#   4 x 32 heads x 16384, fp32, degree 3, block 128:    6.21 -> 5.07 ms / 7.97 -> 6.98 ms
-#   1 x 32 heads x 65536, fp32, degree 2, block 256:    7.34 -> 7.32 ms / 10.31 -> 10.58 ms
-# The last is a tie in the scan and a loss in the step: sta_moments' mixed tile counts free half the
-# compute units early, where the side-stream compressor runs; sta_moments_ws' workgroups all end
-# together.  So: 16-bit inputs or degree 3 (MOMENT_WS_POLICY "auto"); "always" / "never" override.
+# degree <= 3 whenever the article block is a whole number (>= 2) of moment chunks; sta_moments
+# otherwise.  A/B on one MI355X in one session (moment scan / whole step):
+#   1 x 32 heads x 65536, fp32, degree 2, block 256:    6.89 -> 6.38 ms / 9.75 -> 9.61 ms
+#   8 x 16 heads x 4096, bf16, degree 2, block 256:     2.29 -> 1.68 ms / 3.41 -> 2.83 ms
+#   4 x 32 heads x 16384, fp32, degree 3, block 128:    6.13 -> 4.28 ms / 7.88 -> 6.18 ms
+# STA_MOMENT_WS=never / always overrides the choice (a prefill's moment_kernel argument too).
 MOMENT_WS_POLICY = os.environ.get("STA_MOMENT_WS", "auto")  # "auto" | "always" | "never"
 
 
 def use_moments_ws(element_size: int, degree: int) -> bool:
-    if MOMENT_WS_POLICY in ("always", "1"):
-        return True
-    if MOMENT_WS_POLICY in ("never", "0"):
-        return False
-    return element_size == 2 or degree == 3
+    return MOMENT_WS_POLICY not in ("never", "0")
 
 
 def ws_query_block(semantics: str, block: int) -> Optional[int]:

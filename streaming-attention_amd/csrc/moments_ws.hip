@@ -208,31 +208,36 @@ __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[
     vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + vps_off(16 * ct + li, 4 * lg));
     vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + CG * MOM_C + vps_off(16 * ct + li, 4 * lg));
   }
-  floatx4 fa[2], fb[2], fc[2], fe[2];
+  // key reads two tiles ahead: set kt & 1 holds tile kt's, reloaded with tile kt + 2's once its feature
+  // values are formed
+  floatx4 fa[2][2], fb[2][2], fc[2][2], fe[2][2];
   auto load = [&](int kt) {
+    const int b = kt & 1;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      fa[h] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
-      fb[h] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (NX >= 1) fc[h] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
-      if (NX >= 2) fe[h] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
+      fa[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
+      fb[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
+      if (NX >= 1) fc[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
+      if (NX >= 2) fe[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
     }
   };
   load(0);
+  if (NT > 1) load(NT > 1 ? 1 : 0);
 #pragma unroll
   for (int kt = 0; kt < NT; ++kt) {
+    const int b = kt & 1;
     float x[8];
     float dacc = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float y = fa[j >> 2][j & 3] * fb[j >> 2][j & 3];
-      if (NX >= 1) y *= fc[j >> 2][j & 3];
-      if (NX >= 2) y *= fe[j >> 2][j & 3];
+      float y = fa[b][j >> 2][j & 3] * fb[b][j >> 2][j & 3];
+      if (NX >= 1) y *= fc[b][j >> 2][j & 3];
+      if (NX >= 2) y *= fe[b][j >> 2][j & 3];
       if (NX >= 1) y *= m.kcoef[kt];  // NX = 0: the tile coefficient is applied by the query waves
       x[j] = y;
       dacc += y;
     }
-    if (kt + 1 < NT) load(kt + 1);
+    if (kt + 2 < NT) load(kt + 2 < NT ? kt + 2 : 0);
     den_p[kt] += dacc;
     bf16x8 ah, al;
     split_bf16(x, ah, al);
@@ -435,10 +440,10 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first);
   ws_store_kv<DBIG, ES, CG, true>(pre0, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
   __syncthreads();
-  if (nch > 1) ws_load_kv<DBIG, ES, CG, true>(pre1, sl, a, kh, vh, first + MOM_C);  // slot 1
+  ws_load_kv<DBIG, ES, CG, true>(pre1, sl, a, kh, vh, first + MOM_C);  // slot 1
   ws_load_q<DBIG, ES, CG, true>(pre1, sl, a, qh, first);
-  if (nch > 2) ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first + 2 * MOM_C);  // slot 2
-  if (nch > 1) ws_load_q<DBIG, ES, CG, true>(pre0, sl, a, qh, first + MOM_C);
+  ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first + 2 * MOM_C);  // slot 2
+  ws_load_q<DBIG, ES, CG, true>(pre0, sl, a, qh, first + MOM_C);
 
   for (int c = 0; c <= nch; ++c) {
     if constexpr (UPD) {
@@ -567,19 +572,10 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           else
             ws_store_q<DBIG, ES, CG, true>(pre, sl, a, Qs, q_row);
         }
-        const int kv3 = kv_row + 2 * MOM_C, q3 = q_row + 2 * MOM_C;
-        if (c + 3 < nch) {
-          if (kv3 >= 0 && kv3 + MOM_C <= n)
-            ws_load_kv<DBIG, ES, CG, false>(pre, sl, a, kh, vh, kv3);
-          else
-            ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv3);
-        }
-        if (c + 2 < nch) {
-          if (q3 >= 0 && q3 + MOM_C <= n)
-            ws_load_q<DBIG, ES, CG, false>(pre, sl, a, qh, q3);
-          else
-            ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q3);
-        }
+        // slot c + 3: unconditional loads with rows clamped into the sequence (past the end they are
+        // never stored), one code path, so nothing waits on them before their store two iterations on
+        ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + 2 * MOM_C);
+        ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + 2 * MOM_C);
       };
       if (c & 1)
         stage(pre0);
@@ -590,7 +586,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       }
     }
     __syncthreads();
-  }
+    }
   // partials of the last chunk (written by the query waves in iteration nch)
   if constexpr (UPD) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
 }
