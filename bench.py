@@ -110,31 +110,113 @@ def measured_traffic(workload: str, kernel: str):
     return None
 
 
+def host_cpus():
+    """The host the CPU baseline runs on: os.cpu_count(), the CPUs this process may use (its affinity
+    mask, capped by a cgroup v2 cpu.max quota: threads beyond the share only contend) and the CPU model
+    name (the one lscpu prints, read from /proc/cpuinfo).  Returns (info dict, usable thread count)."""
+    allowed = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q_, p_ = pathlib.Path("/sys/fs/cgroup/cpu.max").read_text().split()
+        if q_ != "max":
+            quota = int(q_) / int(p_)
+    except (OSError, ValueError):
+        pass
+    usable = max(1, min(allowed, int(quota) if quota else allowed))
+    model = None
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "cpus_allowed": allowed, "cgroup_cpu_quota": quota,
+            "cpu_model": model}, usable
+
+
+def warm_median(fn, runs=3):
+    """One untimed warm-up call of fn (returning a dict with "total_s"), then the median of `runs` calls
+    (the reference's own timer discipline, fast_article_attention.py:761-770).  Returns (median
+    result, every timed total)."""
+    fn()
+    res = sorted((fn() for _ in range(runs)), key=lambda r: r["total_s"])
+    return res[len(res) // 2], [round(r["total_s"], 3) for r in res]
+
+
+def levels_cpu_sample(oracle, w, positions=8):
+    """Seconds per head of the reference's level semantics on the host (article_causal_attention:
+    ArticleStreamingAttention.update + query per token, streaming_taylor_coreset_attention.py:641-687),
+    sampled: `block` consecutive steps (so exactly one block completion with its compress and merges)
+    from each of `positions` evenly spaced prefixes, with the state sizes of that prefix; the mean
+    per-step cost is scaled by N."""
+    n, blk = w["seq_len"], w["block"]
+    starts = [(j * n // positions) // blk * blk + blk // 2 for j in range(positions)]
+    tot = 0.0
+    for p in starts:
+        t = oracle.time_decode_sample(dim=w["d"], value_dim=w["dv"], degree=w["degree"], block=blk,
+                                      scale=w["scale"], prefix=p, steps=blk, seed=w["seed"])
+        tot += t["s_per_step"]
+    return {"total_s": tot / positions * n, "s_per_step": tot / positions, "prefixes": starts}
+
+
 def cpu_baseline(q, k, v, w):
-    """Reference CPU fast path on one head (bounded sample), via the oracle."""
+    """Reference CPU fast path on one head (bounded sample), via the oracle: one warm-up, then the
+    median of 3 runs, with every usable host thread and with 1 thread; plus the reference's level
+    semantics (the per-token streaming object, which is what the GPU computes) sampled the same way."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import reference_cpu as oracle
 
-    threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "16384"))
+    info, threads = host_cpus()
+    threads = int(os.environ.get("STA_CPU_THREADS", "0")) or threads
+    rows = int(os.environ.get("STA_CPU_SAMPLE_ROWS", "4096"))
+    rows1 = int(os.environ.get("STA_CPU_SAMPLE_ROWS_1T", "2048"))
     # 16-bit inputs: the oracle runs on their values upcast to fp32 (the GPU computes in fp32 too)
-    t = oracle.time_fast_path_sample(q[0, 0].float().contiguous(), k[0, 0].float().contiguous(),
-                                     v[0, 0].float().contiguous(),
-                                     degree=w["degree"], block=w["block"], scale=w["scale"], seed=w["seed"], rows=rows)
+    qh, kh, vh = (x[0, 0].float().contiguous() for x in (q, k, v))
+
+    def sample(r):
+        return lambda: oracle.time_fast_path_sample(qh, kh, vh, degree=w["degree"], block=w["block"],
+                                                    scale=w["scale"], seed=w["seed"], rows=r)
+
     n = w["seq_len"]
-    rows = min(rows, n)
+    torch.set_num_threads(threads)
+    t, totals = warm_median(sample(rows))
+    torch.set_num_threads(1)
+    t1, totals1 = warm_median(sample(rows1))
+    torch.set_num_threads(threads)
+    lev, lev_totals = (warm_median(lambda: levels_cpu_sample(oracle, w))
+                       if w["semantics"].startswith("merge") else (None, None))
+    rows, rows1 = min(rows, n), min(rows1, n)
     general = " with the general feature map (the reference fast path raises for degree 3)" if w["degree"] > 2 else ""
-    return {
+    out = {
         "value": n / t["total_s"],
         "unit": "head-tokens/s",
         "cores": threads,
         "kind": "port",
+        "extrapolated": True,
+        "torch_threads": threads,
+        **info,
+        "one_thread_value": n / t1["total_s"],
+        "runs_s_per_head": totals,
+        "one_thread_runs_s_per_head": totals1,
         "sample": (f"reference CPU fast path restated in oracle/{general} (stream moments, flat sorted_pair coreset, "
                    f"query chunks of 2048), 1 head of the workload (N={n}); token loop, q x reps residual and "
-                   f"in-block residual timed over the first {rows} rows and scaled by N/{rows}, reps built "
-                   f"for all N; per-part seconds/head {json.dumps({k2: round(v2, 3) for k2, v2 in t.items()})}"),
+                   f"in-block residual timed over the first {rows} rows ({rows1} at 1 thread) and scaled by "
+                   f"N/rows, reps built for all N; 1 warm-up then the median of 3 runs; heads are independent "
+                   f"and serial in the reference, so head-tokens/s holds for B*H heads; median per-part "
+                   f"seconds/head {json.dumps({k2: round(v2, 3) for k2, v2 in t.items()})}"),
     }
+    if lev is not None:
+        out["levels_semantics"] = {
+            "value": n / lev["total_s"],
+            "unit": "head-tokens/s",
+            "runs_s_per_head": lev_totals,
+            "sample": (f"the reference's level semantics (per-token update + query of the streaming object, "
+                       f"restated in oracle/), {w['block']} steps from each of the prefixes {lev['prefixes']} "
+                       f"(one block completion each), mean {lev['s_per_step'] * 1e3:.3f} ms/step scaled by N; "
+                       f"1 warm-up then the median of 3"),
+        }
+    return out
 
 
 def main() -> int:
@@ -241,6 +323,25 @@ def main() -> int:
     per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_step": round(tot / args.steps, 4)}
                   for name, (tot, cnt) in timer.totals_ms().items()}
 
+    # cold calls through the public API, each at a seed no earlier call used: host draw replay, their
+    # upload and the kernels (and, the second time, the plan of a shape seen for the first time)
+    def cold_call(fresh_seed, clear_plans):
+        if clear_plans:
+            _plan._cache.clear()
+            _engine._dev_cache.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        api(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"], compressor=w["compressor"],
+            seed=fresh_seed)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    cold_ms = [cold_call(w["seed"] + 7919 * (i + 1), False) for i in range(3)]
+    cold_plan_ms = cold_call(w["seed"] + 7919 * 4, True)
+    t0 = time.perf_counter()
+    _plan.draws_for(plan, _plan.sequence_seeds(w["seed"] + 7919 * 5, bh), d, w["compressor"])
+    draws_ms = (time.perf_counter() - t0) * 1e3
+
     f = _plan.num_features(d, w["degree"])
     mom_flops = 4.0 * f * (dv + 1) * bh * n  # algorithmic: update + query, 2*F*(dv+1) each per head-token
     mom_ms = per_kernel["moments"]["ms_total"] / per_kernel["moments"]["launches"]
@@ -264,7 +365,7 @@ def main() -> int:
         "data": "synthetic",
         "config": w,
         "roofline": {
-            "kernel": "moments_kernel (K1, exact Taylor moment scan)",
+            "kernel": f"{res.moment_kernel} (K1, exact Taylor moment scan)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": peak,
@@ -273,7 +374,7 @@ def main() -> int:
             "products": "split-bf16" if split else "fp32",
             "peak_basis": ("fp32-equivalent flops of split-bf16 products: bf16 dense peak / 3 (three bf16 "
                            "matrix-core products per fp32 product)" if split else "fp32 matrix-core peak"),
-            "traffic": measured_traffic(w["workload"], "moments_kernel"),
+            "traffic": measured_traffic(w["workload"], res.moment_kernel),
             # the same fp32-equivalent rate against the bound fp32 matrix-core products would have
             "achieved_vs_fp32_mfma_peak": achieved / MFMA_FP32_PEAK_TFLOPS,
             "algorithmic_flops_per_launch": mom_flops,
@@ -283,6 +384,13 @@ def main() -> int:
         "kernels_note": ("compress runs on a second stream overlapping moments; its HIP-event interval "
                          "includes the wait for compute units" if _engine.OVERLAP_COMPRESS else ""),
         "host_plan_and_draws_s": round(t_plan, 3),
+        "cold_call_ms": round(sorted(cold_ms)[1], 3),
+        "cold_call_note": ("public API call at a seed no earlier call used (host draw replay for every sequence, "
+                           "its upload, kernels; synchronised), median of 3; the warm ms_per_step reuses the "
+                           "seed's cached draws"),
+        "cold_call_new_shape_ms": round(cold_plan_ms, 3),
+        "host_draws_fresh_seed_ms": round(draws_ms, 3),
+        "host_threads": torch.get_num_threads(),
         "wall_s_timed_region": round(wall, 4),
     }
     if not args.no_cpu_baseline:
@@ -373,27 +481,47 @@ def run_flash(args) -> int:
     }
     if not args.no_cpu_baseline:
         print(f"[bench] flash: timing CPU baseline", file=sys.stderr, flush=True)
-        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
-        torch.set_num_threads(threads)
+        info, threads = host_cpus()
+        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or threads
         chunk = 2048  # query rows per host product (the whole N x N logits of a head would be 17 GB)
         qh, kh, vh = q[0, 0].float(), k[0, 0].float(), v[0, 0].float()
         kt = kh.T.contiguous()
-        t0 = time.perf_counter()
-        for lo in range(0, n, chunk):
-            hi = min(lo + chunk, n)
-            logits = (qh[lo:hi] @ kt[:, :hi]) * w["scale"]
-            mask = torch.arange(hi)[None, :] > torch.arange(lo, hi)[:, None]
-            o = torch.softmax(logits.masked_fill(mask, float("-inf")), dim=-1) @ vh[:hi]
-            assert bool(torch.isfinite(o).all())
-        secs_head = time.perf_counter() - t0
+        los = list(range(0, n, chunk))
+        # a chunk's cost grows with its prefix (its end row): time every eighth chunk and scale by the
+        # ratio of the summed prefix lengths
+        pick = los[len(los) % 8 // 2::8] if len(los) >= 8 else los
+        cost = lambda lo: min(lo + chunk, n)  # noqa: E731
+
+        def sample():
+            t0 = time.perf_counter()
+            for lo in pick:
+                hi = min(lo + chunk, n)
+                logits = (qh[lo:hi] @ kt[:, :hi]) * w["scale"]
+                mask = torch.arange(hi)[None, :] > torch.arange(lo, hi)[:, None]
+                o = torch.softmax(logits.masked_fill(mask, float("-inf")), dim=-1) @ vh[:hi]
+                assert bool(torch.isfinite(o).all())
+            return {"total_s": (time.perf_counter() - t0) * sum(map(cost, los)) / sum(map(cost, pick))}
+
+        torch.set_num_threads(threads)
+        t, totals = warm_median(sample)
+        torch.set_num_threads(1)
+        t1, _ = warm_median(sample, runs=1)
+        torch.set_num_threads(threads)
         line["cpu_baseline"] = {
-            "value": n / secs_head,
+            "value": n / t["total_s"],
             "unit": "head-tokens/s",
             "cores": threads,
             "kind": "port",
+            "extrapolated": True,
+            "torch_threads": threads,
+            **info,
+            "one_thread_value": n / t1["total_s"],
+            "runs_s_per_head": totals,
             "sample": (f"torch fp32 causal softmax attention on the host (the reference's "
-                       f"torch_classical_causal_attention, triton_article_attention.py:123-143) over one whole "
-                       f"head (N={n}) in blocks of {chunk} query rows against their prefix: {secs_head:.2f} s"),
+                       f"torch_classical_causal_attention, triton_article_attention.py:123-143) over one head "
+                       f"(N={n}) in blocks of {chunk} query rows against their prefix: {len(pick)} of the "
+                       f"{len(los)} blocks timed and scaled by their share of the summed prefix lengths; 1 "
+                       f"warm-up then the median of 3 (1 thread: one run after a warm-up)"),
         }
         line["speedup_vs_cpu_baseline"] = value / line["cpu_baseline"]["value"]
     else:
@@ -494,16 +622,28 @@ def run_decode(args) -> int:
         sys.path.insert(0, str(ROOT / "oracle"))
         import reference_cpu as oracle
 
-        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+        info, threads = host_cpus()
+        threads = int(os.environ.get("STA_CPU_THREADS", "0")) or threads
         torch.set_num_threads(threads)
         steps = int(os.environ.get("STA_CPU_DECODE_STEPS", "256"))
         print(f"[bench] timing CPU baseline ({steps} steps of one stream)", file=sys.stderr, flush=True)
-        t = oracle.time_decode_sample(dim=d, value_dim=dv, degree=w["degree"], block=w["block"], scale=w["scale"],
-                                      prefix=w["prefix"], steps=steps, seed=w["seed"])
+
+        def sample():
+            t = oracle.time_decode_sample(dim=d, value_dim=dv, degree=w["degree"], block=w["block"],
+                                          scale=w["scale"], prefix=w["prefix"], steps=steps, seed=w["seed"])
+            return dict(t, total_s=t["s_per_step"])
+
+        t, totals = warm_median(sample)
+        torch.set_num_threads(1)
+        t1, _ = warm_median(sample)
+        torch.set_num_threads(threads)
         cb = {"value": 1.0 / t["s_per_step"], "unit": "stream-tokens/s", "cores": threads, "kind": "port",
+              "extrapolated": True, "torch_threads": threads, **info, "one_thread_value": 1.0 / t1["s_per_step"],
+              "runs_s_per_step": totals,
               "sample": (f"reference ArticleStreamingAttention update+query restated in oracle/ (per-token torch "
                          f"ops), one stream with the state sizes after a {w['prefix']}-token prefix, {steps} steps "
-                         f"(block completions included); the reference runs streams one after another")}
+                         f"(block completions included), 1 warm-up then the median of 3; the reference runs "
+                         f"streams one after another, so stream-tokens/s holds for every stream count")}
         line["cpu_baseline"] = cb
         line["speedup_vs_cpu_baseline"] = value / cb["value"]
     else:

@@ -88,9 +88,8 @@ class DecodeState:
         self.blocks = 0
         self.buf_len = 0
         self.num_compressions = 0
-        self._gens = [torch.Generator(device="cpu") for _ in range(S)]
-        for s, g in enumerate(self._gens):
-            g.manual_seed(self.seed + s)
+        # stream s draws from its own CPU generator seeded seed + s, continued block after block
+        self._gens = _native.DrawSet([self.seed + s for s in range(S)])
         self._draws: Deque[_CompletionDraws] = deque()
 
         # moment query: feature factors in reference order, splits to fill the GPU
@@ -178,21 +177,8 @@ class DecodeState:
         sizes = _plan.completion_call_sizes(blocks_before, self.block, self.compressor)
         n_calls = len(sizes)
         max_in = max(self.block, 2 * self.m)
-        S, d = self.S, self.d
-        dirs = np.zeros((S, n_calls, d), dtype=np.float32)
-        unif = np.zeros((S, n_calls, max_in // 2), dtype=np.float32)
-        perms = np.zeros((S, n_calls, max_in), dtype=np.int32)
-        methods: List[int] = []
-        for s, g in enumerate(self._gens):
-            for c, n_in in enumerate(sizes):
-                method, dvec, u, perm = _plan._draw_one_call(g, n_in, d, self.compressor)
-                if s == 0:
-                    methods.append(method)
-                if dvec is not None:
-                    dirs[s, c] = dvec
-                    unif[s, c, : u.shape[0]] = u
-                if perm is not None:
-                    perms[s, c, : perm.shape[0]] = perm
+        methods = [_plan._call_method(n_in, self.compressor) for n_in in sizes]
+        dirs, unif, perms = self._gens.next(sizes, self.d, self.compressor, max_in)
         dev = self.device
         return _CompletionDraws(
             blocks_before, n_calls, torch.tensor(methods, dtype=torch.int32).to(dev), torch.from_numpy(dirs).to(dev),
@@ -447,7 +433,7 @@ class DecodeState:
             "state_num": self.state_num.cpu(), "state_den": self.state_den.cpu(),
             "buf_k": self.buf_k[:, : self.buf_len].cpu(), "buf_v": self.buf_v[:, : self.buf_len].cpu(),
             **levels,
-            "generators": torch.stack([g.get_state() for g in self._gens]),
+            "generators": self._gens.get_state(),
             "draws": draws,
         }
 
@@ -480,8 +466,7 @@ class DecodeState:
             self.lev_pos[:, :n_lev] = sd["lev_pos"].to(dev)
         self.length, self.blocks, self.buf_len = int(sd["length"]), int(sd["blocks"]), buf_len
         self.num_compressions = int(sd["num_compressions"])
-        for g, st in zip(self._gens, sd["generators"]):
-            g.set_state(st.clone())
+        self._gens.set_state(sd["generators"])
         self._draws = deque(_CompletionDraws(int(d["blocks_before"]), int(d["n_calls"]), d["methods"].to(dev),
                                              d["dirs"].to(dev), d["unif"].to(dev), d["perms"].to(dev))
                             for d in sd["draws"])

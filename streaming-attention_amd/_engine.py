@@ -164,6 +164,7 @@ class PrefillResult:
     feature_count: int
     fsplit: int
     den: Optional[torch.Tensor] = None  # raw denominator (semantics "taylor")
+    moment_kernel: str = ""  # the moment-scan kernel that ran: "moments_ws_kernel" or "moments_kernel"
 
 
 def prefill(
@@ -387,7 +388,8 @@ def prefill(
         _native.check(st, "sta_block_attention")
 
     _run(timer, "block_attention", k24)
-    return PrefillResult(out, node_src, node_w, plan, ft.count, fsplit, out_den)
+    return PrefillResult(out, node_src, node_w, plan, ft.count, fsplit, out_den,
+                         "moments_ws_kernel" if qblock is not None else "moments_kernel")
 
 
 def flash(q3: torch.Tensor, k3: torch.Tensor, v3: torch.Tensor, *, scale: float,

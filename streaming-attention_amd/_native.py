@@ -137,6 +137,109 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+DRAWS_LIB_PATH = _HERE / "libstadraws.so"
+COMPRESSOR_CODES = {"none": 0, "random": 1, "sorted_pair": 2}
+_draws_lib: Optional[ctypes.CDLL] = None
+
+
+def draws_library() -> ctypes.CDLL:
+    """libstadraws.so: the compressor's seed-derived draws replayed on torch's CPU generator
+    (csrc/host_draws.cpp; host only, loaded after torch so that its torch libraries resolve)."""
+    global _draws_lib
+    if _draws_lib is None:
+        if not DRAWS_LIB_PATH.exists():
+            raise ImportError(f"libstadraws.so not found at {DRAWS_LIB_PATH}; build it with "
+                              f"`python -c 'import __graft_entry__ as g; g.build()'`")
+        h = ctypes.CDLL(str(DRAWS_LIB_PATH))
+        p, i = ctypes.c_void_p, ctypes.c_int
+        for name, res, args in (("sta_draws_open", p, [p, i]),
+                                ("sta_draws_close", None, [p]),
+                                ("sta_draws_next", i, [p, p, i, i, i, i, p, p, p]),
+                                ("sta_draws_state_bytes", ctypes.c_int64, []),
+                                ("sta_draws_get_state", i, [p, p]),
+                                ("sta_draws_set_state", i, [p, p]),
+                                ("sta_host_draws", i, [p, i, p, i, i, i, i, p, p, p]),
+                                ("sta_draws_error", ctypes.c_char_p, [])):
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _draws_lib = h
+    return _draws_lib
+
+
+def _draws_fail(h) -> None:
+    raise NativeError(h.sta_draws_error().decode())
+
+
+def _draw_tables(n_seq: int, call_sizes, d: int, compressor: str, max_in: int):
+    import numpy as np
+
+    if compressor not in COMPRESSOR_CODES:
+        raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
+    cc = max(len(call_sizes), 1)
+    sz = np.ascontiguousarray(np.asarray(call_sizes, dtype=np.int32))
+    return (sz, np.zeros((n_seq, cc, d), dtype=np.float32), np.zeros((n_seq, cc, max_in // 2), dtype=np.float32),
+            np.zeros((n_seq, cc, max_in), dtype=np.int32))
+
+
+def host_draws(seeds, call_sizes, d: int, compressor: str, max_in: int):
+    """Draw tables (dirs [S, C, d], unif [S, C, max_in // 2], perms int32 [S, C, max_in]; C = at least 1)
+    of len(seeds) sequences, each on a fresh generator seeded seeds[s], over the compress calls of
+    call_sizes, in call order."""
+    import numpy as np
+
+    sz, dirs, unif, perms = _draw_tables(len(seeds), call_sizes, d, compressor, max_in)
+    sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.int64))
+    h = draws_library()
+    if h.sta_host_draws(sd.ctypes.data, len(seeds), sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor],
+                        max_in, dirs.ctypes.data, unif.ctypes.data, perms.ctypes.data) != 0:
+        _draws_fail(h)
+    return dirs, unif, perms
+
+
+class DrawSet:
+    """Persistent per-stream CPU generators (stream s seeded seeds[s]) that successive compress calls
+    continue; states read and written in torch.Generator.get_state()'s layout."""
+
+    def __init__(self, seeds) -> None:
+        import numpy as np
+
+        self._h = draws_library()
+        sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.int64))
+        self.n = int(sd.shape[0])
+        self._ptr = self._h.sta_draws_open(sd.ctypes.data, self.n)
+        if not self._ptr:
+            _draws_fail(self._h)
+
+    def __del__(self) -> None:
+        if getattr(self, "_ptr", None):
+            self._h.sta_draws_close(self._ptr)
+            self._ptr = None
+
+    def next(self, call_sizes, d: int, compressor: str, max_in: int):
+        """Tables as host_draws, continuing every stream's generator."""
+        sz, dirs, unif, perms = _draw_tables(self.n, call_sizes, d, compressor, max_in)
+        if self._h.sta_draws_next(self._ptr, sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor], max_in,
+                                  dirs.ctypes.data, unif.ctypes.data, perms.ctypes.data) != 0:
+            _draws_fail(self._h)
+        return dirs, unif, perms
+
+    def get_state(self) -> torch.Tensor:
+        """uint8 [n, state bytes]: row s is stream s's torch.Generator.get_state()."""
+        out = torch.empty((self.n, int(self._h.sta_draws_state_bytes())), dtype=torch.uint8)
+        if self._h.sta_draws_get_state(self._ptr, out.data_ptr()) != 0:
+            _draws_fail(self._h)
+        return out
+
+    def set_state(self, states: torch.Tensor) -> None:
+        nb = int(self._h.sta_draws_state_bytes())
+        st = states.to(torch.uint8).contiguous()
+        if tuple(st.shape) != (self.n, nb):
+            raise ValueError(f"generator states must be uint8 [{self.n}, {nb}], got {tuple(st.shape)}")
+        if self._h.sta_draws_set_state(self._ptr, st.data_ptr()) != 0:
+            _draws_fail(self._h)
+
+
 def check(status: int, what: str) -> None:
     if status == STA_OK:
         return

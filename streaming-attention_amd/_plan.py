@@ -24,6 +24,8 @@ from typing import Dict, List, Optional, Tuple
 import numpy as np
 import torch
 
+import _native
+
 TILE_ROWS = 128  # must equal sta_tile_rows()
 NODE_DESC = 8
 NODE_META = 4
@@ -462,10 +464,27 @@ def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str):
     return METHOD_SORTED_PAIR, direction.numpy(), u.numpy(), None
 
 
+def _call_method(n_in: int, compressor: str) -> int:
+    if compressor == "none" or n_in <= 1:
+        return METHOD_COPY
+    if compressor not in ("random", "sorted_pair"):
+        raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
+    return METHOD_PERM if compressor == "random" or n_in <= 2 else METHOD_SORTED_PAIR
+
+
 def _collect_draws(seeds: List[int], call_sizes: List[int], d: int, compressor: str) -> Tuple[Draws, List[int]]:
+    """Draws of every sequence over the compress calls of call_sizes, replayed natively (the same
+    generator calls as _draw_one_call, per sequence on its own generator, sequences in parallel)."""
+    methods = [_call_method(n_in, compressor) for n_in in call_sizes]
+    max_in = max(max(call_sizes) if call_sizes else 2, 2)
+    dirs, unif, perms = _native.host_draws(seeds, call_sizes, d, compressor, max_in)
+    return Draws(dirs, unif, perms, len(call_sizes), max_in), methods
+
+
+def _collect_draws_py(seeds: List[int], call_sizes: List[int], d: int, compressor: str) -> Tuple[Draws, List[int]]:
+    """The same draws one generator call at a time through torch's Python API."""
     n_calls = len(call_sizes)
-    max_in = max(call_sizes) if call_sizes else 2
-    max_in = max(max_in, 2)
+    max_in = max(max(call_sizes) if call_sizes else 2, 2)
     bh = len(seeds)
     dirs = np.zeros((bh, max(n_calls, 1), d), dtype=np.float32)
     unif = np.zeros((bh, max(n_calls, 1), max_in // 2), dtype=np.float32)

@@ -11,6 +11,9 @@ width, value-column tiles, element size).  Objects go to streaming-attention_amd
 
 Packed-fp32 VALU instructions are disabled (-packed-fp32-ops): the kernels are written for the
 scalar fp32 and MFMA paths.
+
+libstadraws.so (csrc/host_draws.cpp, host only) is built beside it with g++ against torch's CPU
+libraries: the replay of the compressor's seed-derived draws on torch's CPU generator.
 """
 
 from __future__ import annotations
@@ -41,6 +44,7 @@ UNITS = tuple(("launch_moments_ws.hip", f"launch_moments_ws_{es}_{ct}", (f"-DSTA
 )
 OBJDIR = HERE / "_build"
 OUT = HERE / "libstreamattn.so"
+DRAWS_OUT = HERE / "libstadraws.so"
 ARCH = os.environ.get("STA_OFFLOAD_ARCH", "gfx950")
 NOISE = "'-packed-fp32-ops' is not a recognized feature for this target"
 
@@ -62,10 +66,33 @@ def _messages(res_out: str) -> list[str]:
     return [ln for ln in res_out.splitlines() if NOISE not in ln]
 
 
+def _draws_cmd(out: pathlib.Path) -> list[str]:
+    import torch.utils.cpp_extension as ext
+    import torch
+
+    inc = ext.include_paths()
+    libs = ext.library_paths()
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+            f"-D_GLIBCXX_USE_CXX11_ABI={int(torch.compiled_with_cxx11_abi())}",
+            *[f"-I{d}" for d in inc], str(CSRC / "host_draws.cpp"), "-o", str(out),
+            *[f"-L{d}" for d in libs], "-lc10", "-ltorch_cpu", *[f"-Wl,-rpath,{d}" for d in libs]]
+
+
 def build(verbose: bool = False, only: str = "") -> pathlib.Path:
     """Compile every unit (or, with `only`, the units whose object stem starts with it, reusing the
-    other objects from an earlier build) and link the library."""
+    other objects from an earlier build) and link the library; libstadraws.so is rebuilt alongside
+    unless `only` names HIP units."""
     OBJDIR.mkdir(exist_ok=True)
+    draws = None
+    if not only or only == "host":
+        tmp_d = DRAWS_OUT.with_suffix(".so.tmp")
+        cmd = _draws_cmd(tmp_d)
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        dlog = open(OBJDIR / "host_draws.log", "w+")
+        draws = (dlog, tmp_d, subprocess.Popen(cmd, stdout=dlog, stderr=subprocess.STDOUT))
+        if only == "host":
+            only = "\0"  # no HIP unit matches
     cc = hipcc()
     jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     pending = [u for u in UNITS if u[1].startswith(only)]
@@ -98,6 +125,16 @@ def build(verbose: bool = False, only: str = "") -> pathlib.Path:
                 print("\n".join(msgs))
             if verbose:
                 print(f"  {stem}: done at {time.time() - t0:.0f} s", flush=True)
+    if draws is not None:
+        dlog, tmp_d, p = draws
+        p.wait()
+        dlog.seek(0)
+        msg = dlog.read()
+        dlog.close()
+        if p.returncode != 0:
+            failed.append("host_draws.cpp:\n" + msg)
+        else:
+            os.replace(tmp_d, DRAWS_OUT)
     if failed:
         raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
     tmp = OUT.with_suffix(".so.tmp")
