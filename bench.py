@@ -323,6 +323,18 @@ def main() -> int:
     per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_step": round(tot / args.steps, 4)}
                   for name, (tot, cnt) in timer.totals_ms().items()}
 
+    # the compressor alone: the same steps with its launches on the main stream, not overlapping the scan
+    overlap = _engine.OVERLAP_COMPRESS
+    _engine.OVERLAP_COMPRESS = False
+    serial = _engine.KernelTimer()
+    for _ in range(3):
+        step(serial)
+    torch.cuda.synchronize()
+    _engine.OVERLAP_COMPRESS = overlap
+    ser = serial.totals_ms()
+    compress_alone = ({"ms_per_step": round(ser["compress"][0] / 3, 4), "launches_per_step": ser["compress"][1] // 3}
+                      if "compress" in ser else None)
+
     # cold calls through the public API, each at a seed no earlier call used: host draw replay, their
     # upload and the kernels (and, the second time, the plan of a shape seen for the first time)
     def cold_call(fresh_seed, clear_plans):
@@ -383,6 +395,7 @@ def main() -> int:
         "kernels": per_kernel,
         "kernels_note": ("compress runs on a second stream overlapping moments; its HIP-event interval "
                          "includes the wait for compute units" if _engine.OVERLAP_COMPRESS else ""),
+        "compress_alone": compress_alone,
         "host_plan_and_draws_s": round(t_plan, 3),
         "cold_call_ms": round(sorted(cold_ms)[1], 3),
         "cold_call_note": ("public API call at a seed no earlier call used (host draw replay for every sequence, "

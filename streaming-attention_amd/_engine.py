@@ -28,9 +28,8 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
 # Run the level / block compressor on a second stream, overlapping the moment scan's tail (the scan's
 # workgroups hold the compute units' LDS, so the compressor's start as the scan's shorter workgroups
-# finish).  On 32 heads x 65536 tokens: 11.47-11.49 ms per step against 11.81-11.88 ms without on one
-# box, no difference (12.15-12.25 against 12.17-12.18 ms) on another.
-OVERLAP_COMPRESS = True
+# finish).  STA_OVERLAP_COMPRESS=0 runs it on the caller's stream (its kernels then time alone).
+OVERLAP_COMPRESS = os.environ.get("STA_OVERLAP_COMPRESS", "1") != "0"
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 

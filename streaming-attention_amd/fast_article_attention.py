@@ -23,8 +23,6 @@ from __future__ import annotations
 
 import argparse
 import math
-import statistics
-import time
 from dataclasses import dataclass
 from typing import List, Optional, Tuple, Union
 
@@ -32,6 +30,7 @@ import torch
 
 import _engine
 import _plan
+from _cli_util import fmt_bytes, pick_device, wall_ms
 
 Tensor = torch.Tensor
 
@@ -60,12 +59,6 @@ _DTYPES = {
 }
 
 
-def _resolve_device(device: Optional[Union[str, torch.device]]) -> torch.device:
-    if device is None or str(device) == "auto":
-        return torch.device("cuda" if torch.cuda.is_available() else "cpu")
-    return torch.device(device)
-
-
 def _resolve_dtype(dtype: Union[str, torch.dtype]) -> torch.dtype:
     if isinstance(dtype, torch.dtype):
         return dtype
@@ -78,21 +71,6 @@ def _resolve_dtype(dtype: Union[str, torch.dtype]) -> torch.dtype:
 def _attention_scale(scale: Optional[float], dim: int) -> float:
     """1/sqrt(D) when scale is None (fast_article_attention.py:76-77)."""
     return float(1.0 / math.sqrt(dim)) if scale is None else float(scale)
-
-
-def _sync(device: torch.device) -> None:
-    if device.type == "cuda":
-        torch.cuda.synchronize(device)
-
-
-def _human_bytes(num_bytes: int) -> str:
-    x = float(num_bytes)
-    units = ("B", "KiB", "MiB", "GiB", "TiB")
-    for unit in units:
-        if abs(x) < 1024.0 or unit == units[-1]:
-            return f"{x:.2f} {unit}"
-        x /= 1024.0
-    return f"{x:.2f} TiB"
 
 
 def exp_taylor(logits: Tensor, degree: int) -> Tensor:
@@ -414,23 +392,10 @@ def _make_data(n: int, d: int, dv: int, *, radius: float, data: str, device: tor
     return q, k, v
 
 
-def _time_call(fn, repeats: int, device: torch.device) -> Tuple[float, float]:
-    """One warm-up, then median and min wall time in ms (fast_article_attention.py:761-770)."""
-    fn()
-    _sync(device)
-    times = []
-    for _ in range(repeats):
-        t0 = time.perf_counter()
-        fn()
-        _sync(device)
-        times.append((time.perf_counter() - t0) * 1000.0)
-    return statistics.median(times), min(times)
-
-
 def _demo(args: argparse.Namespace) -> None:
     if args.threads is not None:
         torch.set_num_threads(args.threads)
-    device = _resolve_device(args.device)
+    device = pick_device(args.device)
     dtype = _resolve_dtype(args.dtype)
     scale = args.scale if args.scale is not None else (1.0 / math.sqrt(args.d) if args.standard_scale else 1.0)
     rows = []
@@ -442,13 +407,13 @@ def _demo(args: argparse.Namespace) -> None:
             seed=args.seed, query_chunk_size=args.query_chunk_size, low_mode=args.low_mode, return_stats=rs)
         exact = classical_causal_attention(q, k, v, scale=scale)
         approx, stats = call(True)
-        classical_ms, _ = _time_call(lambda: classical_causal_attention(q, k, v, scale=scale), args.repeats, device)
-        fast_ms, _ = _time_call(call, args.repeats, torch.device("cuda") if torch.cuda.is_available() else device)
+        classical_ms, _ = wall_ms(lambda: classical_causal_attention(q, k, v, scale=scale), args.repeats, device)
+        fast_ms, _ = wall_ms(call, args.repeats, torch.device("cuda") if torch.cuda.is_available() else device)
         rows.append([
             str(n), f"{safe_relative_l2(approx, exact):.4g}", f"{(approx - exact).abs().max().item():.4g}",
-            f"{classical_ms:.3f}", f"{fast_ms:.3f}", _human_bytes(stats.approx_streaming_state_bytes),
-            _human_bytes(stats.scratch_low_prefix_bytes), _human_bytes(stats.scratch_residual_matrix_bytes),
-            _human_bytes(n * n * torch.tensor([], dtype=dtype).element_size()), str(stats.coreset_items),
+            f"{classical_ms:.3f}", f"{fast_ms:.3f}", fmt_bytes(stats.approx_streaming_state_bytes),
+            fmt_bytes(stats.scratch_low_prefix_bytes), fmt_bytes(stats.scratch_residual_matrix_bytes),
+            fmt_bytes(n * n * torch.tensor([], dtype=dtype).element_size()), str(stats.coreset_items),
         ])
     headers = ["n", "rel_l2", "max_abs", "classical_ms", "fast_ms", "approx_state", "low_scratch",
                "resid_scratch", "score_matrix", "coreset_items"]

@@ -13,7 +13,6 @@ from __future__ import annotations
 
 import argparse
 import math
-import statistics
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple, Union
 
@@ -21,6 +20,7 @@ import torch
 
 import _engine
 import _native
+from _cli_util import event_ms, fmt_bytes
 from fast_article_attention import safe_relative_l2  # noqa: F401  (re-exported like the reference)
 
 Tensor = torch.Tensor
@@ -47,15 +47,6 @@ def _ceil_div(a: int, b: int) -> int:
 
 def _attention_scale(scale: Optional[float], dim: int) -> float:
     return float(1.0 / math.sqrt(dim) if scale is None else scale)
-
-
-def _human_bytes(num_bytes: int) -> str:
-    x = float(num_bytes)
-    for unit in ("B", "KiB", "MiB", "GiB", "TiB"):
-        if abs(x) < 1024.0 or unit == "TiB":
-            return f"{x:.2f} {unit}"
-        x /= 1024.0
-    return f"{x:.2f} TiB"
 
 
 def exp_taylor(x: Tensor, degree: int) -> Tensor:
@@ -104,11 +95,9 @@ def _flatten_bh_qkv(q: Tensor, k: Tensor, v: Tensor) -> Tuple[Tensor, Tensor, Te
     raise ValueError("q/k/v must be [N,D] or [B,H,N,D]")
 
 
-def _unflatten_output(out3: Tensor, original_q_shape: Tuple[int, ...], had_bh: bool) -> Tensor:
-    if not had_bh:
-        return out3[0]
-    b, h, n, _ = original_q_shape
-    return out3.view(b, h, n, out3.shape[-1])
+def _restore_shape(out3: Tensor, q_shape: Tuple[int, ...], batched: bool) -> Tensor:
+    """[BH, N, Dv] kernel output back to the caller's [B, H, N, Dv], or [N, Dv] for one sequence."""
+    return out3.reshape(*q_shape[:-1], out3.shape[-1]) if batched else out3[0]
 
 
 @dataclass(frozen=True)
@@ -211,7 +200,7 @@ def triton_article_causal_attention(
     res = _engine.prefill(q3, k3, v3, degree=degree, block=block_size, scale=_attention_scale(scale, dim),
                           semantics="segment", stride=compress_stride, exp_clamp=True, eps=denominator_eps,
                           out_dtype=out_dtype)
-    out = _unflatten_output(res.out, original_shape, had_bh)
+    out = _restore_shape(res.out, original_shape, had_bh)
     if not return_stats:
         return out
     r = max(0, (n - 1) // block_size) * (block_size // compress_stride)
@@ -250,7 +239,7 @@ def triton_flash_causal_attention(
     if not (q3.dtype == k3.dtype == v3.dtype) or q3.dtype not in _native.DTYPE_CODES:
         q3, k3, v3 = q3.float(), k3.float(), v3.float()
     out3 = _engine.flash(q3, k3, v3, scale=_attention_scale(scale, dim), out_dtype=output_dtype or torch.float32)
-    return _unflatten_output(out3, original_shape, had_bh)
+    return _restore_shape(out3, original_shape, had_bh)
 
 
 # ----------------------------------------------------------------------------- demo / benchmark CLI
@@ -292,23 +281,6 @@ def _resolve_dtype(name: str) -> torch.dtype:
     return _DTYPES[name.lower()]
 
 
-def _bench_gpu_ms(fn, repeats: int) -> float:
-    """Median of `repeats` HIP-event timings after 3 warm-up calls."""
-    for _ in range(3):
-        fn()
-    torch.cuda.synchronize()
-    times: List[float] = []
-    for _ in range(repeats):
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        fn()
-        end.record()
-        torch.cuda.synchronize()
-        times.append(float(start.elapsed_time(end)))
-    return statistics.median(times)
-
-
 def _demo(args: argparse.Namespace) -> None:
     _require_backend()
     if not torch.cuda.is_available():
@@ -330,15 +302,15 @@ def _demo(args: argparse.Namespace) -> None:
         exact = torch_classical_causal_attention(q.float(), k.float(), v.float(), scale=scale)
         flash = triton_flash_causal_attention(q, k, v, scale=scale, **tiles)
         article, stats = triton_article_causal_attention(q, k, v, return_stats=True, **article_kw)
-        torch_ms = _bench_gpu_ms(lambda: torch_classical_causal_attention(q.float(), k.float(), v.float(), scale=scale),
+        torch_ms = event_ms(lambda: torch_classical_causal_attention(q.float(), k.float(), v.float(), scale=scale),
                                  args.repeats)
-        flash_ms = _bench_gpu_ms(lambda: triton_flash_causal_attention(q, k, v, scale=scale, **tiles), args.repeats)
-        article_ms = _bench_gpu_ms(lambda: triton_article_causal_attention(q, k, v, **article_kw), args.repeats)
+        flash_ms = event_ms(lambda: triton_flash_causal_attention(q, k, v, scale=scale, **tiles), args.repeats)
+        article_ms = event_ms(lambda: triton_article_causal_attention(q, k, v, **article_kw), args.repeats)
         print(" | ".join([
             str(n), f"{safe_relative_l2(article, exact):.4g}", f"{(article - exact).abs().max().item():.4g}",
             f"{safe_relative_l2(flash, exact):.4g}", f"{torch_ms:.3f}", f"{flash_ms:.3f}", f"{article_ms:.3f}",
-            str(stats.coreset_items_per_sequence), _human_bytes(stats.coreset_bytes_per_sequence),
-            _human_bytes(stats.kv_bytes_per_sequence), _human_bytes(stats.score_matrix_bytes_per_sequence),
+            str(stats.coreset_items_per_sequence), fmt_bytes(stats.coreset_bytes_per_sequence),
+            fmt_bytes(stats.kv_bytes_per_sequence), fmt_bytes(stats.score_matrix_bytes_per_sequence),
         ]))
 
 
