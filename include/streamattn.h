@@ -9,7 +9,8 @@
  *
  * Conventions
  *   - All tensors are caller-owned device buffers passed as raw pointers; the library never
- *     allocates or frees device memory.  q/k are contiguous [BH, N, D], v is [BH, N, Dv].
+ *     allocates or frees device memory (sta_decode_step_static's fixed static scratch aside).
+ *     q/k are contiguous [BH, N, D], v is [BH, N, Dv].
  *   - dtype codes: STA_F32, STA_BF16, STA_F16 (inputs are read as such, arithmetic is fp32).
  *   - `stream` is a hipStream_t (NULL = the default stream); launches are asynchronous.
  *   - Every function returns STA_OK (0) or a positive status; sta_status_string() names it.
@@ -29,6 +30,10 @@ extern "C" {
 #define STA_ERR_DTYPE 3       /* unknown dtype code                                    */
 #define STA_ERR_HIP 4         /* a HIP runtime call failed (see sta_last_hip_error)    */
 #define STA_ERR_ARG 5         /* null pointer or out-of-range scalar argument          */
+#define STA_ERR_SCRATCH 6     /* working set beyond the static scratch (sta_decode_step_static) */
+
+/* Bytes of the static device scratch of sta_decode_step_static, per device. */
+#define STA_STATIC_SCRATCH_BYTES ((int64_t)16 << 20)
 
 #define STA_F32 0
 #define STA_BF16 1
@@ -188,6 +193,26 @@ int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int6
                     const float* lev_k, const float* lev_v, const float* lev_w, int n_levels, int level_size,
                     uint64_t level_mask, const float* part_num, const float* part_den, int splits, void* out,
                     int out_dtype, float* stats, void* stream);
+
+/*
+ * No counterpart in the reference: a decode step that allocates nothing, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The same launches as sta_decode_moments followed by sta_decode_tail (flags must
+ * include QUERY), with the moment partials part_num [S][splits][ldv] and part_den [S][splits] held in a
+ * static device array of STA_STATIC_SCRATCH_BYTES per device instead of caller buffers
+ * (ldv = 32*ceil(dv/32); S * splits * ldv rounded up to 64, plus S * splits, floats must fit, else
+ * STA_ERR_SCRATCH).  state_num == state_den == NULL: no moment state (compressor "none"), the partials
+ * are zeroed by a kernel.  Every call on a device shares that device's array: calls that overlap on
+ * one device (concurrent streams, or host threads) race; calls on one stream are ordered.  The
+ * first call on a device looks up the array's address there (hipGetSymbolAddress).
+ */
+int64_t sta_static_scratch_bytes(void);
+int sta_decode_step_static(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
+                           int degree, float scale, float eps, int flags, const float* state_num,
+                           const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* buf_k,
+                           float* buf_v, int block, int buf_len, const float* lev_k, const float* lev_v,
+                           const float* lev_w, int n_levels, int level_size, uint64_t level_mask, void* out,
+                           int out_dtype, float* stats, void* stream);
 
 /*
  * Block completion: compress the full buffer (call 0) and merge cat(level i-1, previous output) for

@@ -301,6 +301,41 @@ class DecodeState:
         self.length += 1
         return out
 
+    def step_into(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                  stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """step(q, k, v) written into the caller's `out` [S, dv] without any device allocation: one
+        sta_decode_step_static call (the moment partials live in the library's static scratch).  The
+        inputs must already be contiguous [S, d] / [S, dv] device tensors of one supported dtype; a token
+        that completes a block (compress, merges, host draws) is refused: use step() for it."""
+        if (not self.exact and self.buf_len + 1 == self.block) or (self.exact and self.buf_len == self.cap):
+            raise ValueError("step_into cannot complete a block; call step() for this token")
+        for x, width, what in ((q, self.d, "query"), (k, self.d, "key"), (v, self.dv, "value")):
+            if x.shape != (self.S, width) or x.device != self.device or not x.is_contiguous():
+                raise ValueError(f"{what} must be a contiguous [{self.S}, {width}] tensor on {self.device}")
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _native.DTYPE_CODES:
+            raise ValueError("q, k, v must share one of the dtypes float32, bfloat16, float16")
+        if out.shape != (self.S, self.dv) or out.device != self.device or not out.is_contiguous() or \
+                out.dtype not in _native.DTYPE_CODES:
+            raise ValueError(f"out must be a contiguous [{self.S}, {self.dv}] float32/bfloat16/float16 tensor "
+                             f"on {self.device}")
+        flags = _native.DEC_APPEND | _native.DEC_CURRENT | _native.DEC_QUERY
+
+        def run():
+            st = self.lib.sta_decode_step_static(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), _native.DTYPE_CODES[q.dtype], self.S, self.d, self.dv,
+                self.degree, self.scale, self.eps, flags,
+                None if self.exact else self.state_num.data_ptr(), None if self.exact else self.state_den.data_ptr(),
+                self.F, self.findex.data_ptr(), self.splits, self.buf_k.data_ptr(), self.buf_v.data_ptr(), self.cap,
+                self.buf_len, self.lev_k.data_ptr(), self.lev_v.data_ptr(), self.lev_w.data_ptr(), self.L, self.m,
+                self.blocks if not self.exact else 0, out.data_ptr(), _native.DTYPE_CODES[out.dtype],
+                _native.ptr(stats), self._stream())
+            _native.check(st, "sta_decode_step_static")
+
+        self._launch("decode_step_static", run)
+        self.buf_len += 1
+        self.length += 1
+        return out
+
     def extend(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """update() for every token of k [S, P, d] / v [S, P, dv], in bulk: whole blocks go to the state
         in one moment-accumulate launch and are compressed block by block."""

@@ -22,6 +22,7 @@ STA_ERR_UNSUPPORTED = 2
 STA_ERR_DTYPE = 3
 STA_ERR_HIP = 4
 STA_ERR_ARG = 5
+STA_ERR_SCRATCH = 6
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 PRODUCTS_FP32 = 0
@@ -100,6 +101,17 @@ _SIGNATURES = {
             _i64, _i32, _i32, _c_p, _c_p, _i32, _i32,  # S d dv buf_k buf_v block pos0
             _c_p, _c_p, _c_p, _c_p, _i32, _i32,  # lev_k lev_v lev_w lev_pos n_levels level_size
             _i32, _c_p, _c_p, _c_p, _c_p, _i32, _c_p,  # n_calls methods dirs unif perms max_in stream
+        ],
+    ),
+    "sta_static_scratch_bytes": (_i64, []),
+    "sta_decode_step_static": (
+        _i32,
+        [
+            _c_p, _c_p, _c_p, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _i32,  # q k v dtype S d dv deg scale eps flags
+            _c_p, _c_p, _i32, _c_p, _i32,  # state_num state_den n_feat feat_index splits
+            _c_p, _c_p, _i32, _i32,  # buf_k buf_v block buf_len
+            _c_p, _c_p, _c_p, _i32, _i32, ctypes.c_uint64,  # lev_k lev_v lev_w n_levels level_size mask
+            _c_p, _i32, _c_p, _c_p,  # out out_dtype stats stream
         ],
     ),
     "sta_selftest_mfma": (_i32, [_c_p, _c_p, _c_p]),

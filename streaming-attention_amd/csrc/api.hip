@@ -1,7 +1,10 @@
 // extern "C" entry points of libstreamattn.so (declared in include/streamattn.h): argument checks and
 // kernel launches.  The moment and block-attention kernels are instantiated and launched from their own
 // units (launch_moments.hip, launch_accumulate.hip, launch_block.hip); this unit includes their sources
-// for the argument structs only.  The library allocates nothing; every buffer is the caller's.
+// for the argument structs only.  The library allocates nothing; every buffer is the caller's, except
+// the fixed static scratch of sta_decode_step_static (below).
+#include <mutex>
+
 #include "api_common.hpp"
 #include "block_attn.hip"
 #include "compress.hip"
@@ -14,6 +17,50 @@ thread_local int g_last_hip_error = 0;
 }  // namespace sta_api
 
 using namespace sta_api;
+
+// Device memory of sta_decode_step_static, the entry point for callers that cannot allocate: the
+// decode query's moment partials, part_num [S][splits][ldv] and then part_den [S][splits] from the next
+// 64-float (256-byte) boundary.  Each device the library runs on holds its own copy from module load
+// to process end.  In host code the name is not a device address: kernels get the per-device pointer
+// from static_scratch_ptr().
+static __device__ __align__(256) float scratch[STA_STATIC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Address of `scratch` on `device`, looked up once per device with that device current.
+int static_scratch_ptr(int device, float** out) {
+  if (device < 0 || device >= kMaxDevices) return STA_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    int cur = -1;
+    int st = hip_status(hipGetDevice(&cur));
+    if (st != STA_OK) return st;
+    if (cur != device && (st = hip_status(hipSetDevice(device))) != STA_OK) return st;
+    void* p = nullptr;
+    st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (cur != device) {
+      const int back = hip_status(hipSetDevice(cur));
+      if (st == STA_OK) st = back;
+    }
+    if (st != STA_OK) return st;
+    if (!p) return STA_ERR_HIP;
+    g_scratch_ptr[device] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return STA_OK;
+}
+
+__global__ void zero_fill_kernel(float* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0.f;
+}
+
+}  // namespace
 
 namespace {
 
@@ -60,6 +107,7 @@ const char* sta_status_string(int status) {
     case STA_ERR_DTYPE: return "unknown dtype code";
     case STA_ERR_HIP: return "HIP runtime error";
     case STA_ERR_ARG: return "invalid argument";
+    case STA_ERR_SCRATCH: return "working set exceeds the static scratch (sta_static_scratch_bytes per device)";
     default: return "unknown status";
   }
 }
@@ -313,6 +361,49 @@ int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int6
   else if (vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 2>), grid, dim3(sta::DEC_THREADS), 0, s, a);
   else hipLaunchKernelGGL((sta::decode_tail_kernel<2, 4>), grid, dim3(sta::DEC_THREADS), 0, s, a);
   return check_launch();
+}
+
+int64_t sta_static_scratch_bytes(void) { return STA_STATIC_SCRATCH_BYTES; }
+
+int sta_decode_step_static(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
+                           int degree, float scale, float eps, int flags, const float* state_num,
+                           const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* buf_k,
+                           float* buf_v, int block, int buf_len, const float* lev_k, const float* lev_v,
+                           const float* lev_w, int n_levels, int level_size, uint64_t level_mask, void* out,
+                           int out_dtype, float* stats, void* stream) {
+  if (!(flags & sta::DEC_QUERY)) return STA_ERR_ARG;
+  if (streams <= 0 || splits <= 0 || dv <= 0) return STA_ERR_SHAPE;
+  if (dv > kMaxDv || d > kMaxD) return STA_ERR_UNSUPPORTED;
+  if ((state_num == nullptr) != (state_den == nullptr)) return STA_ERR_ARG;
+  const int64_t ldv = 32 * ((dv + 31) / 32);
+  // part_num, then part_den from the next 64-float boundary, within the static scratch
+  const int64_t num_floats = streams * splits * ldv;
+  const int64_t den_off = (num_floats + 63) / 64 * 64;
+  const int64_t used = den_off + streams * splits;
+  if (streams > (int64_t(1) << 31) || splits > (1 << 20) || used * int64_t(sizeof(float)) > STA_STATIC_SCRATCH_BYTES)
+    return STA_ERR_SCRATCH;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int device = -1;
+  int st = hip_status(s ? hipStreamGetDevice(s, &device) : hipGetDevice(&device));
+  if (st != STA_OK) return st;
+  float* base = nullptr;
+  if ((st = static_scratch_ptr(device, &base)) != STA_OK) return st;
+  float* part_num = base;
+  float* part_den = base + den_off;
+  if (state_num) {
+    st = sta_decode_moments(q, dtype, streams, d, dv, scale, state_num, state_den, n_feat, feat_index, splits,
+                            part_num, part_den, stream);
+  } else {
+    // no moment state (every token answered from the buffer): zero partials, cleared by a kernel so
+    // that the call can sit in a captured graph
+    const int64_t blocks = (used + 255) / 256 < 1024 ? (used + 255) / 256 : 1024;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, base, used);
+    st = check_launch();
+  }
+  if (st != STA_OK) return st;
+  return sta_decode_tail(q, k, v, dtype, streams, d, dv, degree, scale, eps, flags, buf_k, buf_v, block, buf_len,
+                         lev_k, lev_v, lev_w, n_levels, level_size, level_mask, part_num, part_den, splits, out,
+                         out_dtype, stats, stream);
 }
 
 int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, const float* buf_v, int block, int pos0,

@@ -457,6 +457,19 @@ class ArticleStreamingAttention:
         return self._finish(out, stats)
 
     @torch.no_grad()
+    def step_into(self, query: Tensor, key: Tensor, value: Tensor, out: Tensor) -> Tensor:
+        """step() into a caller-owned `out` ([value_dim], or [S, value_dim] batched) with no device
+        allocation, for serving loops and graph capture: the inputs must already be contiguous device
+        tensors of this object's shapes and one dtype; a token that completes a block is refused (call
+        step() for it)."""
+        if self._single:
+            query, key, value, o2 = query.view(1, -1), key.view(1, -1), value.view(1, -1), out.view(1, -1)
+        else:
+            o2 = out
+        self._st.step_into(query, key, value, o2)
+        return out
+
+    @torch.no_grad()
     def extend(self, keys: Tensor, values: Tensor) -> None:
         """update() with every row of keys [P, dim] ([S, P, dim] batched) and values, in bulk."""
         if self._single:

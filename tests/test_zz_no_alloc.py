@@ -1,0 +1,71 @@
+"""sta_decode_step_static, the decode step that allocates nothing (its moment partials live in the
+library's static device scratch), through the C ABI on the GPU: its outputs equal the allocating path
+(sta_decode_moments + sta_decode_tail on caller buffers) bit for bit, token after token, on two calls in
+a row of which the second is smaller, and without a moment state (compressor "none", zeroed partials)."""
+
+import pytest
+import torch
+
+import _native
+import streaming_taylor_coreset_attention as stc
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _lockstep(streams, d, dv, block, prefix, steps, compressor="sorted_pair", dtype=torch.float32, seed=0):
+    """Two identical states: one advanced with step(), the other with step_into() wherever the token
+    does not complete a block; every output compared bit for bit."""
+    print(f"no-alloc lockstep: S={streams} d={d} dv={dv} block={block} prefix={prefix} steps={steps} "
+          f"{compressor} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(1000 + streams)
+    n = prefix + steps
+    q, k, v = ((torch.randn(streams, n, w, generator=g, device=DEV) * 0.125).to(dtype) for w in (d, d, dv))
+    ref, st = (stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=0.125, compressor=compressor,
+                                             device=DEV, dtype=dtype, seed=seed, streams=streams) for _ in range(2))
+    if prefix:
+        ref.extend(k[:, :prefix], v[:, :prefix])
+        st.extend(k[:, :prefix], v[:, :prefix])
+    out = torch.empty((streams, dv), device=DEV, dtype=dtype)
+    used = 0
+    for i in range(prefix, n):
+        qi, ki, vi = q[:, i].contiguous(), k[:, i].contiguous(), v[:, i].contiguous()
+        want = ref.step(qi, ki, vi)
+        s = st._st
+        if (not s.exact and s.buf_len + 1 == s.block) or (s.exact and s.buf_len == s.cap):
+            got = st.step(qi, ki, vi)
+        else:
+            got = st.step_into(qi, ki, vi, out).clone()
+            used += 1
+        assert torch.equal(got, want), f"token {i}"
+    torch.cuda.synchronize()
+    assert used >= steps - steps // block - 1
+    return used
+
+
+def test_static_step_matches_allocating_step_then_a_smaller_call():
+    # first call: 512 streams, d = dv = 64, through a block completion and the level merges around it
+    _lockstep(512, 64, 64, 64, prefix=200, steps=70)
+    # second call, smaller (fewer streams, narrower rows): the scratch keeps the first call's contents,
+    # every partial it reads must have been rewritten
+    _lockstep(24, 32, 40, 32, prefix=45, steps=40)
+
+
+def test_static_step_bf16_and_without_moment_state():
+    _lockstep(64, 64, 64, 64, prefix=100, steps=40, dtype=torch.bfloat16)
+    _lockstep(16, 16, 48, 32, prefix=10, steps=30, compressor="none")
+
+
+def test_static_step_refuses_a_working_set_beyond_the_scratch():
+    lib = _native.lib()
+    cap = lib.sta_static_scratch_bytes()
+    assert cap == 16 << 20
+    dv, splits = 64, 1
+    streams = cap // (4 * (dv + 1)) + 64  # partials of this many streams exceed the scratch
+    dummy = torch.zeros(64, device=DEV)
+    p = dummy.data_ptr()
+    st = lib.sta_decode_step_static(p, p, p, 0, streams, 64, dv, 2, 0.125, 1e-12, _native.DEC_QUERY, p, p, 2145, p,
+                                    splits, p, p, 64, 0, p, p, p, 0, 32, 0, p, 0, None, None)
+    assert st == _native.STA_ERR_SCRATCH
+    assert b"static scratch" in lib.sta_status_string(st)
