@@ -200,10 +200,23 @@ def prefill(
     bh, n, d = q3.shape
     dv = v3.shape[-1]
     lim = _native.limits()
-    if d > lim["max_d"] or dv > lim["max_dv"]:
-        raise ValueError(f"the HIP kernels support D <= {lim['max_d']} and Dv <= {lim['max_dv']}")
+    if d > lim["max_d"]:
+        raise ValueError(f"the HIP kernels support D <= {lim['max_d']} (the degree-2 feature tiles index "
+                         f"key dimensions in 8 bits and are sized for D <= 128)")
     if degree > lim["max_degree"]:
         raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+    if dv > lim["max_dv"]:
+        # value columns are independent given the keys (the denominator and the coreset selections do
+        # not depend on v): wide values run as column groups of at most max_dv, every group recomputing
+        # the same denominator and selections
+        parts = [prefill(q3, k3, v3[..., c0: c0 + lim["max_dv"]].contiguous(), degree=degree, block=block,
+                         scale=scale, semantics=semantics, compressor=compressor, seed=seed, eps=eps,
+                         out_dtype=out_dtype, stride=stride, exp_clamp=exp_clamp, draws=draws, timer=timer,
+                         products=products, residual_products=residual_products, moment_kernel=moment_kernel)
+                 for c0 in range(0, dv, lim["max_dv"])]
+        first = parts[0]
+        return PrefillResult(torch.cat([r.out for r in parts], dim=-1), first.node_src, first.node_w, first.plan,
+                             first.feature_count, first.fsplit, first.den, first.moment_kernel)
     if semantics == "segment" and q3.dtype != torch.float32:
         # segment means are fp32 and the residual kernel reads them with the inputs in one format
         q3, k3, v3 = q3.float(), k3.float(), v3.float()

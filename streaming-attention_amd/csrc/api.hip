@@ -54,6 +54,13 @@ int static_scratch_ptr(int device, float** out) {
   return STA_OK;
 }
 
+// Dynamic LDS above the default 64 KiB needs the kernel's limit raised first (gfx950: 160 KiB per
+// workgroup).
+int lds_limit(const void* kernel, size_t bytes) {
+  if (bytes <= 65536) return STA_OK;
+  return hip_status(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+}
+
 __global__ void zero_fill_kernel(float* p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
@@ -420,6 +427,7 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
   if (level_size != (block + 1) / 2) return STA_ERR_SHAPE;
   if (block > sta::CMP_MAX_IN || 2 * level_size > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
   if (max_in < block || max_in < 2 * level_size) return STA_ERR_ARG;
+  if (max_in > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
   if (streams > 0x7fffffff) return STA_ERR_UNSUPPORTED;
   int dk = 0, ldv = 0;
   sta_decode_layout(d, dv, &dk, &ldv);
@@ -427,7 +435,10 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
   a.buf_k = buf_k; a.buf_v = buf_v; a.B = block; a.d = d; a.dk = dk; a.ldv = ldv; a.pos0 = pos0;
   a.lev_k = lev_k; a.lev_v = lev_v; a.lev_w = lev_w; a.lev_pos = lev_pos; a.L = n_levels; a.m = level_size;
   a.n_calls = n_calls; a.methods = methods; a.dirs = dirs; a.unif = unif; a.perms = perms; a.max_in = max_in;
-  hipLaunchKernelGGL(sta::decode_compress_kernel, dim3(static_cast<unsigned>(streams)), dim3(sta::CMP_THREADS), 0,
+  const size_t smem = sizeof(float) * static_cast<size_t>(sta::dec_cmp_smem_floats(max_in));
+  const int st = lds_limit(reinterpret_cast<const void*>(sta::decode_compress_kernel), smem);
+  if (st != STA_OK) return st;
+  hipLaunchKernelGGL(sta::decode_compress_kernel, dim3(static_cast<unsigned>(streams)), dim3(sta::CMP_THREADS), smem,
                      static_cast<hipStream_t>(stream), a);
   return check_launch();
 }
@@ -447,8 +458,11 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
   a.k = k; a.dtype = dtype; a.n = n; a.d = d; a.batch = batch_nodes; a.desc = node_desc; a.n_nodes = n_nodes;
   a.cap = cap; a.dirs = dirs; a.unif = unif; a.perms = perms; a.n_draws = n_draws; a.max_in = max_in;
   a.node_src = node_src; a.node_w = node_w;
+  const size_t smem = sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in));
+  const int st = lds_limit(reinterpret_cast<const void*>(sta::compress_kernel), smem);
+  if (st != STA_OK) return st;
   hipLaunchKernelGGL(sta::compress_kernel, dim3(static_cast<unsigned>(n_batch), static_cast<unsigned>(bh)),
-                     dim3(sta::CMP_THREADS), 0, static_cast<hipStream_t>(stream), a);
+                     dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
   return check_launch();
 }
 

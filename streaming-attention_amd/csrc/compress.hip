@@ -26,8 +26,19 @@ namespace sta {
 enum NodeKind : int { KIND_RAW = 0, KIND_MERGE = 1 };
 enum NodeMethod : int { M_COPY = 0, M_SORTED_PAIR = 1, M_PERM = 2 };
 constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, unused
-constexpr int CMP_MAX_IN = 1024;
+constexpr int CMP_MAX_IN = 4096;
 constexpr int CMP_THREADS = 256;
+
+// Dynamic LDS of compress_kernel for calls of at most max_in items (M = max_in rounded up to 4):
+// sort keys [M] (16-byte aligned, padded for 4-wide reads), source indices [M], weights [M], sorted
+// positions [M], projection direction [128].
+__host__ __device__ constexpr int cmp_round4(int n) { return (n + 3) & ~3; }
+__host__ __device__ constexpr int cmp_smem_floats(int max_in) { return 4 * cmp_round4(max_in) + 128; }
+// decode_compress_kernel: sort keys, input handles, weights, positions, sorted positions [M] each, the
+// running output's handles, weights, positions [M/2 + 1 rounded up to 4] each, direction [128].
+__host__ __device__ constexpr int dec_cmp_smem_floats(int max_in) {
+  return 5 * cmp_round4(max_in) + 3 * cmp_round4(max_in / 2 + 1) + 128;
+}
 
 struct CompressArgs {
   const void* k;
@@ -122,11 +133,13 @@ __device__ __forceinline__ bool pair_keeps_first(float u, float wa, float wb) {
 }
 
 __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
-  __shared__ int src_s[CMP_MAX_IN];
-  __shared__ float w_s[CMP_MAX_IN];
-  __shared__ __align__(16) float key_s[CMP_MAX_IN];
-  __shared__ int pos_s[CMP_MAX_IN];
-  __shared__ float dir_s[128];
+  extern __shared__ __align__(16) float cmp_smem[];
+  const int M = cmp_round4(a.max_in);
+  float* key_s = cmp_smem;
+  int* src_s = reinterpret_cast<int*>(cmp_smem + M);
+  float* w_s = cmp_smem + 2 * M;
+  int* pos_s = reinterpret_cast<int*>(cmp_smem + 3 * M);
+  float* dir_s = cmp_smem + 4 * M;
 
   const int node = a.batch[blockIdx.x];
   const int64_t bh = blockIdx.y;

@@ -364,15 +364,17 @@ struct DecCmpArgs {
 };
 
 __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecCmpArgs a) {
-  __shared__ int in_h[CMP_MAX_IN];
-  __shared__ float in_w[CMP_MAX_IN];
-  __shared__ int in_p[CMP_MAX_IN];
-  __shared__ __align__(16) float key_s[CMP_MAX_IN];
-  __shared__ int pos_s[CMP_MAX_IN];
-  __shared__ int cur_h[CMP_MAX_IN / 2 + 1];
-  __shared__ float cur_w[CMP_MAX_IN / 2 + 1];
-  __shared__ int cur_p[CMP_MAX_IN / 2 + 1];
-  __shared__ float dir_s[128];
+  extern __shared__ __align__(16) float dcmp_smem[];
+  const int M = cmp_round4(a.max_in), H = cmp_round4(a.max_in / 2 + 1);
+  float* key_s = dcmp_smem;
+  int* in_h = reinterpret_cast<int*>(dcmp_smem + M);
+  float* in_w = dcmp_smem + 2 * M;
+  int* in_p = reinterpret_cast<int*>(dcmp_smem + 3 * M);
+  int* pos_s = reinterpret_cast<int*>(dcmp_smem + 4 * M);
+  int* cur_h = reinterpret_cast<int*>(dcmp_smem + 5 * M);
+  float* cur_w = dcmp_smem + 5 * M + H;
+  int* cur_p = reinterpret_cast<int*>(dcmp_smem + 5 * M + 2 * H);
+  float* dir_s = dcmp_smem + 5 * M + 3 * H;
   const int64_t s = blockIdx.x;
   const int tid = threadIdx.x;
   auto key_row = [&](int h) -> const float* {

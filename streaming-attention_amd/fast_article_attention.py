@@ -156,9 +156,14 @@ def _to_gpu(*tensors: Tensor) -> Tuple[List[Tensor], torch.device]:
 
 
 def _compute_dtype(t: Tensor) -> torch.dtype:
+    """Element type the kernels read: the input's for float32 / bfloat16 / float16; float64 inputs are
+    rounded to float32 (the kernels' arithmetic type; the coreset draws are then the float32 ones) and
+    the callers return float64 outputs."""
     if t.dtype in (torch.float32, torch.bfloat16, torch.float16):
         return t.dtype
-    raise ValueError(f"dtype {t.dtype} is not supported by the HIP kernels (use float32, bfloat16 or float16)")
+    if t.dtype == torch.float64:
+        return torch.float32
+    raise ValueError(f"dtype {t.dtype} is not supported (use float64, float32, bfloat16 or float16)")
 
 
 @torch.no_grad()

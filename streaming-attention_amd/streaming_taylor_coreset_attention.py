@@ -37,7 +37,7 @@ Tensor = torch.Tensor
 
 __all__ = ["ArticleStreamingAttention", "AttentionQueryStats", "CoresetBlock", "article_causal_attention",
            "article_causal_attention_single", "classical_causal_attention", "exp_taylor", "safe_relative_l2",
-           "state_size_trace"]
+           "state_size_trace", "coreset_item_trace"]
 
 
 def exp_taylor(logits: Tensor, degree: int) -> Tensor:
@@ -83,30 +83,36 @@ def _feature_count(dim: int, degree: int, max_monomials: int) -> int:
     return total
 
 
-def state_size_trace(n: int, dim: int, value_dim: int, degree: int, block_size: int, compressor: str,
-                     elem: int) -> List[int]:
-    """Per-token state bytes after update(k_i): moments plus buffer plus level coresets
-    (streaming_taylor_coreset_attention.py:298-306, :495-506, :611-612)."""
-    f = _plan.num_features(dim, degree)
-    moments = f * (1 + value_dim) * elem
-    plan = _plan.levels_plan(n, block_size, compressor) if compressor != "none" else None
-    sizes = []
-    nb_level_items = []
-    level_size = [0] * 64
-    # node size per level for a full level (independent of j)
-    if plan is not None and plan.level_of is not None and n >= block_size:
+def coreset_item_trace(n: int, block_size: int, compressor: str) -> List[int]:
+    """Per-token coreset size (MergeReduceCoreset.num_items after update(k_i): buffered tokens plus the
+    occupied levels' items, streaming_taylor_coreset_attention.py:489-493).  compressor "none" keeps
+    every token (its levels hold whole blocks, uncompressed)."""
+    if compressor == "none":
+        return list(range(1, n + 1))
+    per_level = [0] * 64  # items of an occupied level (the same for every node of a level)
+    plan = _plan.levels_plan(n, block_size, compressor) if n >= block_size else None
+    if plan is not None and plan.level_of is not None:
         for i in range(plan.n_nodes):
-            level_size[int(plan.level_of[i])] = int(plan.meta[i, 0])
+            per_level[int(plan.level_of[i])] = int(plan.meta[i, 0])
+    out = []
     for i in range(n):
         c = (i + 1) // block_size
-        buffered = (i + 1) - c * block_size
-        if compressor == "none":
-            items_bytes = c * block_size * (dim + value_dim + 1) * elem
-        else:
-            items = sum(level_size[l] for l in range(c.bit_length()) if (c >> l) & 1)
-            items_bytes = items * (dim + value_dim + 1) * elem
-        sizes.append(moments + buffered * (dim + value_dim) * elem + items_bytes)
-    del nb_level_items
+        out.append((i + 1) - c * block_size + sum(per_level[l] for l in range(c.bit_length()) if (c >> l) & 1))
+    return out
+
+
+def state_size_trace(n: int, dim: int, value_dim: int, degree: int, block_size: int, compressor: str,
+                     elem: int) -> List[int]:
+    """Per-token state bytes after update(k_i): moments plus buffered tokens (key and value) plus the
+    levels' items (key, value, weight) (streaming_taylor_coreset_attention.py:298-306, :495-506,
+    :611-612)."""
+    moments = _plan.num_features(dim, degree) * (1 + value_dim) * elem
+    items = coreset_item_trace(n, block_size, compressor)
+    sizes = []
+    for i in range(n):
+        buffered = (i + 1) % block_size
+        levels = items[i] - buffered
+        sizes.append(moments + buffered * (dim + value_dim) * elem + levels * (dim + value_dim + 1) * elem)
     return sizes
 
 
@@ -388,8 +394,11 @@ class ArticleStreamingAttention:
         self.compressor = str(compressor)
         self.device = _resolve_gpu(device)
         self.dtype = _resolve_dtype(dtype)
-        if self.dtype not in (torch.float32, torch.bfloat16, torch.float16):
-            raise ValueError(f"dtype {self.dtype} is not supported by the HIP kernels (float32, bfloat16, float16)")
+        if self.dtype not in (torch.float64, torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError(f"dtype {self.dtype} is not supported (float64, float32, bfloat16, float16)")
+        # what the kernels read and write: float64 tokens are rounded to float32 (the kernels' arithmetic
+        # type) and outputs converted back; sizes and views keep the reference's dtype
+        self._kdtype = torch.float32 if self.dtype == torch.float64 else self.dtype
         self.seed = int(seed)
         self.denominator_eps = float(denominator_eps)
         self._single = streams is None
@@ -406,13 +415,13 @@ class ArticleStreamingAttention:
         if tuple(x.shape) != want:
             shape = f"[{width}]" if self._single else f"[{self.streams}, {width}]"
             raise ValueError(f"{what} must have shape {shape}, got {tuple(x.shape)}")
-        return x.to(device=self.device, dtype=self.dtype).reshape(self.streams, width)
+        return x.to(device=self.device, dtype=self._kdtype).reshape(self.streams, width)
 
     def _stats_buffer(self, return_stats: bool) -> Optional[Tensor]:
         return torch.empty((self.streams, 4), device=self.device, dtype=torch.float32) if return_stats else None
 
     def _finish(self, out: Tensor, stats: Optional[Tensor]):
-        out = out[0] if self._single else out
+        out = (out[0] if self._single else out).to(self.dtype)
         if stats is None:
             return out
         st = stats.cpu()
@@ -434,7 +443,7 @@ class ArticleStreamingAttention:
         """low + weighted exp_{>t} tail over items(), divided by clamp(den, eps)
         (streaming_taylor_coreset_attention.py:581-609)."""
         stats = self._stats_buffer(return_stats)
-        out = self._st.query(self._rows(query, self.dim, "query"), out_dtype=self.dtype, stats=stats)
+        out = self._st.query(self._rows(query, self.dim, "query"), out_dtype=self._kdtype, stats=stats)
         return self._finish(out, stats)
 
     def state_size_bytes(self, *, include_feature_map: bool = False) -> int:
@@ -453,7 +462,7 @@ class ArticleStreamingAttention:
         when the token completes a block)."""
         stats = self._stats_buffer(return_stats)
         out = self._st.step(self._rows(query, self.dim, "query"), self._rows(key, self.dim, "key"),
-                            self._rows(value, self.value_dim, "value"), out_dtype=self.dtype, stats=stats)
+                            self._rows(value, self.value_dim, "value"), out_dtype=self._kdtype, stats=stats)
         return self._finish(out, stats)
 
     @torch.no_grad()
@@ -476,7 +485,8 @@ class ArticleStreamingAttention:
             if keys.ndim != 2 or keys.shape[-1] != self.dim or tuple(values.shape) != (keys.shape[0], self.value_dim):
                 raise ValueError("keys / values must have shapes [P, dim] / [P, value_dim]")
             keys, values = keys[None], values[None]
-        self._st.extend(keys.to(device=self.device, dtype=self.dtype), values.to(device=self.device, dtype=self.dtype))
+        self._st.extend(keys.to(device=self.device, dtype=self._kdtype),
+                        values.to(device=self.device, dtype=self._kdtype))
 
     @torch.no_grad()
     def prefill(self, q: Tensor, k: Tensor, v: Tensor) -> Tensor:
@@ -485,18 +495,18 @@ class ArticleStreamingAttention:
         if self._st.length != 0:
             raise ValueError("prefill starts from an empty state; use step() / extend() afterwards")
         one = self._single
-        q3 = (q[None] if one else q).to(device=self.device, dtype=self.dtype).contiguous()
-        k3 = (k[None] if one else k).to(device=self.device, dtype=self.dtype).contiguous()
-        v3 = (v[None] if one else v).to(device=self.device, dtype=self.dtype).contiguous()
+        q3 = (q[None] if one else q).to(device=self.device, dtype=self._kdtype).contiguous()
+        k3 = (k[None] if one else k).to(device=self.device, dtype=self._kdtype).contiguous()
+        v3 = (v[None] if one else v).to(device=self.device, dtype=self._kdtype).contiguous()
         if (q3.ndim != 3 or q3.shape[0] != self.streams or q3.shape[-1] != self.dim or q3.shape != k3.shape
                 or tuple(v3.shape) != (self.streams, q3.shape[1], self.value_dim)):
             raise ValueError("q, k, v must be [P, dim] / [P, value_dim] ([S, P, ...] batched)")
         semantics = "exact" if self.compressor == "none" else "levels"
         res = _engine.prefill(q3, k3, v3, degree=self.degree, block=self.block_size, scale=self.scale,
                               semantics=semantics, compressor=self.compressor, seed=self.seed,
-                              eps=self.denominator_eps, out_dtype=self.dtype)
+                              eps=self.denominator_eps, out_dtype=self._kdtype)
         self._st.extend(k3, v3)
-        return res.out[0] if one else res.out
+        return (res.out[0] if one else res.out).to(self.dtype)
 
     def state_dict(self) -> dict:
         """The streams' state for a later resume (no counterpart in the reference): the decode state's

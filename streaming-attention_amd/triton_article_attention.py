@@ -197,15 +197,17 @@ def triton_article_causal_attention(
     if not (q3.dtype == k3.dtype == v3.dtype):
         q3, k3, v3 = q3.float(), k3.float(), v3.float()
     out_dtype = output_dtype or torch.float32
+    # an output type the kernels do not store (float64) is written as float32 and converted
+    k_out = out_dtype if out_dtype in _native.DTYPE_CODES else torch.float32
     res = _engine.prefill(q3, k3, v3, degree=degree, block=block_size, scale=_attention_scale(scale, dim),
                           semantics="segment", stride=compress_stride, exp_clamp=True, eps=denominator_eps,
-                          out_dtype=out_dtype)
-    out = _restore_shape(res.out, original_shape, had_bh)
+                          out_dtype=k_out)
+    out = _restore_shape(res.out, original_shape, had_bh).to(out_dtype)
     if not return_stats:
         return out
     r = max(0, (n - 1) // block_size) * (block_size // compress_stride)
     ekv = q3.element_size()
-    eo = res.out.element_size()
+    eo = torch.tensor([], dtype=out_dtype).element_size()
     stats = TritonArticleStats(degree, block_size, compress_stride, int(r), int(r * (dim + dv) * ekv),
                                int(n * (dim + dv) * ekv), int(n * n * ekv), int(n * dv * eo))
     return out, stats
@@ -238,8 +240,10 @@ def triton_flash_causal_attention(
         raise ValueError("this compact kernel supports Dv <= 256")
     if not (q3.dtype == k3.dtype == v3.dtype) or q3.dtype not in _native.DTYPE_CODES:
         q3, k3, v3 = q3.float(), k3.float(), v3.float()
-    out3 = _engine.flash(q3, k3, v3, scale=_attention_scale(scale, dim), out_dtype=output_dtype or torch.float32)
-    return _restore_shape(out3, original_shape, had_bh)
+    out_dtype = output_dtype or torch.float32
+    out3 = _engine.flash(q3, k3, v3, scale=_attention_scale(scale, dim),
+                         out_dtype=out_dtype if out_dtype in _native.DTYPE_CODES else torch.float32)
+    return _restore_shape(out3, original_shape, had_bh).to(out_dtype)
 
 
 # ----------------------------------------------------------------------------- demo / benchmark CLI

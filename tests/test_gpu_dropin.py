@@ -1,0 +1,146 @@
+"""Drop-in coverage beyond the headline shapes, on the GPU against the oracle: compress calls above 1024
+items (blocks of 2048 and 4096, flat and levels, prefill and decode), value widths above 256 (column
+groups), float64 inputs (computed as their float32 rounding, returned as float64), and the
+benchmark_attention.py CSV columns."""
+
+import csv
+
+import numpy as np
+import pytest
+import torch
+
+import _engine
+import benchmark_attention as bench_mod
+import fast_article_attention as faa
+import reference_cpu as orc
+import streaming_taylor_coreset_attention as stc
+import triton_article_attention as taa
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def rel(a, b):
+    return orc.rel_l2(torch.as_tensor(a).float().cpu(), torch.as_tensor(b).float().cpu())
+
+
+@pytest.mark.parametrize("block,n,semantics", [(2048, 2 * 2048 + 300, "flat"), (2048, 4 * 2048 + 77, "levels"),
+                                               (4096, 2 * 4096 + 5, "levels"), (1500, 3 * 1500 + 11, "levels")])
+def test_large_blocks_match_the_oracle(block, n, semantics):
+    """Compress calls on up to 4096 items: every node's kept tokens and weights bit-exact against the
+    oracle's compress calls, outputs within 1e-4."""
+    print(f"large block {block} n={n} {semantics}", flush=True)
+    q, k, v = orc.make_data((), n, 32, 32, radius=1.0, data="unit_ball", seed=3)
+    res = _engine.prefill(q[None].to(DEV), k[None].to(DEV), v[None].to(DEV), degree=2, block=block, scale=1.0,
+                          semantics=semantics, compressor="sorted_pair", seed=7)
+    torch.cuda.synchronize()
+    if semantics == "flat":
+        ref = orc.fast_path_forward(q, k, v, degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=7)
+        calls = orc.flat_coreset(k.numpy(), block, "sorted_pair", 7, orc.projection_scores)
+    else:
+        state = orc.LevelState()
+        ref = orc.levels_forward(q, k, v, degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=7,
+                                 state_out=state)
+        calls = state.calls
+    assert rel(res.out[0], ref) < 1e-4
+    src, w = res.node_src.cpu().numpy()[0], res.node_w.cpu().numpy()[0]
+    nodes = [node for node in range(res.plan.n_nodes) if int(res.plan.meta[node, 0]) > 0]
+    assert len(nodes) == len(calls)
+    for node in nodes:
+        size, slot = int(res.plan.meta[node, 0]), int(res.plan.desc[node, 6])
+        assert size == calls[slot].src_out.shape[0]
+        assert np.array_equal(src[node, :size], calls[slot].src_out), f"node {node}"
+        assert np.array_equal(w[node, :size], calls[slot].w_out), f"node {node}"
+
+
+def test_large_block_decode_matches_the_oracle():
+    """Streaming decode with block 2048 (compress calls on 2048 items): a 4200-token prefix through
+    extend(), then 60 steps, against the oracle's level semantics."""
+    s_, prefix, steps, block = 3, 4200, 60, 2048
+    n = prefix + steps
+    q, k, v = orc.make_data((s_,), n, 16, 24, radius=1.0, data="unit_ball", seed=4)
+    st = stc.ArticleStreamingAttention(16, 24, degree=2, block_size=block, scale=1.0, device=DEV, seed=0, streams=s_)
+    st.extend(k[:, :prefix].to(DEV), v[:, :prefix].to(DEV))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(prefix, n)], dim=1)
+    torch.cuda.synchronize()
+    for s in range(s_):
+        ref = orc.levels_forward(q[s], k[s], v[s], degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=s)
+        assert rel(outs[s], ref[prefix:]) < 1e-4
+
+
+@pytest.mark.parametrize("api", ["flat", "levels"])
+def test_value_width_above_256(api):
+    """dv = 300 runs as column groups of 256 + 44: equal to the oracle, and each group equal to a
+    separate call on its columns."""
+    q, k, v = orc.make_data((1, 2), 700, 16, 300, radius=1.0, data="unit_ball", seed=5)
+    fn = faa.fast_article_causal_attention if api == "flat" else stc.article_causal_attention
+    out = fn(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block_size=64, scale=1.0, compressor="sorted_pair", seed=2)
+    narrow = fn(q.to(DEV), k.to(DEV), v[..., 256:].contiguous().to(DEV), degree=2, block_size=64, scale=1.0,
+                compressor="sorted_pair", seed=2)
+    torch.cuda.synchronize()
+    assert out.shape == (1, 2, 700, 300)
+    assert torch.equal(out[..., 256:], narrow)
+    ref_fn = orc.fast_path_forward if api == "flat" else orc.levels_forward
+    for h in range(2):
+        ref = ref_fn(q[0, h], k[0, h], v[0, h], degree=2, block=64, scale=1.0, compressor="sorted_pair", seed=2 + h)
+        assert rel(out[0, h], ref) < 1e-4
+
+
+def test_float64_inputs_follow_their_float32_rounding():
+    """float64 q, k, v: the fast path, the level API, the streaming object and the Triton-semantics API
+    return float64 outputs equal to the float32 run on the rounded inputs (upcast), and within 1e-4
+    of the oracle on those inputs."""
+    q, k, v = orc.make_data((), 600, 16, 16, radius=1.0, data="unit_ball", seed=6)
+    q64, k64, v64 = q.double(), k.double(), v.double()
+    kw = dict(degree=2, block_size=64, scale=1.0, compressor="sorted_pair", seed=1)
+    for fn, ref_fn in ((faa.fast_article_causal_attention, orc.fast_path_forward),
+                       (stc.article_causal_attention, orc.levels_forward)):
+        out64 = fn(q64.to(DEV), k64.to(DEV), v64.to(DEV), **kw)
+        out32 = fn(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+        assert out64.dtype == torch.float64
+        assert torch.equal(out64, out32.double())
+        ref = ref_fn(q, k, v, degree=2, block=64, scale=1.0, compressor="sorted_pair", seed=1)
+        assert rel(out64, ref) < 1e-4
+    # host float64 tensors too (moved to the GPU and back)
+    assert torch.equal(faa.fast_article_causal_attention(q64, k64, v64, **kw),
+                       faa.fast_article_causal_attention(q, k, v, **kw).double())
+    # the streaming object with dtype float64
+    st64 = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV,
+                                         dtype=torch.float64, seed=1)
+    st32 = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV, seed=1)
+    for i in range(150):
+        a = st64.step(q64[i].to(DEV), k64[i].to(DEV), v64[i].to(DEV))
+        b = st32.step(q[i].to(DEV), k[i].to(DEV), v[i].to(DEV))
+        assert a.dtype == torch.float64 and torch.equal(a, b.double())
+    assert st64.state_size_bytes() == 2 * st32.state_size_bytes()
+    # the Triton-semantics API upcasts float64 like the reference, and writes float64 outputs
+    o = taa.triton_article_causal_attention(q64[None, None].to(DEV), k64[None, None].to(DEV),
+                                            v64[None, None].to(DEV), block_size=64, scale=1.0,
+                                            output_dtype=torch.float64)
+    o32 = taa.triton_article_causal_attention(q[None, None].to(DEV), k[None, None].to(DEV), v[None, None].to(DEV),
+                                              block_size=64, scale=1.0)
+    assert o.dtype == torch.float64 and torch.equal(o, o32.double())
+
+
+def test_benchmark_csv_has_the_reference_columns(tmp_path):
+    out = tmp_path / "bench.csv"
+    rows = bench_mod.main(["--sweep-n", "256", "600", "--d", "16", "--dv", "16", "--block-size", "64",
+                           "--repeats", "1", "--csv", str(out)])
+    with out.open() as fh:
+        got = list(csv.DictReader(fh))
+    assert list(got[0].keys()) == list(bench_mod.COLUMNS) and len(got) == 2
+    for r in rows:
+        assert r["rel_l2"] < 0.5 and r["article_median_ms"] > 0 and r["classical_median_ms"] > 0
+    # state columns: the per-token trace of the streaming object
+    st = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV)
+    q, k, v = faa._make_data(600, 16, 16, radius=1.0, data="unit_ball", device=DEV, dtype=torch.float32, seed=0)
+    sizes, items = [], []
+    for i in range(600):
+        st.update(k[i], v[i])
+        sizes.append(st.state_size_bytes())
+        items.append(st.coreset.num_items())
+    assert rows[1]["article_final_state_bytes"] == sizes[-1]
+    assert rows[1]["article_max_state_bytes"] == max(sizes)
+    assert rows[1]["article_max_coreset_items"] == max(items)

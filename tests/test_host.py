@@ -37,7 +37,7 @@ def test_library_exports_header_symbols():
         assert lib.sta_moment_chunk(d) == _plan.moment_chunk(d)
     assert lib.sta_status_string(0) == b"ok"
     lim = _native.limits()
-    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 4, "max_compress_in": 1024}
+    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 4, "max_compress_in": 4096}
 
 
 def test_library_rejects_bad_arguments_without_touching_a_device():
