@@ -118,6 +118,25 @@ int sta_moments_ws_ok(int d, int degree, int slot_tiles, int column_tiles, int d
 /* Bytes of sta_moments_ws' handoff scratch for bh heads, fsplit splits, slot_tiles, column_tiles, dv. */
 int64_t sta_moments_ws_handoff_bytes(int64_t bh, int fsplit, int slot_tiles, int column_tiles, int dv);
 
+/*
+ * sta_moments_ws with each head's sequence cut into nseg segments of seg_blocks query blocks (every
+ * segment non-empty), one workgroup per (head, segment, feature split, column group), for prefills
+ * with too few heads to fill the GPU.  Same outputs (the moment sums of fast_article_attention.py:217-259,
+ * at fp32 rounding: a segment's state starts from the earlier segments' total).  Three launches: the
+ * update side of every segment from a zero state, writing its total to seg_state; an exclusive scan
+ * over the segments; every segment's scan starting from the state before it.
+ *   seg_state: caller-allocated scratch of sta_moments_ws_seg_bytes(...) bytes, 16-byte aligned.
+ *   handoff: sta_moments_ws_handoff_bytes(bh * nseg, ...) bytes.
+ * nseg = 1 is sta_moments_ws (seg_blocks and seg_state unused).
+ */
+int sta_moments_ws_seg(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                       int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles,
+                       int mixed, int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
+                       float* low_num, float* low_den, int nseg, int seg_blocks, float* seg_state, void* stream);
+
+/* Bytes of sta_moments_ws_seg's segment-state scratch. */
+int64_t sta_moments_ws_seg_bytes(int64_t bh, int fsplit, int slot_tiles, int column_tiles, int dv, int nseg);
+
 /* 1 when sta_moments runs (d, degree, dv, wave_tiles, products) with columns = 64: one workgroup per
  * (head, feature split) covering all value columns (split-bf16 products, 32 < dv <= 64, mixed = 0;
  * one workgroup per compute unit). */

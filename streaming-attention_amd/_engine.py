@@ -53,6 +53,9 @@ def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
 #   4 x 32 heads x 16384, fp32, degree 3, block 128:    6.13 -> 4.28 ms / 7.88 -> 6.18 ms
 # STA_MOMENT_WS=never / always overrides the choice (a prefill's moment_kernel argument too).
 MOMENT_WS_POLICY = os.environ.get("STA_MOMENT_WS", "auto")  # "auto" | "always" | "never"
+# Sequence segments of the wave-specialised scan when the heads alone leave compute units idle
+# (STA_WS_SEGMENTS=0: never).
+WS_SEGMENTS = os.environ.get("STA_WS_SEGMENTS", "1") != "0"
 
 
 def use_moments_ws(element_size: int, degree: int) -> bool:
@@ -225,33 +228,6 @@ def prefill(
     stream = _native.stream_handle(dev)
     chunk = _plan.moment_chunk(d)
 
-    # the moment kernel reads rows in 16-byte units: q/k padded with zero dimensions to a whole unit
-    # (zero dimensions only add zero-valued features), v to whole 32-column groups
-    dm = _unit_width(d, q3.element_size())
-    ft = _plan.feature_tiles(dm, degree)
-    k1_products = MOMENT_PRODUCTS if products is None else int(products)
-    qblock = ws_query_block(semantics, block) if (k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 3 and
-                                                  (use_moments_ws(q3.element_size(), degree) if moment_kernel is None
-                                                   else moment_kernel == "ws")) else None
-    ws_ct = 4 if (-(-dv // 32)) % 2 == 0 else 2
-    ws_opts = _native.moment_ws_slot_tiles(dm, degree, ws_ct, dv) if qblock else ()
-    if ws_opts:
-        ms = _plan.moment_split_ws(ft, bh, dv, ws_opts, ws_ct)
-        chunk = qblock
-    else:
-        qblock = None
-        ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
-                                mixed_nts=_native.moment_mixed_tiles(dm, degree),
-                                wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
-    fsplit = ms.fsplit
-    # split products at degree <= 2 apply one coefficient per tile on the query side
-    tile_coef = k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 2
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef, ms.columns,
-                              qblock is not None), dev,
-                             lambda: (_i32(ms.quads, dev),
-                                      _f32(_plan.tile_coefficients(ms.quads, ms.coef, dm) if tile_coef else ms.coef,
-                                           dev)))
-
     raw = semantics == "taylor"
     if semantics in ("exact", "taylor"):
         plan = _plan.exact_plan(n)
@@ -266,6 +242,36 @@ def prefill(
     if plan.call_sizes and max(plan.call_sizes) > lim["max_compress_in"]:
         raise ValueError(f"block_size {block} needs compress calls on {max(plan.call_sizes)} items; "
                          f"the HIP compressor handles at most {lim['max_compress_in']}")
+
+    # the moment kernel reads rows in 16-byte units: q/k padded with zero dimensions to a whole unit
+    # (zero dimensions only add zero-valued features), v to whole 32-column groups
+    dm = _unit_width(d, q3.element_size())
+    ft = _plan.feature_tiles(dm, degree)
+    k1_products = MOMENT_PRODUCTS if products is None else int(products)
+    qblock = ws_query_block(semantics, block) if (k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 3 and
+                                                  (use_moments_ws(q3.element_size(), degree) if moment_kernel is None
+                                                   else moment_kernel == "ws")) else None
+    ws_ct = 4 if (-(-dv // 32)) % 2 == 0 else 2
+    ws_opts = _native.moment_ws_slot_tiles(dm, degree, ws_ct, dv) if qblock else ()
+    nseg, seg_blocks = 1, 0
+    if ws_opts:
+        # few heads: cut each head's scan into segments of whole query blocks (sta_moments_ws_seg)
+        nseg, seg_blocks = _plan.ws_segments(n, shift, qblock, bh, ft, dv, ws_opts, ws_ct) if WS_SEGMENTS else (1, 0)
+        ms = _plan.moment_split_ws(ft, bh * nseg, dv, ws_opts, ws_ct)
+        chunk = qblock
+    else:
+        qblock = None
+        ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
+                                mixed_nts=_native.moment_mixed_tiles(dm, degree),
+                                wide_nts=_native.moment_wide_tiles(dm, degree, dv, k1_products) if MOMENT_WIDE else ())
+    fsplit = ms.fsplit
+    # split products at degree <= 2 apply one coefficient per tile on the query side
+    tile_coef = k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 2
+    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef, ms.columns,
+                              qblock is not None), dev,
+                             lambda: (_i32(ms.quads, dev),
+                                      _f32(_plan.tile_coefficients(ms.quads, ms.coef, dm) if tile_coef else ms.coef,
+                                           dev)))
 
     # ---- host side first: every validation error is raised before anything is launched ----
     pkey = (plan.mode, plan.n, plan.block, compressor if semantics != "segment" else stride)
@@ -299,15 +305,18 @@ def prefill(
     mq, mk, mv = _padded_rows(q3, dm), _padded_rows(k3, dm), _padded_rows(v3, -(-dv // 32) * 32)
 
     if qblock is not None:
-        hbytes = lib.sta_moments_ws_handoff_bytes(bh, fsplit, ms.wave_tiles, ws_ct, dv)
+        hbytes = lib.sta_moments_ws_handoff_bytes(bh * nseg, fsplit, ms.wave_tiles, ws_ct, dv)
         handoff = torch.empty((max(hbytes, 16) // 4,), device=dev, dtype=torch.float32)
+        seg_state = (torch.empty((lib.sta_moments_ws_seg_bytes(bh, fsplit, ms.wave_tiles, ws_ct, dv, nseg) // 4,),
+                                 device=dev, dtype=torch.float32) if nseg > 1 else None)
 
         def k1():
-            st = lib.sta_moments_ws(
+            st = lib.sta_moments_ws_seg(
                 mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
                 float(scale), qblock, shift, fsplit, ms.wave_tiles, int(ms.mixed), ws_ct,
-                fidx.data_ptr(), fcoef.data_ptr(), handoff.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
-            _native.check(st, "sta_moments_ws")
+                fidx.data_ptr(), fcoef.data_ptr(), handoff.data_ptr(), low_num.data_ptr(), low_den.data_ptr(),
+                nseg, seg_blocks, _native.ptr(seg_state), stream)
+            _native.check(st, "sta_moments_ws_seg")
     else:
         def k1():
             st = lib.sta_moments(

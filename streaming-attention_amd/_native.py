@@ -51,6 +51,12 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
          _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],
     ),
+    "sta_moments_ws_seg": (
+        _i32,
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
+         _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p],
+    ),
+    "sta_moments_ws_seg_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32]),
     "sta_moments_ws_ok": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "sta_moments_ws_handoff_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32]),
     "sta_moment_columns_ok": (_i32, [_i32, _i32, _i32, _i32, _i32]),

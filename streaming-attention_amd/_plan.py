@@ -373,6 +373,23 @@ def moment_split_ws(ft: FeatureTiles, bh: int, dv: int, slot_options: Tuple[int,
                     allow_mixed), build)
 
 
+def ws_segments(n: int, shift: int, query_block: int, bh: int, ft: FeatureTiles, dv: int,
+                slot_options: Tuple[int, ...], column_tiles: int, compute_units: int = 256,
+                min_blocks: int = 2) -> Tuple[int, int]:
+    """(nseg, seg_blocks) for sta_moments_ws_seg: when the workgroups of the whole-sequence scan at the
+    split a busy GPU would use (bh x fsplit x csplit) leave compute units idle, each head's scan is cut
+    into nseg segments of seg_blocks query blocks (at least min_blocks), every segment non-empty;
+    (1, 0) otherwise."""
+    full = moment_split_ws(ft, max(bh, compute_units), dv, slot_options, column_tiles)
+    grid = bh * full.fsplit * full.csplit
+    blocks = -(-(n + shift) // query_block)
+    want = min(compute_units // max(grid, 1), blocks // min_blocks)
+    if grid >= compute_units or want <= 1:
+        return 1, 0
+    seg_blocks = -(-blocks // want)
+    return -(-blocks // seg_blocks), seg_blocks
+
+
 def tile_coefficients(quads: np.ndarray, coef: np.ndarray, d: int) -> np.ndarray:
     """The coefficient table of the split-product moment scan at degree <= 2 (moments.hip,
     mom_query_split): every tile's 16 entries set to one value c_t with

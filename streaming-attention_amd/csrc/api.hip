@@ -3,6 +3,7 @@
 // units (launch_moments.hip, launch_accumulate.hip, launch_block.hip); this unit includes their sources
 // for the argument structs only.  The library allocates nothing; every buffer is the caller's, except
 // the fixed static scratch of sta_decode_step_static (below).
+#include <algorithm>
 #include <mutex>
 
 #include "api_common.hpp"
@@ -98,6 +99,24 @@ int dispatch_flash_dvt(const sta::FlashArgs& a, int64_t bh, hipStream_t s) {
   if (a.dv <= 128) return launch_flash<DP, 8, ES>(a, bh, s);
   if (a.dv <= 256) return launch_flash<DP, 16, ES>(a, bh, s);
   return STA_ERR_UNSUPPORTED;
+}
+
+// Exclusive scan over the segments of each (head, feature split, column group): seg_state[p] <- sum of
+// the totals of segments 0 .. p - 1, in segment order (deterministic).  One thread per float of a unit.
+__global__ __launch_bounds__(256) void ws_seg_scan_kernel(float* seg_state, int64_t groups, int nseg, int unit) {
+  const int64_t total = groups * unit;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t g = e / unit;
+    const int64_t off = e - g * unit;
+    float* base = seg_state + g * nseg * static_cast<int64_t>(unit) + off;
+    float acc = 0.f;
+    for (int p = 0; p < nseg; ++p) {
+      const float t = base[static_cast<int64_t>(p) * unit];
+      base[static_cast<int64_t>(p) * unit] = acc;
+      acc += t;
+    }
+  }
 }
 
 }  // namespace
@@ -240,10 +259,17 @@ int64_t sta_moments_ws_handoff_bytes(int64_t bh, int fsplit, int slot_tiles, int
   return bh * fsplit * csplit * 2 * 4 * pairs * column_tiles * 2 * 64 * 16;
 }
 
-int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                   int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles, int mixed,
-                   int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
-                   float* low_num, float* low_den, void* stream) {
+int64_t sta_moments_ws_seg_bytes(int64_t bh, int fsplit, int slot_tiles, int column_tiles, int dv, int nseg) {
+  if (bh <= 0 || fsplit <= 0 || slot_tiles <= 0 || (column_tiles != 2 && column_tiles != 4) || dv <= 0 || nseg <= 0)
+    return -1;
+  const int64_t csplit = (dv + 16 * column_tiles - 1) / (16 * column_tiles);
+  return bh * fsplit * csplit * nseg * sta::ws_seg_floats(slot_tiles, column_tiles) * int64_t(sizeof(float));
+}
+
+int sta_moments_ws_seg(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                       int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles,
+                       int mixed, int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
+                       float* low_num, float* low_den, int nseg, int seg_blocks, float* seg_state, void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !handoff || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || slot_tiles <= 0) return STA_ERR_SHAPE;
@@ -258,6 +284,13 @@ int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64
     return STA_ERR_ARG;
   if (n * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
     return STA_ERR_UNSUPPORTED;
+  // segments of seg_blocks query blocks, every one non-empty
+  const int cpb = query_block / sta::MOM_C;
+  const int64_t nch = (n + shift + sta::MOM_C - 1) / sta::MOM_C;
+  if (nseg <= 0 || (nseg > 1 && (seg_blocks <= 0 || !seg_state))) return STA_ERR_ARG;
+  const int64_t seg_chunks = nseg > 1 ? static_cast<int64_t>(seg_blocks) * cpb : nch;
+  if (nseg > 1 && ((nseg - 1) * seg_chunks >= nch || nseg * seg_chunks < nch)) return STA_ERR_SHAPE;
+  if (nseg > 1 && (reinterpret_cast<uintptr_t>(seg_state) & 15u) != 0) return STA_ERR_ARG;
   sta::WsArgs w;
   sta::MomArgs& a = w.m;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
@@ -265,14 +298,42 @@ int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64
   a.quads = feat_quads; a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
   a.ldo = 32 * ((dv + 31) / 32);
   a.head_rows = n; a.rowmap = nullptr; a.state_num = nullptr; a.state_den = nullptr; a.n_feat = 0;
-  w.cpb = query_block / sta::MOM_C;
+  w.cpb = cpb;
   w.mixed = mixed;
   w.hand = static_cast<uint4*>(handoff);
+  w.nseg = nseg;
+  w.seg_chunks = static_cast<int>(seg_chunks);
+  w.phase = nseg > 1 ? 1 : 0;
+  w.seg_state = nseg > 1 ? seg_state : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nx = moment_extra_factors(degree);
-  if (column_tiles == 4)
-    return esize == 4 ? dispatch_moments_ws<4, 4>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 4>(w, bh, s, slot_tiles, nx);
-  return esize == 4 ? dispatch_moments_ws<4, 2>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 2>(w, bh, s, slot_tiles, nx);
+  auto run = [&]() {
+    if (column_tiles == 4)
+      return esize == 4 ? dispatch_moments_ws<4, 4>(w, bh, s, slot_tiles, nx)
+                        : dispatch_moments_ws<2, 4>(w, bh, s, slot_tiles, nx);
+    return esize == 4 ? dispatch_moments_ws<4, 2>(w, bh, s, slot_tiles, nx)
+                      : dispatch_moments_ws<2, 2>(w, bh, s, slot_tiles, nx);
+  };
+  int st = run();
+  if (st != STA_OK || nseg == 1) return st;
+  // segment totals -> the state before each segment, then every segment's scan from it
+  const int unit = sta::ws_seg_floats(slot_tiles, column_tiles);
+  const int64_t groups = bh * a.fsplit * a.csplit;
+  const int64_t blocks = std::min<int64_t>((groups * unit + 255) / 256, 4096);
+  hipLaunchKernelGGL(ws_seg_scan_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, seg_state, groups,
+                     nseg, unit);
+  if ((st = check_launch()) != STA_OK) return st;
+  w.phase = 2;
+  return run();
+}
+
+int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
+                   int ldv, int degree, float scale, int query_block, int shift, int fsplit, int slot_tiles, int mixed,
+                   int column_tiles, const uint32_t* feat_quads, const float* feat_coef, void* handoff,
+                   float* low_num, float* low_den, void* stream) {
+  return sta_moments_ws_seg(q, k, v, dtype, bh, n, d, dv, ldv, degree, scale, query_block, shift, fsplit, slot_tiles,
+                            mixed, column_tiles, feat_quads, feat_coef, handoff, low_num, low_den, 1, 0, nullptr,
+                            stream);
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,

@@ -14,11 +14,13 @@ namespace {
 template <int NTS, int NX, bool DBIG, int ES, int CT>
 int launch_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::ws_smem_floats(DBIG, 16 * CT, NTS)) * sizeof(float);
-  auto fn = sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT>;
+  // phase 1 of a segmented scan (segment totals) is its own instantiation: no query work at all
+  auto fn = a.phase == 1 ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true>
+                         : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, false>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
-  const int64_t grid = bh * a.m.fsplit * a.m.csplit;
+  const int64_t grid = bh * a.m.fsplit * a.m.csplit * a.nseg;
   if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::WS_THREADS), smem, s, a);
   return check_launch();

@@ -26,6 +26,14 @@
 // denominators) to a per-workgroup handoff buffer in global memory, double-buffered by block parity;
 // the query waves load it in the next iteration, right after their last use of the old copy.  The
 // handoff stays within the workgroup (stores, barrier, loads on one compute unit).
+//
+// Sequence segments (few heads).  With nseg > 1 each (head, feature split, column group) is cut into
+// nseg segments of seg_chunks chunks (whole query blocks), one workgroup each, in two passes.  Phase
+// 1: the update waves sum their segment's keys from a zero state (no queries, no outputs) and write
+// the total to seg_state; an exclusive scan over the segments (ws_seg_scan_kernel, api.hip) turns the
+// totals into S_init(p), the state before segment p.  Phase 2: the ordinary scan of each segment,
+// starting from S_init(p) (the update waves' accumulators and the query waves' operands and
+// denominators are loaded from it) instead of zero.
 #pragma once
 #include "moments.hip"
 
@@ -41,7 +49,15 @@ struct WsArgs {
   int cpb;          // chunks per query block (>= 2)
   int mixed;        // slots 2 and 3 hold NTS - 1 tiles
   uint4* hand;      // [grid][2][4][NPS][CT][2][64]: split state as query operands (see ws_body)
+  int nseg;         // sequence segments per (head, feature split, column group); 1: the whole sequence
+  int seg_chunks;   // chunks per segment (a multiple of cpb)
+  int phase;        // 0: whole sequence; 1: segment totals (update only); 2: segment scans from S_init
+  float* seg_state; // [bh][fsplit][csplit][nseg][ws_seg_floats]: segment totals, then S_init (nseg > 1)
 };
+
+// Per (head, feature split, column group, segment): the 4 update waves' accumulators [4][NTS][CT][64
+// lanes] floatx4, then the denominators [4][NTS][16].
+__host__ __device__ constexpr int ws_seg_floats(int nts, int ct) { return nts * (1024 * ct + 64); }
 
 __host__ __device__ constexpr int ws_kv_floats(bool dbig, int cg) { return mom_krows(dbig) * MOM_LDT + cg * MOM_C; }
 __host__ __device__ constexpr int ws_q_floats(bool dbig) { return MOM_C * mom_ldq(dbig); }
@@ -361,6 +377,26 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
   }
 }
 
+// Staging of iteration c by one thread (keys / values of chunk c + 1, queries of chunk c into LDS from the
+// register set, loads of slot c + 3 into it): the main loop's staging step, for the query waves of a
+// segment-totals pass, which only stage.
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG>& pre, const WsSlots<DBIG, ES, CG>& sl,
+                                              const MomArgs& a, float* kvb, float* qb, int c, int nch, int first,
+                                              const char* kh, const char* vh, const char* qh) {
+  constexpr int KVF = ws_kv_floats(DBIG, CG);
+  constexpr int QF = ws_q_floats(DBIG);
+  const int kv_row = first + (c + 1) * MOM_C;
+  const int q_row = first + c * MOM_C;
+  if (c + 1 < nch) {
+    float* Kt = kvb + ((c + 1) & 1) * KVF;
+    ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
+  }
+  if (c < nch) ws_store_q<DBIG, ES, CG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
+  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + 2 * MOM_C);
+  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + 2 * MOM_C);
+}
+
 // The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
 // out of the NTS the table holds per slot.  Every instantiation runs the same iterations and barriers.
 //
@@ -369,8 +405,9 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 // the lane holds for tile 2 p (.xy) and tile 2 p + 1 (.zw); an odd last tile fills .xy only.  The
 // update wave writes its uint2 halves, the query wave loads whole operands.  The running denominators
 // go to LDS (den_lds[parity][slot][tile * 16 + feature]).
-template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT>
-__device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, int fs, int cs, int slot, int qw) {
+template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT, bool TOT>
+__device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, int fs, int cs, int seg, int slot,
+                                        int qw) {
   const MomArgs& a = wa.m;
   constexpr int CG = 16 * CT;
   constexpr int LDQ = mom_ldq(DBIG);
@@ -392,9 +429,20 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   const int col0 = CG * cs;
   const bool den = cs == 0;
   const int n = static_cast<int>(a.n);
-  const int nch = (n + a.shift + MOM_C - 1) / MOM_C;
-  const int first = -a.shift;
+  const int nch_all = (n + a.shift + MOM_C - 1) / MOM_C;
+  // this workgroup's chunks: [seg * seg_chunks, ...) of the sequence (the whole of it when nseg = 1)
+  const int c_begin = wa.nseg > 1 ? seg * wa.seg_chunks : 0;
+  const int nch = wa.nseg > 1 ? min(wa.seg_chunks, nch_all - c_begin) : nch_all;
+  const int first = -a.shift + c_begin * MOM_C;
   const int cpb = wa.cpb;
+  constexpr bool totals = TOT;            // phase 1: update only, write the segment's total
+  const bool from_init = wa.phase == 2;   // start from the state before the segment
+  // segment state of this (head, feature split, column group, segment): [4][NTS][CT][64] floatx4, den
+  float* const sstate = wa.nseg > 1
+                            ? wa.seg_state + ((((bh * a.fsplit + fs) * a.csplit + cs) * wa.nseg + seg) *
+                                              static_cast<int64_t>(ws_seg_floats(NTS, CT)))
+                            : nullptr;
+  float* const sden = sstate ? sstate + 4 * NTS * CT * 256 : nullptr;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
   const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
   const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
@@ -433,6 +481,51 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   for (int e = tid; e < 2 * (KVF + QF); e += WS_THREADS) smem[e] = 0.f;
   for (int e = tid; e < ws_den_floats(NTS); e += WS_THREADS) denb[e] = 0.f;
   __syncthreads();
+  if constexpr (UPD) {
+    if (from_init) {
+      // phase 2: the accumulators start at S_init; its denominators ride in lane group 0's partials
+      const floatx4* ss = reinterpret_cast<const floatx4*>(sstate) + (slot * NTS) * CT * 64 + lane;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) st[kt][ct] = ss[(kt * CT + ct) * 64];
+        den_p[kt] = lg == 0 ? sden[(slot * NTS + kt) * 16 + li] : 0.f;
+      }
+    }
+  } else {
+    if (from_init) {
+      // phase 2: the rows of the segment's first block see S_init: split it into this wave's operands
+      // and its denominators into block parity 0
+      const floatx4* ss = reinterpret_cast<const floatx4*>(sstate) + (slot * NTS) * CT * 64 + lane;
+      auto tile = [&](int kt, int ct) { return ss[(kt * CT + ct) * 64]; };
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const floatx4 s0 = tile(2 * p, ct), s1 = tile(2 * p + 1, ct);
+          uint4 h, l;
+          split_pair(s0[0], s0[1], h.x, l.x);
+          split_pair(s0[2], s0[3], h.y, l.y);
+          split_pair(s1[0], s1[1], h.z, l.z);
+          split_pair(s1[2], s1[3], h.w, l.w);
+          sh[p][ct] = __builtin_bit_cast(bf16x8, h);
+          sv[p][ct] = __builtin_bit_cast(bf16x8, l);
+        }
+      }
+      if constexpr (ODD) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const floatx4 s0 = tile(NT - 1, ct);
+          split_pair(s0[0], s0[1], oh[ct].x, ov[ct].x);
+          split_pair(s0[2], s0[3], oh[ct].y, ov[ct].y);
+        }
+      }
+      if (den && lg == 0) {
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) denb[slot * NTS * 16 + kt * 16 + li] = sden[(slot * NTS + kt) * 16 + li];
+      }
+    }
+  }
   // two register sets of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is held
   // in set x & 1 from its load (iteration x - 3) to its store into LDS (iteration x - 1), so a load has
   // two iterations to land
@@ -445,12 +538,25 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first + 2 * MOM_C);  // slot 2
   ws_load_q<DBIG, ES, CG, true>(pre0, sl, a, qh, first + MOM_C);
 
+  if constexpr (!UPD && TOT) {
+    {
+      // segment totals: the query waves only stage, with the same iterations and barriers
+      for (int c = 0; c <= nch; ++c) {
+        if (c & 1)
+          ws_stage_step<DBIG, ES, CG>(pre0, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+        else
+          ws_stage_step<DBIG, ES, CG>(pre1, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+        __syncthreads();
+      }
+      return;
+    }
+  }
   for (int c = 0; c <= nch; ++c) {
     if constexpr (UPD) {
       if (c < nch) {
         const float* Kt = kvb + (c & 1) * KVF;
         ws_update<NT, CT, NX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li, lg);
-        if ((c + 1) % cpb == 0 && c + 1 < nch) {
+        if (!totals && (c + 1) % cpb == 0 && c + 1 < nch) {
           // the state the queries of block (c + 1) / cpb see -> handoff (parity of that block)
           const int par = ((c + 1) / cpb) & 1;
 #pragma unroll
@@ -582,24 +688,43 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       else
         stage(pre1);
       if constexpr (UPD) {
-        if (c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
+        if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
       }
     }
     __syncthreads();
     }
   // partials of the last chunk (written by the query waves in iteration nch)
-  if constexpr (UPD) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
+  if constexpr (UPD) {
+    if (!totals) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
+    if (totals) {
+      // phase 1: the segment's total (its keys only) for the scan over segments
+      floatx4* ss = reinterpret_cast<floatx4*>(sstate) + (slot * NTS) * CT * 64 + lane;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) ss[(kt * CT + ct) * 64] = st[kt][ct];
+        float t = den_p[kt];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        if (lg == 0) sden[(slot * NTS + kt) * 16 + li] = t;
+      }
+    }
+  }
 }
 
 // Workgroup -> (head, feature split, column group): consecutive logical ids share an XCD, so a head's
 // workgroups share one L2 for its q / k / v rows.  Waves 0-3 update, 4-7 query.
-template <int NTS, int NX, bool DBIG, int ES, int CT>
+template <int NTS, int NX, bool DBIG, int ES, int CT, bool TOT>
 __global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs wa) {
   const MomArgs& a = wa.m;
   const int wg = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_head = a.fsplit * a.csplit;
+  // logical order (head, segment, feature split, column group): a segment's splits share an XCD
+  const int per_seg = a.fsplit * a.csplit;
+  const int per_head = per_seg * wa.nseg;
   const int64_t bh = wg / per_head;
-  const int rem = wg - static_cast<int>(bh) * per_head;
+  const int rem0 = wg - static_cast<int>(bh) * per_head;
+  const int seg = rem0 / per_seg;
+  const int rem = rem0 - seg * per_seg;
   const int fs = rem / a.csplit;
   const int cs = rem - fs * a.csplit;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -607,15 +732,15 @@ __global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs 
   if (w < 4) {
     const int slot = w;
     if (NTS > 1 && wa.mixed && slot >= 2)
-      ws_body<true, NTL, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, 0);
+      ws_body<true, NTL, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, 0);
     else
-      ws_body<true, NTS, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, 0);
+      ws_body<true, NTS, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, 0);
   } else {
     const int slot = (w - 4 + 2) & 3;
     if (NTS > 1 && wa.mixed && slot >= 2)
-      ws_body<false, NTL, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, w - 4);
+      ws_body<false, NTL, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, w - 4);
     else
-      ws_body<false, NTS, NTS, NX, DBIG, ES, CT>(wa, wg, bh, fs, cs, slot, w - 4);
+      ws_body<false, NTS, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, w - 4);
   }
 }
 
