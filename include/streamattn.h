@@ -167,11 +167,13 @@ int sta_moment_occupancy(int d, int wave_tiles);
  *   (degree 0, 1, ..., each in combinations_with_replacement order), -1 for padding slots.
  *   state_num [BH][n_feat][ld] with ld = 32*ceil(dv/32), state_den [BH][n_feat], fp32, accumulated in
  *   place.  k / v row rules as for sta_moments (16-byte units, ldv a multiple of 32).
+ *   products: STA_PRODUCTS_FP32 or STA_PRODUCTS_SPLIT_BF16 (as for sta_moments; the state and the
+ *   sums stay fp32 either way).
  */
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
                           int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
-                          const float* feat_coef, const int32_t* feat_rows, int n_feat, float* state_num,
-                          float* state_den, void* stream);
+                          const float* feat_coef, const int32_t* feat_rows, int n_feat, int products,
+                          float* state_num, float* state_den, void* stream);
 
 /*
  * Streaming decode (K5) for S streams in lockstep: ArticleStreamingAttention.update / query

@@ -42,6 +42,9 @@ class _CompletionDraws:
     perms: torch.Tensor  # int32 [S, n_calls, max_in]
 
 
+ACCUMULATE_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+
+
 class DecodeState:
     def __init__(self, streams: int, dim: int, value_dim: int, *, degree: int, block: int, scale: float,
                  compressor: str, seed: int, device: torch.device, eps: float = 1e-12) -> None:
@@ -65,6 +68,9 @@ class DecodeState:
         self.compressor, self.seed, self.eps = str(compressor), int(seed), float(eps)
         self.device = device
         self.exact = self.compressor == "none"
+        # matrix-core products of the state accumulation (block completions, extend): split-bf16 as in the
+        # prefill moment scan (the state and every sum stay fp32)
+        self.products = ACCUMULATE_PRODUCTS
         self.m = (self.block + 1) // 2
         if not self.exact and max(self.block, 2 * self.m) > lim["max_compress_in"]:
             raise ValueError(f"block_size {block} exceeds the HIP compressor's {lim['max_compress_in']} items")
@@ -141,7 +147,7 @@ class DecodeState:
             st = self.lib.sta_moment_accumulate(
                 kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, width, self.dv,
                 v.shape[-1], self.degree, ms.fsplit, ms.wave_tiles, quads.data_ptr(), coef.data_ptr(), rows.data_ptr(),
-                self.F, state_num.data_ptr(), state_den.data_ptr(), self._stream())
+                self.F, self.products, state_num.data_ptr(), state_den.data_ptr(), self._stream())
             _native.check(st, "sta_moment_accumulate")
 
         self._launch("moment_accumulate", run)

@@ -86,7 +86,7 @@ _SIGNATURES = {
     "sta_moment_accumulate": (
         _i32,
         [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dtype bh n rows d dv ldv deg fs nt
-         _c_p, _c_p, _c_p, _i32, _c_p, _c_p, _c_p],  # quads coef rows n_feat state_num state_den stream
+         _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],  # quads coef rows n_feat products num den stream
     ),
     "sta_decode_layout": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "sta_decode_moments": (

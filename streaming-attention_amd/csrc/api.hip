@@ -338,14 +338,15 @@ int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
                           int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
-                          const float* feat_coef, const int32_t* feat_rows, int n_feat, float* state_num,
-                          float* state_den, void* stream) {
+                          const float* feat_coef, const int32_t* feat_rows, int n_feat, int products,
+                          float* state_num, float* state_den, void* stream) {
   if (!k || !v || !feat_quads || !feat_coef || !feat_rows || !state_num || !state_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n < 0 || head_rows < n || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0 || n_feat <= 0)
     return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
+  if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
   if (n == 0) return STA_OK;
   const int esize = dtype == STA_F32 ? 4 : 2;
   if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0) return STA_ERR_ARG;
@@ -357,7 +358,8 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
   a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
   a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
-  return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, moment_extra_factors(degree));
+  return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, moment_extra_factors(degree),
+                             products == STA_PRODUCTS_SPLIT_BF16);
 }
 
 int sta_decode_layout(int d, int dv, int* dk, int* ldv) {

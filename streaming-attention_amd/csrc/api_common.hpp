@@ -98,7 +98,7 @@ int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, i
 template <int ES, int CT>
 int dispatch_moments_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s, int nts, int nx);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
-int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx);
+int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, bool split);
 // launch_block.hip, one object per (DP, DVT, ES): the residual / combine kernel (block_attn_kernel) for
 // padded key width DP, value-column tile count DVT and element size ES.
 template <int DP, int DVT, int ES>

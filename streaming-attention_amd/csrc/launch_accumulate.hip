@@ -6,10 +6,10 @@
 namespace sta_api {
 namespace {
 
-template <int NT, int NX, bool DBIG, int ES>
+template <int NT, int NX, bool DBIG, int ES, bool SPLIT>
 int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::mom_acc_smem_floats(DBIG, NT)) * sizeof(float);
-  auto fn = sta::moment_accumulate_kernel<NT, NX, DBIG, ES>;
+  auto fn = sta::moment_accumulate_kernel<NT, NX, DBIG, ES, SPLIT>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);
@@ -21,11 +21,13 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
 
 }  // namespace
 
-int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx) {
+int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, bool split) {
   const bool big = a.d > 64;
 #define STA_CASE(NT, D3, BIG)                                                                       \
-  if (nt == NT && nx == D3 && big == BIG)                                                         \
-    return a.esize == 4 ? launch<NT, D3, BIG, 4>(a, bh, s) : launch<NT, D3, BIG, 2>(a, bh, s);
+  if (nt == NT && nx == D3 && big == BIG) {                                                       \
+    if (split) return a.esize == 4 ? launch<NT, D3, BIG, 4, true>(a, bh, s) : launch<NT, D3, BIG, 2, true>(a, bh, s); \
+    return a.esize == 4 ? launch<NT, D3, BIG, 4, false>(a, bh, s) : launch<NT, D3, BIG, 2, false>(a, bh, s); \
+  }
   STA_MOMENT_CONFIGS(STA_CASE)
 #undef STA_CASE
   return STA_ERR_UNSUPPORTED;

@@ -437,7 +437,9 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 // planner makes every degree <= 2 tile uniform (tile_coefficients in _plan.py): the diagonal tiles
 // x[4k + r] x[4k + s] take 1/2 on all 16 slots (the slot pairs (r, s), (s, r) add up to the
 // off-diagonal monomial), padding slots are zero-valued monomials.
-template <int NT, int CT, int NX, bool DEN, class Mid>
+// KCOEF: apply the key-side coefficient at every degree (the decode state keeps the reference's
+// coefficient-weighted moments; the prefill scan applies degree <= 2 coefficients on the query side).
+template <int NT, int CT, int NX, bool DEN, class Mid, bool KCOEF = false>
 __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* den_s, const float* Kt,
                                                  const float* Vt, const MomLane<NT, NX>& m, int li, int lg,
                                                  Mid mid) {
@@ -472,7 +474,7 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
       float y = fa[j >> 2][kt][j & 3] * fb[j >> 2][kt][j & 3];
       if (NX >= 1) y *= fc[j >> 2][NX >= 1 ? kt : 0][j & 3];
       if (NX >= 2) y *= fe[j >> 2][NX >= 2 ? kt : 0][j & 3];
-      if (NX >= 1) y *= m.kcoef[kt];  // NX = 0: the tile's coefficient is applied by the query
+      if (NX >= 1 || KCOEF) y *= m.kcoef[kt];  // NX = 0: the tile's coefficient is applied by the query
       x[j] = y;
       if constexpr (DEN) dacc += y;
     }
@@ -808,7 +810,9 @@ __host__ __device__ constexpr int mom_acc_smem_floats(bool dbig, int nt) {
 // the accumulators at the start and written back at the end (each (head, feature, column) belongs to
 // exactly one wave of the grid, so the read-modify-write has no race).  Rows [0, n) of every head are
 // read at k + bh * head_rows * d (v: ldv).
-template <int NT, int NX, bool DBIG, int ES>
+// SPLIT: split-bf16 matrix-core products (the staged values as bf16 hi / lo planes, mom_update_split with
+// key-side coefficients) instead of fp32 ones.
+template <int NT, int NX, bool DBIG, int ES, bool SPLIT>
 __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const MomArgs a) {
   constexpr int BUF = mom_buf_floats(DBIG);
   constexpr int CT = 2;
@@ -860,11 +864,15 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
     MomStage<DBIG, 32> stg;
     mom_load<DBIG, ES, 32>(stg, sl, a, kh, kh, vh, c * MOM_C);  // the query slots are staged but not used
     __syncthreads();  // the previous chunk's update is done with the buffer
-    mom_store<DBIG, ES, 32>(stg, sl, a, smem, dummy_abs, c * MOM_C);
+    mom_store<DBIG, ES, 32, SPLIT>(stg, sl, a, smem, dummy_abs, c * MOM_C);
     __syncthreads();
     const float* Kt = smem + MOM_C * mom_ldq(DBIG);
     const float* Vt = Kt + mom_krows(DBIG) * MOM_LDT;
-    mom_update<NT, CT, NX, true>(st, den_s, Kt, Vt, m, li, lg, []() {});
+    auto none = []() {};
+    if constexpr (SPLIT)
+      mom_update_split<NT, CT, NX, true, decltype(none), true>(st, den_s, Kt, Vt, m, li, lg, none);
+    else
+      mom_update<NT, CT, NX, true>(st, den_s, Kt, Vt, m, li, lg, none);
   }
 
   // ---- write the slice back (the denominators once per feature split) ----

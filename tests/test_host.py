@@ -363,7 +363,7 @@ def test_stats_formulas_match_reference(golden):
 
 def test_library_decode_entries_reject_bad_arguments():
     lib = _native.load_library()
-    assert lib.sta_moment_accumulate(None, None, 0, 1, 1, 1, 4, 1, 32, 2, 1, 9, None, None, None, 15, None, None,
+    assert lib.sta_moment_accumulate(None, None, 0, 1, 1, 1, 4, 1, 32, 2, 1, 9, None, None, None, 15, 1, None, None,
                                      None) == _native.STA_ERR_ARG
     assert lib.sta_decode_moments(None, 0, 1, 4, 4, 1.0, None, None, 15, None, 1, None, None, None) == _native.STA_ERR_ARG
     assert lib.sta_decode_tail(None, None, None, 0, 1, 4, 4, 2, 1.0, 1e-12, 8, None, None, 16, 0, None, None, None, 0,
