@@ -141,7 +141,7 @@ def warm_median(fn, runs=3):
     result, every timed total)."""
     fn()
     res = sorted((fn() for _ in range(runs)), key=lambda r: r["total_s"])
-    return res[len(res) // 2], [round(r["total_s"], 3) for r in res]
+    return res[len(res) // 2], [float(f"{r['total_s']:.4g}") for r in res]
 
 
 def levels_cpu_sample(oracle, w, positions=8):
@@ -423,7 +423,11 @@ def run_flash(args) -> int:
     import triton_article_attention as taa
 
     in_dtype = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.flash_dtype]
-    w = dict(FLASH, seq_len=args.seq_len, heads=args.heads, dtype=args.flash_dtype)
+    w = dict(FLASH, dtype=args.flash_dtype)
+    if args.seq_len is not None:
+        w["seq_len"] = args.seq_len
+    if args.heads is not None:
+        w["heads"] = args.heads
     if args.flash_dtype != "fp32":
         w["workload"] = f"flash_c3_{args.flash_dtype}"
     bh, n, d, dv = w["batch"] * w["heads"], w["seq_len"], w["d"], w["dv"]
