@@ -151,6 +151,20 @@ __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG>& st, const WsSl
     st.v[j] = *reinterpret_cast<const uint4*>(vh + r * vrow_b + sl.v_off[j]);
 }
 
+// An empty use of every staged register: the compiler completes their loads before it (where the
+// stores have consumed them already this costs nothing).
+template <bool DBIG, int ES, int CG>
+__device__ __forceinline__ void ws_settle(const WsStage<DBIG, ES, CG>& st) {
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+    asm volatile("" ::"v"(st.q[j].x), "v"(st.q[j].y), "v"(st.q[j].z), "v"(st.q[j].w));
+    asm volatile("" ::"v"(st.k[j].x), "v"(st.k[j].y), "v"(st.k[j].z), "v"(st.k[j].w));
+  }
+#pragma unroll
+  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j)
+    asm volatile("" ::"v"(st.v[j].x), "v"(st.v[j].y), "v"(st.v[j].z), "v"(st.v[j].w));
+}
+
 // queries of the chunk at row0 -> Qs (scaled; column d = 1, or 0 on rows outside the sequence)
 template <bool DBIG, int ES, int CG, bool MASK>
 __device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
@@ -378,7 +392,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 }
 
 // Staging of iteration c by one thread (keys / values of chunk c + 1, queries of chunk c into LDS from the
-// register set, loads of slot c + 3 into it): the main loop's staging step, for the query waves of a
+// registers, loads of slot c + 2 into them): the main loop's staging step, for the query waves of a
 // segment-totals pass, which only stage.
 template <bool DBIG, int ES, int CG>
 __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG>& pre, const WsSlots<DBIG, ES, CG>& sl,
@@ -393,8 +407,8 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG>& pre, const 
     ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
   }
   if (c < nch) ws_store_q<DBIG, ES, CG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
-  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + 2 * MOM_C);
-  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + 2 * MOM_C);
+  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
+  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + MOM_C);
 }
 
 // The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
@@ -526,26 +540,23 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       }
     }
   }
-  // two register sets of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is held
-  // in set x & 1 from its load (iteration x - 3) to its store into LDS (iteration x - 1), so a load has
-  // two iterations to land
-  WsStage<DBIG, ES, CG> pre0, pre1;
-  ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first);
-  ws_store_kv<DBIG, ES, CG, true>(pre0, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
+  // one register set of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is loaded
+  // in iteration x - 2 and stored into LDS in iteration x - 1, so a load has one iteration to land.  (Two
+  // sets alternating by iteration parity gave the loads two iterations, but the compiler merged the
+  // sets with register copies at the loop latch, which wait for every load in flight: 6.42 against
+  // 6.0 ms on c3.)
+  WsStage<DBIG, ES, CG> pre;
+  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, first);
+  ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
   __syncthreads();
-  ws_load_kv<DBIG, ES, CG, true>(pre1, sl, a, kh, vh, first + MOM_C);  // slot 1
-  ws_load_q<DBIG, ES, CG, true>(pre1, sl, a, qh, first);
-  ws_load_kv<DBIG, ES, CG, true>(pre0, sl, a, kh, vh, first + 2 * MOM_C);  // slot 2
-  ws_load_q<DBIG, ES, CG, true>(pre0, sl, a, qh, first + MOM_C);
+  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
+  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, first);
 
   if constexpr (!UPD && TOT) {
     {
       // segment totals: the query waves only stage, with the same iterations and barriers
       for (int c = 0; c <= nch; ++c) {
-        if (c & 1)
-          ws_stage_step<DBIG, ES, CG>(pre0, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
-        else
-          ws_stage_step<DBIG, ES, CG>(pre1, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+        ws_stage_step<DBIG, ES, CG>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
         __syncthreads();
       }
       return;
@@ -588,8 +599,6 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) o[tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-        const bool reload = c % cpb == 0 && c < nch;
-        const int par = (c / cpb) & 1;
         // operands of the first two tiles; each pair's successor is loaded once its features are formed
         WsQOps op0, op1;
         ws_qload<NT, NX, LDQ>(op0, 0, Qs, m, li);
@@ -616,13 +625,6 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) split_bf16(x[tt], ah[tt], al[tt]);
           ws_qpair_mma<CT>(o, ah, al, sh[p], sv[p]);
-          if (reload) {  // the next block's state, into the registers this pair no longer needs
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-              sh[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 0));
-              sv[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 1));
-            }
-          }
         }
         if constexpr (ODD) {
           const floatx4 dn = *reinterpret_cast<const floatx4*>(dnb + (NT - 1) * 16);
@@ -635,13 +637,6 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
             split_pair(x0[2], x0[3], ah[tt].y, al[tt].y);
           }
           ws_qsingle_mma<CT>(o, ah, al, oh, ov);
-          if (reload) {
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-              oh[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 0));
-              ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
-            }
-          }
         }
         // this wave's partials of chunk c - 1 -> red[(c - 1) & 1], column-major (red_off); columns
         // CG + lg: the denominator sums of lane group lg
@@ -657,36 +652,56 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     }
 
     // ---- after the role work, all threads: staging of slot c + 1 (keys / values of chunk c + 1, queries of
-    //      chunk c) from its register set and loads of slot c + 3 into it; update waves: the reduction of
+    //      chunk c) from the registers and loads of slot c + 2 into them; update waves: the reduction of
     //      chunk c - 2's partials ----
     {
-      auto stage = [&](WsStage<DBIG, ES, CG>& pre) {
-        const int kv_row = first + (c + 1) * MOM_C;
-        const int q_row = first + c * MOM_C;
-        if (c + 1 < nch) {
-          float* Kt = kvb + ((c + 1) & 1) * KVF;
-          __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
-          if (kv_row >= 0 && kv_row + MOM_C <= n)
-            ws_store_kv<DBIG, ES, CG, false>(pre, sl, a, Kt, vp, kv_row);
-          else
-            ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, vp, kv_row);
+      const int kv_row = first + (c + 1) * MOM_C;
+      const int q_row = first + c * MOM_C;
+      if (c + 1 < nch) {
+        float* Kt = kvb + ((c + 1) & 1) * KVF;
+        __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
+        if (kv_row >= 0 && kv_row + MOM_C <= n)
+          ws_store_kv<DBIG, ES, CG, false>(pre, sl, a, Kt, vp, kv_row);
+        else
+          ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, vp, kv_row);
+      }
+      if (c < nch) {
+        float* Qs = qb + (c & 1) * QF;
+        if (q_row >= 0 && q_row + MOM_C <= n)
+          ws_store_q<DBIG, ES, CG, false>(pre, sl, a, Qs, q_row);
+        else
+          ws_store_q<DBIG, ES, CG, true>(pre, sl, a, Qs, q_row);
+      }
+      // every path through the (conditional) stores above has the staged registers' loads complete here,
+      // so the loads below into the same registers never wait for the younger handoff loads
+      ws_settle(pre);
+      if constexpr (!UPD) {
+        // the state of the block chunk c starts (the query waves answer chunk c next iteration), written
+        // by the update waves before the last barrier: loaded after this iteration's stores and before
+        // the next slot's loads, so that waiting for the staged rows never waits for these
+        if (c >= 1 && c % cpb == 0 && c < nch) {
+          const int par = (c / cpb) & 1;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              sh[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 0));
+              sv[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 1));
+            }
+          }
+          if constexpr (ODD) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+              oh[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 0));
+              ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
+            }
+          }
         }
-        if (c < nch) {
-          float* Qs = qb + (c & 1) * QF;
-          if (q_row >= 0 && q_row + MOM_C <= n)
-            ws_store_q<DBIG, ES, CG, false>(pre, sl, a, Qs, q_row);
-          else
-            ws_store_q<DBIG, ES, CG, true>(pre, sl, a, Qs, q_row);
-        }
-        // slot c + 3: unconditional loads with rows clamped into the sequence (past the end they are
-        // never stored), one code path, so nothing waits on them before their store two iterations on
-        ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + 2 * MOM_C);
-        ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + 2 * MOM_C);
-      };
-      if (c & 1)
-        stage(pre0);
-      else
-        stage(pre1);
+      }
+      // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
+      // never stored), one code path, so nothing waits on them before their store an iteration on
+      ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
+      ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + MOM_C);
       if constexpr (UPD) {
         if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
       }
