@@ -19,8 +19,9 @@
 //
 // Pipeline (one barrier per chunk).  Iteration c: update waves add chunk c; query waves answer chunk
 // c - 1 (one chunk behind, so the state of a new block is in flight for a whole iteration) and write
-// their partials to red[(c - 1) & 1]; all threads stage the keys / values of chunk c + 1 and the
-// queries of chunk c into the other LDS buffers, issue the global loads of the next slot, and reduce
+// their partials to red[(c - 1) & 1]; the staging threads (ws_stagers) stage the keys / values of chunk
+// c + 1 and the queries of chunk c into the other LDS buffers and issue the global loads of the next
+// slot; all threads reduce
 // red[(c - 2) & 1] over the 4 query waves in a fixed order (deterministic) into the partial outputs.
 // At the last chunk of a block the update waves split their state and write it (and the running
 // denominators) to a per-workgroup handoff buffer in global memory, double-buffered by block parity;
@@ -41,7 +42,10 @@ namespace sta {
 
 constexpr int WS_WAVES = 8;
 constexpr int WS_THREADS = 64 * WS_WAVES;
-constexpr int WS_STAGERS = 512;  // every thread stages a share of each chunk
+// Threads that stage the chunks (STG): at degree <= 2 and d <= 64 the 256 of the update waves (the query
+// waves set the pace of a chunk and the update waves have time to spare: c3 6.04 -> 5.88 ms); at degree 3
+// or d > 64 all 512 (no registers for twice the staged units next to the extra factor or wider rows).
+__host__ __device__ constexpr int ws_stagers(int nx, bool dbig) { return nx == 0 && !dbig ? 256 : 512; }
 constexpr int WS_REDUCERS = 256;  // the update waves reduce the partials
 
 struct WsArgs {
@@ -68,25 +72,25 @@ __host__ __device__ constexpr int ws_smem_floats(bool dbig, int cg, int nts) {
   return 2 * ws_kv_floats(dbig, cg) + 2 * ws_q_floats(dbig) + 2 * ws_red_floats(cg) + ws_den_floats(nts);
 }
 
-// Chunk staging in registers by all 512 threads: unit e = tid + 512 j of 16 bytes (4 fp32 or 8 bf16 /
-// fp16).
+// Chunk staging in registers by the STG staging threads (tid < STG): unit e = tid + STG j of 16 bytes (4
+// fp32 or 8 bf16 / fp16).
 // q: row-major units (token e / uq); k and v: token-fast units (token tid & 31) for the transposed LDS
 // rows.  Geometry per thread is fixed for the whole sequence.
-template <bool DBIG, int ES, int CG>
+template <bool DBIG, int ES, int CG, int STG>
 struct WsStage {
   static constexpr int QU = MOM_C * (DBIG ? 128 : 64) * ES / 16;
-  static constexpr int QV = (QU + WS_STAGERS - 1) / WS_STAGERS;
+  static constexpr int QV = (QU + STG - 1) / STG;
   static constexpr int VU = MOM_C * CG * ES / 16;
-  static constexpr int VV = (VU + WS_STAGERS - 1) / WS_STAGERS;
+  static constexpr int VV = (VU + STG - 1) / STG;
   uint4 q[QV];
   uint4 k[QV];
   uint4 v[VV];
 };
 
-template <bool DBIG, int ES, int CG>
+template <bool DBIG, int ES, int CG, int STG>
 struct WsSlots {
-  static constexpr int QV = WsStage<DBIG, ES, CG>::QV;
-  static constexpr int VV = WsStage<DBIG, ES, CG>::VV;
+  static constexpr int QV = WsStage<DBIG, ES, CG, STG>::QV;
+  static constexpr int VV = WsStage<DBIG, ES, CG, STG>::VV;
   int q_tok[QV];
   uint32_t q_off[QV];
   int q_lds[QV];
@@ -97,16 +101,16 @@ struct WsSlots {
   int v_col[VV];  // -1: unused
 };
 
-template <bool DBIG, int ES, int CG>
-__device__ __forceinline__ WsSlots<DBIG, ES, CG> ws_slots(const MomArgs& a, int col0) {
+template <bool DBIG, int ES, int CG, int STG>
+__device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a, int col0) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int epu = 16 / ES;
-  WsSlots<DBIG, ES, CG> sl;
+  WsSlots<DBIG, ES, CG, STG> sl;
   const int tid = threadIdx.x;
   const int uq = a.d / epu;
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
-    const int e = tid + WS_STAGERS * j;
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
+    const int e = tid + STG * j;
     const int t = e / uq, u = e - t * uq;
     sl.q_use[j] = t < MOM_C;
     sl.q_tok[j] = min(t, MOM_C - 1);
@@ -117,8 +121,8 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG> ws_slots(const MomArgs& a, int 
     sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j) {
-    const int uv = (tid + WS_STAGERS * j) >> 5;
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j) {
+    const int uv = (tid + STG * j) >> 5;
     sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
     sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
   }
@@ -126,53 +130,53 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG> ws_slots(const MomArgs& a, int 
 }
 
 // MASK = false: every row of the chunk lies in the sequence (no clamping)
-template <bool DBIG, int ES, int CG, bool MASK>
-__device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+template <bool DBIG, int ES, int CG, int STG, bool MASK>
+__device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                           const MomArgs& a, const char* qh, int row0) {
   const uint32_t qrow = static_cast<uint32_t>(a.d * ES);
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int r = MASK ? clamp_row(row0 + sl.q_tok[j], static_cast<int>(a.n)) : row0 + sl.q_tok[j];
     st.q[j] = *reinterpret_cast<const uint4*>(qh + static_cast<uint32_t>(r) * qrow + sl.q_off[j]);
   }
 }
 
-template <bool DBIG, int ES, int CG, bool MASK>
-__device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+template <bool DBIG, int ES, int CG, int STG, bool MASK>
+__device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                            const MomArgs& a, const char* kh, const char* vh, int row0) {
   const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
   const int t = row0 + (threadIdx.x & (MOM_C - 1));
   const uint32_t r = static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j)
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j)
     st.k[j] = *reinterpret_cast<const uint4*>(kh + r * krow_b + sl.k_off[j]);
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j)
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j)
     st.v[j] = *reinterpret_cast<const uint4*>(vh + r * vrow_b + sl.v_off[j]);
 }
 
 // An empty use of every staged register: the compiler completes their loads before it (where the
 // stores have consumed them already this costs nothing).
-template <bool DBIG, int ES, int CG>
-__device__ __forceinline__ void ws_settle(const WsStage<DBIG, ES, CG>& st) {
+template <bool DBIG, int ES, int CG, int STG>
+__device__ __forceinline__ void ws_settle(const WsStage<DBIG, ES, CG, STG>& st) {
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     asm volatile("" ::"v"(st.q[j].x), "v"(st.q[j].y), "v"(st.q[j].z), "v"(st.q[j].w));
     asm volatile("" ::"v"(st.k[j].x), "v"(st.k[j].y), "v"(st.k[j].z), "v"(st.k[j].w));
   }
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j)
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j)
     asm volatile("" ::"v"(st.v[j].x), "v"(st.v[j].y), "v"(st.v[j].z), "v"(st.v[j].w));
 }
 
 // queries of the chunk at row0 -> Qs (scaled; column d = 1, or 0 on rows outside the sequence)
-template <bool DBIG, int ES, int CG, bool MASK>
-__device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+template <bool DBIG, int ES, int CG, int STG, bool MASK>
+__device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                            const MomArgs& a, float* Qs, int row0) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr bool wide = ES == 2;
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     if (!sl.q_use[j]) continue;
     const int row = row0 + sl.q_tok[j];
     const float sc = (!MASK || (row >= 0 && row < a.n)) ? a.scale : 0.f;
@@ -187,14 +191,14 @@ __device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG>& st, cons
 }
 
 // keys (transposed, row d = constant) and values (bf16 hi / lo planes, vps_off) of the chunk at row0
-template <bool DBIG, int ES, int CG, bool MASK>
-__device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG>& st, const WsSlots<DBIG, ES, CG>& sl,
+template <bool DBIG, int ES, int CG, int STG, bool MASK>
+__device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                             const MomArgs& a, float* Kt, __bf16* vplane, int row0) {
   constexpr bool wide = ES == 2;
   const int tok = threadIdx.x & (MOM_C - 1);
   const float kok = (!MASK || (row0 + tok >= 0 && row0 + tok < a.n)) ? 1.f : 0.f;
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::QV; ++j) {
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int kd = sl.k_dim[j];
     if (kd < 0) continue;
     float f[8];
@@ -204,7 +208,7 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG>& st, con
       if (m < 4 || wide) Kt[(kd + m) * MOM_LDT + tok] = f[m] * kok;
   }
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG>::VV; ++j) {
+  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j) {
     const int c0 = sl.v_col[j];
     if (c0 < 0) continue;
     float f[8];
@@ -394,8 +398,8 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 // Staging of iteration c by one thread (keys / values of chunk c + 1, queries of chunk c into LDS from the
 // registers, loads of slot c + 2 into them): the main loop's staging step, for the query waves of a
 // segment-totals pass, which only stage.
-template <bool DBIG, int ES, int CG>
-__device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG>& pre, const WsSlots<DBIG, ES, CG>& sl,
+template <bool DBIG, int ES, int CG, int STG>
+__device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, const WsSlots<DBIG, ES, CG, STG>& sl,
                                               const MomArgs& a, float* kvb, float* qb, int c, int nch, int first,
                                               const char* kh, const char* vh, const char* qh) {
   constexpr int KVF = ws_kv_floats(DBIG, CG);
@@ -404,11 +408,11 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG>& pre, const 
   const int q_row = first + c * MOM_C;
   if (c + 1 < nch) {
     float* Kt = kvb + ((c + 1) & 1) * KVF;
-    ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
+    ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
   }
-  if (c < nch) ws_store_q<DBIG, ES, CG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
-  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + MOM_C);
+  if (c < nch) ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
+  ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
+  ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
 }
 
 // The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
@@ -428,6 +432,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   constexpr int KVF = ws_kv_floats(DBIG, CG);
   constexpr int QF = ws_q_floats(DBIG);
   constexpr int REDF = ws_red_floats(CG);
+  constexpr int STG = ws_stagers(NX, DBIG);
   constexpr int NPS = (NTS + 1) / 2;  // operand pairs per slot in the handoff
   constexpr int NP = NT / 2;          // full tile pairs of this wave
   constexpr bool ODD = (NT & 1) != 0;
@@ -463,7 +468,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
-  const WsSlots<DBIG, ES, CG> sl = ws_slots<DBIG, ES, CG>(a, col0);  // used by the update waves only
+  const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0);  // the staging threads' units
   // operand (pair p, column tile ct, hi / lo) of this slot and block parity par
   auto hand_at = [&](int par, int p, int ct, int hl) -> uint4* {
     return wa.hand + ((((static_cast<int64_t>(wg) * 2 + par) * 4 + slot) * NPS + p) * CT + ct) * 128 + hl * 64 + lane;
@@ -545,18 +550,23 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   // sets alternating by iteration parity gave the loads two iterations, but the compiler merged the
   // sets with register copies at the loop latch, which wait for every load in flight: 6.42 against
   // 6.0 ms on c3.)
-  WsStage<DBIG, ES, CG> pre;
-  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, first);
-  ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
+  constexpr bool STAGE = UPD || STG == WS_THREADS;  // this wave stages chunks
+  WsStage<DBIG, ES, CG, STG> pre;
+  if constexpr (STAGE) {
+    ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first);
+    ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
+  }
   __syncthreads();
-  ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
-  ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, first);
+  if constexpr (STAGE) {
+    ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
+    ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
+  }
 
   if constexpr (!UPD && TOT) {
     {
       // segment totals: the query waves only stage, with the same iterations and barriers
       for (int c = 0; c <= nch; ++c) {
-        ws_stage_step<DBIG, ES, CG>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+        if constexpr (STAGE) ws_stage_step<DBIG, ES, CG, STG>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
         __syncthreads();
       }
       return;
@@ -657,24 +667,24 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     {
       const int kv_row = first + (c + 1) * MOM_C;
       const int q_row = first + c * MOM_C;
-      if (c + 1 < nch) {
+      if (STAGE && c + 1 < nch) {
         float* Kt = kvb + ((c + 1) & 1) * KVF;
         __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
         if (kv_row >= 0 && kv_row + MOM_C <= n)
-          ws_store_kv<DBIG, ES, CG, false>(pre, sl, a, Kt, vp, kv_row);
+          ws_store_kv<DBIG, ES, CG, STG, false>(pre, sl, a, Kt, vp, kv_row);
         else
-          ws_store_kv<DBIG, ES, CG, true>(pre, sl, a, Kt, vp, kv_row);
+          ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, vp, kv_row);
       }
-      if (c < nch) {
+      if (STAGE && c < nch) {
         float* Qs = qb + (c & 1) * QF;
         if (q_row >= 0 && q_row + MOM_C <= n)
-          ws_store_q<DBIG, ES, CG, false>(pre, sl, a, Qs, q_row);
+          ws_store_q<DBIG, ES, CG, STG, false>(pre, sl, a, Qs, q_row);
         else
-          ws_store_q<DBIG, ES, CG, true>(pre, sl, a, Qs, q_row);
+          ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, Qs, q_row);
       }
       // every path through the (conditional) stores above has the staged registers' loads complete here,
       // so the loads below into the same registers never wait for the younger handoff loads
-      ws_settle(pre);
+      if constexpr (STAGE) ws_settle<DBIG, ES, CG, STG>(pre);
       if constexpr (!UPD) {
         // the state of the block chunk c starts (the query waves answer chunk c next iteration), written
         // by the update waves before the last barrier: loaded after this iteration's stores and before
@@ -700,8 +710,10 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       }
       // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
       // never stored), one code path, so nothing waits on them before their store an iteration on
-      ws_load_kv<DBIG, ES, CG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-      ws_load_q<DBIG, ES, CG, true>(pre, sl, a, qh, q_row + MOM_C);
+      if constexpr (STAGE) {
+        ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
+        ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
+      }
       if constexpr (UPD) {
         if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
       }
