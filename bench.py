@@ -308,7 +308,9 @@ def main() -> int:
     assert torch.equal(res.out.reshape(api_out.shape), api_out)
     print(f"[bench] warmup done", file=sys.stderr, flush=True)
 
-    timer = _engine.KernelTimer()
+    # timed region: HIP events around the moment scan only (the roofline kernel); events around every
+    # launch would add their own GPU time to the step
+    timer = _engine.KernelTimer(only=("moments",))
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -320,8 +322,20 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_step = start.elapsed_time(end) / args.steps
-    per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_step": round(tot / args.steps, 4)}
-                  for name, (tot, cnt) in timer.totals_ms().items()}
+    mom_tot, mom_launches = timer.totals_ms()["moments"]
+
+    # per-kernel breakdown: 3 more steps with events around every launch
+    brk = _engine.KernelTimer()
+    b0 = torch.cuda.Event(enable_timing=True)
+    b1 = torch.cuda.Event(enable_timing=True)
+    b0.record()
+    for _ in range(3):
+        step(brk)
+    b1.record()
+    torch.cuda.synchronize()
+    per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_step": round(tot / 3, 4)}
+                  for name, (tot, cnt) in brk.totals_ms().items()}
+    per_kernel_step_ms = b0.elapsed_time(b1) / 3
 
     # the compressor alone: the same steps with its launches on the main stream, not overlapping the scan
     overlap = _engine.OVERLAP_COMPRESS
@@ -356,7 +370,7 @@ def main() -> int:
 
     f = _plan.num_features(d, w["degree"])
     mom_flops = 4.0 * f * (dv + 1) * bh * n  # algorithmic: update + query, 2*F*(dv+1) each per head-token
-    mom_ms = per_kernel["moments"]["ms_total"] / per_kernel["moments"]["launches"]
+    mom_ms = mom_tot / mom_launches
     achieved = mom_flops / (mom_ms * 1e-3) / 1e12
     value = bh * n / (ms_step * 1e-3)
     split = _engine.MOMENT_PRODUCTS == _engine._native.PRODUCTS_SPLIT_BF16
@@ -393,8 +407,10 @@ def main() -> int:
             "avg_launch_ms": mom_ms,
         },
         "kernels": per_kernel,
-        "kernels_note": ("compress runs on a second stream overlapping moments; its HIP-event interval "
-                         "includes the wait for compute units" if _engine.OVERLAP_COMPRESS else ""),
+        "kernels_note": ("3 steps after the timed region with HIP events around every launch (they take "
+                         f"{per_kernel_step_ms:.4f} ms per step); "
+                         + ("compress runs on a second stream overlapping moments; its HIP-event interval "
+                            "includes the wait for compute units" if _engine.OVERLAP_COMPRESS else "")),
         "compress_alone": compress_alone,
         "host_plan_and_draws_s": round(t_plan, 3),
         "cold_call_ms": round(sorted(cold_ms)[1], 3),
@@ -576,15 +592,16 @@ def run_decode(args) -> int:
     torch.cuda.synchronize()
     t_prefix = time.perf_counter() - t0
     total = args.warmup + args.steps
-    xs = draw(total, 3, s_total, d)
+    xs = draw(total + args.steps, 3, s_total, d)  # warm-up, timed steps, breakdown steps
     t0 = time.perf_counter()
-    st._st.reserve_draws(total)
+    st._st.reserve_draws(total + args.steps)
     t_draws = time.perf_counter() - t0
     print(f"[bench] decode: prefix {t_prefix:.1f}s, draws {t_draws:.1f}s; warmup", file=sys.stderr, flush=True)
     for i in range(args.warmup):
         st.step(xs[i, 0], xs[i, 1], xs[i, 2])
     torch.cuda.synchronize()
-    timer = _engine.KernelTimer()
+    # timed region: HIP events around the moment-state read only (the roofline kernel)
+    timer = _engine.KernelTimer(only=("decode_moments",))
     st._st.timer = timer
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -595,13 +612,20 @@ def run_decode(args) -> int:
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    st._st.timer = None
     ms_step = start.elapsed_time(end) / args.steps
+    mom_tot, mom_launches = timer.totals_ms()["decode_moments"]
+    # per-kernel breakdown: as many steps again, with events around every launch
+    brk = _engine.KernelTimer()
+    st._st.timer = brk
+    for i in range(total, total + args.steps):
+        st.step(xs[i, 0], xs[i, 1], xs[i, 2])
+    torch.cuda.synchronize()
+    st._st.timer = None
     per_kernel = {name: {"ms_total": round(tot, 4), "launches": cnt, "ms_per_launch": round(tot / cnt, 5)}
-                  for name, (tot, cnt) in timer.totals_ms().items()}
+                  for name, (tot, cnt) in brk.totals_ms().items()}
     f = _plan.num_features(d, w["degree"])
     state_bytes = s_total * f * (dv + 1) * 4  # algorithmic: the moment state is read once per step
-    mom_ms = per_kernel["decode_moments"]["ms_total"] / per_kernel["decode_moments"]["launches"]
+    mom_ms = mom_tot / mom_launches
     achieved = state_bytes / (mom_ms * 1e-3) / 1e9
     value = s_total / (ms_step * 1e-3)  # every stream advances one token per step
     line = {
@@ -630,7 +654,10 @@ def run_decode(args) -> int:
             "avg_launch_ms": mom_ms,
         },
         "kernels": per_kernel,
+        "kernels_note": "the steps after the timed region, with HIP events around every launch",
         "block_completions_timed": (w["prefix"] + total) // w["block"] - (w["prefix"] + args.warmup) // w["block"],
+        "block_completions_breakdown": ((w["prefix"] + total + args.steps) // w["block"]
+                                        - (w["prefix"] + total) // w["block"]),
         "host_prefix_build_s": round(t_prefix, 3),
         "host_draws_s": round(t_draws, 3),
         "wall_s_timed_region": round(wall, 4),

@@ -26,10 +26,11 @@ SEMANTICS = ("flat", "levels", "exact", "segment", "taylor")
 # bf16 products each (about 2^-16 relative error per product; the moment sums agree with the fp32
 # products to a few 1e-6 relative), or plain fp32 products (PRODUCTS_FP32).
 MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
-# Run the level / block compressor on a second stream, overlapping the moment scan's tail (the scan's
-# workgroups hold the compute units' LDS, so the compressor's start as the scan's shorter workgroups
-# finish).  STA_OVERLAP_COMPRESS=0 runs it on the caller's stream (its kernels then time alone).
-OVERLAP_COMPRESS = os.environ.get("STA_OVERLAP_COMPRESS", "1") != "0"
+# Run the level / block compressor on a second stream (STA_OVERLAP_COMPRESS=1) instead of the caller's
+# stream.  Off by default: the moment scan fills every compute unit's registers, so the compressor
+# cannot run beside it, and a compressor launch that starts first delays the scan's workgroups
+# (32 x 65536 tokens: 9.49 ms per prefill on two streams, 9.38 ms on one; 1 head: 0.618 / 0.609 ms).
+OVERLAP_COMPRESS = os.environ.get("STA_OVERLAP_COMPRESS", "0") != "0"
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 
@@ -129,12 +130,18 @@ def _padded_rows(t: torch.Tensor, width: int) -> torch.Tensor:
 
 
 class KernelTimer:
-    """Records HIP events around each launch on the launch stream (for measured per-kernel times)."""
+    """Records HIP events around each launch on the launch stream (for measured per-kernel times).
+    `only`: the launch names to time (None: all); the others run without events (each timed launch
+    adds a pair of event records to the stream, a few microseconds of GPU time)."""
 
-    def __init__(self) -> None:
+    def __init__(self, only: Optional[Tuple[str, ...]] = None) -> None:
         self.events: Dict[str, list] = {}
+        self.only = None if only is None else frozenset(only)
 
     def wrap(self, name: str, fn: Callable[[], None]) -> None:
+        if self.only is not None and name not in self.only:
+            fn()
+            return
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
@@ -326,9 +333,8 @@ def prefill(
                 fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
             _native.check(st, "sta_moments")
 
-    # The compressor needs only the keys and the draws: on a second stream (default priority), released
-    # before the moment scan is queued, it runs in the compute units the scan leaves idle (its shorter
-    # workgroups finish first).
+    # The compressor needs only the keys and the draws: with OVERLAP_COMPRESS it goes on a second stream
+    # (default priority), released before the moment scan is queued.
     main = torch.cuda.current_stream(dev)
     side = _side_stream(dev) if (OVERLAP_COMPRESS and semantics != "segment" and plan.batches) else main
     if side is not main:

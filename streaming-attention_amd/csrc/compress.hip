@@ -58,38 +58,88 @@ struct CompressArgs {
   float* node_w;      // [BH][n_nodes][cap]
 };
 
-// Projection score <row, dir> of one key row: fp64 accumulation in dimension order, rounded to fp32
-// once (every fp32 x fp32 product is exact in fp64, so the score is a fixed function of the inputs).  The
-// row starts at element offset `off` of k (fp32 / bf16 / fp16) and is read in 16-byte units when `vec`
-// (row start 16-byte aligned and d a whole number of units).
-__device__ __forceinline__ float projection_score_row(const void* k, int64_t off, int d, int dtype, bool vec,
-                                                      const float* dir) {
-  double acc = 0.0;
+// A bf16 / fp16 element from its 16 bits.
+__device__ __forceinline__ float half_bits_to_float(uint16_t h, int dtype) {
+  return dtype == BF16 ? __uint_as_float(static_cast<uint32_t>(h) << 16)
+                       : static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Projection scores <row, dir> of one or two key rows (`two`): fp64 accumulation in dimension order,
+// rounded to fp32 once (every fp32 x fp32 product is exact in fp64, so a score is a fixed function of
+// the inputs).  Row r starts at element offset off_r of k_r (fp32 / bf16 / fp16) and is read in
+// 16-byte units when `vec` (row starts 16-byte aligned, d a whole number of units).  The units of both
+// rows are loaded 8 at a time before their products are accumulated, so up to 16 loads are in flight
+// instead of one load per accumulation step.
+__device__ __forceinline__ void projection_scores2(const void* k0, int64_t off0, const void* k1, int64_t off1,
+                                                   bool two, int d, int dtype, bool vec, const float* dir,
+                                                   float& s0, float& s1) {
+  constexpr int B = 8;
+  double a0 = 0.0, a1 = 0.0;
   if (vec && dtype == F32) {
-    const floatx4* r = reinterpret_cast<const floatx4*>(static_cast<const float*>(k) + off);
-    for (int u = 0; u < d / 4; ++u) {
-      const floatx4 x = r[u];
+    const floatx4* r0 = reinterpret_cast<const floatx4*>(static_cast<const float*>(k0) + off0);
+    const floatx4* r1 = reinterpret_cast<const floatx4*>(static_cast<const float*>(k1) + off1);
+    const int nu = d / 4;
+    for (int u0 = 0; u0 < nu; u0 += B) {
+      floatx4 x0[B], x1[B];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fma(static_cast<double>(x[e]), static_cast<double>(dir[4 * u + e]), acc);
+      for (int t = 0; t < B; ++t) {
+        if (u0 + t < nu) {
+          x0[t] = r0[u0 + t];
+          if (two) x1[t] = r1[u0 + t];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < B; ++t) {
+        if (u0 + t < nu) {
+          const float* dr = dir + 4 * (u0 + t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a0 = fma(static_cast<double>(x0[t][e]), static_cast<double>(dr[e]), a0);
+          if (two) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a1 = fma(static_cast<double>(x1[t][e]), static_cast<double>(dr[e]), a1);
+          }
+        }
+      }
     }
   } else if (vec) {
-    const uint4* r = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(k) + off);
-    for (int u = 0; u < d / 8; ++u) {
-      const uint4 x = r[u];
-      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+    const uint4* r0 = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(k0) + off0);
+    const uint4* r1 = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(k1) + off1);
+    const int nu = d / 8;
+    for (int u0 = 0; u0 < nu; u0 += B) {
+      uint4 x0[B], x1[B];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t h = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
-        const float f = dtype == BF16 ? __uint_as_float(static_cast<uint32_t>(h) << 16)
-                                      : static_cast<float>(__builtin_bit_cast(_Float16, h));
-        acc = fma(static_cast<double>(f), static_cast<double>(dir[8 * u + e]), acc);
+      for (int t = 0; t < B; ++t) {
+        if (u0 + t < nu) {
+          x0[t] = r0[u0 + t];
+          if (two) x1[t] = r1[u0 + t];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < B; ++t) {
+        if (u0 + t < nu) {
+          const float* dr = dir + 8 * (u0 + t);
+          const uint32_t w0[4] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w};
+          const uint32_t w1[4] = {x1[t].x, x1[t].y, x1[t].z, x1[t].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const double de = static_cast<double>(dr[e]);
+            const int sh = (e & 1) * 16;
+            a0 = fma(static_cast<double>(half_bits_to_float(static_cast<uint16_t>(w0[e >> 1] >> sh), dtype)), de, a0);
+            if (two)
+              a1 = fma(static_cast<double>(half_bits_to_float(static_cast<uint16_t>(w1[e >> 1] >> sh), dtype)), de, a1);
+          }
+        }
       }
     }
   } else {
-    for (int col = 0; col < d; ++col)
-      acc = fma(static_cast<double>(load_elem(k, off + col, dtype)), static_cast<double>(dir[col]), acc);
+    for (int col = 0; col < d; ++col) {
+      const double de = static_cast<double>(dir[col]);
+      a0 = fma(static_cast<double>(load_elem(k0, off0 + col, dtype)), de, a0);
+      if (two) a1 = fma(static_cast<double>(load_elem(k1, off1 + col, dtype)), de, a1);
+    }
   }
-  return static_cast<float>(acc);
+  s0 = static_cast<float>(a0);
+  s1 = static_cast<float>(a1);
 }
 
 // Unsigned key whose order is the float order (-0 = +0; NaN above everything), so that (key, position)
@@ -102,25 +152,39 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
 }
 
 // Stable ascending order of n keys (ties by position): pos_s[rank(i)] = i with rank(i) = #{j: key_j <
-// key_i} + #{j < i: key_j == key_i}.  key_s holds the scores on entry (overwritten with sort keys);
-// n <= CMP_MAX_IN; two barriers.
+// key_i} + #{j < i: key_j == key_i} = #{j < i: key_j <= key_i} + #{j > i: key_j < key_i}.  A wave ranks
+// 64 consecutive items i0 .. i0 + 63 at a time: keys before i0 are compared with <=, keys after the
+// band with <, only the band itself needs the position test (one compare and one add per key elsewhere).
+// key_s holds the scores on entry (overwritten with sort keys); n <= CMP_MAX_IN; nthreads a multiple of
+// 64; two barriers.
 __device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int tid, int nthreads) {
   uint32_t* uk = reinterpret_cast<uint32_t*>(key_s);
   for (int i = tid; i < n; i += nthreads) uk[i] = sort_key(key_s[i]);
   for (int i = n + tid; i < ((n + 3) & ~3); i += nthreads) uk[i] = 0xffffffffu;  // padding of the 4-wide reads
   __syncthreads();
-  for (int i = tid; i < n; i += nthreads) {
-    const uint32_t me = uk[i];
+  const int n4 = (n + 3) & ~3;
+  const int lane = tid & 63;
+  for (int i0 = tid - lane; i0 < n; i0 += nthreads) {  // wave-uniform
+    const int i = i0 + lane;
+    const uint32_t me = i < n ? uk[i] : 0u;
     int rank = 0;
-    const int n4 = (n + 3) & ~3;
-    for (int j = 0; j < n4; j += 4) {
+    for (int j = 0; j < i0; j += 4) {
+      const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
+      rank += (o.x <= me ? 1 : 0) + (o.y <= me ? 1 : 0) + (o.z <= me ? 1 : 0) + (o.w <= me ? 1 : 0);
+    }
+    const int band = min(i0 + 64, n4);
+    for (int j = i0; j < band; j += 4) {
       const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
       rank += (o.x < me || (o.x == me && j + 0 < i)) ? 1 : 0;
       rank += (o.y < me || (o.y == me && j + 1 < i)) ? 1 : 0;
       rank += (o.z < me || (o.z == me && j + 2 < i)) ? 1 : 0;
       rank += (o.w < me || (o.w == me && j + 3 < i)) ? 1 : 0;
     }
-    pos_s[rank] = i;
+    for (int j = band; j < n4; j += 4) {  // padding keys (0xffffffff) are never below a key
+      const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
+      rank += (o.x < me ? 1 : 0) + (o.y < me ? 1 : 0) + (o.z < me ? 1 : 0) + (o.w < me ? 1 : 0);
+    }
+    if (i < n) pos_s[rank] = i;
   }
   __syncthreads();
 }
@@ -194,8 +258,15 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   __syncthreads();
   const int epu = a.dtype == F32 ? 4 : 8;
   const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
-  for (int i = tid; i < n_in; i += CMP_THREADS)
-    key_s[i] = projection_score_row(a.k, (bh * a.n + src_s[i]) * a.d, a.d, a.dtype, vec, dir_s);
+  for (int i = tid; i < n_in; i += 2 * CMP_THREADS) {  // items i and i + CMP_THREADS together
+    const int i1 = i + CMP_THREADS;
+    const bool two = i1 < n_in;
+    float s0, s1;
+    projection_scores2(a.k, (bh * a.n + src_s[i]) * a.d, a.k, (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d,
+                       a.dtype, vec, dir_s, s0, s1);
+    key_s[i] = s0;
+    if (two) key_s[i1] = s1;
+  }
 
   // ---- stable ascending order of (score, position) ----
   rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);

@@ -428,8 +428,15 @@ __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecC
       // sorted_pair: fp64 projection scores of the input rows, stable ascending sort, pair selection
       for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = a.dirs[slot * a.d + e];
       __syncthreads();
-      for (int j = tid; j < n; j += CMP_THREADS)
-        key_s[j] = projection_score_row(key_row(in_h[j]), 0, a.d, F32, (a.d & 3) == 0, dir_s);
+      for (int j = tid; j < n; j += 2 * CMP_THREADS) {  // rows j and j + CMP_THREADS together
+        const int j1 = j + CMP_THREADS;
+        const bool two = j1 < n;
+        float s0, s1;
+        projection_scores2(key_row(in_h[j]), 0, key_row(in_h[two ? j1 : j]), 0, two, a.d, F32, (a.d & 3) == 0, dir_s,
+                           s0, s1);
+        key_s[j] = s0;
+        if (two) key_s[j1] = s1;
+      }
       rank_sort(key_s, pos_s, n, tid, CMP_THREADS);
       const float* u = a.unif + slot * (a.max_in / 2);
       const int pc = n / 2;

@@ -21,12 +21,12 @@
 // c - 1 (one chunk behind, so the state of a new block is in flight for a whole iteration) and write
 // their partials to red[(c - 1) & 1]; the staging threads (ws_stagers) stage the keys / values of chunk
 // c + 1 and the queries of chunk c into the other LDS buffers and issue the global loads of the next
-// slot; all threads reduce
-// red[(c - 2) & 1] over the 4 query waves in a fixed order (deterministic) into the partial outputs.
-// At the last chunk of a block the update waves split their state and write it (and the running
-// denominators) to a per-workgroup handoff buffer in global memory, double-buffered by block parity;
-// the query waves load it in the next iteration, right after their last use of the old copy.  The
-// handoff stays within the workgroup (stores, barrier, loads on one compute unit).
+// slot; the update waves reduce red[(c - 2) & 1] over the 4 query waves in a fixed order
+// (deterministic) into the partial outputs.  At the last chunk of a block the update waves split their
+// state and write it to a per-workgroup handoff buffer in global memory (one copy; two by block parity
+// when a block is 2 chunks) and the running denominators to LDS (two by block parity); the query waves
+// load the state in the next iteration, right after their last use of the old copy.  The handoff stays
+// within the workgroup (stores, barrier, loads on one compute unit).
 //
 // Sequence segments (few heads).  With nseg > 1 each (head, feature split, column group) is cut into
 // nseg segments of seg_chunks chunks (whole query blocks), one workgroup each, in two passes.  Phase
@@ -454,6 +454,10 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   const int nch = wa.nseg > 1 ? min(wa.seg_chunks, nch_all - c_begin) : nch_all;
   const int first = -a.shift + c_begin * MOM_C;
   const int cpb = wa.cpb;
+  // handoff copies: the query waves load a block's state in the iteration after the update waves write
+  // it and first use it one iteration later; with cpb >= 3 the next write comes after that iteration's
+  // barrier, so one copy serves (half the footprint in L2), with cpb = 2 two alternate by block parity
+  const int hmask = cpb >= 3 ? 0 : 1;
   constexpr bool totals = TOT;            // phase 1: update only, write the segment's total
   const bool from_init = wa.phase == 2;   // start from the state before the segment
   // segment state of this (head, feature split, column group, segment): [4][NTS][CT][64] floatx4, den
@@ -580,6 +584,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
         if (!totals && (c + 1) % cpb == 0 && c + 1 < nch) {
           // the state the queries of block (c + 1) / cpb see -> handoff (parity of that block)
           const int par = ((c + 1) / cpb) & 1;
+          const int hp = par & hmask;
 #pragma unroll
           for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
@@ -587,8 +592,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
               uint32_t h0, h1, l0, l1;
               split_pair(st[kt][ct][0], st[kt][ct][1], h0, l0);
               split_pair(st[kt][ct][2], st[kt][ct][3], h1, l1);
-              reinterpret_cast<uint2*>(hand_at(par, kt >> 1, ct, 0))[kt & 1] = uint2{h0, h1};
-              reinterpret_cast<uint2*>(hand_at(par, kt >> 1, ct, 1))[kt & 1] = uint2{l0, l1};
+              reinterpret_cast<uint2*>(hand_at(hp, kt >> 1, ct, 0))[kt & 1] = uint2{h0, h1};
+              reinterpret_cast<uint2*>(hand_at(hp, kt >> 1, ct, 1))[kt & 1] = uint2{l0, l1};
             }
             if (den) {
               float t = den_p[kt];
@@ -690,7 +695,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
         // by the update waves before the last barrier: loaded after this iteration's stores and before
         // the next slot's loads, so that waiting for the staged rows never waits for these
         if (c >= 1 && c % cpb == 0 && c < nch) {
-          const int par = (c / cpb) & 1;
+          const int par = (c / cpb) & hmask;
 #pragma unroll
           for (int p = 0; p < NP; ++p) {
 #pragma unroll
