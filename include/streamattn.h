@@ -254,7 +254,7 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
  * and MergeReduceCoreset._compress* (streaming_taylor_coreset_attention.py:413-467) for level merges.
  *   batch_nodes[n_batch]: node ids to compute in this launch (their inputs must already exist).
  *   node_desc[n_nodes][8]: kind (0 raw block, 1 merge), a, b (raw: first token; merge: child ids),
- *     n_in, n_out, method (0 copy, 1 sorted_pair, 2 permutation), draw slot, unused.
+ *     n_in, n_out, method (0 copy, 1 sorted_pair, 2 permutation), draw slot, n_out of child a (merge; 0 raw).
  *   dirs [BH][n_draws][D] (normalised projection), unif [BH][n_draws][max_in/2] (pair uniforms),
  *   perms [BH][n_draws][max_in] (randperm draws): the seed-derived draws, replayed by the host.
  *   outputs: node_src [BH][n_nodes][cap] (global token index of each kept item), node_w (its weight).

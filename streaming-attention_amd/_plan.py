@@ -655,7 +655,8 @@ def levels_plan(n: int, block: int, compressor: str) -> NodePlan:
                 if lev == 0:
                     desc[i] = [KIND_RAW, j * block, 0, n_in_of[i], sizes[i], 0, slot[i], 0]
                 else:
-                    desc[i] = [KIND_MERGE, nid(lev - 1, 2 * j), nid(lev - 1, 2 * j + 1), n_in_of[i], sizes[i], 0, slot[i], 0]
+                    a_ = nid(lev - 1, 2 * j)
+                    desc[i] = [KIND_MERGE, a_, nid(lev - 1, 2 * j + 1), n_in_of[i], sizes[i], 0, slot[i], sizes[a_]]
                 level_of[i] = lev
                 if j % 2 == 0:
                     lo = (j + 1) * (1 << lev) * block - 1

@@ -25,7 +25,7 @@ namespace sta {
 
 enum NodeKind : int { KIND_RAW = 0, KIND_MERGE = 1 };
 enum NodeMethod : int { M_COPY = 0, M_SORTED_PAIR = 1, M_PERM = 2 };
-constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, unused
+constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, n_out of child a (merge)
 constexpr int CMP_MAX_IN = 4096;
 constexpr int CMP_THREADS = 256;
 
@@ -164,27 +164,48 @@ __device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int t
   __syncthreads();
   const int n4 = (n + 3) & ~3;
   const int lane = tid & 63;
-  for (int i0 = tid - lane; i0 < n; i0 += nthreads) {  // wave-uniform
+  // i0 and the loop bounds are wave-uniform (scalar loops); the key reads are issued 4 at a time (16
+  // keys) before they are compared, into two counters
+  for (int i0 = __builtin_amdgcn_readfirstlane(tid - lane); i0 < n; i0 += nthreads) {
     const int i = i0 + lane;
     const uint32_t me = i < n ? uk[i] : 0u;
-    int rank = 0;
-    for (int j = 0; j < i0; j += 4) {
-      const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
-      rank += (o.x <= me ? 1 : 0) + (o.y <= me ? 1 : 0) + (o.z <= me ? 1 : 0) + (o.w <= me ? 1 : 0);
+    int r0 = 0, r1 = 0;
+    for (int j = 0; j < i0; j += 16) {  // i0 is a multiple of 64
+      uint4 o[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] = *reinterpret_cast<const uint4*>(uk + j + 4 * t);
+#pragma unroll
+      for (int t = 0; t < 4; t += 2) {
+        r0 += (o[t].x <= me ? 1 : 0) + (o[t].y <= me ? 1 : 0) + (o[t].z <= me ? 1 : 0) + (o[t].w <= me ? 1 : 0);
+        r1 += (o[t + 1].x <= me ? 1 : 0) + (o[t + 1].y <= me ? 1 : 0) + (o[t + 1].z <= me ? 1 : 0) +
+              (o[t + 1].w <= me ? 1 : 0);
+      }
     }
     const int band = min(i0 + 64, n4);
     for (int j = i0; j < band; j += 4) {
       const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
-      rank += (o.x < me || (o.x == me && j + 0 < i)) ? 1 : 0;
-      rank += (o.y < me || (o.y == me && j + 1 < i)) ? 1 : 0;
-      rank += (o.z < me || (o.z == me && j + 2 < i)) ? 1 : 0;
-      rank += (o.w < me || (o.w == me && j + 3 < i)) ? 1 : 0;
+      r0 += (o.x < me || (o.x == me && j + 0 < i)) ? 1 : 0;
+      r1 += (o.y < me || (o.y == me && j + 1 < i)) ? 1 : 0;
+      r0 += (o.z < me || (o.z == me && j + 2 < i)) ? 1 : 0;
+      r1 += (o.w < me || (o.w == me && j + 3 < i)) ? 1 : 0;
     }
-    for (int j = band; j < n4; j += 4) {  // padding keys (0xffffffff) are never below a key
+    int j = band;
+    for (; j + 16 <= n4; j += 16) {  // padding keys (0xffffffff) are never below a key
+      uint4 o[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] = *reinterpret_cast<const uint4*>(uk + j + 4 * t);
+#pragma unroll
+      for (int t = 0; t < 4; t += 2) {
+        r0 += (o[t].x < me ? 1 : 0) + (o[t].y < me ? 1 : 0) + (o[t].z < me ? 1 : 0) + (o[t].w < me ? 1 : 0);
+        r1 += (o[t + 1].x < me ? 1 : 0) + (o[t + 1].y < me ? 1 : 0) + (o[t + 1].z < me ? 1 : 0) +
+              (o[t + 1].w < me ? 1 : 0);
+      }
+    }
+    for (; j < n4; j += 4) {
       const uint4 o = *reinterpret_cast<const uint4*>(uk + j);
-      rank += (o.x < me ? 1 : 0) + (o.y < me ? 1 : 0) + (o.z < me ? 1 : 0) + (o.w < me ? 1 : 0);
+      r0 += (o.x < me ? 1 : 0) + (o.y < me ? 1 : 0) + (o.z < me ? 1 : 0) + (o.w < me ? 1 : 0);
     }
-    if (i < n) pos_s[rank] = i;
+    if (i < n) pos_s[r0 + r1] = i;
   }
   __syncthreads();
 }
@@ -210,19 +231,31 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   const int tid = threadIdx.x;
   const int32_t* dsc = a.desc + static_cast<int64_t>(node) * NODE_DESC;
   const int kind = dsc[0], ia = dsc[1], ib = dsc[2], n_in = dsc[3], n_out = dsc[4];
-  const int method = dsc[5], slot = dsc[6];
+  const int method = dsc[5], slot = dsc[6], na = dsc[7];
   // descriptors come from the host plan; refuse anything the LDS arrays cannot hold (uniform exit)
   if (n_in <= 0 || n_in > CMP_MAX_IN || n_in > a.max_in || n_out > a.cap) return;
   if (kind == KIND_RAW && (ia < 0 || ia + n_in > a.n)) return;
+  if (kind == KIND_MERGE && (na < 0 || na > n_in)) return;
 
-  // ---- gather the input item list ----
+  // ---- gather the input item list; in the same round trip the projection direction and the uniforms
+  //      of this thread's first two pairs ----
+  const bool pairs = method == M_SORTED_PAIR;
+  const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);
+  const int pc = n_in / 2;
+  float u_first[2] = {0.f, 0.f};
+  if (pairs) {
+    const float* dir = a.dirs + (bh * a.n_draws + slot) * a.d;
+    for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = dir[e];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if (tid + r * CMP_THREADS < pc) u_first[r] = u[tid + r * CMP_THREADS];
+  }
   if (kind == KIND_RAW) {
     for (int i = tid; i < n_in; i += CMP_THREADS) {
       src_s[i] = ia + i;
       w_s[i] = 1.0f;
     }
   } else {
-    const int na = a.desc[static_cast<int64_t>(ia) * NODE_DESC + 4];
     const int64_t baseA = (bh * a.n_nodes + ia) * a.cap;
     const int64_t baseB = (bh * a.n_nodes + ib) * a.cap;
     for (int i = tid; i < n_in; i += CMP_THREADS) {
@@ -253,9 +286,6 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   }
 
   // ---- sorted_pair: projection scores (fp64 accumulation, fixed index order), one item per thread ----
-  const float* dir = a.dirs + (bh * a.n_draws + slot) * a.d;
-  for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = dir[e];
-  __syncthreads();
   const int epu = a.dtype == F32 ? 4 : 8;
   const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
   for (int i = tid; i < n_in; i += 2 * CMP_THREADS) {  // items i and i + CMP_THREADS together
@@ -272,12 +302,11 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
 
   // ---- pair selection with weight transfer ----
-  const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);
-  const int pc = n_in / 2;
   for (int p = tid; p < pc; p += CMP_THREADS) {
     const int ia2 = pos_s[2 * p], ib2 = pos_s[2 * p + 1];
     const float wa = w_s[ia2], wb = w_s[ib2];
-    const bool choose_a = pair_keeps_first(u[p], wa, wb);
+    const int r = (p - tid) / CMP_THREADS;
+    const bool choose_a = pair_keeps_first(r < 2 ? u_first[r] : u[p], wa, wb);
     a.node_src[obase + p] = choose_a ? src_s[ia2] : src_s[ib2];
     a.node_w[obase + p] = wa + wb;
   }
