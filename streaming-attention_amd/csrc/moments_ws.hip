@@ -99,14 +99,16 @@ struct WsSlots {
   int k_dim[QV];  // -1: unused
   uint32_t v_off[VV];
   int v_col[VV];  // -1: unused
+  int sidx;       // this thread's index among the staging threads
 };
 
 template <bool DBIG, int ES, int CG, int STG>
-__device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a, int col0) {
+__device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a, int col0, int sidx) {
   constexpr int LDQ = mom_ldq(DBIG);
   constexpr int epu = 16 / ES;
   WsSlots<DBIG, ES, CG, STG> sl;
-  const int tid = threadIdx.x;
+  const int tid = sidx;
+  sl.sidx = sidx;
   const int uq = a.d / epu;
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
@@ -145,7 +147,7 @@ template <bool DBIG, int ES, int CG, int STG, bool MASK>
 __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                            const MomArgs& a, const char* kh, const char* vh, int row0) {
   const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
-  const int t = row0 + (threadIdx.x & (MOM_C - 1));
+  const int t = row0 + (sl.sidx & (MOM_C - 1));
   const uint32_t r = static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j)
@@ -186,7 +188,7 @@ __device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG, STG>& st,
     *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
     if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
   }
-  const int tid = threadIdx.x;
+  const int tid = sl.sidx;
   if (tid < MOM_C) Qs[tid * LDQ + a.d] = (!MASK || (row0 + tid >= 0 && row0 + tid < a.n)) ? 1.f : 0.f;
 }
 
@@ -195,7 +197,7 @@ template <bool DBIG, int ES, int CG, int STG, bool MASK>
 __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                             const MomArgs& a, float* Kt, __bf16* vplane, int row0) {
   constexpr bool wide = ES == 2;
-  const int tok = threadIdx.x & (MOM_C - 1);
+  const int tok = sl.sidx & (MOM_C - 1);
   const float kok = (!MASK || (row0 + tok >= 0 && row0 + tok < a.n)) ? 1.f : 0.f;
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
@@ -223,7 +225,7 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
       }
     }
   }
-  if (threadIdx.x < MOM_C) Kt[a.d * MOM_LDT + threadIdx.x] = kok;
+  if (sl.sidx < MOM_C) Kt[a.d * MOM_LDT + sl.sidx] = kok;
 }
 
 // Update wave: S[f][col] += phi_k(tok)[f] V[tok][col] over the chunk for the slot's NT tiles and the
@@ -395,10 +397,10 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
   }
 }
 
-// Staging of iteration c by one thread (keys / values of chunk c + 1, queries of chunk c into LDS from the
-// registers, loads of slot c + 2 into them): the main loop's staging step, for the query waves of a
-// segment-totals pass, which only stage.
-template <bool DBIG, int ES, int CG, int STG>
+// Staging of iteration c by one thread (keys / values of chunk c + 1, with WQ queries of chunk c, into
+// LDS from the registers, loads of slot c + 2 into them): the main loop's staging step, for the query
+// waves of a segment-totals pass, which only stage (keys and values: that pass has no queries).
+template <bool DBIG, int ES, int CG, int STG, bool WQ>
 __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, const WsSlots<DBIG, ES, CG, STG>& sl,
                                               const MomArgs& a, float* kvb, float* qb, int c, int nch, int first,
                                               const char* kh, const char* vh, const char* qh) {
@@ -410,9 +412,9 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, c
     float* Kt = kvb + ((c + 1) & 1) * KVF;
     ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
   }
-  if (c < nch) ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
+  if (WQ && c < nch) ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
   ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-  ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
+  if (WQ) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
 }
 
 // The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
@@ -432,7 +434,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   constexpr int KVF = ws_kv_floats(DBIG, CG);
   constexpr int QF = ws_q_floats(DBIG);
   constexpr int REDF = ws_red_floats(CG);
-  constexpr int STG = ws_stagers(NX, DBIG);
+  // staging threads: in a segment-totals pass the query waves (indices tid - 256), else ws_stagers
+  constexpr int STG = TOT ? 256 : ws_stagers(NX, DBIG);
   constexpr int NPS = (NTS + 1) / 2;  // operand pairs per slot in the handoff
   constexpr int NP = NT / 2;          // full tile pairs of this wave
   constexpr bool ODD = (NT & 1) != 0;
@@ -472,7 +475,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
-  const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0);  // the staging threads' units
+  const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0, TOT ? tid - 256 : tid);
   // operand (pair p, column tile ct, hi / lo) of this slot and block parity par
   auto hand_at = [&](int par, int p, int ct, int hl) -> uint4* {
     return wa.hand + ((((static_cast<int64_t>(wg) * 2 + par) * 4 + slot) * NPS + p) * CT + ct) * 128 + hl * 64 + lane;
@@ -554,7 +557,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   // sets alternating by iteration parity gave the loads two iterations, but the compiler merged the
   // sets with register copies at the loop latch, which wait for every load in flight: 6.42 against
   // 6.0 ms on c3.)
-  constexpr bool STAGE = UPD || STG == WS_THREADS;  // this wave stages chunks
+  // this wave stages chunks: in a segment-totals pass the query waves (the update waves only update)
+  constexpr bool STAGE = TOT ? !UPD : (UPD || STG == WS_THREADS);
   WsStage<DBIG, ES, CG, STG> pre;
   if constexpr (STAGE) {
     ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first);
@@ -563,18 +567,16 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   __syncthreads();
   if constexpr (STAGE) {
     ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
-    ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
+    if constexpr (!TOT) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
   }
 
   if constexpr (!UPD && TOT) {
-    {
-      // segment totals: the query waves only stage, with the same iterations and barriers
-      for (int c = 0; c <= nch; ++c) {
-        if constexpr (STAGE) ws_stage_step<DBIG, ES, CG, STG>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
-        __syncthreads();
-      }
-      return;
+    // segment totals: the query waves stage the keys and values, with the same iterations and barriers
+    for (int c = 0; c <= nch; ++c) {
+      ws_stage_step<DBIG, ES, CG, STG, false>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+      __syncthreads();
     }
+    return;
   }
   for (int c = 0; c <= nch; ++c) {
     if constexpr (UPD) {
