@@ -366,6 +366,8 @@ __device__ __forceinline__ void ws_qsingle_mma(floatx4 (&o)[2][CT], const uint2 
 }
 
 // Fixed-order sum of the 4 query waves' partials of the chunk at row0 -> low_num rows of the CG columns
+// (non-temporal stores: the partials are read only by the next kernel, and the workgroups' state
+// handoff, rewritten every query block, should keep its place in L2)
 // (CG * 8 threads, 4 tokens each) and, with den, low_den (columns CG .. CG + 3 of a wave's partials: the
 // denominator sums of its 4 lane groups).
 constexpr int WS_RCOLS_EXTRA = 4;
@@ -384,7 +386,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
     for (int q = 1; q < 4; ++q) acc += *reinterpret_cast<const floatx4*>(red + q * WS + red_off(col, t4));
     float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) dst[r * a.ldo] = acc[r];
+    for (int r = 0; r < 4; ++r) __builtin_nontemporal_store(acc[r], dst + r * a.ldo);
   }
   if (den && tid >= WS_REDUCERS - MOM_C) {
     const int tok = tid - (WS_REDUCERS - MOM_C);
@@ -393,7 +395,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
     for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int g = 0; g < 4; ++g) dsum += red[q * WS + red_off(CG + g, tok)];
-    a.low_den[obase + row0 + tok] = dsum;
+    __builtin_nontemporal_store(dsum, a.low_den + obase + row0 + tok);
   }
 }
 
