@@ -580,7 +580,69 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     }
     return;
   }
+  // staging of slot c + 1 (keys / values of chunk c + 1, queries of chunk c) from the registers and
+  // loads of slot c + 2 into them; update waves: the reduction of chunk c - 2's partials.  The update
+  // waves do it before their products (it touches only the next chunk's buffers and the partials of
+  // two chunks back), so their VALU and matrix-core phases fall against the query waves' other ones;
+  // the query waves after theirs (their state reload follows the last use of the old copy)
+  auto stage_block = [&](int c) {
+      {
+        const int kv_row = first + (c + 1) * MOM_C;
+        const int q_row = first + c * MOM_C;
+        if (STAGE && c + 1 < nch) {
+          float* Kt = kvb + ((c + 1) & 1) * KVF;
+          __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
+          if (kv_row >= 0 && kv_row + MOM_C <= n)
+            ws_store_kv<DBIG, ES, CG, STG, false>(pre, sl, a, Kt, vp, kv_row);
+          else
+            ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, vp, kv_row);
+        }
+        if (STAGE && c < nch) {
+          float* Qs = qb + (c & 1) * QF;
+          if (q_row >= 0 && q_row + MOM_C <= n)
+            ws_store_q<DBIG, ES, CG, STG, false>(pre, sl, a, Qs, q_row);
+          else
+            ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, Qs, q_row);
+        }
+        // every path through the (conditional) stores above has the staged registers' loads complete here,
+        // so the loads below into the same registers never wait for the younger handoff loads
+        if constexpr (STAGE) ws_settle<DBIG, ES, CG, STG>(pre);
+        if constexpr (!UPD) {
+          // the state of the block chunk c starts (the query waves answer chunk c next iteration), written
+          // by the update waves before the last barrier: loaded after this iteration's stores and before
+          // the next slot's loads, so that waiting for the staged rows never waits for these
+          if (c >= 1 && c % cpb == 0 && c < nch) {
+            const int par = (c / cpb) & hmask;
+  #pragma unroll
+            for (int p = 0; p < NP; ++p) {
+  #pragma unroll
+              for (int ct = 0; ct < CT; ++ct) {
+                sh[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 0));
+                sv[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 1));
+              }
+            }
+            if constexpr (ODD) {
+  #pragma unroll
+              for (int ct = 0; ct < CT; ++ct) {
+                oh[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 0));
+                ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
+              }
+            }
+          }
+        }
+        // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
+        // never stored), one code path, so nothing waits on them before their store an iteration on
+        if constexpr (STAGE) {
+          ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
+          ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
+        }
+        if constexpr (UPD) {
+          if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
+        }
+      }
+  };
   for (int c = 0; c <= nch; ++c) {
+    if constexpr (UPD) stage_block(c);
     if constexpr (UPD) {
       if (c < nch) {
         const float* Kt = kvb + (c & 1) * KVF;
@@ -670,63 +732,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       }
     }
 
-    // ---- after the role work, all threads: staging of slot c + 1 (keys / values of chunk c + 1, queries of
-    //      chunk c) from the registers and loads of slot c + 2 into them; update waves: the reduction of
-    //      chunk c - 2's partials ----
-    {
-      const int kv_row = first + (c + 1) * MOM_C;
-      const int q_row = first + c * MOM_C;
-      if (STAGE && c + 1 < nch) {
-        float* Kt = kvb + ((c + 1) & 1) * KVF;
-        __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
-        if (kv_row >= 0 && kv_row + MOM_C <= n)
-          ws_store_kv<DBIG, ES, CG, STG, false>(pre, sl, a, Kt, vp, kv_row);
-        else
-          ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, vp, kv_row);
-      }
-      if (STAGE && c < nch) {
-        float* Qs = qb + (c & 1) * QF;
-        if (q_row >= 0 && q_row + MOM_C <= n)
-          ws_store_q<DBIG, ES, CG, STG, false>(pre, sl, a, Qs, q_row);
-        else
-          ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, Qs, q_row);
-      }
-      // every path through the (conditional) stores above has the staged registers' loads complete here,
-      // so the loads below into the same registers never wait for the younger handoff loads
-      if constexpr (STAGE) ws_settle<DBIG, ES, CG, STG>(pre);
-      if constexpr (!UPD) {
-        // the state of the block chunk c starts (the query waves answer chunk c next iteration), written
-        // by the update waves before the last barrier: loaded after this iteration's stores and before
-        // the next slot's loads, so that waiting for the staged rows never waits for these
-        if (c >= 1 && c % cpb == 0 && c < nch) {
-          const int par = (c / cpb) & hmask;
-#pragma unroll
-          for (int p = 0; p < NP; ++p) {
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-              sh[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 0));
-              sv[p][ct] = __builtin_bit_cast(bf16x8, *hand_at(par, p, ct, 1));
-            }
-          }
-          if constexpr (ODD) {
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-              oh[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 0));
-              ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
-            }
-          }
-        }
-      }
-      // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
-      // never stored), one code path, so nothing waits on them before their store an iteration on
-      if constexpr (STAGE) {
-        ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-        ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
-      }
-      if constexpr (UPD) {
-        if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
-      }
-    }
+    if constexpr (!UPD) stage_block(c);
     __syncthreads();
     }
   // partials of the last chunk (written by the query waves in iteration nch)
