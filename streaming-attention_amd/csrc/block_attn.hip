@@ -144,7 +144,10 @@ __host__ __device__ constexpr int split_key_pos(int r) {
   return 32 * (r >> 5) + 8 * ((r >> 2) & 3) + 4 * ((r >> 4) & 1) + (r & 3);
 }
 
-template <int DP, int DVT, int RS, int ES, bool SPLIT>
+// KVX (split products, bf16 inputs): the key and value rows are exact in bf16, so their lo planes are
+// zero: the products with them (kl·qh in X, vl·ph in num) and the lo planes themselves are left out
+// (X and num are those of the three-product form, bit for bit).
+template <int DP, int DVT, int RS, int ES, bool SPLIT, bool KVX = false>
 __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_kernel(const BlockArgs a) {
   constexpr int KB = block_kb(DP, DVT);  // keys per LDS stage
   constexpr int NSUB = KB / 16;                         // 16-key subtiles per stage
@@ -303,16 +306,18 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           for (int h = 0; h < 2; ++h) {
             const int off = (16 * (2 * sp + h) + li) * LDKB + 32 * m + 8 * lg;
             kh[h] = *reinterpret_cast<const bf16x8*>(Kh + off);
-            kl[h] = *reinterpret_cast<const bf16x8*>(Kl + off);
+            if constexpr (!KVX) kl[h] = *reinterpret_cast<const bf16x8*>(Kl + off);
           }
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kh[h], ql[rs][m], xq[h][rs]);
+          if constexpr (!KVX) {
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kl[h], qh[rs][m], xq[h][rs]);
+              for (int rs = 0; rs < RS; ++rs) xq[h][rs] = mfma_bf16(kl[h], qh[rs][m], xq[h][rs]);
+          }
 #pragma unroll
           for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -332,11 +337,13 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
         for (int ct = 0; ct < DVT; ++ct) {
           const int off = (16 * ct + li) * LDVB + 32 * sp + 8 * lg;
           const bf16x8 vh = *reinterpret_cast<const bf16x8*>(Vh + off);
-          const bf16x8 vl = *reinterpret_cast<const bf16x8*>(Vl + off);
 #pragma unroll
           for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vh, pl[rs], num[rs][ct]);
+          if constexpr (!KVX) {
+            const bf16x8 vl = *reinterpret_cast<const bf16x8*>(Vl + off);
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vl, ph[rs], num[rs][ct]);
+            for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vl, ph[rs], num[rs][ct]);
+          }
 #pragma unroll
           for (int rs = 0; rs < RS; ++rs) num[rs][ct] = mfma_bf16(vh, ph[rs], num[rs][ct]);
         }
@@ -524,7 +531,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           split_pair(f[0], f[1], h0, l0);
           split_pair(f[2], f[3], h1, l1);
           *reinterpret_cast<uint2*>(Kh + r * LDKB + 4 * u) = uint2{h0, h1};
-          *reinterpret_cast<uint2*>(Kl + r * LDKB + 4 * u) = uint2{l0, l1};
+          if constexpr (!KVX) *reinterpret_cast<uint2*>(Kl + r * LDKB + 4 * u) = uint2{l0, l1};
         }
       }
 #pragma unroll
@@ -538,7 +545,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           for (int m = 0; m < 4; ++m) {
             const __bf16 h = static_cast<__bf16>(f[m]);
             Vh[(4 * u + m) * LDVB + pos] = h;
-            Vl[(4 * u + m) * LDVB + pos] = static_cast<__bf16>(f[m] - static_cast<float>(h));
+            if constexpr (!KVX) Vl[(4 * u + m) * LDVB + pos] = static_cast<__bf16>(f[m] - static_cast<float>(h));
           }
         }
       }

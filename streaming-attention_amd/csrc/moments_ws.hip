@@ -192,8 +192,9 @@ __device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG, STG>& st,
   if (tid < MOM_C) Qs[tid * LDQ + a.d] = (!MASK || (row0 + tid >= 0 && row0 + tid < a.n)) ? 1.f : 0.f;
 }
 
-// keys (transposed, row d = constant) and values (bf16 hi / lo planes, vps_off) of the chunk at row0
-template <bool DBIG, int ES, int CG, int STG, bool MASK>
+// keys (transposed, row d = constant) and values (bf16 hi / lo planes, vps_off) of the chunk at row0;
+// VX: bf16 values, whose lo plane is zero and not written (nor read)
+template <bool DBIG, int ES, int CG, int STG, bool MASK, bool VX = false>
 __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                             const MomArgs& a, float* Kt, __bf16* vplane, int row0) {
   constexpr bool wide = ES == 2;
@@ -221,7 +222,7 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
         const float x = f[m] * kok;
         const __bf16 h = static_cast<__bf16>(x);
         vplane[vps_off(c0 + m, tok)] = h;
-        vplane[CG * MOM_C + vps_off(c0 + m, tok)] = static_cast<__bf16>(x - static_cast<float>(h));
+        if constexpr (!VX) vplane[CG * MOM_C + vps_off(c0 + m, tok)] = static_cast<__bf16>(x - static_cast<float>(h));
       }
     }
   }
@@ -234,7 +235,7 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
 // the 32 tokens (the token mapping of mom_update_split).  The next tile's key reads are issued as soon
 // as the current tile's feature values are formed (into the same registers), so they land while the
 // current tile's operands are split and its products issue.
-template <int NT, int CT, int NX>
+template <int NT, int CT, int NX, bool VX>
 __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[NT], const float* Kt,
                                           const __bf16* vplane, const MomLane<NT, NX>& m, int li, int lg) {
   constexpr int CG = 16 * CT;
@@ -242,7 +243,7 @@ __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     vh[ct] = *reinterpret_cast<const bf16x8*>(vplane + vps_off(16 * ct + li, 4 * lg));
-    vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + CG * MOM_C + vps_off(16 * ct + li, 4 * lg));
+    if constexpr (!VX) vl[ct] = *reinterpret_cast<const bf16x8*>(vplane + CG * MOM_C + vps_off(16 * ct + li, 4 * lg));
   }
   // key reads two tiles ahead: set kt & 1 holds tile kt's, reloaded with tile kt + 2's once its feature
   // values are formed
@@ -277,8 +278,10 @@ __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[
     den_p[kt] += dacc;
     bf16x8 ah, al;
     split_bf16(x, ah, al);
+    if constexpr (!VX) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vl[ct], st[kt][ct]);
+      for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(ah, vl[ct], st[kt][ct]);
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) st[kt][ct] = mfma_bf16(al, vh[ct], st[kt][ct]);
 #pragma unroll
@@ -402,7 +405,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 // Staging of iteration c by one thread (keys / values of chunk c + 1, with WQ queries of chunk c, into
 // LDS from the registers, loads of slot c + 2 into them): the main loop's staging step, for the query
 // waves of a segment-totals pass, which only stage (keys and values: that pass has no queries).
-template <bool DBIG, int ES, int CG, int STG, bool WQ>
+template <bool DBIG, int ES, int CG, int STG, bool WQ, bool VX>
 __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, const WsSlots<DBIG, ES, CG, STG>& sl,
                                               const MomArgs& a, float* kvb, float* qb, int c, int nch, int first,
                                               const char* kh, const char* vh, const char* qh) {
@@ -412,7 +415,8 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, c
   const int q_row = first + c * MOM_C;
   if (c + 1 < nch) {
     float* Kt = kvb + ((c + 1) & 1) * KVF;
-    ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), kv_row);
+    ws_store_kv<DBIG, ES, CG, STG, true, VX>(pre, sl, a, Kt, reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT),
+                                             kv_row);
   }
   if (WQ && c < nch) ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
   ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
@@ -427,7 +431,7 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, c
 // the lane holds for tile 2 p (.xy) and tile 2 p + 1 (.zw); an odd last tile fills .xy only.  The
 // update wave writes its uint2 halves, the query wave loads whole operands.  The running denominators
 // go to LDS (den_lds[parity][slot][tile * 16 + feature]).
-template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT, bool TOT>
+template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT, bool TOT, bool VX>
 __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, int fs, int cs, int seg, int slot,
                                         int qw) {
   const MomArgs& a = wa.m;
@@ -564,7 +568,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   WsStage<DBIG, ES, CG, STG> pre;
   if constexpr (STAGE) {
     ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first);
-    ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT), first);
+    ws_store_kv<DBIG, ES, CG, STG, true, VX>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT),
+                                             first);
   }
   __syncthreads();
   if constexpr (STAGE) {
@@ -575,7 +580,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   if constexpr (!UPD && TOT) {
     // segment totals: the query waves stage the keys and values, with the same iterations and barriers
     for (int c = 0; c <= nch; ++c) {
-      ws_stage_step<DBIG, ES, CG, STG, false>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+      ws_stage_step<DBIG, ES, CG, STG, false, VX>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
       __syncthreads();
     }
     return;
@@ -593,9 +598,9 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           float* Kt = kvb + ((c + 1) & 1) * KVF;
           __bf16* vp = reinterpret_cast<__bf16*>(Kt + mom_krows(DBIG) * MOM_LDT);
           if (kv_row >= 0 && kv_row + MOM_C <= n)
-            ws_store_kv<DBIG, ES, CG, STG, false>(pre, sl, a, Kt, vp, kv_row);
+            ws_store_kv<DBIG, ES, CG, STG, false, VX>(pre, sl, a, Kt, vp, kv_row);
           else
-            ws_store_kv<DBIG, ES, CG, STG, true>(pre, sl, a, Kt, vp, kv_row);
+            ws_store_kv<DBIG, ES, CG, STG, true, VX>(pre, sl, a, Kt, vp, kv_row);
         }
         if (STAGE && c < nch) {
           float* Qs = qb + (c & 1) * QF;
@@ -646,7 +651,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     if constexpr (UPD) {
       if (c < nch) {
         const float* Kt = kvb + (c & 1) * KVF;
-        ws_update<NT, CT, NX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li, lg);
+        ws_update<NT, CT, NX, VX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li,
+                                  lg);
         if (!totals && (c + 1) % cpb == 0 && c + 1 < nch) {
           // the state the queries of block (c + 1) / cpb see -> handoff (parity of that block)
           const int par = ((c + 1) / cpb) & 1;
@@ -756,7 +762,9 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
 
 // Workgroup -> (head, feature split, column group): consecutive logical ids share an XCD, so a head's
 // workgroups share one L2 for its q / k / v rows.  Waves 0-3 update, 4-7 query.
-template <int NTS, int NX, bool DBIG, int ES, int CT, bool TOT>
+// VX: bf16 values (ES = 2, dtype BF16), exact in bf16: the update leaves out the product with their zero
+// lo plane (the state is that of the three-product form, bit for bit)
+template <int NTS, int NX, bool DBIG, int ES, int CT, bool TOT, bool VX>
 __global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs wa) {
   const MomArgs& a = wa.m;
   const int wg = xcd_remap(blockIdx.x, gridDim.x);
@@ -774,15 +782,15 @@ __global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs 
   if (w < 4) {
     const int slot = w;
     if (NTS > 1 && wa.mixed && slot >= 2)
-      ws_body<true, NTL, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, 0);
+      ws_body<true, NTL, NTS, NX, DBIG, ES, CT, TOT, VX>(wa, wg, bh, fs, cs, seg, slot, 0);
     else
-      ws_body<true, NTS, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, 0);
+      ws_body<true, NTS, NTS, NX, DBIG, ES, CT, TOT, VX>(wa, wg, bh, fs, cs, seg, slot, 0);
   } else {
     const int slot = (w - 4 + 2) & 3;
     if (NTS > 1 && wa.mixed && slot >= 2)
-      ws_body<false, NTL, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, w - 4);
+      ws_body<false, NTL, NTS, NX, DBIG, ES, CT, TOT, VX>(wa, wg, bh, fs, cs, seg, slot, w - 4);
     else
-      ws_body<false, NTS, NTS, NX, DBIG, ES, CT, TOT>(wa, wg, bh, fs, cs, seg, slot, w - 4);
+      ws_body<false, NTS, NTS, NX, DBIG, ES, CT, TOT, VX>(wa, wg, bh, fs, cs, seg, slot, w - 4);
   }
 }
 
