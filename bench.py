@@ -243,8 +243,8 @@ def main() -> int:
     if args.warmup is None:
         args.warmup = 8 if decode else (1 if flash else 2)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (heads shard with no "
-              f"communication across GPUs; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the heads shard with no "
+              f"communication across GPUs: one process per GPU runs its share of the heads)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
