@@ -309,16 +309,47 @@ __device__ __forceinline__ void ws_qload(WsQOps& o, int u, const float* Qs, cons
   }
 }
 
-// phi_q of token tt (4 features of the lane's quad) from loaded operands; dq += phi_q . den
+// phi_q of token tt (4 features of the lane's quad) from loaded operands
 template <int NX>
-__device__ __forceinline__ void ws_qfeat(float (&x)[4], float& dq, const WsQOps& o, int tt, const floatx4& dn, bool den) {
+__device__ __forceinline__ void ws_qfeat(float (&x)[4], const WsQOps& o, int tt) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     float y = o.a[tt] * o.b[tt][s];
     if (NX >= 1) y *= o.c[tt];
     if (NX >= 2) y *= o.e[tt];
     x[s] = y;
-    if (den) dq = fmaf(y, dn[s], dq);
+  }
+}
+
+// The frozen denominators of a slot as one more column tile of the query products: column 0 holds
+// them (lanes li = 0), the other 15 columns are zero, so phi_q . den comes out of the matrix cores in
+// column 0 of the tile (lanes li = 0, rows 4 lg + r) with the same split products as the numerators.
+// src: the slot's [NTS][16] denominators; the pair layout of ws_qpair_mma (features 4 lg .. 4 lg + 3 of
+// tiles 2 p and 2 p + 1), the odd tile's as in ws_qsingle_mma.
+template <int NT>
+__device__ __forceinline__ void ws_den_ops(bf16x8 (&dh)[NT / 2 > 0 ? NT / 2 : 1], bf16x8 (&dl)[NT / 2 > 0 ? NT / 2 : 1],
+                                           uint2& odh, uint2& odl, const float* src, int li, int lg) {
+  // every lane loads (in bounds, no branch), lanes li != 0 keep zeros
+  const bool on = li == 0;
+#pragma unroll
+  for (int p = 0; p < NT / 2; ++p) {
+    const floatx4 d0 = *reinterpret_cast<const floatx4*>(src + (2 * p) * 16 + 4 * lg);
+    const floatx4 d1 = *reinterpret_cast<const floatx4*>(src + (2 * p + 1) * 16 + 4 * lg);
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = on ? d0[j] : 0.f;
+      x[4 + j] = on ? d1[j] : 0.f;
+    }
+    split_bf16(x, dh[p], dl[p]);
+  }
+  if constexpr ((NT & 1) != 0) {
+    const floatx4 d0 = *reinterpret_cast<const floatx4*>(src + (NT - 1) * 16 + 4 * lg);
+    float x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = on ? d0[j] : 0.f;
+    split_pair(x[0], x[1], odh.x, odl.x);
+    split_pair(x[2], x[3], odh.y, odl.y);
   }
 }
 
@@ -395,9 +426,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
     const int tok = tid - (WS_REDUCERS - MOM_C);
     float dsum = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) dsum += red[q * WS + red_off(CG + g, tok)];
+    for (int q = 0; q < 4; ++q) dsum += red[q * WS + red_off(CG, tok)];
     __builtin_nontemporal_store(dsum, a.low_den + obase + row0 + tok);
   }
 }
@@ -491,6 +520,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   float den_p[UPD ? NT : 1];  // per-lane partial denominators (this lane's tokens)
   bf16x8 sh[UPD || NP == 0 ? 1 : NP][CT], sv[UPD || NP == 0 ? 1 : NP][CT];
   uint2 oh[CT], ov[CT];  // the odd last tile's operands
+  bf16x8 dh[UPD || NP == 0 ? 1 : NP], dl[UPD || NP == 0 ? 1 : NP];  // the denominators' column tile
+  uint2 odh = uint2{0u, 0u}, odl = uint2{0u, 0u};
   if constexpr (UPD) {
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
@@ -506,6 +537,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       for (int p = 0; p < NP; ++p) sh[p][ct] = sv[p][ct] = z;
       oh[ct] = ov[ct] = uint2{0u, 0u};
     }
+#pragma unroll
+    for (int p = 0; p < (NP > 0 ? NP : 1); ++p) dh[p] = dl[p] = z;
   }
 
   // zero every staging buffer (padding rows / columns are never written again) and the denominators of
@@ -552,10 +585,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           split_pair(s0[2], s0[3], oh[ct].y, ov[ct].y);
         }
       }
-      if (den && lg == 0) {
-#pragma unroll
-        for (int kt = 0; kt < NT; ++kt) denb[slot * NTS * 16 + kt * 16 + li] = sden[(slot * NTS + kt) * 16 + li];
-      }
+      if (den) ws_den_ops<NT>(dh, dl, odh, odl, sden + slot * NTS * 16, li, lg);
     }
   }
   // one register set of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is loaded
@@ -633,6 +663,9 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
                 ov[ct] = *reinterpret_cast<const uint2*>(hand_at(par, NT / 2, ct, 1));
               }
             }
+            // the block's denominators (written with the state, block parity): zero in a workgroup
+            // without the denominator column
+            ws_den_ops<NT>(dh, dl, odh, odl, denb + (((c / cpb) & 1) * 4 + slot) * NTS * 16, li, lg);
           }
         }
         // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
@@ -679,28 +712,26 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     } else {
       if (c >= 1) {
         const float* Qs = qb + ((c - 1) & 1) * QF;
-        const float* dnb = denb + ((((c - 1) / cpb) & 1) * 4 + slot) * NTS * 16 + 4 * lg;
-        floatx4 o[2][CT];
-        float dq[2] = {0.f, 0.f};
+        floatx4 o[2][CT], od[2][1];  // od: the denominators' column tile (column 0)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) o[tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+          od[tt][0] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
         // operands of the first two tiles; each pair's successor is loaded once its features are formed
         WsQOps op0, op1;
         ws_qload<NT, NX, LDQ>(op0, 0, Qs, m, li);
         if (NT > 1) ws_qload<NT, NX, LDQ>(op1, NT > 1 ? 1 : 0, Qs, m, li);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-          const floatx4 dn0 = *reinterpret_cast<const floatx4*>(dnb + 2 * p * 16);
-          const floatx4 dn1 = *reinterpret_cast<const floatx4*>(dnb + (2 * p + 1) * 16);
           bf16x8 ah[2], al[2];
           float x[2][8];
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
             float x0[4], x1[4];
-            ws_qfeat<NX>(x0, dq[tt], op0, tt, dn0, den);
-            ws_qfeat<NX>(x1, dq[tt], op1, tt, dn1, den);
+            ws_qfeat<NX>(x0, op0, tt);
+            ws_qfeat<NX>(x1, op1, tt);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               x[tt][j] = x0[j];
@@ -712,28 +743,31 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) split_bf16(x[tt], ah[tt], al[tt]);
           ws_qpair_mma<CT>(o, ah, al, sh[p], sv[p]);
+          const bf16x8 dhp[1] = {dh[p]}, dlp[1] = {dl[p]};
+          ws_qpair_mma<1>(od, ah, al, dhp, dlp);
         }
         if constexpr (ODD) {
-          const floatx4 dn = *reinterpret_cast<const floatx4*>(dnb + (NT - 1) * 16);
           uint2 ah[2], al[2];
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) {
             float x0[4];
-            ws_qfeat<NX>(x0, dq[tt], op0, tt, dn, den);
+            ws_qfeat<NX>(x0, op0, tt);
             split_pair(x0[0], x0[1], ah[tt].x, al[tt].x);
             split_pair(x0[2], x0[3], ah[tt].y, al[tt].y);
           }
           ws_qsingle_mma<CT>(o, ah, al, oh, ov);
+          const uint2 odhp[1] = {odh}, odlp[1] = {odl};
+          ws_qsingle_mma<1>(od, ah, al, odhp, odlp);
         }
-        // this wave's partials of chunk c - 1 -> red[(c - 1) & 1], column-major (red_off); columns
-        // CG + lg: the denominator sums of lane group lg
+        // this wave's partials of chunk c - 1 -> red[(c - 1) & 1], column-major (red_off); column CG:
+        // the denominator sums (column 0 of the denominators' tile, lanes li = 0)
         float* rw = redb + ((c - 1) & 1) * REDF + qw * (CG + WS_RCOLS_EXTRA) * MOM_LDR;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
             *reinterpret_cast<floatx4*>(rw + red_off(16 * ct + li, 16 * tt + 4 * lg)) = o[tt][ct];
-          if (den) rw[red_off(CG + lg, 16 * tt + li)] = dq[tt];
+          if (den && li == 0) *reinterpret_cast<floatx4*>(rw + red_off(CG, 16 * tt + 4 * lg)) = od[tt][0];
         }
       }
     }
