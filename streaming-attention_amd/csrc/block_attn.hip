@@ -627,8 +627,12 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // ---- epilogue: add the moment partials, normalise, store ----
   // The fsplit partials of a row are summed in the order f = 0, 1, ...  Every load of a group of
   // EPI_GROUP partials is issued before the first sum (a partial past fsplit re-reads the last one and
-  // is dropped; a column past dv reads column 0 and is not stored), so a group costs one round trip.
-  constexpr int EPI_GROUP = DVT <= 4 ? 8 : 32 / DVT;  // at most 128 registers of loads in flight
+  // is dropped; a column past dv reads column 0 and is not stored).  One partial per group: on c3 (32
+  // heads x 65536, 8 partials per row) the kernel takes 2.76-2.80 ms against 2.87-2.96 ms with all 8
+  // loads in flight per row (same sums, bit for bit): the partial reads are 4.4 GB, as much HBM time as
+  // the rest of the kernel's wait, and fewer loads in flight per wave leave the other workgroups' gathers
+  // less queued behind them.
+  constexpr int EPI_GROUP = 1;
   const bool raw = a.out_den != nullptr;
   const int fs = a.fsplit;
   const int64_t pden_stride = a.low_rows, pnum_stride = a.low_rows * a.low_ld;
