@@ -464,6 +464,24 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   // and which of them are real (row of the batch, column inside the row)
   constexpr int KU = DP / 4, VU = DV / 4;
   constexpr int KPT = block_kpt(DP, DVT), VPT = block_vpt(DP, DVT);
+  // value units in key pairs (split products, an even count of units per thread covering the batch
+  // exactly): units 2 k and 2 k + 1 of a thread are keys 2 rp and 2 rp + 1 of one column unit, which sit
+  // next to each other in the value planes (split_key_pos), so the commit splits them as packed pairs
+  // and writes 32-bit words; otherwise key-fast single units
+  constexpr bool VPAIR = SPLIT && VPT % 2 == 0 && KB * VU == 256 * VPT;
+  auto vunit = [&](int i, int& r, int& u) -> bool {
+    if constexpr (VPAIR) {
+      const int pe = tid + 256 * (i >> 1);
+      r = 2 * (pe % (KB / 2)) + (i & 1);
+      u = pe / (KB / 2);
+      return true;
+    } else {
+      const int e = tid + 256 * i;
+      r = e % KB;  // key-fast: conflict-light transposed writes
+      u = e / KB;
+      return e < KB * VU;
+    }
+  };
   uint4 pk[KPT], pv[VPT];
   uint32_t pk_ok = 0, pv_ok = 0;
   int pj = -1, plo = 0, phi = -1;
@@ -501,9 +519,9 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int e = tid + 256 * i;
-      const int r = e % KB, u = e / KB;  // key-fast: conflict-light transposed writes
-      const int src = (e < KB * VU) ? src_of(node, off, r) : -1;
+      int r, u;
+      const bool in = vunit(i, r, u);
+      const int src = in ? src_of(node, off, r) : -1;
       const bool ok = src >= 0 && 4 * u < ldv;
       pv_ok |= ok ? (1u << i) : 0u;
       pv[i] = load_unit<ES>(vb, vbase2 + static_cast<int64_t>(src >= 0 ? src : 0) * ldv + min(4 * u, ldv - 4));
@@ -534,18 +552,39 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           if constexpr (!KVX) *reinterpret_cast<uint2*>(Kl + r * LDKB + 4 * u) = uint2{l0, l1};
         }
       }
+      if constexpr (VPAIR) {
 #pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int e = tid + 256 * i;
-        if (e < KB * VU) {
-          const int r = e % KB, u = e / KB;
-          const floatx4 f = unit_to_f4<ES>(pv[i], a.dtype, ((pv_ok >> i) & 1u) ? 1.f : 0.f);
-          const int pos = split_key_pos(r);
+        for (int k = 0; k < VPT / 2; ++k) {
+          int r, u;
+          vunit(2 * k, r, u);
+          const floatx4 f0 = unit_to_f4<ES>(pv[2 * k], a.dtype, ((pv_ok >> (2 * k)) & 1u) ? 1.f : 0.f);
+          const floatx4 f1 = unit_to_f4<ES>(pv[2 * k + 1], a.dtype, ((pv_ok >> (2 * k + 1)) & 1u) ? 1.f : 0.f);
+          const int pos = split_key_pos(r);  // even: key r + 1 at pos + 1
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
-            const __bf16 h = static_cast<__bf16>(f[m]);
-            Vh[(4 * u + m) * LDVB + pos] = h;
-            if constexpr (!KVX) Vl[(4 * u + m) * LDVB + pos] = static_cast<__bf16>(f[m] - static_cast<float>(h));
+            uint32_t h, l;
+            if constexpr (KVX) {
+              h = pk_bf16(f0[m], f1[m]);  // exact bf16 values: the lo plane is zero and not kept
+            } else {
+              split_pair(f0[m], f1[m], h, l);
+              *reinterpret_cast<uint32_t*>(Vl + (4 * u + m) * LDVB + pos) = l;
+            }
+            *reinterpret_cast<uint32_t*>(Vh + (4 * u + m) * LDVB + pos) = h;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+          int r, u;
+          if (vunit(i, r, u)) {
+            const floatx4 f = unit_to_f4<ES>(pv[i], a.dtype, ((pv_ok >> i) & 1u) ? 1.f : 0.f);
+            const int pos = split_key_pos(r);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+              const __bf16 h = static_cast<__bf16>(f[m]);
+              Vh[(4 * u + m) * LDVB + pos] = h;
+              if constexpr (!KVX) Vl[(4 * u + m) * LDVB + pos] = static_cast<__bf16>(f[m] - static_cast<float>(h));
+            }
           }
         }
       }
