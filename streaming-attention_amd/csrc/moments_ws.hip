@@ -82,6 +82,10 @@ struct WsStage {
   static constexpr int QV = (QU + STG - 1) / STG;
   static constexpr int VU = MOM_C * CG * ES / 16;
   static constexpr int VV = (VU + STG - 1) / STG;
+  // token pairs (fp32 rows, two key and two value units per thread): units 0 and 1 are one 16-byte
+  // unit of tokens 2 p and 2 p + 1, which sit next to each other in the transposed key rows and the
+  // value planes, so the stores are 8-byte key pairs and packed 32-bit bf16 pairs
+  static constexpr bool PAIR = !DBIG && ES == 4 && QV == 2 && VV == 2 && QU == 2 * STG && VU == 2 * STG;
   uint4 q[QV];
   uint4 k[QV];
   uint4 v[VV];
@@ -110,6 +114,7 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
   const int tid = sidx;
   sl.sidx = sidx;
   const int uq = a.d / epu;
+  constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int e = tid + STG * j;
@@ -118,13 +123,13 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
     sl.q_tok[j] = min(t, MOM_C - 1);
     sl.q_off[j] = static_cast<uint32_t>(u * 16);
     sl.q_lds[j] = t * LDQ + u * epu;
-    const int uk = e >> 5;
+    const int uk = PAIR ? tid >> 4 : e >> 5;
     sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
     sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j) {
-    const int uv = (tid + STG * j) >> 5;
+    const int uv = PAIR ? tid >> 4 : (tid + STG * j) >> 5;
     sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
     sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
   }
@@ -146,15 +151,19 @@ __device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG, STG>& st, const 
 template <bool DBIG, int ES, int CG, int STG, bool MASK>
 __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                            const MomArgs& a, const char* kh, const char* vh, int row0) {
+  constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
   const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
-  const int t = row0 + (sl.sidx & (MOM_C - 1));
-  const uint32_t r = static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
+  // the token of unit j: one per thread, or the pair 2 p, 2 p + 1
+  auto row = [&](int j) -> uint32_t {
+    const int t = row0 + (PAIR ? 2 * (sl.sidx & 15) + j : sl.sidx & (MOM_C - 1));
+    return static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
+  };
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j)
-    st.k[j] = *reinterpret_cast<const uint4*>(kh + r * krow_b + sl.k_off[j]);
+    st.k[j] = *reinterpret_cast<const uint4*>(kh + row(j) * krow_b + sl.k_off[j]);
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j)
-    st.v[j] = *reinterpret_cast<const uint4*>(vh + r * vrow_b + sl.v_off[j]);
+    st.v[j] = *reinterpret_cast<const uint4*>(vh + row(j) * vrow_b + sl.v_off[j]);
 }
 
 // An empty use of every staged register: the compiler completes their loads before it (where the
@@ -198,8 +207,32 @@ template <bool DBIG, int ES, int CG, int STG, bool MASK, bool VX = false>
 __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                             const MomArgs& a, float* Kt, __bf16* vplane, int row0) {
   constexpr bool wide = ES == 2;
+  auto in_seq = [&](int t) { return (!MASK || (row0 + t >= 0 && row0 + t < a.n)) ? 1.f : 0.f; };
+  if constexpr (WsStage<DBIG, ES, CG, STG>::PAIR) {
+    const int t0 = 2 * (sl.sidx & 15);
+    const float ok0 = in_seq(t0), ok1 = in_seq(t0 + 1);
+    const int kd = sl.k_dim[0];
+    if (kd >= 0) {
+      const floatx4 f0 = __builtin_bit_cast(floatx4, st.k[0]), f1 = __builtin_bit_cast(floatx4, st.k[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) *reinterpret_cast<floatx2*>(Kt + (kd + m) * MOM_LDT + t0) = floatx2{f0[m] * ok0, f1[m] * ok1};
+    }
+    const int c0 = sl.v_col[0];
+    if (c0 >= 0) {
+      const floatx4 f0 = __builtin_bit_cast(floatx4, st.v[0]), f1 = __builtin_bit_cast(floatx4, st.v[1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        uint32_t h, l;
+        split_pair(f0[m] * ok0, f1[m] * ok1, h, l);
+        *reinterpret_cast<uint32_t*>(vplane + vps_off(c0 + m, t0)) = h;  // t0 even: t0 + 1 is the next bf16
+        if constexpr (!VX) *reinterpret_cast<uint32_t*>(vplane + CG * MOM_C + vps_off(c0 + m, t0)) = l;
+      }
+    }
+    if (sl.sidx < MOM_C) Kt[a.d * MOM_LDT + sl.sidx] = in_seq(sl.sidx);
+    return;
+  }
   const int tok = sl.sidx & (MOM_C - 1);
-  const float kok = (!MASK || (row0 + tok >= 0 && row0 + tok < a.n)) ? 1.f : 0.f;
+  const float kok = in_seq(tok);
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int kd = sl.k_dim[j];
