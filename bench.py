@@ -222,8 +222,8 @@ def cpu_baseline(q, k, v, w):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 10; decode 256)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed steps first (default 2; decode 8)")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default: prefill >= 10 steps and >= 0.3 s of GPU time; decode 256; flash 3)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps first (default: prefill >= 0.2 s of GPU time; decode 8; flash 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seq-len", type=int, default=None, help="override the prefill workload's N")
     ap.add_argument("--heads", type=int, default=None, help="override the prefill workload's heads")
@@ -238,6 +238,10 @@ def main() -> int:
     args = ap.parse_args()
     decode = args.workload == DECODE["workload"]
     flash = args.workload == FLASH["workload"]
+    # prefill without --steps / --warmup: sized from a measured step (warm-up >= 0.2 s of GPU time, the
+    # timed region >= 0.3 s and at least 10 steps), so a small workload is timed at steady clocks
+    args.auto_steps = args.steps is None and not (decode or flash)
+    args.auto_warmup = args.warmup is None and not (decode or flash)
     if args.steps is None:
         args.steps = 256 if decode else (3 if flash else 10)
     if args.warmup is None:
@@ -302,7 +306,22 @@ def main() -> int:
     api_out = api(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"],
                   compressor=w["compressor"], seed=w["seed"])
     res = step()
-    for _ in range(args.warmup - 1):
+    if args.auto_steps or args.auto_warmup:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(2):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        est_s = max(e0.elapsed_time(e1) / 2e3, 1e-6)
+        if args.auto_warmup:
+            args.warmup = max(args.warmup, 3 + math.ceil(0.2 / est_s))
+        if args.auto_steps:
+            args.steps = min(2000, max(args.steps, math.ceil(0.3 / est_s)))
+        done = 3
+    else:
+        done = 1
+    for _ in range(args.warmup - done):
         step()
     torch.cuda.synchronize()
     assert torch.equal(res.out.reshape(api_out.shape), api_out)
@@ -383,6 +402,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "steps_rule": ("sized from a measured step: warm-up >= 0.2 s, timed region >= 0.3 s of GPU time and >= 10 "
+                       "steps" if args.auto_steps else "as given"),
         "ms_per_step": ms_step,
         "higher_is_better": True,
         "scaling": "weak",
