@@ -86,6 +86,9 @@ struct WsStage {
   // unit of tokens 2 p and 2 p + 1, which sit next to each other in the transposed key rows and the
   // value planes, so the stores are 8-byte key pairs and packed 32-bit bf16 pairs
   static constexpr bool PAIR = !DBIG && ES == 4 && QV == 2 && VV == 2 && QU == 2 * STG && VU == 2 * STG;
+  // the same for 16-bit rows (one key and one value unit per thread): 8-byte half units (4 elements) of
+  // tokens 2 p and 2 p + 1 held in one register set, {token 2 p: elements 0..3, token 2 p + 1: 0..3}
+  static constexpr bool PAIR16 = !DBIG && ES == 2 && QV == 1 && VV == 1 && QU == STG && VU == STG;
   uint4 q[QV];
   uint4 k[QV];
   uint4 v[VV];
@@ -115,6 +118,7 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
   sl.sidx = sidx;
   const int uq = a.d / epu;
   constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
+  constexpr bool PAIR16 = WsStage<DBIG, ES, CG, STG>::PAIR16;
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int e = tid + STG * j;
@@ -123,15 +127,27 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
     sl.q_tok[j] = min(t, MOM_C - 1);
     sl.q_off[j] = static_cast<uint32_t>(u * 16);
     sl.q_lds[j] = t * LDQ + u * epu;
-    const int uk = PAIR ? tid >> 4 : e >> 5;
-    sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
-    sl.k_dim[j] = uk < uq ? uk * epu : -1;
+    if constexpr (PAIR16) {  // half unit tid >> 4: elements 4 hu .. 4 hu + 3
+      const int hu = tid >> 4;
+      sl.k_off[j] = static_cast<uint32_t>(min(hu, a.d / 4 - 1) * 8);
+      sl.k_dim[j] = 4 * hu < a.d ? 4 * hu : -1;
+    } else {
+      const int uk = PAIR ? tid >> 4 : e >> 5;
+      sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
+      sl.k_dim[j] = uk < uq ? uk * epu : -1;
+    }
   }
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j) {
-    const int uv = PAIR ? tid >> 4 : (tid + STG * j) >> 5;
-    sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
-    sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
+    if constexpr (PAIR16) {
+      const int hu = tid >> 4;
+      sl.v_off[j] = static_cast<uint32_t>((col0 + min(4 * hu, CG - 4)) * ES);
+      sl.v_col[j] = 4 * hu < CG ? 4 * hu : -1;
+    } else {
+      const int uv = PAIR ? tid >> 4 : (tid + STG * j) >> 5;
+      sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
+      sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
+    }
   }
   return sl;
 }
@@ -152,12 +168,22 @@ template <bool DBIG, int ES, int CG, int STG, bool MASK>
 __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                            const MomArgs& a, const char* kh, const char* vh, int row0) {
   constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
+  constexpr bool PAIR16 = WsStage<DBIG, ES, CG, STG>::PAIR16;
   const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
   // the token of unit j: one per thread, or the pair 2 p, 2 p + 1
   auto row = [&](int j) -> uint32_t {
-    const int t = row0 + (PAIR ? 2 * (sl.sidx & 15) + j : sl.sidx & (MOM_C - 1));
+    const int t = row0 + (PAIR || PAIR16 ? 2 * (sl.sidx & 15) + j : sl.sidx & (MOM_C - 1));
     return static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
   };
+  if constexpr (PAIR16) {
+    const uint2 k0 = *reinterpret_cast<const uint2*>(kh + row(0) * krow_b + sl.k_off[0]);
+    const uint2 k1 = *reinterpret_cast<const uint2*>(kh + row(1) * krow_b + sl.k_off[0]);
+    const uint2 v0 = *reinterpret_cast<const uint2*>(vh + row(0) * vrow_b + sl.v_off[0]);
+    const uint2 v1 = *reinterpret_cast<const uint2*>(vh + row(1) * vrow_b + sl.v_off[0]);
+    st.k[0] = uint4{k0.x, k0.y, k1.x, k1.y};
+    st.v[0] = uint4{v0.x, v0.y, v1.x, v1.y};
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j)
     st.k[j] = *reinterpret_cast<const uint4*>(kh + row(j) * krow_b + sl.k_off[j]);
@@ -225,6 +251,34 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
         uint32_t h, l;
         split_pair(f0[m] * ok0, f1[m] * ok1, h, l);
         *reinterpret_cast<uint32_t*>(vplane + vps_off(c0 + m, t0)) = h;  // t0 even: t0 + 1 is the next bf16
+        if constexpr (!VX) *reinterpret_cast<uint32_t*>(vplane + CG * MOM_C + vps_off(c0 + m, t0)) = l;
+      }
+    }
+    if (sl.sidx < MOM_C) Kt[a.d * MOM_LDT + sl.sidx] = in_seq(sl.sidx);
+    return;
+  }
+  if constexpr (WsStage<DBIG, ES, CG, STG>::PAIR16) {
+    const int t0 = 2 * (sl.sidx & 15);
+    const float ok0 = in_seq(t0), ok1 = in_seq(t0 + 1);
+    const int kd = sl.k_dim[0];
+    if (kd >= 0) {
+      float f[8];  // token t0: f[0..3], token t0 + 1: f[4..7]
+      unit_floats<ES>(st.k[0], a.dtype, f);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) *reinterpret_cast<floatx2*>(Kt + (kd + m) * MOM_LDT + t0) = floatx2{f[m] * ok0, f[4 + m] * ok1};
+    }
+    const int c0 = sl.v_col[0];
+    if (c0 >= 0) {
+      float f[8];
+      unit_floats<ES>(st.v[0], a.dtype, f);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        uint32_t h, l = 0u;
+        if constexpr (VX)
+          h = pk_bf16(f[m] * ok0, f[4 + m] * ok1);  // exact bf16 values: no lo plane
+        else
+          split_pair(f[m] * ok0, f[4 + m] * ok1, h, l);
+        *reinterpret_cast<uint32_t*>(vplane + vps_off(c0 + m, t0)) = h;
         if constexpr (!VX) *reinterpret_cast<uint32_t*>(vplane + CG * MOM_C + vps_off(c0 + m, t0)) = l;
       }
     }
