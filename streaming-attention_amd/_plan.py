@@ -15,6 +15,7 @@ The projection direction is normalised with the same torch ops as the reference
 
 from __future__ import annotations
 
+import heapq
 import itertools
 import math
 import threading
@@ -70,10 +71,54 @@ def _factorial_inverse(combo: Tuple[int, ...]) -> float:
 
 # ----------------------------------------------------------------------------- feature tiles
 
+
+def _window_cover(d: int, deg: int) -> List[Tuple[Tuple[Tuple[int, ...], int], List[Tuple[int, ...]]]]:
+    """The degree-`deg` monomials in x[0..d) assigned to quad windows: a window (fixed, m) holds the 4
+    monomials fixed + (v,) for v in [4 m, 4 m + 4) (fixed: deg - 1 non-decreasing factors), the form a
+    quad of the moment kernel reads (the shared factors and one aligned 4-element block).  Every
+    monomial lies in up to deg windows (its value in each factor position as the varying one); the cover
+    takes windows greedily by the number of still uncovered monomials they hold (ties: the smallest key),
+    which leaves fewer padding slots than one row per prefix when the rows are short (d = 16, degree 3:
+    208 windows for 816 monomials against 260 rows' quads)."""
+    mons = list(itertools.combinations_with_replacement(range(d), deg))
+    wins: Dict[Tuple[Tuple[int, ...], int], List[int]] = {}
+    mon_w: List[List[Tuple[Tuple[int, ...], int]]] = [[] for _ in mons]
+    for i, mono in enumerate(mons):
+        seen = set()
+        for t in range(deg):
+            key = (mono[:t] + mono[t + 1:], mono[t] // 4)
+            if key in seen:
+                continue
+            seen.add(key)
+            wins.setdefault(key, []).append(i)
+            mon_w[i].append(key)
+    cnt = {k: len(v) for k, v in wins.items()}
+    heap = [(-c, k) for k, c in cnt.items()]
+    heapq.heapify(heap)
+    covered = [False] * len(mons)
+    out = []
+    while heap:
+        negc, key = heapq.heappop(heap)
+        c = cnt[key]
+        if c == 0:
+            continue
+        if -negc != c:  # stale entry: requeue with the current count
+            heapq.heappush(heap, (-c, key))
+            continue
+        got = [i for i in wins[key] if not covered[i]]
+        for i in got:
+            covered[i] = True
+            for k2 in mon_w[i]:
+                cnt[k2] -= 1
+        out.append((key, [mons[i] for i in got]))
+    assert all(covered)
+    return out
+
 MOM_WAVES = 4  # waves per moment workgroup (sta_moments)
 OCC2_SPEEDUP = 1.2  # per-tile throughput of two resident moment workgroups per CU vs one
 WIDE_COST = 1.2  # time per tile of a 64-column workgroup (split products) vs a 32-column one alone
 MOM_MAX_WAVE_TILES = 16  # largest per-wave tile count the kernel is instantiated for
+COVER_MAX_MONOMIALS = 200_000  # largest degree-3 / 4 monomial set packed by the window cover
 
 
 @dataclass(frozen=True)
@@ -146,15 +191,29 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
         if degree >= 2:
             for a in range(d):
                 add_row((a,), a, d, False)
-        if degree >= 3:
-            for a in range(d):
-                for b2 in range(a, d):
-                    add_row((a, b2), b2, d, False)
-        if degree >= 4:
-            for a in range(d):
-                for b2 in range(a, d):
-                    for b3 in range(b2, d):
-                        add_row((a, b2, b3), b3, d, False)
+        # degrees 3 and 4: the window cover (fewer padding slots than rows cut at multiples of 4); rows
+        # for very large sets (degree 4 at d = 64: 0.77 M monomials, where the greedy cover takes
+        # seconds of host time per process)
+        for deg in range(3, degree + 1):
+            if math.comb(d + deg - 1, deg) > COVER_MAX_MONOMIALS:
+                for pre in itertools.combinations_with_replacement(range(d), deg - 1):
+                    add_row(pre, pre[-1], d, False)
+                continue
+            for (fixed, m), got in _window_cover(d, deg):
+                mine = set(got)
+                ids = list(fixed) + [one] * (3 - len(fixed))
+                cs = []
+                for s in range(4):
+                    mono = tuple(sorted(fixed + (4 * m + s,))) if 4 * m + s < d else None
+                    if mono is not None and mono in mine:
+                        cs.append(_factorial_inverse(mono))
+                        slot_combos.append(mono)
+                        count += 1
+                    else:  # padding, or a monomial another window holds
+                        cs.append(0.0)
+                        slot_combos.append(None)
+                quads.append(ids[0] | ((4 * m) << 8) | (ids[1] << 16) | (ids[2] << 24))
+                coefs.append(cs)
         # Tiles: first every run of 4 quads that share (b, i2, i3) and take 4 consecutive first factors
         # i0 = 4k .. 4k+3, then the remaining quads in row order.  In the kernel's update a tile's 16
         # lanes then read 4 distinct key rows per factor (x[i0] by quad, x[b + s] by slot), a pattern the
