@@ -2,6 +2,7 @@
 the header declares; the seed-derived draws the product replays equal the reference's; level-tree
 plans follow the reference's cascade; the Python API raises the reference's exceptions."""
 
+import itertools
 import pathlib
 import re
 
@@ -416,3 +417,25 @@ def test_completion_calls_follow_the_level_plan(block, comp):
     for b in range(c):
         sizes += _plan.completion_call_sizes(b, block, comp)
     assert sizes == _plan.levels_plan(c * block, block, comp).call_sizes
+
+
+@pytest.mark.parametrize("d,deg", [(16, 3), (32, 3), (5, 3), (16, 4), (6, 4)])
+def test_window_cover_holds_every_monomial_once_in_fewer_quads(d, deg):
+    """The degree-3 / 4 window cover: every monomial of the degree (the oracle's list) in exactly one
+    window, each window a quad the kernel can read (deg - 1 shared factors, one aligned 4-element
+    block), and no more windows than rows cut at multiples of 4 (the packing it replaced)."""
+    cover = _plan._window_cover(d, deg)
+    held = [m for _, got in cover for m in got]
+    assert sorted(held) == sorted(m for m in orc.monomials(d, deg) if len(m) == deg)
+    assert len(held) == len(set(held))
+    for (fixed, m), got in cover:
+        assert len(fixed) == deg - 1 and list(fixed) == sorted(fixed) and 1 <= len(got) <= 4
+        for mono in got:
+            rest = list(mono)
+            for f in fixed:
+                rest.remove(f)
+            assert len(rest) == 1 and rest[0] // 4 == m
+    rows = sum((d - 4 * (pre[-1] // 4)) // 4 for pre in itertools.combinations_with_replacement(range(d), deg - 1))
+    assert len(cover) <= rows
+    if (d, deg) == (16, 3):
+        assert len(cover) == 208 and _plan.feature_tiles(16, 3).n_tiles == 64
