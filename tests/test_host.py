@@ -435,7 +435,7 @@ def test_window_cover_holds_every_monomial_once_in_fewer_quads(d, deg):
             for f in fixed:
                 rest.remove(f)
             assert len(rest) == 1 and rest[0] // 4 == m
-    rows = sum((d - 4 * (pre[-1] // 4)) // 4 for pre in itertools.combinations_with_replacement(range(d), deg - 1))
+    rows = sum(-(-(d - 4 * (pre[-1] // 4)) // 4) for pre in itertools.combinations_with_replacement(range(d), deg - 1))
     assert len(cover) <= rows
     if (d, deg) == (16, 3):
         assert len(cover) == 208 and _plan.feature_tiles(16, 3).n_tiles == 64
