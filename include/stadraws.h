@@ -39,6 +39,15 @@ void sta_draws_close(void* handle);
 int sta_draws_next(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
                    float* dirs, float* unif, int32_t* perms);
 
+/* The same with the directions and uniforms drawn as float64 when f64 = 1 (dirs / unif are double
+ * tables): the reference draws them in the keys' dtype (fast_article_attention.py:339, :348;
+ * streaming_taylor_coreset_attention.py:441, :456), so a float64 caller's draws come from torch's double
+ * sampling path.  f64 = 0 is sta_host_draws / sta_draws_next (float tables). */
+int sta_host_draws_typed(const int64_t* seeds, int n_seq, const int32_t* call_sizes, int n_calls, int d,
+                         int compressor, int max_in, int f64, void* dirs, void* unif, int32_t* perms);
+int sta_draws_next_typed(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
+                         int f64, void* dirs, void* unif, int32_t* perms);
+
 /* Generator states in torch.Generator.get_state()'s CPU layout: out / in are [n_seq, state_bytes]. */
 int64_t sta_draws_state_bytes(void);
 int sta_draws_get_state(void* handle, uint8_t* out);

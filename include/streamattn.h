@@ -38,6 +38,7 @@ extern "C" {
 #define STA_F32 0
 #define STA_BF16 1
 #define STA_F16 2
+#define STA_F64 3 /* sta_compress_nodes only: float64 keys scored in fp64 against float64 draws */
 
 #define STA_PRODUCTS_FP32 0       /* matrix-core products in fp32                                 */
 #define STA_PRODUCTS_SPLIT_BF16 1 /* fp32 operands as bf16 hi + lo, three bf16 products            */
@@ -51,7 +52,8 @@ const char* sta_status_string(int status);
 /* hipError_t of the last failing HIP call made by this library on this thread (0 if none). */
 int sta_last_hip_error(void);
 
-/* Kernel limits: max D, max Dv, max Taylor degree, max compressor input size. */
+/* Kernel limits: max D, max Dv, max Taylor degree, max compressor input size.  Within them: degree
+ * 5 .. 8 needs D <= 64; the exact flash baseline (sta_flash_attention) takes D <= 128. */
 int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
 
 /*
@@ -71,9 +73,19 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *     sum (e.g. 1/2 on every slot of a diagonal tile x[4k+r] x[4k+s]; the planner's
  *     tile_coefficients).  wave_tiles must be a count the library is built for
  *     (sta_moment_wave_tiles).
- *   q and k rows are d elements long and v rows ldv (a multiple of 32, >= dv); rows are read in
+ *   q and k rows are ld_qk elements apart and v rows ldv (a multiple of 32, >= dv); rows are read in
  *     16-byte units, so d times the element size must be a multiple of 16 (pad rows with zero columns
  *     otherwise: zero dimensions only add zero-valued features), and q, k, v must be 16-byte aligned.
+ *   d is the staged key width (at most 128).  windows == NULL: rows are d long (ld_qk == d) and the
+ *     feature indices are dimensions.  Keys wider than 128 (ld_qk a multiple of 32, 128 <= ld_qk <= 256,
+ *     degree <= 4) go through dimension windows: windows [fsplit][4] (device, int32) gives, for every
+ *     feature split, the first row dimension of its 4 blocks of 32 dimensions (entries clamped to
+ *     [0, ld_qk - 32]); the split stages d = 128 "virtual" dimensions 32 b + j = row dimension
+ *     windows[4 fs + b] + j, and its feature quads index those virtual dimensions (the planner assigns
+ *     every monomial to one split whose window holds its dimensions).
+ *   Degrees 5 .. 8 (d <= 64): STA_PRODUCTS_FP32 and 32 columns only; each quad is then two words,
+ *     i0 | b<<8 | i2<<16 | i3<<24 and i4 | i5<<8 | i6<<16 | i7<<24 (feat_quads [fsplit][4][wave_tiles][4][2]),
+ *     the features x[i0] x[b+s] x[i2] ... x[i7] (unused factors = d).
  *   grid: bh * fsplit * ceil(dv/columns) workgroups of 256 threads.
  *   products: STA_PRODUCTS_FP32 (fp32 matrix cores; products of the fp32 features exact) or
  *     STA_PRODUCTS_SPLIT_BF16 (each fp32 operand as bf16 hi + lo, three bf16 matrix-core products per
@@ -84,10 +96,10 @@ int sta_limits(int* max_d, int* max_dv, int* max_degree, int* max_compress_in);
  *   outputs (fp32, partial over feature splits), in the layout sta_moment_partials_layout gives:
  *     low_num [BH][fsplit][rows][ld], low_den [BH][fsplit][rows], row i stored at row_offset + i.
  */
-int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
-                int products, int columns, const uint32_t* feat_quads, const float* feat_coef, float* low_num,
-                float* low_den, void* stream);
+int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int ld_qk,
+                int dv, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
+                int products, int columns, const uint32_t* feat_quads, const float* feat_coef,
+                const int32_t* windows, float* low_num, float* low_den, void* stream);
 
 /*
  * Wave-specialised form of sta_moments (split-bf16 products, degree <= 3): moments over all keys before
@@ -153,8 +165,10 @@ int sta_moment_wave_tiles(int d, int degree, int want);
  * (head, split) including guard rows, row stride of low_num, and the storage row of sequence row 0. */
 int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* row_offset);
 
-/* Moment workgroups the kernel keeps resident per compute unit at (d, per-wave tile count): 1 or 2. */
+/* Moment workgroups the kernel keeps resident per compute unit at (d, per-wave tile count): 1 or 2
+ * (degree <= 4; sta_moment_occupancy_degree for any degree). */
 int sta_moment_occupancy(int d, int wave_tiles);
+int sta_moment_occupancy_degree(int d, int degree, int wave_tiles);
 
 /*
  * Persistent moment state update (the decode state; K1's update without the query):
@@ -166,14 +180,15 @@ int sta_moment_occupancy(int d, int wave_tiles);
  *   [fsplit][4][wave_tiles][16]: the state row of every feature slot in the reference's feature order
  *   (degree 0, 1, ..., each in combinations_with_replacement order), -1 for padding slots.
  *   state_num [BH][n_feat][ld] with ld = 32*ceil(dv/32), state_den [BH][n_feat], fp32, accumulated in
- *   place.  k / v row rules as for sta_moments (16-byte units, ldv a multiple of 32).
+ *   place.  k / v row rules, ld_k and windows (keys wider than 128) as for sta_moments' q / k.
  *   products: STA_PRODUCTS_FP32 or STA_PRODUCTS_SPLIT_BF16 (as for sta_moments; the state and the
- *   sums stay fp32 either way).
+ *   sums stay fp32 either way; degrees 5 .. 8 need STA_PRODUCTS_FP32).
  */
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
-                          int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
-                          const float* feat_coef, const int32_t* feat_rows, int n_feat, int products,
-                          float* state_num, float* state_den, void* stream);
+                          int ld_k, int dv, int ldv, int degree, int fsplit, int wave_tiles,
+                          const uint32_t* feat_quads, const float* feat_coef, const int32_t* feat_rows,
+                          const int32_t* windows, int n_feat, int products, float* state_num, float* state_den,
+                          void* stream);
 
 /*
  * Streaming decode (K5) for S streams in lockstep: ArticleStreamingAttention.update / query
@@ -187,18 +202,20 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
  * part lives in their exact exponential instead of the moments).
  */
 
-/* Row lengths of the decode buffers: dk = 4*ceil(d/4), ldv = 32*ceil(dv/32). */
+/* Row lengths of the decode buffers: dk = 4*ceil(d/4) (32*ceil(d/32) for d > 128), ldv = 32*ceil(dv/32). */
 int sta_decode_layout(int d, int dv, int* dk, int* ldv);
 
 /*
  * Moment part of a decode query: part_num[s][p][c] = sum over features f of split p of
  * phi_q(scale*q_s)[f] state_num[s][f][c] (part_den likewise), splits = feature splits per stream.
- * feat_index [F]: factors of feature f packed i0 | i1 << 8 | i2 << 16 | i3 << 24 into x = [scale*q, 1]
- * (index d is the constant 1 and fills the unused factors).  Replaces TaylorMomentSketch.query (streaming_taylor_coreset_attention.py:282-296).
+ * feat_index: the factors of every feature into x = [scale*q, 1] (index d is the constant 1 and fills
+ * the unused factors); index_width 4: uint32 [F] packed i0 | i1 << 8 | i2 << 16 | i3 << 24 (d < 255,
+ * degree <= 4); index_width 8: uint16 [F][8] (d <= 256, degree <= 8).
+ * Replaces TaylorMomentSketch.query (streaming_taylor_coreset_attention.py:282-296).
  */
 int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv, float scale, const float* state_num,
-                       const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* part_num,
-                       float* part_den, void* stream);
+                       const float* state_den, int n_feat, const void* feat_index, int index_width, int splits,
+                       float* part_num, float* part_den, void* stream);
 
 /*
  * Buffer append and query of a decode step.  flags: 1 APPEND (write k, v [S][d|dv] into buffer slot
@@ -230,8 +247,8 @@ int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int6
 int64_t sta_static_scratch_bytes(void);
 int sta_decode_step_static(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
                            int degree, float scale, float eps, int flags, const float* state_num,
-                           const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* buf_k,
-                           float* buf_v, int block, int buf_len, const float* lev_k, const float* lev_v,
+                           const float* state_den, int n_feat, const void* feat_index, int index_width, int splits,
+                           float* buf_k, float* buf_v, int block, int buf_len, const float* lev_k, const float* lev_v,
                            const float* lev_w, int n_levels, int level_size, uint64_t level_mask, void* out,
                            int out_dtype, float* stats, void* stream);
 
@@ -242,11 +259,16 @@ int sta_decode_step_static(const void* q, const void* k, const void* v, int dtyp
  * [S][n_calls][d], unif [S][n_calls][max_in/2], perms [S][n_calls][max_in] as for sta_compress_nodes;
  * pos0 = sequence position of buffer row 0.  Replaces MergeReduceCoreset.append's compression and
  * _insert_level (streaming_taylor_coreset_attention.py:387-467).
+ *   score_f64 = 1 (a float64 caller, whose reference runs its compress calls in float64): dirs and unif
+ *   are double, and the projection scores are taken in fp64 from buf_k64 [S][block][dk] / lev_k64
+ *   [S][n_levels][level_size][dk], the float64 values of the key rows; lev_k64 rows are written beside
+ *   lev_k's.  score_f64 = 0: dirs / unif are float and buf_k64 / lev_k64 are ignored (may be NULL).
  */
 int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, const float* buf_v, int block, int pos0,
                         float* lev_k, float* lev_v, float* lev_w, int32_t* lev_pos, int n_levels, int level_size,
-                        int n_calls, const int32_t* methods, const float* dirs, const float* unif,
-                        const int32_t* perms, int max_in, void* stream);
+                        int n_calls, const int32_t* methods, const void* dirs, const void* unif,
+                        const int32_t* perms, int max_in, int score_f64, const double* buf_k64, double* lev_k64,
+                        void* stream);
 
 /*
  * Block compressor for one batch of coreset nodes (K3), all heads at once.
@@ -257,11 +279,14 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
  *     n_in, n_out, method (0 copy, 1 sorted_pair, 2 permutation), draw slot, n_out of child a (merge; 0 raw).
  *   dirs [BH][n_draws][D] (normalised projection), unif [BH][n_draws][max_in/2] (pair uniforms),
  *   perms [BH][n_draws][max_in] (randperm draws): the seed-derived draws, replayed by the host.
+ *   dtype STA_F64: k is float64 and dirs / unif are double (the draws of a float64 caller); scores are
+ *   fp64 products and sums kept whole for the sort, the pair rule is decided in fp64.  Otherwise dirs /
+ *   unif are float and scores are fp64 sums of the fp32 products rounded to fp32.
  *   outputs: node_src [BH][n_nodes][cap] (global token index of each kept item), node_w (its weight).
  */
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
-                       int n_batch, const int32_t* node_desc, int n_nodes, int cap, const float* dirs,
-                       const float* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
+                       int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
+                       const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
                        float* node_w, void* stream);
 
 /*
@@ -293,8 +318,8 @@ int sta_segment_mean(const void* k, const void* v, int dtype, int64_t bh, int64_
  *     (segment means; fp32 inputs only), NULL otherwise.
  *   exp_clamp: 1 evaluates exp(min(x, 80)) as the Triton kernel does.
  *   products: STA_PRODUCTS_FP32 or STA_PRODUCTS_SPLIT_BF16 for the logits q.k and the weighted value
- *     sums (see sta_moments); weights, exponentials and all sums stay fp32.  Degree 4 needs
- *     STA_PRODUCTS_FP32 (STA_ERR_UNSUPPORTED otherwise).
+ *     sums (see sta_moments); weights, exponentials and all sums stay fp32.  Degrees 4 .. 8 need
+ *     STA_PRODUCTS_FP32 (STA_ERR_UNSUPPORTED otherwise).  d <= 256.
  *   out: [BH][N][Dv] in out_dtype.
  *   out_den: NULL for the normalised output; otherwise out must be fp32 and receives the numerator
  *     and out_den [BH][N] the denominator, unnormalised (the low_num/low_den pair of

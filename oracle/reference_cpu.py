@@ -154,13 +154,16 @@ def low_sums_direct(q: Tensor, k: Tensor, v: Tensor, degree: int, scale: float) 
 
 def projection_scores(keys: np.ndarray, direction: np.ndarray) -> np.ndarray:
     """<k, dir> accumulated in float64 in index order, rounded once to float32 (the order the HIP
-    compressor uses; each fp32*fp32 product is exact in float64)."""
+    compressor uses; each fp32*fp32 product is exact in float64).  float64 keys (a float64 caller,
+    whose reference compress calls run in float64, fast_article_attention.py:339-341,
+    streaming_taylor_coreset_attention.py:441-444): every product rounded to float64, then added, in
+    index order, and the float64 score kept whole."""
     k64 = keys.astype(np.float64)
     d64 = direction.astype(np.float64)
     acc = np.zeros(keys.shape[0], dtype=np.float64)
     for a in range(keys.shape[1]):
         acc = acc + k64[:, a] * d64[a]
-    return acc.astype(np.float32)
+    return acc if keys.dtype == np.float64 else acc.astype(np.float32)
 
 
 def sorted_pair_select(src: np.ndarray, w: np.ndarray, scores: np.ndarray, u: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
@@ -175,8 +178,12 @@ def sorted_pair_select(src: np.ndarray, w: np.ndarray, scores: np.ndarray, u: np
     wa = w[a].astype(np.float32)
     wb = w[b].astype(np.float32)
     wsum = (wa + wb).astype(np.float32)
-    prob = (wa / np.maximum(wsum, np.float32(1e-30))).astype(np.float32)
-    choose_a = u[:pc].astype(np.float32) < prob
+    if u.dtype == np.float64:  # float64 draws: the rule in float64 (weights held in float32)
+        wa64, wb64 = wa.astype(np.float64), wb.astype(np.float64)
+        choose_a = u[:pc] < wa64 / np.maximum(wa64 + wb64, 1e-30)
+    else:
+        prob = (wa / np.maximum(wsum, np.float32(1e-30))).astype(np.float32)
+        choose_a = u[:pc].astype(np.float32) < prob
     out_src = np.where(choose_a, src[a], src[b])
     out_w = wsum
     if n % 2 == 1:
@@ -210,19 +217,24 @@ class CompressCall:
     w_out: Optional[np.ndarray] = None
 
 
-def draw_for_call(g: torch.Generator, n: int, d: int, compressor: str):
+def draw_for_call(g: torch.Generator, n: int, d: int, compressor: str, dtype: torch.dtype = torch.float32):
     """Generator consumption of one compress call on n items
-    (fast_article_attention.py:326-348; streaming_taylor_coreset_attention.py:413-456)."""
+    (fast_article_attention.py:326-348; streaming_taylor_coreset_attention.py:413-456); the direction
+    and uniforms are drawn in the keys' dtype, as the reference draws them (float64 for float64 keys)."""
     if compressor == "none" or n <= 1:
         return "copy", None, None, None
     if compressor == "random" or n <= 2:
         return "perm", None, None, torch.randperm(n, generator=g).numpy()
     if compressor != "sorted_pair":
         raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
-    direction = torch.randn(d, generator=g, dtype=torch.float32)
+    direction = torch.randn(d, generator=g, dtype=dtype)
     direction = direction / torch.clamp(torch.linalg.vector_norm(direction), min=1e-12)
-    u = torch.rand(n // 2, generator=g, dtype=torch.float32)
+    u = torch.rand(n // 2, generator=g, dtype=dtype)
     return "sorted_pair", direction.numpy(), u.numpy(), None
+
+
+def _draw_dtype(keys_all: np.ndarray) -> torch.dtype:
+    return torch.float64 if keys_all.dtype == np.float64 else torch.float32
 
 
 def run_call(call: CompressCall, keys_all: np.ndarray, score_fn=projection_scores) -> None:
@@ -248,7 +260,7 @@ def flat_coreset(k: np.ndarray, block: int, compressor: str, seed: int, score_fn
         if end >= n:
             break
         src = np.arange(start, end, dtype=np.int64)
-        method, dvec, u, perm = draw_for_call(g, end - start, d, compressor)
+        method, dvec, u, perm = draw_for_call(g, end - start, d, compressor, _draw_dtype(k))
         c = CompressCall(0, src, np.ones(end - start, np.float32), method, dvec, u, perm)
         run_call(c, k, score_fn)
         calls.append(c)
@@ -270,7 +282,7 @@ def level_block_complete(state: LevelState, g: torch.Generator, block_src: np.nd
     d = keys_all.shape[1]
 
     def compress(src, w, level):
-        method, dvec, u, perm = draw_for_call(g, src.shape[0], d, compressor)
+        method, dvec, u, perm = draw_for_call(g, src.shape[0], d, compressor, _draw_dtype(keys_all))
         c = CompressCall(level, src, w, method, dvec, u, perm)
         run_call(c, keys_all, score_fn)
         state.calls.append(c)
@@ -309,14 +321,14 @@ def _residual(x: Tensor, degree: int) -> Tensor:
 
 def fast_path_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block: int = 128, scale: Optional[float] = None,
                       compressor: str = "sorted_pair", seed: int = 0, query_chunk: int = 2048, eps: float = 1e-12,
-                      reference_scores: bool = False, calls_out: Optional[list] = None) -> Tensor:
+                      reference_scores: bool = False, calls_out: Optional[list] = None, low: str = "stream") -> Tensor:
     """The reference CPU fast path for one [N, D] sequence (fast_article_attention.py:522-598):
     stream moments + completed-block reps (chunked q x reps) + exact in-block residual, fp32.
     reference_scores=True projects with torch's `keys @ direction` exactly as the reference does
     (fast_article_attention.py:341) instead of the fixed-order scores the HIP kernel uses."""
     n, dim = q.shape
     s = attention_scale(scale, dim)
-    low_num, low_den = low_sums_stream(q, k, v, degree, s)
+    low_num, low_den = _low_sums(q, k, v, degree, s, low)
     tail_den = torch.zeros(n, dtype=q.dtype)
     tail_num = torch.zeros(n, v.shape[-1], dtype=q.dtype)
     if compressor == "none":
@@ -404,9 +416,20 @@ def torch_scores(keys: np.ndarray, direction: np.ndarray) -> np.ndarray:
     return (torch.from_numpy(np.ascontiguousarray(keys)) @ torch.from_numpy(direction)).numpy()
 
 
+def _low_sums(q: Tensor, k: Tensor, v: Tensor, degree: int, scale: float, low: str) -> Tuple[Tensor, Tensor]:
+    """The moment sums by the reference's token loop ("stream") or their closed form ("direct", for
+    feature maps too large to materialise; equal in exact arithmetic, test_stream_moments_equal_closed_form)."""
+    if low == "stream":
+        return low_sums_stream(q, k, v, degree, scale)
+    if low == "direct":
+        num, den = low_sums_direct(q, k, v, degree, scale)
+        return num.to(q.dtype), den.to(q.dtype)
+    raise ValueError("low must be 'stream' or 'direct'")
+
+
 def levels_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block: int = 128, scale: Optional[float] = None,
                    compressor: str = "sorted_pair", seed: int = 0, eps: float = 1e-12, reference_scores: bool = False,
-                   state_out: Optional[LevelState] = None) -> Tensor:
+                   state_out: Optional[LevelState] = None, low: str = "stream") -> Tensor:
     """Streaming semantics of ArticleStreamingAttention for a whole [N, D] sequence
     (streaming_taylor_coreset_attention.py:576-609, :641-687): for every token, update(k_i, v_i) then
     query(q_i).  Queries see the exact moments over keys <= i, the uncompressed buffer (weight 1) and
@@ -414,7 +437,7 @@ def levels_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block: i
     is answered from the compressed levels.  Vectorised per block."""
     n, dim = q.shape
     s = attention_scale(scale, dim)
-    low_num, low_den = low_sums_stream(q, k, v, degree, s)
+    low_num, low_den = _low_sums(q, k, v, degree, s, low)
     out = torch.empty(n, v.shape[-1], dtype=q.dtype)
     state = state_out if state_out is not None else LevelState()
     g = torch.Generator(device="cpu")
@@ -594,7 +617,7 @@ class StreamingAttentionCPU:
         n = weights.numel()
         if self.compressor == "none" or n <= 1:
             return keys, values, weights
-        method, dvec, u, perm = draw_for_call(self.g, n, self.dim, self.compressor)
+        method, dvec, u, perm = draw_for_call(self.g, n, self.dim, self.compressor, keys.dtype)
         if method == "perm":
             m = (n + 1) // 2
             p = torch.from_numpy(perm[:m]).long()

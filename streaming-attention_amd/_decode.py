@@ -11,6 +11,11 @@ Host state: length (tokens per stream), blocks (completed blocks = the level-occ
 buf_len, and one torch CPU generator per stream that the compress calls draw from in the reference's
 order (randn(d) + rand(n//2) per sorted_pair call, randperm(n) for n <= 2 or "random").
 
+A float64 stream (score_f64) also keeps the float64 values of the buffered and level key rows
+(buf_k64 [S, cap, dk], lev_k64 [S, L, m, dk]) and draws its directions and uniforms as float64: its
+compress calls score and select as the reference's float64 run does; every other computation reads the
+float32 rows.
+
 Per decode step (update then query of one token per stream): sta_decode_moments (state read) and
 sta_decode_tail (append + buffer / level items + combine).  When the token completes a block:
 sta_moment_accumulate (buffer -> state) and sta_decode_compress (buffer -> level 0 and the merge
@@ -26,6 +31,7 @@ from typing import Deque, Dict, List, Optional, Tuple
 import numpy as np
 import torch
 
+import _engine
 import _native
 import _plan
 
@@ -37,8 +43,8 @@ class _CompletionDraws:
     blocks_before: int
     n_calls: int
     methods: torch.Tensor  # int32 [n_calls]
-    dirs: torch.Tensor  # float32 [S, n_calls, d]
-    unif: torch.Tensor  # float32 [S, n_calls, max_in // 2]
+    dirs: torch.Tensor  # float32 [S, n_calls, d] (float64 for a float64 stream)
+    unif: torch.Tensor  # float32 [S, n_calls, max_in // 2] (likewise)
     perms: torch.Tensor  # int32 [S, n_calls, max_in]
 
 
@@ -47,7 +53,8 @@ ACCUMULATE_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
 
 class DecodeState:
     def __init__(self, streams: int, dim: int, value_dim: int, *, degree: int, block: int, scale: float,
-                 compressor: str, seed: int, device: torch.device, eps: float = 1e-12) -> None:
+                 compressor: str, seed: int, device: torch.device, eps: float = 1e-12,
+                 score_f64: bool = False) -> None:
         if streams <= 0:
             raise ValueError("streams must be positive")
         if dim <= 0 or value_dim <= 0:
@@ -55,12 +62,11 @@ class DecodeState:
         if block < 2:
             raise ValueError("block_size must be at least 2")
         lim = _native.limits()
-        if dim > lim["max_d"] or value_dim > lim["max_dv"]:
-            raise ValueError(f"the HIP kernels support D <= {lim['max_d']} and Dv <= {lim['max_dv']}")
+        if value_dim > lim["max_dv"]:
+            raise ValueError(f"the HIP decode kernels support Dv <= {lim['max_dv']}")
         if degree < 0:
             raise ValueError("degree must be non-negative")
-        if degree > lim["max_degree"]:
-            raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+        _engine.check_kernel_limits(dim, degree)
         if device.type != "cuda":
             raise ValueError("the HIP decode state lives on a ROCm GPU device")
         self.S, self.d, self.dv = int(streams), int(dim), int(value_dim)
@@ -69,8 +75,8 @@ class DecodeState:
         self.device = device
         self.exact = self.compressor == "none"
         # matrix-core products of the state accumulation (block completions, extend): split-bf16 as in the
-        # prefill moment scan (the state and every sum stay fp32)
-        self.products = ACCUMULATE_PRODUCTS
+        # prefill moment scan (the state and every sum stay fp32); fp32 products at degree 5 .. 8
+        self.products = ACCUMULATE_PRODUCTS if self.degree <= 4 else _native.PRODUCTS_FP32
         self.m = (self.block + 1) // 2
         if not self.exact and max(self.block, 2 * self.m) > lim["max_compress_in"]:
             raise ValueError(f"block_size {block} exceeds the HIP compressor's {lim['max_compress_in']} items")
@@ -90,6 +96,11 @@ class DecodeState:
         self.lev_v = torch.zeros((S, 1, 1, self.ldv), **f32)
         self.lev_w = torch.zeros((S, 1, 1), **f32)
         self.lev_pos = torch.zeros((S, 1, 1), device=dev, dtype=torch.int32)
+        # float64 key rows of a float64 stream (the compressor's scores); none for compressor "none"
+        self.score_f64 = bool(score_f64) and not self.exact
+        f64 = dict(device=dev, dtype=torch.float64)
+        self.buf_k64 = torch.zeros((S, self.cap, self.dk), **f64) if self.score_f64 else None
+        self.lev_k64 = torch.zeros((S, 1, 1, self.dk), **f64) if self.score_f64 else None
         self.length = 0
         self.blocks = 0
         self.buf_len = 0
@@ -99,7 +110,9 @@ class DecodeState:
         self._draws: Deque[_CompletionDraws] = deque()
 
         # moment query: feature factors in reference order, splits to fill the GPU
-        self.findex = torch.from_numpy(_plan.feature_index(self.d, self.degree).view(np.int32)).to(dev)
+        self.findex_width = _plan.feature_index_width(self.d, self.degree)
+        fi = _plan.feature_index(self.d, self.degree)
+        self.findex = torch.from_numpy(fi.view(np.int32) if fi.dtype == np.uint32 else fi.view(np.int16)).to(dev)
         self.splits = max(1, min(-(-2048 // S), self.F // 64 if self.F >= 64 else 1))
         self.part_num = torch.zeros((S, self.splits, self.ldv), **f32)
         self.part_den = torch.zeros((S, self.splits), **f32)
@@ -117,10 +130,17 @@ class DecodeState:
         return _native.stream_handle(self.device)
 
     def _acc_table(self, width: int):
-        """Moment-accumulate tables for rows `width` elements long: (split, quads, coef, rows)."""
+        """Moment-accumulate tables for rows `width` elements long: (split, quads, coef, rows, windows,
+        staged width); keys wider than the 128 staged dimensions through dimension windows."""
         if width not in self._acc_tables:
-            ft = _plan.feature_tiles(width, self.degree)
-            ms = _plan.moment_split(ft, self.S, self.dv, _native.moment_wave_tile_options(width, self.degree))
+            if width > _engine.STAGED_D:
+                wt = _plan.window_tiles(width, self.degree)
+                ft = _plan.window_feature_tiles(wt)
+                ms = _plan.moment_split_windows(wt, self.S, self.dv,
+                                                _native.moment_wave_tile_options(_engine.STAGED_D, self.degree))
+            else:
+                ft = _plan.feature_tiles(width, self.degree)
+                ms = _plan.moment_split(ft, self.S, self.dv, _native.moment_wave_tile_options(width, self.degree))
             rows = _plan.split_state_rows(ft, ms, self.d)
             dev = self.device
             self._acc_tables[width] = (
@@ -128,6 +148,8 @@ class DecodeState:
                 torch.from_numpy(ms.quads.view(np.int32)).to(dev),
                 torch.from_numpy(ms.coef).to(dev),
                 torch.from_numpy(rows).to(dev),
+                torch.from_numpy(ms.win).to(dev) if ms.win is not None else None,
+                ft.d,
             )
         return self._acc_tables[width]
 
@@ -139,15 +161,15 @@ class DecodeState:
             return
         width = k.shape[-1]
         assert k.is_contiguous() and v.is_contiguous() and k.shape[1] == head_rows == v.shape[1]
-        ms, quads, coef, rows = self._acc_table(width)
+        ms, quads, coef, rows, win, staged = self._acc_table(width)
         kp = k.data_ptr() + row_off * width * k.element_size()
         vp = v.data_ptr() + row_off * v.shape[-1] * v.element_size()
 
         def run():
             st = self.lib.sta_moment_accumulate(
-                kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, width, self.dv,
+                kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, staged, width, self.dv,
                 v.shape[-1], self.degree, ms.fsplit, ms.wave_tiles, quads.data_ptr(), coef.data_ptr(), rows.data_ptr(),
-                self.F, self.products, state_num.data_ptr(), state_den.data_ptr(), self._stream())
+                _native.ptr(win), self.F, self.products, state_num.data_ptr(), state_den.data_ptr(), self._stream())
             _native.check(st, "sta_moment_accumulate")
 
         self._launch("moment_accumulate", run)
@@ -162,12 +184,17 @@ class DecodeState:
         lv = torch.zeros((S, new_l, m, self.ldv), **f32)
         lw = torch.zeros((S, new_l, m), **f32)
         lp = torch.zeros((S, new_l, m), device=self.device, dtype=torch.int32)
+        lk64 = torch.zeros((S, new_l, m, self.dk), device=self.device, dtype=torch.float64) if self.score_f64 else None
         if self.L:
             lk[:, : self.L] = self.lev_k
             lv[:, : self.L] = self.lev_v
             lw[:, : self.L] = self.lev_w
             lp[:, : self.L] = self.lev_pos
+            if lk64 is not None:
+                lk64[:, : self.L] = self.lev_k64
         self.lev_k, self.lev_v, self.lev_w, self.lev_pos, self.L = lk, lv, lw, lp, new_l
+        if lk64 is not None:
+            self.lev_k64 = lk64
 
     def _grow_buffer(self) -> None:
         new_cap = 2 * self.cap
@@ -184,7 +211,7 @@ class DecodeState:
         n_calls = len(sizes)
         max_in = max(self.block, 2 * self.m)
         methods = [_plan._call_method(n_in, self.compressor) for n_in in sizes]
-        dirs, unif, perms = self._gens.next(sizes, self.d, self.compressor, max_in)
+        dirs, unif, perms = self._gens.next(sizes, self.d, self.compressor, max_in, f64=self.score_f64)
         dev = self.device
         return _CompletionDraws(
             blocks_before, n_calls, torch.tensor(methods, dtype=torch.int32).to(dev), torch.from_numpy(dirs).to(dev),
@@ -221,7 +248,8 @@ class DecodeState:
                 self.S, self.d, self.dv, self.buf_k.data_ptr(), self.buf_v.data_ptr(), self.block,
                 self.length - self.block, self.lev_k.data_ptr(), self.lev_v.data_ptr(), self.lev_w.data_ptr(),
                 self.lev_pos.data_ptr(), self.L, self.m, dr.n_calls, dr.methods.data_ptr(), dr.dirs.data_ptr(),
-                dr.unif.data_ptr(), dr.perms.data_ptr(), dr.perms.shape[-1], self._stream())
+                dr.unif.data_ptr(), dr.perms.data_ptr(), dr.perms.shape[-1], int(self.score_f64),
+                _native.ptr(self.buf_k64), _native.ptr(self.lev_k64), self._stream())
             _native.check(st, "sta_decode_compress")
 
         self._launch("decode_compress", run)
@@ -265,19 +293,29 @@ class DecodeState:
         def run():
             st = self.lib.sta_decode_moments(
                 q.data_ptr(), _native.DTYPE_CODES[q.dtype], self.S, self.d, self.dv, self.scale,
-                self.state_num.data_ptr(), self.state_den.data_ptr(), self.F, self.findex.data_ptr(), self.splits,
-                self.part_num.data_ptr(), self.part_den.data_ptr(), self._stream())
+                self.state_num.data_ptr(), self.state_den.data_ptr(), self.F, self.findex.data_ptr(),
+                self.findex_width, self.splits, self.part_num.data_ptr(), self.part_den.data_ptr(), self._stream())
             _native.check(st, "sta_decode_moments")
 
         self._launch("decode_moments", run)
 
+    def _put_k64(self, k64: Optional[torch.Tensor], lo: int, hi: int) -> None:
+        """Buffer rows [lo, hi) of a float64 stream take the float64 keys k64 [S, hi - lo, d]."""
+        if not self.score_f64:
+            return
+        if k64 is None or k64.dtype != torch.float64 or tuple(k64.shape) != (self.S, hi - lo, self.d):
+            raise ValueError(f"a float64 stream needs the float64 keys [{self.S}, {hi - lo}, {self.d}]")
+        self.buf_k64[:, lo:hi, : self.d] = k64.to(self.device)
+
     # ------------------------------------------------------------------ public operations
-    def update(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Append one token per stream (MergeReduceCoreset.append + TaylorMomentSketch.update)."""
+    def update(self, k: torch.Tensor, v: torch.Tensor, k64: Optional[torch.Tensor] = None) -> None:
+        """Append one token per stream (MergeReduceCoreset.append + TaylorMomentSketch.update); k64
+        [S, d]: the float64 keys of a float64 stream."""
         k = self._check_rows(k, self.d, "key")
         v = self._check_rows(v, self.dv, "value").to(k.dtype)
         if self.exact and self.buf_len == self.cap:
             self._grow_buffer()
+        self._put_k64(None if k64 is None else k64[:, None], self.buf_len, self.buf_len + 1)
         self._tail(None, k, v, _native.DEC_APPEND, torch.float32, None)
         self.buf_len += 1
         self.length += 1
@@ -291,16 +329,17 @@ class DecodeState:
         return self._tail(q, None, None, _native.DEC_QUERY, out_dtype, stats)
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out_dtype: torch.dtype = torch.float32,
-             stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+             stats: Optional[torch.Tensor] = None, k64: Optional[torch.Tensor] = None) -> torch.Tensor:
         """update(k, v) then query(q) for every stream, fused into two launches unless the token
-        completes a block."""
+        completes a block (k64: as for update)."""
         completes = (not self.exact and self.buf_len + 1 == self.block) or (self.exact and self.buf_len == self.cap)
         if completes:
-            self.update(k, v)
+            self.update(k, v, k64)
             return self.query(q, out_dtype, stats)
         q = self._check_rows(q, self.d, "query")
         k = self._check_rows(k, self.d, "key").to(q.dtype)
         v = self._check_rows(v, self.dv, "value").to(q.dtype)
+        self._put_k64(None if k64 is None else k64[:, None], self.buf_len, self.buf_len + 1)
         self._moments(q)
         out = self._tail(q, k, v, _native.DEC_APPEND | _native.DEC_CURRENT | _native.DEC_QUERY, out_dtype, stats)
         self.buf_len += 1
@@ -315,6 +354,8 @@ class DecodeState:
         that completes a block (compress, merges, host draws) is refused: use step() for it."""
         if (not self.exact and self.buf_len + 1 == self.block) or (self.exact and self.buf_len == self.cap):
             raise ValueError("step_into cannot complete a block; call step() for this token")
+        if self.score_f64:
+            raise ValueError("step_into takes float32 / bfloat16 / float16 tokens; a float64 stream uses step()")
         for x, width, what in ((q, self.d, "query"), (k, self.d, "key"), (v, self.dv, "value")):
             if x.shape != (self.S, width) or x.device != self.device or not x.is_contiguous():
                 raise ValueError(f"{what} must be a contiguous [{self.S}, {width}] tensor on {self.device}")
@@ -331,7 +372,8 @@ class DecodeState:
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), _native.DTYPE_CODES[q.dtype], self.S, self.d, self.dv,
                 self.degree, self.scale, self.eps, flags,
                 None if self.exact else self.state_num.data_ptr(), None if self.exact else self.state_den.data_ptr(),
-                self.F, self.findex.data_ptr(), self.splits, self.buf_k.data_ptr(), self.buf_v.data_ptr(), self.cap,
+                self.F, self.findex.data_ptr(), self.findex_width, self.splits, self.buf_k.data_ptr(),
+                self.buf_v.data_ptr(), self.cap,
                 self.buf_len, self.lev_k.data_ptr(), self.lev_v.data_ptr(), self.lev_w.data_ptr(), self.L, self.m,
                 self.blocks if not self.exact else 0, out.data_ptr(), _native.DTYPE_CODES[out.dtype],
                 _native.ptr(stats), self._stream())
@@ -342,11 +384,14 @@ class DecodeState:
         self.length += 1
         return out
 
-    def extend(self, k: torch.Tensor, v: torch.Tensor) -> None:
+    def extend(self, k: torch.Tensor, v: torch.Tensor, k64: Optional[torch.Tensor] = None) -> None:
         """update() for every token of k [S, P, d] / v [S, P, dv], in bulk: whole blocks go to the state
-        in one moment-accumulate launch and are compressed block by block."""
+        in one moment-accumulate launch and are compressed block by block (k64 [S, P, d]: the float64
+        keys of a float64 stream)."""
         if k.ndim != 3 or k.shape[0] != self.S or k.shape[2] != self.d:
             raise ValueError(f"keys must have shape [{self.S}, P, {self.d}], got {tuple(k.shape)}")
+        if self.score_f64 and (k64 is None or tuple(k64.shape) != tuple(k.shape)):
+            raise ValueError(f"a float64 stream needs the float64 keys [{self.S}, P, {self.d}]")
         if v.shape != (self.S, k.shape[1], self.dv):
             raise ValueError(f"values must have shape [{self.S}, {k.shape[1]}, {self.dv}], got {tuple(v.shape)}")
         k = k.to(self.device)
@@ -363,6 +408,8 @@ class DecodeState:
                 self._grow_buffer()
             self.buf_k[:, self.buf_len: self.buf_len + n, : self.d] = k[:, lo:hi].float()
             self.buf_v[:, self.buf_len: self.buf_len + n, : self.dv] = v[:, lo:hi].float()
+            if self.score_f64:
+                self._put_k64(k64[:, lo:hi], self.buf_len, self.buf_len + n)
             self.buf_len += n
             self.length += n
 
@@ -380,7 +427,8 @@ class DecodeState:
         nb = (p_total - i) // self.block
         if nb > 0:
             esize = k.element_size()
-            width = -(-self.d // (16 // esize)) * (16 // esize)
+            unit = _plan.WINDOW_BLOCK if self.d > _engine.STAGED_D else 16 // esize
+            width = -(-self.d // unit) * unit
             lo, hi = i, i + nb * self.block
             if width == self.d and k.is_contiguous() and k.data_ptr() % 16 == 0:
                 kp, koff = k, lo  # read in place
@@ -453,7 +501,8 @@ class DecodeState:
     # ------------------------------------------------------------------ save / resume
     def _config(self) -> Dict[str, object]:
         return {"streams": self.S, "dim": self.d, "value_dim": self.dv, "degree": self.degree, "block": self.block,
-                "scale": self.scale, "compressor": self.compressor, "seed": self.seed, "eps": self.eps}
+                "scale": self.scale, "compressor": self.compressor, "seed": self.seed, "eps": self.eps,
+                "score_f64": self.score_f64}
 
     def state_dict(self) -> Dict[str, object]:
         """The streams' whole state on the host: configuration, counters, moments, buffered tokens, level
@@ -474,6 +523,8 @@ class DecodeState:
             "state_num": self.state_num.cpu(), "state_den": self.state_den.cpu(),
             "buf_k": self.buf_k[:, : self.buf_len].cpu(), "buf_v": self.buf_v[:, : self.buf_len].cpu(),
             **levels,
+            **({"buf_k64": self.buf_k64[:, : self.buf_len].cpu(),
+                "lev_k64": self.lev_k64[:, : self.L].cpu()} if self.score_f64 else {}),
             "generators": self._gens.get_state(),
             "draws": draws,
         }
@@ -505,6 +556,12 @@ class DecodeState:
             self.lev_v[:, :n_lev] = sd["lev_v"].to(dev)
             self.lev_w[:, :n_lev] = sd["lev_w"].to(dev)
             self.lev_pos[:, :n_lev] = sd["lev_pos"].to(dev)
+        if self.score_f64:
+            self.buf_k64.zero_()
+            self.buf_k64[:, :buf_len] = sd["buf_k64"].to(dev)
+            if n_lev:
+                self.lev_k64.zero_()
+                self.lev_k64[:, :n_lev] = sd["lev_k64"].to(dev)
         self.length, self.blocks, self.buf_len = int(sd["length"]), int(sd["blocks"]), buf_len
         self.num_compressions = int(sd["num_compressions"])
         self._gens.set_state(sd["generators"])
@@ -516,4 +573,6 @@ class DecodeState:
         """Bytes of device memory this state holds."""
         ts = [self.state_num, self.state_den, self.buf_k, self.buf_v, self.lev_k, self.lev_v, self.lev_w,
               self.lev_pos, self.part_num, self.part_den, self.findex]
+        if self.score_f64:
+            ts += [self.buf_k64, self.lev_k64]
         return int(sum(t.numel() * t.element_size() for t in ts))

@@ -119,6 +119,24 @@ def _unit_width(width: int, element_size: int) -> int:
     return -(-width // per_unit) * per_unit
 
 
+STAGED_D = 128  # key dimensions the moment kernels stage whole; wider keys go through dimension windows
+MAX_D_HIGH_DEGREE = 64  # degree 5 .. 8
+
+
+def check_kernel_limits(d: int, degree: int) -> None:
+    """The HIP kernels' key width and degree limits (sta_limits), with the reference's exception types:
+    ValueError for the key width, NotImplementedError for the degree."""
+    lim = _native.limits()
+    if d > lim["max_d"]:
+        raise ValueError(f"the HIP kernels support D <= {lim['max_d']}")
+    if degree > lim["max_degree"]:
+        raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+    if degree >= 5 and d > MAX_D_HIGH_DEGREE:
+        raise NotImplementedError(f"the HIP kernels support Taylor degree >= 5 for D <= {MAX_D_HIGH_DEGREE}")
+    if degree >= 4 and d > STAGED_D:
+        raise NotImplementedError(f"the HIP kernels support Taylor degree 4 for D <= {STAGED_D}")
+
+
 def _padded_rows(t: torch.Tensor, width: int) -> torch.Tensor:
     """t itself when its rows already have `width` elements and it is 16-byte aligned, else a copy
     zero-padded to `width` columns."""
@@ -196,9 +214,13 @@ def prefill(
     products: Optional[int] = None,
     residual_products: Optional[int] = None,
     moment_kernel: Optional[str] = None,
+    score_keys: Optional[torch.Tensor] = None,
 ) -> PrefillResult:
     """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype.  moment_kernel:
-    "ws" (sta_moments_ws where it applies), "chunked" (sta_moments) or None (use_moments_ws)."""
+    "ws" (sta_moments_ws where it applies), "chunked" (sta_moments) or None (use_moments_ws).
+    score_keys: the float64 keys of a float64 caller ([BH, N, D], contiguous, on the device; k3 is
+    their float32 rounding): the compressor then draws its directions and uniforms as float64 and
+    scores these keys in fp64, as the reference's float64 run does."""
     if semantics not in SEMANTICS:
         raise ValueError(f"semantics must be one of {SEMANTICS}")
     for t in (q3, k3, v3):
@@ -210,11 +232,12 @@ def prefill(
     bh, n, d = q3.shape
     dv = v3.shape[-1]
     lim = _native.limits()
-    if d > lim["max_d"]:
-        raise ValueError(f"the HIP kernels support D <= {lim['max_d']} (the degree-2 feature tiles index "
-                         f"key dimensions in 8 bits and are sized for D <= 128)")
-    if degree > lim["max_degree"]:
-        raise NotImplementedError(f"the HIP kernels support Taylor degree <= {lim['max_degree']}")
+    if score_keys is not None:
+        _native.require_device(score_keys)
+        if score_keys.dtype != torch.float64 or tuple(score_keys.shape) != (bh, n, d) or \
+                not score_keys.is_contiguous():
+            raise ValueError("score_keys must be the contiguous float64 [BH, N, D] keys")
+    check_kernel_limits(d, degree)
     if dv > lim["max_dv"]:
         # value columns are independent given the keys (the denominator and the coreset selections do
         # not depend on v): wide values run as column groups of at most max_dv, every group recomputing
@@ -222,7 +245,8 @@ def prefill(
         parts = [prefill(q3, k3, v3[..., c0: c0 + lim["max_dv"]].contiguous(), degree=degree, block=block,
                          scale=scale, semantics=semantics, compressor=compressor, seed=seed, eps=eps,
                          out_dtype=out_dtype, stride=stride, exp_clamp=exp_clamp, draws=draws, timer=timer,
-                         products=products, residual_products=residual_products, moment_kernel=moment_kernel)
+                         products=products, residual_products=residual_products, moment_kernel=moment_kernel,
+                         score_keys=score_keys)
                  for c0 in range(0, dv, lim["max_dv"])]
         first = parts[0]
         return PrefillResult(torch.cat([r.out for r in parts], dim=-1), first.node_src, first.node_w, first.plan,
@@ -251,11 +275,17 @@ def prefill(
                          f"the HIP compressor handles at most {lim['max_compress_in']}")
 
     # the moment kernel reads rows in 16-byte units: q/k padded with zero dimensions to a whole unit
-    # (zero dimensions only add zero-valued features), v to whole 32-column groups
-    dm = _unit_width(d, q3.element_size())
-    ft = _plan.feature_tiles(dm, degree)
+    # (zero dimensions only add zero-valued features), v to whole 32-column groups; keys wider than the
+    # 128 staged dimensions to whole 32-dimension window blocks
+    windowed = d > STAGED_D
+    dm = -(-d // _plan.WINDOW_BLOCK) * _plan.WINDOW_BLOCK if windowed else _unit_width(d, q3.element_size())
+    wt = _plan.window_tiles(dm, degree) if windowed else None
+    ft = _plan.window_feature_tiles(wt) if windowed else _plan.feature_tiles(dm, degree)
     k1_products = MOMENT_PRODUCTS if products is None else int(products)
+    if degree >= 5:
+        k1_products = _native.PRODUCTS_FP32  # the degree 5 .. 8 scan runs fp32 products
     qblock = ws_query_block(semantics, block) if (k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 3 and
+                                                  not windowed and
                                                   (use_moments_ws(q3.element_size(), degree) if moment_kernel is None
                                                    else moment_kernel == "ws")) else None
     ws_ct = 4 if (-(-dv // 32)) % 2 == 0 else 2
@@ -266,6 +296,9 @@ def prefill(
         nseg, seg_blocks = _plan.ws_segments(n, shift, qblock, bh, ft, dv, ws_opts, ws_ct) if WS_SEGMENTS else (1, 0)
         ms = _plan.moment_split_ws(ft, bh * nseg, dv, ws_opts, ws_ct)
         chunk = qblock
+    elif windowed:
+        qblock = None
+        ms = _plan.moment_split_windows(wt, bh, dv, _native.moment_wave_tile_options(STAGED_D, degree))
     else:
         qblock = None
         ms = _plan.moment_split(ft, bh, dv, _native.moment_wave_tile_options(dm, degree),
@@ -274,11 +307,12 @@ def prefill(
     fsplit = ms.fsplit
     # split products at degree <= 2 apply one coefficient per tile on the query side
     tile_coef = k1_products == _native.PRODUCTS_SPLIT_BF16 and degree <= 2
-    fidx, fcoef = _on_device(("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef, ms.columns,
-                              qblock is not None), dev,
-                             lambda: (_i32(ms.quads, dev),
-                                      _f32(_plan.tile_coefficients(ms.quads, ms.coef, dm) if tile_coef else ms.coef,
-                                           dev)))
+    fidx, fcoef, fwin = _on_device(
+        ("mtable", dm, degree, bh, dv, ms.mixed, ms.wave_tiles, ms.fsplit, tile_coef, ms.columns, qblock is not None),
+        dev,
+        lambda: (_i32(ms.quads, dev),
+                 _f32(_plan.tile_coefficients(ms.quads, ms.coef, ft.d) if tile_coef else ms.coef, dev),
+                 _i32(ms.win, dev) if ms.win is not None else None))
 
     # ---- host side first: every validation error is raised before anything is launched ----
     pkey = (plan.mode, plan.n, plan.block, compressor if semantics != "segment" else stride)
@@ -286,13 +320,16 @@ def prefill(
         ("plan",) + pkey, dev,
         lambda: (_i32(plan.meta, dev), _i32(plan.tile_ptr, dev), _i32(np.maximum(plan.tile_nodes, 0) if plan.tile_nodes.size else np.zeros(1, np.int32), dev)),
     )
+    f64 = score_keys is not None
     if semantics != "segment" and plan.batches:
         seeds = _plan.sequence_seeds(seed, bh)
+        fdraw = (lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float64)).to(dev)) if f64 else \
+            (lambda a: _f32(a, dev))
         if draws is None:
-            dr, desc = _plan.draws_for(plan, seeds, d, compressor)
+            dr, desc = _plan.draws_for(plan, seeds, d, compressor, f64)
             dirs_d, unif_d, perms_d, desc_d = _on_device(
-                ("draws",) + pkey + (seeds, d), dev,
-                lambda: (_f32(dr.dirs, dev), _f32(dr.unif, dev), _i32(dr.perms, dev), _i32(desc, dev)),
+                ("draws",) + pkey + (seeds, d, f64), dev,
+                lambda: (fdraw(dr.dirs), fdraw(dr.unif), _i32(dr.perms, dev), _i32(desc, dev)),
             )
         else:
             dr = draws
@@ -301,8 +338,10 @@ def prefill(
             if (dr.dirs.shape != (bh, n_calls, d) or dr.max_in < need or dr.unif.shape != (bh, n_calls, dr.max_in // 2)
                     or dr.perms.shape != (bh, n_calls, dr.max_in)):
                 raise ValueError("explicit draws do not match the compress-call layout of this configuration")
+            if (dr.dirs.dtype == np.float64) != f64:
+                raise ValueError("explicit draws must be float64 exactly when score_keys are given")
             _, desc = _plan.draws_for(plan, seeds[:1], d, compressor)
-            dirs_d, unif_d, perms_d, desc_d = (_f32(dr.dirs, dev), _f32(dr.unif, dev), _i32(dr.perms, dev), _i32(desc, dev))
+            dirs_d, unif_d, perms_d, desc_d = (fdraw(dr.dirs), fdraw(dr.unif), _i32(dr.perms, dev), _i32(desc, dev))
         batches_d = _on_device(("batches",) + pkey, dev, lambda: [_i32(b, dev) for b in plan.batches])
 
     lrows, lld, _ = _native.moment_partials_layout(n, dv)
@@ -327,10 +366,11 @@ def prefill(
     else:
         def k1():
             st = lib.sta_moments(
-                mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, dm, dv, mv.shape[-1], degree,
+                mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), dt, bh, n, ft.d, dm, dv, mv.shape[-1], degree,
                 float(scale), chunk, shift,
                 fsplit, ms.wave_tiles, int(ms.mixed), k1_products, ms.columns,
-                fidx.data_ptr(), fcoef.data_ptr(), low_num.data_ptr(), low_den.data_ptr(), stream)
+                fidx.data_ptr(), fcoef.data_ptr(), _native.ptr(fwin), low_num.data_ptr(), low_den.data_ptr(),
+                stream)
             _native.check(st, "sta_moments")
 
     # The compressor needs only the keys and the draws: with OVERLAP_COMPRESS it goes on a second stream
@@ -378,7 +418,8 @@ def prefill(
             for bd in batches_d:
                 def k3_launch(bd=bd):
                     st = lib.sta_compress_nodes(
-                        k3.data_ptr(), dt, bh, n, d, bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(),
+                        (score_keys if f64 else k3).data_ptr(), _native.STA_F64 if f64 else dt, bh, n, d,
+                        bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(),
                         plan.n_nodes, plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(),
                         dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(), k3_stream)
                     _native.check(st, "sta_compress_nodes")
@@ -398,7 +439,7 @@ def prefill(
     if residual_products is not None:
         k2_products = int(residual_products)
     elif semantics in EXACT_SEMANTICS or (n_nodes_arg == 0 and n_rep_arg == 0) or degree > 3:
-        # no coreset item (the result is exact attention), or degree 4 (the fp32-product kernel's Taylor)
+        # no coreset item (the result is exact attention), or degree >= 4 (the fp32-product kernel's Taylor)
         k2_products = _native.PRODUCTS_FP32
     else:
         k2_products = RESIDUAL_PRODUCTS

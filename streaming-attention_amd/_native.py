@@ -25,6 +25,7 @@ STA_ERR_ARG = 5
 STA_ERR_SCRATCH = 6
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+STA_F64 = 3  # sta_compress_nodes' float64 scoring
 PRODUCTS_FP32 = 0
 PRODUCTS_SPLIT_BF16 = 1
 
@@ -43,8 +44,8 @@ _SIGNATURES = {
     "sta_moment_chunk": (_i32, [_i32]),
     "sta_moments": (
         _i32,
-        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32,
-         _i32, _c_p, _c_p, _c_p, _c_p, _c_p],
+        [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32,
+         _i32, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p],  # ... d ld_qk dv ldv ... quads coef windows num den stream
     ),
     "sta_moments_ws": (
         _i32,
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "sta_moment_mixed_ok": (_i32, [_i32, _i32, _i32]),
     "sta_moment_wave_tiles": (_i32, [_i32, _i32, _i32]),
     "sta_moment_occupancy": (_i32, [_i32, _i32]),
+    "sta_moment_occupancy_degree": (_i32, [_i32, _i32, _i32]),
     "sta_moment_partials_layout": (_i32, [_i64, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "sta_compress_nodes": (
         _i32,
@@ -85,12 +87,12 @@ _SIGNATURES = {
     ),
     "sta_moment_accumulate": (
         _i32,
-        [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dtype bh n rows d dv ldv deg fs nt
-         _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],  # quads coef rows n_feat products num den stream
+        [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dt bh n rows d ld dv ldv deg fs nt
+         _c_p, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],  # quads coef rows windows n_feat products num den stream
     ),
     "sta_decode_layout": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "sta_decode_moments": (
-        _i32, [_c_p, _i32, _i64, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _i32, _c_p, _c_p, _c_p],
+        _i32, [_c_p, _i32, _i64, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p],
     ),
     "sta_decode_tail": (
         _i32,
@@ -106,7 +108,8 @@ _SIGNATURES = {
         [
             _i64, _i32, _i32, _c_p, _c_p, _i32, _i32,  # S d dv buf_k buf_v block pos0
             _c_p, _c_p, _c_p, _c_p, _i32, _i32,  # lev_k lev_v lev_w lev_pos n_levels level_size
-            _i32, _c_p, _c_p, _c_p, _c_p, _i32, _c_p,  # n_calls methods dirs unif perms max_in stream
+            _i32, _c_p, _c_p, _c_p, _c_p, _i32,  # n_calls methods dirs unif perms max_in
+            _i32, _c_p, _c_p, _c_p,  # score_f64 buf_k64 lev_k64 stream
         ],
     ),
     "sta_static_scratch_bytes": (_i64, []),
@@ -114,7 +117,7 @@ _SIGNATURES = {
         _i32,
         [
             _c_p, _c_p, _c_p, _i32, _i64, _i32, _i32, _i32, _f32, _f32, _i32,  # q k v dtype S d dv deg scale eps flags
-            _c_p, _c_p, _i32, _c_p, _i32,  # state_num state_den n_feat feat_index splits
+            _c_p, _c_p, _i32, _c_p, _i32, _i32,  # state_num state_den n_feat feat_index index_width splits
             _c_p, _c_p, _i32, _i32,  # buf_k buf_v block buf_len
             _c_p, _c_p, _c_p, _i32, _i32, ctypes.c_uint64,  # lev_k lev_v lev_w n_levels level_size mask
             _c_p, _i32, _c_p, _c_p,  # out out_dtype stats stream
@@ -173,6 +176,8 @@ def draws_library() -> ctypes.CDLL:
         for name, res, args in (("sta_draws_open", p, [p, i]),
                                 ("sta_draws_close", None, [p]),
                                 ("sta_draws_next", i, [p, p, i, i, i, i, p, p, p]),
+                                ("sta_draws_next_typed", i, [p, p, i, i, i, i, i, p, p, p]),
+                                ("sta_host_draws_typed", i, [p, i, p, i, i, i, i, i, p, p, p]),
                                 ("sta_draws_state_bytes", ctypes.c_int64, []),
                                 ("sta_draws_get_state", i, [p, p]),
                                 ("sta_draws_set_state", i, [p, p]),
@@ -189,28 +194,31 @@ def _draws_fail(h) -> None:
     raise NativeError(h.sta_draws_error().decode())
 
 
-def _draw_tables(n_seq: int, call_sizes, d: int, compressor: str, max_in: int):
+def _draw_tables(n_seq: int, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
     import numpy as np
 
     if compressor not in COMPRESSOR_CODES:
         raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
     cc = max(len(call_sizes), 1)
     sz = np.ascontiguousarray(np.asarray(call_sizes, dtype=np.int32))
-    return (sz, np.zeros((n_seq, cc, d), dtype=np.float32), np.zeros((n_seq, cc, max_in // 2), dtype=np.float32),
+    ft = np.float64 if f64 else np.float32
+    return (sz, np.zeros((n_seq, cc, d), dtype=ft), np.zeros((n_seq, cc, max_in // 2), dtype=ft),
             np.zeros((n_seq, cc, max_in), dtype=np.int32))
 
 
-def host_draws(seeds, call_sizes, d: int, compressor: str, max_in: int):
+def host_draws(seeds, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
     """Draw tables (dirs [S, C, d], unif [S, C, max_in // 2], perms int32 [S, C, max_in]; C = at least 1)
     of len(seeds) sequences, each on a fresh generator seeded seeds[s], over the compress calls of
-    call_sizes, in call order."""
+    call_sizes, in call order.  f64: the directions and uniforms are drawn as float64 (the draws of a
+    float64 caller), else float32."""
     import numpy as np
 
-    sz, dirs, unif, perms = _draw_tables(len(seeds), call_sizes, d, compressor, max_in)
+    sz, dirs, unif, perms = _draw_tables(len(seeds), call_sizes, d, compressor, max_in, f64)
     sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.int64))
     h = draws_library()
-    if h.sta_host_draws(sd.ctypes.data, len(seeds), sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor],
-                        max_in, dirs.ctypes.data, unif.ctypes.data, perms.ctypes.data) != 0:
+    if h.sta_host_draws_typed(sd.ctypes.data, len(seeds), sz.ctypes.data, len(call_sizes), d,
+                              COMPRESSOR_CODES[compressor], max_in, int(f64), dirs.ctypes.data, unif.ctypes.data,
+                              perms.ctypes.data) != 0:
         _draws_fail(h)
     return dirs, unif, perms
 
@@ -234,11 +242,12 @@ class DrawSet:
             self._h.sta_draws_close(self._ptr)
             self._ptr = None
 
-    def next(self, call_sizes, d: int, compressor: str, max_in: int):
+    def next(self, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
         """Tables as host_draws, continuing every stream's generator."""
-        sz, dirs, unif, perms = _draw_tables(self.n, call_sizes, d, compressor, max_in)
-        if self._h.sta_draws_next(self._ptr, sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor], max_in,
-                                  dirs.ctypes.data, unif.ctypes.data, perms.ctypes.data) != 0:
+        sz, dirs, unif, perms = _draw_tables(self.n, call_sizes, d, compressor, max_in, f64)
+        if self._h.sta_draws_next_typed(self._ptr, sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor],
+                                        max_in, int(f64), dirs.ctypes.data, unif.ctypes.data,
+                                        perms.ctypes.data) != 0:
             _draws_fail(self._h)
         return dirs, unif, perms
 
@@ -286,7 +295,7 @@ _wave_tile_options: dict = {}
 
 def moment_wave_tile_options(d: int, degree: int) -> tuple:
     """((per-wave tile count, workgroups resident per compute unit), ...) the moment kernel is built
-    for at (d, degree)."""
+    for at (staged width d, degree)."""
     key = (d, degree)
     if key not in _wave_tile_options:
         l = lib()
@@ -294,7 +303,7 @@ def moment_wave_tile_options(d: int, degree: int) -> tuple:
         for want in range(1, 65):
             nt = l.sta_moment_wave_tiles(d, degree, want)
             if nt > 0:
-                opts.add((nt, l.sta_moment_occupancy(d, nt)))
+                opts.add((nt, l.sta_moment_occupancy_degree(d, degree, nt)))
         _wave_tile_options[key] = tuple(sorted(opts))
     return _wave_tile_options[key]
 

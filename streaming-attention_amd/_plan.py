@@ -118,16 +118,18 @@ MOM_WAVES = 4  # waves per moment workgroup (sta_moments)
 OCC2_SPEEDUP = 1.2  # per-tile throughput of two resident moment workgroups per CU vs one
 WIDE_COST = 1.2  # time per tile of a 64-column workgroup (split products) vs a 32-column one alone
 MOM_MAX_WAVE_TILES = 16  # largest per-wave tile count the kernel is instantiated for
-COVER_MAX_MONOMIALS = 200_000  # largest degree-3 / 4 monomial set packed by the window cover
+COVER_MAX_MONOMIALS = 50_000  # largest degree-3 / 4 monomial set packed by the window cover (<= 0.5 s)
 
 
 @dataclass(frozen=True)
 class FeatureTiles:
     """The monomial basis through `degree` laid out for the moment kernel: tiles of 16 features made of
-    4 quads; quad q of tile t is quads[4 t + q] (packed i0 | b << 8 | i2 << 16 | i3 << 24) and holds the
-    features x[i0] * x[b + s] * x[i2] * x[i3], s = 0..3, with b a multiple of 4 and x[d] = 1 (so
-    i0 = i2 = i3 = d reduces the degree).  coef[16 t + 4 q + s] is the key-side coefficient 1/prod(alpha!) of feature s of the quad,
-    0 where b + s is not a valid last factor (padding; x[b + s] is then 0 or the constant 1).
+    4 quads; quad q of tile t is quads[(4 t + q) * qw : (4 t + q + 1) * qw], packed i0 | b << 8 | i2 << 16 |
+    i3 << 24 (qw = 1, degree <= 4) and a second word i4 | i5 << 8 | i6 << 16 | i7 << 24 (qw = 2, degree
+    5 .. 8), and holds the features x[i0] * x[b + s] * x[i2] * ... (the degree - 2 extra factors), s = 0..3,
+    with b a multiple of 4 and x[d] = 1 (so i0 = i2 = ... = d reduces the degree).
+    coef[16 t + 4 q + s] is the key-side coefficient 1/prod(alpha!) of feature s of the quad, 0 where
+    b + s is not a valid last factor (padding; x[b + s] is then 0 or the constant 1).
 
     Same set of monomials as the reference's feature map (fast_article_attention.py:151-181,
     streaming_taylor_coreset_attention.py:118-216); the order differs, which the moment sums do not
@@ -139,19 +141,171 @@ class FeatureTiles:
     degree: int
     count: int
     n_tiles: int
-    quads: np.ndarray  # uint32 [n_tiles * 4]
+    quads: np.ndarray  # uint32 [n_tiles * 4 * qw]
     coef: np.ndarray  # float32 [n_tiles * 16]
-    combos: Tuple[Optional[Tuple[int, ...]], ...] = ()  # sorted multi-index of each slot, None for padding
+    # the monomial of every slot: mono_len [n_tiles * 16] its degree (-1 for padding), mono [n_tiles * 16,
+    # max(degree, 1)] its factors ascending in the first mono_len columns (-1 after)
+    mono_len: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int8))
+    mono: np.ndarray = field(default_factory=lambda: np.zeros((0, 1), np.int32))
+    qw: int = 1  # 32-bit words per quad
+
+    def combo(self, slot: int) -> Optional[Tuple[int, ...]]:
+        """The sorted multi-index of a slot (None for padding)."""
+        n = int(self.mono_len[slot])
+        return None if n < 0 else tuple(int(x) for x in self.mono[slot, :n])
+
+
+def quad_words(degree: int) -> int:
+    """32-bit words per feature quad of a degree (the moment kernel's mom_quad_words)."""
+    return 2 if degree >= 5 else 1
+
+
+def _pack_quad(i0: int, b: int, extras: Tuple[int, ...], one: int, qw: int) -> List[int]:
+    """Words of a quad: i0 | b << 8 | e0 << 16 | e1 << 24 [, e2 | e3 << 8 | e4 << 16 | e5 << 24]; unused
+    extra factors are `one` (the constant x[d] = 1)."""
+    ex = list(extras) + [one] * (4 * qw - 2 - len(extras))
+    words = [i0 | (b << 8) | (ex[0] << 16) | (ex[1] << 24)]
+    if qw == 2:
+        words.append(ex[2] | (ex[3] << 8) | (ex[4] << 16) | (ex[5] << 24))
+    return words
+
+
+class _Quads:
+    """Quads under construction as arrays: i0 [n], b [n], extras [n, 6] (unused = the constant index),
+    coef [n, 4], per-slot monomials mono [n, 4, width] ascending with -1 after mono_len [n, 4] (-1 for
+    padding slots)."""
+
+    def __init__(self, width: int) -> None:
+        self.width = max(width, 1)
+        self.parts: List[Tuple[np.ndarray, ...]] = []
+
+    def add_arrays(self, i0, b, extras, coef, mono, mono_len) -> None:
+        n = i0.shape[0]
+        ex = np.full((n, 6), -1, dtype=np.int32)
+        ex[:, : extras.shape[1]] = extras
+        mo = np.full((n, 4, self.width), -1, dtype=np.int32)
+        mo[:, :, : mono.shape[2]] = mono
+        self.parts.append((i0.astype(np.int32), b.astype(np.int32), ex, coef.astype(np.float64), mo,
+                           mono_len.astype(np.int8)))
+
+    def add_lists(self, quads: List[Tuple[int, int, Tuple[int, ...]]], coefs: List[List[float]],
+                  combos: List[Optional[Tuple[int, ...]]]) -> None:
+        if not quads:
+            return
+        n = len(quads)
+        i0 = np.asarray([q[0] for q in quads])
+        b = np.asarray([q[1] for q in quads])
+        ex = np.full((n, 6), -1, dtype=np.int32)
+        for i, q in enumerate(quads):
+            ex[i, : len(q[2])] = q[2]
+        mo = np.full((n, 4, self.width), -1, dtype=np.int32)
+        ml = np.full((n, 4), -1, dtype=np.int8)
+        for i, c in enumerate(combos):
+            if c is not None:
+                ml[i // 4, i % 4] = len(c)
+                mo[i // 4, i % 4, : len(c)] = c
+        self.add_arrays(i0, b, ex, np.asarray(coefs, dtype=np.float64).reshape(n, 4), mo, ml)
+
+    def cat(self):
+        if not self.parts:
+            return (np.zeros(0, np.int32), np.zeros(0, np.int32), np.zeros((0, 6), np.int32),
+                    np.zeros((0, 4)), np.zeros((0, 4, self.width), np.int32), np.zeros((0, 4), np.int8))
+        return tuple(np.concatenate([p[i] for p in self.parts]) for i in range(6))
+
+
+def _row_quads(qs: _Quads, d: int, prefixes: np.ndarray) -> int:
+    """Quads of the rows prefix + (c,), c from the prefix's last factor to d - 1, for every sorted prefix
+    row of `prefixes` [P, L] (L >= 1), built with numpy: the row is cut at multiples of 4; a slot's
+    coefficient is 1/prod(alpha!) of its monomial.  Returns the number of features."""
+    pn, ln = prefixes.shape
+    if pn == 0:
+        return 0
+    lo = prefixes[:, -1].astype(np.int64)
+    nq = (d - 1) // 4 - lo // 4 + 1
+    rowid = np.repeat(np.arange(pn), nq)
+    k = np.arange(int(nq.sum())) - np.repeat(np.cumsum(nq) - nq, nq)
+    b = (lo[rowid] // 4) * 4 + 4 * k
+    c = b[:, None] + np.arange(4)[None, :]
+    valid = (c >= lo[rowid][:, None]) & (c < d)
+    # 1/prod(alpha!) of the prefix and the run length of its last factor
+    run = np.ones(pn, dtype=np.int64)
+    prod = np.ones(pn, dtype=np.float64)
+    for j in range(1, ln):
+        run = np.where(prefixes[:, j] == prefixes[:, j - 1], run + 1, 1)
+        prod *= run
+    base = 1.0 / prod
+    coef = np.where(c == lo[rowid][:, None], (base / (run + 1))[rowid][:, None], base[rowid][:, None])
+    coef = np.where(valid, coef, 0.0)
+    mono = np.concatenate([np.broadcast_to(prefixes[rowid][:, None, :], (rowid.shape[0], 4, ln)), c[:, :, None]], axis=2)
+    mono_len = np.where(valid, ln + 1, -1)
+    qs.add_arrays(prefixes[rowid, 0], b, prefixes[rowid, 1:], coef, mono, mono_len)
+    return int(valid.sum())
+
+
+def _rows_to_tiles(d: int, degree: int, qs: _Quads, count: int, reorder: bool) -> FeatureTiles:
+    """Tiles of 4 quads from the quads in order.  reorder: first every run of 4 quads that share (b,
+    extras) and take 4 consecutive first factors i0 = 4k .. 4k+3, then the remaining quads in order.  In
+    the kernel's update a tile's 16 lanes then read 4 distinct key rows per factor (x[i0] by quad,
+    x[b + s] by slot), a pattern the transposed key rows serve without LDS bank conflicts, and the query
+    reads one 16-byte block x[b..b+3] per token for all 4 quads."""
+    one = d
+    qw = quad_words(degree)
+    i0, b, ex, coef, mono, mono_len = qs.cat()
+    nq = i0.shape[0]
+    ex = np.where(ex < 0, one, ex)
+    order = np.arange(nq)
+    if reorder and nq:
+        real = i0 != one
+        idx = np.nonzero(real)[0]
+        # group the real quads by (extras, b, i0 >> 2); a group of 4 distinct i0 is a run
+        keys = [i0[idx]] + [i0[idx] >> 2, b[idx]] + [ex[idx, j] for j in range(6)]
+        srt = idx[np.lexsort(keys)]
+        gk = np.stack([ex[srt, j] for j in range(6)] + [b[srt], i0[srt] >> 2], axis=1)
+        new_grp = np.ones(srt.shape[0], dtype=bool)
+        new_grp[1:] = np.any(gk[1:] != gk[:-1], axis=1)
+        gid = np.cumsum(new_grp) - 1
+        gsize = np.bincount(gid)
+        first_pos = np.full(gsize.shape[0], nq, dtype=np.int64)
+        np.minimum.at(first_pos, gid, srt)
+        in_run = gsize[gid] == 4
+        run_members = srt[in_run]
+        run_gid = gid[in_run]
+        # runs in the order of their first quad, members by i0
+        run_order = np.lexsort((i0[run_members], first_pos[run_gid]))
+        head = run_members[run_order]
+        rest_mask = np.ones(nq, dtype=bool)
+        rest_mask[head] = False
+        order = np.concatenate([head, np.nonzero(rest_mask)[0]])
+    i0, b, ex, coef, mono, mono_len = i0[order], b[order], ex[order], coef[order], mono[order], mono_len[order]
+    n_tiles = -(-nq // 4)
+    pad = np.asarray(_pack_quad(one + 1, d // 4 * 4, (), one, qw), dtype=np.uint32)
+    q = np.tile(pad, n_tiles * 4)
+    if nq:
+        w0 = (i0 | (b << 8) | (ex[:, 0] << 16) | (ex[:, 1] << 24)).astype(np.uint32)
+        if qw == 2:
+            w1 = (ex[:, 2] | (ex[:, 3] << 8) | (ex[:, 4] << 16) | (ex[:, 5] << 24)).astype(np.uint32)
+            q[: 2 * nq] = np.stack([w0, w1], axis=1).reshape(-1)
+        else:
+            q[:nq] = w0
+    c = np.zeros(n_tiles * 16, dtype=np.float32)
+    c[: 4 * nq] = coef.reshape(-1)
+    ml = np.full(n_tiles * 16, -1, dtype=np.int8)
+    ml[: 4 * nq] = mono_len.reshape(-1)
+    mo = np.full((n_tiles * 16, qs.width), -1, dtype=np.int32)
+    mo[: 4 * nq] = mono.reshape(-1, qs.width)
+    return FeatureTiles(d, degree, count, n_tiles, q, c, ml, mo, qw)
 
 
 def feature_tiles(d: int, degree: int) -> FeatureTiles:
-    if degree > 4 or d > 252 or (degree == 4 and d > 64):
-        raise NotImplementedError("the HIP feature map supports degree <= 3 with D <= 252 and degree 4 with "
-                                  "D <= 64")
+    """Feature tiles of the basis through `degree` of x[0 .. d) for a staged key width d <= 128 (degree
+    5 .. 8: d <= 64; wider keys: window_tiles)."""
+    if degree > 8 or d > 128 or (degree >= 5 and d > 64):
+        raise NotImplementedError("the HIP feature map supports degree <= 4 with D <= 128 (wider keys through "
+                                  "dimension windows) and degree 5 .. 8 with D <= 64")
 
     def build():
         one = d
-        quads: List[int] = []
+        quads: List[Tuple[int, int, Tuple[int, ...]]] = []
         coefs: List[List[float]] = []
         slot_combos: List[Optional[Tuple[int, ...]]] = []
         count = 0
@@ -164,14 +318,13 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
             if last < lo:
                 return
             i0 = prefix[0] if len(prefix) >= 1 else one
-            i2 = prefix[1] if len(prefix) >= 2 else one
-            i3 = prefix[2] if len(prefix) >= 3 else one
+            extras = tuple(prefix[1:])
             for b in range((lo // 4) * 4, last + 1, 4):
                 if not any(lo <= c < hi or (with_const and c == d) for c in range(b, b + 4)):
                     continue  # no feature in this quad (degree 0: only the constant's quad is kept)
                 cs = []
-                for s in range(4):
-                    c = b + s
+                for s_ in range(4):
+                    c = b + s_
                     if lo <= c < hi:
                         cs.append(_factorial_inverse(tuple(sorted(prefix + (c,)))))
                         slot_combos.append(tuple(sorted(prefix + (c,))))
@@ -183,7 +336,7 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
                     else:
                         cs.append(0.0)
                         slot_combos.append(None)
-                quads.append(i0 | (b << 8) | (i2 << 16) | (i3 << 24))
+                quads.append((i0, b, extras))
                 coefs.append(cs)
 
         # degree 0 and 1: x_c for c < d plus the constant, all with prefix ()
@@ -192,19 +345,19 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
             for a in range(d):
                 add_row((a,), a, d, False)
         # degrees 3 and 4: the window cover (fewer padding slots than rows cut at multiples of 4); rows
-        # for very large sets (degree 4 at d = 64: 0.77 M monomials, where the greedy cover takes
-        # seconds of host time per process)
+        # (built with numpy) for large sets, where the greedy cover takes seconds of host time, and for
+        # degrees 5 .. 8
+        qs = _Quads(degree)
+        big_rows = []
         for deg in range(3, degree + 1):
-            if math.comb(d + deg - 1, deg) > COVER_MAX_MONOMIALS:
-                for pre in itertools.combinations_with_replacement(range(d), deg - 1):
-                    add_row(pre, pre[-1], d, False)
+            if deg >= 5 or math.comb(d + deg - 1, deg) > COVER_MAX_MONOMIALS:
+                big_rows.append(deg)
                 continue
             for (fixed, m), got in _window_cover(d, deg):
                 mine = set(got)
-                ids = list(fixed) + [one] * (3 - len(fixed))
                 cs = []
-                for s in range(4):
-                    mono = tuple(sorted(fixed + (4 * m + s,))) if 4 * m + s < d else None
+                for s_ in range(4):
+                    mono = tuple(sorted(fixed + (4 * m + s_,))) if 4 * m + s_ < d else None
                     if mono is not None and mono in mine:
                         cs.append(_factorial_inverse(mono))
                         slot_combos.append(mono)
@@ -212,38 +365,123 @@ def feature_tiles(d: int, degree: int) -> FeatureTiles:
                     else:  # padding, or a monomial another window holds
                         cs.append(0.0)
                         slot_combos.append(None)
-                quads.append(ids[0] | ((4 * m) << 8) | (ids[1] << 16) | (ids[2] << 24))
+                quads.append((fixed[0] if fixed else one, 4 * m, tuple(fixed[1:])))
                 coefs.append(cs)
-        # Tiles: first every run of 4 quads that share (b, i2, i3) and take 4 consecutive first factors
-        # i0 = 4k .. 4k+3, then the remaining quads in row order.  In the kernel's update a tile's 16
-        # lanes then read 4 distinct key rows per factor (x[i0] by quad, x[b + s] by slot), a pattern the
-        # transposed key rows serve without LDS bank conflicts, and the query reads one 16-byte block
-        # x[b..b+3] per token for all 4 quads.
-        runs: Dict[Tuple[int, int, int, int], List[int]] = {}
-        for idx, qd in enumerate(quads):
-            i0, b, i2, i3 = qd & 255, (qd >> 8) & 255, (qd >> 16) & 255, qd >> 24
-            if i0 != one:
-                runs.setdefault((i3, i2, b, i0 >> 2), []).append(idx)
-        order: List[int] = []
-        for (_, _, _, k4), idxs in runs.items():
-            if sorted(quads[i] & 255 for i in idxs) == [4 * k4 + t for t in range(4)]:
-                order += sorted(idxs, key=lambda i: quads[i] & 255)
-        taken = set(order)
-        order += [i for i in range(len(quads)) if i not in taken]
-        quads = [quads[i] for i in order]
-        coefs = [coefs[i] for i in order]
-        slot_combos = [c for i in order for c in slot_combos[4 * i: 4 * i + 4]]
-        n_tiles = -(-len(quads) // 4)
-        # padding: first factor x[d + 1] = 0, so every padding slot is a zero-valued monomial
-        pad_quad = (one + 1) | ((d // 4 * 4) << 8) | (one << 16) | (one << 24)
-        q = np.full(n_tiles * 4, pad_quad, dtype=np.uint32)
-        c = np.zeros(n_tiles * 16, dtype=np.float32)
-        q[: len(quads)] = np.asarray(quads, dtype=np.uint32)
-        c[: 4 * len(coefs)] = np.asarray(coefs, dtype=np.float32).reshape(-1)
-        combos = tuple(slot_combos) + (None,) * (n_tiles * 16 - len(slot_combos))
-        return FeatureTiles(d, degree, count, n_tiles, q, c, combos)
+        qs.add_lists(quads, coefs, slot_combos)
+        for deg in big_rows:
+            pre = np.asarray(list(itertools.combinations_with_replacement(range(d), deg - 1)), dtype=np.int64)
+            count += _row_quads(qs, d, pre.reshape(-1, deg - 1))
+        return _rows_to_tiles(d, degree, qs, count, reorder=degree <= 4)
 
     return _cached(("ftiles", d, degree), build)
+
+
+# ----------------------------------------------------------------------------- dimension windows
+WINDOW_BLOCK = 32  # dimensions per window block
+WINDOW_BLOCKS = 4  # blocks per window (128 staged dimensions)
+
+
+@dataclass(frozen=True)
+class WindowTiles:
+    """The basis through `degree` (<= 4) of keys wider than the 128 staged dimensions: every monomial is
+    assigned to one window of 4 blocks of 32 row dimensions holding all its factors, and each window's
+    monomials are tiled over the window's 128 virtual dimensions (virtual 32 b + j = row dimension
+    blocks[b] + j).  tiles[w] is window w's FeatureTiles (virtual indices, constant x[128] = 1; combos in
+    ROW dimensions); blocks[w] the first row dimension of each of its 4 blocks."""
+
+    d: int  # row width (a multiple of 32)
+    degree: int
+    count: int
+    blocks: Tuple[Tuple[int, ...], ...]
+    tiles: Tuple[FeatureTiles, ...]
+
+    @property
+    def n_tiles(self) -> int:
+        return sum(t.n_tiles for t in self.tiles)
+
+
+def window_tiles(d: int, degree: int) -> WindowTiles:
+    """Windows for a row width d > 128 (a multiple of 32, at most 256) and degree <= 4.  The block sets
+    (the distinct 32-dimension blocks of a monomial's factors, at most `degree` of them) are covered
+    greedily by 4-block windows, each set assigned to the first window that covers it (most monomials
+    first); every window's monomials form rows by their leading factors as in feature_tiles."""
+    if d % WINDOW_BLOCK or d <= 128 or degree > 4:
+        raise NotImplementedError("dimension windows need a row width above 128 (a multiple of 32) and degree <= 4")
+
+    def build():
+        nb = d // WINDOW_BLOCK
+        vd = WINDOW_BLOCK * WINDOW_BLOCKS
+        sets = [frozenset(c) for r in range(1, min(degree, nb) + 1) for c in itertools.combinations(range(nb), r)]
+
+        def weight(sset):  # monomials whose distinct blocks are exactly sset
+            k = len(sset)
+            return sum(math.comb(WINDOW_BLOCK * k + l - 1, l) for l in range(k, degree + 1)) if k else 1
+
+        left = set(sets)
+        chosen: List[Tuple[Tuple[int, ...], List[frozenset]]] = []
+        cands = list(itertools.combinations(range(nb), WINDOW_BLOCKS))
+        while left:
+            best = max(cands, key=lambda w: (sum(weight(x) for x in left if x <= set(w)), tuple(-i for i in w)))
+            got = [x for x in left if x <= set(best)]
+            left -= set(got)
+            chosen.append((best, got))
+        if not chosen:  # degree 0: the constant feature alone
+            chosen.append((tuple(range(WINDOW_BLOCKS)), []))
+        tiles = []
+        count = 0
+        for wi, (wblocks, got) in enumerate(chosen):
+            vpos = {b: k for k, b in enumerate(wblocks)}
+            mine = set(got)
+
+            def virt(dim):
+                return WINDOW_BLOCK * vpos[dim // WINDOW_BLOCK] + dim % WINDOW_BLOCK
+
+            # the window's monomials (row dimensions, sorted), then rows by leading factors in virtual order
+            rows: Dict[Tuple[int, ...], List[int]] = {}
+            real_of: Dict[Tuple[int, ...], Tuple[int, ...]] = {}
+            dims = [b * WINDOW_BLOCK + j for b in wblocks for j in range(WINDOW_BLOCK)]
+            for l in range(1, degree + 1):
+                for mono in itertools.combinations_with_replacement(dims, l):
+                    if frozenset(m // WINDOW_BLOCK for m in mono) not in mine:
+                        continue
+                    v = tuple(sorted(virt(m) for m in mono))
+                    rows.setdefault(v[:-1], []).append(v[-1])
+                    real_of[v] = mono
+            quads, coefs, combos = [], [], []
+            if wi == 0:
+                rows.setdefault((), [])  # the constant feature (x[vd] = 1) lives in window 0's () row
+            n = 0
+            for prefix in sorted(rows):
+                cs_set = set(rows[prefix])
+                with_const = prefix == () and wi == 0
+                lasts = sorted(cs_set | ({vd} if with_const else set()))
+                for b in sorted({4 * (c // 4) for c in lasts}):
+                    cf = []
+                    for s_ in range(4):
+                        c = b + s_
+                        if c in cs_set:
+                            v = tuple(sorted(prefix + (c,)))
+                            cf.append(_factorial_inverse(v))
+                            combos.append(real_of[v])
+                            n += 1
+                        elif with_const and c == vd:
+                            cf.append(1.0)
+                            combos.append(())
+                            n += 1
+                        else:
+                            cf.append(0.0)
+                            combos.append(None)
+                    quads.append((prefix[0] if prefix else vd, b, tuple(prefix[1:])))
+                    coefs.append(cf)
+            qs = _Quads(degree)
+            qs.add_lists(quads, coefs, combos)
+            tiles.append(_rows_to_tiles(vd, degree, qs, n, reorder=True))
+            count += n
+        assert count == num_features(d, degree), (count, num_features(d, degree))
+        return WindowTiles(d, degree, count, tuple(tuple(b * WINDOW_BLOCK for b in w) for w, _ in chosen),
+                           tuple(tiles))
+
+    return _cached(("wtiles", d, degree), build)
 
 
 def reference_feature_order(d: int, degree: int) -> Dict[Tuple[int, ...], int]:
@@ -261,20 +499,32 @@ def reference_feature_order(d: int, degree: int) -> Dict[Tuple[int, ...], int]:
     return _cached(("reforder", d, degree), build)
 
 
+def feature_index_width(d: int, degree: int) -> int:
+    """Factor slots per feature of feature_index (sta_decode_moments' index_width): 4 (8-bit factors
+    packed in a uint32) for d < 255 and degree <= 4, else 8 (uint16 factors)."""
+    return 4 if d < 255 and degree <= 4 else 8
+
+
 def feature_index(d: int, degree: int) -> np.ndarray:
-    """uint32 [F]: the factors of reference feature f packed i0 | i1 << 8 | i2 << 16 | i3 << 24, indices into
-    x = [x_0 .. x_{d-1}, 1] (index d is the constant 1 filling the unused factors)."""
+    """The factors of every reference feature f as indices into x = [x_0 .. x_{d-1}, 1] (index d is the
+    constant 1 filling the unused factors): uint32 [F] packed i0 | i1 << 8 | i2 << 16 | i3 << 24 when
+    feature_index_width is 4, else uint16 [F, 8]."""
+    if degree > 8:
+        raise NotImplementedError("the HIP feature map supports degree <= 8")
 
     def build():
         order = reference_feature_order(d, degree)
-        out = np.zeros(len(order), dtype=np.uint32)
+        if feature_index_width(d, degree) == 4:
+            out = np.zeros(len(order), dtype=np.uint32)
+            for combo, f in order.items():
+                idx = list(combo) + [d] * (4 - len(combo))
+                out[f] = idx[0] | (idx[1] << 8) | (idx[2] << 16) | (idx[3] << 24)
+            return out
+        out16 = np.full((len(order), 8), d, dtype=np.uint16)
         for combo, f in order.items():
-            idx = list(combo) + [d] * (4 - len(combo))
-            out[f] = idx[0] | (idx[1] << 8) | (idx[2] << 16) | (idx[3] << 24)
-        return out
+            out16[f, : len(combo)] = combo
+        return out16
 
-    if degree > 4 or d > 255:
-        raise NotImplementedError("the HIP feature map supports degree <= 4 and D <= 255")
     return _cached(("findex", d, degree), build)
 
 
@@ -294,6 +544,7 @@ class MomentSplit:
     coef: np.ndarray  # float32 [fsplit * 4 * wave_tiles * 16]
     mixed: bool = False  # splits fs >= fsplit / 2 run wave_tiles - 1 tiles per wave
     columns: int = 32  # value columns per workgroup
+    win: Optional[np.ndarray] = None  # int32 [fsplit * 4]: each split's window blocks (keys wider than 128)
 
 
 def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int, int], ...],
@@ -357,10 +608,11 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
             sizes = [base + (1 if i < extra else 0) for i in range(parts)]
         off = np.zeros(parts + 1, dtype=np.int32)
         off[1:] = np.cumsum(sizes)
-        pad_quad = (ft.d + 1) | ((ft.d // 4 * 4) << 8) | (ft.d << 16) | (ft.d << 24)  # zero-valued slots
-        quads = np.full((parts, nt, 4), pad_quad, dtype=np.uint32)
+        # zero-valued padding slots
+        pad = np.asarray(_pack_quad(ft.d + 1, ft.d // 4 * 4, (), ft.d, ft.qw), dtype=np.uint32)
+        quads = np.tile(pad, (parts, nt, 4, 1))
         coef = np.zeros((parts, nt, 16), dtype=np.float32)
-        tiles_q = ft.quads.reshape(t, 4)
+        tiles_q = ft.quads.reshape(t, 4, ft.qw)
         tiles_c = ft.coef.reshape(t, 16)
         for j in range(parts):
             cnt = sizes[j]
@@ -370,6 +622,71 @@ def moment_split(ft: FeatureTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int
 
     return _cached(("msplit", ft.d, ft.degree, bh, dv, tuple(nt_options), compute_units, tuple(mixed_nts),
                     tuple(wide_nts)), build)
+
+
+def window_feature_tiles(wt: WindowTiles) -> FeatureTiles:
+    """The windows' tiles as one table (virtual indices, row-dimension combos), window after window."""
+
+    def build():
+        qw = wt.tiles[0].qw
+        return FeatureTiles(WINDOW_BLOCK * WINDOW_BLOCKS, wt.degree, wt.count, wt.n_tiles,
+                            np.concatenate([t.quads for t in wt.tiles]), np.concatenate([t.coef for t in wt.tiles]),
+                            np.concatenate([t.mono_len for t in wt.tiles]), np.concatenate([t.mono for t in wt.tiles]),
+                            qw)
+
+    return _cached(("wft", wt.d, wt.degree), build)
+
+
+def moment_split_windows(wt: WindowTiles, bh: int, dv: int, nt_options: Tuple[Tuple[int, int], ...],
+                         compute_units: int = 256) -> MomentSplit:
+    """Work split of the moment kernel for keys wider than 128: every feature split holds the tiles of
+    one window (its table entry win[4 fs .. 4 fs + 3] names the window's blocks), window w taking
+    ceil(tiles_w / (4 wave_tiles)) splits with its tiles balanced over their waves; wave_tiles
+    minimises rounds of workgroups x tiles per wave as in moment_split.  The table's tile ranges index
+    window_feature_tiles(wt)."""
+
+    def build():
+        csplit = -(-dv // 32)
+        best = None
+        for nt, occ in sorted(nt_options):
+            splits = [-(-t.n_tiles // (MOM_WAVES * nt)) for t in wt.tiles]
+            fsplit = sum(splits)
+            rounds = -(-(bh * fsplit * csplit) // (compute_units * occ))
+            cost = rounds * nt * occ / (OCC2_SPEEDUP if occ == 2 else 1.0)
+            if best is None or cost < best[0] - 1e-9:
+                best = (cost, nt, splits)
+        if best is None:
+            raise ValueError("no supported per-wave tile count for the windowed feature tiles")
+        _, nt, splits = best
+        fsplit = sum(splits)
+        parts = fsplit * MOM_WAVES
+        qw = wt.tiles[0].qw
+        ft = window_feature_tiles(wt)
+        pad = np.asarray(_pack_quad(ft.d + 1, ft.d // 4 * 4, (), ft.d, qw), dtype=np.uint32)
+        quads = np.tile(pad, (parts, nt, 4, 1))
+        coef = np.zeros((parts, nt, 16), dtype=np.float32)
+        win = np.zeros(fsplit * 4, dtype=np.int32)
+        off = np.zeros(parts + 1, dtype=np.int32)
+        tiles_q = ft.quads.reshape(ft.n_tiles, 4, qw)
+        tiles_c = ft.coef.reshape(ft.n_tiles, 16)
+        fs, base, j = 0, 0, 0
+        for w, t in enumerate(wt.tiles):
+            nparts = MOM_WAVES * splits[w]
+            b_, extra = divmod(t.n_tiles, nparts)
+            for p_ in range(nparts):
+                cnt = b_ + (1 if p_ < extra else 0)
+                quads[j, :cnt] = tiles_q[base:base + cnt]
+                coef[j, :cnt] = tiles_c[base:base + cnt]
+                base += cnt
+                off[j + 1] = base
+                j += 1
+            for _ in range(splits[w]):
+                win[4 * fs: 4 * fs + 4] = wt.blocks[w]
+                fs += 1
+        assert j == parts and base == ft.n_tiles
+        return MomentSplit(fsplit, csplit, nt, off, quads.reshape(-1), coef.reshape(-1), False, 32, win)
+
+    return _cached(("msplit_win", wt.d, wt.degree, bh, dv, tuple(nt_options), compute_units), build)
 
 
 def moment_split_ws(ft: FeatureTiles, bh: int, dv: int, slot_options: Tuple[int, ...], column_tiles: int,
@@ -484,26 +801,61 @@ def tile_coefficients(quads: np.ndarray, coef: np.ndarray, d: int) -> np.ndarray
     return out.reshape(np.asarray(coef).shape)
 
 
+def reference_rank(mono: np.ndarray, mono_len: np.ndarray, d: int, degree: int) -> np.ndarray:
+    """Index of every monomial (rows of mono, factors ascending in the first mono_len columns) in the
+    reference's feature order for dimension d: degree 0, 1, ..., each in
+    itertools.combinations_with_replacement(range(d), l) order (streaming_taylor_coreset_attention.py:
+    160-176).  A sorted multiset a_1 <= .. <= a_l is the strictly increasing b_i = a_i + i - 1 in
+    range(n), n = d + l - 1, whose lexicographic rank is sum_i [C(n - b_{i-1} - 1, l - i + 1) -
+    C(n - b_i, l - i + 1)] (b_0 = -1).  -1 where mono_len < 0."""
+    top = d + degree + 1
+    pas = np.zeros((top + 1, degree + 2), dtype=np.int64)
+    pas[:, 0] = 1
+    for n_ in range(1, top + 1):
+        pas[n_, 1:] = pas[n_ - 1, 1:] + pas[n_ - 1, :-1]
+    offset = np.zeros(degree + 2, dtype=np.int64)
+    for l in range(1, degree + 2):
+        offset[l] = offset[l - 1] + (math.comb(d + l - 2, l - 1) if l - 1 > 0 else 1)
+    out = np.full(mono_len.shape[0], -1, dtype=np.int64)
+    for l in range(0, degree + 1):
+        sel = np.nonzero(mono_len == l)[0]
+        if sel.size == 0:
+            continue
+        if l == 0:
+            out[sel] = 0
+            continue
+        n_ = d + l - 1
+        bb = mono[sel, :l].astype(np.int64) + np.arange(l)[None, :]
+        prev = np.concatenate([np.full((sel.size, 1), -1, dtype=np.int64), bb[:, :-1]], axis=1)
+        rank = np.zeros(sel.size, dtype=np.int64)
+        for i in range(l):
+            k = l - i
+            rank += pas[n_ - prev[:, i] - 1, k] - pas[n_ - bb[:, i], k]
+        out[sel] = offset[l] + rank
+    return out
+
+
 def split_state_rows(ft: FeatureTiles, ms: MomentSplit, d: int) -> np.ndarray:
     """int32 [fsplit * 4 * wave_tiles * 16]: the reference-order feature row (for the true dimension d
-    <= ft.d) of every feature slot of the split's table, -1 for padding slots and for monomials that
-    involve a padding dimension >= d (their keys are zero there)."""
+    <= ft.d, or the row dimensions of a windowed table) of every feature slot of the split's table, -1
+    for padding slots and for monomials that involve a padding dimension >= d (their keys are zero
+    there)."""
 
     def build():
-        order = reference_feature_order(d, ft.degree)
-        slot_row = np.full(ft.n_tiles * 16, -1, dtype=np.int32)
-        for i, combo in enumerate(ft.combos):
-            if combo is not None and all(c < d for c in combo):
-                slot_row[i] = order[combo]
+        ml = ft.mono_len.astype(np.int64)
+        inside = np.all((ft.mono < d) | (np.arange(ft.mono.shape[1])[None, :] >= ml[:, None]), axis=1)
+        slot_row = np.where(inside & (ml >= 0), reference_rank(ft.mono, np.where(inside, ml, -1), d, ft.degree), -1)
         parts = ms.tile_off.shape[0] - 1
         rows = np.full((parts, ms.wave_tiles, 16), -1, dtype=np.int32)
         for j in range(parts):
             a, b = int(ms.tile_off[j]), int(ms.tile_off[j + 1])
             rows[j, : b - a] = slot_row[16 * a: 16 * b].reshape(b - a, 16)
-        assert sorted(r for r in rows.reshape(-1) if r >= 0) == list(range(len(order)))
+        got = np.sort(rows[rows >= 0])
+        assert got.size == num_features(d, ft.degree) and np.array_equal(got, np.arange(got.size))
         return rows.reshape(-1)
 
-    return _cached(("srows", ft.d, ft.degree, d, ms.fsplit, ms.wave_tiles, ms.tile_off.tobytes()), build)
+    return _cached(("srows", ft.d, ft.degree, d, ms.fsplit, ms.wave_tiles, ms.tile_off.tobytes(),
+                    ms.win.tobytes() if ms.win is not None else b""), build)
 
 
 # ----------------------------------------------------------------------------- draws
@@ -518,15 +870,16 @@ def _compressed_size(n_in: int, compressor: str) -> int:
 class Draws:
     """Seed-derived randomness of every compress call, per sequence, in reference call order."""
 
-    dirs: np.ndarray  # float32 [BH, n_calls, d]
-    unif: np.ndarray  # float32 [BH, n_calls, max_in // 2]
+    dirs: np.ndarray  # float32 [BH, n_calls, d] (float64 for a float64 caller)
+    unif: np.ndarray  # float32 [BH, n_calls, max_in // 2] (float64 likewise)
     perms: np.ndarray  # int32 [BH, n_calls, max_in]
     n_calls: int
     max_in: int
 
 
-def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str):
-    """Consume the generator exactly as one reference compress call on n_in items does."""
+def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str, dtype: torch.dtype = torch.float32):
+    """Consume the generator exactly as one reference compress call on n_in items does (directions and
+    uniforms in `dtype`, the keys' dtype of the reference call)."""
     if compressor == "none" or n_in <= 1:
         return METHOD_COPY, None, None, None
     if compressor not in ("random", "sorted_pair"):
@@ -534,9 +887,9 @@ def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str):
     if compressor == "random" or n_in <= 2:
         perm = torch.randperm(n_in, generator=g)
         return METHOD_PERM, None, None, perm.numpy().astype(np.int32)
-    direction = torch.randn(d, generator=g, dtype=torch.float32)
+    direction = torch.randn(d, generator=g, dtype=dtype)
     direction = direction / torch.clamp(torch.linalg.vector_norm(direction), min=1e-12)
-    u = torch.rand(n_in // 2, generator=g, dtype=torch.float32)
+    u = torch.rand(n_in // 2, generator=g, dtype=dtype)
     return METHOD_SORTED_PAIR, direction.numpy(), u.numpy(), None
 
 
@@ -548,29 +901,34 @@ def _call_method(n_in: int, compressor: str) -> int:
     return METHOD_PERM if compressor == "random" or n_in <= 2 else METHOD_SORTED_PAIR
 
 
-def _collect_draws(seeds: List[int], call_sizes: List[int], d: int, compressor: str) -> Tuple[Draws, List[int]]:
+def _collect_draws(seeds: List[int], call_sizes: List[int], d: int, compressor: str,
+                   f64: bool = False) -> Tuple[Draws, List[int]]:
     """Draws of every sequence over the compress calls of call_sizes, replayed natively (the same
-    generator calls as _draw_one_call, per sequence on its own generator, sequences in parallel)."""
+    generator calls as _draw_one_call, per sequence on its own generator, sequences in parallel); f64:
+    directions and uniforms drawn as float64 (a float64 caller's)."""
     methods = [_call_method(n_in, compressor) for n_in in call_sizes]
     max_in = max(max(call_sizes) if call_sizes else 2, 2)
-    dirs, unif, perms = _native.host_draws(seeds, call_sizes, d, compressor, max_in)
+    dirs, unif, perms = _native.host_draws(seeds, call_sizes, d, compressor, max_in, f64=f64)
     return Draws(dirs, unif, perms, len(call_sizes), max_in), methods
 
 
-def _collect_draws_py(seeds: List[int], call_sizes: List[int], d: int, compressor: str) -> Tuple[Draws, List[int]]:
+def _collect_draws_py(seeds: List[int], call_sizes: List[int], d: int, compressor: str,
+                      f64: bool = False) -> Tuple[Draws, List[int]]:
     """The same draws one generator call at a time through torch's Python API."""
     n_calls = len(call_sizes)
     max_in = max(max(call_sizes) if call_sizes else 2, 2)
     bh = len(seeds)
-    dirs = np.zeros((bh, max(n_calls, 1), d), dtype=np.float32)
-    unif = np.zeros((bh, max(n_calls, 1), max_in // 2), dtype=np.float32)
+    ft = np.float64 if f64 else np.float32
+    dirs = np.zeros((bh, max(n_calls, 1), d), dtype=ft)
+    unif = np.zeros((bh, max(n_calls, 1), max_in // 2), dtype=ft)
     perms = np.zeros((bh, max(n_calls, 1), max_in), dtype=np.int32)
     methods: List[int] = []
     for h, seed in enumerate(seeds):
         g = torch.Generator(device="cpu")
         g.manual_seed(int(seed))
         for c, n_in in enumerate(call_sizes):
-            method, dvec, u, perm = _draw_one_call(g, n_in, d, compressor)
+            method, dvec, u, perm = _draw_one_call(g, n_in, d, compressor,
+                                                   torch.float64 if f64 else torch.float32)
             if h == 0:
                 methods.append(method)
             if dvec is not None:
@@ -754,11 +1112,13 @@ def segment_plan(n: int, block: int, stride: int) -> Tuple[NodePlan, int, int]:
     return _cached(("segment", n, block, stride), build)
 
 
-def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str) -> Tuple[Draws, np.ndarray]:
-    """Draw table for every sequence plus the node descriptors with their compress method filled in."""
+def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str,
+              f64: bool = False) -> Tuple[Draws, np.ndarray]:
+    """Draw table for every sequence plus the node descriptors with their compress method filled in
+    (f64: float64 directions and uniforms)."""
 
     def build():
-        draws, methods = _collect_draws(list(seeds), plan.call_sizes, d, compressor)
+        draws, methods = _collect_draws(list(seeds), plan.call_sizes, d, compressor, f64)
         desc = plan.desc.copy()
         if plan.mode in (MODE_FLAT, MODE_LEVELS) and plan.call_sizes:
             for i in range(desc.shape[0]):
@@ -767,7 +1127,7 @@ def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str) -
                 desc[i, 5] = methods[desc[i, 6]]
         return draws, desc
 
-    return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor), build)
+    return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor, bool(f64)), build)
 
 
 def completion_call_sizes(blocks_before: int, block: int, compressor: str) -> List[int]:

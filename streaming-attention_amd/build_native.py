@@ -2,7 +2,7 @@
 
     python streaming-attention_amd/build_native.py
 
-The library is 89 objects compiled in parallel and linked into one shared object: api.hip (entry
+The library is 99 objects compiled in parallel and linked into one shared object: api.hip (entry
 points, compressor and decode kernels), launch_moments_ws.hip (the wave-specialised moment scan, per
 element size and column-tile count), launch_moments.hip (fp32 and split-bf16 products, 32 or 64
 columns), launch_accumulate.hip, and
@@ -36,7 +36,7 @@ UNITS = tuple(("launch_moments_ws.hip", f"launch_moments_ws_{es}_{ct}", (f"-DSTA
     ("launch_accumulate.hip", "launch_accumulate", ()),
 ) + tuple(("launch_block.hip", f"launch_block_{dp}_{dvt}_{es}",
            (f"-DSTA_BLOCK_DP={dp}", f"-DSTA_BLOCK_DVT={dvt}", f"-DSTA_BLOCK_ES={es}"))
-          for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + tuple(
+          for dp in (256, 128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + tuple(
     ("launch_flash.hip", f"launch_flash_{dp}_{dvt}_{es}",
      (f"-DSTA_FLASH_DP={dp}", f"-DSTA_FLASH_DVT={dvt}", f"-DSTA_FLASH_ES={es}"))
     for dp in (128, 64, 32, 16) for dvt in (4, 2, 8, 1, 16) for es in (4, 2)) + (
@@ -83,24 +83,25 @@ def build(verbose: bool = False, only: str = "") -> pathlib.Path:
     other objects from an earlier build) and link the library; libstadraws.so is rebuilt alongside
     unless `only` names HIP units."""
     OBJDIR.mkdir(exist_ok=True)
+    with_host = not only or only == "host"
+    hip_only = "\0" if only == "host" else only  # "\0": no HIP unit matches
+    cc = hipcc()
+    jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    pending = [u for u in UNITS if u[1].startswith(hip_only)]
+    running, failed = [], []
+    objs = [str(OBJDIR / f"{stem}.o") for _, stem, _ in UNITS if not stem.startswith(hip_only)]
+    # every check that can refuse the build runs before any compiler process is started
+    missing = [o for o in objs if not pathlib.Path(o).exists()]
+    if missing:
+        raise RuntimeError(f"objects of an earlier build are missing: {missing[:3]}; build without `only`")
     draws = None
-    if not only or only == "host":
+    if with_host:
         tmp_d = DRAWS_OUT.with_suffix(".so.tmp")
         cmd = _draws_cmd(tmp_d)
         if verbose:
             print(" ".join(cmd), flush=True)
         dlog = open(OBJDIR / "host_draws.log", "w+")
         draws = (dlog, tmp_d, subprocess.Popen(cmd, stdout=dlog, stderr=subprocess.STDOUT))
-        if only == "host":
-            only = "\0"  # no HIP unit matches
-    cc = hipcc()
-    jobs = max(1, min(len(UNITS), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
-    pending = [u for u in UNITS if u[1].startswith(only)]
-    running, failed = [], []
-    objs = [str(OBJDIR / f"{stem}.o") for _, stem, _ in UNITS if not stem.startswith(only)]
-    missing = [o for o in objs if not pathlib.Path(o).exists()]
-    if missing:
-        raise RuntimeError(f"objects of an earlier build are missing: {missing[:3]}; build without `only`")
     t0 = time.time()
     while pending or running:
         while pending and len(running) < jobs:

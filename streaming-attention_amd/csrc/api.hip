@@ -153,7 +153,7 @@ int sta_flash_attention(const void* q, const void* k, const void* v, int dtype, 
   if (!q || !k || !v || !out) return STA_ERR_ARG;
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0) return STA_ERR_SHAPE;
-  if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
+  if (d > kMaxFlashD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
   if (ld_qk < d || ld_qk % 4 != 0 || ld_v < dv || ld_v % 4 != 0) return STA_ERR_ARG;
   if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
     return STA_ERR_ARG;
@@ -191,7 +191,7 @@ int sta_moment_partials_layout(int64_t n, int dv, int64_t* rows, int* ld, int* r
 }
 
 int sta_moment_mixed_ok(int d, int degree, int wave_tiles) {
-  return (d > 0 && d <= 64 && degree >= 0 && degree <= kMaxDegree && (wave_tiles == 4 || wave_tiles == 5) &&
+  return (d > 0 && d <= 64 && degree >= 0 && degree <= 4 && (wave_tiles == 4 || wave_tiles == 5) &&
           moment_wave_tiles(d, degree, wave_tiles) == wave_tiles)
              ? 1
              : 0;
@@ -205,15 +205,34 @@ int sta_moment_occupancy(int d, int wave_tiles) {
   return (wave_tiles > 0 && d > 0) ? sta::mom_wg_per_cu(wave_tiles, d > 64) : 0;
 }
 
-int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int dv,
-                int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
-                int products, int columns, const uint32_t* feat_quads, const float* feat_coef, float* low_num,
-                float* low_den, void* stream) {
+int sta_moment_occupancy_degree(int d, int degree, int wave_tiles) {
+  return (wave_tiles > 0 && d > 0 && degree >= 0)
+             ? sta::mom_wg_per_cu(wave_tiles, d > 64, 32, moment_extra_factors(degree))
+             : 0;
+}
+
+// Row stride and window checks shared by sta_moments and sta_moment_accumulate: without windows the
+// rows are d long (ld_qk == d); with windows d is the staged width kMaxStagedD, ld_qk a multiple of 32
+// of at least 128 and at most kMaxD, degree <= kMaxDegreeWindows.
+static int window_check(int d, int ld_qk, int degree, const int32_t* windows) {
+  if (!windows) return ld_qk == d ? STA_OK : STA_ERR_ARG;
+  if (d != kMaxStagedD || ld_qk < kMaxStagedD || ld_qk > kMaxD || ld_qk % 32 != 0) return STA_ERR_ARG;
+  if (degree > kMaxDegreeWindows) return STA_ERR_UNSUPPORTED;
+  return STA_OK;
+}
+
+int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t bh, int64_t n, int d, int ld_qk,
+                int dv, int ldv, int degree, float scale, int chunk, int shift, int fsplit, int wave_tiles, int mixed,
+                int products, int columns, const uint32_t* feat_quads, const float* feat_coef,
+                const int32_t* windows, float* low_num, float* low_den, void* stream) {
   if (!q || !k || !v || !feat_quads || !feat_coef || !low_num || !low_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0) return STA_ERR_SHAPE;
-  if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
+  if (d > kMaxStagedD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
+  if (const int wst = window_check(d, ld_qk, degree, windows); wst != STA_OK) return wst;
+  // degree >= 5 runs fp32 products on 32 columns only
+  if (moment_extra_factors(degree) >= 3 && (products != STA_PRODUCTS_FP32 || columns != 32)) return STA_ERR_UNSUPPORTED;
   if (chunk != sta_moment_chunk(d) || shift < 0 || shift >= chunk) return STA_ERR_ARG;
   if (mixed != 0 && (mixed != 1 || fsplit % 2 != 0 || !sta_moment_mixed_ok(d, degree, wave_tiles))) return STA_ERR_ARG;
   if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
@@ -225,13 +244,13 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
   if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0) return STA_ERR_ARG;
   if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0)
     return STA_ERR_ARG;
-  if (n * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+  if (n * static_cast<int64_t>(ldv > ld_qk ? ldv : ld_qk) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
     return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + columns - 1) / columns; a.quads = feat_quads;
   a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
-  a.ldo = 32 * ((dv + 31) / 32);
+  a.ldo = 32 * ((dv + 31) / 32); a.ldk = ld_qk; a.win = windows;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (columns == 64) return dispatch_moments<true, 64>(a, bh, s, wave_tiles, moment_extra_factors(degree));
   return products == STA_PRODUCTS_SPLIT_BF16 ? dispatch_moments<true, 32>(a, bh, s, wave_tiles, moment_extra_factors(degree))
@@ -239,7 +258,7 @@ int sta_moments(const void* q, const void* k, const void* v, int dtype, int64_t 
 }
 
 int sta_moments_ws_ok(int d, int degree, int slot_tiles, int column_tiles, int dv) {
-  if (d <= 0 || d > kMaxD || degree < 0 || degree > 3 || dv <= 0 || dv > kMaxDv) return 0;
+  if (d <= 0 || d > kMaxStagedD || degree < 0 || degree > 3 || dv <= 0 || dv > kMaxDv) return 0;
   if (column_tiles != 4 && column_tiles != 2) return 0;
   if (column_tiles == 4 && ((dv + 31) / 32) % 2 != 0) return 0;
   const int nx = moment_extra_factors(degree);
@@ -296,7 +315,7 @@ int sta_moments_ws_seg(const void* q, const void* k, const void* v, int dtype, i
   a.q = q; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = scale; a.shift = shift;
   a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 16 * column_tiles - 1) / (16 * column_tiles);
   a.quads = feat_quads; a.fcoef = feat_coef; a.low_num = low_num; a.low_den = low_den; a.ldv = ldv; a.esize = esize;
-  a.ldo = 32 * ((dv + 31) / 32);
+  a.ldo = 32 * ((dv + 31) / 32); a.ldk = d; a.win = nullptr;
   a.head_rows = n; a.rowmap = nullptr; a.state_num = nullptr; a.state_den = nullptr; a.n_feat = 0;
   w.cpb = cpb;
   w.mixed = mixed;
@@ -337,26 +356,31 @@ int sta_moments_ws(const void* q, const void* k, const void* v, int dtype, int64
 }
 
 int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
-                          int dv, int ldv, int degree, int fsplit, int wave_tiles, const uint32_t* feat_quads,
-                          const float* feat_coef, const int32_t* feat_rows, int n_feat, int products,
-                          float* state_num, float* state_den, void* stream) {
+                          int ld_k, int dv, int ldv, int degree, int fsplit, int wave_tiles,
+                          const uint32_t* feat_quads, const float* feat_coef, const int32_t* feat_rows,
+                          const int32_t* windows, int n_feat, int products, float* state_num, float* state_den,
+                          void* stream) {
   if (!k || !v || !feat_quads || !feat_coef || !feat_rows || !state_num || !state_den) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (bh <= 0 || n < 0 || head_rows < n || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0 || n_feat <= 0)
     return STA_ERR_SHAPE;
-  if (d > kMaxD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
+  if (d > kMaxStagedD || dv > kMaxDv || degree < 0 || degree > kMaxDegree) return STA_ERR_UNSUPPORTED;
   if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles) return STA_ERR_UNSUPPORTED;
   if (products != STA_PRODUCTS_FP32 && products != STA_PRODUCTS_SPLIT_BF16) return STA_ERR_ARG;
+  if (const int wst = window_check(d, ld_k, degree, windows); wst != STA_OK) return wst;
+  if (moment_extra_factors(degree) >= 3 && products != STA_PRODUCTS_FP32) return STA_ERR_UNSUPPORTED;
   if (n == 0) return STA_OK;
   const int esize = dtype == STA_F32 ? 4 : 2;
   if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0) return STA_ERR_ARG;
   if (((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0) return STA_ERR_ARG;
-  if (head_rows * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+  if (head_rows * static_cast<int64_t>(ldv > ld_k ? ldv : ld_k) * esize >= (int64_t(1) << 32) ||
+      n >= (int64_t(1) << 30))
     return STA_ERR_UNSUPPORTED;
   sta::MomArgs a;
   a.q = k; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = 1.0f; a.shift = 0;
   a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
   a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
+  a.ldk = ld_k; a.win = windows;
   a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
   return dispatch_accumulate(a, bh, static_cast<hipStream_t>(stream), wave_tiles, moment_extra_factors(degree),
                              products == STA_PRODUCTS_SPLIT_BF16);
@@ -365,15 +389,18 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
 int sta_decode_layout(int d, int dv, int* dk, int* ldv) {
   if (d <= 0 || dv <= 0 || !dk || !ldv) return STA_ERR_ARG;
   if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
-  *dk = 4 * ((d + 3) / 4);
+  // keys wider than the staged 128 dimensions in whole 32-dimension blocks (the accumulation's windows)
+  *dk = d > kMaxStagedD ? 32 * ((d + 31) / 32) : 4 * ((d + 3) / 4);
   *ldv = 32 * ((dv + 31) / 32);
   return STA_OK;
 }
 
 int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv, float scale, const float* state_num,
-                       const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* part_num,
+                       const float* state_den, int n_feat, const void* feat_index, int index_width, int splits,
+                       float* part_num,
                        float* part_den, void* stream) {
   if (!q || !state_num || !state_den || !feat_index || !part_num || !part_den) return STA_ERR_ARG;
+  if (index_width != 4 && index_width != 8) return STA_ERR_ARG;
   if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
   if (streams <= 0 || d <= 0 || dv <= 0 || n_feat <= 0 || splits <= 0 || splits > n_feat) return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
@@ -384,8 +411,12 @@ int sta_decode_moments(const void* q, int dtype, int64_t streams, int d, int dv,
   a.q = q; a.dtype = dtype; a.d = d; a.scale = scale; a.state_num = state_num; a.state_den = state_den;
   a.n_feat = n_feat; a.ldm = 32 * ((dv + 31) / 32); a.rowfeat = feat_index; a.splits = splits;
   a.rows_per_split = (n_feat + splits - 1) / splits; a.part_num = part_num; a.part_den = part_den;
-  hipLaunchKernelGGL(sta::decode_moments_kernel, dim3(static_cast<unsigned>(grid)), dim3(sta::DEC_THREADS), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (index_width == 8)
+    hipLaunchKernelGGL(sta::decode_moments_kernel<true>, dim3(static_cast<unsigned>(grid)), dim3(sta::DEC_THREADS), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(sta::decode_moments_kernel<false>, dim3(static_cast<unsigned>(grid)), dim3(sta::DEC_THREADS), 0,
+                       static_cast<hipStream_t>(stream), a);
   return check_launch();
 }
 
@@ -422,14 +453,18 @@ int sta_decode_tail(const void* q, const void* k, const void* v, int dtype, int6
   a.out_dtype = out_dtype; a.stats = stats;
   const dim3 grid(static_cast<unsigned>(streams));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int kc = d <= 64 ? 1 : 2;
+  const int kc = d <= 64 ? 1 : (d <= 128 ? 2 : 4);
   const int vc = dv <= 64 ? 1 : (dv <= 128 ? 2 : 4);
-  if (kc == 1 && vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 1>), grid, dim3(sta::DEC_THREADS), 0, s, a);
-  else if (kc == 1 && vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 2>), grid, dim3(sta::DEC_THREADS), 0, s, a);
-  else if (kc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 4>), grid, dim3(sta::DEC_THREADS), 0, s, a);
-  else if (vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 1>), grid, dim3(sta::DEC_THREADS), 0, s, a);
-  else if (vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 2>), grid, dim3(sta::DEC_THREADS), 0, s, a);
-  else hipLaunchKernelGGL((sta::decode_tail_kernel<2, 4>), grid, dim3(sta::DEC_THREADS), 0, s, a);
+  const dim3 blk(sta::DEC_THREADS);
+  if (kc == 1 && vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 1>), grid, blk, 0, s, a);
+  else if (kc == 1 && vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 2>), grid, blk, 0, s, a);
+  else if (kc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<1, 4>), grid, blk, 0, s, a);
+  else if (kc == 2 && vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 1>), grid, blk, 0, s, a);
+  else if (kc == 2 && vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 2>), grid, blk, 0, s, a);
+  else if (kc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<2, 4>), grid, blk, 0, s, a);
+  else if (vc == 1) hipLaunchKernelGGL((sta::decode_tail_kernel<4, 1>), grid, blk, 0, s, a);
+  else if (vc == 2) hipLaunchKernelGGL((sta::decode_tail_kernel<4, 2>), grid, blk, 0, s, a);
+  else hipLaunchKernelGGL((sta::decode_tail_kernel<4, 4>), grid, blk, 0, s, a);
   return check_launch();
 }
 
@@ -437,7 +472,8 @@ int64_t sta_static_scratch_bytes(void) { return STA_STATIC_SCRATCH_BYTES; }
 
 int sta_decode_step_static(const void* q, const void* k, const void* v, int dtype, int64_t streams, int d, int dv,
                            int degree, float scale, float eps, int flags, const float* state_num,
-                           const float* state_den, int n_feat, const uint32_t* feat_index, int splits, float* buf_k,
+                           const float* state_den, int n_feat, const void* feat_index, int index_width, int splits,
+                           float* buf_k,
                            float* buf_v, int block, int buf_len, const float* lev_k, const float* lev_v,
                            const float* lev_w, int n_levels, int level_size, uint64_t level_mask, void* out,
                            int out_dtype, float* stats, void* stream) {
@@ -461,7 +497,8 @@ int sta_decode_step_static(const void* q, const void* k, const void* v, int dtyp
   float* part_num = base;
   float* part_den = base + den_off;
   if (state_num) {
-    st = sta_decode_moments(q, dtype, streams, d, dv, scale, state_num, state_den, n_feat, feat_index, splits,
+    st = sta_decode_moments(q, dtype, streams, d, dv, scale, state_num, state_den, n_feat, feat_index, index_width,
+                            splits,
                             part_num, part_den, stream);
   } else {
     // no moment state (every token answered from the buffer): zero partials, cleared by a kernel so
@@ -478,10 +515,13 @@ int sta_decode_step_static(const void* q, const void* k, const void* v, int dtyp
 
 int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, const float* buf_v, int block, int pos0,
                         float* lev_k, float* lev_v, float* lev_w, int32_t* lev_pos, int n_levels, int level_size,
-                        int n_calls, const int32_t* methods, const float* dirs, const float* unif,
-                        const int32_t* perms, int max_in, void* stream) {
+                        int n_calls, const int32_t* methods, const void* dirs, const void* unif,
+                        const int32_t* perms, int max_in, int score_f64, const double* buf_k64, double* lev_k64,
+                        void* stream) {
   if (!buf_k || !buf_v || !lev_k || !lev_v || !lev_w || !lev_pos || !methods || !dirs || !unif || !perms)
     return STA_ERR_ARG;
+  if (score_f64 != 0 && score_f64 != 1) return STA_ERR_ARG;
+  if (score_f64 && (!buf_k64 || !lev_k64)) return STA_ERR_ARG;
   if (streams <= 0 || d <= 0 || dv <= 0 || block < 2 || pos0 < 0 || n_levels <= 0 || level_size <= 0)
     return STA_ERR_SHAPE;
   if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;
@@ -498,7 +538,8 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
   a.buf_k = buf_k; a.buf_v = buf_v; a.B = block; a.d = d; a.dk = dk; a.ldv = ldv; a.pos0 = pos0;
   a.lev_k = lev_k; a.lev_v = lev_v; a.lev_w = lev_w; a.lev_pos = lev_pos; a.L = n_levels; a.m = level_size;
   a.n_calls = n_calls; a.methods = methods; a.dirs = dirs; a.unif = unif; a.perms = perms; a.max_in = max_in;
-  const size_t smem = sizeof(float) * static_cast<size_t>(sta::dec_cmp_smem_floats(max_in));
+  a.f64 = score_f64; a.buf_k64 = buf_k64; a.lev_k64 = lev_k64;
+  const size_t smem = sizeof(float) * static_cast<size_t>(sta::dec_cmp_smem_floats(max_in, score_f64 != 0));
   const int st = lds_limit(reinterpret_cast<const void*>(sta::decode_compress_kernel), smem);
   if (st != STA_OK) return st;
   hipLaunchKernelGGL(sta::decode_compress_kernel, dim3(static_cast<unsigned>(streams)), dim3(sta::CMP_THREADS), smem,
@@ -507,11 +548,12 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
 }
 
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
-                       int n_batch, const int32_t* node_desc, int n_nodes, int cap, const float* dirs,
-                       const float* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
+                       int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
+                       const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
                        float* node_w, void* stream) {
   if (!k || !batch_nodes || !node_desc || !node_src || !node_w) return STA_ERR_ARG;
-  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  const bool f64 = dtype == STA_F64;
+  if (!dtype_ok(dtype) && !f64) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || n_nodes <= 0 || cap <= 0 || max_in <= 0) return STA_ERR_SHAPE;
   if (d > kMaxD || max_in > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
   if (n_batch <= 0) return STA_OK;
@@ -520,8 +562,8 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
   sta::CompressArgs a;
   a.k = k; a.dtype = dtype; a.n = n; a.d = d; a.batch = batch_nodes; a.desc = node_desc; a.n_nodes = n_nodes;
   a.cap = cap; a.dirs = dirs; a.unif = unif; a.perms = perms; a.n_draws = n_draws; a.max_in = max_in;
-  a.node_src = node_src; a.node_w = node_w;
-  const size_t smem = sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in));
+  a.node_src = node_src; a.node_w = node_w; a.f64 = f64 ? 1 : 0;
+  const size_t smem = sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in, f64));
   const int st = lds_limit(reinterpret_cast<const void*>(sta::compress_kernel), smem);
   if (st != STA_OK) return st;
   hipLaunchKernelGGL(sta::compress_kernel, dim3(static_cast<unsigned>(n_batch), static_cast<unsigned>(bh)),
@@ -592,7 +634,8 @@ int sta_block_attention(const void* q, const void* k, const void* v, int dtype, 
   if (d <= 16) return f32 ? dispatch_dvt<16, 4>(a, bh, s) : dispatch_dvt<16, 2>(a, bh, s);
   if (d <= 32) return f32 ? dispatch_dvt<32, 4>(a, bh, s) : dispatch_dvt<32, 2>(a, bh, s);
   if (d <= 64) return f32 ? dispatch_dvt<64, 4>(a, bh, s) : dispatch_dvt<64, 2>(a, bh, s);
-  return f32 ? dispatch_dvt<128, 4>(a, bh, s) : dispatch_dvt<128, 2>(a, bh, s);
+  if (d <= 128) return f32 ? dispatch_dvt<128, 4>(a, bh, s) : dispatch_dvt<128, 2>(a, bh, s);
+  return f32 ? dispatch_dvt<256, 4>(a, bh, s) : dispatch_dvt<256, 2>(a, bh, s);
 }
 
 int sta_selftest_mfma(const float* a, const float* b, float* d_out) {

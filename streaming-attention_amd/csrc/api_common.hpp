@@ -32,25 +32,37 @@ inline int check_launch() { return hip_status(hipGetLastError()); }
 
 inline bool dtype_ok(int dt) { return dt == STA_F32 || dt == STA_BF16 || dt == STA_F16; }
 
-constexpr int kMaxD = 128;
+// Key width: rows up to 128 dimensions are staged whole; wider keys (up to kMaxD) through dimension
+// windows (MomArgs::win): every feature split stages the 4 blocks of 32 dimensions its monomials use.
+constexpr int kMaxD = 256;
+constexpr int kMaxStagedD = 128;
 constexpr int kMaxDv = 256;
-constexpr int kMaxDegree = 4;
+constexpr int kMaxDegree = 8;
+constexpr int kMaxDegreeWindows = 4;  // a monomial of degree <= 4 touches at most the 4 blocks of a window
+constexpr int kMaxDHighDegree = 64;   // degree >= 5 (NX >= 3): rows of at most 64 dimensions
 constexpr int kTileRows = 128;
+constexpr int kMaxFlashD = 128;  // the exact flash baseline (the reference's Triton bound)
 
-// Per-wave tile counts the moment kernels are instantiated for, per (degree 3, d > 64).  Every entry
-// must appear in STA_MOMENT_CONFIGS.
+// Per-wave tile counts the moment kernels are instantiated for, per (extra factors, d > 64).  Every
+// entry must appear in STA_MOMENT_CONFIGS (or STA_MOMENT_CONFIGS_HI).
 constexpr int kNtD2[] = {2, 4, 5, 9, 16};
 constexpr int kNtD3[] = {4, 8, 16};
 constexpr int kNtBigD2[] = {5, 16};
 constexpr int kNtBigD3[] = {4, 16};
-constexpr int kNtD4[] = {4, 8, 16};  // degree 4: d <= 64 only
+constexpr int kNtD4[] = {4, 8, 16};
+constexpr int kNtBigD4[] = {4, 16};
+constexpr int kNtHi[] = {4};  // degree 5 .. 8: d <= 64, fp32 products
 
 // X(NT, NX, DBIG) for every instantiated moment configuration; NX = extra factors per feature quad
 // (0: degree <= 2, 1: degree 3, 2: degree 4).
 #define STA_MOMENT_CONFIGS(X)                                                                       \
   X(2, 0, false) X(4, 0, false) X(5, 0, false) X(9, 0, false) X(16, 0, false)                       \
   X(4, 1, false) X(8, 1, false) X(16, 1, false) X(5, 0, true) X(16, 0, true)                        \
-  X(4, 1, true) X(16, 1, true) X(4, 2, false) X(8, 2, false) X(16, 2, false)
+  X(4, 1, true) X(16, 1, true) X(4, 2, false) X(8, 2, false) X(16, 2, false)                        \
+  X(4, 2, true) X(16, 2, true)
+
+// Degrees 5 .. 8 (NX = 3 .. 6): fp32 products only (the fp32-product scan and accumulation).
+#define STA_MOMENT_CONFIGS_HI(X) X(4, 3, false) X(4, 4, false) X(4, 5, false) X(4, 6, false)
 
 // X(NTS, NX, DBIG) of the wave-specialised moment kernels (moments_ws_kernel; split-bf16 products,
 // degree <= 3): tiles per slot, extra factors per quad, d > 64.
@@ -79,11 +91,14 @@ inline bool moment_columns64_ok(int d, int degree, int dv, int wave_tiles, int p
 // extra factors per feature quad of a degree (the NX of the moment kernels)
 inline int moment_extra_factors(int degree) { return degree <= 2 ? 0 : degree - 2; }
 
+// d: the staged (virtual) key width, at most kMaxStagedD.
 inline int moment_wave_tiles(int d, int degree, int want) {
   if (want < 1) want = 1;
   const int nx = moment_extra_factors(degree);
   const bool big = d > 64;
-  if (nx >= 2) return big ? -1 : next_nt(kNtD4, want);
+  if (d > kMaxStagedD) return -1;
+  if (nx >= 3) return big ? -1 : next_nt(kNtHi, want);
+  if (nx == 2) return big ? next_nt(kNtBigD4, want) : next_nt(kNtD4, want);
   if (!big) return nx ? next_nt(kNtD3, want) : next_nt(kNtD2, want);
   return nx ? next_nt(kNtBigD3, want) : next_nt(kNtBigD2, want);
 }

@@ -88,21 +88,26 @@ __device__ __forceinline__ int64_t residual_start(int64_t i, int mode, int block
 // The logits come out in base 2: the staged queries carry scale * log2(e), so y = x log2(e) for the
 // natural logit x, exp(x) = exp2(y) on the hardware exp2 (about 1 ulp; the fused residual needs the
 // difference exp(x) - exp_{<=t}(x) to the 1e-4 relative tolerance of the outputs, not correct rounding)
-// and the Taylor truncation sum_{r<=deg} x^r / r! (deg <= 4) is the Horner form in y,
-// 1 + y (k1 + y (k2 + y (k3 + y k4))) with k_r = (ln 2)^r / r! for r <= deg and 0 above, within a few
+// and the Taylor truncation sum_{r<=deg} x^r / r! (deg <= 8) is the Horner form in y,
+// 1 + y (k1 + y (k2 + y (k3 + ...))) with k_r = (ln 2)^r / r! for r <= deg and 0 above, within a few
 // ulp of the reference's term-by-term sum.  D4: the fp32-product kernel, which serves degree 4, takes
-// the fourth fused multiply-add; the split-product kernel stops at degree 3 (three for every degree;
-// sta_block_attention rejects split products with degree 4).
+// the fourth fused multiply-add; HD: its high-degree instantiation (degree 5 .. 8) the eighth; the
+// split-product kernel stops at degree 3 (three for every degree; sta_block_attention rejects split
+// products with degree 4 or more).
 struct TaylorCoef2 {
-  float k1, k2, k3, k4;
+  float k1, k2, k3, k4, k5, k6, k7, k8;
 };
 __host__ __device__ inline TaylorCoef2 taylor_coef2(int deg) {
   return TaylorCoef2{deg >= 1 ? 0.693147180560f : 0.f, deg >= 2 ? 0.240226506959f : 0.f,
-                     deg >= 3 ? 0.0555041086648f : 0.f, deg >= 4 ? 0.00961812910763f : 0.f};
+                     deg >= 3 ? 0.0555041086648f : 0.f, deg >= 4 ? 0.00961812910763f : 0.f,
+                     deg >= 5 ? 1.33335581464e-3f : 0.f, deg >= 6 ? 1.54035303934e-4f : 0.f,
+                     deg >= 7 ? 1.52527338041e-5f : 0.f, deg >= 8 ? 1.32154867902e-6f : 0.f};
 }
-template <bool D4>
+template <bool D4, bool HD = false>
 __device__ __forceinline__ float taylor2(float y, const TaylorCoef2& c) {
-  const float t3 = D4 ? fmaf(y, c.k4, c.k3) : c.k3;
+  float t4 = c.k4;
+  if constexpr (HD) t4 = fmaf(y, fmaf(y, fmaf(y, fmaf(y, c.k8, c.k7), c.k6), c.k5), c.k4);
+  const float t3 = (D4 || HD) ? fmaf(y, t4, c.k3) : c.k3;
   return fmaf(y, fmaf(y, fmaf(y, t3, c.k2), c.k1), 1.0f);
 }
 constexpr float LOG2E = 1.44269504f;
@@ -147,7 +152,8 @@ __host__ __device__ constexpr int split_key_pos(int r) {
 // KVX (split products, bf16 inputs): the key and value rows are exact in bf16, so their lo planes are
 // zero: the products with them (kl·qh in X, vl·ph in num) and the lo planes themselves are left out
 // (X and num are those of the three-product form, bit for bit).
-template <int DP, int DVT, int RS, int ES, bool SPLIT, bool KVX = false>
+// HD (fp32 products only): the Taylor polynomial through degree 8 (degree 5 .. 8).
+template <int DP, int DVT, int RS, int ES, bool SPLIT, bool KVX = false, bool HD = false>
 __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_kernel(const BlockArgs a) {
   constexpr int KB = block_kb(DP, DVT);  // keys per LDS stage
   constexpr int NSUB = KB / 16;                         // 16-key subtiles per stage
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
           const int i = myrow[rs];
           const float yv = X[rs][r];
           const float ex = __builtin_amdgcn_exp2f(FAST ? yv : fminf(yv, ymax));
-          const float tp = FAST ? fmaf(yv, fmaf(yv, tc.k2, tc.k1), 1.0f) : taylor2<!SPLIT>(yv, tc);
+          const float tp = FAST ? fmaf(yv, fmaf(yv, tc.k2, tc.k1), 1.0f) : taylor2<!SPLIT, HD>(yv, tc);
           float p;
           if constexpr (FULL) {
             p = (ex - tp) * w;  // rows outside the sequence have zero queries and are never stored

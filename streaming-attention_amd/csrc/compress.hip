@@ -15,6 +15,13 @@
 // first with probability w_a / max(w_a + w_b, 1e-30) (u_p < prob); the kept item carries w_a + w_b;
 // an odd last item is kept with its own weight.
 //
+// float64 scoring (f64 = 1): the reference runs a float64 caller's compress calls in float64
+// (directions and uniforms drawn as float64, scores keys @ direction in float64,
+// fast_article_attention.py:339-348, streaming_taylor_coreset_attention.py:441-457).  The kernels then
+// read the float64 key rows, the float64 direction and uniforms, keep the full fp64 score (rounded fp64
+// products added in index order) as a 64-bit sort key and decide u < w_a / max(w_a + w_b, 1e-30) in
+// fp64.
+//
 // A node is latency-bound work for one workgroup: every thread scores its own items straight from
 // the key rows (16-byte loads, fp64 chain in dimension order), then the sorted order comes from one
 // rank computation per item (count of smaller keys plus equal keys at lower positions), so the whole
@@ -28,16 +35,22 @@ enum NodeMethod : int { M_COPY = 0, M_SORTED_PAIR = 1, M_PERM = 2 };
 constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, n_out of child a (merge)
 constexpr int CMP_MAX_IN = 4096;
 constexpr int CMP_THREADS = 256;
+constexpr int CMP_MAX_D = 256;  // key width the direction buffer holds
 
 // Dynamic LDS of compress_kernel for calls of at most max_in items (M = max_in rounded up to 4):
-// sort keys [M] (16-byte aligned, padded for 4-wide reads), source indices [M], weights [M], sorted
-// positions [M], projection direction [128].
+// sort keys [M] (16-byte aligned, padded for 4-wide reads; [2M] as 64-bit keys with f64), source
+// indices [M], weights [M], sorted positions [M], projection direction [CMP_MAX_D] floats (doubles
+// with f64).
 __host__ __device__ constexpr int cmp_round4(int n) { return (n + 3) & ~3; }
-__host__ __device__ constexpr int cmp_smem_floats(int max_in) { return 4 * cmp_round4(max_in) + 128; }
-// decode_compress_kernel: sort keys, input handles, weights, positions, sorted positions [M] each, the
-// running output's handles, weights, positions [M/2 + 1 rounded up to 4] each, direction [128].
-__host__ __device__ constexpr int dec_cmp_smem_floats(int max_in) {
-  return 5 * cmp_round4(max_in) + 3 * cmp_round4(max_in / 2 + 1) + 128;
+__host__ __device__ constexpr int cmp_key_floats(int max_in, bool f64) { return (f64 ? 2 : 1) * cmp_round4(max_in); }
+__host__ __device__ constexpr int cmp_smem_floats(int max_in, bool f64 = false) {
+  return cmp_key_floats(max_in, f64) + 3 * cmp_round4(max_in) + (f64 ? 2 : 1) * CMP_MAX_D;
+}
+// decode_compress_kernel: sort keys (as above), input handles, weights, positions, sorted positions [M]
+// each, the running output's handles, weights, positions [M/2 + 1 rounded up to 4] each, direction.
+__host__ __device__ constexpr int dec_cmp_smem_floats(int max_in, bool f64 = false) {
+  return cmp_key_floats(max_in, f64) + 4 * cmp_round4(max_in) + 3 * cmp_round4(max_in / 2 + 1) +
+         (f64 ? 2 : 1) * CMP_MAX_D;
 }
 
 struct CompressArgs {
@@ -49,13 +62,14 @@ struct CompressArgs {
   const int32_t* desc;   // [n_nodes][NODE_DESC]
   int n_nodes;
   int cap;
-  const float* dirs;      // [BH][n_draws][d]
-  const float* unif;      // [BH][n_draws][max_in / 2]
+  const void* dirs;       // [BH][n_draws][d] float (double with f64)
+  const void* unif;       // [BH][n_draws][max_in / 2] float (double with f64)
   const int32_t* perms;   // [BH][n_draws][max_in]
   int n_draws;
   int max_in;
   int32_t* node_src;  // [BH][n_nodes][cap]
   float* node_w;      // [BH][n_nodes][cap]
+  int f64;            // 1: k is float64 [BH][n][d], draws float64 (float64 scoring)
 };
 
 // A bf16 / fp16 element from its 16 bits.
@@ -216,15 +230,77 @@ __device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int t
 __device__ __forceinline__ bool pair_keeps_first(float u, float wa, float wb) {
   return u < __fdiv_rn(wa, fmaxf(wa + wb, 1e-30f));
 }
+// The same in fp64 (float64 scoring: float64 uniforms; the weights are integers or products of n/m
+// factors held in fp32, converted exactly).
+__device__ __forceinline__ bool pair_keeps_first64(double u, float wa, float wb) {
+  const double a = static_cast<double>(wa), b = static_cast<double>(wb);
+  return u < a / fmax(a + b, 1e-30);
+}
+
+// Projection score of one float64 row: each fp64 product rounded, then added, in dimension order (no
+// fused multiply-add, so the score is a fixed function of the inputs; 16-byte loads of two elements
+// when `vec`).
+__device__ __forceinline__ double fp64_mul_add(double acc, double x, double y) { return __dadd_rn(acc, __dmul_rn(x, y)); }
+__device__ __forceinline__ double projection_score64(const double* row, int d, bool vec, const double* dir) {
+  double acc = 0.0;
+  if (vec) {
+    const double2* r = reinterpret_cast<const double2*>(row);
+    const int nu = d / 2;
+    for (int u0 = 0; u0 < nu; u0 += 8) {
+      double2 x[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (u0 + t < nu) x[t] = r[u0 + t];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (u0 + t < nu) {
+          acc = fp64_mul_add(acc, x[t].x, dir[2 * (u0 + t)]);
+          acc = fp64_mul_add(acc, x[t].y, dir[2 * (u0 + t) + 1]);
+        }
+      }
+    }
+  } else {
+    for (int col = 0; col < d; ++col) acc = fp64_mul_add(acc, row[col], dir[col]);
+  }
+  return acc;
+}
+
+// 64-bit unsigned key whose order is the double order (-0 = +0; NaN above everything).
+__device__ __forceinline__ uint64_t sort_key64(double f) {
+  if (f == 0.0) return 0x8000000000000000ull;
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(f));
+  if ((u & 0x7fffffffffffffffull) > 0x7ff0000000000000ull) return 0xffffffffffffffffull;
+  return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// Stable ascending order of n 64-bit keys (ties by position), the rule of rank_sort without its
+// banded fast path: every thread counts, for each of its items, the keys below it and the equal keys
+// at lower positions (float64 scoring only).  Two barriers.
+__device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int n, int tid, int nthreads) {
+  __syncthreads();
+  for (int i = tid; i < n; i += nthreads) {
+    const uint64_t me = uk[i];
+    int r = 0;
+    for (int j = 0; j < n; ++j) {
+      const uint64_t o = uk[j];
+      r += (o < me || (o == me && j < i)) ? 1 : 0;
+    }
+    pos_s[r] = i;
+  }
+  __syncthreads();
+}
 
 __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
   extern __shared__ __align__(16) float cmp_smem[];
   const int M = cmp_round4(a.max_in);
+  const bool f64 = a.f64 != 0;
+  const int KA = cmp_key_floats(a.max_in, f64);
   float* key_s = cmp_smem;
-  int* src_s = reinterpret_cast<int*>(cmp_smem + M);
-  float* w_s = cmp_smem + 2 * M;
-  int* pos_s = reinterpret_cast<int*>(cmp_smem + 3 * M);
-  float* dir_s = cmp_smem + 4 * M;
+  int* src_s = reinterpret_cast<int*>(cmp_smem + KA);
+  float* w_s = cmp_smem + KA + M;
+  int* pos_s = reinterpret_cast<int*>(cmp_smem + KA + 2 * M);
+  float* dir_s = cmp_smem + KA + 3 * M;  // 8-byte aligned: KA and M are multiples of 4
+  double* dir64_s = reinterpret_cast<double*>(dir_s);
 
   const int node = a.batch[blockIdx.x];
   const int64_t bh = blockIdx.y;
@@ -240,15 +316,21 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   // ---- gather the input item list; in the same round trip the projection direction and the uniforms
   //      of this thread's first two pairs ----
   const bool pairs = method == M_SORTED_PAIR;
-  const float* u = a.unif + (bh * a.n_draws + slot) * (a.max_in / 2);
+  const int64_t uoff = (bh * a.n_draws + slot) * (a.max_in / 2);
+  const float* u = static_cast<const float*>(a.unif) + uoff;
+  const double* u64 = static_cast<const double*>(a.unif) + uoff;
   const int pc = n_in / 2;
-  float u_first[2] = {0.f, 0.f};
+  double u_first[2] = {0.0, 0.0};  // a float uniform converts exactly
   if (pairs) {
-    const float* dir = a.dirs + (bh * a.n_draws + slot) * a.d;
-    for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = dir[e];
+    const int64_t doff = (bh * a.n_draws + slot) * a.d;
+    if (f64) {
+      for (int e = tid; e < a.d; e += CMP_THREADS) dir64_s[e] = static_cast<const double*>(a.dirs)[doff + e];
+    } else {
+      for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = static_cast<const float*>(a.dirs)[doff + e];
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r)
-      if (tid + r * CMP_THREADS < pc) u_first[r] = u[tid + r * CMP_THREADS];
+      if (tid + r * CMP_THREADS < pc) u_first[r] = f64 ? u64[tid + r * CMP_THREADS] : u[tid + r * CMP_THREADS];
   }
   if (kind == KIND_RAW) {
     for (int i = tid; i < n_in; i += CMP_THREADS) {
@@ -286,27 +368,36 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   }
 
   // ---- sorted_pair: projection scores (fp64 accumulation, fixed index order), one item per thread ----
-  const int epu = a.dtype == F32 ? 4 : 8;
-  const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
-  for (int i = tid; i < n_in; i += 2 * CMP_THREADS) {  // items i and i + CMP_THREADS together
-    const int i1 = i + CMP_THREADS;
-    const bool two = i1 < n_in;
-    float s0, s1;
-    projection_scores2(a.k, (bh * a.n + src_s[i]) * a.d, a.k, (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d,
-                       a.dtype, vec, dir_s, s0, s1);
-    key_s[i] = s0;
-    if (two) key_s[i1] = s1;
+  if (f64) {
+    const double* k64 = static_cast<const double*>(a.k);
+    const bool vec64 = (a.d % 2) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
+    uint64_t* uk = reinterpret_cast<uint64_t*>(key_s);
+    for (int i = tid; i < n_in; i += CMP_THREADS)
+      uk[i] = sort_key64(projection_score64(k64 + (bh * a.n + src_s[i]) * a.d, a.d, vec64, dir64_s));
+    rank_sort64(uk, pos_s, n_in, tid, CMP_THREADS);
+  } else {
+    const int epu = a.dtype == F32 ? 4 : 8;
+    const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
+    for (int i = tid; i < n_in; i += 2 * CMP_THREADS) {  // items i and i + CMP_THREADS together
+      const int i1 = i + CMP_THREADS;
+      const bool two = i1 < n_in;
+      float s0, s1;
+      projection_scores2(a.k, (bh * a.n + src_s[i]) * a.d, a.k, (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d,
+                         a.dtype, vec, dir_s, s0, s1);
+      key_s[i] = s0;
+      if (two) key_s[i1] = s1;
+    }
+    // ---- stable ascending order of (score, position) ----
+    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
   }
-
-  // ---- stable ascending order of (score, position) ----
-  rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
 
   // ---- pair selection with weight transfer ----
   for (int p = tid; p < pc; p += CMP_THREADS) {
     const int ia2 = pos_s[2 * p], ib2 = pos_s[2 * p + 1];
     const float wa = w_s[ia2], wb = w_s[ib2];
     const int r = (p - tid) / CMP_THREADS;
-    const bool choose_a = pair_keeps_first(r < 2 ? u_first[r] : u[p], wa, wb);
+    const bool choose_a = f64 ? pair_keeps_first64(r < 2 ? u_first[r] : u64[p], wa, wb)
+                              : pair_keeps_first(r < 2 ? static_cast<float>(u_first[r]) : u[p], wa, wb);
     a.node_src[obase + p] = choose_a ? src_s[ia2] : src_s[ib2];
     a.node_w[obase + p] = wa + wb;
   }

@@ -28,7 +28,7 @@ namespace sta {
 
 constexpr int DEC_THREADS = 256;
 constexpr int DEC_GROUPS = DEC_THREADS / 16;  // items in flight per workgroup pass (16 lanes per item)
-constexpr int DEC_MAX_X = 136;                // staged query features x[0..d] (d <= 128) plus zeros
+constexpr int DEC_MAX_X = 260;                // staged query features x[0..d] (d <= 256) plus zeros
 
 enum DecFlags : int { DEC_APPEND = 1, DEC_CURRENT = 2, DEC_QUERY = 4 };
 
@@ -45,13 +45,31 @@ struct DecMomArgs {
   const float* state_den;  // [S][n_feat]
   int n_feat;
   int ldm;                  // a multiple of 32
-  const uint32_t* rowfeat;  // [n_feat] factors i0 | i1 << 8 | i2 << 16 | i3 << 24 of x = [s q, 1] (index d = 1)
+  // the factors of every feature in x = [s q, 1] (index d = 1): WIDE = false: [n_feat] uint32 i0 | i1 << 8 |
+  // i2 << 16 | i3 << 24 (d < 255, degree <= 4); WIDE = true: [n_feat][8] uint16 (any d, degree <= 8)
+  const void* rowfeat;
   int splits;
   int rows_per_split;
   float* part_num;  // [S][splits][ldm]
   float* part_den;  // [S][splits]
 };
 
+template <bool WIDE>
+__device__ __forceinline__ float dec_feature(const DecMomArgs& a, const float* xs, int row) {
+  if constexpr (WIDE) {
+    const uint4 w = static_cast<const uint4*>(a.rowfeat)[row];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float ph = 1.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ph *= xs[(ws[j >> 1] >> (16 * (j & 1))) & 0xffffu];
+    return ph;
+  } else {
+    const uint32_t pf = static_cast<const uint32_t*>(a.rowfeat)[row];
+    return xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u] * xs[pf >> 24];
+  }
+}
+
+template <bool WIDE>
 __global__ __launch_bounds__(DEC_THREADS) void decode_moments_kernel(const DecMomArgs a) {
   __shared__ float xs[DEC_MAX_X];
   __shared__ floatx4 red[DEC_THREADS];
@@ -85,8 +103,7 @@ __global__ __launch_bounds__(DEC_THREADS) void decode_moments_kernel(const DecMo
         // the state is streamed once per step: non-temporal loads keep it from displacing cached data
         S[u] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(sn + static_cast<int64_t>(rr) * a.ldm));
         D[u] = __builtin_nontemporal_load(sd + rr);
-        const uint32_t pf = a.rowfeat[rr];
-        const float ph = xs[pf & 255u] * xs[(pf >> 8) & 255u] * xs[(pf >> 16) & 255u] * xs[pf >> 24];
+        const float ph = dec_feature<WIDE>(a, xs, rr);
         phi[u] = row < f1 ? ph : 0.f;
       }
 #pragma unroll
@@ -185,17 +202,26 @@ __device__ __forceinline__ float dec_dot(const floatx4 (&x)[KC], const floatx4 (
 }
 
 // exp(z) on the hardware exp2 (about 1 ulp) and the Taylor truncation sum_{r<=deg} z^r / r! by Horner
-// (c1..c3 = [deg >= r] / r!): the residual exp - exp_{<=t} and the buffered tokens' exp need 1e-5
+// (c_r = [deg >= r] / r!, r <= 8): the residual exp - exp_{<=t} and the buffered tokens' exp need 1e-5
 // relative, not the reference's term-by-term rounding.
 struct DecTaylor {
-  float c1, c2, c3, c4;
+  float c[9];
 };
 __device__ __forceinline__ DecTaylor dec_taylor(int deg) {
-  return DecTaylor{deg >= 1 ? 1.f : 0.f, deg >= 2 ? 0.5f : 0.f, deg >= 3 ? 0.166666672f : 0.f,
-                   deg >= 4 ? 0.0416666679f : 0.f};
+  DecTaylor t;
+  float f = 1.f;
+#pragma unroll
+  for (int r = 0; r <= 8; ++r) {
+    if (r > 0) f /= static_cast<float>(r);
+    t.c[r] = r <= deg ? f : 0.f;
+  }
+  return t;
 }
 __device__ __forceinline__ float dec_tp(float z, const DecTaylor& t) {
-  return fmaf(z, fmaf(z, fmaf(z, fmaf(z, t.c4, t.c3), t.c2), t.c1), 1.f);
+  float p = t.c[8];
+#pragma unroll
+  for (int r = 7; r >= 0; --r) p = fmaf(z, p, t.c[r]);
+  return p;
 }
 __device__ __forceinline__ float dec_exp(float z) { return __builtin_amdgcn_exp2f(z * 1.44269504f); }
 
@@ -357,28 +383,39 @@ struct DecCmpArgs {
   int L, m;
   int n_calls;
   const int32_t* methods;  // [n_calls] M_SORTED_PAIR or M_PERM
-  const float* dirs;       // [S][n_calls][d]
-  const float* unif;       // [S][n_calls][max_in / 2]
+  const void* dirs;        // [S][n_calls][d] float (double with f64)
+  const void* unif;        // [S][n_calls][max_in / 2] float (double with f64)
   const int32_t* perms;    // [S][n_calls][max_in]
   int max_in;
+  // float64 scoring (f64 = 1): the key rows' float64 values, [S][B][dk] and [S][L][m][dk], scored in
+  // fp64 against the float64 direction; lev_k64 rows follow lev_k's
+  int f64;
+  const double* buf_k64;
+  double* lev_k64;
 };
 
 __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecCmpArgs a) {
   extern __shared__ __align__(16) float dcmp_smem[];
+  const bool f64 = a.f64 != 0;
   const int M = cmp_round4(a.max_in), H = cmp_round4(a.max_in / 2 + 1);
+  const int KA = cmp_key_floats(a.max_in, f64);
   float* key_s = dcmp_smem;
-  int* in_h = reinterpret_cast<int*>(dcmp_smem + M);
-  float* in_w = dcmp_smem + 2 * M;
-  int* in_p = reinterpret_cast<int*>(dcmp_smem + 3 * M);
-  int* pos_s = reinterpret_cast<int*>(dcmp_smem + 4 * M);
-  int* cur_h = reinterpret_cast<int*>(dcmp_smem + 5 * M);
-  float* cur_w = dcmp_smem + 5 * M + H;
-  int* cur_p = reinterpret_cast<int*>(dcmp_smem + 5 * M + 2 * H);
-  float* dir_s = dcmp_smem + 5 * M + 3 * H;
+  int* in_h = reinterpret_cast<int*>(dcmp_smem + KA);
+  float* in_w = dcmp_smem + KA + M;
+  int* in_p = reinterpret_cast<int*>(dcmp_smem + KA + 2 * M);
+  int* pos_s = reinterpret_cast<int*>(dcmp_smem + KA + 3 * M);
+  int* cur_h = reinterpret_cast<int*>(dcmp_smem + KA + 4 * M);
+  float* cur_w = dcmp_smem + KA + 4 * M + H;
+  int* cur_p = reinterpret_cast<int*>(dcmp_smem + KA + 4 * M + 2 * H);
+  float* dir_s = dcmp_smem + KA + 4 * M + 3 * H;  // 8-byte aligned: KA, M, H are multiples of 4
+  double* dir64_s = reinterpret_cast<double*>(dir_s);
   const int64_t s = blockIdx.x;
   const int tid = threadIdx.x;
   auto key_row = [&](int h) -> const float* {
     return h < a.B ? a.buf_k + (s * a.B + h) * a.dk : a.lev_k + (s * a.L * a.m + (h - a.B)) * a.dk;
+  };
+  auto key_row64 = [&](int h) -> const double* {
+    return h < a.B ? a.buf_k64 + (s * a.B + h) * a.dk : a.lev_k64 + (s * a.L * a.m + (h - a.B)) * a.dk;
   };
   auto val_row = [&](int h) -> const float* {
     return h < a.B ? a.buf_v + (s * a.B + h) * a.ldv : a.lev_v + (s * a.L * a.m + (h - a.B)) * a.ldv;
@@ -426,24 +463,35 @@ __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecC
       m_cur = mo;
     } else {
       // sorted_pair: fp64 projection scores of the input rows, stable ascending sort, pair selection
-      for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = a.dirs[slot * a.d + e];
-      __syncthreads();
-      for (int j = tid; j < n; j += 2 * CMP_THREADS) {  // rows j and j + CMP_THREADS together
-        const int j1 = j + CMP_THREADS;
-        const bool two = j1 < n;
-        float s0, s1;
-        projection_scores2(key_row(in_h[j]), 0, key_row(in_h[two ? j1 : j]), 0, two, a.d, F32, (a.d & 3) == 0, dir_s,
-                           s0, s1);
-        key_s[j] = s0;
-        if (two) key_s[j1] = s1;
+      if (f64) {
+        for (int e = tid; e < a.d; e += CMP_THREADS) dir64_s[e] = static_cast<const double*>(a.dirs)[slot * a.d + e];
+        __syncthreads();
+        uint64_t* uk = reinterpret_cast<uint64_t*>(key_s);
+        for (int j = tid; j < n; j += CMP_THREADS)
+          uk[j] = sort_key64(projection_score64(key_row64(in_h[j]), a.d, (a.dk & 1) == 0, dir64_s));
+        rank_sort64(uk, pos_s, n, tid, CMP_THREADS);
+      } else {
+        for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = static_cast<const float*>(a.dirs)[slot * a.d + e];
+        __syncthreads();
+        for (int j = tid; j < n; j += 2 * CMP_THREADS) {  // rows j and j + CMP_THREADS together
+          const int j1 = j + CMP_THREADS;
+          const bool two = j1 < n;
+          float s0, s1;
+          projection_scores2(key_row(in_h[j]), 0, key_row(in_h[two ? j1 : j]), 0, two, a.d, F32, (a.d & 3) == 0,
+                             dir_s, s0, s1);
+          key_s[j] = s0;
+          if (two) key_s[j1] = s1;
+        }
+        rank_sort(key_s, pos_s, n, tid, CMP_THREADS);
       }
-      rank_sort(key_s, pos_s, n, tid, CMP_THREADS);
-      const float* u = a.unif + slot * (a.max_in / 2);
+      const float* u = static_cast<const float*>(a.unif) + slot * (a.max_in / 2);
+      const double* u64 = static_cast<const double*>(a.unif) + slot * (a.max_in / 2);
       const int pc = n / 2;
       for (int p = tid; p < pc; p += CMP_THREADS) {
         const int ia = pos_s[2 * p], ib = pos_s[2 * p + 1];
         const float wa = in_w[ia], wb = in_w[ib];
-        const int keep = pair_keeps_first(u[p], wa, wb) ? ia : ib;
+        const bool first = f64 ? pair_keeps_first64(u64[p], wa, wb) : pair_keeps_first(u[p], wa, wb);
+        const int keep = first ? ia : ib;
         cur_h[p] = in_h[keep];
         cur_w[p] = wa + wb;
         cur_p[p] = in_p[keep];
@@ -465,6 +513,7 @@ __global__ __launch_bounds__(CMP_THREADS) void decode_compress_kernel(const DecC
   for (int e = tid; e < m_cur * a.dk; e += CMP_THREADS) {
     const int j = e / a.dk, col = e - j * a.dk;
     a.lev_k[(ob + j) * a.dk + col] = key_row(cur_h[j])[col];
+    if (f64) a.lev_k64[(ob + j) * a.dk + col] = key_row64(cur_h[j])[col];
   }
   for (int e = tid; e < m_cur * a.ldv; e += CMP_THREADS) {
     const int j = e / a.ldv, col = e - j * a.ldv;

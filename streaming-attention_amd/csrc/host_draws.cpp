@@ -12,6 +12,8 @@
 // A plain C ABI (no torch types in the signatures).  Built with g++ against libtorch_cpu / libc10 into
 // libstadraws.so, separate from the HIP library.
 
+#include "../../include/stadraws.h"
+
 #include <ATen/ATen.h>
 #include <ATen/CPUGeneratorImpl.h>
 #include <ATen/Parallel.h>
@@ -24,6 +26,7 @@
 #include <mutex>
 #include <string>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -37,10 +40,14 @@ int fail(const std::string& msg) {
   return 1;
 }
 
-// One sequence's calls; rows are zero-filled by the caller where a call draws nothing.
-void replay(at::Generator& g, const int32_t* sizes, int n_calls, int d, int comp, float* dirs, float* unif,
+// One sequence's calls; rows are zero-filled by the caller where a call draws nothing.  The direction
+// and uniforms are drawn in the element type T (float, or double for a float64 caller: the reference
+// draws them in the keys' dtype, fast_article_attention.py:339, :348; streaming_taylor_coreset_attention.py:441,
+// :456), which selects torch's float or double sampling path.
+template <class T>
+void replay(at::Generator& g, const int32_t* sizes, int n_calls, int d, int comp, T* dirs, T* unif,
             int32_t* perms, int max_in) {
-  const auto f32 = at::TensorOptions().dtype(at::kFloat);
+  const auto f32 = at::TensorOptions().dtype(std::is_same<T, double>::value ? at::kDouble : at::kFloat);
   for (int c = 0; c < n_calls; ++c) {
     const int64_t n_in = sizes[c];
     if (comp == COMP_NONE || n_in <= 1) continue;
@@ -53,9 +60,9 @@ void replay(at::Generator& g, const int32_t* sizes, int n_calls, int d, int comp
     }
     at::Tensor dir = at::randn({d}, g, f32);
     dir = dir / at::clamp(at::linalg_vector_norm(dir), 1e-12);
-    std::memcpy(dirs + static_cast<int64_t>(c) * d, dir.data_ptr<float>(), sizeof(float) * d);
+    std::memcpy(dirs + static_cast<int64_t>(c) * d, dir.data_ptr<T>(), sizeof(T) * d);
     at::Tensor u = at::rand({n_in / 2}, g, f32);
-    std::memcpy(unif + static_cast<int64_t>(c) * (max_in / 2), u.data_ptr<float>(), sizeof(float) * (n_in / 2));
+    std::memcpy(unif + static_cast<int64_t>(c) * (max_in / 2), u.data_ptr<T>(), sizeof(T) * (n_in / 2));
   }
 }
 
@@ -67,12 +74,14 @@ struct DrawSet {
   std::vector<at::Generator> gens;  // one per sequence / stream, in order
 };
 
-// Runs every sequence's calls, sequences spread over up to at::get_num_threads() threads.
-int run_calls(DrawSet& set, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in, float* dirs,
-              float* unif, int32_t* perms) {
+// Runs every sequence's calls, sequences spread over up to at::get_num_threads() threads; dirs / unif
+// are float, or double when f64.
+int run_calls(DrawSet& set, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in, int f64,
+              void* dirs, void* unif, int32_t* perms) {
   const int64_t n_seq = static_cast<int64_t>(set.gens.size());
   if (n_calls < 0 || d <= 0 || max_in < 2) return fail("sta_draws: bad sizes");
   if (compressor < COMP_NONE || compressor > COMP_SORTED_PAIR) return fail("sta_draws: bad compressor");
+  if (f64 != 0 && f64 != 1) return fail("sta_draws: bad element type flag");
   for (int c = 0; c < n_calls; ++c)
     if (call_sizes[c] < 0 || call_sizes[c] > max_in) return fail("sta_draws: call size above max_in");
   std::atomic<int> bad{0};
@@ -82,8 +91,12 @@ int run_calls(DrawSet& set, const int32_t* call_sizes, int n_calls, int d, int c
   auto work = [&]() {
     for (int64_t s = next.fetch_add(1); s < n_seq; s = next.fetch_add(1)) {
       try {
-        replay(set.gens[s], call_sizes, n_calls, d, compressor, dirs + s * n_calls * d,
-               unif + s * n_calls * (max_in / 2), perms + s * n_calls * max_in, max_in);
+        if (f64)
+          replay(set.gens[s], call_sizes, n_calls, d, compressor, static_cast<double*>(dirs) + s * n_calls * d,
+                 static_cast<double*>(unif) + s * n_calls * (max_in / 2), perms + s * n_calls * max_in, max_in);
+        else
+          replay(set.gens[s], call_sizes, n_calls, d, compressor, static_cast<float*>(dirs) + s * n_calls * d,
+                 static_cast<float*>(unif) + s * n_calls * (max_in / 2), perms + s * n_calls * max_in, max_in);
       } catch (const std::exception& e) {
         std::lock_guard<std::mutex> lock(mu);
         if (bad.fetch_add(1) == 0) first_err = e.what();
@@ -136,8 +149,16 @@ void sta_draws_close(void* handle) { delete static_cast<DrawSet*>(handle); }
 // compressor: 0 none, 1 random, 2 sorted_pair.  Returns 0, or 1 with sta_draws_error() set.
 int sta_draws_next(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
                    float* dirs, float* unif, int32_t* perms) {
+  return sta_draws_next_typed(handle, call_sizes, n_calls, d, compressor, max_in, 0, dirs, unif, perms);
+}
+
+// sta_draws_next with the directions and uniforms drawn as float64 (f64 = 1; dirs / unif are double
+// tables) or float32 (f64 = 0; float tables).
+int sta_draws_next_typed(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
+                         int f64, void* dirs, void* unif, int32_t* perms) {
   if (!handle) return fail("sta_draws_next: null handle");
-  return run_calls(*static_cast<DrawSet*>(handle), call_sizes, n_calls, d, compressor, max_in, dirs, unif, perms);
+  return run_calls(*static_cast<DrawSet*>(handle), call_sizes, n_calls, d, compressor, max_in, f64, dirs, unif,
+                   perms);
 }
 
 // Bytes of one generator's state (the layout torch.Generator.get_state() returns for a CPU generator).
@@ -185,9 +206,14 @@ int sta_draws_set_state(void* handle, const uint8_t* in) {
 // One-shot form: fresh generators seeded seeds[s], run through the calls, then released.
 int sta_host_draws(const int64_t* seeds, int n_seq, const int32_t* call_sizes, int n_calls, int d, int compressor,
                    int max_in, float* dirs, float* unif, int32_t* perms) {
+  return sta_host_draws_typed(seeds, n_seq, call_sizes, n_calls, d, compressor, max_in, 0, dirs, unif, perms);
+}
+
+int sta_host_draws_typed(const int64_t* seeds, int n_seq, const int32_t* call_sizes, int n_calls, int d,
+                         int compressor, int max_in, int f64, void* dirs, void* unif, int32_t* perms) {
   void* h = sta_draws_open(seeds, n_seq);
   if (!h) return 1;
-  const int st = sta_draws_next(h, call_sizes, n_calls, d, compressor, max_in, dirs, unif, perms);
+  const int st = sta_draws_next_typed(h, call_sizes, n_calls, d, compressor, max_in, f64, dirs, unif, perms);
   sta_draws_close(h);
   return st;
 }

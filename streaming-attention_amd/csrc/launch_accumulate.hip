@@ -30,6 +30,11 @@ int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt
   }
   STA_MOMENT_CONFIGS(STA_CASE)
 #undef STA_CASE
+#define STA_CASE(NT, NX, BIG)                                                                       \
+  if (nt == NT && nx == NX && big == BIG && !split)                                               \
+    return a.esize == 4 ? launch<NT, NX, BIG, 4, false>(a, bh, s) : launch<NT, NX, BIG, 2, false>(a, bh, s);
+  STA_MOMENT_CONFIGS_HI(STA_CASE)
+#undef STA_CASE
   return STA_ERR_UNSUPPORTED;
 }
 

@@ -1,9 +1,9 @@
 // Launch of the residual / combine kernel (block_attn_kernel) for one configuration.  The build compiles
-// this unit once per padded key width DP (16, 32, 64, 128), value-column tile count DVT (1, 2, 4, 8,
-// 16) and element size ES (4: fp32, 2: bf16 / fp16), given as -DSTA_BLOCK_DP=, -DSTA_BLOCK_DVT= and
-// -DSTA_BLOCK_ES=, so the forty configurations compile in parallel; each object holds the fp32-product
-// and the split-bf16-product kernel of its configuration (16-bit objects also the split kernel for bf16
-// key / value rows, which leaves out their zero lo planes).
+// this unit once per padded key width DP (16, 32, 64, 128, 256), value-column tile count DVT (1, 2, 4,
+// 8, 16) and element size ES (4: fp32, 2: bf16 / fp16), given as -DSTA_BLOCK_DP=, -DSTA_BLOCK_DVT= and
+// -DSTA_BLOCK_ES=, so the fifty configurations compile in parallel; each object holds the fp32-product
+// kernel (and its degree 5 .. 8 form) and the split-bf16-product kernel of its configuration (16-bit
+// objects also the split kernel for bf16 key / value rows, which leaves out their zero lo planes).
 #include "api_common.hpp"
 #include "block_attn.hip"
 
@@ -23,6 +23,9 @@ int launch_block(const sta::BlockArgs& a, int64_t bh, hipStream_t s) {
   else if (a.split)
     hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES, true>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
                        s, a);
+  else if (a.degree > 4)
+    hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES, false, false, true>), dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL((sta::block_attn_kernel<DP, DVT, 2, ES, false>), dim3(static_cast<unsigned>(grid)), dim3(256), 0,
                        s, a);

@@ -50,6 +50,9 @@ int dispatch_moments(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, i
   STA_MOMENT_CONFIGS_64(STA_CASE)
 #else
   STA_MOMENT_CONFIGS(STA_CASE)
+#if !STA_MOM_SPLIT
+  STA_MOMENT_CONFIGS_HI(STA_CASE)
+#endif
 #endif
 #undef STA_CASE
   return STA_ERR_UNSUPPORTED;

@@ -10,7 +10,8 @@
 // Feature layout.  The monomials are grouped in quads x[i0] x[b+s] x[i2] x[i3], s = 0..3, b a multiple of
 // 4 (x[d] = 1 lowers the degree; see feature_tiles in _plan.py), 4 quads per tile of 16 features.  NX:
 // the number of factors besides x[i0] and x[b+s] the instantiation multiplies in (0: degree <= 2,
-// 1: degree 3, 2: degree 4).  The
+// 1: degree 3, ..., 6: degree 8; a quad is one 32-bit word of 8-bit indices i0 | b | i2 | i3, and a
+// second word i4 | i5 | i6 | i7 when NX >= 3).  The
 // tiles are split over `fsplit` workgroups and over the 4 waves of a workgroup, every wave holding
 // exactly NT tiles (the host pads with zero tiles, so the loops are branch-free and fully unrolled).
 // A workgroup also owns one 32-wide group of value columns (csplit = ceil(dv/32) per feature split).
@@ -91,13 +92,19 @@ struct MomArgs {
   int fsplit;             // feature splits (workgroups per head and column group)
   int mixed;              // 1: feature splits fs >= fsplit / 2 hold one tile less per wave (see moments_kernel)
   int csplit;             // 32-column groups
-  const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4] packed (i0 | b << 8 | i2 << 16 | i3 << 24)
+  const uint32_t* quads;  // [fsplit][4 waves][NT tiles][4][mom_quad_words(NX)] packed (i0 | b << 8 | i2 << 16 | i3 << 24,
+                          // then i4 | i5 << 8 | i6 << 16 | i7 << 24)
   const float* fcoef;     // [fsplit][4 waves][NT tiles][16] key-side coefficient, 0 for padding
   float* low_num;         // [BH][fsplit][n + 2*MOM_GUARD][ldo], row r at r + MOM_GUARD
   float* low_den;         // [BH][fsplit][n + 2*MOM_GUARD]
   int ldo;                // low_num row stride: 32 * csplit
-  int ldv;                // row stride of v (elements): a multiple of 32, >= dv; q and k rows are d long
+  int ldv;                // row stride of v (elements): a multiple of 32, >= dv
   int esize;              // bytes per input element (4 or 2)
+  int ldk;                // row stride of q and k (elements): d, or the padded key width with windows
+  // Dimension windows (keys wider than the staged rows): feature split fs stages the d = 128 "virtual"
+  // dimensions 32 b + j (b < 4, j < 32) from the row's dimension win[4 fs + b] + j, and its feature
+  // table indexes those virtual dimensions.  nullptr: virtual dimension = row dimension.
+  const int32_t* win;
   // moment_accumulate_kernel only: persistent state in the reference's feature order
   int64_t head_rows;      // rows between consecutive heads of k / v (>= n)
   const int32_t* rowmap;  // [fsplit][4 waves][NT tiles][16] state row of each feature slot, -1 for padding
@@ -105,6 +112,13 @@ struct MomArgs {
   float* state_den;       // [BH][n_feat]
   int n_feat;
 };
+
+// 32-bit words per feature quad: i0, b and two extra factors in the first, four more in the second
+__host__ __device__ constexpr int mom_quad_words(int nx) { return nx >= 3 ? 2 : 1; }
+// Extra factor e (0 .. 5) of a quad from its words.
+__device__ __forceinline__ int quad_factor(uint32_t w0, uint32_t w1, int e) {
+  return static_cast<int>(((e < 2 ? w0 : w1) >> (e < 2 ? 16 + 8 * e : 8 * (e - 2))) & 255u);
+}
 
 __host__ __device__ constexpr int mom_ldq(bool dbig) { return dbig ? 132 : 68; }
 __host__ __device__ constexpr int mom_krows(bool dbig) { return dbig ? 132 : 68; }
@@ -118,9 +132,9 @@ __host__ __device__ constexpr int mom_smem_floats(bool dbig, int nt, int cg = 32
   return 2 * mom_buf_floats(dbig, cg) + 2 * mom_red_floats(cg) + MOM_WAVES * nt * 16 + 8;
 }
 // Workgroups per compute unit an instantiation is built for (registers <= 256 and LDS <= 80 KiB for 2;
-// the 64-column kernels need 124 KiB of LDS).
-__host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig, int cg = 32) {
-  return (nt <= 5 && !dbig && cg == 32) ? 2 : 1;
+// the 64-column kernels need 124 KiB of LDS; degree >= 5 needs the registers of one).
+__host__ __device__ constexpr int mom_wg_per_cu(int nt, bool dbig, int cg = 32, int nx = 0) {
+  return (nt <= 5 && !dbig && cg == 32 && nx <= 2) ? 2 : 1;
 }
 
 // Chunk staging in registers: 16-byte units (4 fp32 or 8 bf16/fp16 elements).  The host guarantees
@@ -152,23 +166,38 @@ struct MomSlots {
   int v_col[VV];       // first column (within the workgroup's CG) of the unit, or -1 when unused
 };
 
+// Byte offset within a q / k row of the 16-byte unit that holds virtual dimensions [u epu, (u + 1) epu):
+// the identity without windows, else dimension win[b] + j for virtual dimension 32 b + j.
+// Window entries are clamped to [0, ldk - 32], so every staged unit lies in the row whatever the table
+// holds.
+template <int ES>
+__device__ __forceinline__ uint32_t unit_offset(int u, const int32_t* win, int ldk) {
+  constexpr int epu = 16 / ES;
+  if (!win) return static_cast<uint32_t>(u * 16);
+  const int vd = u * epu;
+  const int first = min(max(win[vd >> 5], 0), ldk - 32);
+  return static_cast<uint32_t>((first + (vd & 31)) * ES);
+}
+
+// win: this workgroup's 4 window entries (MomArgs::win + 4 fs), or nullptr.
 template <bool DBIG, int ES, int CG>
-__device__ __forceinline__ MomSlots<DBIG, CG> mom_slots(const MomArgs& a, int col0, int dummy) {
+__device__ __forceinline__ MomSlots<DBIG, CG> mom_slots(const MomArgs& a, int col0, int dummy,
+                                                       const int32_t* win = nullptr) {
   constexpr int LDQ = mom_ldq(DBIG);
   MomSlots<DBIG, CG> sl;
   const int tid = threadIdx.x;
   constexpr int epu = 16 / ES;
-  const int uq = a.d / epu;  // units per q/k row
+  const int uq = a.d / epu;  // units per staged q/k row
 #pragma unroll
   for (int j = 0; j < MomStage<DBIG, CG>::QV; ++j) {
     const int e = tid + MOM_THREADS * j;
     const int t = e / uq, u = e - t * uq;
     sl.q_use[j] = t < MOM_C;
     sl.q_tok[j] = min(t, MOM_C - 1);
-    sl.q_off[j] = static_cast<uint32_t>(u * 16);
+    sl.q_off[j] = unit_offset<ES>(u, win, a.ldk);
     sl.q_lds[j] = t < MOM_C ? t * LDQ + u * epu : dummy;
     const int uk = e >> 5;
-    sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
+    sl.k_off[j] = unit_offset<ES>(min(uk, uq - 1), win, a.ldk);
     sl.k_dim[j] = uk < uq ? uk * epu : -1;
   }
 #pragma unroll
@@ -190,7 +219,7 @@ __host__ __device__ constexpr bool mom_full_slots(bool dbig, int es, int d) { re
 template <bool DBIG, int ES, int CG, bool MASK = true>
 __device__ __forceinline__ void mom_load(MomStage<DBIG, CG>& st, const MomSlots<DBIG, CG>& sl, const MomArgs& a,
                                          const char* qh, const char* kh, const char* vh, int row0) {
-  const uint32_t qrow = static_cast<uint32_t>(a.d * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
+  const uint32_t qrow = static_cast<uint32_t>(a.ldk * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
   const int ktok = row0 + (threadIdx.x & (MOM_C - 1));
   const uint32_t krow = static_cast<uint32_t>(MASK ? clamp_row(ktok, a.n) : ktok);
 #pragma unroll
@@ -335,30 +364,35 @@ __device__ __forceinline__ void mom_reduce_store(const MomArgs& a, const float* 
 }
 
 // Per-lane feature offsets of a wave's NT tiles (constant over the sequence).  Query side: columns of
-// x[i0], x[b..b+3], x[i2] of quad lg in the row-major queries.  Update side: Kt rows of feature li plus
-// the token offset 4 lg (token blocks lg and lg + 4), and the key-side coefficient of feature li.
+// x[i0], x[b..b+3] and the NX extra factors of quad lg in the row-major queries.  Update side: Kt rows of
+// feature li plus the token offset 4 lg (token blocks lg and lg + 4), and the key-side coefficient of
+// feature li.
 template <int NT, int NX>
 struct MomLane {
-  int qa[NT], qb[NT], qc[NX >= 1 ? NT : 1], qe[NX >= 2 ? NT : 1];
-  int ka[NT], kb[NT], kc[NX >= 1 ? NT : 1], ke[NX >= 2 ? NT : 1];
+  static constexpr int NXA = NX > 0 ? NX : 1;
+  int qa[NT], qb[NT], qx[NXA][NT];
+  int ka[NT], kb[NT], kx[NXA][NT];
   float kcoef[NT];
 };
 
 template <int NT, int NX>
 __device__ __forceinline__ MomLane<NT, NX> mom_lane(const MomArgs& a, int64_t tile0, int li, int lg) {
+  constexpr int QW = mom_quad_words(NX);
   MomLane<NT, NX> m;
 #pragma unroll
   for (int kt = 0; kt < NT; ++kt) {
-    const uint32_t pq = a.quads[(tile0 + kt) * 4 + lg];
+    const uint32_t* qq = a.quads + ((tile0 + kt) * 4 + lg) * QW;
+    const uint32_t pq = qq[0], pq1 = QW > 1 ? qq[QW > 1 ? 1 : 0] : 0u;
     m.qa[kt] = static_cast<int>(pq & 255u);
     m.qb[kt] = static_cast<int>((pq >> 8) & 255u);
-    if (NX >= 1) m.qc[NX >= 1 ? kt : 0] = static_cast<int>((pq >> 16) & 255u);
-    if (NX >= 2) m.qe[NX >= 2 ? kt : 0] = static_cast<int>((pq >> 24) & 255u);
-    const uint32_t pk = a.quads[(tile0 + kt) * 4 + (li >> 2)];
+#pragma unroll
+    for (int e = 0; e < NX; ++e) m.qx[e][kt] = quad_factor(pq, pq1, e);
+    const uint32_t* kq = a.quads + ((tile0 + kt) * 4 + (li >> 2)) * QW;
+    const uint32_t pk = kq[0], pk1 = QW > 1 ? kq[QW > 1 ? 1 : 0] : 0u;
     m.ka[kt] = static_cast<int>(pk & 255u) * MOM_LDT + 4 * lg;
     m.kb[kt] = (static_cast<int>((pk >> 8) & 255u) + (li & 3)) * MOM_LDT + 4 * lg;
-    if (NX >= 1) m.kc[NX >= 1 ? kt : 0] = static_cast<int>((pk >> 16) & 255u) * MOM_LDT + 4 * lg;
-    if (NX >= 2) m.ke[NX >= 2 ? kt : 0] = static_cast<int>((pk >> 24) & 255u) * MOM_LDT + 4 * lg;
+#pragma unroll
+    for (int e = 0; e < NX; ++e) m.kx[e][kt] = quad_factor(pk, pk1, e) * MOM_LDT + 4 * lg;
     m.kcoef[kt] = a.fcoef[(tile0 + kt) * 16 + li];
   }
   return m;
@@ -377,14 +411,15 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
     vv[0][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg);
     vv[1][ct] = *reinterpret_cast<const floatx4*>(Vt + (16 * ct + li) * MOM_LDT + 4 * lg + 16);
   }
-  floatx4 fa[2][NT], fb[2][NT], fc[2][NX >= 1 ? NT : 1], fe[2][NX >= 2 ? NT : 1];
+  constexpr int NXA = MomLane<NT, NX>::NXA;
+  floatx4 fa[2][NT], fb[2][NT], fx[2][NXA][NT];
   auto uload = [&](int h) {
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
       fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (NX >= 1) fc[h][NX >= 1 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
-      if (NX >= 2) fe[h][NX >= 2 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
+#pragma unroll
+      for (int x = 0; x < NX; ++x) fx[h][x][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kx[x][kt] + 16 * h);
     }
   };
   uload(0);
@@ -401,8 +436,8 @@ __device__ __forceinline__ void mom_update(floatx4 (&st)[NT][CT], float* den_s, 
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
         float x = fa[h][kt][e] * fb[h][kt][e];
-        if (NX >= 1) x *= fc[h][NX >= 1 ? kt : 0][e];
-        if (NX >= 2) x *= fe[h][NX >= 2 ? kt : 0][e];
+#pragma unroll
+        for (int f = 0; f < NX; ++f) x *= fx[h][f][kt][e];
         x *= m.kcoef[kt];
         if constexpr (DEN) dacc[kt] += x;
 #pragma unroll
@@ -443,15 +478,16 @@ template <int NT, int CT, int NX, bool DEN, class Mid, bool KCOEF = false>
 __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* den_s, const float* Kt,
                                                  const float* Vt, const MomLane<NT, NX>& m, int li, int lg,
                                                  Mid mid) {
-  floatx4 fa[2][NT], fb[2][NT], fc[2][NX >= 1 ? NT : 1], fe[2][NX >= 2 ? NT : 1];
+  constexpr int NXA = MomLane<NT, NX>::NXA;
+  floatx4 fa[2][NT], fb[2][NT], fx[2][NXA][NT];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
       fa[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
       fb[h][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (NX >= 1) fc[h][NX >= 1 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
-      if (NX >= 2) fe[h][NX >= 2 ? kt : 0] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
+#pragma unroll
+      for (int x = 0; x < NX; ++x) fx[h][x][kt] = *reinterpret_cast<const floatx4*>(Kt + m.kx[x][kt] + 16 * h);
     }
   // the staged bf16 planes (mom_store<..., true>, vps_off): column 16 ct + li, tokens tok(lg, 0..7)
   constexpr int CG = 16 * CT;
@@ -472,8 +508,8 @@ __device__ __forceinline__ void mom_update_split(floatx4 (&st)[NT][CT], float* d
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float y = fa[j >> 2][kt][j & 3] * fb[j >> 2][kt][j & 3];
-      if (NX >= 1) y *= fc[j >> 2][NX >= 1 ? kt : 0][j & 3];
-      if (NX >= 2) y *= fe[j >> 2][NX >= 2 ? kt : 0][j & 3];
+#pragma unroll
+      for (int f = 0; f < NX; ++f) y *= fx[j >> 2][f][kt][j & 3];
       if (NX >= 1 || KCOEF) y *= m.kcoef[kt];  // NX = 0: the tile's coefficient is applied by the query
       x[j] = y;
       if constexpr (DEN) dacc += y;
@@ -535,13 +571,14 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
       {
         const float a0 = (NX == 0) ? qrow[16 * tt * LDQ + m.qa[t0]] * m.kcoef[t0] : qrow[16 * tt * LDQ + m.qa[t0]];
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[t0]);
-        const float c0 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? t0 : 0]] : 1.f;
-        const float e0 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? t0 : 0]] : 1.f;
+        float c0[MomLane<NT, NX>::NXA];
+#pragma unroll
+        for (int f = 0; f < NX; ++f) c0[f] = qrow[16 * tt * LDQ + m.qx[f][t0]];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           float y = a0 * b0[s];
-          if (NX >= 1) y *= c0;
-          if (NX >= 2) y *= e0;
+#pragma unroll
+          for (int f = 0; f < NX; ++f) y *= c0[f];
           x[s] = y;
           if constexpr (DEN) dq[tt] = fmaf(y, dn0[s], dq[tt]);
         }
@@ -550,13 +587,14 @@ __device__ __forceinline__ void mom_query_split(floatx4 (&o)[2][2][CT], float (&
         const int u = has1 ? t1 : t0;
         const float a1 = (NX == 0) ? qrow[16 * tt * LDQ + m.qa[u]] * m.kcoef[u] : qrow[16 * tt * LDQ + m.qa[u]];
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[u]);
-        const float c1 = (NX >= 1) ? qrow[16 * tt * LDQ + m.qc[NX >= 1 ? u : 0]] : 1.f;
-        const float e1 = (NX >= 2) ? qrow[16 * tt * LDQ + m.qe[NX >= 2 ? u : 0]] : 1.f;
+        float c1[MomLane<NT, NX>::NXA];
+#pragma unroll
+        for (int f = 0; f < NX; ++f) c1[f] = qrow[16 * tt * LDQ + m.qx[f][u]];
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           float y = a1 * b1[s];
-          if (NX >= 1) y *= c1;
-          if (NX >= 2) y *= e1;
+#pragma unroll
+          for (int f = 0; f < NX; ++f) y *= c1[f];
           x[4 + s] = y;
           if constexpr (DEN) dq[tt] = fmaf(y, dn1[s], dq[tt]);
         }
@@ -621,10 +659,10 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
   const int nchunks = (n + a.shift + MOM_C - 1) / MOM_C;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
   const int first = -a.shift;
-  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
-  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
+  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.ldk * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.ldk * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
-  const MomSlots<DBIG, CG> sl = mom_slots<DBIG, ES, CG>(a, col0, dummy_abs);
+  const MomSlots<DBIG, CG> sl = mom_slots<DBIG, ES, CG>(a, col0, dummy_abs, a.win ? a.win + 4 * fs : nullptr);
 
   // zero both chunk buffers (their padding rows / columns are never written again) and the denominators
   for (int e = tid; e < 2 * BUF; e += MOM_THREADS) smem[e] = 0.f;
@@ -656,7 +694,7 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
     if constexpr (SPLIT) {
       mom_query_split<NT, CT, NX, DEN, LDQ>(o, dq, st, Qs, den_s, m, li, lg);
     } else {
-      float x0[2][TT], x2[2][TT], x3[2][TT];
+      float x0[2][TT], xe[2][MomLane<NT, NX>::NXA][TT];
       floatx4 x1[2][TT], dn[2];
       const float* qrow = Qs + li * LDQ;
       auto qload = [&](int kt, int buf) {
@@ -664,8 +702,8 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
         for (int tt = 0; tt < TT; ++tt) {
           x0[buf][tt] = qrow[16 * tt * LDQ + m.qa[kt]];
           x1[buf][tt] = *reinterpret_cast<const floatx4*>(qrow + 16 * tt * LDQ + m.qb[kt]);
-          if (NX >= 1) x2[buf][tt] = qrow[16 * tt * LDQ + m.qc[NX >= 1 ? kt : 0]];
-          if (NX >= 2) x3[buf][tt] = qrow[16 * tt * LDQ + m.qe[NX >= 2 ? kt : 0]];
+#pragma unroll
+          for (int f = 0; f < NX; ++f) xe[buf][f][tt] = qrow[16 * tt * LDQ + m.qx[f][kt]];
         }
         if constexpr (DEN) dn[buf] = *reinterpret_cast<const floatx4*>(den_s + 16 * kt + 4 * lg);
       };
@@ -679,8 +717,8 @@ __device__ __forceinline__ void moments_body(const MomArgs& a, int64_t bh, int f
 #pragma unroll
           for (int tt = 0; tt < TT; ++tt) {
             float x = x0[cb][tt] * x1[cb][tt][s];
-            if (NX >= 1) x *= x2[cb][tt];
-            if (NX >= 2) x *= x3[cb][tt];
+#pragma unroll
+            for (int f = 0; f < NX; ++f) x *= xe[cb][f][tt];
             if constexpr (DEN) dq[tt] = fmaf(x, dn[cb][s], dq[tt]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) o[cb][tt][ct] = mfma4(x, st[kt][ct][s], o[cb][tt][ct]);
@@ -778,11 +816,11 @@ __device__ __forceinline__ void mom_workgroup(const MomArgs& a, int64_t& bh, int
 // their own), at one workgroup per compute unit (124 KiB of LDS).
 // FULL: mom_full_slots(DBIG, ES, a.d) (the host picks the instantiation).
 template <int NT, int NX, bool DBIG, int ES, bool SPLIT, int CG, bool FULL>
-__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG)) void moments_kernel(const MomArgs a) {
+__global__ __launch_bounds__(MOM_THREADS, mom_wg_per_cu(NT, DBIG, CG, NX)) void moments_kernel(const MomArgs a) {
   int64_t bh;
   int fs, cs;
   mom_workgroup(a, bh, fs, cs);
-  constexpr bool MIX = (NT == 4 || NT == 5) && !DBIG && CG == 32;
+  constexpr bool MIX = (NT == 4 || NT == 5) && !DBIG && CG == 32 && NX <= 2;
   if (MIX && a.mixed && fs >= a.fsplit / 2) {
     constexpr int NTL = MIX ? NT - 1 : NT;
     if (cs == 0)
@@ -855,9 +893,9 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
     }
   }
 
-  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.d * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.ldk * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * ES;
-  const MomSlots<DBIG, 32> sl = mom_slots<DBIG, ES, 32>(a, col0, dummy_abs);
+  const MomSlots<DBIG, 32> sl = mom_slots<DBIG, ES, 32>(a, col0, dummy_abs, a.win ? a.win + 4 * fs : nullptr);
   const int nchunks = static_cast<int>((a.n + MOM_C - 1) / MOM_C);
   for (int e = tid; e < BUF; e += MOM_THREADS) smem[e] = 0.f;  // padding rows / columns stay 0
   for (int c = 0; c < nchunks; ++c) {

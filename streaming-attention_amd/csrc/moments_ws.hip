@@ -156,7 +156,7 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
 template <bool DBIG, int ES, int CG, int STG, bool MASK>
 __device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
                                           const MomArgs& a, const char* qh, int row0) {
-  const uint32_t qrow = static_cast<uint32_t>(a.d * ES);
+  const uint32_t qrow = static_cast<uint32_t>(a.ldk * ES);
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
     const int r = MASK ? clamp_row(row0 + sl.q_tok[j], static_cast<int>(a.n)) : row0 + sl.q_tok[j];
@@ -169,7 +169,7 @@ __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const
                                            const MomArgs& a, const char* kh, const char* vh, int row0) {
   constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
   constexpr bool PAIR16 = WsStage<DBIG, ES, CG, STG>::PAIR16;
-  const uint32_t krow_b = static_cast<uint32_t>(a.d * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
+  const uint32_t krow_b = static_cast<uint32_t>(a.ldk * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
   // the token of unit j: one per thread, or the pair 2 p, 2 p + 1
   auto row = [&](int j) -> uint32_t {
     const int t = row0 + (PAIR || PAIR16 ? 2 * (sl.sidx & 15) + j : sl.sidx & (MOM_C - 1));
@@ -341,8 +341,8 @@ __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[
     for (int h = 0; h < 2; ++h) {
       fa[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.ka[kt] + 16 * h);
       fb[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kb[kt] + 16 * h);
-      if (NX >= 1) fc[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kc[NX >= 1 ? kt : 0] + 16 * h);
-      if (NX >= 2) fe[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.ke[NX >= 2 ? kt : 0] + 16 * h);
+      if (NX >= 1) fc[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kx[0][kt] + 16 * h);
+      if (NX >= 2) fe[b][h] = *reinterpret_cast<const floatx4*>(Kt + m.kx[NX >= 2 ? 1 : 0][kt] + 16 * h);
     }
   };
   load(0);
@@ -391,8 +391,8 @@ __device__ __forceinline__ void ws_qload(WsQOps& o, int u, const float* Qs, cons
     const float* qr = Qs + (li + 16 * tt) * LDQ;
     o.a[tt] = (NX == 0) ? qr[m.qa[u]] * m.kcoef[u] : qr[m.qa[u]];
     o.b[tt] = *reinterpret_cast<const floatx4*>(qr + m.qb[u]);
-    if (NX >= 1) o.c[tt] = qr[m.qc[NX >= 1 ? u : 0]];
-    if (NX >= 2) o.e[tt] = qr[m.qe[NX >= 2 ? u : 0]];
+    if (NX >= 1) o.c[tt] = qr[m.qx[0][u]];
+    if (NX >= 2) o.e[tt] = qr[m.qx[NX >= 2 ? 1 : 0][u]];
   }
 }
 
@@ -592,8 +592,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
                             : nullptr;
   float* const sden = sstate ? sstate + 4 * NTS * CT * 256 : nullptr;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
-  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.d * ES;
-  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.d * ES;
+  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.ldk * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.ldk * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);

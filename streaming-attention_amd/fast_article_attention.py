@@ -157,13 +157,21 @@ def _to_gpu(*tensors: Tensor) -> Tuple[List[Tensor], torch.device]:
 
 def _compute_dtype(t: Tensor) -> torch.dtype:
     """Element type the kernels read: the input's for float32 / bfloat16 / float16; float64 inputs are
-    rounded to float32 (the kernels' arithmetic type; the coreset draws are then the float32 ones) and
-    the callers return float64 outputs."""
+    rounded to float32 (the kernels' arithmetic type) and the callers return float64 outputs, while the
+    coreset compressor scores the float64 keys with float64 draws (_score_keys)."""
     if t.dtype in (torch.float32, torch.bfloat16, torch.float16):
         return t.dtype
     if t.dtype == torch.float64:
         return torch.float32
     raise ValueError(f"dtype {t.dtype} is not supported (use float64, float32, bfloat16 or float16)")
+
+
+def _score_keys(k3: Tensor) -> Optional[Tensor]:
+    """The keys the compressor scores for a float64 caller: the float64 keys themselves, since the
+    reference runs a float64 caller's compress calls in float64 (float64 directions and uniforms, scores
+    keys @ direction in float64; fast_article_attention.py:339-348, streaming_taylor_coreset_attention.py:
+    441-457).  None for the other dtypes (their scores come from the rows the kernels read)."""
+    return k3.contiguous() if k3.dtype == torch.float64 else None
 
 
 @torch.no_grad()
@@ -261,11 +269,13 @@ def _check_compressor(compressor: str, n: int, block_size: int) -> None:
         raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
 
 
-def _run_bh(q3, k3, v3, *, degree, block_size, scale, compressor, seed, denominator_eps, out_dtype, draws=None):
+def _run_bh(q3, k3, v3, *, degree, block_size, scale, compressor, seed, denominator_eps, out_dtype, draws=None,
+            score_keys=None):
     semantics = "exact" if compressor == "none" else "flat"
     res = _engine.prefill(
         q3, k3, v3, degree=degree, block=block_size, scale=scale, semantics=semantics, compressor=compressor,
-        seed=seed, eps=denominator_eps, out_dtype=out_dtype, draws=draws)
+        seed=seed, eps=denominator_eps, out_dtype=out_dtype, draws=draws,
+        score_keys=score_keys if semantics == "flat" else None)
     return res
 
 
@@ -307,7 +317,7 @@ def fast_article_causal_attention_single(
     dt = _compute_dtype(qg)
     res = _run_bh(qg.to(dt)[None], kg.to(dt)[None], vg.to(dt)[None], degree=degree, block_size=block_size,
                   scale=_attention_scale(scale, dim), compressor=compressor, seed=seed,
-                  denominator_eps=denominator_eps, out_dtype=dt)
+                  denominator_eps=denominator_eps, out_dtype=dt, score_keys=_score_keys(kg[None]))
     out = res.out[0].to(device=home, dtype=q.dtype)
     if not return_stats:
         return out
@@ -360,7 +370,8 @@ def fast_article_causal_attention(
     k3 = kg.to(dt).reshape(bsz * heads, n, dim)
     v3 = vg.to(dt).reshape(bsz * heads, n, dv)
     res = _run_bh(q3, k3, v3, degree=degree, block_size=block_size, scale=_attention_scale(scale, dim),
-                  compressor=compressor, seed=seed, denominator_eps=denominator_eps, out_dtype=dt)
+                  compressor=compressor, seed=seed, denominator_eps=denominator_eps, out_dtype=dt,
+                  score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)))
     out = res.out.reshape(bsz, heads, n, dv).to(device=home, dtype=q.dtype)
     if not return_stats:
         return out

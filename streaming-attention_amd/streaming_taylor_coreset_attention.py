@@ -31,7 +31,7 @@ import torch
 import _decode
 import _engine
 import _plan
-from fast_article_attention import _compute_dtype, _resolve_dtype, _to_gpu
+from fast_article_attention import _compute_dtype, _resolve_dtype, _score_keys, _to_gpu
 
 Tensor = torch.Tensor
 
@@ -192,7 +192,8 @@ def article_causal_attention(
     v3 = vg.to(dt).reshape(bsz * heads, n, dv)
     semantics = "exact" if compressor == "none" else "levels"
     res = _engine.prefill(q3, k3, v3, degree=degree, block=block_size, scale=s, semantics=semantics,
-                          compressor=compressor, seed=seed, out_dtype=dt)
+                          compressor=compressor, seed=seed, out_dtype=dt,
+                          score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)) if semantics == "levels" else None)
     out = res.out.reshape(bsz, heads, n, dv).to(device=home, dtype=q.dtype)
     if not return_state_sizes:
         return out
@@ -403,9 +404,12 @@ class ArticleStreamingAttention:
         self.denominator_eps = float(denominator_eps)
         self._single = streams is None
         self.streams = 1 if streams is None else int(streams)
+        # a float64 object's compress calls score its float64 keys with float64 draws, as the reference's
+        # float64 run does (streaming_taylor_coreset_attention.py:441-457)
         self._st = _decode.DecodeState(self.streams, self.dim, self.value_dim, degree=self.degree,
                                        block=self.block_size, scale=self.scale, compressor=self.compressor,
-                                       seed=self.seed, device=self.device, eps=self.denominator_eps)
+                                       seed=self.seed, device=self.device, eps=self.denominator_eps,
+                                       score_f64=self.dtype == torch.float64)
         self.sketch = _SketchView(self)
         self.coreset = _CoresetView(self)
 
@@ -416,6 +420,12 @@ class ArticleStreamingAttention:
             shape = f"[{width}]" if self._single else f"[{self.streams}, {width}]"
             raise ValueError(f"{what} must have shape {shape}, got {tuple(x.shape)}")
         return x.to(device=self.device, dtype=self._kdtype).reshape(self.streams, width)
+
+    def _keys64(self, key: Tensor) -> Optional[Tensor]:
+        """The float64 keys [S, dim] of a float64 object (None otherwise); shapes already checked."""
+        if self.dtype != torch.float64:
+            return None
+        return key.to(device=self.device, dtype=torch.float64).reshape(self.streams, self.dim)
 
     def _stats_buffer(self, return_stats: bool) -> Optional[Tensor]:
         return torch.empty((self.streams, 4), device=self.device, dtype=torch.float32) if return_stats else None
@@ -436,7 +446,8 @@ class ArticleStreamingAttention:
     @torch.no_grad()
     def update(self, key: Tensor, value: Tensor) -> None:
         """sketch.update(k, v); coreset.append(k, v) (streaming_taylor_coreset_attention.py:576-579)."""
-        self._st.update(self._rows(key, self.dim, "key"), self._rows(value, self.value_dim, "value"))
+        self._st.update(self._rows(key, self.dim, "key"), self._rows(value, self.value_dim, "value"),
+                        self._keys64(key))
 
     @torch.no_grad()
     def query(self, query: Tensor, *, return_stats: bool = False) -> Union[Tensor, Tuple[Tensor, AttentionQueryStats]]:
@@ -462,7 +473,8 @@ class ArticleStreamingAttention:
         when the token completes a block)."""
         stats = self._stats_buffer(return_stats)
         out = self._st.step(self._rows(query, self.dim, "query"), self._rows(key, self.dim, "key"),
-                            self._rows(value, self.value_dim, "value"), out_dtype=self._kdtype, stats=stats)
+                            self._rows(value, self.value_dim, "value"), out_dtype=self._kdtype, stats=stats,
+                            k64=self._keys64(key))
         return self._finish(out, stats)
 
     @torch.no_grad()
@@ -486,7 +498,8 @@ class ArticleStreamingAttention:
                 raise ValueError("keys / values must have shapes [P, dim] / [P, value_dim]")
             keys, values = keys[None], values[None]
         self._st.extend(keys.to(device=self.device, dtype=self._kdtype),
-                        values.to(device=self.device, dtype=self._kdtype))
+                        values.to(device=self.device, dtype=self._kdtype),
+                        keys.to(device=self.device, dtype=torch.float64) if self.dtype == torch.float64 else None)
 
     @torch.no_grad()
     def prefill(self, q: Tensor, k: Tensor, v: Tensor) -> Tensor:
@@ -497,6 +510,8 @@ class ArticleStreamingAttention:
         one = self._single
         q3 = (q[None] if one else q).to(device=self.device, dtype=self._kdtype).contiguous()
         k3 = (k[None] if one else k).to(device=self.device, dtype=self._kdtype).contiguous()
+        k64 = ((k[None] if one else k).to(device=self.device, dtype=torch.float64).contiguous()
+               if self.dtype == torch.float64 else None)
         v3 = (v[None] if one else v).to(device=self.device, dtype=self._kdtype).contiguous()
         if (q3.ndim != 3 or q3.shape[0] != self.streams or q3.shape[-1] != self.dim or q3.shape != k3.shape
                 or tuple(v3.shape) != (self.streams, q3.shape[1], self.value_dim)):
@@ -504,8 +519,9 @@ class ArticleStreamingAttention:
         semantics = "exact" if self.compressor == "none" else "levels"
         res = _engine.prefill(q3, k3, v3, degree=self.degree, block=self.block_size, scale=self.scale,
                               semantics=semantics, compressor=self.compressor, seed=self.seed,
-                              eps=self.denominator_eps, out_dtype=self._kdtype)
-        self._st.extend(k3, v3)
+                              eps=self.denominator_eps, out_dtype=self._kdtype,
+                              score_keys=k64 if semantics == "levels" else None)
+        self._st.extend(k3, v3, k64)
         return (res.out[0] if one else res.out).to(self.dtype)
 
     def state_dict(self) -> dict:

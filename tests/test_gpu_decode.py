@@ -293,7 +293,7 @@ def test_decode_errors():
         bad.update(torch.zeros(4, device=DEV), torch.zeros(2, device=DEV))
     lib = _native.lib()
     assert lib.sta_decode_compress(1, 4, 2, None, None, 2, 0, None, None, None, None, 1, 1, 1, None, None, None,
-                                   None, 2, None) == _native.STA_ERR_ARG
+                                   None, 2, 0, None, None, None) == _native.STA_ERR_ARG
 
 
 @pytest.mark.parametrize("comp,dtype", [("sorted_pair", torch.float32), ("random", torch.bfloat16),

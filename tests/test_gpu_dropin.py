@@ -1,7 +1,7 @@
 """Drop-in coverage beyond the headline shapes, on the GPU against the oracle: compress calls above 1024
 items (blocks of 2048 and 4096, flat and levels, prefill and decode), value widths above 256 (column
-groups), float64 inputs (computed as their float32 rounding, returned as float64), and the
-benchmark_attention.py CSV columns."""
+groups), float64 inputs (compress calls drawn and scored in float64, everything else computed on the
+float32 rounding, outputs float64), and the benchmark_attention.py CSV columns."""
 
 import csv
 
@@ -88,39 +88,105 @@ def test_value_width_above_256(api):
         assert rel(out[0, h], ref) < 1e-4
 
 
-def test_float64_inputs_follow_their_float32_rounding():
-    """float64 q, k, v: the fast path, the level API, the streaming object and the Triton-semantics API
-    return float64 outputs equal to the float32 run on the rounded inputs (upcast), and within 1e-4
-    of the oracle on those inputs."""
-    q, k, v = orc.make_data((), 600, 16, 16, radius=1.0, data="unit_ball", seed=6)
-    q64, k64, v64 = q.double(), k.double(), v.double()
+def _nodes_equal_calls(res, calls):
+    src, w = res.node_src.cpu().numpy()[0], res.node_w.cpu().numpy()[0]
+    nodes = [node for node in range(res.plan.n_nodes) if int(res.plan.meta[node, 0]) > 0]
+    assert len(nodes) == len(calls)
+    for node in nodes:
+        size, slot = int(res.plan.meta[node, 0]), int(res.plan.desc[node, 6])
+        assert np.array_equal(src[node, :size], calls[slot].src_out), f"node {node}"
+        assert np.array_equal(w[node, :size], calls[slot].w_out), f"node {node}"
+    return src
+
+
+@pytest.mark.parametrize("semantics", ["flat", "levels"])
+def test_float64_selections_follow_the_float64_draws(semantics):
+    """float64 keys: the compressor draws float64 directions and uniforms and scores the float64 keys
+    in fp64, as the reference's float64 run does: every node bit-exact against the oracle's float64
+    compress calls (which differ from the float32 run's), outputs within 1e-4 of the oracle's float64
+    forward."""
+    n, block = 1100, 64
+    q, k, v = orc.make_data((), n, 16, 16, radius=1.0, data="unit_ball", seed=6, dtype=torch.float64)
+    kd = k[None].to(DEV).contiguous()
+    res = _engine.prefill(q[None].float().to(DEV), k[None].float().to(DEV), v[None].float().to(DEV), degree=2,
+                          block=block, scale=1.0, semantics=semantics, compressor="sorted_pair", seed=3,
+                          score_keys=kd)
+    res32 = _engine.prefill(q[None].float().to(DEV), k[None].float().to(DEV), v[None].float().to(DEV), degree=2,
+                            block=block, scale=1.0, semantics=semantics, compressor="sorted_pair", seed=3)
+    torch.cuda.synchronize()
+    if semantics == "flat":
+        calls = orc.flat_coreset(k.numpy(), block, "sorted_pair", 3, orc.projection_scores)
+        ref = orc.fast_path_forward(q, k, v, degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=3)
+    else:
+        state = orc.LevelState()
+        ref = orc.levels_forward(q, k, v, degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=3,
+                                 state_out=state)
+        calls = state.calls
+    assert calls[0].direction.dtype == np.float64 and calls[0].uniforms.dtype == np.float64
+    src64 = _nodes_equal_calls(res, calls)
+    assert not np.array_equal(src64, res32.node_src.cpu().numpy()[0]), "float64 and float32 draws selected alike"
+    assert rel(res.out[0], ref) < 1e-4
+
+
+def test_float64_public_apis():
+    """float64 q, k, v through the public APIs: float64 outputs within 1e-4 of the oracle's float64
+    forward (whose compress calls draw and score in float64); the streaming object (prefill, extend,
+    step) keeps the float64 levels of the oracle's cascade; the Triton-semantics API (segment means,
+    no draws) equals its float32 run on the rounded inputs."""
+    n = 700
+    q, k, v = orc.make_data((), n, 16, 16, radius=1.0, data="unit_ball", seed=6, dtype=torch.float64)
     kw = dict(degree=2, block_size=64, scale=1.0, compressor="sorted_pair", seed=1)
     for fn, ref_fn in ((faa.fast_article_causal_attention, orc.fast_path_forward),
                        (stc.article_causal_attention, orc.levels_forward)):
-        out64 = fn(q64.to(DEV), k64.to(DEV), v64.to(DEV), **kw)
-        out32 = fn(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+        out64 = fn(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
         assert out64.dtype == torch.float64
-        assert torch.equal(out64, out32.double())
         ref = ref_fn(q, k, v, degree=2, block=64, scale=1.0, compressor="sorted_pair", seed=1)
         assert rel(out64, ref) < 1e-4
-    # host float64 tensors too (moved to the GPU and back)
-    assert torch.equal(faa.fast_article_causal_attention(q64, k64, v64, **kw),
-                       faa.fast_article_causal_attention(q, k, v, **kw).double())
-    # the streaming object with dtype float64
-    st64 = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV,
-                                         dtype=torch.float64, seed=1)
-    st32 = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV, seed=1)
-    for i in range(150):
-        a = st64.step(q64[i].to(DEV), k64[i].to(DEV), v64[i].to(DEV))
-        b = st32.step(q[i].to(DEV), k[i].to(DEV), v[i].to(DEV))
-        assert a.dtype == torch.float64 and torch.equal(a, b.double())
-    assert st64.state_size_bytes() == 2 * st32.state_size_bytes()
+        # host float64 tensors too (moved to the GPU and back)
+        assert torch.equal(fn(q, k, v, **kw), out64.cpu())
+    state = orc.LevelState()
+    ref = orc.levels_forward(q, k, v, degree=2, block=64, scale=1.0, compressor="sorted_pair", seed=1,
+                             state_out=state)
+    # the streaming object with dtype float64: prefill 300 rows, extend 200, then step token by token
+    st = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV,
+                                       dtype=torch.float64, seed=1)
+    out_p = st.prefill(q[:300].to(DEV), k[:300].to(DEV), v[:300].to(DEV))
+    st.extend(k[300:500].to(DEV), v[300:500].to(DEV))
+    outs = torch.stack([st.step(q[i].to(DEV), k[i].to(DEV), v[i].to(DEV)) for i in range(500, n)])
+    torch.cuda.synchronize()
+    assert out_p.dtype == torch.float64 and outs.dtype == torch.float64
+    assert rel(out_p, ref[:300]) < 1e-4 and rel(outs, ref[500:]) < 1e-4
+    got = [lv for lv in st._st.level_items()]
+    want = state.levels
+    assert len([g for g in got if g is not None]) == len([w for w in want if w is not None])
+    for lvl, item in enumerate(got):
+        if item is None:
+            assert lvl >= len(want) or want[lvl] is None
+            continue
+        keys, _, w, pos = item
+        assert np.array_equal(pos[0].cpu().numpy(), want[lvl][0]), f"level {lvl}"
+        assert np.array_equal(w[0].cpu().numpy(), want[lvl][1]), f"level {lvl}"
+        assert torch.equal(st._st.lev_k64[0, lvl, :, :16].cpu(), k[torch.from_numpy(want[lvl][0])])
+    assert st.state_size_bytes() == st._st.reference_state_bytes(8) == 2 * st._st.reference_state_bytes(4)
+    # save / resume of a float64 stream keeps its float64 key rows
+    sd = st.state_dict()
+    st2 = stc.ArticleStreamingAttention(16, 16, degree=2, block_size=64, scale=1.0, device=DEV,
+                                        dtype=torch.float64, seed=1)
+    st2.load_state_dict(sd)
+    nb = st._st.buf_len
+    assert torch.equal(st2._st.lev_k64, st._st.lev_k64)
+    assert torch.equal(st2._st.buf_k64[:, :nb], st._st.buf_k64[:, :nb])
+    assert torch.equal(st2.step(q[0].to(DEV), k[0].to(DEV), v[0].to(DEV)), st.step(q[0].to(DEV), k[0].to(DEV),
+                                                                                      v[0].to(DEV)))
+    with pytest.raises(ValueError):
+        st.step_into(q[0].float().to(DEV), k[0].float().to(DEV), v[0].float().to(DEV),
+                     torch.empty(16, device=DEV))
     # the Triton-semantics API upcasts float64 like the reference, and writes float64 outputs
-    o = taa.triton_article_causal_attention(q64[None, None].to(DEV), k64[None, None].to(DEV),
-                                            v64[None, None].to(DEV), block_size=64, scale=1.0,
-                                            output_dtype=torch.float64)
-    o32 = taa.triton_article_causal_attention(q[None, None].to(DEV), k[None, None].to(DEV), v[None, None].to(DEV),
-                                              block_size=64, scale=1.0)
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    o = taa.triton_article_causal_attention(q[None, None].to(DEV), k[None, None].to(DEV), v[None, None].to(DEV),
+                                            block_size=64, scale=1.0, output_dtype=torch.float64)
+    o32 = taa.triton_article_causal_attention(q32[None, None].to(DEV), k32[None, None].to(DEV),
+                                              v32[None, None].to(DEV), block_size=64, scale=1.0)
     assert o.dtype == torch.float64 and torch.equal(o, o32.double())
 
 

@@ -102,13 +102,28 @@ def test_ws_raw_moments_against_closed_form():
 
 
 def test_ws_rejects_bad_arguments():
+    """Refusals before any launch; every pointer is a real device buffer sized for the arguments, so a
+    validation slip would give a wrong status, not a stray access."""
     lib = _native.lib()
-    # query block below two chunks, column tiles of 4 with an odd number of 32-column groups, no handoff
-    args = dict(qb=64, ct=4, dv=64, hand=16)
-    def call(qb=64, ct=4, dv=64, hand=16):
-        return lib.sta_moments_ws(16, 16, 16, 0, 1, 64, 64, dv, 64, 2, 1.0, qb, 0, 8, 5, 1, ct, 16, 16, hand, 16, 16, None)
+    bh, n, d, dv, fsplit, nts = 1, 64, 64, 64, 8, 5
+    q = torch.zeros((bh, n, d), device=DEV)
+    k = torch.zeros((bh, n, d), device=DEV)
+    v = torch.zeros((bh, n, dv), device=DEV)
+    quads = torch.zeros(fsplit * 4 * nts * 4, device=DEV, dtype=torch.int32)
+    coef = torch.zeros(fsplit * 4 * nts * 16, device=DEV)
+    hand = torch.zeros(max(lib.sta_moments_ws_handoff_bytes(bh, fsplit, nts, 4, dv), 16) // 4, device=DEV)
+    rows, ld, _ = _native.moment_partials_layout(n, dv)
+    low_num = torch.zeros((bh, fsplit, rows, ld), device=DEV)
+    low_den = torch.zeros((bh, fsplit, rows), device=DEV)
+
+    def call(qb=64, ct=4, dv_=dv, with_hand=True):
+        return lib.sta_moments_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, bh, n, d, dv_, 64, 2, 1.0, qb, 0,
+                                  fsplit, nts, 1, ct, quads.data_ptr(), coef.data_ptr(),
+                                  hand.data_ptr() if with_hand else None, low_num.data_ptr(), low_den.data_ptr(),
+                                  None)
+    # query block below two chunks or not a whole number of chunks, column tiles of 4 with an odd number
+    # of 32-column groups, no handoff
     assert call(qb=32) == _native.STA_ERR_ARG
     assert call(qb=48) == _native.STA_ERR_ARG
-    assert call(ct=4, dv=32) == _native.STA_ERR_UNSUPPORTED
-    assert call(hand=None) == _native.STA_ERR_ARG
-    del args
+    assert call(ct=4, dv_=32) == _native.STA_ERR_UNSUPPORTED
+    assert call(with_hand=False) == _native.STA_ERR_ARG

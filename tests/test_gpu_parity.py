@@ -247,11 +247,13 @@ def test_degree4_without_compression_is_exact_taylor_and_limits():
     v = torch.randn(40, 5)
     out = stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=4, block_size=41, scale=1.0)
     assert torch.allclose(out.cpu().double(), orc.classical_attention(q, k, v, 1.0), atol=3e-6, rtol=3e-6)
+    # degree 4 runs up to d = 128 (the wide-key test file covers d = 100), degree 5 .. 8 up to d = 64;
+    # beyond, the kernels refuse with NotImplementedError
     with pytest.raises(NotImplementedError):
-        stc.article_causal_attention(torch.randn(8, 72, device=DEV), torch.randn(8, 72, device=DEV),
-                                     torch.randn(8, 4, device=DEV), degree=4, block_size=4)
+        stc.article_causal_attention(torch.randn(8, 130, device=DEV), torch.randn(8, 130, device=DEV),
+                                     torch.randn(8, 4, device=DEV), degree=4, block_size=4, max_monomials=10 ** 9)
     with pytest.raises(NotImplementedError):
-        stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=5, block_size=8)
+        stc.article_causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), degree=9, block_size=8)
 
 
 # --------------------------------------------------------------------------- against the oracle, more shapes

@@ -38,19 +38,35 @@ def test_library_exports_header_symbols():
         assert lib.sta_moment_chunk(d) == _plan.moment_chunk(d)
     assert lib.sta_status_string(0) == b"ok"
     lim = _native.limits()
-    assert lim == {"max_d": 128, "max_dv": 256, "max_degree": 4, "max_compress_in": 4096}
+    assert lim == {"max_d": 256, "max_dv": 256, "max_degree": 8, "max_compress_in": 4096}
 
 
 def test_library_rejects_bad_arguments_without_touching_a_device():
     lib = _native.load_library()
     # null pointers / bad sizes are refused before any launch
-    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, 0, 32, None, None, None,
-                           None, None) == _native.STA_ERR_ARG
-    assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, 64, 2, 1.0, 32, 0, 8, 5, 0, 2, 32, 16, 16, 16, 16,
+    assert lib.sta_moments(None, None, None, 0, 1, 1, 4, 4, 1, 32, 2, 1.0, 32, 0, 1, 9, 0, 0, 32, None, None, None,
+                           None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, 64, 64, 2, 1.0, 32, 0, 8, 5, 0, 2, 32, 16, 16, None, 16, 16,
                            None) == _native.STA_ERR_ARG  # unknown products mode
     for mixed, products, columns, dv in [(1, 1, 64, 64), (0, 0, 64, 64), (0, 1, 64, 32), (0, 1, 48, 64)]:
-        assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, dv, 64, 2, 1.0, 32, 0, 8, 5, mixed, products, columns, 16,
-                               16, 16, 16, None) == _native.STA_ERR_ARG  # 64 columns: split, unmixed, 32 < dv <= 64
+        assert lib.sta_moments(16, 16, 16, 0, 1, 64, 64, 64, dv, 64, 2, 1.0, 32, 0, 8, 5, mixed, products, columns,
+                               16, 16, None, 16, 16, None) == _native.STA_ERR_ARG  # 64 columns: split, unmixed, 32 < dv <= 64
+    # row stride without windows must be d; windows need the staged width 128, a whole number of 32-wide
+    # blocks up to 256 and degree <= 4; degree 5 .. 8 runs fp32 products only
+    args = dict(q=16, d=64, ld=64, degree=2, products=1, win=None)
+
+    def mom(**kw):
+        a = dict(args, **kw)
+        nt = max(lib.sta_moment_wave_tiles(min(a["d"], 128), min(a["degree"], 8), 4), 4)
+        return lib.sta_moments(a["q"], 16, 16, 0, 1, 64, a["d"], a["ld"], 64, 64, a["degree"], 1.0, 32, 0, 8, nt, 0,
+                               a["products"], 32, 16, 16, a["win"], 16, 16, None)
+    assert mom(ld=96) == _native.STA_ERR_ARG
+    assert mom(d=128, ld=200, win=16) == _native.STA_ERR_ARG
+    assert mom(d=128, ld=288, win=16) == _native.STA_ERR_ARG
+    assert mom(d=64, ld=256, win=16) == _native.STA_ERR_ARG
+    assert mom(d=160, ld=160) == _native.STA_ERR_UNSUPPORTED
+    assert mom(degree=5, products=1) == _native.STA_ERR_UNSUPPORTED
+    assert mom(degree=9, products=0) == _native.STA_ERR_UNSUPPORTED
     assert lib.sta_moment_columns_ok(64, 2, 64, 5, 1) == 1
     assert lib.sta_moment_columns_ok(64, 2, 64, 5, 0) == 0 and lib.sta_moment_columns_ok(64, 3, 64, 5, 1) == 0
     assert lib.sta_moment_columns_ok(64, 2, 32, 5, 1) == 0 and lib.sta_moment_columns_ok(64, 2, 64, 4, 1) == 0
@@ -130,15 +146,23 @@ def test_level_plan_intervals_follow_binary_counter():
         assert vis <= set(plan.tile_nodes[plan.tile_ptr[t]:plan.tile_ptr[t + 1]].tolist())
 
 
+def _quad_factors(words):
+    """(i0, b, extra factors...) of a packed quad: one word (degree <= 4) or two (degree 5 .. 8)."""
+    w = [int(x) for x in words]
+    ids = [w[0] & 255, (w[0] >> 8) & 255, (w[0] >> 16) & 255, w[0] >> 24]
+    if len(w) > 1:
+        ids += [w[1] & 255, (w[1] >> 8) & 255, (w[1] >> 16) & 255, w[1] >> 24]
+    return ids
+
+
 def _quad_features(ft):
     """(monomial, coef) of every feature slot of a quad table: monomial = sorted factors without the
     constant index d; slots beyond the constant (index > d) are reported as None."""
     out = []
-    for q, packed in enumerate(ft.quads):
-        i0, b, i2, i3 = (int(packed) & 255, (int(packed) >> 8) & 255, (int(packed) >> 16) & 255,
-                         int(packed) >> 24)
+    for q, words in enumerate(ft.quads.reshape(-1, ft.qw)):
+        i0, b, *extra = _quad_factors(words)
         for s in range(4):
-            ids = (i0, b + s, i2, i3)
+            ids = (i0, b + s, *extra)
             coef = float(ft.coef[4 * q + s])
             mono = None if max(ids) > ft.d else tuple(sorted(i for i in ids if i != ft.d))
             out.append((mono, coef))
@@ -146,21 +170,22 @@ def _quad_features(ft):
 
 
 @pytest.mark.parametrize("d,degree", [(5, 3), (64, 2), (32, 2), (16, 3), (8, 0), (12, 1), (128, 2), (6, 2), (6, 4),
-                                      (16, 4)])
+                                      (16, 4), (8, 5), (16, 5), (6, 8), (4, 7), (72, 4)])
 def test_feature_tiles_cover_the_monomial_basis(d, degree):
     ft = _plan.feature_tiles(d, degree)
     assert ft.count == _plan.num_features(d, degree)
-    assert ft.quads.shape == (4 * ft.n_tiles,) and ft.coef.shape == (16 * ft.n_tiles,)
+    assert ft.qw == (2 if degree >= 5 else 1)
+    assert ft.quads.shape == (4 * ft.n_tiles * ft.qw,) and ft.coef.shape == (16 * ft.n_tiles,)
     feats = _quad_features(ft)
     live = sorted((m, np.float32(c).item()) for m, c in feats if c != 0.0)
     expect = sorted((m, np.float32(orc.inv_multinomial(m)).item()) for m in orc.monomials(d, degree))
     assert live == expect
     # every slot reads inside the staged row: factors up to d + 3 (the constant, then zero padding);
     # padding quads take the zero x[d + 1] as first factor
-    for packed in ft.quads:
-        b = (int(packed) >> 8) & 255
+    for words in ft.quads.reshape(-1, ft.qw):
+        i0, b, *extra = _quad_factors(words)
         assert b % 4 == 0 and b + 3 <= ft.d + 3
-        assert max((int(packed) >> 16) & 255, int(packed) >> 24) <= ft.d and int(packed) & 255 <= ft.d + 1
+        assert max(extra) <= ft.d and i0 <= ft.d + 1
 
 
 @pytest.mark.parametrize("d,degree", [(64, 2), (32, 2), (128, 2), (8, 0), (12, 1), (16, 2), (4, 2)])
@@ -203,11 +228,40 @@ def test_tile_coefficients_preserve_every_tile_polynomial(d, degree):
 
 def test_feature_tiles_limits():
     with pytest.raises(NotImplementedError):
-        _plan.feature_tiles(72, 4)  # degree 4 only for d <= 64
+        _plan.feature_tiles(68, 5)  # degree 5 .. 8 only for d <= 64
     with pytest.raises(NotImplementedError):
-        _plan.feature_tiles(8, 5)
+        _plan.feature_tiles(8, 9)
+    with pytest.raises(NotImplementedError):
+        _plan.feature_tiles(160, 2)  # wider than the staged rows: window_tiles
+    with pytest.raises(NotImplementedError):
+        _plan.window_tiles(160, 5)
     ft = _plan.feature_tiles(16, 4)
     assert ft.count == 4845 and 16 * ft.n_tiles >= 4845
+
+
+@pytest.mark.parametrize("d,degree", [(160, 2), (256, 2), (192, 1), (256, 0), (160, 3)])
+def test_window_tiles_cover_the_monomial_basis(d, degree):
+    """Keys wider than 128: every monomial of the d row dimensions sits in exactly one slot of one
+    window, with its coefficient; a slot's virtual factors map through its window's blocks to the
+    slot's monomial; each window holds 4 distinct 32-dimension blocks."""
+    wt = _plan.window_tiles(d, degree)
+    assert wt.count == _plan.num_features(d, degree)
+    seen = {}
+    for blocks, ft in zip(wt.blocks, wt.tiles):
+        assert len(set(blocks)) == 4 and all(b % 32 == 0 and b + 32 <= d for b in blocks)
+        real = lambda v: blocks[v // 32] + v % 32 if v < 128 else None  # noqa: E731
+        for slot, (mono, coef) in enumerate(_quad_features(ft)):
+            if coef == 0.0:
+                continue
+            got = ft.combo(slot)
+            assert got is not None and tuple(sorted(real(v) for v in mono)) == got
+            assert np.float32(coef) == np.float32(orc.inv_multinomial(got))
+            assert got not in seen
+            seen[got] = coef
+    assert len(seen) == _plan.num_features(d, degree)
+    rows = _plan.reference_rank(np.asarray([list(m) + [-1] * (max(degree, 1) - len(m)) for m in seen], dtype=np.int32),
+                                np.asarray([len(m) for m in seen], dtype=np.int8), d, degree)
+    assert np.array_equal(np.sort(rows), np.arange(len(seen)))
 
 
 def test_feature_tiles_padding_is_small():
@@ -364,48 +418,73 @@ def test_stats_formulas_match_reference(golden):
 
 def test_library_decode_entries_reject_bad_arguments():
     lib = _native.load_library()
-    assert lib.sta_moment_accumulate(None, None, 0, 1, 1, 1, 4, 1, 32, 2, 1, 9, None, None, None, 15, 1, None, None,
-                                     None) == _native.STA_ERR_ARG
-    assert lib.sta_decode_moments(None, 0, 1, 4, 4, 1.0, None, None, 15, None, 1, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_moment_accumulate(None, None, 0, 1, 1, 1, 4, 4, 1, 32, 2, 1, 9, None, None, None, None, 15, 1,
+                                     None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_moments(None, 0, 1, 4, 4, 1.0, None, None, 15, None, 4, 1, None, None,
+                                  None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_moments(16, 0, 1, 4, 4, 1.0, 16, 16, 15, 16, 6, 1, 16, 16,
+                                  None) == _native.STA_ERR_ARG  # index width 4 or 8
     assert lib.sta_decode_tail(None, None, None, 0, 1, 4, 4, 2, 1.0, 1e-12, 8, None, None, 16, 0, None, None, None, 0,
                                8, 0, None, None, 1, None, 0, None, None) == _native.STA_ERR_ARG
     assert lib.sta_decode_compress(1, 4, 2, None, None, 2, 0, None, None, None, None, 1, 1, 1, None, None, None,
-                                   None, 2, None) == _native.STA_ERR_ARG
+                                   None, 2, 0, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_decode_compress(1, 4, 2, 16, 16, 2, 0, 16, 16, 16, 16, 1, 1, 1, 16, 16, 16,
+                                   16, 2, 1, None, None, None) == _native.STA_ERR_ARG  # float64 scoring needs its rows
     assert _native.decode_layout(6, 5) == (8, 32)
     assert _native.decode_layout(64, 130) == (64, 160)
+    assert _native.decode_layout(130, 8) == (160, 32)  # wide keys in whole 32-dimension blocks
 
 
-@pytest.mark.parametrize("d,degree", [(4, 2), (5, 3), (64, 2), (16, 3), (3, 0), (7, 1), (6, 4), (16, 4)])
+@pytest.mark.parametrize("d,degree", [(4, 2), (5, 3), (64, 2), (16, 3), (3, 0), (7, 1), (6, 4), (16, 4), (6, 6),
+                                      (4, 8), (256, 2), (255, 1)])
 def test_feature_index_is_reference_order(d, degree):
     idx = _plan.feature_index(d, degree)
     combos = orc.monomials(d, degree)
-    assert idx.shape == (len(combos),)
-    for f, c in enumerate(combos):
-        full = list(c) + [d] * (4 - len(c))
-        assert int(idx[f]) == full[0] | (full[1] << 8) | (full[2] << 16) | (full[3] << 24)
+    assert idx.shape[0] == len(combos)
+    if _plan.feature_index_width(d, degree) == 4:
+        assert idx.dtype == np.uint32 and idx.ndim == 1
+        for f, c in enumerate(combos):
+            full = list(c) + [d] * (4 - len(c))
+            assert int(idx[f]) == full[0] | (full[1] << 8) | (full[2] << 16) | (full[3] << 24)
+    else:
+        assert idx.dtype == np.uint16 and idx.shape[1] == 8 and (degree > 4 or d >= 255)
+        for f, c in enumerate(combos):
+            assert idx[f].tolist() == list(c) + [d] * (8 - len(c))
 
 
 @pytest.mark.parametrize("width,d,degree,bh,dv", [(64, 64, 2, 2048, 64), (8, 6, 3, 1, 5), (16, 16, 3, 96, 64),
-                                                  (8, 5, 2, 3, 16), (128, 128, 2, 2, 130), (4, 4, 1, 7, 3)])
+                                                  (8, 5, 2, 3, 16), (128, 128, 2, 2, 130), (4, 4, 1, 7, 3),
+                                                  (8, 7, 5, 3, 16), (8, 8, 6, 1, 8), (160, 150, 2, 4, 16),
+                                                  (256, 256, 2, 2, 64)])
 def test_split_state_rows_cover_reference_features(width, d, degree, bh, dv):
     """Every reference feature of dimension d has exactly one slot in the accumulate table; each slot's
-    monomial (the quad's factors) is that feature's monomial."""
-    ft = _plan.feature_tiles(width, degree)
-    opts = ((2, 2), (4, 2), (5, 2), (9, 2), (16, 1)) if degree < 3 else ((4, 2), (8, 1), (16, 1))
-    ms = _plan.moment_split(ft, bh, dv, opts)
+    monomial (the quad's factors, through the split's window for keys wider than 128) is that
+    feature's monomial."""
+    if width > 128:
+        wt = _plan.window_tiles(width, degree)
+        ft = _plan.window_feature_tiles(wt)
+        ms = _plan.moment_split_windows(wt, bh, dv, ((5, 1), (16, 1)))
+    else:
+        ft = _plan.feature_tiles(width, degree)
+        opts = (((2, 2), (4, 2), (5, 2), (9, 2), (16, 1)) if degree < 3 else
+                ((4, 1),) if degree >= 5 else ((4, 2), (8, 1), (16, 1)))
+        ms = _plan.moment_split(ft, bh, dv, opts)
     rows = _plan.split_state_rows(ft, ms, d)
     order = _plan.reference_feature_order(d, degree)
     inv = {f: c for c, f in order.items()}
     assert sorted(r for r in rows if r >= 0) == list(range(_plan.num_features(d, degree)))
-    quads = ms.quads.reshape(-1, 4)  # [parts * wave_tiles, 4]
+    quads = ms.quads.reshape(-1, 4, ft.qw)  # [parts * wave_tiles, 4, words]
     coef = ms.coef.reshape(-1, 16)
     for slot, r in enumerate(rows):
         if r < 0:
             continue
         tile, q, s = slot // 16, (slot % 16) // 4, slot % 4
-        pq = int(quads[tile, q])
-        fac = sorted(f for f in (pq & 255, ((pq >> 8) & 255) + s, (pq >> 16) & 255) if f < width)
-        assert tuple(fac) == inv[r]
+        i0, b, *extra = _quad_factors(quads[tile, q])
+        fac = [f for f in (i0, b + s, *extra) if f < ft.d]
+        if ms.win is not None:  # virtual dimension 32 j + i of split fs = row dimension win[4 fs + j] + i
+            fs = tile // (4 * ms.wave_tiles)
+            fac = [int(ms.win[4 * fs + f // 32]) + f % 32 for f in fac]
+        assert tuple(sorted(fac)) == inv[r]
         assert coef[tile, slot % 16] == np.float32(orc.inv_multinomial(inv[r]))
 
 

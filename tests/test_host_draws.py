@@ -18,7 +18,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 def test_library_exports_header_symbols():
     text = (ROOT / "include" / "stadraws.h").read_text()
     syms = set(re.findall(r"^\s*(?:int64_t|int|void\*|void|const char\*)\s+(sta_\w+)\s*\(", text, flags=re.M))
-    assert len(syms) == 8
+    assert len(syms) == 10
     lib = _native.draws_library()
     for s in syms:
         assert hasattr(lib, s), s
@@ -36,15 +36,23 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("f64", [False, True])
 @pytest.mark.parametrize("seeds,sizes,d,comp", CASES)
-def test_native_draws_equal_python_replay(seeds, sizes, d, comp):
-    nat, m_nat = _plan._collect_draws(list(seeds), list(sizes), d, comp)
-    py, m_py = _plan._collect_draws_py(list(seeds), list(sizes), d, comp)
+def test_native_draws_equal_python_replay(seeds, sizes, d, comp, f64):
+    """The native replay equals torch's own calls, for float32 draws and for the float64 draws of a
+    float64 caller (which consume the generator differently: different values, not a rounding)."""
+    nat, m_nat = _plan._collect_draws(list(seeds), list(sizes), d, comp, f64)
+    py, m_py = _plan._collect_draws_py(list(seeds), list(sizes), d, comp, f64)
     assert m_nat == m_py
     for a, b in ((nat.dirs, py.dirs), (nat.unif, py.unif), (nat.perms, py.perms)):
         assert a.shape == b.shape and a.dtype == b.dtype
         assert np.array_equal(a, b)
     assert (nat.n_calls, nat.max_in) == (py.n_calls, py.max_in)
+    if f64 and comp == "sorted_pair":
+        assert nat.dirs.dtype == np.float64
+        f32, _ = _plan._collect_draws(list(seeds), list(sizes), d, comp, False)
+        drawn = np.abs(f32.dirs).sum(-1) > 0
+        assert not np.allclose(nat.dirs[drawn], f32.dirs[drawn].astype(np.float64), atol=1e-6)
 
 
 def test_draw_set_continues_and_round_trips_state():

@@ -224,6 +224,36 @@ def test_fixed_order_scores_agree_with_reference_order(golden):
     assert total_diff == 0  # none expected at these sizes
 
 
+@pytest.mark.parametrize("seed", [0, 3, 11])
+def test_float64_selections_follow_float64_draws_and_torch_order(seed):
+    """float64 keys: the oracle's compress calls draw float64 directions and uniforms (the reference
+    draws in the keys' dtype, fast_article_attention.py:339, :348; streaming_taylor_coreset_attention.py:
+    441, :456), its fixed-order fp64 scores sort exactly like torch's float64 `keys @ direction`, and the
+    selections differ from the float32 run's (a float32 draw for float64 keys is a different draw,
+    not a rounding)."""
+    q, k, v = orc.make_data((), 2048 + 37, 24, 8, radius=1.0, data="unit_ball", seed=seed, dtype=torch.float64)
+    k64 = k.numpy()
+    for build in (lambda kk, fn: orc.flat_coreset(kk, 128, "sorted_pair", seed, fn),
+                  lambda kk, fn: _level_calls(kk, 128, seed, fn)):
+        fixed = build(k64, orc.projection_scores)
+        torch_order = build(k64, orc.torch_scores)
+        f32 = build(k64.astype(np.float32), orc.projection_scores)
+        assert fixed[0].direction.dtype == np.float64 and fixed[0].uniforms.dtype == np.float64
+        assert len(fixed) == len(torch_order) == len(f32)
+        for a, b in zip(fixed, torch_order):
+            assert np.array_equal(a.src_out, b.src_out) and np.array_equal(a.w_out, b.w_out)
+        assert any(not np.array_equal(a.src_out, c.src_out) for a, c in zip(fixed, f32))
+
+
+def _level_calls(k_np, block, seed, score_fn):
+    state = orc.LevelState()
+    g = torch.Generator().manual_seed(seed)
+    for start in range(0, k_np.shape[0] - block + 1, block):
+        orc.level_block_complete(state, g, np.arange(start, start + block, dtype=np.int64), k_np, "sorted_pair",
+                                 score_fn)
+    return state.calls
+
+
 def test_flat_fixed_order_selection_equals_reference(golden):
     for name, comp_prefix in (("flat_c1", "sorted_pair_"), ("flat_oddblock", "")):
         g = golden(name)

@@ -58,14 +58,25 @@ def test_static_step_bf16_and_without_moment_state():
 
 
 def test_static_step_refuses_a_working_set_beyond_the_scratch():
+    """A working set beyond the static scratch is refused before any launch.  Every pointer is a real
+    device buffer sized for the arguments (degree 0: one feature; blocks of 2, no levels), so a
+    validation slip would give a wrong status, not a stray access."""
     lib = _native.lib()
     cap = lib.sta_static_scratch_bytes()
     assert cap == 16 << 20
-    dv, splits = 64, 1
+    d, dv, splits, block = 64, 64, 1, 2
     streams = cap // (4 * (dv + 1)) + 64  # partials of this many streams exceed the scratch
-    dummy = torch.zeros(64, device=DEV)
-    p = dummy.data_ptr()
-    st = lib.sta_decode_step_static(p, p, p, 0, streams, 64, dv, 2, 0.125, 1e-12, _native.DEC_QUERY, p, p, 2145, p,
-                                    splits, p, p, 64, 0, p, p, p, 0, 32, 0, p, 0, None, None)
+    z = dict(device=DEV, dtype=torch.float32)
+    q, k, v = torch.zeros((streams, d), **z), torch.zeros((streams, d), **z), torch.zeros((streams, dv), **z)
+    state_num, state_den = torch.zeros((streams, 1, dv), **z), torch.zeros((streams, 1), **z)
+    findex = torch.zeros(1, device=DEV, dtype=torch.int32)
+    buf_k, buf_v = torch.zeros((streams, block, d), **z), torch.zeros((streams, block, dv), **z)
+    lev = torch.zeros(4, **z)
+    out = torch.zeros((streams, dv), **z)
+    st = lib.sta_decode_step_static(q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, streams, d, dv, 0, 0.125, 1e-12,
+                                    _native.DEC_QUERY, state_num.data_ptr(), state_den.data_ptr(), 1,
+                                    findex.data_ptr(), 4, splits, buf_k.data_ptr(), buf_v.data_ptr(), block, 0,
+                                    lev.data_ptr(), lev.data_ptr(), lev.data_ptr(), 0, 1, 0, out.data_ptr(), 0, None,
+                                    None)
     assert st == _native.STA_ERR_SCRATCH
     assert b"static scratch" in lib.sta_status_string(st)
