@@ -631,12 +631,66 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
   if constexpr (SPLIT && DPS != DP) {  // dimensions [DP, DPS) of the key planes are never written: zero
     for (int e = tid; e < KB * LDKB; e += 256) Kh[e] = Kl[e] = static_cast<__bf16>(0.f);
   }
+  // Moment partials: a.fsplit partial sums per row (the feature splits of the moment scan), RS * fsplit
+  // (strip, split) pairs per lane.  Pair p = RS f + rs is loaded during batch p (issued after the next
+  // batch's row prefetch, so it has the batch's products to land) and added into the strip's value
+  // accumulators and denominator right after the batch; the pairs beyond the tile's batch count are
+  // added in the epilogue.  The accumulator layout is the partials' (lane (li, lg): row li, columns
+  // 16 ct + 4 lg + r), so no exchange is needed.  Rows outside the sequence read a clamped row and are
+  // never stored.  The fp32-product kernels (no register room for the in-flight pair: they would spill)
+  // add every pair in the epilogue.
+  constexpr bool PAIR_OVERLAP = SPLIT;
+  const int fs = a.fsplit;
+  const int64_t pden_stride = a.low_rows, pnum_stride = a.low_rows * a.low_ld;
+  const float* pden[RS];
+  const float* pnum[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) {
+    const int64_t i = min(max(myrow[rs], 0), n - 1);
+    pden[rs] = a.low_den + bh * fs * pden_stride + a.low_off + i;
+    pnum[rs] = a.low_num + (bh * fs * a.low_rows + a.low_off + i) * a.low_ld;
+  }
+  const int n_pairs = RS * fs;
+  float pair_d = 0.f;
+  floatx4 pair_n[DVT];
+  auto pair_load = [&](int p) {
+    const int f = p / RS, rs = p - f * RS;
+    const float* pd = pden[0];
+    const float* pn = pnum[0];
+#pragma unroll
+    for (int r2 = 1; r2 < RS; ++r2) {
+      if (rs == r2) {
+        pd = pden[r2];
+        pn = pnum[r2];
+      }
+    }
+    pair_d = __builtin_nontemporal_load(pd + f * pden_stride);
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) {
+      const int c0 = 16 * ct + 4 * lg;
+      pair_n[ct] = __builtin_nontemporal_load(
+          reinterpret_cast<const floatx4*>(pn + f * pnum_stride + (c0 < a.dv ? c0 : 0)));
+    }
+  };
+  auto pair_add = [&](int p) {
+    const int rs = p % RS;
+#pragma unroll
+    for (int r2 = 0; r2 < RS; ++r2) {
+      if (r2 == rs) {
+        if (lg == 0) den[r2] += pair_d;  // the lane-group sum below counts it once per row
+#pragma unroll
+        for (int ct = 0; ct < DVT; ++ct) num[r2][ct] += pair_n[ct];
+      }
+    }
+  };
+
   if (p_cur < p_end) fill();  // the first list chunk
   __syncthreads();
   bool cur_node = n_a == 0;
   int cur_off = cur_node ? 0 : kstart;
   bool have = n_a > 0 || llen > 0;
   if (have) prefetch(cur_node, cur_off);
+  int pairs_done = 0;
   for (int b = 0; have; ++b) {
     __syncthreads();  // every wave is done with the staging buffers of the previous batch
     commit();
@@ -656,6 +710,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     // staged batch and list visible; whether every staged item is active on all rows of the tile
     const bool full = __syncthreads_and(item_full ? 1 : 0) != 0;
     if (nxt_have) prefetch(nxt_node, nxt_off);
+    const bool pair = PAIR_OVERLAP && pairs_done < n_pairs;
+    if (pair) pair_load(pairs_done);
     if (cur_node && full && fast)
       process(node_batch_full_fast{});
     else if (cur_node && full)
@@ -664,23 +720,18 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
       process(node_batch{});
     else if (cur_off <= wrow_hi)
       process(block_batch{});  // some key of the batch precedes some row of this wave
+    if (pair) pair_add(pairs_done++);
     cur_node = nxt_node;
     cur_off = nxt_off;
     have = nxt_have;
   }
 
-  // ---- epilogue: add the moment partials, normalise, store ----
-  // The fsplit partials of a row are summed in the order f = 0, 1, ...  Every load of a group of
-  // EPI_GROUP partials is issued before the first sum (a partial past fsplit re-reads the last one and
-  // is dropped; a column past dv reads column 0 and is not stored).  One partial per group: on c3 (32
-  // heads x 65536, 8 partials per row) the kernel takes 2.76-2.80 ms against 2.87-2.96 ms with all 8
-  // loads in flight per row (same sums, bit for bit): the partial reads are 4.4 GB, as much HBM time as
-  // the rest of the kernel's wait, and fewer loads in flight per wave leave the other workgroups' gathers
-  // less queued behind them.
-  constexpr int EPI_GROUP = 1;
+  // ---- epilogue: the remaining moment partials, normalise, store ----
+  for (; pairs_done < n_pairs; ++pairs_done) {
+    pair_load(pairs_done);
+    pair_add(pairs_done);
+  }
   const bool raw = a.out_den != nullptr;
-  const int fs = a.fsplit;
-  const int64_t pden_stride = a.low_rows, pnum_stride = a.low_rows * a.low_ld;
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) {
     float dsum = den[rs];
@@ -688,37 +739,8 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     dsum += __shfl_xor(dsum, 32);
     if (!rvalid[rs]) continue;
     const int64_t i = myrow[rs];
-    const float* pd = a.low_den + bh * fs * pden_stride + a.low_off + i;
-    const float* pn = a.low_num + (bh * fs * a.low_rows + a.low_off + i) * a.low_ld;
-    float lowd = 0.f;
-    floatx4 lown[DVT];
-#pragma unroll
-    for (int ct = 0; ct < DVT; ++ct) lown[ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int f0 = 0; f0 < fs; f0 += EPI_GROUP) {
-      float gd[EPI_GROUP];
-      floatx4 gn[EPI_GROUP][DVT];
-#pragma unroll
-      for (int j = 0; j < EPI_GROUP; ++j) {
-        const int64_t f = min(f0 + j, fs - 1);
-        gd[j] = __builtin_nontemporal_load(pd + f * pden_stride);
-#pragma unroll
-        for (int ct = 0; ct < DVT; ++ct) {
-          const int c0 = 16 * ct + 4 * lg;
-          gn[j][ct] = __builtin_nontemporal_load(
-              reinterpret_cast<const floatx4*>(pn + f * pnum_stride + (c0 < a.dv ? c0 : 0)));
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < EPI_GROUP; ++j) {
-        if (f0 + j < fs) {
-          lowd += gd[j];
-#pragma unroll
-          for (int ct = 0; ct < DVT; ++ct) lown[ct] += gn[j][ct];
-        }
-      }
-    }
-    if (raw && lg == 0) a.out_den[bh * a.n + i] = lowd + dsum;
-    const float dn = fmaxf(lowd + dsum, a.eps);
+    if (raw && lg == 0) a.out_den[bh * a.n + i] = dsum;
+    const float dn = fmaxf(dsum, a.eps);
 #pragma unroll
     for (int ct = 0; ct < DVT; ++ct) {
       const int c0 = 16 * ct + 4 * lg;
@@ -727,7 +749,7 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
       for (int r = 0; r < 4; ++r) {
         const int col = c0 + r;
         if (col < a.dv) {
-          const float numv = num[rs][ct][r] + lown[ct][r];
+          const float numv = num[rs][ct][r];
           if (raw)
             static_cast<float*>(a.out)[(bh * a.n + i) * a.dv + col] = numv;
           else
