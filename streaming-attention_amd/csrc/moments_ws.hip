@@ -496,15 +496,25 @@ template <int CG>
 __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
                                                 int col0, bool den) {
   constexpr int WS = (CG + WS_RCOLS_EXTRA) * MOM_LDR;
+  constexpr int IT = CG * 8 / WS_REDUCERS;
   const int tid = threadIdx.x;  // < WS_REDUCERS
+  // every LDS read first (one wait for all of them instead of one per read), then the sums in the
+  // fixed wave order
+  floatx4 part[IT][4];
 #pragma unroll
-  for (int e0 = 0; e0 < CG * 8; e0 += WS_REDUCERS) {
-    const int e = e0 + tid;
-    const int col = e % CG;
-    const int t4 = 4 * (e / CG);
-    floatx4 acc = *reinterpret_cast<const floatx4*>(red + red_off(col, t4));
+  for (int it = 0; it < IT; ++it) {
+    const int e = it * WS_REDUCERS + tid;
+    const int col = e % CG, t4 = 4 * (e / CG);
 #pragma unroll
-    for (int q = 1; q < 4; ++q) acc += *reinterpret_cast<const floatx4*>(red + q * WS + red_off(col, t4));
+    for (int q = 0; q < 4; ++q) part[it][q] = *reinterpret_cast<const floatx4*>(red + q * WS + red_off(col, t4));
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int e = it * WS_REDUCERS + tid;
+    const int col = e % CG, t4 = 4 * (e / CG);
+    floatx4 acc = part[it][0];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) acc += part[it][q];
     float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
 #pragma unroll
     for (int r = 0; r < 4; ++r) __builtin_nontemporal_store(acc[r], dst + r * a.ldo);
