@@ -383,6 +383,20 @@ def main() -> int:
 
     cold_ms = [cold_call(w["seed"] + 7919 * (i + 1), False) for i in range(3)]
     cold_plan_ms = cold_call(w["seed"] + 7919 * 4, True)
+
+    # reference_scores=True: every compress call on the host in torch's CPU `keys @ direction` order (key
+    # copy to the host, host draw replay and selection, node-table upload, then the GPU kernels); the
+    # first call at a fresh seed, then the best of two more at that seed (draws cached)
+    def ref_call(seed_):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        api(qd, kd, vd, degree=w["degree"], block_size=w["block"], scale=w["scale"], compressor=w["compressor"],
+            seed=seed_, reference_scores=True)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    ref_cold_ms = ref_call(w["seed"] + 7919 * 6)
+    ref_warm_ms = min(ref_call(w["seed"] + 7919 * 6) for _ in range(2))
     t0 = time.perf_counter()
     _plan.draws_for(plan, _plan.sequence_seeds(w["seed"] + 7919 * 5, bh), d, w["compressor"])
     draws_ms = (time.perf_counter() - t0) * 1e3
@@ -440,6 +454,10 @@ def main() -> int:
                            "seed's cached draws"),
         "cold_call_new_shape_ms": round(cold_plan_ms, 3),
         "host_draws_fresh_seed_ms": round(draws_ms, 3),
+        "reference_scores_ms": {"cold": round(ref_cold_ms, 3), "warm": round(ref_warm_ms, 3),
+                                "note": ("public API call with reference_scores=True (compress calls run on the "
+                                         "host in the order of torch's CPU keys @ direction; keys copied to "
+                                         "the host); cold: a fresh seed; warm: the same seed again")},
         "host_threads": torch.get_num_threads(),
         "wall_s_timed_region": round(wall, 4),
     }

@@ -39,14 +39,37 @@ void sta_draws_close(void* handle);
 int sta_draws_next(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
                    float* dirs, float* unif, int32_t* perms);
 
-/* The same with the directions and uniforms drawn as float64 when f64 = 1 (dirs / unif are double
- * tables): the reference draws them in the keys' dtype (fast_article_attention.py:339, :348;
- * streaming_taylor_coreset_attention.py:441, :456), so a float64 caller's draws come from torch's double
- * sampling path.  f64 = 0 is sta_host_draws / sta_draws_next (float tables). */
+/* The same with the directions and uniforms drawn in the element type draw_type: the reference draws
+ * them in the keys' dtype (fast_article_attention.py:339, :348; streaming_taylor_coreset_attention.py:441,
+ * :456), which selects torch's float, double or 16-bit sampling path.  draw_type: STA_DRAW_F32 (float
+ * tables; sta_host_draws / sta_draws_next), STA_DRAW_F64 (double tables), STA_DRAW_BF16 / STA_DRAW_F16
+ * (float tables holding the 16-bit values exactly). */
+#define STA_DRAW_F32 0
+#define STA_DRAW_F64 1
+#define STA_DRAW_BF16 2
+#define STA_DRAW_F16 3
 int sta_host_draws_typed(const int64_t* seeds, int n_seq, const int32_t* call_sizes, int n_calls, int d,
-                         int compressor, int max_in, int f64, void* dirs, void* unif, int32_t* perms);
+                         int compressor, int max_in, int draw_type, void* dirs, void* unif, int32_t* perms);
 int sta_draws_next_typed(void* handle, const int32_t* call_sizes, int n_calls, int d, int compressor, int max_in,
-                         int f64, void* dirs, void* unif, int32_t* perms);
+                         int draw_type, void* dirs, void* unif, int32_t* perms);
+
+/* Reference-order selections: every compress call of a prefill's node plan run on the host, with the
+ * items ordered as the reference orders them, by torch's CPU `keys @ direction` and torch.argsort in the
+ * keys' dtype (fast_article_attention.py:339-361; streaming_taylor_coreset_attention.py:413-467), instead
+ * of the HIP compressor's fixed-order fp64 scores (sta_compress_nodes).  The reference's score order
+ * belongs to the host's BLAS, so this reproduces its selections on the host it runs on.
+ *   keys      [n_seq, n, d] host rows in key_type (an STA_DRAW_* code), laid out as the caller's tensor
+ *   levels    1: merge-and-reduce levels (raw blocks stacked fresh, permutation weights w * n / m);
+ *             0: flat block coreset (raw blocks as views of the rows, permutation weights n / m)
+ *   desc      int32 [n_nodes, 8] the node plan sta_compress_nodes runs (kind, a, b, n_in, n_out, method,
+ *             draw slot, n_out of child a), children before parents
+ *   dirs, unif, perms  the draw tables of sta_host_draws_typed for key_type, [n_seq, n_calls, ...]
+ *   threads   host threads (0: torch's intra-op thread count)
+ *   node_src  int32 [n_seq, n_nodes, cap], node_w float [n_seq, n_nodes, cap]: the tables
+ *             sta_block_attention reads (global token index and weight of every kept item) */
+int sta_host_select(const void* keys, int key_type, int64_t n_seq, int64_t n, int d, int levels,
+                    const int32_t* desc, int n_nodes, int cap, const void* dirs, const void* unif,
+                    const int32_t* perms, int n_calls, int max_in, int threads, int32_t* node_src, float* node_w);
 
 /* Generator states in torch.Generator.get_state()'s CPU layout: out / in are [n_seq, state_bytes]. */
 int64_t sta_draws_state_bytes(void);

@@ -324,8 +324,9 @@ def fast_path_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block
                       reference_scores: bool = False, calls_out: Optional[list] = None, low: str = "stream") -> Tensor:
     """The reference CPU fast path for one [N, D] sequence (fast_article_attention.py:522-598):
     stream moments + completed-block reps (chunked q x reps) + exact in-block residual, fp32.
-    reference_scores=True projects with torch's `keys @ direction` exactly as the reference does
-    (fast_article_attention.py:341) instead of the fixed-order scores the HIP kernel uses."""
+    reference_scores=True orders each compress call as the reference does, by torch's `keys @ direction`
+    and argsort (fast_article_attention.py:340-341), instead of the fixed-order scores the HIP kernel
+    uses."""
     n, dim = q.shape
     s = attention_scale(scale, dim)
     low_num, low_den = _low_sums(q, k, v, degree, s, low)
@@ -340,7 +341,7 @@ def fast_path_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block
             tail_den[st:en] = r.sum(-1)
             tail_num[st:en] = r @ v
     else:
-        score_fn = torch_scores if reference_scores else projection_scores
+        score_fn = torch_order_scores if reference_scores else projection_scores
         calls = flat_coreset(k.numpy(), block, compressor, seed, score_fn)
         if calls_out is not None:
             calls_out.extend(calls)
@@ -416,6 +417,16 @@ def torch_scores(keys: np.ndarray, direction: np.ndarray) -> np.ndarray:
     return (torch.from_numpy(np.ascontiguousarray(keys)) @ torch.from_numpy(direction)).numpy()
 
 
+def torch_order_scores(keys: np.ndarray, direction: np.ndarray) -> np.ndarray:
+    """The rank of every key in torch.argsort(keys @ direction), as float64 scores: a stable sort of
+    them is the reference's own order, including the order torch's argsort gives exactly equal scores
+    (fast_article_attention.py:341, streaming_taylor_coreset_attention.py:443-444)."""
+    order = torch.argsort(torch.from_numpy(np.ascontiguousarray(keys)) @ torch.from_numpy(direction)).numpy()
+    rank = np.empty(order.shape[0], dtype=np.float64)
+    rank[order] = np.arange(order.shape[0], dtype=np.float64)
+    return rank
+
+
 def _low_sums(q: Tensor, k: Tensor, v: Tensor, degree: int, scale: float, low: str) -> Tuple[Tensor, Tensor]:
     """The moment sums by the reference's token loop ("stream") or their closed form ("direct", for
     feature maps too large to materialise; equal in exact arithmetic, test_stream_moments_equal_closed_form)."""
@@ -442,7 +453,7 @@ def levels_forward(q: Tensor, k: Tensor, v: Tensor, *, degree: int = 2, block: i
     state = state_out if state_out is not None else LevelState()
     g = torch.Generator(device="cpu")
     g.manual_seed(int(seed))
-    score_fn = torch_scores if reference_scores else projection_scores
+    score_fn = torch_order_scores if reference_scores else projection_scores
     k_np = k.numpy()
 
     def tail_for(rows: Tensor, items_src: np.ndarray, items_w: np.ndarray, buf_lo: int, rows_idx: np.ndarray):

@@ -215,12 +215,16 @@ def prefill(
     residual_products: Optional[int] = None,
     moment_kernel: Optional[str] = None,
     score_keys: Optional[torch.Tensor] = None,
+    reference_keys: Optional[torch.Tensor] = None,
 ) -> PrefillResult:
     """Run the whole prefill for contiguous [BH, N, D] device tensors of one dtype.  moment_kernel:
     "ws" (sta_moments_ws where it applies), "chunked" (sta_moments) or None (use_moments_ws).
     score_keys: the float64 keys of a float64 caller ([BH, N, D], contiguous, on the device; k3 is
     their float32 rounding): the compressor then draws its directions and uniforms as float64 and
-    scores these keys in fp64, as the reference's float64 run does."""
+    scores these keys in fp64, as the reference's float64 run does.
+    reference_keys: the caller's keys in their own dtype as a contiguous CPU [BH, N, D] tensor: the
+    compress calls then run on the host in the reference's own score order (torch's CPU
+    `keys @ direction` and argsort, _plan.reference_selection) instead of the HIP compressor."""
     if semantics not in SEMANTICS:
         raise ValueError(f"semantics must be one of {SEMANTICS}")
     for t in (q3, k3, v3):
@@ -237,6 +241,12 @@ def prefill(
         if score_keys.dtype != torch.float64 or tuple(score_keys.shape) != (bh, n, d) or \
                 not score_keys.is_contiguous():
             raise ValueError("score_keys must be the contiguous float64 [BH, N, D] keys")
+    if reference_keys is not None:
+        if reference_keys.device.type != "cpu" or not reference_keys.is_contiguous() or \
+                tuple(reference_keys.shape) != (bh, n, d) or reference_keys.dtype not in _native.DRAW_TYPES:
+            raise ValueError("reference_keys must be the caller's contiguous CPU [BH, N, D] keys")
+        if draws is not None:
+            raise ValueError("reference_keys take the draws of their own dtype; explicit draws do not apply")
     check_kernel_limits(d, degree)
     if dv > lim["max_dv"]:
         # value columns are independent given the keys (the denominator and the coreset selections do
@@ -246,7 +256,7 @@ def prefill(
                          scale=scale, semantics=semantics, compressor=compressor, seed=seed, eps=eps,
                          out_dtype=out_dtype, stride=stride, exp_clamp=exp_clamp, draws=draws, timer=timer,
                          products=products, residual_products=residual_products, moment_kernel=moment_kernel,
-                         score_keys=score_keys)
+                         score_keys=score_keys, reference_keys=reference_keys)
                  for c0 in range(0, dv, lim["max_dv"])]
         first = parts[0]
         return PrefillResult(torch.cat([r.out for r in parts], dim=-1), first.node_src, first.node_w, first.plan,
@@ -321,7 +331,12 @@ def prefill(
         lambda: (_i32(plan.meta, dev), _i32(plan.tile_ptr, dev), _i32(np.maximum(plan.tile_nodes, 0) if plan.tile_nodes.size else np.zeros(1, np.int32), dev)),
     )
     f64 = score_keys is not None
-    if semantics != "segment" and plan.batches:
+    host_select = reference_keys is not None and semantics in ("flat", "levels") and bool(plan.batches)
+    if host_select:
+        # every compress call on the host, in the reference's score order; the tables go up like an input
+        src_np, w_np = _plan.reference_selection(plan, _plan.sequence_seeds(seed, bh), reference_keys, compressor)
+        host_nodes = (torch.from_numpy(src_np).to(dev), torch.from_numpy(w_np).to(dev))
+    if semantics != "segment" and plan.batches and not host_select:
         seeds = _plan.sequence_seeds(seed, bh)
         fdraw = (lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float64)).to(dev)) if f64 else \
             (lambda a: _f32(a, dev))
@@ -376,7 +391,8 @@ def prefill(
     # The compressor needs only the keys and the draws: with OVERLAP_COMPRESS it goes on a second stream
     # (default priority), released before the moment scan is queued.
     main = torch.cuda.current_stream(dev)
-    side = _side_stream(dev) if (OVERLAP_COMPRESS and semantics != "segment" and plan.batches) else main
+    side = _side_stream(dev) if (OVERLAP_COMPRESS and semantics != "segment" and plan.batches and
+                                 not host_select) else main
     if side is not main:
         side.wait_stream(main)
 
@@ -407,6 +423,8 @@ def prefill(
                          torch.full((bh, plan.n_nodes, plan.cap), float(stride), device=dev, dtype=torch.float32)),
             )
             del rpb
+    elif host_select:
+        node_src, node_w = host_nodes
     elif plan.batches:
         node_src = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.int32)
         node_w = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.float32)

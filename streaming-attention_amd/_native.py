@@ -182,6 +182,8 @@ def draws_library() -> ctypes.CDLL:
                                 ("sta_draws_get_state", i, [p, p]),
                                 ("sta_draws_set_state", i, [p, p]),
                                 ("sta_host_draws", i, [p, i, p, i, i, i, i, p, p, p]),
+                                ("sta_host_select", i, [p, i, ctypes.c_int64, ctypes.c_int64, i, i, p, i, i, p, p,
+                                                        p, i, i, i, p, p]),
                                 ("sta_draws_error", ctypes.c_char_p, [])):
             fn = getattr(h, name)
             fn.restype = res
@@ -194,33 +196,83 @@ def _draws_fail(h) -> None:
     raise NativeError(h.sta_draws_error().decode())
 
 
-def _draw_tables(n_seq: int, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
+# element types of the draws (stadraws.h STA_DRAW_*): the keys' dtype
+DRAW_TYPES = {torch.float32: 0, torch.float64: 1, torch.bfloat16: 2, torch.float16: 3}
+
+
+def draw_type(f64: bool = False, dtype: Optional[torch.dtype] = None) -> int:
+    """The STA_DRAW_* code of draws in `dtype` (float32, float64, bfloat16, float16), or of float64 /
+    float32 draws by the f64 flag when dtype is None."""
+    if dtype is None:
+        return 1 if f64 else 0
+    if dtype not in DRAW_TYPES:
+        raise ValueError(f"no draws in {dtype}")
+    return DRAW_TYPES[dtype]
+
+
+def _draw_tables(n_seq: int, call_sizes, d: int, compressor: str, max_in: int, dt: int = 0):
     import numpy as np
 
     if compressor not in COMPRESSOR_CODES:
         raise ValueError("compressor must be one of {'sorted_pair', 'random', 'none'}")
     cc = max(len(call_sizes), 1)
     sz = np.ascontiguousarray(np.asarray(call_sizes, dtype=np.int32))
-    ft = np.float64 if f64 else np.float32
+    ft = np.float64 if dt == 1 else np.float32
     return (sz, np.zeros((n_seq, cc, d), dtype=ft), np.zeros((n_seq, cc, max_in // 2), dtype=ft),
             np.zeros((n_seq, cc, max_in), dtype=np.int32))
 
 
-def host_draws(seeds, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
+def host_draws(seeds, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False,
+               dtype: Optional[torch.dtype] = None):
     """Draw tables (dirs [S, C, d], unif [S, C, max_in // 2], perms int32 [S, C, max_in]; C = at least 1)
     of len(seeds) sequences, each on a fresh generator seeded seeds[s], over the compress calls of
-    call_sizes, in call order.  f64: the directions and uniforms are drawn as float64 (the draws of a
-    float64 caller), else float32."""
+    call_sizes, in call order.  The directions and uniforms are drawn in `dtype` (the keys' dtype, as the
+    reference draws them; float64 tables for float64, float32 tables holding the values otherwise), or
+    as float64 / float32 by the f64 flag when dtype is None."""
     import numpy as np
 
-    sz, dirs, unif, perms = _draw_tables(len(seeds), call_sizes, d, compressor, max_in, f64)
+    dt = draw_type(f64, dtype)
+    sz, dirs, unif, perms = _draw_tables(len(seeds), call_sizes, d, compressor, max_in, dt)
     sd = np.ascontiguousarray(np.asarray(seeds, dtype=np.int64))
     h = draws_library()
     if h.sta_host_draws_typed(sd.ctypes.data, len(seeds), sz.ctypes.data, len(call_sizes), d,
-                              COMPRESSOR_CODES[compressor], max_in, int(f64), dirs.ctypes.data, unif.ctypes.data,
+                              COMPRESSOR_CODES[compressor], max_in, dt, dirs.ctypes.data, unif.ctypes.data,
                               perms.ctypes.data) != 0:
         _draws_fail(h)
     return dirs, unif, perms
+
+
+def host_select(keys: torch.Tensor, levels: bool, desc, n_nodes: int, cap: int, dirs, unif, perms,
+                threads: int = 0):
+    """Reference-order selections (sta_host_select): every compress call of a node plan run on the host
+    with torch's CPU `keys @ direction` and argsort in the keys' dtype.  keys: contiguous CPU [S, N, d]
+    (float32 / float64 / bfloat16 / float16; laid out as the caller's tensor); desc: int32 [n_nodes, 8]
+    with methods filled; dirs / unif / perms: the draw tables of host_draws in the keys' dtype.
+    Returns (node_src int32 [S, n_nodes, cap], node_w float32 [S, n_nodes, cap]) as numpy arrays."""
+    import numpy as np
+
+    if keys.device.type != "cpu" or not keys.is_contiguous() or keys.dim() != 3 or keys.dtype not in DRAW_TYPES:
+        raise ValueError("host_select needs contiguous CPU [S, N, d] keys of a float dtype")
+    s_, n, d = keys.shape
+    dt = DRAW_TYPES[keys.dtype]
+    want = np.float64 if dt == 1 else np.float32
+    desc = np.ascontiguousarray(desc, dtype=np.int32)
+    dirs, unif = np.ascontiguousarray(dirs), np.ascontiguousarray(unif)
+    perms = np.ascontiguousarray(perms, dtype=np.int32)
+    if dirs.dtype != want or unif.dtype != want:
+        raise ValueError("draw tables must be float64 for float64 keys and float32 otherwise")
+    if dirs.ndim != 3 or dirs.shape[0] != s_ or dirs.shape[2] != d or unif.shape[:2] != dirs.shape[:2] or \
+            perms.shape[:2] != dirs.shape[:2] or unif.shape[2] * 2 > perms.shape[2] or desc.shape != (n_nodes, 8):
+        raise ValueError("draw tables or node plan do not match the keys")
+    n_calls, max_in = int(dirs.shape[1]), int(perms.shape[2])
+    node_src = np.zeros((s_, n_nodes, cap), dtype=np.int32)
+    node_w = np.zeros((s_, n_nodes, cap), dtype=np.float32)
+    h = draws_library()
+    if h.sta_host_select(keys.data_ptr(), dt, s_, n, d, int(bool(levels)), desc.ctypes.data, n_nodes, cap,
+                         dirs.ctypes.data, unif.ctypes.data, perms.ctypes.data, n_calls, max_in, int(threads),
+                         node_src.ctypes.data, node_w.ctypes.data) != 0:
+        _draws_fail(h)
+    return node_src, node_w
 
 
 class DrawSet:
@@ -242,11 +294,13 @@ class DrawSet:
             self._h.sta_draws_close(self._ptr)
             self._ptr = None
 
-    def next(self, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False):
+    def next(self, call_sizes, d: int, compressor: str, max_in: int, f64: bool = False,
+             dtype: Optional[torch.dtype] = None):
         """Tables as host_draws, continuing every stream's generator."""
-        sz, dirs, unif, perms = _draw_tables(self.n, call_sizes, d, compressor, max_in, f64)
+        dt = draw_type(f64, dtype)
+        sz, dirs, unif, perms = _draw_tables(self.n, call_sizes, d, compressor, max_in, dt)
         if self._h.sta_draws_next_typed(self._ptr, sz.ctypes.data, len(call_sizes), d, COMPRESSOR_CODES[compressor],
-                                        max_in, int(f64), dirs.ctypes.data, unif.ctypes.data,
+                                        max_in, dt, dirs.ctypes.data, unif.ctypes.data,
                                         perms.ctypes.data) != 0:
             _draws_fail(self._h)
         return dirs, unif, perms

@@ -890,7 +890,8 @@ def _draw_one_call(g: torch.Generator, n_in: int, d: int, compressor: str, dtype
     direction = torch.randn(d, generator=g, dtype=dtype)
     direction = direction / torch.clamp(torch.linalg.vector_norm(direction), min=1e-12)
     u = torch.rand(n_in // 2, generator=g, dtype=dtype)
-    return METHOD_SORTED_PAIR, direction.numpy(), u.numpy(), None
+    table = torch.float64 if dtype == torch.float64 else torch.float32  # 16-bit values held exactly
+    return METHOD_SORTED_PAIR, direction.to(table).numpy(), u.to(table).numpy(), None
 
 
 def _call_method(n_in: int, compressor: str) -> int:
@@ -902,23 +903,25 @@ def _call_method(n_in: int, compressor: str) -> int:
 
 
 def _collect_draws(seeds: List[int], call_sizes: List[int], d: int, compressor: str,
-                   f64: bool = False) -> Tuple[Draws, List[int]]:
+                   f64: bool = False, dtype: Optional[torch.dtype] = None) -> Tuple[Draws, List[int]]:
     """Draws of every sequence over the compress calls of call_sizes, replayed natively (the same
     generator calls as _draw_one_call, per sequence on its own generator, sequences in parallel); f64:
-    directions and uniforms drawn as float64 (a float64 caller's)."""
+    directions and uniforms drawn as float64 (a float64 caller's); dtype, when given: drawn in that
+    dtype (float64 tables for float64, float32 tables otherwise)."""
     methods = [_call_method(n_in, compressor) for n_in in call_sizes]
     max_in = max(max(call_sizes) if call_sizes else 2, 2)
-    dirs, unif, perms = _native.host_draws(seeds, call_sizes, d, compressor, max_in, f64=f64)
+    dirs, unif, perms = _native.host_draws(seeds, call_sizes, d, compressor, max_in, f64=f64, dtype=dtype)
     return Draws(dirs, unif, perms, len(call_sizes), max_in), methods
 
 
 def _collect_draws_py(seeds: List[int], call_sizes: List[int], d: int, compressor: str,
-                      f64: bool = False) -> Tuple[Draws, List[int]]:
+                      f64: bool = False, dtype: Optional[torch.dtype] = None) -> Tuple[Draws, List[int]]:
     """The same draws one generator call at a time through torch's Python API."""
     n_calls = len(call_sizes)
     max_in = max(max(call_sizes) if call_sizes else 2, 2)
     bh = len(seeds)
-    ft = np.float64 if f64 else np.float32
+    tdt = dtype if dtype is not None else (torch.float64 if f64 else torch.float32)
+    ft = np.float64 if tdt == torch.float64 else np.float32
     dirs = np.zeros((bh, max(n_calls, 1), d), dtype=ft)
     unif = np.zeros((bh, max(n_calls, 1), max_in // 2), dtype=ft)
     perms = np.zeros((bh, max(n_calls, 1), max_in), dtype=np.int32)
@@ -928,7 +931,7 @@ def _collect_draws_py(seeds: List[int], call_sizes: List[int], d: int, compresso
         g.manual_seed(int(seed))
         for c, n_in in enumerate(call_sizes):
             method, dvec, u, perm = _draw_one_call(g, n_in, d, compressor,
-                                                   torch.float64 if f64 else torch.float32)
+                                                   tdt)
             if h == 0:
                 methods.append(method)
             if dvec is not None:
@@ -1113,12 +1116,12 @@ def segment_plan(n: int, block: int, stride: int) -> Tuple[NodePlan, int, int]:
 
 
 def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str,
-              f64: bool = False) -> Tuple[Draws, np.ndarray]:
+              f64: bool = False, dtype: Optional[torch.dtype] = None) -> Tuple[Draws, np.ndarray]:
     """Draw table for every sequence plus the node descriptors with their compress method filled in
-    (f64: float64 directions and uniforms)."""
+    (f64: float64 directions and uniforms; dtype, when given: drawn in that dtype)."""
 
     def build():
-        draws, methods = _collect_draws(list(seeds), plan.call_sizes, d, compressor, f64)
+        draws, methods = _collect_draws(list(seeds), plan.call_sizes, d, compressor, f64, dtype)
         desc = plan.desc.copy()
         if plan.mode in (MODE_FLAT, MODE_LEVELS) and plan.call_sizes:
             for i in range(desc.shape[0]):
@@ -1127,7 +1130,23 @@ def draws_for(plan: NodePlan, seeds: Tuple[int, ...], d: int, compressor: str,
                 desc[i, 5] = methods[desc[i, 6]]
         return draws, desc
 
-    return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor, bool(f64)), build)
+    return _cached(("draws", plan.mode, plan.n, plan.block, tuple(seeds), d, compressor, bool(f64), dtype), build)
+
+
+def reference_selection(plan: NodePlan, seeds: Tuple[int, ...], keys: torch.Tensor, compressor: str,
+                        threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+    """Node tables (node_src int32, node_w float32 [S, n_nodes, cap]) of a flat or levels plan with every
+    compress call ordered as the reference orders it: torch's CPU `keys @ direction` and argsort in the
+    keys' dtype on the draws of that dtype (sta_host_select).  keys: contiguous CPU [S, N, d] in the
+    caller's dtype and layout."""
+    if plan.mode not in (MODE_FLAT, MODE_LEVELS) or not plan.batches:
+        raise ValueError("reference_selection needs a flat or levels plan with compress calls")
+    s_, n, d = keys.shape
+    if n != plan.n or len(seeds) != s_:
+        raise ValueError("keys do not match the plan and seeds")
+    dr, desc = draws_for(plan, tuple(seeds), d, compressor, dtype=keys.dtype)
+    return _native.host_select(keys, plan.mode == MODE_LEVELS, desc, plan.n_nodes, plan.cap, dr.dirs, dr.unif,
+                               dr.perms, threads)
 
 
 def completion_call_sizes(blocks_before: int, block: int, compressor: str) -> List[int]:

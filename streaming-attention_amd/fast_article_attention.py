@@ -166,6 +166,18 @@ def _compute_dtype(t: Tensor) -> torch.dtype:
     raise ValueError(f"dtype {t.dtype} is not supported (use float64, float32, bfloat16 or float16)")
 
 
+def _reference_keys(k: Tensor, bh: int, n: int, dim: int, on: bool) -> Optional[Tensor]:
+    """For reference_scores=True: the caller's keys in their own dtype as the contiguous CPU
+    [B*H, N, D] rows the reference scores (its k[b, h] are views of the caller's tensor, so a contiguous
+    CPU tensor is used as it is; other keys are copied to the host).  None when off."""
+    if not on:
+        return None
+    k3 = k.reshape(bh, n, dim)
+    if k3.device.type == "cpu" and k3.is_contiguous():
+        return k3
+    return k3.contiguous().cpu()
+
+
 def _score_keys(k3: Tensor) -> Optional[Tensor]:
     """The keys the compressor scores for a float64 caller: the float64 keys themselves, since the
     reference runs a float64 caller's compress calls in float64 (float64 directions and uniforms, scores
@@ -270,12 +282,13 @@ def _check_compressor(compressor: str, n: int, block_size: int) -> None:
 
 
 def _run_bh(q3, k3, v3, *, degree, block_size, scale, compressor, seed, denominator_eps, out_dtype, draws=None,
-            score_keys=None):
+            score_keys=None, reference_keys=None):
     semantics = "exact" if compressor == "none" else "flat"
     res = _engine.prefill(
         q3, k3, v3, degree=degree, block=block_size, scale=scale, semantics=semantics, compressor=compressor,
         seed=seed, eps=denominator_eps, out_dtype=out_dtype, draws=draws,
-        score_keys=score_keys if semantics == "flat" else None)
+        score_keys=score_keys if semantics == "flat" else None,
+        reference_keys=reference_keys if semantics == "flat" else None)
     return res
 
 
@@ -294,8 +307,11 @@ def fast_article_causal_attention_single(
     low_mode: str = "auto",
     denominator_eps: float = 1e-12,
     return_stats: bool = False,
+    reference_scores: bool = False,
 ) -> Union[Tensor, Tuple[Tensor, FastArticleStats]]:
-    """One [N,D] sequence (fast_article_attention.py:522-631)."""
+    """One [N,D] sequence (fast_article_attention.py:522-631).  reference_scores: order every compress
+    call as the reference does on this host (torch's CPU `keys @ direction` and argsort, run on the
+    host) instead of the GPU compressor's fixed-order fp64 scores; see fast_article_causal_attention."""
     if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
         raise ValueError("q,k,v must have shapes [N,D], [N,D], [N,Dv]")
     if q.shape != k.shape:
@@ -317,7 +333,8 @@ def fast_article_causal_attention_single(
     dt = _compute_dtype(qg)
     res = _run_bh(qg.to(dt)[None], kg.to(dt)[None], vg.to(dt)[None], degree=degree, block_size=block_size,
                   scale=_attention_scale(scale, dim), compressor=compressor, seed=seed,
-                  denominator_eps=denominator_eps, out_dtype=dt, score_keys=_score_keys(kg[None]))
+                  denominator_eps=denominator_eps, out_dtype=dt, score_keys=_score_keys(kg[None]),
+                  reference_keys=_reference_keys(k, 1, n, dim, reference_scores))
     out = res.out[0].to(device=home, dtype=q.dtype)
     if not return_stats:
         return out
@@ -340,12 +357,21 @@ def fast_article_causal_attention(
     low_mode: str = "auto",
     denominator_eps: float = 1e-12,
     return_stats: bool = False,
+    reference_scores: bool = False,
 ) -> Union[Tensor, Tuple[Tensor, FastArticleStats]]:
     """[N,D] or [B,H,N,D] (fast_article_attention.py:634-719).  All B*H sequences run in one set of
-    launches; sequence (b, h) uses seed + b*H + h as in the reference."""
+    launches; sequence (b, h) uses seed + b*H + h as in the reference.
+
+    reference_scores (not in the reference; default off): the GPU compressor orders a compress call's
+    keys by fp64 projection scores summed in a fixed order, reproducible on any machine.  The reference
+    sorts torch's CPU `keys @ direction`, whose fp32 summation order belongs to the host's BLAS, so on
+    near-ties (scores a few ulps apart) the two orders can keep different tokens.  With
+    reference_scores=True every compress call runs on the host with those same torch calls, in the
+    keys' dtype, and the selections are the reference's on this host; the keys are copied to the host
+    and the selection takes host time (the moment scan and the residual still run on the GPU)."""
     kwargs = dict(degree=degree, block_size=block_size, scale=scale, compressor=compressor, seed=seed,
                   query_chunk_size=query_chunk_size, low_mode=low_mode, denominator_eps=denominator_eps,
-                  return_stats=return_stats)
+                  return_stats=return_stats, reference_scores=reference_scores)
     if q.ndim == 2:
         return fast_article_causal_attention_single(q, k, v, **kwargs)
     if q.ndim != 4:
@@ -371,7 +397,8 @@ def fast_article_causal_attention(
     v3 = vg.to(dt).reshape(bsz * heads, n, dv)
     res = _run_bh(q3, k3, v3, degree=degree, block_size=block_size, scale=_attention_scale(scale, dim),
                   compressor=compressor, seed=seed, denominator_eps=denominator_eps, out_dtype=dt,
-                  score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)))
+                  score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)),
+                  reference_keys=_reference_keys(k, bsz * heads, n, dim, reference_scores))
     out = res.out.reshape(bsz, heads, n, dv).to(device=home, dtype=q.dtype)
     if not return_stats:
         return out

@@ -31,7 +31,7 @@ import torch
 import _decode
 import _engine
 import _plan
-from fast_article_attention import _compute_dtype, _resolve_dtype, _score_keys, _to_gpu
+from fast_article_attention import _compute_dtype, _reference_keys, _resolve_dtype, _score_keys, _to_gpu
 
 Tensor = torch.Tensor
 
@@ -129,8 +129,10 @@ def article_causal_attention_single(
     seed: int = 0,
     max_monomials: int = 5_000_000,
     return_state_sizes: bool = False,
+    reference_scores: bool = False,
 ) -> Union[Tensor, Tuple[Tensor, List[int]]]:
-    """One [N,D] sequence (streaming_taylor_coreset_attention.py:641-687)."""
+    """One [N,D] sequence (streaming_taylor_coreset_attention.py:641-687); reference_scores as in
+    article_causal_attention."""
     if q.ndim != 2 or k.ndim != 2 or v.ndim != 2:
         raise ValueError("q, k, v must have shapes [N,D], [N,D], [N,Dv]")
     if q.shape != k.shape:
@@ -139,7 +141,8 @@ def article_causal_attention_single(
         raise ValueError("v must have same sequence length as q/k")
     out = article_causal_attention(q[None, None], k[None, None], v[None, None], degree=degree,
                                    block_size=block_size, scale=scale, compressor=compressor, seed=seed,
-                                   max_monomials=max_monomials, return_state_sizes=return_state_sizes)
+                                   max_monomials=max_monomials, return_state_sizes=return_state_sizes,
+                                   reference_scores=reference_scores)
     if return_state_sizes:
         o, sizes = out
         return o[0, 0], sizes
@@ -159,13 +162,18 @@ def article_causal_attention(
     seed: int = 0,
     max_monomials: int = 5_000_000,
     return_state_sizes: bool = False,
+    reference_scores: bool = False,
 ) -> Union[Tensor, Tuple[Tensor, List[int]]]:
     """[N,D] or [B,H,N,D] (streaming_taylor_coreset_attention.py:690-754); sequence (b, h) uses
-    seed + b*H + h.  All sequences run in one set of launches."""
+    seed + b*H + h.  All sequences run in one set of launches.  reference_scores (not in the reference;
+    default off): every compress call of the level cascade runs on the host, ordered by torch's CPU
+    `keys @ direction` and argsort in the keys' dtype as the reference orders it on this host, instead of
+    the GPU compressor's fixed-order fp64 scores (see fast_article_causal_attention)."""
     if q.ndim == 2:
         return article_causal_attention_single(q, k, v, degree=degree, block_size=block_size, scale=scale,
                                                compressor=compressor, seed=seed, max_monomials=max_monomials,
-                                               return_state_sizes=return_state_sizes)
+                                               return_state_sizes=return_state_sizes,
+                                               reference_scores=reference_scores)
     if q.ndim != 4:
         raise ValueError("q/k/v must be [N,D] or [B,H,N,D]")
     if q.shape != k.shape:
@@ -193,7 +201,9 @@ def article_causal_attention(
     semantics = "exact" if compressor == "none" else "levels"
     res = _engine.prefill(q3, k3, v3, degree=degree, block=block_size, scale=s, semantics=semantics,
                           compressor=compressor, seed=seed, out_dtype=dt,
-                          score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)) if semantics == "levels" else None)
+                          score_keys=_score_keys(kg.reshape(bsz * heads, n, dim)) if semantics == "levels" else None,
+                          reference_keys=_reference_keys(k, bsz * heads, n, dim,
+                                                         reference_scores and semantics == "levels"))
     out = res.out.reshape(bsz, heads, n, dv).to(device=home, dtype=q.dtype)
     if not return_state_sizes:
         return out

@@ -2,7 +2,10 @@
 
 Run in the development container only (the reference tree is not available on the GPU machines):
 
-    python tests/golden/make_golden.py [/path/to/reference]
+    python tests/golden/make_golden.py [/path/to/reference] [case ...]
+
+With case names, only those cases are written (the selection cases below: selection_dtypes,
+selection_near_ties); without, every case.
 
 The reference's public functions are called on fixed synthetic inputs.  While they run, the torch
 RNG calls (randn / rand / randperm) and argsort are wrapped so that the draws the reference consumed,
@@ -23,6 +26,7 @@ import torch
 
 OUT = pathlib.Path(__file__).resolve().parent
 REF = pathlib.Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+ONLY = set(sys.argv[2:])
 
 
 class Recorder:
@@ -90,6 +94,84 @@ def save(name: str, arrays: dict, meta: dict) -> None:
     print(f"wrote {name}.npz ({sum(a.nbytes for a in arrays.values())} raw bytes)")
 
 
+def cpu_model() -> str:
+    for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+        if line.startswith("model name"):
+            return line.split(":", 1)[1].strip()
+    return "unknown"
+
+
+def spied_levels(stc, k, run):
+    """Runs `run()` with MergeReduceCoreset._compress wrapped; returns every call's (src_in, w_in, src_out,
+    w_out) as token indices into k and weights (float64 for the 16-bit and float64 runs)."""
+    compressed = []
+    orig = stc.MergeReduceCoreset._compress
+
+    def spy(self, block):
+        out = orig(self, block)
+        compressed.append((token_index(k, block.keys), block.weights.double().numpy().copy(),
+                           token_index(k, out.keys), out.weights.double().numpy().copy()))
+        return out
+
+    stc.MergeReduceCoreset._compress = spy
+    try:
+        result = run()
+    finally:
+        stc.MergeReduceCoreset._compress = orig
+    return result, compressed
+
+
+def selection_cases(faa, stc, base_meta) -> None:
+    """Coreset selections of the reference in each input dtype (its draws and pair rule run in the keys'
+    dtype), and on keys whose projections nearly tie (rows repeated with one coordinate moved by one
+    ulp), where the order of torch's CPU `keys @ direction` decides which token is kept.  The host's
+    CPU model goes into the metadata: the near-tie orders belong to its BLAS code path."""
+    cpu = torch.device("cpu")
+    if not ONLY or "selection_dtypes" in ONLY:
+        arrays, meta = {}, dict(base_meta, cpu_model=cpu_model(), cases=[])
+        for tag, dtype in (("f64", torch.float64), ("bf16", torch.bfloat16), ("f16", torch.float16)):
+            n, d, dv, B, seed = 320, 16, 8, 32, 13
+            q, k, v = faa._make_data(n, d, dv, radius=1.0, data="unit_ball", device=cpu, dtype=dtype, seed=seed)
+            out, calls = spied_levels(stc, k, lambda: stc.article_causal_attention(
+                q, k, v, degree=2, block_size=B, scale=1.0, compressor="sorted_pair", seed=seed))
+            arrays[f"{tag}_k"] = k.double().numpy()
+            arrays[f"{tag}_levels_ncalls"] = np.array(len(calls))
+            for ci, (si, wi, so, wo) in enumerate(calls):
+                arrays[f"{tag}_levels_call{ci}_src_out"] = so
+                arrays[f"{tag}_levels_call{ci}_w_out"] = wo
+            reps = faa._build_completed_block_reps(k, v, block_size=B, compressor="sorted_pair", seed=seed)
+            arrays[f"{tag}_flat_rep_idx"] = token_index(k, reps.keys)
+            arrays[f"{tag}_flat_rep_w"] = reps.weights.double().numpy()
+            meta["cases"].append(dict(tag=tag, n=n, d=d, dv=dv, block=B, seed=seed))
+        save("selection_dtypes", arrays, meta)
+    if not ONLY or "selection_near_ties" in ONLY:
+        n_base, copies, d, dv, B, seed = 48, 8, 16, 8, 32, 21
+        g = torch.Generator().manual_seed(seed)
+        base = torch.randn(n_base, d, generator=g) * 0.5
+        k = base.repeat_interleave(copies, 0)
+        for r in range(k.shape[0]):
+            j = r % copies
+            if j:
+                c = j - 1
+                k[r, c] = torch.nextafter(k[r, c], torch.tensor(float("inf")))
+        perm = torch.randperm(k.shape[0], generator=g)
+        k = k[perm].contiguous()
+        n = k.shape[0]
+        q = torch.randn(n, d, generator=g) * 0.5
+        v = torch.randn(n, dv, generator=g)
+        _, calls = spied_levels(stc, k, lambda: stc.article_causal_attention(
+            q, k, v, degree=2, block_size=B, scale=1.0, compressor="sorted_pair", seed=seed))
+        arrays = {"q": q.numpy(), "k": k.numpy(), "v": v.numpy(), "levels_ncalls": np.array(len(calls))}
+        for ci, (si, wi, so, wo) in enumerate(calls):
+            arrays[f"levels_call{ci}_src_out"] = so
+            arrays[f"levels_call{ci}_w_out"] = wo.astype(np.float32)
+        reps = faa._build_completed_block_reps(k, v, block_size=B, compressor="sorted_pair", seed=seed)
+        arrays["flat_rep_idx"] = token_index(k, reps.keys)
+        arrays["flat_rep_w"] = reps.weights.numpy()
+        save("selection_near_ties", arrays, dict(base_meta, cpu_model=cpu_model(), n=n, d=d, dv=dv, block=B,
+                                                 seed=seed))
+
+
 def main() -> None:
     sys.path.insert(0, str(REF))
     faa = importlib.import_module("fast_article_attention")
@@ -97,6 +179,9 @@ def main() -> None:
     taa = importlib.import_module("triton_article_attention")
     torch.set_num_threads(1)
     base_meta = {"torch": torch.__version__, "generator": "cpu"}
+    if ONLY:
+        selection_cases(faa, stc, base_meta)
+        return
 
     # ---- flat fast path (config c1 shape) ----
     n, d, dv, B = 1024, 32, 32, 128
@@ -216,6 +301,7 @@ def main() -> None:
                       "key2": faa._taylor_features_degree012(x, 2, key_side=True).numpy(),
                       "query2": faa._taylor_features_degree012(x, 2, key_side=False).numpy(),
                       "taylor3": faa.exp_taylor(x, 3).numpy()}, base_meta)
+    selection_cases(faa, stc, base_meta)
 
 
 if __name__ == "__main__":

@@ -18,7 +18,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 def test_library_exports_header_symbols():
     text = (ROOT / "include" / "stadraws.h").read_text()
     syms = set(re.findall(r"^\s*(?:int64_t|int|void\*|void|const char\*)\s+(sta_\w+)\s*\(", text, flags=re.M))
-    assert len(syms) == 10
+    assert len(syms) == 11
     lib = _native.draws_library()
     for s in syms:
         assert hasattr(lib, s), s
@@ -36,13 +36,15 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("f64", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("seeds,sizes,d,comp", CASES)
-def test_native_draws_equal_python_replay(seeds, sizes, d, comp, f64):
-    """The native replay equals torch's own calls, for float32 draws and for the float64 draws of a
-    float64 caller (which consume the generator differently: different values, not a rounding)."""
-    nat, m_nat = _plan._collect_draws(list(seeds), list(sizes), d, comp, f64)
-    py, m_py = _plan._collect_draws_py(list(seeds), list(sizes), d, comp, f64)
+def test_native_draws_equal_python_replay(seeds, sizes, d, comp, dtype):
+    """The native replay equals torch's own calls, for float32 draws, the float64 draws of a float64
+    caller (which consume the generator differently: different values, not a rounding) and the 16-bit
+    draws of a 16-bit caller (their values held exactly in float32 tables)."""
+    f64 = dtype == torch.float64
+    nat, m_nat = _plan._collect_draws(list(seeds), list(sizes), d, comp, dtype=dtype)
+    py, m_py = _plan._collect_draws_py(list(seeds), list(sizes), d, comp, dtype=dtype)
     assert m_nat == m_py
     for a, b in ((nat.dirs, py.dirs), (nat.unif, py.unif), (nat.perms, py.perms)):
         assert a.shape == b.shape and a.dtype == b.dtype
