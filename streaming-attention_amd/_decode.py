@@ -51,6 +51,38 @@ class _CompletionDraws:
 ACCUMULATE_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
 
 
+class StaticScratchOwners:
+    """Who uses each device's static scratch (sta_decode_step_static keeps the moment partials in one
+    library array per device, so calls that overlap on a device overwrite each other's partials).  A
+    decode state claims its device's scratch for one stream at its first allocation-free step; a call
+    from another state, or from the same state on another stream, is refused until the owner releases
+    it (which first waits for the owner's stream, so the owner's last call has finished)."""
+
+    def __init__(self) -> None:
+        self._owner: Dict[int, Tuple[int, int]] = {}  # device index -> (owner id, stream handle)
+
+    def claim(self, device: int, owner: int, stream: int) -> None:
+        held = self._owner.get(device)
+        if held is not None and held != (owner, stream):
+            what = "another decode state" if held[0] != owner else f"this decode state on another stream ({held[1]:#x})"
+            raise ValueError(f"the static scratch of device {device} is in use by {what}; calls that overlap on "
+                             f"one device would overwrite each other's partials: release_static() the owner first")
+        self._owner[device] = (owner, stream)
+
+    def release(self, device: int, owner: int) -> bool:
+        """Drops `owner`'s claim on `device`; True when it held one."""
+        if self._owner.get(device, (None,))[0] == owner:
+            del self._owner[device]
+            return True
+        return False
+
+    def holder(self, device: int) -> Optional[Tuple[int, int]]:
+        return self._owner.get(device)
+
+
+STATIC_OWNERS = StaticScratchOwners()
+
+
 class DecodeState:
     def __init__(self, streams: int, dim: int, value_dim: int, *, degree: int, block: int, scale: float,
                  compressor: str, seed: int, device: torch.device, eps: float = 1e-12,
@@ -73,6 +105,7 @@ class DecodeState:
         self.degree, self.block, self.scale = int(degree), int(block), float(scale)
         self.compressor, self.seed, self.eps = str(compressor), int(seed), float(eps)
         self.device = device
+        self._dev_index = device.index if device.index is not None else torch.cuda.current_device()
         self.exact = self.compressor == "none"
         # matrix-core products of the state accumulation (block completions, extend): split-bf16 as in the
         # prefill moment scan (the state and every sum stay fp32); fp32 products at degree 5 .. 8
@@ -366,6 +399,9 @@ class DecodeState:
             raise ValueError(f"out must be a contiguous [{self.S}, {self.dv}] float32/bfloat16/float16 tensor "
                              f"on {self.device}")
         flags = _native.DEC_APPEND | _native.DEC_CURRENT | _native.DEC_QUERY
+        stream = self._stream()
+        STATIC_OWNERS.claim(self._dev_index, id(self), stream)
+        self._static_stream = stream
 
         def run():
             st = self.lib.sta_decode_step_static(
@@ -383,6 +419,20 @@ class DecodeState:
         self.buf_len += 1
         self.length += 1
         return out
+
+    def release_static(self) -> None:
+        """Gives up this state's claim on its device's static scratch after waiting for the stream of its
+        allocation-free steps, so that another state (or another stream) may use step_into."""
+        if STATIC_OWNERS.holder(self._dev_index) == (id(self), getattr(self, "_static_stream", None)):
+            torch.cuda.ExternalStream(self._static_stream, device=self.device).synchronize()
+        STATIC_OWNERS.release(self._dev_index, id(self))
+
+    def __del__(self) -> None:
+        try:
+            if STATIC_OWNERS.holder(self._dev_index) is not None:
+                self.release_static()
+        except Exception:
+            pass
 
     def extend(self, k: torch.Tensor, v: torch.Tensor, k64: Optional[torch.Tensor] = None) -> None:
         """update() for every token of k [S, P, d] / v [S, P, dv], in bulk: whole blocks go to the state
@@ -482,10 +532,12 @@ class DecodeState:
             return self.length
         return self.buf_len + self.m * bin(self.blocks).count("1")
 
-    def reference_state_bytes(self, elem: int, include_feature_map: bool = False) -> int:
+    def reference_state_bytes(self, elem: int, include_feature_map: bool = False,
+                              value_dim: Optional[int] = None) -> int:
         """ArticleStreamingAttention.state_size_bytes of one stream for element size `elem`
-        (streaming_taylor_coreset_attention.py:298-306, :495-506, :611-612)."""
-        d, dv = self.d, self.dv
+        (streaming_taylor_coreset_attention.py:298-306, :495-506, :611-612); value_dim: the object's
+        whole value width when this state holds one column group of it."""
+        d, dv = self.d, self.dv if value_dim is None else int(value_dim)
         total = self.F * (1 + dv) * elem
         if include_feature_map:
             for l in range(1, self.degree + 1):
@@ -576,3 +628,111 @@ class DecodeState:
         if self.score_f64:
             ts += [self.buf_k64, self.lev_k64]
         return int(sum(t.numel() * t.element_size() for t in ts))
+
+
+class ColumnGroups:
+    """Value widths above the decode kernels' max_dv: one DecodeState per group of at most max_dv value
+    columns, every group fed the same keys with the same seeds.  A stream's selections, denominators
+    and statistics depend on its keys and draws only, so every group keeps the same coreset (the same
+    tokens and weights) and the groups' outputs concatenate to the whole value width; the key-side work
+    (feature moments of the denominators, compression) runs once per group.  The reference's streaming
+    object has no value-width bound (streaming_taylor_coreset_attention.py:523-575)."""
+
+    def __init__(self, streams: int, dim: int, value_dim: int, **kw) -> None:
+        w = _native.limits()["max_dv"]
+        if value_dim <= w:
+            raise ValueError("ColumnGroups is for value widths above the kernels' max_dv; use DecodeState")
+        self.bounds = [(c0, min(c0 + w, value_dim)) for c0 in range(0, value_dim, w)]
+        self.groups = [DecodeState(streams, dim, c1 - c0, **kw) for c0, c1 in self.bounds]
+        self.dv = int(value_dim)
+
+    def __getattr__(self, name: str):
+        # counters, shapes and key-side state are the same in every group: group 0's
+        if name in ("groups", "bounds", "dv"):
+            raise AttributeError(name)
+        return getattr(self.groups[0], name)
+
+    @property
+    def timer(self):
+        return self.groups[0].timer
+
+    @timer.setter
+    def timer(self, t) -> None:
+        for g in self.groups:
+            g.timer = t
+
+    def _cols(self, v: Optional[torch.Tensor]) -> List[Optional[torch.Tensor]]:
+        if v is None:
+            return [None] * len(self.groups)
+        if v.shape[-1] != self.dv:
+            raise ValueError(f"values must have {self.dv} columns, got {v.shape[-1]}")
+        return [v[..., c0:c1].contiguous() for c0, c1 in self.bounds]
+
+    def reserve_draws(self, tokens: int) -> int:
+        return [g.reserve_draws(tokens) for g in self.groups][0]
+
+    def update(self, k: torch.Tensor, v: torch.Tensor, k64: Optional[torch.Tensor] = None) -> None:
+        for g, vg in zip(self.groups, self._cols(v)):
+            g.update(k, vg, k64)
+
+    def query(self, q: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+              stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return torch.cat([g.query(q, out_dtype, stats if i == 0 else None) for i, g in enumerate(self.groups)], -1)
+
+    def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out_dtype: torch.dtype = torch.float32,
+             stats: Optional[torch.Tensor] = None, k64: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return torch.cat([g.step(q, k, vg, out_dtype, stats if i == 0 else None, k64)
+                          for i, (g, vg) in enumerate(zip(self.groups, self._cols(v)))], -1)
+
+    def release_static(self) -> None:
+        for g in self.groups:
+            g.release_static()
+
+    def step_into(self, q, k, v, out, stats=None):
+        raise ValueError(f"step_into writes one kernel call's columns: value_dim {self.dv} runs as column groups; "
+                         f"use step()")
+
+    def extend(self, k: torch.Tensor, v: torch.Tensor, k64: Optional[torch.Tensor] = None) -> None:
+        for g, vg in zip(self.groups, self._cols(v)):
+            g.extend(k, vg, k64)
+
+    def full_moments(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        parts = [g.full_moments() for g in self.groups]
+        return parts[0][0], torch.cat([p[1] for p in parts], -1)
+
+    def level_items(self):
+        per = [g.level_items() for g in self.groups]
+        out = []
+        for lv in zip(*per):
+            if lv[0] is None:
+                out.append(None)
+            else:
+                out.append((lv[0][0], torch.cat([x[1] for x in lv], -1), lv[0][2], lv[0][3]))
+        return out
+
+    def buffer_items(self):
+        per = [g.buffer_items() for g in self.groups]
+        return per[0][0], torch.cat([p[1] for p in per], -1), per[0][2]
+
+    def reference_state_bytes(self, elem: int, include_feature_map: bool = False) -> int:
+        return self.groups[0].reference_state_bytes(elem, include_feature_map, value_dim=self.dv)
+
+    def state_dict(self) -> Dict[str, object]:
+        return {"format": 2, "value_dim": self.dv, "column_groups": [g.state_dict() for g in self.groups]}
+
+    def load_state_dict(self, sd: Dict[str, object]) -> None:
+        if sd.get("format") != 2 or sd.get("value_dim") != self.dv or \
+                len(sd.get("column_groups", ())) != len(self.groups):
+            raise ValueError("decode state does not match this object's value column groups")
+        for g, gsd in zip(self.groups, sd["column_groups"]):
+            g.load_state_dict(gsd)
+
+    def device_bytes(self) -> int:
+        return sum(g.device_bytes() for g in self.groups)
+
+
+def decode_state(streams: int, dim: int, value_dim: int, **kw):
+    """A DecodeState, or ColumnGroups of them when value_dim exceeds the kernels' max_dv."""
+    if value_dim > _native.limits()["max_dv"]:
+        return ColumnGroups(streams, dim, value_dim, **kw)
+    return DecodeState(streams, dim, value_dim, **kw)

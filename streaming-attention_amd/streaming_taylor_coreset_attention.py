@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import argparse
 import math
+import weakref
 from dataclasses import dataclass
 from typing import List, Optional, Tuple, Union
 
@@ -264,7 +265,7 @@ class _SketchView:
     den_moments / num_moments per degree, in the reference's feature order."""
 
     def __init__(self, owner: "ArticleStreamingAttention") -> None:
-        self._o = owner
+        self._o = weakref.proxy(owner)  # no reference cycle: the object and its state go when it does
 
     @property
     def length(self) -> int:
@@ -307,7 +308,7 @@ class _CoresetView:
     :332-506)."""
 
     def __init__(self, owner: "ArticleStreamingAttention") -> None:
-        self._o = owner
+        self._o = weakref.proxy(owner)  # no reference cycle: the object and its state go when it does
 
     @property
     def length(self) -> int:
@@ -416,7 +417,7 @@ class ArticleStreamingAttention:
         self.streams = 1 if streams is None else int(streams)
         # a float64 object's compress calls score its float64 keys with float64 draws, as the reference's
         # float64 run does (streaming_taylor_coreset_attention.py:441-457)
-        self._st = _decode.DecodeState(self.streams, self.dim, self.value_dim, degree=self.degree,
+        self._st = _decode.decode_state(self.streams, self.dim, self.value_dim, degree=self.degree,
                                        block=self.block_size, scale=self.scale, compressor=self.compressor,
                                        seed=self.seed, device=self.device, eps=self.denominator_eps,
                                        score_f64=self.dtype == torch.float64)
@@ -492,13 +493,19 @@ class ArticleStreamingAttention:
         """step() into a caller-owned `out` ([value_dim], or [S, value_dim] batched) with no device
         allocation, for serving loops and graph capture: the inputs must already be contiguous device
         tensors of this object's shapes and one dtype; a token that completes a block is refused (call
-        step() for it)."""
+        step() for it).  The device's static scratch serves one object on one stream at a time: another
+        object's (or another stream's) step_into is refused until this one calls release_static()."""
         if self._single:
             query, key, value, o2 = query.view(1, -1), key.view(1, -1), value.view(1, -1), out.view(1, -1)
         else:
             o2 = out
         self._st.step_into(query, key, value, o2)
         return out
+
+    def release_static(self) -> None:
+        """Lets another object (or another stream) use step_into on this device: waits for this object's
+        allocation-free steps and gives up its claim on the device's static scratch."""
+        self._st.release_static()
 
     @torch.no_grad()
     def extend(self, keys: Tensor, values: Tensor) -> None:

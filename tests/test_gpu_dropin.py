@@ -88,6 +88,48 @@ def test_value_width_above_256(api):
         assert rel(out[0, h], ref) < 1e-4
 
 
+def test_streaming_value_width_above_256():
+    """ArticleStreamingAttention with value_dim 600 (column groups of 256 + 256 + 88, every group fed the
+    same keys and seeds): prefill, extend and steps through block completions against the oracle's level
+    semantics; every group keeps the same coreset; the moments, the level items and a save / resume
+    cover all 600 columns; step_into refuses (one kernel call's columns only)."""
+    s_, n, d, dv, block, prompt = 2, 330, 16, 600, 64, 150
+    print("streaming value width 600", flush=True)
+    q, k, v = orc.make_data((s_,), n, d, dv, radius=1.0, data="unit_ball", seed=8)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    st = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=1.0, device=DEV, seed=0, streams=s_)
+    out_p = st.prefill(qd[:, :100], kd[:, :100], vd[:, :100])
+    st.extend(kd[:, 100:prompt], vd[:, 100:prompt])
+    outs = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(prompt, n - 20)], dim=1)
+    saved = st.state_dict()
+    st2 = stc.ArticleStreamingAttention(d, dv, degree=2, block_size=block, scale=1.0, device=DEV, seed=0, streams=s_)
+    st2.load_state_dict(saved)
+    tail1 = torch.stack([st.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(n - 20, n)], dim=1)
+    tail2 = torch.stack([st2.step(qd[:, i], kd[:, i], vd[:, i]) for i in range(n - 20, n)], dim=1)
+    den, num = st._st.full_moments()
+    torch.cuda.synchronize()
+    assert out_p.shape == (s_, 100, dv) and outs.shape == (s_, n - 20 - prompt, dv)
+    assert torch.equal(tail1, tail2)
+    groups = st._st.groups
+    assert [g.dv for g in groups] == [256, 256, 88]
+    for lv in range(len(groups[0].level_items())):
+        items = [g.level_items()[lv] for g in groups]
+        if items[0] is not None:
+            assert all(torch.equal(it[3], items[0][3]) and torch.equal(it[2], items[0][2]) for it in items)
+    for s in range(s_):
+        ref = orc.levels_forward(q[s], k[s], v[s], degree=2, block=block, scale=1.0, compressor="sorted_pair", seed=s)
+        assert rel(out_p[s], ref[:100]) < 1e-4
+        assert rel(outs[s], ref[prompt: n - 20]) < 1e-4
+        assert rel(tail1[s], ref[n - 20:]) < 1e-4
+        fk = orc.features(k[s].double(), 2, True)
+        assert rel(num[s], fk.T @ v[s].double()) < 2e-5 and rel(den[s], fk.sum(0)) < 2e-5
+    items = st.coreset.items()
+    assert items.values.shape[-1] == dv
+    with pytest.raises(ValueError, match="column groups"):
+        st.step_into(qd[:, 0].contiguous(), kd[:, 0].contiguous(), vd[:, 0].contiguous(),
+                     torch.empty(s_, dv, device=DEV))
+
+
 def _nodes_equal_calls(res, calls):
     src, w = res.node_src.cpu().numpy()[0], res.node_w.cpu().numpy()[0]
     nodes = [node for node in range(res.plan.n_nodes) if int(res.plan.meta[node, 0]) > 0]

@@ -518,3 +518,22 @@ def test_window_cover_holds_every_monomial_once_in_fewer_quads(d, deg):
     assert len(cover) <= rows
     if (d, deg) == (16, 3):
         assert len(cover) == 208 and _plan.feature_tiles(16, 3).n_tiles == 64
+
+
+def test_static_scratch_owner_registry():
+    """One decode state on one stream per device may use the static scratch; others are refused until
+    the owner releases it (the allocation-free step's overlap guard; CPU logic only)."""
+    import _decode
+
+    reg = _decode.StaticScratchOwners()
+    reg.claim(0, owner=1, stream=0x10)
+    reg.claim(0, owner=1, stream=0x10)  # the owner again, same stream
+    reg.claim(1, owner=2, stream=0x20)  # another device is independent
+    with pytest.raises(ValueError, match="another decode state"):
+        reg.claim(0, owner=2, stream=0x10)
+    with pytest.raises(ValueError, match="another stream"):
+        reg.claim(0, owner=1, stream=0x11)
+    assert not reg.release(0, owner=2)
+    assert reg.release(0, owner=1)
+    reg.claim(0, owner=2, stream=0x11)
+    assert reg.holder(0) == (2, 0x11)

@@ -40,6 +40,7 @@ def _lockstep(streams, d, dv, block, prefix, steps, compressor="sorted_pair", dt
             used += 1
         assert torch.equal(got, want), f"token {i}"
     torch.cuda.synchronize()
+    st.release_static()
     assert used >= steps - steps // block - 1
     return used
 
@@ -80,3 +81,30 @@ def test_static_step_refuses_a_working_set_beyond_the_scratch():
                                     None)
     assert st == _native.STA_ERR_SCRATCH
     assert b"static scratch" in lib.sta_status_string(st)
+
+
+def test_static_scratch_serves_one_object_and_stream_at_a_time():
+    """The device's static scratch is claimed by the first object's step_into on its stream; another
+    object's step_into, or the same object's on another stream, is refused (their partials would
+    overwrite each other) until release_static()."""
+    print("no-alloc owner check", flush=True)
+    d, dv, s_ = 16, 16, 4
+    a, b = (stc.ArticleStreamingAttention(d, dv, degree=2, block_size=64, scale=0.25, device=DEV, streams=s_)
+            for _ in range(2))
+    x = torch.randn(s_, d, device=DEV) * 0.25
+    y = torch.randn(s_, dv, device=DEV)
+    out = torch.empty(s_, dv, device=DEV)
+    a.step_into(x, x, y, out)
+    with pytest.raises(ValueError, match="another decode state"):
+        b.step_into(x, x, y, out)
+    side = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(side):
+        with pytest.raises(ValueError, match="another stream"):
+            a.step_into(x, x, y, out)
+    a.release_static()
+    b.step_into(x, x, y, out)
+    want = a.step(x, x, y)  # a's second token, allocating path
+    got = b.step_into(x, x, y, out)  # b's second token: the same inputs, so the same outputs
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    b.release_static()
