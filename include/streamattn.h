@@ -283,11 +283,19 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
  *   fp64 products and sums kept whole for the sort, the pair rule is decided in fp64.  Otherwise dirs /
  *   unif are float and scores are fp64 sums of the fp32 products rounded to fp32.
  *   outputs: node_src [BH][n_nodes][cap] (global token index of each kept item), node_w (its weight).
+ *   Ancestor scores (levels plans, fp32 / 16-bit keys; anc_levels = 0 and NULLs: off): in a launch that
+ *     passes anc [n_nodes][anc_levels] (the draw slots of each raw node's ancestors at levels 1 ..
+ *     anc_levels, -1 where that call is not sorted_pair), each raw node's call also projects its key
+ *     rows onto those directions and writes level_scores [BH][anc_levels][n]; in later launches (anc
+ *     NULL, the same anc_levels and level_scores) a merge node at level 1 .. anc_levels (node_level
+ *     [n_nodes]) reads its items' scores there instead of gathering their key rows.  Every score is the
+ *     fp64 chain the merge would compute, so the nodes are the same bit for bit.  anc_levels <= 4.
  */
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
                        int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
                        const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
-                       float* node_w, void* stream);
+                       float* node_w, const int32_t* node_level, const int32_t* anc, int anc_levels,
+                       float* level_scores, void* stream);
 
 /*
  * Segment-mean representatives of completed blocks (the Triton path's coreset).

@@ -31,6 +31,13 @@ MOMENT_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
 # cannot run beside it, and a compressor launch that starts first delays the scan's workgroups
 # (32 x 65536 tokens: 9.49 ms per prefill on two streams, 9.38 ms on one; 1 head: 0.618 / 0.609 ms).
 OVERLAP_COMPRESS = os.environ.get("STA_OVERLAP_COMPRESS", "0") != "0"
+# Levels plans: the level-0 compress calls also score their key rows for their ancestors' calls
+# (sta_compress_nodes' ancestor scores), so the merges read 4 bytes per item instead of a key row.
+# The nodes are the same bit for bit either way (STA_ANCESTOR_SCORES=0 keeps the gathers).
+ANCESTOR_SCORES = os.environ.get("STA_ANCESTOR_SCORES", "1") != "0"
+# levels scored that way (at most 4): each costs the level-0 calls one more fp64 chain per row, and pays
+# where a level's gathers are large
+ANCESTOR_LEVELS = int(os.environ.get("STA_ANCESTOR_LEVELS", "3"))
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 
@@ -358,6 +365,14 @@ def prefill(
             _, desc = _plan.draws_for(plan, seeds[:1], d, compressor)
             dirs_d, unif_d, perms_d, desc_d = (fdraw(dr.dirs), fdraw(dr.unif), _i32(dr.perms, dev), _i32(desc, dev))
         batches_d = _on_device(("batches",) + pkey, dev, lambda: [_i32(b, dev) for b in plan.batches])
+        # levels: the level-0 calls also score their rows for their ancestors' calls, which then read
+        # one score per item instead of gathering key rows (float64 scoring keeps the gathers)
+        anc_levels, anc_d, level_d = 0, None, None
+        if ANCESTOR_SCORES and not f64:
+            anc_levels, level_of, anc = _plan.ancestor_table(plan, desc, ANCESTOR_LEVELS)
+            if anc_levels:
+                anc_d, level_d = _on_device(("anc", anc_levels) + pkey, dev,
+                                            lambda: (_i32(anc, dev), _i32(level_of, dev)))
 
     lrows, lld, _ = _native.moment_partials_layout(n, dv)
     low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
@@ -428,18 +443,23 @@ def prefill(
     elif plan.batches:
         node_src = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.int32)
         node_w = torch.empty((bh, plan.n_nodes, plan.cap), device=dev, dtype=torch.float32)
+        lscore = torch.empty((bh, anc_levels, n), device=dev, dtype=torch.float32) if anc_levels else None
         if side is not main:
             node_src.record_stream(side)
             node_w.record_stream(side)
+            if lscore is not None:
+                lscore.record_stream(side)
         with torch.cuda.stream(side):
             k3_stream = _native.stream_handle(dev)
-            for bd in batches_d:
-                def k3_launch(bd=bd):
+            for bi, bd in enumerate(batches_d):
+                def k3_launch(bd=bd, first=bi == 0):
                     st = lib.sta_compress_nodes(
                         (score_keys if f64 else k3).data_ptr(), _native.STA_F64 if f64 else dt, bh, n, d,
                         bd.data_ptr(), int(bd.numel()), desc_d.data_ptr(),
                         plan.n_nodes, plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(),
-                        dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(), k3_stream)
+                        dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(),
+                        _native.ptr(level_d), _native.ptr(anc_d) if first else None, anc_levels,
+                        _native.ptr(lscore), k3_stream)
                     _native.check(st, "sta_compress_nodes")
 
                 _run(timer, "compress", k3_launch)

@@ -68,7 +68,8 @@ _SIGNATURES = {
     "sta_moment_partials_layout": (_i32, [_i64, _i32, ctypes.POINTER(_i64), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "sta_compress_nodes": (
         _i32,
-        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p, _c_p],
+        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p,
+         _c_p, _c_p, _i32, _c_p, _c_p],  # ... node_src node_w node_level anc anc_levels level_scores stream
     ),
     "sta_segment_mean": (_i32, [_c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _c_p, _c_p, _c_p]),
     "sta_block_attention": (

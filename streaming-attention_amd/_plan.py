@@ -1093,6 +1093,34 @@ def levels_plan(n: int, block: int, compressor: str) -> NodePlan:
     return _cached(("levels", n, block, compressor), build)
 
 
+CMP_MAX_ANC = 4  # ancestor levels a level-0 compress call can score (sta_compress_nodes)
+
+
+def ancestor_table(plan: NodePlan, desc: np.ndarray,
+                   max_levels: int = CMP_MAX_ANC) -> Tuple[int, Optional[np.ndarray], Optional[np.ndarray]]:
+    """Ancestor scores of a levels plan (sta_compress_nodes): (anc_levels, node_level int32 [n_nodes], anc
+    int32 [n_nodes, anc_levels]) where anc[node (0, j), l - 1] is the draw slot of node (l, j >> l), the
+    call that later sorts block j's surviving tokens at level l, or -1 where that call is not
+    sorted_pair; rows of merge nodes are -1.  (0, None, None) when the plan has no merge levels or its
+    level-0 calls do not project (desc: the plan's descriptors with methods filled in)."""
+    if plan.mode != MODE_LEVELS or plan.level_of is None or len(plan.batches) < 2 or max_levels < 1:
+        return 0, None, None
+    levels = len(plan.batches)
+    a_lev = min(levels - 1, max_levels, CMP_MAX_ANC)
+    first = [int(b[0]) for b in plan.batches]
+    counts = [len(b) for b in plan.batches]
+    if not np.all(desc[first[0]: first[0] + counts[0], 5] == METHOD_SORTED_PAIR):
+        return 0, None, None
+    anc = np.full((plan.n_nodes, a_lev), -1, dtype=np.int32)
+    for l in range(1, a_lev + 1):
+        j = np.arange(counts[0]) >> l
+        ok = j < counts[l]
+        node = first[l] + np.minimum(j, counts[l] - 1)
+        slot = np.where(ok & (desc[node, 5] == METHOD_SORTED_PAIR), desc[node, 6], -1)
+        anc[first[0]: first[0] + counts[0], l - 1] = slot
+    return a_lev, plan.level_of.astype(np.int32), anc
+
+
 def segment_plan(n: int, block: int, stride: int) -> Tuple[NodePlan, int, int]:
     """Segment-mean reps of completed blocks with a later query (triton_article_attention.py:189-245,
     active for i >= (rep_block+1)*B with weight = stride, :353-357)."""

@@ -550,9 +550,13 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
                        int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
                        const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
-                       float* node_w, void* stream) {
+                       float* node_w, const int32_t* node_level, const int32_t* anc, int anc_levels,
+                       float* level_scores, void* stream) {
   if (!k || !batch_nodes || !node_desc || !node_src || !node_w) return STA_ERR_ARG;
   const bool f64 = dtype == STA_F64;
+  if (anc_levels < 0 || anc_levels > sta::CMP_MAX_ANC) return STA_ERR_ARG;
+  if (anc_levels > 0 && (f64 || !node_level || !level_scores)) return STA_ERR_ARG;
+  if (anc && anc_levels <= 0) return STA_ERR_ARG;
   if (!dtype_ok(dtype) && !f64) return STA_ERR_DTYPE;
   if (bh <= 0 || n <= 0 || d <= 0 || n_nodes <= 0 || cap <= 0 || max_in <= 0) return STA_ERR_SHAPE;
   if (d > kMaxD || max_in > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
@@ -563,11 +567,19 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
   a.k = k; a.dtype = dtype; a.n = n; a.d = d; a.batch = batch_nodes; a.desc = node_desc; a.n_nodes = n_nodes;
   a.cap = cap; a.dirs = dirs; a.unif = unif; a.perms = perms; a.n_draws = n_draws; a.max_in = max_in;
   a.node_src = node_src; a.node_w = node_w; a.f64 = f64 ? 1 : 0;
-  const size_t smem = sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in, f64));
-  const int st = lds_limit(reinterpret_cast<const void*>(sta::compress_kernel), smem);
+  a.anc = anc; a.node_level = node_level; a.anc_levels = anc_levels; a.lscore = level_scores;
+  const size_t smem =
+      sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in, f64, anc ? 2 * (1 + anc_levels) * d : 0));
+  // the ancestor-scoring instantiation for a launch that passes the ancestor table (its raw nodes)
+  const void* fn = anc ? reinterpret_cast<const void*>(sta::compress_kernel<true>)
+                       : reinterpret_cast<const void*>(sta::compress_kernel<false>);
+  const int st = lds_limit(fn, smem);
   if (st != STA_OK) return st;
-  hipLaunchKernelGGL(sta::compress_kernel, dim3(static_cast<unsigned>(n_batch), static_cast<unsigned>(bh)),
-                     dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
+  const dim3 grid(static_cast<unsigned>(n_batch), static_cast<unsigned>(bh));
+  if (anc)
+    hipLaunchKernelGGL(sta::compress_kernel<true>, grid, dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(sta::compress_kernel<false>, grid, dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
   return check_launch();
 }
 

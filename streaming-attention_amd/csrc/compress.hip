@@ -36,15 +36,20 @@ constexpr int NODE_DESC = 8;  // kind, a, b, n_in, n_out, method, draw_slot, n_o
 constexpr int CMP_MAX_IN = 4096;
 constexpr int CMP_THREADS = 256;
 constexpr int CMP_MAX_D = 256;  // key width the direction buffer holds
+// Ancestor scores (levels plans): a level-0 call also projects its key rows onto the directions of its
+// node's ancestors at levels 1 .. CMP_MAX_ANC, so the merges there read one score per item instead of
+// gathering the item's key row (the lower levels, where the merges' gathers are largest).
+constexpr int CMP_MAX_ANC = 4;
 
 // Dynamic LDS of compress_kernel for calls of at most max_in items (M = max_in rounded up to 4):
 // sort keys [M] (16-byte aligned, padded for 4-wide reads; [2M] as 64-bit keys with f64), source
 // indices [M], weights [M], sorted positions [M], projection direction [CMP_MAX_D] floats (doubles
-// with f64).
+// with f64), then with ancestor scores the node's and its ancestors' directions as doubles
+// [1 + anc][d] (anc_dirs = 2 (1 + anc) d floats).
 __host__ __device__ constexpr int cmp_round4(int n) { return (n + 3) & ~3; }
 __host__ __device__ constexpr int cmp_key_floats(int max_in, bool f64) { return (f64 ? 2 : 1) * cmp_round4(max_in); }
-__host__ __device__ constexpr int cmp_smem_floats(int max_in, bool f64 = false) {
-  return cmp_key_floats(max_in, f64) + 3 * cmp_round4(max_in) + (f64 ? 2 : 1) * CMP_MAX_D;
+__host__ __device__ constexpr int cmp_smem_floats(int max_in, bool f64 = false, int anc_dirs = 0) {
+  return cmp_key_floats(max_in, f64) + 3 * cmp_round4(max_in) + (f64 ? 2 : 1) * CMP_MAX_D + anc_dirs;
 }
 // decode_compress_kernel: sort keys (as above), input handles, weights, positions, sorted positions [M]
 // each, the running output's handles, weights, positions [M/2 + 1 rounded up to 4] each, direction.
@@ -70,6 +75,13 @@ struct CompressArgs {
   int32_t* node_src;  // [BH][n_nodes][cap]
   float* node_w;      // [BH][n_nodes][cap]
   int f64;            // 1: k is float64 [BH][n][d], draws float64 (float64 scoring)
+  // ancestor scores (fp32 / 16-bit keys): anc [n_nodes][anc_levels] the draw slots of a raw node's
+  // ancestors at levels 1 .. anc_levels (-1: no sorted_pair call there), node_level [n_nodes], lscore
+  // [BH][anc_levels][n] the scores of every key row for its ancestor at each level; anc_levels = 0: off
+  const int32_t* anc;
+  const int32_t* node_level;
+  int anc_levels;
+  float* lscore;
 };
 
 // A bf16 / fp16 element from its 16 bits.
@@ -154,6 +166,40 @@ __device__ __forceinline__ void projection_scores2(const void* k0, int64_t off0,
   }
   s0 = static_cast<float>(a0);
   s1 = static_cast<float>(a1);
+}
+
+// Projection scores of one key row onto its node's direction (dird[0 .. d)) and its ancestors'
+// (dird[(1 + l) d ..) for l < na), the directions held as doubles: every chain accumulates the fp64
+// products in dimension order, as projection_scores2 does, so each equals the score the call at that
+// level would compute from the row.  acc[0] is the node's own score, acc[1 + l] the ancestor's at level
+// 1 + l.  fp32 rows are read in 16-byte units when `vec`; each element is converted once.
+__device__ __forceinline__ void projection_scores_anc(const void* k, int64_t off, int d, int dtype, bool vec,
+                                                      const double* dird, int na, double (&acc)[1 + CMP_MAX_ANC]) {
+#pragma unroll
+  for (int l = 0; l <= CMP_MAX_ANC; ++l) acc[l] = 0.0;
+  auto step = [&](double x, int col) {
+#pragma unroll
+    for (int l = 0; l <= CMP_MAX_ANC; ++l)
+      if (l <= na) acc[l] = fma(x, dird[l * d + col], acc[l]);
+  };
+  if (vec && dtype == F32) {
+    const floatx4* r = reinterpret_cast<const floatx4*>(static_cast<const float*>(k) + off);
+    const int nu = d / 4;
+    for (int u0 = 0; u0 < nu; u0 += 8) {
+      floatx4 x[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if (u0 + t < nu) x[t] = r[u0 + t];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (u0 + t >= nu) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) step(static_cast<double>(x[t][e]), 4 * (u0 + t) + e);
+      }
+    }
+  } else {
+    for (int col = 0; col < d; ++col) step(static_cast<double>(load_elem(k, off + col, dtype)), col);
+  }
 }
 
 // Unsigned key whose order is the float order (-0 = +0; NaN above everything), so that (key, position)
@@ -290,6 +336,9 @@ __device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int 
   __syncthreads();
 }
 
+// ANC: the launch of raw (level-0) nodes that also write their ancestors' scores (a separate
+// instantiation: its score registers would cost every other launch occupancy)
+template <bool ANC>
 __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
   extern __shared__ __align__(16) float cmp_smem[];
   const int M = cmp_round4(a.max_in);
@@ -321,12 +370,25 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   const double* u64 = static_cast<const double*>(a.unif) + uoff;
   const int pc = n_in / 2;
   double u_first[2] = {0.0, 0.0};  // a float uniform converts exactly
+  // ancestor scores: a raw node's ancestors with a sorted_pair call (their directions follow the
+  // node's own in LDS; slots of -1 get a zero direction, their scores are not written)
+  const int na_lev = (ANC && kind == KIND_RAW && !f64 && a.anc_levels > 0) ? a.anc_levels : 0;
+  double* dird_s = reinterpret_cast<double*>(dir_s + CMP_MAX_D);  // 8-byte aligned: CMP_MAX_D is even
+  const int32_t* anc = a.anc + static_cast<int64_t>(node) * (na_lev > 0 ? na_lev : 0);
   if (pairs) {
     const int64_t doff = (bh * a.n_draws + slot) * a.d;
     if (f64) {
       for (int e = tid; e < a.d; e += CMP_THREADS) dir64_s[e] = static_cast<const double*>(a.dirs)[doff + e];
     } else {
       for (int e = tid; e < a.d; e += CMP_THREADS) dir_s[e] = static_cast<const float*>(a.dirs)[doff + e];
+      // with ancestor scores: the node's direction and its ancestors' as doubles after the float one
+      for (int e = tid; e < (na_lev > 0 ? (1 + na_lev) * a.d : 0); e += CMP_THREADS) {
+        const int l = e / a.d;
+        const int s_l = l == 0 ? slot : anc[l - 1];
+        dird_s[e] = s_l >= 0 ? static_cast<double>(
+                                   static_cast<const float*>(a.dirs)[(bh * a.n_draws + s_l) * a.d + (e - l * a.d)])
+                             : 0.0;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r)
@@ -375,6 +437,27 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
     for (int i = tid; i < n_in; i += CMP_THREADS)
       uk[i] = sort_key64(projection_score64(k64 + (bh * a.n + src_s[i]) * a.d, a.d, vec64, dir64_s));
     rank_sort64(uk, pos_s, n_in, tid, CMP_THREADS);
+  } else if (na_lev > 0) {
+    // level-0 call with ancestor scores: the node's own score and the scores for its ancestors' calls
+    // from one pass over each row
+    const bool vec = a.dtype == F32 && (a.d % 4) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
+    for (int i = tid; i < n_in; i += CMP_THREADS) {
+      double acc[1 + CMP_MAX_ANC];
+      projection_scores_anc(a.k, (bh * a.n + src_s[i]) * a.d, a.d, a.dtype, vec, dird_s, na_lev, acc);
+      key_s[i] = static_cast<float>(acc[0]);
+#pragma unroll
+      for (int l = 0; l < CMP_MAX_ANC; ++l) {
+        if (l >= na_lev) break;
+        if (anc[l] >= 0) a.lscore[(bh * na_lev + l) * a.n + src_s[i]] = static_cast<float>(acc[1 + l]);
+      }
+    }
+    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
+  } else if (kind == KIND_MERGE && !f64 && a.anc_levels > 0 && a.node_level[node] >= 1 &&
+             a.node_level[node] <= a.anc_levels) {
+    // a merge whose items' scores for this call were written by their level-0 calls
+    const float* ls = a.lscore + (bh * a.anc_levels + (a.node_level[node] - 1)) * a.n;
+    for (int i = tid; i < n_in; i += CMP_THREADS) key_s[i] = ls[src_s[i]];
+    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
   } else {
     const int epu = a.dtype == F32 ? 4 : 8;
     const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;

@@ -368,3 +368,38 @@ def test_cpu_inputs_round_trip():
     out = faa.fast_article_causal_attention(q, k, v, degree=2, block_size=64, scale=1.0)
     assert out.device.type == "cpu"
     assert rel(out, orc.fast_path_forward(q, k, v, degree=2, block=64, scale=1.0)) < FP32_TOL
+
+
+@pytest.mark.parametrize("n,d,block,dtype,comp", [(3000, 16, 64, torch.float32, "sorted_pair"),
+                                                  (2100, 64, 32, torch.bfloat16, "sorted_pair"),
+                                                  (1500, 6, 33, torch.float32, "sorted_pair"),
+                                                  (900, 160, 16, torch.float16, "sorted_pair"),
+                                                  (600, 8, 2, torch.float32, "sorted_pair"),
+                                                  (700, 8, 16, torch.float32, "random")])
+def test_ancestor_scores_keep_every_node(n, d, block, dtype, comp, monkeypatch):
+    """The level-0 compress calls' scores for their ancestors' calls (read by the merges instead of
+    gathering key rows) give every node bit for bit as the gathers do, and the oracle's cascade."""
+    print(f"ancestor scores n={n} d={d} block={block} {dtype} {comp}", flush=True)
+    q, k, v = orc.make_data((2,), n, d, 8, radius=1.0, data="unit_ball", seed=n + d)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    res = {}
+    for on in (True, False):
+        monkeypatch.setattr(_engine, "ANCESTOR_SCORES", on)
+        r = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block=block, scale=0.5, semantics="levels",
+                            compressor=comp, seed=4)
+        res[on] = (r.node_src.cpu(), r.node_w.cpu(), r.out.float().cpu(), r.plan)
+    torch.cuda.synchronize()
+    assert torch.equal(res[True][0], res[False][0]) and torch.equal(res[True][1], res[False][1])
+    assert torch.equal(res[True][2], res[False][2])
+    plan = res[True][3]
+    for h in range(2):
+        state = orc.LevelState()
+        g = torch.Generator(device="cpu")
+        g.manual_seed(4 + h)
+        keys = k[h].float().numpy()
+        for b in range(n // block):
+            orc.level_block_complete(state, g, np.arange(b * block, (b + 1) * block, dtype=np.int64), keys, comp)
+        for node in range(plan.n_nodes):
+            size = int(plan.meta[node, 0])
+            c = state.calls[int(plan.desc[node, 6])]
+            assert np.array_equal(res[True][0][h, node, :size].numpy(), c.src_out), f"head {h} node {node}"

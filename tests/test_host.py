@@ -70,7 +70,8 @@ def test_library_rejects_bad_arguments_without_touching_a_device():
     assert lib.sta_moment_columns_ok(64, 2, 64, 5, 1) == 1
     assert lib.sta_moment_columns_ok(64, 2, 64, 5, 0) == 0 and lib.sta_moment_columns_ok(64, 3, 64, 5, 1) == 0
     assert lib.sta_moment_columns_ok(64, 2, 32, 5, 1) == 0 and lib.sta_moment_columns_ok(64, 2, 64, 4, 1) == 0
-    assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None, None) == _native.STA_ERR_ARG
+    assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None,
+                                  None, None, 0, None, None) == _native.STA_ERR_ARG
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
     # flash: null pointers, D beyond the limit, strides not whole 4-element units, misaligned rows
     assert lib.sta_flash_attention(None, 16, 16, 0, 1, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_ARG
@@ -537,3 +538,25 @@ def test_static_scratch_owner_registry():
     assert reg.release(0, owner=1)
     reg.claim(0, owner=2, stream=0x11)
     assert reg.holder(0) == (2, 0x11)
+
+
+def test_ancestor_table_slots():
+    """Each level-0 node's ancestor at level l is node (l, j >> l), whose draw slot the table holds; off
+    for flat plans, random compressors (permutation calls) and single-level plans."""
+    plan = _plan.levels_plan(64 * 37, 64, "sorted_pair")
+    _, desc = _plan.draws_for(plan, (0,), 8, "sorted_pair")
+    a, level_of, anc = _plan.ancestor_table(plan, desc)
+    assert len(plan.batches) - 1 == 5 and a == 4 and anc.shape == (plan.n_nodes, a)
+    first = [int(b[0]) for b in plan.batches]
+    for j in range(len(plan.batches[0])):
+        for l in range(1, a + 1):
+            if (j >> l) < len(plan.batches[l]):
+                assert anc[first[0] + j, l - 1] == desc[first[l] + (j >> l), 6]
+            else:
+                assert anc[first[0] + j, l - 1] == -1
+    assert (anc[first[1]:] == -1).all() and list(level_of[first[2]: first[2] + 2]) == [2, 2]
+    for p2, comp in ((_plan.flat_plan(5000, 64, "sorted_pair"), "sorted_pair"),
+                     (_plan.levels_plan(5000, 64, "random"), "random"),
+                     (_plan.levels_plan(100, 64, "sorted_pair"), "sorted_pair")):
+        _, dsc = _plan.draws_for(p2, (0,), 8, comp)
+        assert _plan.ancestor_table(p2, dsc)[0] == 0
