@@ -625,11 +625,15 @@ def run_decode(args) -> int:
           flush=True)
     t0 = time.perf_counter()
     chunk = 4096
+    ext_timer = _engine.KernelTimer(only=("moment_accumulate",))  # the state accumulation of each chunk
+    st._st.timer = ext_timer
     for lo in range(0, w["prefix"], chunk):
         n = min(chunk, w["prefix"] - lo)
         st.extend(draw(s_total, n, d), draw(s_total, n, dv))
     torch.cuda.synchronize()
+    st._st.timer = None
     t_prefix = time.perf_counter() - t0
+    ext_ms = [s_.elapsed_time(e_) for s_, e_ in ext_timer.events.get("moment_accumulate", [])]
     total = args.warmup + args.steps
     xs = draw(total + args.steps, 3, s_total, d)  # warm-up, timed steps, breakdown steps
     t0 = time.perf_counter()
@@ -698,6 +702,9 @@ def run_decode(args) -> int:
         "block_completions_breakdown": ((w["prefix"] + total + args.steps) // w["block"]
                                         - (w["prefix"] + total) // w["block"]),
         "host_prefix_build_s": round(t_prefix, 3),
+        "extend_accumulate_ms": [round(x, 3) for x in ext_ms],
+        "extend_accumulate_note": (f"state accumulation of each extend() chunk of up to {chunk} tokens of every "
+                                   "stream while the prefix is built (HIP events)"),
         "host_draws_s": round(t_draws, 3),
         "wall_s_timed_region": round(wall, 4),
     }

@@ -191,6 +191,21 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
                           void* stream);
 
 /*
+ * sta_moment_accumulate on the wave-specialised kernel's update-only pass (split-bf16 products, degree
+ * <= 3, d <= 128): 4 update waves per workgroup keep the state of 4 slots of slot_tiles feature tiles x
+ * 16 column_tiles columns in matrix-core accumulators, loaded from and stored back to the persistent
+ * state through feat_rows; the other 4 waves stage the chunks.  Tables in the layout of sta_moments_ws
+ * ([fsplit][4 slots][slot_tiles][...], mixed: slots 2 and 3 one tile less) with the per-feature key-side
+ * coefficients; ldv and the state's row stride 32 ceil(dv / 32) multiples of 16 column_tiles.  Same
+ * reference function as sta_moment_accumulate (TaylorMomentSketch.update,
+ * streaming_taylor_coreset_attention.py:265-280).
+ */
+int sta_moment_accumulate_ws(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
+                             int ld_k, int dv, int ldv, int degree, int fsplit, int slot_tiles, int mixed,
+                             int column_tiles, const uint32_t* feat_quads, const float* feat_coef,
+                             const int32_t* feat_rows, int n_feat, float* state_num, float* state_den, void* stream);
+
+/*
  * Streaming decode (K5) for S streams in lockstep: ArticleStreamingAttention.update / query
  * (streaming_taylor_coreset_attention.py:576-609).  The state of stream s (fp32, caller-owned):
  *   moments of the tokens of completed blocks   state_num [S][F][ldv], state_den [S][F] (reference order)

@@ -24,6 +24,7 @@ cascade), then the query.
 
 from __future__ import annotations
 
+import os
 from collections import deque
 from dataclasses import dataclass
 from typing import Deque, Dict, List, Optional, Tuple
@@ -49,6 +50,10 @@ class _CompletionDraws:
 
 
 ACCUMULATE_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
+# block completions and extend() on the wave-specialised kernel's update-only pass where it applies
+# (split products, degree <= 3, d <= 128); STA_ACCUMULATE_WS=0 keeps the chunked accumulation kernel
+ACCUMULATE_WS = os.environ.get("STA_ACCUMULATE_WS", "1") != "0"
+ACCUMULATE_WS_MIN_ROWS = 512
 
 
 class StaticScratchOwners:
@@ -186,6 +191,27 @@ class DecodeState:
             )
         return self._acc_tables[width]
 
+    def _acc_table_ws(self, width: int):
+        """Tables of the wave-specialised accumulation (sta_moment_accumulate_ws) for rows `width` elements
+        long, or None where it does not apply (fp32 products, degree >= 4, keys wider than the staged
+        128 dimensions): (split, column tiles, quads, coef, rows)."""
+        key = ("ws", width)
+        if key not in self._acc_tables:
+            entry = None
+            ct = 4 if (-(-self.dv // 32)) % 2 == 0 else 2
+            if (ACCUMULATE_WS and self.products == _native.PRODUCTS_SPLIT_BF16 and self.degree <= 3
+                    and width <= _engine.STAGED_D):
+                opts = _native.moment_ws_slot_tiles(width, self.degree, ct, self.dv)
+                if opts:
+                    ft = _plan.feature_tiles(width, self.degree)
+                    ms = _plan.moment_split_ws(ft, self.S, self.dv, opts, ct)
+                    rows = _plan.split_state_rows(ft, ms, self.d)
+                    dev = self.device
+                    entry = (ms, ct, torch.from_numpy(ms.quads.view(np.int32)).to(dev),
+                             torch.from_numpy(ms.coef).to(dev), torch.from_numpy(rows).to(dev))
+            self._acc_tables[key] = entry
+        return self._acc_tables[key]
+
     def _accumulate(self, k: torch.Tensor, v: torch.Tensor, n: int, head_rows: int, state_num: torch.Tensor,
                     state_den: torch.Tensor, row_off: int = 0) -> None:
         """state += moments of rows [row_off, row_off + n) of k [S, head_rows, width] / v [S, head_rows, ldv]
@@ -194,9 +220,25 @@ class DecodeState:
             return
         width = k.shape[-1]
         assert k.is_contiguous() and v.is_contiguous() and k.shape[1] == head_rows == v.shape[1]
-        ms, quads, coef, rows, win, staged = self._acc_table(width)
         kp = k.data_ptr() + row_off * width * k.element_size()
         vp = v.data_ptr() + row_off * v.shape[-1] * v.element_size()
+        # the wave-specialised pass pays for its state load / store and pipeline fill over long runs of
+        # rows (extend); a block completion's rows go to the chunked kernel (c5: 256 rows of 2048 streams
+        # 1.8 against 2.6 ms; 4096 rows 23.2 against 10.0 ms)
+        ws = self._acc_table_ws(width) if n >= ACCUMULATE_WS_MIN_ROWS else None
+        if ws is not None:
+            ms, ct, quads, coef, rows = ws
+
+            def run_ws():
+                st = self.lib.sta_moment_accumulate_ws(
+                    kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, width, width, self.dv, v.shape[-1],
+                    self.degree, ms.fsplit, ms.wave_tiles, int(ms.mixed), ct, quads.data_ptr(), coef.data_ptr(),
+                    rows.data_ptr(), self.F, state_num.data_ptr(), state_den.data_ptr(), self._stream())
+                _native.check(st, "sta_moment_accumulate_ws")
+
+            self._launch("moment_accumulate", run_ws)
+            return
+        ms, quads, coef, rows, win, staged = self._acc_table(width)
 
         def run():
             st = self.lib.sta_moment_accumulate(

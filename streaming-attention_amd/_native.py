@@ -86,6 +86,11 @@ _SIGNATURES = {
     "sta_flash_attention": (
         _i32, [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _c_p, _i32, _c_p],
     ),
+    "sta_moment_accumulate_ws": (
+        _i32,
+        [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,  # ... fs nts mixed ct
+         _c_p, _c_p, _c_p, _i32, _c_p, _c_p, _c_p],  # quads coef rows n_feat num den stream
+    ),
     "sta_moment_accumulate": (
         _i32,
         [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,  # k v dt bh n rows d ld dv ldv deg fs nt

@@ -386,6 +386,48 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
                              products == STA_PRODUCTS_SPLIT_BF16);
 }
 
+int sta_moment_accumulate_ws(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
+                             int ld_k, int dv, int ldv, int degree, int fsplit, int slot_tiles, int mixed,
+                             int column_tiles, const uint32_t* feat_quads, const float* feat_coef,
+                             const int32_t* feat_rows, int n_feat, float* state_num, float* state_den, void* stream) {
+  if (!k || !v || !feat_quads || !feat_coef || !feat_rows || !state_num || !state_den) return STA_ERR_ARG;
+  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  if (bh <= 0 || n < 0 || head_rows < n || d <= 0 || dv <= 0 || fsplit <= 0 || slot_tiles <= 0 || n_feat <= 0)
+    return STA_ERR_SHAPE;
+  if (!sta_moments_ws_ok(d, degree, slot_tiles, column_tiles, dv)) return STA_ERR_UNSUPPORTED;
+  if (mixed != 0 && (mixed != 1 || slot_tiles < 2)) return STA_ERR_ARG;
+  const int esize = dtype == STA_F32 ? 4 : 2;
+  const int ldo = 32 * ((dv + 31) / 32);  // the state's row stride
+  if ((d * esize) % 16 != 0 || ld_k < d || (ld_k * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0 ||
+      ldv % (16 * column_tiles) != 0 || ldo % (16 * column_tiles) != 0)
+    return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0) return STA_ERR_ARG;
+  if (head_rows * static_cast<int64_t>(ldv > ld_k ? ldv : ld_k) * esize >= (int64_t(1) << 32) ||
+      n >= (int64_t(1) << 30))
+    return STA_ERR_UNSUPPORTED;
+  if (n == 0) return STA_OK;
+  sta::WsArgs w;
+  sta::MomArgs& a = w.m;
+  a.q = k; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = 1.0f; a.shift = 0;
+  a.fsplit = fsplit; a.mixed = mixed; a.csplit = (dv + 16 * column_tiles - 1) / (16 * column_tiles);
+  a.quads = feat_quads; a.fcoef = feat_coef; a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv;
+  a.esize = esize; a.ldo = ldo; a.ldk = ld_k; a.win = nullptr;
+  a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den;
+  a.n_feat = n_feat;
+  w.cpb = 2;  // no query blocks in the update-only pass
+  w.mixed = mixed;
+  w.hand = nullptr;
+  w.nseg = 1;
+  w.seg_chunks = static_cast<int>((n + sta::MOM_C - 1) / sta::MOM_C);
+  w.phase = 3;
+  w.seg_state = nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nx = moment_extra_factors(degree);
+  if (column_tiles == 4)
+    return esize == 4 ? dispatch_moments_ws<4, 4>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 4>(w, bh, s, slot_tiles, nx);
+  return esize == 4 ? dispatch_moments_ws<4, 2>(w, bh, s, slot_tiles, nx) : dispatch_moments_ws<2, 2>(w, bh, s, slot_tiles, nx);
+}
+
 int sta_decode_layout(int d, int dv, int* dk, int* ldv) {
   if (d <= 0 || dv <= 0 || !dk || !ldv) return STA_ERR_ARG;
   if (d > kMaxD || dv > kMaxDv) return STA_ERR_UNSUPPORTED;

@@ -14,10 +14,12 @@ namespace {
 template <int NTS, int NX, bool DBIG, int ES, int CT>
 int launch_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::ws_smem_floats(DBIG, 16 * CT, NTS)) * sizeof(float);
-  // phase 1 of a segmented scan (segment totals) is its own instantiation: no query work at all; bf16
-  // values (exact in bf16) take the instantiation without the products of their zero lo plane
+  // phase 1 of a segmented scan (segment totals) and phase 3 (accumulation into a persistent state) are
+  // the update-only instantiation: no query work at all; bf16 values (exact in bf16) take the
+  // instantiation without the products of their zero lo plane
   const bool vx = ES == 2 && a.m.dtype == sta::BF16;
-  auto fn = a.phase == 1 ? (vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true, ES == 2>
+  const bool tot = a.phase == 1 || a.phase == 3;
+  auto fn = tot ? (vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true, ES == 2>
                                : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true, false>)
                          : (vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, false, ES == 2>
                                : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, false, false>);

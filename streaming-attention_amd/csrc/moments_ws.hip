@@ -322,7 +322,9 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
 // the 32 tokens (the token mapping of mom_update_split).  The next tile's key reads are issued as soon
 // as the current tile's feature values are formed (into the same registers), so they land while the
 // current tile's operands are split and its products issue.
-template <int NT, int CT, int NX, bool VX>
+// KC: the key-side coefficient also at NX = 0 (a persistent state in the reference's feature order; the
+// scan applies the tile coefficients on the query side instead)
+template <int NT, int CT, int NX, bool VX, bool KC = false>
 __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[NT], const float* Kt,
                                           const __bf16* vplane, const MomLane<NT, NX>& m, int li, int lg) {
   constexpr int CG = 16 * CT;
@@ -357,7 +359,7 @@ __device__ __forceinline__ void ws_update(floatx4 (&st)[NT][CT], float (&den_p)[
       float y = fa[b][j >> 2][j & 3] * fb[b][j >> 2][j & 3];
       if (NX >= 1) y *= fc[b][j >> 2][j & 3];
       if (NX >= 2) y *= fe[b][j >> 2][j & 3];
-      if (NX >= 1) y *= m.kcoef[kt];  // NX = 0: the tile coefficient is applied by the query waves
+      if (NX >= 1 || KC) y *= m.kcoef[kt];  // NX = 0: the tile coefficient is applied by the query waves
       x[j] = y;
       dacc += y;
     }
@@ -602,9 +604,13 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
                             : nullptr;
   float* const sden = sstate ? sstate + 4 * NTS * CT * 256 : nullptr;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
-  const char* qh = static_cast<const char*>(a.q) + bh * a.n * a.ldk * ES;
-  const char* kh = static_cast<const char*>(a.k) + bh * a.n * a.ldk * ES;
-  const char* vh = static_cast<const char*>(a.v) + bh * a.n * a.ldv * ES;
+  // phase 3 (update only, TOT): accumulate into a persistent state in the reference's feature order
+  // (a decode state), rows [0, n) of every head at head_rows rows apart
+  const bool persist = TOT && wa.phase == 3;
+  const int64_t hstride = persist ? a.head_rows : a.n;
+  const char* qh = static_cast<const char*>(a.q) + bh * hstride * a.ldk * ES;
+  const char* kh = static_cast<const char*>(a.k) + bh * hstride * a.ldk * ES;
+  const char* vh = static_cast<const char*>(a.v) + bh * hstride * a.ldv * ES;
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
   const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0, TOT ? tid - 256 : tid);
@@ -643,6 +649,26 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   for (int e = tid; e < 2 * (KVF + QF); e += WS_THREADS) smem[e] = 0.f;
   for (int e = tid; e < ws_den_floats(NTS); e += WS_THREADS) denb[e] = 0.f;
   __syncthreads();
+  if constexpr (UPD && TOT) {
+    if (persist) {
+      // phase 3: the accumulators start at the persistent state (rowmap: the state row of every feature
+      // slot, -1 for padding); its denominators ride in lane group 0's partials
+      const float* snum = a.state_num + bh * a.n_feat * a.ldo;
+      const float* sdn = a.state_den + bh * a.n_feat;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+            st[kt][ct][r] = row >= 0 ? snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] : 0.f;
+        }
+        const int row = a.rowmap[(tile0 + kt) * 16 + li];
+        den_p[kt] = (lg == 0 && row >= 0) ? sdn[row] : 0.f;
+      }
+    }
+  }
   if constexpr (UPD) {
     if (from_init) {
       // phase 2: the accumulators start at S_init; its denominators ride in lane group 0's partials
@@ -781,7 +807,11 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     if constexpr (UPD) {
       if (c < nch) {
         const float* Kt = kvb + (c & 1) * KVF;
-        ws_update<NT, CT, NX, VX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li,
+        if (TOT && persist)
+          ws_update<NT, CT, NX, VX, TOT>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT),
+                                         m, li, lg);
+        else
+          ws_update<NT, CT, NX, VX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li,
                                   lg);
         if (!totals && (c + 1) % cpb == 0 && c + 1 < nch) {
           // the state the queries of block (c + 1) / cpb see -> handoff (parity of that block)
@@ -875,7 +905,28 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   // partials of the last chunk (written by the query waves in iteration nch)
   if constexpr (UPD) {
     if (!totals) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
-    if (totals) {
+    if (totals && persist) {
+      // phase 3: the slice back into the persistent state (each (head, feature, column) belongs to one
+      // lane of the grid); the denominators from column group 0
+      float* snum = a.state_num + bh * a.n_feat * a.ldo;
+      float* sdn = a.state_den + bh * a.n_feat;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+          if (row >= 0) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] = st[kt][ct][r];
+          }
+        }
+        float t = den_p[kt];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        const int row = a.rowmap[(tile0 + kt) * 16 + li];
+        if (lg == 0 && cs == 0 && row >= 0) sdn[row] = t;
+      }
+    } else if (totals) {
       // phase 1: the segment's total (its keys only) for the scan over segments
       floatx4* ss = reinterpret_cast<floatx4*>(sstate) + (slot * NTS) * CT * 64 + lane;
 #pragma unroll

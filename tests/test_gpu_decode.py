@@ -246,6 +246,49 @@ def test_sketch_moments_closed_form(monkeypatch, products):
     assert rel(num, phi.T @ v.double()) < (1e-6 if products == _native.PRODUCTS_FP32 else MOM_TOL)
 
 
+@pytest.mark.parametrize("S,n,head_rows,d,dv,degree,dtype", [
+    (3, 300, 320, 16, 24, 2, torch.float32), (2, 257, 257, 64, 64, 2, torch.float32),
+    (2, 200, 256, 128, 100, 2, torch.float32), (2, 190, 192, 16, 64, 3, torch.float32),
+    (2, 300, 300, 64, 64, 2, torch.bfloat16), (1, 70, 80, 8, 8, 0, torch.float32),
+    (1, 90, 96, 12, 40, 1, torch.float32)])
+def test_accumulate_ws_matches_chunked_and_closed_form(monkeypatch, S, n, head_rows, d, dv, degree, dtype):
+    """The state accumulation on the wave-specialised update-only pass (sta_moment_accumulate_ws) and on
+    the chunked kernel, from the same nonzero state: both equal the fp64 closed form
+    state0 + sum_j phi_k(k_j) [v_j, 1] in the reference's feature order (split-bf16 products)."""
+    print(f"accumulate ws S={S} n={n} rows={head_rows} d={d} dv={dv} degree={degree} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(n + d)
+    states = {}
+    monkeypatch.setattr(_decode, "ACCUMULATE_WS_MIN_ROWS", 1)
+    for ws in (True, False):
+        monkeypatch.setattr(_decode, "ACCUMULATE_WS", ws)
+        st = _decode.DecodeState(S, d, dv, degree=degree, block=64, scale=1.0, compressor="sorted_pair", seed=0,
+                                 device=DEV)
+        if ws:
+            assert st._acc_table_ws(st.dk) is not None
+            k = torch.zeros(S, head_rows, st.dk)
+            k[:, :, :d] = torch.randn(S, head_rows, d, generator=g) * 0.4
+            v = torch.zeros(S, head_rows, st.ldv)
+            v[:, :, :dv] = torch.randn(S, head_rows, dv, generator=g)
+            k, v = k.to(dtype), v.to(dtype)
+            num0 = torch.randn(S, st.F, st.ldv, generator=g)
+            num0[..., dv:] = 0
+            den0 = torch.randn(S, st.F, generator=g)
+        st.state_num.copy_(num0.to(DEV))
+        st.state_den.copy_(den0.to(DEV))
+        st._accumulate(k.to(DEV).contiguous(), v.to(DEV).contiguous(), n, head_rows, st.state_num, st.state_den)
+        torch.cuda.synchronize()
+        states[ws] = (st.state_num.cpu().double(), st.state_den.cpu().double())
+    for s in range(S):
+        phi = orc.features(k[s, :n, :d].double(), degree, key_side=True)
+        want_num = num0[s].double()[:, :dv] + phi.T @ v[s, :n, :dv].double()
+        want_den = den0[s].double() + phi.sum(0)
+        for ws in (True, False):
+            num, den = states[ws]
+            assert rel(num[s][:, :dv], want_num) < MOM_TOL, (ws, s)
+            assert rel(den[s], want_den) < 1e-6, (ws, s)
+            assert torch.all(num[s][:, dv:] == 0)
+
+
 def test_query_stats_split():
     """return_stats: denominator = low + tail, with the reference's split: low over every token (the
     sketch holds the buffered tokens too), tail over items() = buffer (weight 1) + levels."""
