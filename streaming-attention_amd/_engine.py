@@ -38,6 +38,10 @@ ANCESTOR_SCORES = os.environ.get("STA_ANCESTOR_SCORES", "1") != "0"
 # levels scored that way (at most 4): each costs the level-0 calls one more fp64 chain per row, and pays
 # where a level's gathers are large
 ANCESTOR_LEVELS = int(os.environ.get("STA_ANCESTOR_LEVELS", "3"))
+# only for key rows of at least this many bytes: a short row's gather costs the merges little, and the
+# extra chains cost the level-0 calls more (1x32x65536, d = 64 fp32: 0.393 -> 0.375 ms; 4x32x16384,
+# d = 16: 0.26 -> 0.30 ms)
+ANCESTOR_MIN_ROW_BYTES = 256
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 
@@ -368,7 +372,7 @@ def prefill(
         # levels: the level-0 calls also score their rows for their ancestors' calls, which then read
         # one score per item instead of gathering key rows (float64 scoring keeps the gathers)
         anc_levels, anc_d, level_d = 0, None, None
-        if ANCESTOR_SCORES and not f64:
+        if ANCESTOR_SCORES and not f64 and d * k3.element_size() >= ANCESTOR_MIN_ROW_BYTES:
             anc_levels, level_of, anc = _plan.ancestor_table(plan, desc, ANCESTOR_LEVELS)
             if anc_levels:
                 anc_d, level_d = _on_device(("anc", anc_levels) + pkey, dev,

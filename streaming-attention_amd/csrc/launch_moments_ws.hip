@@ -1,6 +1,8 @@
 // Launches of the wave-specialised prefill moment scan (moments_ws_kernel, split-bf16 products).  The
 // build compiles this unit once per element size and column-tile count (-DSTA_WS_ES=4|2,
 // -DSTA_WS_CT=4|2); each object holds the configurations of STA_MOMENT_WS_CONFIGS.
+#include <type_traits>
+
 #include "api_common.hpp"
 #include "moments_ws.hip"
 
@@ -14,15 +16,16 @@ namespace {
 template <int NTS, int NX, bool DBIG, int ES, int CT>
 int launch_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s) {
   const size_t smem = static_cast<size_t>(sta::ws_smem_floats(DBIG, 16 * CT, NTS)) * sizeof(float);
-  // phase 1 of a segmented scan (segment totals) and phase 3 (accumulation into a persistent state) are
-  // the update-only instantiation: no query work at all; bf16 values (exact in bf16) take the
-  // instantiation without the products of their zero lo plane
+  // phase 1 of a segmented scan (segment totals, TOT 1) and phase 3 (accumulation into a persistent
+  // state, TOT 2) are update-only instantiations: no query work at all; bf16 values (exact in bf16) take
+  // the instantiation without the products of their zero lo plane
   const bool vx = ES == 2 && a.m.dtype == sta::BF16;
-  const bool tot = a.phase == 1 || a.phase == 3;
-  auto fn = tot ? (vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true, ES == 2>
-                               : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, true, false>)
-                         : (vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, false, ES == 2>
-                               : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, false, false>);
+  auto pick = [&](auto tot) {
+    constexpr int T = decltype(tot)::value;
+    return vx ? sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, T, ES == 2> : sta::moments_ws_kernel<NTS, NX, DBIG, ES, CT, T, false>;
+  };
+  auto fn = a.phase == 1 ? pick(std::integral_constant<int, 1>{})
+                         : a.phase == 3 ? pick(std::integral_constant<int, 2>{}) : pick(std::integral_constant<int, 0>{});
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
   if (e != hipSuccess) return hip_status(e);

@@ -559,7 +559,7 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, c
 // the lane holds for tile 2 p (.xy) and tile 2 p + 1 (.zw); an odd last tile fills .xy only.  The
 // update wave writes its uint2 halves, the query wave loads whole operands.  The running denominators
 // go to LDS (den_lds[parity][slot][tile * 16 + feature]).
-template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT, bool TOT, bool VX>
+template <bool UPD, int NT, int NTS, int NX, bool DBIG, int ES, int CT, int TOT, bool VX>
 __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, int fs, int cs, int seg, int slot,
                                         int qw) {
   const MomArgs& a = wa.m;
@@ -569,7 +569,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   constexpr int QF = ws_q_floats(DBIG);
   constexpr int REDF = ws_red_floats(CG);
   // staging threads: in a segment-totals pass the query waves (indices tid - 256), else ws_stagers
-  constexpr int STG = TOT ? 256 : ws_stagers(NX, DBIG);
+  constexpr int STG = TOT != 0 ? 256 : ws_stagers(NX, DBIG);
   constexpr int NPS = (NTS + 1) / 2;  // operand pairs per slot in the handoff
   constexpr int NP = NT / 2;          // full tile pairs of this wave
   constexpr bool ODD = (NT & 1) != 0;
@@ -595,7 +595,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   // it and first use it one iteration later; with cpb >= 3 the next write comes after that iteration's
   // barrier, so one copy serves (half the footprint in L2), with cpb = 2 two alternate by block parity
   const int hmask = cpb >= 3 ? 0 : 1;
-  constexpr bool totals = TOT;            // phase 1: update only, write the segment's total
+  constexpr bool totals = TOT != 0;       // phases 1 and 3: update only (TOT 1 and 2)
   const bool from_init = wa.phase == 2;   // start from the state before the segment
   // segment state of this (head, feature split, column group, segment): [4][NTS][CT][64] floatx4, den
   float* const sstate = wa.nseg > 1
@@ -604,16 +604,17 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
                             : nullptr;
   float* const sden = sstate ? sstate + 4 * NTS * CT * 256 : nullptr;
   const int64_t obase = (bh * a.fsplit + fs) * (a.n + 2 * MOM_GUARD) + MOM_GUARD;
-  // phase 3 (update only, TOT): accumulate into a persistent state in the reference's feature order
-  // (a decode state), rows [0, n) of every head at head_rows rows apart
-  const bool persist = TOT && wa.phase == 3;
+  // TOT = 2 (phase 3, update only): accumulate into a persistent state in the reference's feature order
+  // (a decode state), rows [0, n) of every head at head_rows rows apart; its own instantiation, so the
+  // segment-totals pass (TOT = 1) keeps its registers
+  constexpr bool persist = TOT == 2;
   const int64_t hstride = persist ? a.head_rows : a.n;
   const char* qh = static_cast<const char*>(a.q) + bh * hstride * a.ldk * ES;
   const char* kh = static_cast<const char*>(a.k) + bh * hstride * a.ldk * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * hstride * a.ldv * ES;
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
-  const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0, TOT ? tid - 256 : tid);
+  const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0, TOT != 0 ? tid - 256 : tid);
   // operand (pair p, column tile ct, hi / lo) of this slot and block parity par
   auto hand_at = [&](int par, int p, int ct, int hl) -> uint4* {
     return wa.hand + ((((static_cast<int64_t>(wg) * 2 + par) * 4 + slot) * NPS + p) * CT + ct) * 128 + hl * 64 + lane;
@@ -649,8 +650,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   for (int e = tid; e < 2 * (KVF + QF); e += WS_THREADS) smem[e] = 0.f;
   for (int e = tid; e < ws_den_floats(NTS); e += WS_THREADS) denb[e] = 0.f;
   __syncthreads();
-  if constexpr (UPD && TOT) {
-    if (persist) {
+  if constexpr (UPD && persist) {
+    {
       // phase 3: the accumulators start at the persistent state (rowmap: the state row of every feature
       // slot, -1 for padding); its denominators ride in lane group 0's partials
       const float* snum = a.state_num + bh * a.n_feat * a.ldo;
@@ -717,7 +718,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   // sets with register copies at the loop latch, which wait for every load in flight: 6.42 against
   // 6.0 ms on c3.)
   // this wave stages chunks: in a segment-totals pass the query waves (the update waves only update)
-  constexpr bool STAGE = TOT ? !UPD : (UPD || STG == WS_THREADS);
+  constexpr bool STAGE = TOT != 0 ? !UPD : (UPD || STG == WS_THREADS);
   WsStage<DBIG, ES, CG, STG> pre;
   if constexpr (STAGE) {
     ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first);
@@ -727,10 +728,10 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   __syncthreads();
   if constexpr (STAGE) {
     ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
-    if constexpr (!TOT) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
+    if constexpr (TOT == 0) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
   }
 
-  if constexpr (!UPD && TOT) {
+  if constexpr (!UPD && TOT != 0) {
     // segment totals: the query waves stage the keys and values, with the same iterations and barriers
     for (int c = 0; c <= nch; ++c) {
       ws_stage_step<DBIG, ES, CG, STG, false, VX>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
@@ -807,9 +808,9 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     if constexpr (UPD) {
       if (c < nch) {
         const float* Kt = kvb + (c & 1) * KVF;
-        if (TOT && persist)
-          ws_update<NT, CT, NX, VX, TOT>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT),
-                                         m, li, lg);
+        if constexpr (persist)
+          ws_update<NT, CT, NX, VX, true>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT),
+                                          m, li, lg);
         else
           ws_update<NT, CT, NX, VX>(st, den_p, Kt, reinterpret_cast<const __bf16*>(Kt + mom_krows(DBIG) * MOM_LDT), m, li,
                                   lg);
@@ -946,7 +947,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
 // workgroups share one L2 for its q / k / v rows.  Waves 0-3 update, 4-7 query.
 // VX: bf16 values (ES = 2, dtype BF16), exact in bf16: the update leaves out the product with their zero
 // lo plane (the state is that of the three-product form, bit for bit)
-template <int NTS, int NX, bool DBIG, int ES, int CT, bool TOT, bool VX>
+template <int NTS, int NX, bool DBIG, int ES, int CT, int TOT, bool VX>
 __global__ __launch_bounds__(WS_THREADS, 1) void moments_ws_kernel(const WsArgs wa) {
   const MomArgs& a = wa.m;
   const int wg = xcd_remap(blockIdx.x, gridDim.x);

@@ -383,6 +383,7 @@ def test_ancestor_scores_keep_every_node(n, d, block, dtype, comp, monkeypatch):
     q, k, v = orc.make_data((2,), n, d, 8, radius=1.0, data="unit_ball", seed=n + d)
     q, k, v = (x.to(dtype) for x in (q, k, v))
     res = {}
+    monkeypatch.setattr(_engine, "ANCESTOR_MIN_ROW_BYTES", 0)
     for on in (True, False):
         monkeypatch.setattr(_engine, "ANCESTOR_SCORES", on)
         r = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block=block, scale=0.5, semantics="levels",
