@@ -313,6 +313,28 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
                        float* level_scores, void* stream);
 
 /*
+ * Merge nodes of several levels of a levels plan in one launch (K3): the compress calls of
+ * MergeReduceCoreset._insert_level's cascade (streaming_taylor_coreset_attention.py:396-411, each call
+ * :413-467), the same node values as sta_compress_nodes run level by level.  Each node is computed by
+ * one wave; a workgroup of `waves` waves (1, 2, 4, 8 or 16) runs `phases` rounds with a barrier after
+ * each, so a round may read the nodes of the rounds before it:
+ *   node_table [n_groups][phases][waves]: the node each wave computes in each round (-1: none), the
+ *     same for every head (grid n_groups x bh).  A node's children must be nodes of an earlier launch or
+ *     of an earlier round of the same workgroup (e.g. a subtree: 2^(phases-1) nodes of one level, then
+ *     their parents, ..., its root);
+ *   node_level, anc_levels, level_scores: as sta_compress_nodes' later launches (merges at levels 1 ..
+ *     anc_levels read the scores their level-0 calls wrote).
+ * Other arguments as sta_compress_nodes.  LDS: the call's arrays for every wave, waves * (4 M + 256)
+ * floats with M = max_in rounded up to 4 (float64: waves * (5 M + 512)); STA_ERR_UNSUPPORTED above
+ * 160 KiB.
+ */
+int sta_compress_merges(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* node_table,
+                        int n_groups, int phases, int waves, const int32_t* node_desc, int n_nodes, int cap,
+                        const void* dirs, const void* unif, const int32_t* perms, int n_draws, int max_in,
+                        int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
+                        float* level_scores, void* stream);
+
+/*
  * Segment-mean representatives of completed blocks (the Triton path's coreset).
  * Replaces build_segment_mean_coreset (triton_article_attention.py:189-245).
  *   n_rep = ((N-1)//block) * (block/stride); outputs rep_k [BH][n_rep][D], rep_v [BH][n_rep][Dv] fp32.

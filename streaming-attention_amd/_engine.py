@@ -42,6 +42,13 @@ ANCESTOR_LEVELS = int(os.environ.get("STA_ANCESTOR_LEVELS", "3"))
 # extra chains cost the level-0 calls more (1x32x65536, d = 64 fp32: 0.393 -> 0.375 ms; 4x32x16384,
 # d = 16: 0.26 -> 0.30 ms)
 ANCESTOR_MIN_ROW_BYTES = 256
+# Levels plans, STA_MERGE_WAVES=W > 0: the merge levels as subtrees of up to W nodes per workgroup, one
+# wave per node (sta_compress_merges: log2(W) + 1 levels per launch; W = 16 puts 32 x 65536 tokens'
+# 8 merge levels in 2 launches) instead of one launch per level; the nodes are the same bit for bit.
+# Off by default: a node's rank sort on one wave is 4x longer, and the top levels have one node per
+# head (32 x 65536 tokens: 3 launches in 0.45 ms against 9 in 0.375 ms; 4 x 32 x 16384: 3 in 0.248 ms
+# against 8 in 0.253 ms).
+MERGE_WAVES = int(os.environ.get("STA_MERGE_WAVES", "0"))
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 
@@ -377,6 +384,14 @@ def prefill(
             if anc_levels:
                 anc_d, level_d = _on_device(("anc", anc_levels) + pkey, dev,
                                             lambda: (_i32(anc, dev), _i32(level_of, dev)))
+        merge_l = []
+        if MERGE_WAVES > 0 and plan.mode == _plan.MODE_LEVELS:
+            def build_merges():
+                launches = _plan.merge_launches(plan, dr.max_in, f64, MERGE_WAVES)
+                _plan.check_merge_launches(plan, desc, launches)
+                return [(ln, _i32(ln.table, dev)) for ln in launches]
+
+            merge_l = _on_device(("merges", MERGE_WAVES, dr.max_in, f64) + pkey, dev, build_merges)
 
     lrows, lld, _ = _native.moment_partials_layout(n, dv)
     low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
@@ -455,7 +470,8 @@ def prefill(
                 lscore.record_stream(side)
         with torch.cuda.stream(side):
             k3_stream = _native.stream_handle(dev)
-            for bi, bd in enumerate(batches_d):
+            # with merge launches: the level-0 batch alone, then the subtrees
+            for bi, bd in enumerate(batches_d[:1] if merge_l else batches_d):
                 def k3_launch(bd=bd, first=bi == 0):
                     st = lib.sta_compress_nodes(
                         (score_keys if f64 else k3).data_ptr(), _native.STA_F64 if f64 else dt, bh, n, d,
@@ -467,6 +483,17 @@ def prefill(
                     _native.check(st, "sta_compress_nodes")
 
                 _run(timer, "compress", k3_launch)
+            for ln, table_d in merge_l:
+                def k3_merges(ln=ln, table_d=table_d):
+                    st = lib.sta_compress_merges(
+                        (score_keys if f64 else k3).data_ptr(), _native.STA_F64 if f64 else dt, bh, n, d,
+                        table_d.data_ptr(), ln.groups, ln.phases, ln.waves, desc_d.data_ptr(),
+                        plan.n_nodes, plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(),
+                        dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(),
+                        _native.ptr(level_d), anc_levels, _native.ptr(lscore), k3_stream)
+                    _native.check(st, "sta_compress_merges")
+
+                _run(timer, "compress", k3_merges)
         if side is not main:
             main.wait_stream(side)
 

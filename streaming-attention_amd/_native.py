@@ -71,6 +71,11 @@ _SIGNATURES = {
         [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32, _c_p, _c_p,
          _c_p, _c_p, _i32, _c_p, _c_p],  # ... node_src node_w node_level anc anc_levels level_scores stream
     ),
+    "sta_compress_merges": (
+        _i32,
+        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32,
+         _c_p, _c_p, _c_p, _i32, _c_p, _c_p],  # ... node_src node_w node_level anc_levels level_scores stream
+    ),
     "sta_segment_mean": (_i32, [_c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _c_p, _c_p, _c_p]),
     "sta_block_attention": (
         _i32,

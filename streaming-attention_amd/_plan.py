@@ -1093,7 +1093,7 @@ def levels_plan(n: int, block: int, compressor: str) -> NodePlan:
     return _cached(("levels", n, block, compressor), build)
 
 
-CMP_MAX_ANC = 4  # ancestor levels a level-0 compress call can score (sta_compress_nodes)
+CMP_MAX_ANC = 4  # ancestor levels a level-0 compress call can score (sta_compress_nodes / _leaves)
 
 
 def ancestor_table(plan: NodePlan, desc: np.ndarray,
@@ -1119,6 +1119,87 @@ def ancestor_table(plan: NodePlan, desc: np.ndarray,
         slot = np.where(ok & (desc[node, 5] == METHOD_SORTED_PAIR), desc[node, 6], -1)
         anc[first[0]: first[0] + counts[0], l - 1] = slot
     return a_lev, plan.level_of.astype(np.int32), anc
+
+
+CMP_MAX_D = 256  # key width of the compressor's direction buffer (csrc/compress.hip)
+
+
+def compress_region_floats(max_in: int, f64: bool) -> int:
+    """LDS floats of one compress call's arrays (cmp_smem_floats without ancestor directions)."""
+    m = (max_in + 3) & ~3
+    return (2 if f64 else 1) * m + 3 * m + (2 if f64 else 1) * CMP_MAX_D
+
+
+@dataclass
+class MergeLaunch:
+    """One sta_compress_merges launch: table int32 [groups, phases, waves] of node ids (-1: idle)."""
+    table: np.ndarray
+    waves: int
+    phases: int
+    levels: Tuple[int, int]  # first and last tree level it computes
+
+    @property
+    def groups(self) -> int:
+        return int(self.table.shape[0])
+
+
+def merge_launches(plan: NodePlan, max_in: int, f64: bool, max_waves: int = 16,
+                   lds_bytes: int = 160 * 1024) -> List[MergeLaunch]:
+    """The merge levels of a levels plan as sta_compress_merges launches of subtrees: a launch starting at
+    level l0 gives each workgroup W = 2^k waves (at most max_waves, within lds_bytes of LDS) and the W
+    consecutive nodes (l0, j) of its group, then in round r the W >> r nodes (l0 + r, j) above them, for
+    k + 1 levels (fewer at the top), so every node's children are computed by an earlier launch or round
+    of its own workgroup.  Empty for plans without merge levels."""
+    if plan.mode != MODE_LEVELS or len(plan.batches) < 2:
+        return []
+    region = compress_region_floats(max_in, f64) * 4
+    cap_w = 1
+    while cap_w * 2 <= max_waves and cap_w * 2 * region <= lds_bytes:
+        cap_w *= 2
+    counts = [len(b) for b in plan.batches]
+    launches: List[MergeLaunch] = []
+    l0 = 1
+    while l0 < len(counts):
+        w = 1
+        while w < min(cap_w, counts[l0]):
+            w *= 2
+        depth = min(w.bit_length(), len(counts) - l0)
+        groups = -(-counts[l0] // w)
+        table = np.full((groups, depth, w), -1, dtype=np.int32)
+        for r in range(depth):
+            per = w >> r
+            for j in range(counts[l0 + r]):
+                table[j // per, r, j % per] = plan.batches[l0 + r][j]
+        launches.append(MergeLaunch(table, w, depth, (l0, l0 + depth - 1)))
+        l0 += depth
+    return launches
+
+
+def check_merge_launches(plan: NodePlan, desc: np.ndarray, launches: List[MergeLaunch]) -> None:
+    """Every merge node exactly once, after both its children (raw nodes: the first launch; merges: an
+    earlier launch, or an earlier round of the same workgroup).  Raises ValueError otherwise."""
+    done = np.zeros(plan.n_nodes, dtype=bool)
+    done[plan.batches[0]] = True
+    seen = np.zeros(plan.n_nodes, dtype=bool)
+    for ln in launches:
+        before = done.copy()
+        for g in range(ln.groups):
+            mine = before.copy()
+            for r in range(ln.phases):
+                nodes = [int(x) for x in ln.table[g, r] if x >= 0]
+                for node in nodes:
+                    if desc[node, 0] != KIND_MERGE or seen[node]:
+                        raise ValueError(f"merge launch lists node {node} twice or a raw node")
+                    a, b = int(desc[node, 1]), int(desc[node, 2])
+                    if not (mine[a] and mine[b]):
+                        raise ValueError(f"merge node {node} is scheduled before its children {a}, {b}")
+                    seen[node] = True
+                for node in nodes:
+                    mine[node] = True
+                    done[node] = True
+    merges = desc[: plan.n_nodes, 0] == KIND_MERGE
+    if not np.array_equal(seen, merges):
+        raise ValueError("merge launches leave merge nodes out")
 
 
 def segment_plan(n: int, block: int, stride: int) -> Tuple[NodePlan, int, int]:

@@ -589,39 +589,80 @@ int sta_decode_compress(int64_t streams, int d, int dv, const float* buf_k, cons
   return check_launch();
 }
 
+namespace {
+// Checks and argument block shared by sta_compress_nodes and sta_compress_tree (status in *st).
+sta::CompressArgs compress_args(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
+                                int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
+                                const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
+                                float* node_w, const int32_t* node_level, const int32_t* anc, int anc_levels,
+                                float* level_scores, size_t* smem, int* st) {
+  sta::CompressArgs a{};
+  *st = STA_OK;
+  const bool f64 = dtype == STA_F64;
+  if (!k || !batch_nodes || !node_desc || !node_src || !node_w) *st = STA_ERR_ARG;
+  else if (anc_levels < 0 || anc_levels > sta::CMP_MAX_ANC) *st = STA_ERR_ARG;
+  else if (anc_levels > 0 && (f64 || !level_scores)) *st = STA_ERR_ARG;
+  else if (anc && anc_levels <= 0) *st = STA_ERR_ARG;
+  else if (!dtype_ok(dtype) && !f64) *st = STA_ERR_DTYPE;
+  else if (bh <= 0 || n <= 0 || d <= 0 || n_nodes <= 0 || cap <= 0 || max_in <= 0) *st = STA_ERR_SHAPE;
+  else if (d > kMaxD || max_in > sta::CMP_MAX_IN) *st = STA_ERR_UNSUPPORTED;
+  else if (n_batch > 0 && bh > 65535) *st = STA_ERR_UNSUPPORTED;
+  else if (n_batch > 0 && n_draws > 0 && (!dirs || !unif || !perms)) *st = STA_ERR_ARG;
+  a.k = k; a.dtype = dtype; a.n = n; a.d = d; a.batch = batch_nodes; a.desc = node_desc; a.n_nodes = n_nodes;
+  a.cap = cap; a.dirs = dirs; a.unif = unif; a.perms = perms; a.n_draws = n_draws; a.max_in = max_in;
+  a.node_src = node_src; a.node_w = node_w; a.f64 = f64 ? 1 : 0;
+  a.anc = anc; a.node_level = node_level; a.anc_levels = anc_levels; a.lscore = level_scores;
+  *smem = sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in, f64, anc ? 2 * (1 + anc_levels) * d : 0));
+  return a;
+}
+}  // namespace
+
 int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* batch_nodes,
                        int n_batch, const int32_t* node_desc, int n_nodes, int cap, const void* dirs,
                        const void* unif, const int32_t* perms, int n_draws, int max_in, int32_t* node_src,
                        float* node_w, const int32_t* node_level, const int32_t* anc, int anc_levels,
                        float* level_scores, void* stream) {
-  if (!k || !batch_nodes || !node_desc || !node_src || !node_w) return STA_ERR_ARG;
-  const bool f64 = dtype == STA_F64;
-  if (anc_levels < 0 || anc_levels > sta::CMP_MAX_ANC) return STA_ERR_ARG;
-  if (anc_levels > 0 && (f64 || !node_level || !level_scores)) return STA_ERR_ARG;
-  if (anc && anc_levels <= 0) return STA_ERR_ARG;
-  if (!dtype_ok(dtype) && !f64) return STA_ERR_DTYPE;
-  if (bh <= 0 || n <= 0 || d <= 0 || n_nodes <= 0 || cap <= 0 || max_in <= 0) return STA_ERR_SHAPE;
-  if (d > kMaxD || max_in > sta::CMP_MAX_IN) return STA_ERR_UNSUPPORTED;
-  if (n_batch <= 0) return STA_OK;
-  if (bh > 65535) return STA_ERR_UNSUPPORTED;
-  if (n_draws > 0 && (!dirs || !unif || !perms)) return STA_ERR_ARG;
-  sta::CompressArgs a;
-  a.k = k; a.dtype = dtype; a.n = n; a.d = d; a.batch = batch_nodes; a.desc = node_desc; a.n_nodes = n_nodes;
-  a.cap = cap; a.dirs = dirs; a.unif = unif; a.perms = perms; a.n_draws = n_draws; a.max_in = max_in;
-  a.node_src = node_src; a.node_w = node_w; a.f64 = f64 ? 1 : 0;
-  a.anc = anc; a.node_level = node_level; a.anc_levels = anc_levels; a.lscore = level_scores;
-  const size_t smem =
-      sizeof(float) * static_cast<size_t>(sta::cmp_smem_floats(max_in, f64, anc ? 2 * (1 + anc_levels) * d : 0));
+  size_t smem = 0;
+  int st = STA_OK;
+  const sta::CompressArgs a = compress_args(k, dtype, bh, n, d, batch_nodes, n_batch, node_desc, n_nodes, cap, dirs,
+                                            unif, perms, n_draws, max_in, node_src, node_w, node_level, anc,
+                                            anc_levels, level_scores, &smem, &st);
+  if (st == STA_OK && anc_levels > 0 && !node_level) st = STA_ERR_ARG;  // merges read their levels
+  if (st != STA_OK || n_batch <= 0) return st;
   // the ancestor-scoring instantiation for a launch that passes the ancestor table (its raw nodes)
   const void* fn = anc ? reinterpret_cast<const void*>(sta::compress_kernel<true>)
                        : reinterpret_cast<const void*>(sta::compress_kernel<false>);
-  const int st = lds_limit(fn, smem);
+  st = lds_limit(fn, smem);
   if (st != STA_OK) return st;
   const dim3 grid(static_cast<unsigned>(n_batch), static_cast<unsigned>(bh));
   if (anc)
     hipLaunchKernelGGL(sta::compress_kernel<true>, grid, dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
   else
     hipLaunchKernelGGL(sta::compress_kernel<false>, grid, dim3(sta::CMP_THREADS), smem, static_cast<hipStream_t>(stream), a);
+  return check_launch();
+}
+
+int sta_compress_merges(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* node_table,
+                        int n_groups, int phases, int waves, const int32_t* node_desc, int n_nodes, int cap,
+                        const void* dirs, const void* unif, const int32_t* perms, int n_draws, int max_in,
+                        int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
+                        float* level_scores, void* stream) {
+  size_t smem = 0;
+  int st = STA_OK;
+  const sta::CompressArgs a = compress_args(k, dtype, bh, n, d, node_table, n_groups, node_desc, n_nodes, cap, dirs,
+                                            unif, perms, n_draws, max_in, node_src, node_w, node_level, nullptr,
+                                            anc_levels, level_scores, &smem, &st);
+  if (st == STA_OK && anc_levels > 0 && !node_level) st = STA_ERR_ARG;
+  if (st != STA_OK) return st;
+  if (phases <= 0 || waves <= 0 || waves > 16 || (waves & (waves - 1)) != 0) return STA_ERR_ARG;
+  if (n_groups <= 0) return STA_OK;
+  const int region = sta::cmp_smem_floats(max_in, dtype == STA_F64);
+  smem = sizeof(float) * static_cast<size_t>(region) * static_cast<size_t>(waves);
+  if (smem > 160 * 1024) return STA_ERR_UNSUPPORTED;
+  st = lds_limit(reinterpret_cast<const void*>(sta::compress_merge_kernel), smem);
+  if (st != STA_OK) return st;
+  hipLaunchKernelGGL(sta::compress_merge_kernel, dim3(static_cast<unsigned>(n_groups), static_cast<unsigned>(bh)),
+                     dim3(64 * waves), smem, static_cast<hipStream_t>(stream), a, node_table, phases, waves, region);
   return check_launch();
 }
 

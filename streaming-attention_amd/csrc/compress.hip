@@ -94,12 +94,12 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h, int dtype) {
 // rounded to fp32 once (every fp32 x fp32 product is exact in fp64, so a score is a fixed function of
 // the inputs).  Row r starts at element offset off_r of k_r (fp32 / bf16 / fp16) and is read in
 // 16-byte units when `vec` (row starts 16-byte aligned, d a whole number of units).  The units of both
-// rows are loaded 8 at a time before their products are accumulated, so up to 16 loads are in flight
+// rows are loaded B at a time before their products are accumulated, so up to 2 B loads are in flight
 // instead of one load per accumulation step.
+template <int B = 8>
 __device__ __forceinline__ void projection_scores2(const void* k0, int64_t off0, const void* k1, int64_t off1,
                                                    bool two, int d, int dtype, bool vec, const float* dir,
                                                    float& s0, float& s1) {
-  constexpr int B = 8;
   double a0 = 0.0, a1 = 0.0;
   if (vec && dtype == F32) {
     const floatx4* r0 = reinterpret_cast<const floatx4*>(static_cast<const float*>(k0) + off0);
@@ -211,17 +211,37 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The threads that compute one compress call together: the whole workgroup (CMP_THREADS threads,
+// workgroup barriers) or one wave (64 lanes; its LDS accesses are ordered by the wave's own
+// instruction order, so a code-motion barrier stands in for the workgroup barrier).
+struct BlockGroup {
+  static constexpr int threads = CMP_THREADS;
+  int tid;
+  __device__ __forceinline__ void sync() const { __syncthreads(); }
+};
+struct WaveGroup {
+  static constexpr int threads = 64;
+  int tid;  // lane
+  __device__ __forceinline__ void sync() const {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
 // Stable ascending order of n keys (ties by position): pos_s[rank(i)] = i with rank(i) = #{j: key_j <
 // key_i} + #{j < i: key_j == key_i} = #{j < i: key_j <= key_i} + #{j > i: key_j < key_i}.  A wave ranks
 // 64 consecutive items i0 .. i0 + 63 at a time: keys before i0 are compared with <=, keys after the
 // band with <, only the band itself needs the position test (one compare and one add per key elsewhere).
-// key_s holds the scores on entry (overwritten with sort keys); n <= CMP_MAX_IN; nthreads a multiple of
-// 64; two barriers.
-__device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int tid, int nthreads) {
+// key_s holds the scores on entry (overwritten with sort keys); n <= CMP_MAX_IN; two group barriers.
+template <class G>
+__device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, const G& g) {
+  const int tid = g.tid;
+  constexpr int nthreads = G::threads;
   uint32_t* uk = reinterpret_cast<uint32_t*>(key_s);
   for (int i = tid; i < n; i += nthreads) uk[i] = sort_key(key_s[i]);
   for (int i = n + tid; i < ((n + 3) & ~3); i += nthreads) uk[i] = 0xffffffffu;  // padding of the 4-wide reads
-  __syncthreads();
+  g.sync();
   const int n4 = (n + 3) & ~3;
   const int lane = tid & 63;
   // i0 and the loop bounds are wave-uniform (scalar loops); the key reads are issued 4 at a time (16
@@ -267,7 +287,11 @@ __device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int t
     }
     if (i < n) pos_s[r0 + r1] = i;
   }
-  __syncthreads();
+  g.sync();
+}
+__device__ __forceinline__ void rank_sort(float* key_s, int* pos_s, int n, int tid, int nthreads) {
+  rank_sort(key_s, pos_s, n, BlockGroup{tid});
+  (void)nthreads;  // CMP_THREADS
 }
 
 // Keep-first decision of the weighted pair rule: u < w_a / max(w_a + w_b, 1e-30)
@@ -322,9 +346,10 @@ __device__ __forceinline__ uint64_t sort_key64(double f) {
 // Stable ascending order of n 64-bit keys (ties by position), the rule of rank_sort without its
 // banded fast path: every thread counts, for each of its items, the keys below it and the equal keys
 // at lower positions (float64 scoring only).  Two barriers.
-__device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int n, int tid, int nthreads) {
-  __syncthreads();
-  for (int i = tid; i < n; i += nthreads) {
+template <class G>
+__device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int n, const G& g) {
+  g.sync();
+  for (int i = g.tid; i < n; i += G::threads) {
     const uint64_t me = uk[i];
     int r = 0;
     for (int j = 0; j < n; ++j) {
@@ -333,14 +358,21 @@ __device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int 
     }
     pos_s[r] = i;
   }
-  __syncthreads();
+  g.sync();
+}
+__device__ __forceinline__ void rank_sort64(const uint64_t* uk, int* pos_s, int n, int tid, int nthreads) {
+  rank_sort64(uk, pos_s, n, BlockGroup{tid});
+  (void)nthreads;  // CMP_THREADS
 }
 
-// ANC: the launch of raw (level-0) nodes that also write their ancestors' scores (a separate
-// instantiation: its score registers would cost every other launch occupancy)
-template <bool ANC>
-__global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
-  extern __shared__ __align__(16) float cmp_smem[];
+// One compress call: node `node` of sequence bh, computed by the threads of group g in their LDS region
+// smem (cmp_smem_floats floats, 16-byte aligned).  ANC: raw (level-0) nodes also write their
+// ancestors' scores (a separate instantiation: its score registers would cost every other launch
+// occupancy).  Ends without a barrier after its last LDS read.
+template <bool ANC, class G>
+__device__ __forceinline__ void compress_node(const CompressArgs& a, const int node, const int64_t bh, const G& g,
+                                              float* cmp_smem) {
+  constexpr int CMP_THREADS = G::threads;  // the group's threads, in every loop below
   const int M = cmp_round4(a.max_in);
   const bool f64 = a.f64 != 0;
   const int KA = cmp_key_floats(a.max_in, f64);
@@ -351,9 +383,7 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   float* dir_s = cmp_smem + KA + 3 * M;  // 8-byte aligned: KA and M are multiples of 4
   double* dir64_s = reinterpret_cast<double*>(dir_s);
 
-  const int node = a.batch[blockIdx.x];
-  const int64_t bh = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tid = g.tid;
   const int32_t* dsc = a.desc + static_cast<int64_t>(node) * NODE_DESC;
   const int kind = dsc[0], ia = dsc[1], ib = dsc[2], n_in = dsc[3], n_out = dsc[4];
   const int method = dsc[5], slot = dsc[6], na = dsc[7];
@@ -402,13 +432,16 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   } else {
     const int64_t baseA = (bh * a.n_nodes + ia) * a.cap;
     const int64_t baseB = (bh * a.n_nodes + ib) * a.cap;
+    // the children's token indices index key rows and score rows below: clamped to the sequence, so a
+    // child list that was never written reads rows of this sequence instead of faulting
+    const int hi = static_cast<int>(a.n - 1);
     for (int i = tid; i < n_in; i += CMP_THREADS) {
       const int64_t p = i < na ? baseA + i : baseB + (i - na);
-      src_s[i] = a.node_src[p];
+      src_s[i] = min(max(a.node_src[p], 0), hi);
       w_s[i] = a.node_w[p];
     }
   }
-  __syncthreads();
+  g.sync();
 
   const int64_t obase = (bh * a.n_nodes + node) * a.cap;
   if (method == M_COPY) {
@@ -436,7 +469,7 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
     uint64_t* uk = reinterpret_cast<uint64_t*>(key_s);
     for (int i = tid; i < n_in; i += CMP_THREADS)
       uk[i] = sort_key64(projection_score64(k64 + (bh * a.n + src_s[i]) * a.d, a.d, vec64, dir64_s));
-    rank_sort64(uk, pos_s, n_in, tid, CMP_THREADS);
+    rank_sort64(uk, pos_s, n_in, g);
   } else if (na_lev > 0) {
     // level-0 call with ancestor scores: the node's own score and the scores for its ancestors' calls
     // from one pass over each row
@@ -451,13 +484,13 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
         if (anc[l] >= 0) a.lscore[(bh * na_lev + l) * a.n + src_s[i]] = static_cast<float>(acc[1 + l]);
       }
     }
-    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
+    rank_sort(key_s, pos_s, n_in, g);
   } else if (kind == KIND_MERGE && !f64 && a.anc_levels > 0 && a.node_level[node] >= 1 &&
              a.node_level[node] <= a.anc_levels) {
     // a merge whose items' scores for this call were written by their level-0 calls
     const float* ls = a.lscore + (bh * a.anc_levels + (a.node_level[node] - 1)) * a.n;
     for (int i = tid; i < n_in; i += CMP_THREADS) key_s[i] = ls[src_s[i]];
-    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
+    rank_sort(key_s, pos_s, n_in, g);
   } else {
     const int epu = a.dtype == F32 ? 4 : 8;
     const bool vec = (a.d % epu) == 0 && (reinterpret_cast<uintptr_t>(a.k) & 15u) == 0;
@@ -465,13 +498,16 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
       const int i1 = i + CMP_THREADS;
       const bool two = i1 < n_in;
       float s0, s1;
-      projection_scores2(a.k, (bh * a.n + src_s[i]) * a.d, a.k, (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d,
-                         a.dtype, vec, dir_s, s0, s1);
+      // (a wave computing a node alone keeps 4 units of each row in flight: its registers are shared
+      // by every round of the merge launch)
+      projection_scores2<G::threads == 64 ? 4 : 8>(a.k, (bh * a.n + src_s[i]) * a.d, a.k,
+                                                   (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d, a.dtype, vec,
+                                                   dir_s, s0, s1);
       key_s[i] = s0;
       if (two) key_s[i1] = s1;
     }
     // ---- stable ascending order of (score, position) ----
-    rank_sort(key_s, pos_s, n_in, tid, CMP_THREADS);
+    rank_sort(key_s, pos_s, n_in, g);
   }
 
   // ---- pair selection with weight transfer ----
@@ -488,6 +524,32 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
     const int il = pos_s[n_in - 1];
     a.node_src[obase + pc] = src_s[il];
     a.node_w[obase + pc] = w_s[il];
+  }
+}
+
+// One node of a.batch per workgroup (x) and sequence (y).
+template <bool ANC>
+__global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArgs a) {
+  extern __shared__ __align__(16) float cmp_smem[];
+  compress_node<ANC>(a, a.batch[blockIdx.x], blockIdx.y, BlockGroup{static_cast<int>(threadIdx.x)}, cmp_smem);
+}
+
+// Merge nodes of several tree levels in one launch: workgroup x of sequence y runs `phases` rounds; in
+// round r its wave w computes node table[(x * phases + r) * waves + w] (-1: none) alone, then the
+// workgroup meets at a barrier, so a round may read what the rounds before it wrote (the children of
+// a subtree of merges: 2^(phases-1) nodes of the lowest level, then their parents, ...).  Each wave
+// has its own LDS region of region_floats floats.
+__global__ __launch_bounds__(1024) void compress_merge_kernel(const CompressArgs a, const int32_t* table, int phases,
+                                                              int waves, int region_floats) {
+  extern __shared__ __align__(16) float cmp_smem[];
+  const int wave = threadIdx.x >> 6;
+  const WaveGroup g{static_cast<int>(threadIdx.x & 63)};
+  float* smem = cmp_smem + wave * region_floats;
+  const int32_t* t = table + static_cast<int64_t>(blockIdx.x) * phases * waves + wave;
+  for (int r = 0; r < phases; ++r) {
+    const int node = __builtin_amdgcn_readfirstlane(t[r * waves]);
+    if (node >= 0 && node < a.n_nodes) compress_node<false>(a, node, blockIdx.y, g, smem);
+    __syncthreads();  // this round's node lists (global memory) before the next round reads them
   }
 }
 

@@ -370,6 +370,50 @@ def test_cpu_inputs_round_trip():
     assert rel(out, orc.fast_path_forward(q, k, v, degree=2, block=64, scale=1.0)) < FP32_TOL
 
 
+@pytest.mark.parametrize("n,d,block,dtype,comp,anc", [(3000, 16, 64, torch.float32, "sorted_pair", True),
+                                                      (5000, 64, 16, torch.float32, "sorted_pair", True),
+                                                      (2100, 64, 32, torch.bfloat16, "sorted_pair", False),
+                                                      (1500, 6, 33, torch.float32, "sorted_pair", True),
+                                                      (700, 8, 16, torch.float32, "random", False),
+                                                      (900, 24, 64, torch.float64, "sorted_pair", False)])
+def test_merge_launches_match_level_launches(n, d, block, dtype, comp, anc, monkeypatch):
+    """The merge levels as subtree launches (sta_compress_merges, one wave per node) give every node of
+    every head bit for bit as the launches level by level, for workgroups of 16, 4 and 1 waves, and the
+    oracle's cascade."""
+    print(f"merge launches n={n} d={d} block={block} {dtype} {comp} anc={anc}", flush=True)
+    q, k, v = orc.make_data((3,), n, d, 8, radius=1.0, data="unit_ball", seed=n + d + 1)
+    # float64: float32 inputs with the float64 keys scored in fp64 (score_keys), as a float64 caller's
+    k64 = k.double() if dtype == torch.float64 else None
+    q, k, v = (x.to(torch.float32 if dtype == torch.float64 else dtype) for x in (q, k, v))
+    monkeypatch.setattr(_engine, "ANCESTOR_MIN_ROW_BYTES", 0)
+    monkeypatch.setattr(_engine, "ANCESTOR_SCORES", anc)
+    res = {}
+    for waves in (0, 16, 4, 1):
+        monkeypatch.setattr(_engine, "MERGE_WAVES", waves)
+        r = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block=block, scale=0.5, semantics="levels",
+                            compressor=comp, seed=7, score_keys=None if k64 is None else k64.to(DEV).contiguous())
+        torch.cuda.synchronize()
+        res[waves] = (r.node_src.cpu(), r.node_w.cpu(), r.out.float().cpu(), r.plan)
+    base = res[0]
+    for waves in (16, 4, 1):
+        src, w, out, _ = res[waves]
+        assert torch.equal(src, base[0]) and torch.equal(w, base[1]), f"{waves} waves"
+        assert torch.equal(out, base[2]), f"{waves} waves"
+    plan = base[3]
+    if dtype != torch.float64:  # the float64 cascade is pinned by the float64 selection tests
+        for h in range(3):
+            state = orc.LevelState()
+            g = torch.Generator(device="cpu")
+            g.manual_seed(7 + h)
+            keys = k[h].float().numpy()
+            for b in range(n // block):
+                orc.level_block_complete(state, g, np.arange(b * block, (b + 1) * block, dtype=np.int64), keys, comp)
+            for node in range(plan.n_nodes):
+                size = int(plan.meta[node, 0])
+                c = state.calls[int(plan.desc[node, 6])]
+                assert np.array_equal(res[16][0][h, node, :size].numpy(), c.src_out), f"head {h} node {node}"
+
+
 @pytest.mark.parametrize("n,d,block,dtype,comp", [(3000, 16, 64, torch.float32, "sorted_pair"),
                                                   (2100, 64, 32, torch.bfloat16, "sorted_pair"),
                                                   (1500, 6, 33, torch.float32, "sorted_pair"),
