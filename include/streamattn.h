@@ -191,6 +191,20 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
                           void* stream);
 
 /*
+ * Block form of sta_moment_accumulate for short runs of rows (a decode block completion): the same
+ * state update, bit for bit, for split-bf16 products, degree <= 2, d <= 64 (rows d elements apart,
+ * no windows) and (wave_tiles, column_tiles) = (2, 2), (4, 2) or (2, 4) (sta_moment_accumulate's
+ * feature tables at that tile count).  One workgroup per (head, group of 16 column_tiles value
+ * columns; 32 ceil(dv / 32) a multiple of it) stages up to 256 rows at a time once, then runs every
+ * feature slice of the state through them (more rows: groups of 256, the state read and written per
+ * group).  STA_ERR_UNSUPPORTED outside those limits.
+ */
+int sta_moment_accumulate_block(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows,
+                                int d, int dv, int ldv, int degree, int fsplit, int wave_tiles, int column_tiles,
+                                const uint32_t* feat_quads, const float* feat_coef, const int32_t* feat_rows,
+                                int n_feat, float* state_num, float* state_den, void* stream);
+
+/*
  * sta_moment_accumulate on the wave-specialised kernel's update-only pass (split-bf16 products, degree
  * <= 3, d <= 128): 4 update waves per workgroup keep the state of 4 slots of slot_tiles feature tiles x
  * 16 column_tiles columns in matrix-core accumulators, loaded from and stored back to the persistent

@@ -54,6 +54,15 @@ ACCUMULATE_PRODUCTS = _native.PRODUCTS_SPLIT_BF16
 # (split products, degree <= 3, d <= 128); STA_ACCUMULATE_WS=0 keeps the chunked accumulation kernel
 ACCUMULATE_WS = os.environ.get("STA_ACCUMULATE_WS", "1") != "0"
 ACCUMULATE_WS_MIN_ROWS = 512
+# Shorter runs of rows (a block completion) through the block accumulation (sta_moment_accumulate_block:
+# the rows staged once per workgroup, every feature slice of the state run through them with the next
+# slice's loads in flight; split products, degree <= 2, d <= 64) with this many tiles per wave;
+# STA_ACCUMULATE_BLOCK=0 keeps the chunked kernel (the state is the same bit for bit).
+ACCUMULATE_BLOCK = os.environ.get("STA_ACCUMULATE_BLOCK", "1") != "0"
+ACCUMULATE_BLOCK_TILES = int(os.environ.get("STA_ACCUMULATE_BLOCK_TILES", "2"))
+# value columns per workgroup: 64 (every key feature generated once per stream) where the state's rows
+# are whole groups of 64, else 32
+ACCUMULATE_BLOCK_COLUMNS = int(os.environ.get("STA_ACCUMULATE_BLOCK_COLUMNS", "64"))
 
 
 class StaticScratchOwners:
@@ -212,6 +221,31 @@ class DecodeState:
             self._acc_tables[key] = entry
         return self._acc_tables[key]
 
+    def _block_column_tiles(self) -> int:
+        ldo = 32 * (-(-self.dv // 32))
+        return 4 if ACCUMULATE_BLOCK_COLUMNS == 64 and ldo % 64 == 0 and ACCUMULATE_BLOCK_TILES == 2 else 2
+
+    def _acc_table_block(self, width: int):
+        """Tables of the block accumulation (sta_moment_accumulate_block) for rows `width` elements long
+        (the chunked kernel's table layout at ACCUMULATE_BLOCK_TILES tiles per wave), or None where it
+        does not apply: (split, quads, coef, rows)."""
+        key = ("block", width, ACCUMULATE_BLOCK_TILES)
+        if key not in self._acc_tables:
+            entry = None
+            if (ACCUMULATE_BLOCK and self.products == _native.PRODUCTS_SPLIT_BF16 and self.degree <= 2
+                    and width <= 64):
+                opts = tuple(o for o in _native.moment_wave_tile_options(width, self.degree)
+                             if o[0] == ACCUMULATE_BLOCK_TILES)
+                if opts:
+                    ft = _plan.feature_tiles(width, self.degree)
+                    ms = _plan.moment_split(ft, self.S, self.dv, opts)
+                    rows = _plan.split_state_rows(ft, ms, self.d)
+                    dev = self.device
+                    entry = (ms, torch.from_numpy(ms.quads.view(np.int32)).to(dev), torch.from_numpy(ms.coef).to(dev),
+                             torch.from_numpy(rows).to(dev))
+            self._acc_tables[key] = entry
+        return self._acc_tables[key]
+
     def _accumulate(self, k: torch.Tensor, v: torch.Tensor, n: int, head_rows: int, state_num: torch.Tensor,
                     state_den: torch.Tensor, row_off: int = 0) -> None:
         """state += moments of rows [row_off, row_off + n) of k [S, head_rows, width] / v [S, head_rows, ldv]
@@ -237,6 +271,20 @@ class DecodeState:
                 _native.check(st, "sta_moment_accumulate_ws")
 
             self._launch("moment_accumulate", run_ws)
+            return
+        blk = self._acc_table_block(width)
+        if blk is not None:
+            ms, quads, coef, rows = blk
+
+            def run_block():
+                st = self.lib.sta_moment_accumulate_block(
+                    kp, vp, _native.DTYPE_CODES[k.dtype], self.S, n, head_rows, width, self.dv, v.shape[-1],
+                    self.degree, ms.fsplit, ms.wave_tiles, self._block_column_tiles(), quads.data_ptr(),
+                    coef.data_ptr(), rows.data_ptr(), self.F, state_num.data_ptr(), state_den.data_ptr(),
+                    self._stream())
+                _native.check(st, "sta_moment_accumulate_block")
+
+            self._launch("moment_accumulate", run_block)
             return
         ms, quads, coef, rows, win, staged = self._acc_table(width)
 

@@ -91,6 +91,11 @@ _SIGNATURES = {
     "sta_flash_attention": (
         _i32, [_c_p, _c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _c_p, _i32, _c_p],
     ),
+    "sta_moment_accumulate_block": (
+        _i32,
+        [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _i32, _c_p,
+         _c_p, _c_p],  # k v dtype bh n head_rows d dv ldv degree fsplit wave_tiles column_tiles quads coef rows ...
+    ),
     "sta_moment_accumulate_ws": (
         _i32,
         [_c_p, _c_p, _i32, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,  # ... fs nts mixed ct

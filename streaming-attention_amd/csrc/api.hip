@@ -386,6 +386,36 @@ int sta_moment_accumulate(const void* k, const void* v, int dtype, int64_t bh, i
                              products == STA_PRODUCTS_SPLIT_BF16);
 }
 
+int sta_moment_accumulate_block(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows,
+                                int d, int dv, int ldv, int degree, int fsplit, int wave_tiles, int column_tiles,
+                                const uint32_t* feat_quads, const float* feat_coef, const int32_t* feat_rows,
+                                int n_feat, float* state_num, float* state_den, void* stream) {
+  if (!k || !v || !feat_quads || !feat_coef || !feat_rows || !state_num || !state_den) return STA_ERR_ARG;
+  if (!dtype_ok(dtype)) return STA_ERR_DTYPE;
+  if (bh <= 0 || n < 0 || head_rows < n || d <= 0 || dv <= 0 || fsplit <= 0 || wave_tiles <= 0 || n_feat <= 0)
+    return STA_ERR_SHAPE;
+  if (d > 64 || dv > kMaxDv || degree < 0 || degree > 2) return STA_ERR_UNSUPPORTED;
+  if (moment_wave_tiles(d, degree, wave_tiles) != wave_tiles ||
+      !accumulate_block_ok(wave_tiles, moment_extra_factors(degree), column_tiles))
+    return STA_ERR_UNSUPPORTED;
+  if (n == 0) return STA_OK;
+  const int esize = dtype == STA_F32 ? 4 : 2;
+  // the state's rows are 32 ceil(dv / 32) floats, whole column groups of 16 column_tiles
+  if ((d * esize) % 16 != 0 || ldv < dv || ldv % 32 != 0 || (32 * ((dv + 31) / 32)) % (16 * column_tiles) != 0)
+    return STA_ERR_ARG;
+  if (((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u) != 0) return STA_ERR_ARG;
+  if (head_rows * static_cast<int64_t>(ldv > d ? ldv : d) * esize >= (int64_t(1) << 32) || n >= (int64_t(1) << 30))
+    return STA_ERR_UNSUPPORTED;
+  sta::MomArgs a;
+  a.q = k; a.k = k; a.v = v; a.dtype = dtype; a.n = n; a.d = d; a.dv = dv; a.scale = 1.0f; a.shift = 0;
+  a.fsplit = fsplit; a.mixed = 0; a.csplit = (dv + 31) / 32; a.quads = feat_quads; a.fcoef = feat_coef;
+  a.low_num = nullptr; a.low_den = nullptr; a.ldv = ldv; a.esize = esize; a.ldo = 32 * a.csplit;
+  a.ldk = d; a.win = nullptr;
+  a.head_rows = head_rows; a.rowmap = feat_rows; a.state_num = state_num; a.state_den = state_den; a.n_feat = n_feat;
+  return dispatch_accumulate_block(a, bh, static_cast<hipStream_t>(stream), wave_tiles, moment_extra_factors(degree),
+                                   column_tiles);
+}
+
 int sta_moment_accumulate_ws(const void* k, const void* v, int dtype, int64_t bh, int64_t n, int64_t head_rows, int d,
                              int ld_k, int dv, int ldv, int degree, int fsplit, int slot_tiles, int mixed,
                              int column_tiles, const uint32_t* feat_quads, const float* feat_coef,

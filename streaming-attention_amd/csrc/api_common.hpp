@@ -72,6 +72,10 @@ constexpr int kNtHi[] = {4};  // degree 5 .. 8: d <= 64, fp32 products
   X(3, 0, true) X(5, 0, true)
 constexpr int kWsNts[] = {2, 3, 4, 5};
 
+// X(NT, NX, CT) of the block accumulation (moment_block_kernel: split-bf16 products, d <= 64; degree
+// <= 2: more tiles, column tiles or extra factors spill its registers next to the prefetched slice).
+#define STA_MOMENT_BLOCK_CONFIGS(X) X(2, 0, 2) X(4, 0, 2) X(2, 0, 4)
+
 // X(NT, NX, DBIG) of the 64-column (split-product) moment kernels.
 #define STA_MOMENT_CONFIGS_64(X) X(5, 0, false)
 
@@ -114,6 +118,14 @@ template <int ES, int CT>
 int dispatch_moments_ws(const sta::WsArgs& a, int64_t bh, hipStream_t s, int nts, int nx);
 // launch_accumulate.hip: in-place accumulation into a decode state (moment_accumulate_kernel).
 int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, bool split);
+int dispatch_accumulate_block(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, int ct);
+// 1 when moment_block_kernel is built for (wave tiles, extra factors, column tiles).
+inline bool accumulate_block_ok(int nt, int nx, int ct) {
+#define STA_CASE(NT, NX, CT) if (nt == NT && nx == NX && ct == CT) return true;
+  STA_MOMENT_BLOCK_CONFIGS(STA_CASE)
+#undef STA_CASE
+  return false;
+}
 // launch_block.hip, one object per (DP, DVT, ES): the residual / combine kernel (block_attn_kernel) for
 // padded key width DP, value-column tile count DVT and element size ES.
 template <int DP, int DVT, int ES>

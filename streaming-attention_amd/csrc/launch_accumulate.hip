@@ -19,7 +19,29 @@ int launch(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
   return check_launch();
 }
 
+template <int NT, int NX, int ES, int CT>
+int launch_block(const sta::MomArgs& a, int64_t bh, hipStream_t s) {
+  const size_t smem = static_cast<size_t>(sta::momb_smem_floats(NT, CT)) * sizeof(float);
+  auto fn = sta::moment_block_kernel<NT, NX, ES, CT>;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+  if (e != hipSuccess) return hip_status(e);
+  const int64_t grid = bh * (a.csplit * 32 / (16 * CT));
+  if (grid <= 0 || grid > 0x7fffffff) return STA_ERR_SHAPE;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(grid)), dim3(sta::MOMB_THREADS), smem, s, a);
+  return check_launch();
+}
+
 }  // namespace
+
+int dispatch_accumulate_block(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, int ct) {
+#define STA_CASE(NT, NX, CT)                                                                        \
+  if (nt == NT && nx == NX && ct == CT)                                                           \
+    return a.esize == 4 ? launch_block<NT, NX, 4, CT>(a, bh, s) : launch_block<NT, NX, 2, CT>(a, bh, s);
+  STA_MOMENT_BLOCK_CONFIGS(STA_CASE)
+#undef STA_CASE
+  return STA_ERR_UNSUPPORTED;
+}
 
 int dispatch_accumulate(const sta::MomArgs& a, int64_t bh, hipStream_t s, int nt, int nx, bool split) {
   const bool big = a.d > 64;

@@ -931,4 +931,185 @@ __global__ __launch_bounds__(MOM_THREADS, 1) void moment_accumulate_kernel(const
   }
 }
 
+// Block form of moment_accumulate_kernel (split-bf16 products, d <= 64 without windows): one workgroup of
+// MOMB_WAVES waves per (head, 32-column group) stages up to MOMB_CHUNKS chunks of its rows at once (keys
+// transposed, values as bf16 hi / lo planes, the layouts of mom_store), then every wave takes the
+// chunked kernel's wave slices j = wave, wave + MOMB_WAVES, ... (NT tiles each, tile0 = j NT) and runs
+// the staged chunks through mom_update_split with no barrier, the next slice's state and feature table
+// loads in flight meanwhile.  A slice's accumulators see the chunks in the same order and through the
+// same products as moment_accumulate_kernel's, so the state is the same bit for bit; the rows are staged
+// once per column group instead of once per feature split.  More than MOMB_CHUNKS chunks: groups of
+// chunks, the state read and written back per group.
+constexpr int MOMB_WAVES = 8;
+constexpr int MOMB_THREADS = 64 * MOMB_WAVES;
+constexpr int MOMB_CHUNKS = 8;
+// LDS floats of one staged chunk: transposed keys (mom_krows(false) rows) and the value planes of the
+// workgroup's 16 CT columns
+__host__ __device__ constexpr int momb_chunk_floats(int ct) { return mom_krows(false) * MOM_LDT + 16 * ct * MOM_LDT; }
+__host__ __device__ constexpr int momb_smem_floats(int nt, int ct) {
+  return MOMB_CHUNKS * momb_chunk_floats(ct) + MOMB_WAVES * nt * 16 + 8;
+}
+
+// CT column tiles of 16 per workgroup (2: 32 columns, a.csplit groups; 4: 64 columns, every key feature
+// generated once per head; the products of each 16-column tile are the same either way).
+template <int NT, int NX, int ES, int CT>
+__global__ __launch_bounds__(MOMB_THREADS, 1) void moment_block_kernel(const MomArgs a) {
+  constexpr int CG = 16 * CT;
+  constexpr int CF = momb_chunk_floats(CT);
+  constexpr int KROWS = mom_krows(false);
+  constexpr int EPU = 16 / ES;
+  extern __shared__ float smem[];
+  float* den_all = smem + MOMB_CHUNKS * CF;
+
+  const int groups = a.csplit * 32 / CG;  // column groups per head (the host keeps a.ldo a multiple of CG)
+  const int wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / groups;
+  const int cs = wg - static_cast<int>(bh) * groups;
+  const int col0 = CG * cs;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  float* den_s = den_all + wave * NT * 16;
+  float* snum = a.state_num + bh * a.n_feat * a.ldo;
+  float* sden = a.state_den + bh * a.n_feat;
+  const char* kh = static_cast<const char*>(a.k) + bh * a.head_rows * a.ldk * ES;
+  const char* vh = static_cast<const char*>(a.v) + bh * a.head_rows * a.ldv * ES;
+  const int uq = a.d / EPU;                         // key units per row
+  const int n_slices = a.fsplit * MOM_WAVES;        // the chunked kernel's wave slices
+  const int n_rows = static_cast<int>(a.n);
+
+  // the state of slice j (rowmap order) into accumulators, its denominators into registers
+  auto load_slice = [&](int j, floatx4 (&st)[NT][CT], float (&dn)[NT]) {
+    const int64_t tile0 = static_cast<int64_t>(j) * NT;
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          st[kt][ct][r] = row >= 0 ? snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] : 0.f;
+      }
+      const int row = a.rowmap[(tile0 + kt) * 16 + li];
+      dn[kt] = row >= 0 ? sden[row] : 0.f;
+    }
+  };
+
+  for (int e = tid; e < MOMB_CHUNKS * CF; e += MOMB_THREADS) smem[e] = 0.f;  // padding rows stay 0
+  for (int g0 = 0; g0 < n_rows; g0 += MOMB_CHUNKS * MOM_C) {
+    const int nch = min(MOMB_CHUNKS, (n_rows - g0 + MOM_C - 1) / MOM_C);
+    // ---- stage the group's chunks: unit loads first (rows clamped into the sequence), then the stores;
+    //      token-fast units so that a half-wave writes one transposed row / plane row ----
+    {
+      constexpr int KJ = MOMB_CHUNKS * MOM_C * (64 / EPU) / MOMB_THREADS;  // key units per thread (max)
+      constexpr int VJ = MOMB_CHUNKS * MOM_C * (CG / EPU) / MOMB_THREADS;  // value units per thread
+      const int kunits = nch * MOM_C * uq, vunits = nch * MOM_C * (CG / EPU);
+      uint4 ku[KJ], vu[VJ];
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        const int e = min(tid + MOMB_THREADS * j, kunits - 1);
+        const int c = e / (MOM_C * uq), r = e - c * (MOM_C * uq);
+        const int row = clamp_row(g0 + c * MOM_C + (r & (MOM_C - 1)), n_rows);
+        ku[j] = *reinterpret_cast<const uint4*>(kh + (static_cast<int64_t>(row) * a.ldk + (r >> 5) * EPU) * ES);
+      }
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        const int e = min(tid + MOMB_THREADS * j, vunits - 1);
+        const int c = e / (MOM_C * (CG / EPU)), r = e - c * (MOM_C * (CG / EPU));
+        const int row = clamp_row(g0 + c * MOM_C + (r & (MOM_C - 1)), n_rows);
+        vu[j] = *reinterpret_cast<const uint4*>(vh + (static_cast<int64_t>(row) * a.ldv + col0 + (r >> 5) * EPU) * ES);
+      }
+      __syncthreads();  // the previous group's updates are done with the chunk buffers
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        const int e = tid + MOMB_THREADS * j;
+        if (e < kunits) {
+          const int c = e / (MOM_C * uq), r = e - c * (MOM_C * uq);
+          const int tok = r & (MOM_C - 1), u = r >> 5;
+          const float kok = g0 + c * MOM_C + tok < n_rows ? 1.f : 0.f;
+          float f[8];
+          unit_floats<ES>(ku[j], a.dtype, f);
+          float* kt = smem + c * CF;
+#pragma unroll
+          for (int m = 0; m < EPU; ++m) kt[(u * EPU + m) * MOM_LDT + tok] = f[m] * kok;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        const int e = tid + MOMB_THREADS * j;
+        if (e < vunits) {
+          const int c = e / (MOM_C * (CG / EPU)), r = e - c * (MOM_C * (CG / EPU));
+          const int tok = r & (MOM_C - 1), u = r >> 5;
+          const float kok = g0 + c * MOM_C + tok < n_rows ? 1.f : 0.f;
+          float f[8];
+          unit_floats<ES>(vu[j], a.dtype, f);
+          __bf16* vp = reinterpret_cast<__bf16*>(smem + c * CF + KROWS * MOM_LDT);
+#pragma unroll
+          for (int m = 0; m < EPU; ++m) {
+            const float x = f[m] * kok;
+            const __bf16 h = static_cast<__bf16>(x);
+            const __bf16 l = static_cast<__bf16>(x - static_cast<float>(h));
+            vp[vps_off(u * EPU + m, tok)] = h;
+            vp[CG * MOM_C + vps_off(u * EPU + m, tok)] = l;
+          }
+        }
+      }
+      // the constant factor: 1 on rows inside the sequence, 0 outside
+      for (int e = tid; e < nch * MOM_C; e += MOMB_THREADS) {
+        const int c = e >> 5, tok = e & (MOM_C - 1);
+        smem[c * CF + a.d * MOM_LDT + tok] = g0 + c * MOM_C + tok < n_rows ? 1.f : 0.f;
+      }
+      __syncthreads();
+    }
+
+    // ---- the wave's slices, each through every staged chunk; the next slice's loads in flight ----
+    auto none = []() {};
+    floatx4 st[NT][CT];
+    float dn[NT];
+    int j = wave;
+    if (j < n_slices) load_slice(j, st, dn);
+    while (j < n_slices) {
+      MomLane<NT, NX> m = mom_lane<NT, NX>(a, static_cast<int64_t>(j) * NT, li, lg);
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt)
+        if (lg == 0) den_s[16 * kt + li] = dn[kt];
+      const int jn = j + MOMB_WAVES;
+      floatx4 stn[NT][CT];
+      float dnn[NT];
+      if (jn < n_slices) load_slice(jn, stn, dnn);
+      for (int c = 0; c < nch; ++c) {
+        const float* Kt = smem + c * CF;
+        mom_update_split<NT, CT, NX, true, decltype(none), true>(st, den_s, Kt, Kt + KROWS * MOM_LDT, m, li, lg, none);
+      }
+      // write the slice back (the denominators once per column group 0)
+      const int64_t tile0 = static_cast<int64_t>(j) * NT;
+#pragma unroll
+      for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+          if (row >= 0) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] = st[kt][ct][r];
+          }
+        }
+        if (lg == 0 && cs == 0) {
+          const int row = a.rowmap[(tile0 + kt) * 16 + li];
+          if (row >= 0) sden[row] = den_s[16 * kt + li];
+        }
+      }
+      j = jn;
+      if (j < n_slices) {
+#pragma unroll
+        for (int kt = 0; kt < NT; ++kt) {
+          dn[kt] = dnn[kt];
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) st[kt][ct] = stn[kt][ct];
+        }
+      }
+    }
+  }
+}
+
 }  // namespace sta

@@ -289,6 +289,55 @@ def test_accumulate_ws_matches_chunked_and_closed_form(monkeypatch, S, n, head_r
             assert torch.all(num[s][:, dv:] == 0)
 
 
+@pytest.mark.parametrize("S,n,head_rows,d,dv,degree,dtype,tiles,cols", [
+    (3, 256, 256, 64, 64, 2, torch.float32, 4, 32), (2, 300, 320, 16, 24, 2, torch.float32, 4, 32),
+    (2, 100, 128, 64, 100, 2, torch.float32, 2, 64), (2, 257, 260, 48, 64, 1, torch.bfloat16, 4, 32),
+    (1, 33, 40, 8, 8, 0, torch.float32, 2, 64), (2, 256, 256, 64, 64, 2, torch.bfloat16, 2, 64),
+    (1, 600, 600, 32, 64, 2, torch.float16, 4, 32), (3, 256, 256, 64, 64, 2, torch.float32, 2, 32),
+    (2, 520, 520, 64, 64, 2, torch.float32, 2, 64)])
+def test_accumulate_block_matches_chunked(monkeypatch, S, n, head_rows, d, dv, degree, dtype, tiles, cols):
+    """The block accumulation (sta_moment_accumulate_block: rows staged once per workgroup, every feature
+    slice run through them) gives the chunked kernel's state bit for bit from the same nonzero state
+    (runs of 1 to 3 groups of 256 rows, 1 to 4 column groups of 32 or 64 columns, 2 and 4 tiles per
+    wave), and the fp64 closed form state0 + sum_j phi_k(k_j) [v_j, 1]."""
+    print(f"accumulate block S={S} n={n} rows={head_rows} d={d} dv={dv} degree={degree} {dtype} nt={tiles} "
+          f"cols={cols}", flush=True)
+    g = torch.Generator().manual_seed(n + d + 1)
+    states = {}
+    monkeypatch.setattr(_decode, "ACCUMULATE_WS", False)
+    monkeypatch.setattr(_decode, "ACCUMULATE_BLOCK_TILES", tiles)
+    monkeypatch.setattr(_decode, "ACCUMULATE_BLOCK_COLUMNS", cols)
+    for blk in (True, False):
+        monkeypatch.setattr(_decode, "ACCUMULATE_BLOCK", blk)
+        st = _decode.DecodeState(S, d, dv, degree=degree, block=64, scale=1.0, compressor="sorted_pair", seed=0,
+                                 device=DEV)
+        if blk:
+            assert st._acc_table_block(st.dk) is not None
+            k = torch.zeros(S, head_rows, st.dk)
+            k[:, :, :d] = torch.randn(S, head_rows, d, generator=g) * 0.4
+            v = torch.zeros(S, head_rows, st.ldv)
+            v[:, :, :dv] = torch.randn(S, head_rows, dv, generator=g)
+            k, v = k.to(dtype), v.to(dtype)
+            num0 = torch.randn(S, st.F, st.ldv, generator=g)
+            num0[..., dv:] = 0
+            den0 = torch.randn(S, st.F, generator=g)
+        else:
+            assert st._acc_table_block(st.dk) is None
+        st.state_num.copy_(num0.to(DEV))
+        st.state_den.copy_(den0.to(DEV))
+        st._accumulate(k.to(DEV).contiguous(), v.to(DEV).contiguous(), n, head_rows, st.state_num, st.state_den)
+        torch.cuda.synchronize()
+        states[blk] = (st.state_num.cpu(), st.state_den.cpu())
+    assert torch.equal(states[True][0], states[False][0]) and torch.equal(states[True][1], states[False][1])
+    for s in range(S):
+        phi = orc.features(k[s, :n, :d].double(), degree, key_side=True)
+        want_num = num0[s].double()[:, :dv] + phi.T @ v[s, :n, :dv].double()
+        want_den = den0[s].double() + phi.sum(0)
+        num, den = (x.double() for x in states[True])
+        assert rel(num[s][:, :dv], want_num) < MOM_TOL and rel(den[s], want_den) < 1e-6, s
+        assert torch.all(num[s][:, dv:] == 0)
+
+
 def test_query_stats_split():
     """return_stats: denominator = low + tail, with the reference's split: low over every token (the
     sketch holds the buffered tokens too), tail over items() = buffer (weight 1) + levels."""
