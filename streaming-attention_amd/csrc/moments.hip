@@ -979,20 +979,32 @@ __global__ __launch_bounds__(MOMB_THREADS, 1) void moment_block_kernel(const Mom
   const int n_slices = a.fsplit * MOM_WAVES;        // the chunked kernel's wave slices
   const int n_rows = static_cast<int>(a.n);
 
-  // the state of slice j (rowmap order) into accumulators, its denominators into registers
-  auto load_slice = [&](int j, floatx4 (&st)[NT][CT], float (&dn)[NT]) {
+  // state rows of slice j's accumulator elements (rowmap, -1: padding) and of its denominators
+  struct Rows {
+    int r[NT][4];
+    int d[NT];
+  };
+  auto load_rows = [&](int j, Rows& R) {
     const int64_t tile0 = static_cast<int64_t>(j) * NT;
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
+      for (int r = 0; r < 4; ++r) R.r[kt][r] = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+      R.d[kt] = a.rowmap[(tile0 + kt) * 16 + li];
+    }
+  };
+  // a slice's state into accumulators, its denominators into registers
+  auto load_state = [&](const Rows& R, floatx4 (&st)[NT][CT], float (&dn)[NT]) {
+#pragma unroll
+    for (int kt = 0; kt < NT; ++kt) {
+#pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+        const int row = R.r[kt][r];
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
           st[kt][ct][r] = row >= 0 ? snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] : 0.f;
       }
-      const int row = a.rowmap[(tile0 + kt) * 16 + li];
-      dn[kt] = row >= 0 ? sden[row] : 0.f;
+      dn[kt] = R.d[kt] >= 0 ? sden[R.d[kt]] : 0.f;
     }
   };
 
@@ -1063,41 +1075,47 @@ __global__ __launch_bounds__(MOMB_THREADS, 1) void moment_block_kernel(const Mom
       __syncthreads();
     }
 
-    // ---- the wave's slices, each through every staged chunk; the next slice's loads in flight ----
+    // ---- the wave's slices, each through every staged chunk.  Pipelined: while slice j runs, the state
+    //      and feature tables of slice j + W and the state rows of slice j + 2 W are in flight ----
     auto none = []() {};
     floatx4 st[NT][CT];
     float dn[NT];
+    Rows rn;
     int j = wave;
-    if (j < n_slices) load_slice(j, st, dn);
+    if (j < n_slices) {
+      load_rows(j, rn);
+      load_state(rn, st, dn);
+    }
+    if (j + MOMB_WAVES < n_slices) load_rows(j + MOMB_WAVES, rn);
+    MomLane<NT, NX> m = mom_lane<NT, NX>(a, static_cast<int64_t>(min(j, n_slices - 1)) * NT, li, lg);
     while (j < n_slices) {
-      MomLane<NT, NX> m = mom_lane<NT, NX>(a, static_cast<int64_t>(j) * NT, li, lg);
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt)
         if (lg == 0) den_s[16 * kt + li] = dn[kt];
       const int jn = j + MOMB_WAVES;
       floatx4 stn[NT][CT];
       float dnn[NT];
-      if (jn < n_slices) load_slice(jn, stn, dnn);
+      Rows rc, rnn;
+      load_rows(j, rc);  // this slice's rows again, for its stores (no wait before the updates)
+      if (jn < n_slices) load_state(rn, stn, dnn);
+      if (jn + MOMB_WAVES < n_slices) load_rows(jn + MOMB_WAVES, rnn);
+      const MomLane<NT, NX> mn = mom_lane<NT, NX>(a, static_cast<int64_t>(min(jn, n_slices - 1)) * NT, li, lg);
       for (int c = 0; c < nch; ++c) {
         const float* Kt = smem + c * CF;
         mom_update_split<NT, CT, NX, true, decltype(none), true>(st, den_s, Kt, Kt + KROWS * MOM_LDT, m, li, lg, none);
       }
       // write the slice back (the denominators once per column group 0)
-      const int64_t tile0 = static_cast<int64_t>(j) * NT;
 #pragma unroll
       for (int kt = 0; kt < NT; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = a.rowmap[(tile0 + kt) * 16 + 4 * lg + r];
+          const int row = rc.r[kt][r];
           if (row >= 0) {
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) snum[static_cast<int64_t>(row) * a.ldo + col0 + 16 * ct + li] = st[kt][ct][r];
           }
         }
-        if (lg == 0 && cs == 0) {
-          const int row = a.rowmap[(tile0 + kt) * 16 + li];
-          if (row >= 0) sden[row] = den_s[16 * kt + li];
-        }
+        if (lg == 0 && cs == 0 && rc.d[kt] >= 0) sden[rc.d[kt]] = den_s[16 * kt + li];
       }
       j = jn;
       if (j < n_slices) {
@@ -1107,6 +1125,8 @@ __global__ __launch_bounds__(MOMB_THREADS, 1) void moment_block_kernel(const Mom
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) st[kt][ct] = stn[kt][ct];
         }
+        rn = rnn;
+        m = mn;
       }
     }
   }
