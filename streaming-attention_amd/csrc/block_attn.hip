@@ -726,7 +726,30 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     have = nxt_have;
   }
 
-  // ---- epilogue: the remaining moment partials, normalise, store ----
+  // ---- epilogue: the remaining moment partials, two pairs in flight (the batch loop's registers are
+  //      free; each pair still added in order: pair p's values are parked while p + 1's load is issued),
+  //      normalise, store ----
+  for (; pairs_done + 1 < n_pairs; pairs_done += 2) {
+    pair_load(pairs_done);
+    const float d0 = pair_d;
+    floatx4 n0[DVT];
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) n0[ct] = pair_n[ct];
+    pair_load(pairs_done + 1);
+    const float d1 = pair_d;
+    pair_d = d0;
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) {
+      const floatx4 t = pair_n[ct];
+      pair_n[ct] = n0[ct];
+      n0[ct] = t;
+    }
+    pair_add(pairs_done);
+    pair_d = d1;
+#pragma unroll
+    for (int ct = 0; ct < DVT; ++ct) pair_n[ct] = n0[ct];
+    pair_add(pairs_done + 1);
+  }
   for (; pairs_done < n_pairs; ++pairs_done) {
     pair_load(pairs_done);
     pair_add(pairs_done);
