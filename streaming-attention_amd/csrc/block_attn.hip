@@ -684,12 +684,15 @@ __global__ __launch_bounds__(256, block_occupancy(DP, DVT, RS)) void block_attn_
     }
   };
 
-  if (p_cur < p_end) fill();  // the first list chunk
-  __syncthreads();
   bool cur_node = n_a == 0;
   int cur_off = cur_node ? 0 : kstart;
+  // the first batch of the tile's own keys needs no list: its rows are in flight while the list's
+  // chain of loads (tile list, node metadata, item indices) runs
+  if (!cur_node) prefetch(false, cur_off);
+  if (p_cur < p_end) fill();  // the first list chunk
+  __syncthreads();
   bool have = n_a > 0 || llen > 0;
-  if (have) prefetch(cur_node, cur_off);
+  if (have && cur_node) prefetch(true, cur_off);
   int pairs_done = 0;
   for (int b = 0; have; ++b) {
     __syncthreads();  // every wave is done with the staging buffers of the previous batch
