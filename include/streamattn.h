@@ -329,23 +329,25 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
 /*
  * Merge nodes of several levels of a levels plan in one launch (K3): the compress calls of
  * MergeReduceCoreset._insert_level's cascade (streaming_taylor_coreset_attention.py:396-411, each call
- * :413-467), the same node values as sta_compress_nodes run level by level.  Each node is computed by
- * one wave; a workgroup of `waves` waves (1, 2, 4, 8 or 16) runs `phases` rounds with a barrier after
- * each, so a round may read the nodes of the rounds before it:
- *   node_table [n_groups][phases][waves]: the node each wave computes in each round (-1: none), the
- *     same for every head (grid n_groups x bh).  A node's children must be nodes of an earlier launch or
- *     of an earlier round of the same workgroup (e.g. a subtree: 2^(phases-1) nodes of one level, then
- *     their parents, ..., its root);
+ * :413-467), the same node values as sta_compress_nodes run level by level.  A workgroup of `groups`
+ * thread groups runs `steps` steps with a barrier after each, so a step may read the nodes of the
+ * steps before it; in a step each group computes one node:
+ *   group_threads 256: groups (<= 4) of 256 threads in lockstep (every group takes the same number of
+ *     workgroup barriers per step, whatever its call does); 64: groups (<= 16) of one wave each;
+ *   node_table [n_groups][steps][groups]: the node each group computes in each step (-1: none), the
+ *     same for every head (grid n_groups x bh).  A node's children must be nodes of an earlier launch
+ *     or of an earlier step of the same workgroup (e.g. a subtree: the nodes of one level, then their
+ *     parents, ..., its root);
  *   node_level, anc_levels, level_scores: as sta_compress_nodes' later launches (merges at levels 1 ..
  *     anc_levels read the scores their level-0 calls wrote).
- * Other arguments as sta_compress_nodes.  LDS: the call's arrays for every wave, waves * (4 M + 256)
- * floats with M = max_in rounded up to 4 (float64: waves * (5 M + 512)); STA_ERR_UNSUPPORTED above
+ * Other arguments as sta_compress_nodes.  LDS: the call's arrays for every group, groups * (4 M + 256)
+ * floats with M = max_in rounded up to 4 (float64: groups * (5 M + 512)); STA_ERR_UNSUPPORTED above
  * 160 KiB.
  */
 int sta_compress_merges(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* node_table,
-                        int n_groups, int phases, int waves, const int32_t* node_desc, int n_nodes, int cap,
-                        const void* dirs, const void* unif, const int32_t* perms, int n_draws, int max_in,
-                        int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
+                        int n_groups, int steps, int groups, int group_threads, const int32_t* node_desc,
+                        int n_nodes, int cap, const void* dirs, const void* unif, const int32_t* perms, int n_draws,
+                        int max_in, int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
                         float* level_scores, void* stream);
 
 /*

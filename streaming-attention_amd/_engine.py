@@ -42,13 +42,17 @@ ANCESTOR_LEVELS = int(os.environ.get("STA_ANCESTOR_LEVELS", "3"))
 # extra chains cost the level-0 calls more (1x32x65536, d = 64 fp32: 0.393 -> 0.375 ms; 4x32x16384,
 # d = 16: 0.26 -> 0.30 ms)
 ANCESTOR_MIN_ROW_BYTES = 256
-# Levels plans, STA_MERGE_WAVES=W > 0: the merge levels as subtrees of up to W nodes per workgroup, one
-# wave per node (sta_compress_merges: log2(W) + 1 levels per launch; W = 16 puts 32 x 65536 tokens'
-# 8 merge levels in 2 launches) instead of one launch per level; the nodes are the same bit for bit.
-# Off by default: a node's rank sort on one wave is 4x longer, and the top levels have one node per
-# head (32 x 65536 tokens: 3 launches in 0.45 ms against 9 in 0.375 ms; 4 x 32 x 16384: 3 in 0.248 ms
-# against 8 in 0.253 ms).
-MERGE_WAVES = int(os.environ.get("STA_MERGE_WAVES", "0"))
+# Levels plans: the merge levels as subtree launches (sta_compress_merges): a workgroup takes up to 16
+# nodes of one level and the nodes above them, computing a level's nodes in steps with a barrier between
+# (32 x 65536 tokens: 8 merge levels in 2 launches instead of 8).  "group": four 256-thread groups in
+# lockstep, one node each per step; "wave": one wave per node, 16 waves; "auto": waves for compress calls
+# of at most 128 items (a wave sorts them in a quarter of the work of 256), groups above
+# (32 x 65536 tokens, 256-item calls: 9 launches 372-379 us, groups 355-372, waves 418-432;
+# 4 x 32 x 16384, 128-item calls: 9 launches 258-261 us, groups 271-281, waves 238-250);
+# "0": sta_compress_nodes level by level.  The nodes are the same bit for bit either way.
+MERGE_LAUNCHES = os.environ.get("STA_MERGE_LAUNCHES", "auto")
+MERGE_GROUPS = int(os.environ.get("STA_MERGE_GROUPS", "4"))  # 256-thread groups per workgroup
+MERGE_BOTTOM = int(os.environ.get("STA_MERGE_BOTTOM", "16"))  # nodes of a subtree's lowest level
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
 
@@ -385,13 +389,17 @@ def prefill(
                 anc_d, level_d = _on_device(("anc", anc_levels) + pkey, dev,
                                             lambda: (_i32(anc, dev), _i32(level_of, dev)))
         merge_l = []
-        if MERGE_WAVES > 0 and plan.mode == _plan.MODE_LEVELS:
+        if MERGE_LAUNCHES in ("group", "wave", "auto") and plan.mode == _plan.MODE_LEVELS:
+            wave = MERGE_LAUNCHES == "wave" or (MERGE_LAUNCHES == "auto" and dr.max_in <= 128)
+            gt = 64 if wave else 256
+
             def build_merges():
-                launches = _plan.merge_launches(plan, dr.max_in, f64, MERGE_WAVES)
+                launches = _plan.merge_launches(plan, dr.max_in, f64, group_threads=gt, groups=MERGE_GROUPS,
+                                                bottom=MERGE_BOTTOM)
                 _plan.check_merge_launches(plan, desc, launches)
                 return [(ln, _i32(ln.table, dev)) for ln in launches]
 
-            merge_l = _on_device(("merges", MERGE_WAVES, dr.max_in, f64) + pkey, dev, build_merges)
+            merge_l = _on_device(("merges", gt, MERGE_GROUPS, MERGE_BOTTOM, dr.max_in, f64) + pkey, dev, build_merges)
 
     lrows, lld, _ = _native.moment_partials_layout(n, dv)
     low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
@@ -487,7 +495,7 @@ def prefill(
                 def k3_merges(ln=ln, table_d=table_d):
                     st = lib.sta_compress_merges(
                         (score_keys if f64 else k3).data_ptr(), _native.STA_F64 if f64 else dt, bh, n, d,
-                        table_d.data_ptr(), ln.groups, ln.phases, ln.waves, desc_d.data_ptr(),
+                        table_d.data_ptr(), ln.workgroups, ln.steps, ln.groups, ln.group_threads, desc_d.data_ptr(),
                         plan.n_nodes, plan.cap, dirs_d.data_ptr(), unif_d.data_ptr(), perms_d.data_ptr(),
                         dr.dirs.shape[1], dr.max_in, node_src.data_ptr(), node_w.data_ptr(),
                         _native.ptr(level_d), anc_levels, _native.ptr(lscore), k3_stream)

@@ -73,8 +73,8 @@ _SIGNATURES = {
     ),
     "sta_compress_merges": (
         _i32,
-        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32, _i32,
-         _c_p, _c_p, _c_p, _i32, _c_p, _c_p],  # ... node_src node_w node_level anc_levels level_scores stream
+        [_c_p, _i32, _i64, _i64, _i32, _c_p, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p, _c_p, _c_p, _i32,
+         _i32, _c_p, _c_p, _c_p, _i32, _c_p, _c_p],  # k .. table n_groups steps groups group_threads desc ...
     ),
     "sta_segment_mean": (_i32, [_c_p, _c_p, _i32, _i64, _i64, _i32, _i32, _i32, _i32, _i64, _c_p, _c_p, _c_p]),
     "sta_block_attention": (

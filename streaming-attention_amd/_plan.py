@@ -1132,61 +1132,71 @@ def compress_region_floats(max_in: int, f64: bool) -> int:
 
 @dataclass
 class MergeLaunch:
-    """One sta_compress_merges launch: table int32 [groups, phases, waves] of node ids (-1: idle)."""
+    """One sta_compress_merges launch: table int32 [workgroups, steps, groups] of node ids (-1: idle),
+    groups of group_threads threads (64: one wave per node; 256: lockstep groups)."""
     table: np.ndarray
-    waves: int
-    phases: int
+    groups: int
+    steps: int
     levels: Tuple[int, int]  # first and last tree level it computes
+    group_threads: int = 256
 
     @property
-    def groups(self) -> int:
+    def workgroups(self) -> int:
         return int(self.table.shape[0])
 
 
-def merge_launches(plan: NodePlan, max_in: int, f64: bool, max_waves: int = 16,
-                   lds_bytes: int = 160 * 1024) -> List[MergeLaunch]:
-    """The merge levels of a levels plan as sta_compress_merges launches of subtrees: a launch starting at
-    level l0 gives each workgroup W = 2^k waves (at most max_waves, within lds_bytes of LDS) and the W
-    consecutive nodes (l0, j) of its group, then in round r the W >> r nodes (l0 + r, j) above them, for
-    k + 1 levels (fewer at the top), so every node's children are computed by an earlier launch or round
-    of its own workgroup.  Empty for plans without merge levels."""
+def merge_launches(plan: NodePlan, max_in: int, f64: bool, group_threads: int = 256, groups: int = 4,
+                   bottom: int = 16, lds_bytes: int = 160 * 1024) -> List[MergeLaunch]:
+    """The merge levels of a levels plan as sta_compress_merges launches of subtrees.  A launch starting
+    at level l0 gives each workgroup B = 2^k consecutive nodes (l0, j) (at most `bottom`) and the B >> r
+    nodes (l0 + r, j) above them for k + 1 levels (fewer at the top); its G groups take a level's nodes
+    G at a time, one step each (64-thread groups: G = B, one step per level; 256-thread groups: G <=
+    `groups`, at most 1024 threads).  A workgroup's LDS (G call regions) stays within lds_bytes.  Every
+    node's children are then computed by an earlier launch or an earlier step of its own workgroup.
+    Empty for plans without merge levels."""
     if plan.mode != MODE_LEVELS or len(plan.batches) < 2:
         return []
     region = compress_region_floats(max_in, f64) * 4
-    cap_w = 1
-    while cap_w * 2 <= max_waves and cap_w * 2 * region <= lds_bytes:
-        cap_w *= 2
+    cap_g = 1
+    limit = min(16, bottom) if group_threads == 64 else min(groups, 1024 // group_threads)
+    while cap_g * 2 <= limit and cap_g * 2 * region <= lds_bytes:
+        cap_g *= 2
     counts = [len(b) for b in plan.batches]
     launches: List[MergeLaunch] = []
     l0 = 1
     while l0 < len(counts):
-        w = 1
-        while w < min(cap_w, counts[l0]):
-            w *= 2
-        depth = min(w.bit_length(), len(counts) - l0)
-        groups = -(-counts[l0] // w)
-        table = np.full((groups, depth, w), -1, dtype=np.int32)
+        b = 1
+        while b < min(bottom if group_threads != 64 else cap_g, counts[l0]):
+            b *= 2
+        g = b if group_threads == 64 else min(cap_g, b)
+        depth = min(b.bit_length(), len(counts) - l0)
+        per_level = [-(-(b >> r) // g) for r in range(depth)]
+        n_wg = -(-counts[l0] // b)
+        table = np.full((n_wg, sum(per_level), g), -1, dtype=np.int32)
+        base = 0
         for r in range(depth):
-            per = w >> r
+            per = b >> r
             for j in range(counts[l0 + r]):
-                table[j // per, r, j % per] = plan.batches[l0 + r][j]
-        launches.append(MergeLaunch(table, w, depth, (l0, l0 + depth - 1)))
+                q = j % per
+                table[j // per, base + q // g, q % g] = plan.batches[l0 + r][j]
+            base += per_level[r]
+        launches.append(MergeLaunch(table, g, int(sum(per_level)), (l0, l0 + depth - 1), group_threads))
         l0 += depth
     return launches
 
 
 def check_merge_launches(plan: NodePlan, desc: np.ndarray, launches: List[MergeLaunch]) -> None:
     """Every merge node exactly once, after both its children (raw nodes: the first launch; merges: an
-    earlier launch, or an earlier round of the same workgroup).  Raises ValueError otherwise."""
+    earlier launch, or an earlier step of the same workgroup).  Raises ValueError otherwise."""
     done = np.zeros(plan.n_nodes, dtype=bool)
     done[plan.batches[0]] = True
     seen = np.zeros(plan.n_nodes, dtype=bool)
     for ln in launches:
         before = done.copy()
-        for g in range(ln.groups):
+        for w in range(ln.workgroups):
             mine = before.copy()
-            for r in range(ln.phases):
-                nodes = [int(x) for x in ln.table[g, r] if x >= 0]
+            for r in range(ln.steps):
+                nodes = [int(x) for x in ln.table[w, r] if x >= 0]
                 for node in nodes:
                     if desc[node, 0] != KIND_MERGE or seen[node]:
                         raise ValueError(f"merge launch lists node {node} twice or a raw node")

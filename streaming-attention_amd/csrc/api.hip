@@ -673,9 +673,9 @@ int sta_compress_nodes(const void* k, int dtype, int64_t bh, int64_t n, int d, c
 }
 
 int sta_compress_merges(const void* k, int dtype, int64_t bh, int64_t n, int d, const int32_t* node_table,
-                        int n_groups, int phases, int waves, const int32_t* node_desc, int n_nodes, int cap,
-                        const void* dirs, const void* unif, const int32_t* perms, int n_draws, int max_in,
-                        int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
+                        int n_groups, int steps, int groups, int group_threads, const int32_t* node_desc,
+                        int n_nodes, int cap, const void* dirs, const void* unif, const int32_t* perms, int n_draws,
+                        int max_in, int32_t* node_src, float* node_w, const int32_t* node_level, int anc_levels,
                         float* level_scores, void* stream) {
   size_t smem = 0;
   int st = STA_OK;
@@ -684,15 +684,24 @@ int sta_compress_merges(const void* k, int dtype, int64_t bh, int64_t n, int d, 
                                             anc_levels, level_scores, &smem, &st);
   if (st == STA_OK && anc_levels > 0 && !node_level) st = STA_ERR_ARG;
   if (st != STA_OK) return st;
-  if (phases <= 0 || waves <= 0 || waves > 16 || (waves & (waves - 1)) != 0) return STA_ERR_ARG;
+  if (group_threads != 64 && group_threads != sta::CMP_THREADS) return STA_ERR_ARG;
+  if (steps <= 0 || groups <= 0 || groups * group_threads > 1024) return STA_ERR_ARG;
   if (n_groups <= 0) return STA_OK;
   const int region = sta::cmp_smem_floats(max_in, dtype == STA_F64);
-  smem = sizeof(float) * static_cast<size_t>(region) * static_cast<size_t>(waves);
+  smem = sizeof(float) * static_cast<size_t>(region) * static_cast<size_t>(groups);
   if (smem > 160 * 1024) return STA_ERR_UNSUPPORTED;
-  st = lds_limit(reinterpret_cast<const void*>(sta::compress_merge_kernel), smem);
+  const void* fn = group_threads == 64 ? reinterpret_cast<const void*>(sta::compress_merge_kernel<64>)
+                                       : reinterpret_cast<const void*>(sta::compress_merge_kernel<sta::CMP_THREADS>);
+  st = lds_limit(fn, smem);
   if (st != STA_OK) return st;
-  hipLaunchKernelGGL(sta::compress_merge_kernel, dim3(static_cast<unsigned>(n_groups), static_cast<unsigned>(bh)),
-                     dim3(64 * waves), smem, static_cast<hipStream_t>(stream), a, node_table, phases, waves, region);
+  const dim3 grid(static_cast<unsigned>(n_groups), static_cast<unsigned>(bh));
+  const dim3 block(static_cast<unsigned>(group_threads * groups));
+  if (group_threads == 64)
+    hipLaunchKernelGGL(sta::compress_merge_kernel<64>, grid, block, smem, static_cast<hipStream_t>(stream), a,
+                       node_table, steps, groups, region);
+  else
+    hipLaunchKernelGGL(sta::compress_merge_kernel<sta::CMP_THREADS>, grid, block, smem,
+                       static_cast<hipStream_t>(stream), a, node_table, steps, groups, region);
   return check_launch();
 }
 

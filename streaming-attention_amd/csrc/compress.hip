@@ -216,11 +216,30 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
 // instruction order, so a code-motion barrier stands in for the workgroup barrier).
 struct BlockGroup {
   static constexpr int threads = CMP_THREADS;
+  static constexpr int row_batch = 8;  // 16-byte units of a gathered key row in flight (projection_scores2)
   int tid;
   __device__ __forceinline__ void sync() const { __syncthreads(); }
 };
+// CMP_THREADS threads of a larger workgroup computing one compress call, in lockstep with the other
+// groups: sync() is the workgroup barrier, counted, so that every group can pad its step to the same
+// number of barriers (CMP_NODE_SYNCS) whatever path its call took.
+struct LockGroup {
+  static constexpr int threads = CMP_THREADS;
+  static constexpr int row_batch = 4;  // the registers of a 1024-thread workgroup
+  int tid;
+  int* syncs;
+  __device__ __forceinline__ void sync() const {
+    __syncthreads();
+    ++*syncs;
+  }
+};
+// Workgroup barriers a compress call takes on any path: none (refused descriptor), 1 (the input list
+// gathered: copy / permutation calls) or 3 (and the two of rank_sort / rank_sort64: sorted_pair).
+constexpr int CMP_NODE_SYNCS = 3;
+
 struct WaveGroup {
   static constexpr int threads = 64;
+  static constexpr int row_batch = 4;
   int tid;  // lane
   __device__ __forceinline__ void sync() const {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -498,11 +517,10 @@ __device__ __forceinline__ void compress_node(const CompressArgs& a, const int n
       const int i1 = i + CMP_THREADS;
       const bool two = i1 < n_in;
       float s0, s1;
-      // (a wave computing a node alone keeps 4 units of each row in flight: its registers are shared
-      // by every round of the merge launch)
-      projection_scores2<G::threads == 64 ? 4 : 8>(a.k, (bh * a.n + src_s[i]) * a.d, a.k,
-                                                   (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d, a.dtype, vec,
-                                                   dir_s, s0, s1);
+      // (groups of a merge launch keep 4 units of each row in flight: their registers are shared by
+      // every step of the launch)
+      projection_scores2<G::row_batch>(a.k, (bh * a.n + src_s[i]) * a.d, a.k,
+                                       (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d, a.dtype, vec, dir_s, s0, s1);
       key_s[i] = s0;
       if (two) key_s[i1] = s1;
     }
@@ -534,22 +552,31 @@ __global__ __launch_bounds__(CMP_THREADS) void compress_kernel(const CompressArg
   compress_node<ANC>(a, a.batch[blockIdx.x], blockIdx.y, BlockGroup{static_cast<int>(threadIdx.x)}, cmp_smem);
 }
 
-// Merge nodes of several tree levels in one launch: workgroup x of sequence y runs `phases` rounds; in
-// round r its wave w computes node table[(x * phases + r) * waves + w] (-1: none) alone, then the
-// workgroup meets at a barrier, so a round may read what the rounds before it wrote (the children of
-// a subtree of merges: 2^(phases-1) nodes of the lowest level, then their parents, ...).  Each wave
-// has its own LDS region of region_floats floats.
-__global__ __launch_bounds__(1024) void compress_merge_kernel(const CompressArgs a, const int32_t* table, int phases,
-                                                              int waves, int region_floats) {
+// Merge nodes of several tree levels in one launch: workgroup x of sequence y runs `steps` steps; in
+// step r its group g (GT threads: one wave, or CMP_THREADS threads in lockstep with the other groups)
+// computes node table[(x * steps + r) * groups + g] (-1: none), then the workgroup meets at a barrier,
+// so a step may read what the steps before it wrote (a subtree of merges: the nodes of its lowest
+// level, then their parents, ...).  Each group has its own LDS region of region_floats floats.
+template <int GT>
+__global__ __launch_bounds__(1024) void compress_merge_kernel(const CompressArgs a, const int32_t* table, int steps,
+                                                              int groups, int region_floats) {
   extern __shared__ __align__(16) float cmp_smem[];
-  const int wave = threadIdx.x >> 6;
-  const WaveGroup g{static_cast<int>(threadIdx.x & 63)};
-  float* smem = cmp_smem + wave * region_floats;
-  const int32_t* t = table + static_cast<int64_t>(blockIdx.x) * phases * waves + wave;
-  for (int r = 0; r < phases; ++r) {
-    const int node = __builtin_amdgcn_readfirstlane(t[r * waves]);
-    if (node >= 0 && node < a.n_nodes) compress_node<false>(a, node, blockIdx.y, g, smem);
-    __syncthreads();  // this round's node lists (global memory) before the next round reads them
+  const int grp = threadIdx.x / GT;
+  const int gtid = threadIdx.x - grp * GT;
+  float* smem = cmp_smem + grp * region_floats;
+  const int32_t* t = table + static_cast<int64_t>(blockIdx.x) * steps * groups + grp;
+  for (int r = 0; r < steps; ++r) {
+    const int node = __builtin_amdgcn_readfirstlane(t[r * groups]);
+    const bool real = node >= 0 && node < a.n_nodes;
+    if constexpr (GT == 64) {
+      if (real) compress_node<false>(a, node, blockIdx.y, WaveGroup{gtid}, smem);
+    } else {
+      // every group takes exactly CMP_NODE_SYNCS workgroup barriers per step (padding after its call)
+      int syncs = 0;
+      if (real) compress_node<false>(a, node, blockIdx.y, LockGroup{gtid, &syncs}, smem);
+      for (int k = __builtin_amdgcn_readfirstlane(syncs); k < CMP_NODE_SYNCS; ++k) __syncthreads();
+    }
+    __syncthreads();  // this step's node lists (global memory) and LDS reads before the next step
   }
 }
 

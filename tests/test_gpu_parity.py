@@ -377,9 +377,9 @@ def test_cpu_inputs_round_trip():
                                                       (700, 8, 16, torch.float32, "random", False),
                                                       (900, 24, 64, torch.float64, "sorted_pair", False)])
 def test_merge_launches_match_level_launches(n, d, block, dtype, comp, anc, monkeypatch):
-    """The merge levels as subtree launches (sta_compress_merges, one wave per node) give every node of
-    every head bit for bit as the launches level by level, for workgroups of 16, 4 and 1 waves, and the
-    oracle's cascade."""
+    """The merge levels as subtree launches (sta_compress_merges) give every node of every head bit for
+    bit as the launches level by level: lockstep 256-thread groups (4 groups under 16 nodes, 2 under 4,
+    1 under 2) and one wave per node (16 and 4 waves); and the oracle's cascade."""
     print(f"merge launches n={n} d={d} block={block} {dtype} {comp} anc={anc}", flush=True)
     q, k, v = orc.make_data((3,), n, d, 8, radius=1.0, data="unit_ball", seed=n + d + 1)
     # float64: float32 inputs with the float64 keys scored in fp64 (score_keys), as a float64 caller's
@@ -388,17 +388,20 @@ def test_merge_launches_match_level_launches(n, d, block, dtype, comp, anc, monk
     monkeypatch.setattr(_engine, "ANCESTOR_MIN_ROW_BYTES", 0)
     monkeypatch.setattr(_engine, "ANCESTOR_SCORES", anc)
     res = {}
-    for waves in (0, 16, 4, 1):
-        monkeypatch.setattr(_engine, "MERGE_WAVES", waves)
+    variants = [("0", 4, 16), ("group", 4, 16), ("group", 2, 4), ("group", 1, 2), ("wave", 4, 16), ("wave", 4, 4)]
+    for mode, groups, bottom in variants:
+        monkeypatch.setattr(_engine, "MERGE_LAUNCHES", mode)
+        monkeypatch.setattr(_engine, "MERGE_GROUPS", groups)
+        monkeypatch.setattr(_engine, "MERGE_BOTTOM", bottom)
         r = _engine.prefill(q.to(DEV), k.to(DEV), v.to(DEV), degree=2, block=block, scale=0.5, semantics="levels",
                             compressor=comp, seed=7, score_keys=None if k64 is None else k64.to(DEV).contiguous())
         torch.cuda.synchronize()
-        res[waves] = (r.node_src.cpu(), r.node_w.cpu(), r.out.float().cpu(), r.plan)
-    base = res[0]
-    for waves in (16, 4, 1):
-        src, w, out, _ = res[waves]
-        assert torch.equal(src, base[0]) and torch.equal(w, base[1]), f"{waves} waves"
-        assert torch.equal(out, base[2]), f"{waves} waves"
+        res[(mode, groups, bottom)] = (r.node_src.cpu(), r.node_w.cpu(), r.out.float().cpu(), r.plan)
+    base = res[variants[0]]
+    for key in variants[1:]:
+        src, w, out, _ = res[key]
+        assert torch.equal(src, base[0]) and torch.equal(w, base[1]), key
+        assert torch.equal(out, base[2]), key
     plan = base[3]
     if dtype != torch.float64:  # the float64 cascade is pinned by the float64 selection tests
         for h in range(3):
@@ -411,7 +414,7 @@ def test_merge_launches_match_level_launches(n, d, block, dtype, comp, anc, monk
             for node in range(plan.n_nodes):
                 size = int(plan.meta[node, 0])
                 c = state.calls[int(plan.desc[node, 6])]
-                assert np.array_equal(res[16][0][h, node, :size].numpy(), c.src_out), f"head {h} node {node}"
+                assert np.array_equal(res[variants[1]][0][h, node, :size].numpy(), c.src_out), f"head {h} node {node}"
 
 
 @pytest.mark.parametrize("n,d,block,dtype,comp", [(3000, 16, 64, torch.float32, "sorted_pair"),

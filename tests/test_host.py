@@ -73,14 +73,15 @@ def test_library_rejects_bad_arguments_without_touching_a_device():
     assert lib.sta_compress_nodes(None, 0, 1, 1, 1, None, 1, None, 1, 1, None, None, None, 0, 2, None, None,
                                   None, None, 0, None, None) == _native.STA_ERR_ARG
     # merge launches: the compress_nodes checks, then the round layout and the LDS of every wave
-    def merges(dtype=0, phases=2, waves=4, max_in=256, k=16):
-        return lib.sta_compress_merges(k, dtype, 1, 64, 8, 16, 1, phases, waves, 16, 3, 2, None, None, None, 0,
+    def merges(dtype=0, steps=2, groups=4, gt=64, max_in=256, k=16):
+        return lib.sta_compress_merges(k, dtype, 1, 64, 8, 16, 1, steps, groups, gt, 16, 3, 2, None, None, None, 0,
                                        max_in, 16, 16, None, 0, None, None)
     assert merges(k=None) == _native.STA_ERR_ARG
     assert merges(dtype=9) == _native.STA_ERR_DTYPE
-    assert merges(phases=0) == _native.STA_ERR_ARG
-    assert merges(waves=3) == _native.STA_ERR_ARG and merges(waves=32) == _native.STA_ERR_ARG
-    assert merges(waves=16, max_in=4096) == _native.STA_ERR_UNSUPPORTED
+    assert merges(steps=0) == _native.STA_ERR_ARG and merges(groups=0) == _native.STA_ERR_ARG
+    assert merges(gt=128) == _native.STA_ERR_ARG and merges(groups=17) == _native.STA_ERR_ARG
+    assert merges(gt=256, groups=5) == _native.STA_ERR_ARG
+    assert merges(groups=16, max_in=4096) == _native.STA_ERR_UNSUPPORTED
     assert lib.sta_segment_mean(1, 1, 0, 1, 10, 4, 4, 8, 3, 0, 1, 1, None) == _native.STA_ERR_SHAPE
     # flash: null pointers, D beyond the limit, strides not whole 4-element units, misaligned rows
     assert lib.sta_flash_attention(None, 16, 16, 0, 1, 8, 4, 4, 4, 4, 1.0, 16, 0, None) == _native.STA_ERR_ARG
@@ -549,27 +550,36 @@ def test_static_scratch_owner_registry():
     assert reg.holder(0) == (2, 0x11)
 
 
-@pytest.mark.parametrize("n,block,waves", [(64 * 256, 64, 16), (64 * 37, 64, 16), (5000, 16, 4), (4096, 256, 1),
-                                            (128 * 1000, 128, 8)])
-def test_merge_launches(n, block, waves):
+@pytest.mark.parametrize("n,block,gt,groups,bottom", [(64 * 256, 64, 256, 4, 16), (64 * 37, 64, 256, 4, 16),
+                                                     (5000, 16, 256, 2, 4), (4096, 256, 256, 1, 1),
+                                                     (128 * 1000, 128, 256, 4, 8), (64 * 256, 64, 64, 0, 16),
+                                                     (5000, 16, 64, 0, 4), (128 * 1000, 128, 64, 0, 8)])
+def test_merge_launches(n, block, gt, groups, bottom):
     """Subtree launches of a levels plan: every merge node once, after its children (an earlier launch
-    or an earlier round of its own workgroup); log2(waves) + 1 levels per launch; the LDS of a
-    workgroup's waves limits their number."""
+    or an earlier step of its own workgroup); log2(bottom) + 1 levels per launch, a level's nodes taken
+    `groups` at a time by 256-thread groups (one step per level with one wave per node); the LDS of a
+    workgroup's groups limits their number."""
     plan = _plan.levels_plan(n, block, "sorted_pair")
     _, desc = _plan.draws_for(plan, (0,), 8, "sorted_pair")
-    ls = _plan.merge_launches(plan, block, False, waves)
+    ls = _plan.merge_launches(plan, block, False, group_threads=gt, groups=groups, bottom=bottom)
     _plan.check_merge_launches(plan, desc, ls)
     merge_levels = len(plan.batches) - 1
-    assert sum(ln.phases for ln in ls) == merge_levels
-    assert ls[0].waves == min(waves, 1 << (len(plan.batches[1]) - 1).bit_length())
-    assert len(ls) == -(-merge_levels // waves.bit_length()) or ls[-1].waves < waves
-    # waves limited by LDS: 4096-item calls need 66 KiB each
-    assert _plan.merge_launches(_plan.levels_plan(8192 * 4, 4096, "sorted_pair"), 4096, False, 16)[0].waves == 2
-    # a schedule that computes a parent in the round of its children, or leaves a merge out, is refused
-    bad = [_plan.MergeLaunch(ln.table.copy(), ln.waves, ln.phases, ln.levels) for ln in ls]
-    if bad[0].phases > 1:
-        t = bad[0].table
-        t[0, 1, 0], t[0, 0, 0] = t[0, 0, 0], t[0, 1, 0]
+    assert sum(ln.levels[1] - ln.levels[0] + 1 for ln in ls) == merge_levels
+    b0 = min(bottom, 1 << (len(plan.batches[1]) - 1).bit_length())
+    assert ls[0].levels[1] - ls[0].levels[0] + 1 == min(b0.bit_length(), merge_levels)
+    assert ls[0].groups == (b0 if gt == 64 else min(groups, b0))
+    assert all(ln.groups * ln.group_threads <= 1024 for ln in ls)
+    if gt == 64:
+        assert all(ln.steps == ln.levels[1] - ln.levels[0] + 1 for ln in ls)
+    # groups limited by LDS: 4096-item calls need 66 KiB each
+    big = _plan.levels_plan(8192 * 4, 4096, "sorted_pair")
+    assert _plan.merge_launches(big, 4096, False, group_threads=gt, groups=4, bottom=16)[0].groups == 2
+    # a schedule that computes a parent in the step of its children, or leaves a merge out, is refused
+    bad = [_plan.MergeLaunch(ln.table.copy(), ln.groups, ln.steps, ln.levels, ln.group_threads) for ln in ls]
+    t = bad[0].table
+    last = t.shape[1] - 1
+    if last > 0:
+        t[0, last, 0], t[0, 0, 0] = t[0, 0, 0], t[0, last, 0]
         with pytest.raises(ValueError):
             _plan.check_merge_launches(plan, desc, bad)
     with pytest.raises(ValueError):
