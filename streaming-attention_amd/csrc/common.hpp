@@ -53,6 +53,16 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Buffer resource of raw memory at p (stride 0, the largest record count, the gfx9 data-format word):
+// a buffer access addresses base + a per-lane 32-bit offset + a uniform 32-bit offset, so a loop
+// whose per-lane offsets are invariant and whose uniform offset advances needs no per-lane 64-bit
+// address arithmetic.  Callers keep every offset sum below 2^32 and inside their own allocation.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, -1, 0x00020000);
+}
+// the cache-policy operand of a non-temporal buffer store
+constexpr int BUF_NT = 2;
+
 // Split-bf16 products (bf16 matrix cores at 16x the fp32 rate).  An fp32 value x is carried as
 // hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even: x - hi is exact in fp32 and
 // |x - hi - lo| <= 2^-9 |x - hi| <= 2^-18 |x|.  A product is taken as hi.hi' + hi.lo' + lo.hi' (bf16

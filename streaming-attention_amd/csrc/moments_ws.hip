@@ -98,16 +98,26 @@ template <bool DBIG, int ES, int CG, int STG>
 struct WsSlots {
   static constexpr int QV = WsStage<DBIG, ES, CG, STG>::QV;
   static constexpr int VV = WsStage<DBIG, ES, CG, STG>::VV;
+  // *_rel: byte offset of the unit from the start of the chunk's first row (the unit's token times the
+  // row stride plus its offset in the row), so that a chunk inside the sequence loads from one uniform
+  // row address plus these loop-invariant offsets
   int q_tok[QV];
-  uint32_t q_off[QV];
+  uint32_t q_rel[QV];
   int q_lds[QV];
   bool q_use[QV];
-  uint32_t k_off[QV];
+  uint32_t k_rel[QV];
   int k_dim[QV];  // -1: unused
-  uint32_t v_off[VV];
+  uint32_t v_rel[VV];
   int v_col[VV];  // -1: unused
   int sidx;       // this thread's index among the staging threads
 };
+
+// token of staged key / value unit j (PAIR16: unit 0's two half units, j = 0, 1)
+template <bool DBIG, int ES, int CG, int STG>
+__device__ __forceinline__ int ws_kv_tok(int sidx, int j) {
+  constexpr bool pair = WsStage<DBIG, ES, CG, STG>::PAIR || WsStage<DBIG, ES, CG, STG>::PAIR16;
+  return pair ? 2 * (sidx & 15) + j : sidx & (MOM_C - 1);
+}
 
 template <bool DBIG, int ES, int CG, int STG>
 __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a, int col0, int sidx) {
@@ -117,6 +127,7 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
   const int tid = sidx;
   sl.sidx = sidx;
   const int uq = a.d / epu;
+  const uint32_t qrow = static_cast<uint32_t>(a.ldk * ES), vrow = static_cast<uint32_t>(a.ldv * ES);
   constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
   constexpr bool PAIR16 = WsStage<DBIG, ES, CG, STG>::PAIR16;
 #pragma unroll
@@ -125,71 +136,116 @@ __device__ __forceinline__ WsSlots<DBIG, ES, CG, STG> ws_slots(const MomArgs& a,
     const int t = e / uq, u = e - t * uq;
     sl.q_use[j] = t < MOM_C;
     sl.q_tok[j] = min(t, MOM_C - 1);
-    sl.q_off[j] = static_cast<uint32_t>(u * 16);
+    sl.q_rel[j] = static_cast<uint32_t>(sl.q_tok[j]) * qrow + static_cast<uint32_t>(u * 16);
     sl.q_lds[j] = t * LDQ + u * epu;
+    const uint32_t ktok = static_cast<uint32_t>(ws_kv_tok<DBIG, ES, CG, STG>(tid, j));
     if constexpr (PAIR16) {  // half unit tid >> 4: elements 4 hu .. 4 hu + 3
       const int hu = tid >> 4;
-      sl.k_off[j] = static_cast<uint32_t>(min(hu, a.d / 4 - 1) * 8);
+      sl.k_rel[j] = ktok * qrow + static_cast<uint32_t>(min(hu, a.d / 4 - 1) * 8);
       sl.k_dim[j] = 4 * hu < a.d ? 4 * hu : -1;
     } else {
       const int uk = PAIR ? tid >> 4 : e >> 5;
-      sl.k_off[j] = static_cast<uint32_t>(min(uk, uq - 1) * 16);
+      sl.k_rel[j] = ktok * qrow + static_cast<uint32_t>(min(uk, uq - 1) * 16);
       sl.k_dim[j] = uk < uq ? uk * epu : -1;
     }
   }
 #pragma unroll
   for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j) {
+    const uint32_t vtok = static_cast<uint32_t>(ws_kv_tok<DBIG, ES, CG, STG>(tid, j));
     if constexpr (PAIR16) {
       const int hu = tid >> 4;
-      sl.v_off[j] = static_cast<uint32_t>((col0 + min(4 * hu, CG - 4)) * ES);
+      sl.v_rel[j] = vtok * vrow + static_cast<uint32_t>((col0 + min(4 * hu, CG - 4)) * ES);
       sl.v_col[j] = 4 * hu < CG ? 4 * hu : -1;
     } else {
       const int uv = PAIR ? tid >> 4 : (tid + STG * j) >> 5;
-      sl.v_off[j] = static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
+      sl.v_rel[j] = vtok * vrow + static_cast<uint32_t>((col0 + min(uv * epu, CG - epu)) * ES);
       sl.v_col[j] = uv * epu < CG ? uv * epu : -1;
     }
   }
   return sl;
 }
 
-// MASK = false: every row of the chunk lies in the sequence (no clamping)
-template <bool DBIG, int ES, int CG, int STG, bool MASK>
-__device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
-                                          const MomArgs& a, const char* qh, int row0) {
-  const uint32_t qrow = static_cast<uint32_t>(a.ldk * ES);
+// MASK = false: every row of the chunk lies in the sequence: one uniform row address plus each unit's
+// loop-invariant offset.  MASK = true: rows clamped into the sequence one by one.
+// The head's q / k / v rows as buffer resources (a head's rows span < 2^31 bytes, which the kernel's
+// callers check).
+struct WsRows {
+  __amdgpu_buffer_rsrc_t q, k, v;
+};
+
+// Offsets of the staged units of the chunk at row0 in the buffers of WsRows: with every row of the
+// chunk in the sequence, one uniform row offset (so) and the loop-invariant per-unit offsets; else
+// so = 0 and each unit's row clamped into the sequence (its staged value is zeroed).  Only the
+// offsets depend on the case, so the loads themselves are one code path.
+template <int U>
+struct WsOffs {
+  uint32_t v[U];
+  int so;
+};
+
+template <int U>
+__device__ __forceinline__ WsOffs<U> ws_offs(const uint32_t (&rel)[U], const int (&tok)[U], uint32_t rowb, int row0,
+                                             int n) {
+  WsOffs<U> o;
+  if (row0 >= 0 && row0 + MOM_C <= n) {
+    o.so = static_cast<int>(static_cast<uint32_t>(row0) * rowb);
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j) {
-    const int r = MASK ? clamp_row(row0 + sl.q_tok[j], static_cast<int>(a.n)) : row0 + sl.q_tok[j];
-    st.q[j] = *reinterpret_cast<const uint4*>(qh + static_cast<uint32_t>(r) * qrow + sl.q_off[j]);
+    for (int j = 0; j < U; ++j) o.v[j] = rel[j];
+  } else {
+    o.so = 0;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const uint32_t r = static_cast<uint32_t>(clamp_row(row0 + tok[j], n));
+      o.v[j] = r * rowb + (rel[j] - static_cast<uint32_t>(tok[j]) * rowb);
+    }
   }
+  return o;
 }
 
-template <bool DBIG, int ES, int CG, int STG, bool MASK>
+template <bool DBIG, int ES, int CG, int STG>
+__device__ __forceinline__ void ws_load_q(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
+                                          const MomArgs& a, const WsRows& rs, int row0) {
+  constexpr int QV = WsStage<DBIG, ES, CG, STG>::QV;
+  const WsOffs<QV> o = ws_offs<QV>(sl.q_rel, sl.q_tok, static_cast<uint32_t>(a.ldk * ES), row0, static_cast<int>(a.n));
+#pragma unroll
+  for (int j = 0; j < QV; ++j)
+    st.q[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.q, o.v[j], o.so, 0));
+}
+
+template <bool DBIG, int ES, int CG, int STG>
 __device__ __forceinline__ void ws_load_kv(WsStage<DBIG, ES, CG, STG>& st, const WsSlots<DBIG, ES, CG, STG>& sl,
-                                           const MomArgs& a, const char* kh, const char* vh, int row0) {
-  constexpr bool PAIR = WsStage<DBIG, ES, CG, STG>::PAIR;
+                                           const MomArgs& a, const WsRows& rs, int row0) {
   constexpr bool PAIR16 = WsStage<DBIG, ES, CG, STG>::PAIR16;
+  constexpr int QV = WsStage<DBIG, ES, CG, STG>::QV, VV = WsStage<DBIG, ES, CG, STG>::VV;
   const uint32_t krow_b = static_cast<uint32_t>(a.ldk * ES), vrow_b = static_cast<uint32_t>(a.ldv * ES);
-  // the token of unit j: one per thread, or the pair 2 p, 2 p + 1
-  auto row = [&](int j) -> uint32_t {
-    const int t = row0 + (PAIR || PAIR16 ? 2 * (sl.sidx & 15) + j : sl.sidx & (MOM_C - 1));
-    return static_cast<uint32_t>(MASK ? clamp_row(t, static_cast<int>(a.n)) : t);
-  };
+  const int n = static_cast<int>(a.n);
   if constexpr (PAIR16) {
-    const uint2 k0 = *reinterpret_cast<const uint2*>(kh + row(0) * krow_b + sl.k_off[0]);
-    const uint2 k1 = *reinterpret_cast<const uint2*>(kh + row(1) * krow_b + sl.k_off[0]);
-    const uint2 v0 = *reinterpret_cast<const uint2*>(vh + row(0) * vrow_b + sl.v_off[0]);
-    const uint2 v1 = *reinterpret_cast<const uint2*>(vh + row(1) * vrow_b + sl.v_off[0]);
+    // half units of tokens 2 p and 2 p + 1 (k_rel / v_rel: token 2 p's)
+    const int t0 = ws_kv_tok<DBIG, ES, CG, STG>(sl.sidx, 0);
+    const uint32_t krel[2] = {sl.k_rel[0], sl.k_rel[0] + krow_b}, vrel[2] = {sl.v_rel[0], sl.v_rel[0] + vrow_b};
+    const int tok[2] = {t0, t0 + 1};
+    const WsOffs<2> ko = ws_offs<2>(krel, tok, krow_b, row0, n), vo = ws_offs<2>(vrel, tok, vrow_b, row0, n);
+    const uint2 k0 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.k, ko.v[0], ko.so, 0));
+    const uint2 k1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.k, ko.v[1], ko.so, 0));
+    const uint2 v0 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.v, vo.v[0], vo.so, 0));
+    const uint2 v1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs.v, vo.v[1], vo.so, 0));
     st.k[0] = uint4{k0.x, k0.y, k1.x, k1.y};
     st.v[0] = uint4{v0.x, v0.y, v1.x, v1.y};
     return;
   }
+  int ktok[QV], vtok[VV];
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::QV; ++j)
-    st.k[j] = *reinterpret_cast<const uint4*>(kh + row(j) * krow_b + sl.k_off[j]);
+  for (int j = 0; j < QV; ++j) ktok[j] = ws_kv_tok<DBIG, ES, CG, STG>(sl.sidx, j);
 #pragma unroll
-  for (int j = 0; j < WsStage<DBIG, ES, CG, STG>::VV; ++j)
-    st.v[j] = *reinterpret_cast<const uint4*>(vh + row(j) * vrow_b + sl.v_off[j]);
+  for (int j = 0; j < VV; ++j) vtok[j] = ws_kv_tok<DBIG, ES, CG, STG>(sl.sidx, j);
+  const WsOffs<QV> ko = ws_offs<QV>(sl.k_rel, ktok, krow_b, row0, n);
+  const WsOffs<VV> vo = ws_offs<VV>(sl.v_rel, vtok, vrow_b, row0, n);
+#pragma unroll
+  for (int j = 0; j < QV; ++j)
+    st.k[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.k, ko.v[j], ko.so, 0));
+#pragma unroll
+  for (int j = 0; j < VV; ++j)
+    st.v[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.v, vo.v[j], vo.so, 0));
 }
 
 // An empty use of every staged register: the compiler completes their loads before it (where the
@@ -220,8 +276,9 @@ __device__ __forceinline__ void ws_store_q(const WsStage<DBIG, ES, CG, STG>& st,
     float f[8];
     unit_floats<ES>(st.q[j], a.dtype, f);
     float* qd = Qs + sl.q_lds[j];
-    *reinterpret_cast<floatx4*>(qd) = floatx4{f[0], f[1], f[2], f[3]} * sc;
-    if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4], f[5], f[6], f[7]} * sc;
+    // element by element (a vector times sc kept a splat of sc in four scalar registers)
+    *reinterpret_cast<floatx4*>(qd) = floatx4{f[0] * sc, f[1] * sc, f[2] * sc, f[3] * sc};
+    if constexpr (wide) *reinterpret_cast<floatx4*>(qd + 4) = floatx4{f[4] * sc, f[5] * sc, f[6] * sc, f[7] * sc};
   }
   const int tid = sl.sidx;
   if (tid < MOM_C) Qs[tid * LDQ + a.d] = (!MASK || (row0 + tid >= 0 && row0 + tid < a.n)) ? 1.f : 0.f;
@@ -240,8 +297,14 @@ __device__ __forceinline__ void ws_store_kv(const WsStage<DBIG, ES, CG, STG>& st
     const int kd = sl.k_dim[0];
     if (kd >= 0) {
       const floatx4 f0 = __builtin_bit_cast(floatx4, st.k[0]), f1 = __builtin_bit_cast(floatx4, st.k[1]);
+      // two 4-byte stores per dimension (one ds_write2_b32 from the loaded registers as they are; an
+      // 8-byte store would need the pair copied into adjacent registers first)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) *reinterpret_cast<floatx2*>(Kt + (kd + m) * MOM_LDT + t0) = floatx2{f0[m] * ok0, f1[m] * ok1};
+      for (int m = 0; m < 4; ++m) {
+        float* kp = Kt + (kd + m) * MOM_LDT + t0;
+        kp[0] = f0[m] * ok0;
+        kp[1] = f1[m] * ok1;
+      }
     }
     const int c0 = sl.v_col[0];
     if (c0 >= 0) {
@@ -494,11 +557,30 @@ __device__ __forceinline__ void ws_qsingle_mma(floatx4 (&o)[2][CT], const uint2 
 // (CG * 8 threads, 4 tokens each) and, with den, low_den (columns CG .. CG + 3 of a wave's partials: the
 // denominator sums of its 4 lane groups).
 constexpr int WS_RCOLS_EXTRA = 4;
+// Byte offsets of a reducing thread's output units from the chunk's first output row (4 rows of one
+// column per unit): loop-invariant, so every chunk's stores take one uniform row address plus these.
+template <int CG>
+struct WsRedRel {
+  static constexpr int IT = CG * 8 / WS_REDUCERS;
+  uint32_t rel[IT];
+};
+template <int CG>
+__device__ __forceinline__ WsRedRel<CG> ws_red_rel(const MomArgs& a, int tid) {
+  WsRedRel<CG> rr;
+#pragma unroll
+  for (int it = 0; it < WsRedRel<CG>::IT; ++it) {
+    const int e = it * WS_REDUCERS + tid;
+    const int col = e % CG, t4 = 4 * (e / CG);
+    rr.rel[it] = static_cast<uint32_t>(t4 * a.ldo + col) * 4u;
+  }
+  return rr;
+}
+
 template <int CG>
 __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* red, int64_t obase, int64_t row0,
-                                                int col0, bool den) {
+                                                int col0, bool den, const WsRedRel<CG>& rr) {
   constexpr int WS = (CG + WS_RCOLS_EXTRA) * MOM_LDR;
-  constexpr int IT = CG * 8 / WS_REDUCERS;
+  constexpr int IT = WsRedRel<CG>::IT;
   const int tid = threadIdx.x;  // < WS_REDUCERS
   // every LDS read first (one wait for all of them instead of one per read), then the sums in the
   // fixed wave order
@@ -510,16 +592,22 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 #pragma unroll
     for (int q = 0; q < 4; ++q) part[it][q] = *reinterpret_cast<const floatx4*>(red + q * WS + red_off(col, t4));
   }
+  // the chunk's first output row of this column group as a buffer resource (uniform; rebuilt per chunk
+  // by scalar instructions, so the offsets stay small at any sequence length)
+  const __amdgpu_buffer_rsrc_t out = raw_rsrc(a.low_num + (obase + row0) * a.ldo + col0);
+  const int rstep = __builtin_amdgcn_readfirstlane(a.ldo * 4);
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int e = it * WS_REDUCERS + tid;
-    const int col = e % CG, t4 = 4 * (e / CG);
     floatx4 acc = part[it][0];
 #pragma unroll
     for (int q = 1; q < 4; ++q) acc += part[it][q];
-    float* dst = a.low_num + (obase + row0 + t4) * a.ldo + col0 + col;
+    // (each element through a float first: hipcc lowered __builtin_bit_cast of the vector element acc[r]
+    // itself to element 0 for every r)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) __builtin_nontemporal_store(acc[r], dst + r * a.ldo);
+    for (int r = 0; r < 4; ++r) {
+      const float x = acc[r];
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), out, rr.rel[it], r * rstep, BUF_NT);
+    }
   }
   if (den && tid >= WS_REDUCERS - MOM_C) {
     const int tok = tid - (WS_REDUCERS - MOM_C);
@@ -536,7 +624,7 @@ __device__ __forceinline__ void ws_reduce_store(const MomArgs& a, const float* r
 template <bool DBIG, int ES, int CG, int STG, bool WQ, bool VX>
 __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, const WsSlots<DBIG, ES, CG, STG>& sl,
                                               const MomArgs& a, float* kvb, float* qb, int c, int nch, int first,
-                                              const char* kh, const char* vh, const char* qh) {
+                                              const WsRows& rs) {
   constexpr int KVF = ws_kv_floats(DBIG, CG);
   constexpr int QF = ws_q_floats(DBIG);
   const int kv_row = first + (c + 1) * MOM_C;
@@ -547,8 +635,8 @@ __device__ __forceinline__ void ws_stage_step(WsStage<DBIG, ES, CG, STG>& pre, c
                                              kv_row);
   }
   if (WQ && c < nch) ws_store_q<DBIG, ES, CG, STG, true>(pre, sl, a, qb + (c & 1) * QF, q_row);
-  ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-  if (WQ) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
+  ws_load_kv<DBIG, ES, CG, STG>(pre, sl, a, rs, kv_row + MOM_C);
+  if (WQ) ws_load_q<DBIG, ES, CG, STG>(pre, sl, a, rs, q_row + MOM_C);
 }
 
 // The whole scan for one wave: UPD = update wave (slot = w) or query wave (slot = (w + 2) & 3), NT tiles
@@ -612,9 +700,11 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   const char* qh = static_cast<const char*>(a.q) + bh * hstride * a.ldk * ES;
   const char* kh = static_cast<const char*>(a.k) + bh * hstride * a.ldk * ES;
   const char* vh = static_cast<const char*>(a.v) + bh * hstride * a.ldv * ES;
+  const WsRows rs{raw_rsrc(qh), raw_rsrc(kh), raw_rsrc(vh)};
   const int64_t tile0 = (static_cast<int64_t>(fs) * 4 + slot) * NTS;
   const MomLane<NT, NX> m = mom_lane<NT, NX>(a, tile0, li, lg);
   const WsSlots<DBIG, ES, CG, STG> sl = ws_slots<DBIG, ES, CG, STG>(a, col0, TOT != 0 ? tid - 256 : tid);
+  const WsRedRel<CG> rrel = ws_red_rel<CG>(a, tid);
   // operand (pair p, column tile ct, hi / lo) of this slot and block parity par
   auto hand_at = [&](int par, int p, int ct, int hl) -> uint4* {
     return wa.hand + ((((static_cast<int64_t>(wg) * 2 + par) * 4 + slot) * NPS + p) * CT + ct) * 128 + hl * 64 + lane;
@@ -721,20 +811,20 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   constexpr bool STAGE = TOT != 0 ? !UPD : (UPD || STG == WS_THREADS);
   WsStage<DBIG, ES, CG, STG> pre;
   if constexpr (STAGE) {
-    ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first);
+    ws_load_kv<DBIG, ES, CG, STG>(pre, sl, a, rs, first);
     ws_store_kv<DBIG, ES, CG, STG, true, VX>(pre, sl, a, kvb, reinterpret_cast<__bf16*>(kvb + mom_krows(DBIG) * MOM_LDT),
                                              first);
   }
   __syncthreads();
   if constexpr (STAGE) {
-    ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, first + MOM_C);  // slot 1
-    if constexpr (TOT == 0) ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, first);
+    ws_load_kv<DBIG, ES, CG, STG>(pre, sl, a, rs, first + MOM_C);  // slot 1
+    if constexpr (TOT == 0) ws_load_q<DBIG, ES, CG, STG>(pre, sl, a, rs, first);
   }
 
   if constexpr (!UPD && TOT != 0) {
     // segment totals: the query waves stage the keys and values, with the same iterations and barriers
     for (int c = 0; c <= nch; ++c) {
-      ws_stage_step<DBIG, ES, CG, STG, false, VX>(pre, sl, a, kvb, qb, c, nch, first, kh, vh, qh);
+      ws_stage_step<DBIG, ES, CG, STG, false, VX>(pre, sl, a, kvb, qb, c, nch, first, rs);
       __syncthreads();
     }
     return;
@@ -795,11 +885,12 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
         // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
         // never stored), one code path, so nothing waits on them before their store an iteration on
         if constexpr (STAGE) {
-          ws_load_kv<DBIG, ES, CG, STG, true>(pre, sl, a, kh, vh, kv_row + MOM_C);
-          ws_load_q<DBIG, ES, CG, STG, true>(pre, sl, a, qh, q_row + MOM_C);
+          ws_load_kv<DBIG, ES, CG, STG>(pre, sl, a, rs, kv_row + MOM_C);
+          ws_load_q<DBIG, ES, CG, STG>(pre, sl, a, rs, q_row + MOM_C);
         }
         if constexpr (UPD) {
-          if (!totals && c >= 2) ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den);
+          if (!totals && c >= 2)
+            ws_reduce_store<CG>(a, redb + (c & 1) * REDF, obase, first + (c - 2) * MOM_C, col0, den, rrel);
         }
       }
   };
@@ -905,7 +996,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     }
   // partials of the last chunk (written by the query waves in iteration nch)
   if constexpr (UPD) {
-    if (!totals) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den);
+    if (!totals) ws_reduce_store<CG>(a, redb + ((nch - 1) & 1) * REDF, obase, first + (nch - 1) * MOM_C, col0, den, rrel);
     if (totals && persist) {
       // phase 3: the slice back into the persistent state (each (head, feature, column) belongs to one
       // lane of the grid); the denominators from column group 0
