@@ -473,36 +473,18 @@ __device__ __forceinline__ void ws_qfeat(float (&x)[4], const WsQOps& o, int tt)
   }
 }
 
-// The frozen denominators of a slot as one more column tile of the query products: column 0 holds
-// them (lanes li = 0), the other 15 columns are zero, so phi_q . den comes out of the matrix cores in
-// column 0 of the tile (lanes li = 0, rows 4 lg + r) with the same split products as the numerators.
-// src: the slot's [NTS][16] denominators; the pair layout of ws_qpair_mma (features 4 lg .. 4 lg + 3 of
-// tiles 2 p and 2 p + 1), the odd tile's as in ws_qsingle_mma.
+// The frozen denominators of a slot for the query waves' VALU dot phi_q . den: the fp32 values of the
+// features the lane forms, in the pair layout of ws_qpair_mma (features 4 lg .. 4 lg + 3 of tiles 2 p
+// and 2 p + 1: dv[p][0], dv[p][1]) and the odd tile's (od).  src: the slot's [NTS][16] denominators.
 template <int NT>
-__device__ __forceinline__ void ws_den_ops(bf16x8 (&dh)[NT / 2 > 0 ? NT / 2 : 1], bf16x8 (&dl)[NT / 2 > 0 ? NT / 2 : 1],
-                                           uint2& odh, uint2& odl, const float* src, int li, int lg) {
-  // every lane loads (in bounds, no branch), lanes li != 0 keep zeros
-  const bool on = li == 0;
+__device__ __forceinline__ void ws_den_vals(floatx4 (&dv)[NT / 2 > 0 ? NT / 2 : 1][2], floatx4& od, const float* src,
+                                            int lg) {
 #pragma unroll
   for (int p = 0; p < NT / 2; ++p) {
-    const floatx4 d0 = *reinterpret_cast<const floatx4*>(src + (2 * p) * 16 + 4 * lg);
-    const floatx4 d1 = *reinterpret_cast<const floatx4*>(src + (2 * p + 1) * 16 + 4 * lg);
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = on ? d0[j] : 0.f;
-      x[4 + j] = on ? d1[j] : 0.f;
-    }
-    split_bf16(x, dh[p], dl[p]);
+    dv[p][0] = *reinterpret_cast<const floatx4*>(src + (2 * p) * 16 + 4 * lg);
+    dv[p][1] = *reinterpret_cast<const floatx4*>(src + (2 * p + 1) * 16 + 4 * lg);
   }
-  if constexpr ((NT & 1) != 0) {
-    const floatx4 d0 = *reinterpret_cast<const floatx4*>(src + (NT - 1) * 16 + 4 * lg);
-    float x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = on ? d0[j] : 0.f;
-    split_pair(x[0], x[1], odh.x, odl.x);
-    split_pair(x[2], x[3], odh.y, odl.y);
-  }
+  if constexpr ((NT & 1) != 0) od = *reinterpret_cast<const floatx4*>(src + (NT - 1) * 16 + 4 * lg);
 }
 
 typedef short shortx4 __attribute__((ext_vector_type(4)));
@@ -554,8 +536,8 @@ __device__ __forceinline__ void ws_qsingle_mma(floatx4 (&o)[2][CT], const uint2 
 // Fixed-order sum of the 4 query waves' partials of the chunk at row0 -> low_num rows of the CG columns
 // (non-temporal stores: the partials are read only by the next kernel, and the workgroups' state
 // handoff, rewritten every query block, should keep its place in L2)
-// (CG * 8 threads, 4 tokens each) and, with den, low_den (columns CG .. CG + 3 of a wave's partials: the
-// denominator sums of its 4 lane groups).
+// (CG * 8 threads, 4 tokens each) and, with den, low_den (column CG of a wave's partials: its
+// denominator sums).
 constexpr int WS_RCOLS_EXTRA = 4;
 // Byte offsets of a reducing thread's output units from the chunk's first output row (4 rows of one
 // column per unit): loop-invariant, so every chunk's stores take one uniform row address plus these.
@@ -714,8 +696,8 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   float den_p[UPD ? NT : 1];  // per-lane partial denominators (this lane's tokens)
   bf16x8 sh[UPD || NP == 0 ? 1 : NP][CT], sv[UPD || NP == 0 ? 1 : NP][CT];
   uint2 oh[CT], ov[CT];  // the odd last tile's operands
-  bf16x8 dh[UPD || NP == 0 ? 1 : NP], dl[UPD || NP == 0 ? 1 : NP];  // the denominators' column tile
-  uint2 odh = uint2{0u, 0u}, odl = uint2{0u, 0u};
+  floatx4 dvv[UPD || NP == 0 ? 1 : NP][2];  // the frozen denominators of the lane's features (fp32)
+  floatx4 odv = floatx4{0.f, 0.f, 0.f, 0.f};
   if constexpr (UPD) {
 #pragma unroll
     for (int kt = 0; kt < NT; ++kt) {
@@ -732,7 +714,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
       oh[ct] = ov[ct] = uint2{0u, 0u};
     }
 #pragma unroll
-    for (int p = 0; p < (NP > 0 ? NP : 1); ++p) dh[p] = dl[p] = z;
+    for (int p = 0; p < (NP > 0 ? NP : 1); ++p) dvv[p][0] = dvv[p][1] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
   // zero every staging buffer (padding rows / columns are never written again) and the denominators of
@@ -774,7 +756,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
   } else {
     if (from_init) {
       // phase 2: the rows of the segment's first block see S_init: split it into this wave's operands
-      // and its denominators into block parity 0
+      // and take its denominators
       const floatx4* ss = reinterpret_cast<const floatx4*>(sstate) + (slot * NTS) * CT * 64 + lane;
       auto tile = [&](int kt, int ct) { return ss[(kt * CT + ct) * 64]; };
 #pragma unroll
@@ -799,7 +781,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           split_pair(s0[2], s0[3], oh[ct].y, ov[ct].y);
         }
       }
-      if (den) ws_den_ops<NT>(dh, dl, odh, odl, sden + slot * NTS * 16, li, lg);
+      if (den) ws_den_vals<NT>(dvv, odv, sden + slot * NTS * 16, lg);
     }
   }
   // one register set of staged units: slot x (keys / values of chunk x, queries of chunk x - 1) is loaded
@@ -879,7 +861,7 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
             }
             // the block's denominators (written with the state, block parity): zero in a workgroup
             // without the denominator column
-            ws_den_ops<NT>(dh, dl, odh, odl, denb + (((c / cpb) & 1) * 4 + slot) * NTS * 16, li, lg);
+            ws_den_vals<NT>(dvv, odv, denb + (((c / cpb) & 1) * 4 + slot) * NTS * 16, lg);
           }
         }
         // slot c + 2: unconditional loads with rows clamped into the sequence (past the end they are
@@ -931,12 +913,12 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
     } else {
       if (c >= 1) {
         const float* Qs = qb + ((c - 1) & 1) * QF;
-        floatx4 o[2][CT], od[2][1];  // od: the denominators' column tile (column 0)
+        floatx4 o[2][CT];
+        float dq[2] = {0.f, 0.f};  // phi_q . den over the lane's features, row li + 16 tt (VALU, fp32)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct) o[tt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
-          od[tt][0] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
         // operands of the first two tiles; each pair's successor is loaded once its features are formed
         WsQOps op0, op1;
@@ -959,11 +941,20 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           }
           if (2 * p + 2 < NT) ws_qload<NT, NX, LDQ>(op0, 2 * p + 2 < NT ? 2 * p + 2 : 0, Qs, m, li);
           if (2 * p + 3 < NT) ws_qload<NT, NX, LDQ>(op1, 2 * p + 3 < NT ? 2 * p + 3 : 0, Qs, m, li);
+          // the denominators' dot from the fp32 features, before the in-place split consumes them
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dq[tt] = fmaf(x[tt][j], dvv[p][0][j], dq[tt]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dq[tt] = fmaf(x[tt][4 + j], dvv[p][1][j], dq[tt]);
+          }
+          // materialised here, ahead of the split (left to the compiler, the chain sinks to its one use
+          // after the products and every feature value then needs a copy next to its in-place split)
+          asm volatile("" : "+v"(dq[0]), "+v"(dq[1]));
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) split_bf16(x[tt], ah[tt], al[tt]);
           ws_qpair_mma<CT>(o, ah, al, sh[p], sv[p]);
-          const bf16x8 dhp[1] = {dh[p]}, dlp[1] = {dl[p]};
-          ws_qpair_mma<1>(od, ah, al, dhp, dlp);
         }
         if constexpr (ODD) {
           uint2 ah[2], al[2];
@@ -971,22 +962,28 @@ __device__ __forceinline__ void ws_body(const WsArgs& wa, int wg, int64_t bh, in
           for (int tt = 0; tt < 2; ++tt) {
             float x0[4];
             ws_qfeat<NX>(x0, op0, tt);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dq[tt] = fmaf(x0[j], odv[j], dq[tt]);
+            asm volatile("" : "+v"(dq[tt]));
             split_pair(x0[0], x0[1], ah[tt].x, al[tt].x);
             split_pair(x0[2], x0[3], ah[tt].y, al[tt].y);
           }
           ws_qsingle_mma<CT>(o, ah, al, oh, ov);
-          const uint2 odhp[1] = {odh}, odlp[1] = {odl};
-          ws_qsingle_mma<1>(od, ah, al, odhp, odlp);
         }
         // this wave's partials of chunk c - 1 -> red[(c - 1) & 1], column-major (red_off); column CG:
-        // the denominator sums (column 0 of the denominators' tile, lanes li = 0)
+        // the denominator sums (the lanes' dots summed over the 4 lane groups)
         float* rw = redb + ((c - 1) & 1) * REDF + qw * (CG + WS_RCOLS_EXTRA) * MOM_LDR;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
             *reinterpret_cast<floatx4*>(rw + red_off(16 * ct + li, 16 * tt + 4 * lg)) = o[tt][ct];
-          if (den && li == 0) *reinterpret_cast<floatx4*>(rw + red_off(CG, 16 * tt + 4 * lg)) = od[tt][0];
+          if (den) {
+            float t = dq[tt];
+            t += __shfl_xor(t, 16);
+            t += __shfl_xor(t, 32);
+            if (lg == 0) rw[red_off(CG, 16 * tt + li)] = t;
+          }
         }
       }
     }
