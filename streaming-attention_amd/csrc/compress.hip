@@ -173,6 +173,10 @@ __device__ __forceinline__ void projection_scores2(const void* k0, int64_t off0,
 // products in dimension order, as projection_scores2 does, so each equals the score the call at that
 // level would compute from the row.  acc[0] is the node's own score, acc[1 + l] the ancestor's at level
 // 1 + l.  fp32 rows are read in 16-byte units when `vec`; each element is converted once.
+// rows of the level-0 launch read 4 units (64 bytes) at a time: 74 registers, 6 workgroups per compute
+// unit (8 units: 90 registers, 5 per unit, c3 level 0 0.367 -> 0.338 ms for the 3 launches; 2 units:
+// 66 registers, 7 per unit, 0.392 ms)
+constexpr int ANC_RB = 4;
 __device__ __forceinline__ void projection_scores_anc(const void* k, int64_t off, int d, int dtype, bool vec,
                                                       const double* dird, int na, double (&acc)[1 + CMP_MAX_ANC]) {
 #pragma unroll
@@ -185,13 +189,13 @@ __device__ __forceinline__ void projection_scores_anc(const void* k, int64_t off
   if (vec && dtype == F32) {
     const floatx4* r = reinterpret_cast<const floatx4*>(static_cast<const float*>(k) + off);
     const int nu = d / 4;
-    for (int u0 = 0; u0 < nu; u0 += 8) {
-      floatx4 x[8];
+    for (int u0 = 0; u0 < nu; u0 += ANC_RB) {
+      floatx4 x[ANC_RB];
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
+      for (int t = 0; t < ANC_RB; ++t)
         if (u0 + t < nu) x[t] = r[u0 + t];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < ANC_RB; ++t) {
         if (u0 + t >= nu) continue;
 #pragma unroll
         for (int e = 0; e < 4; ++e) step(static_cast<double>(x[t][e]), 4 * (u0 + t) + e);
@@ -518,8 +522,9 @@ __device__ __forceinline__ void compress_node(const CompressArgs& a, const int n
       const bool two = i1 < n_in;
       float s0, s1;
       // (groups of a merge launch keep 4 units of each row in flight: their registers are shared by
-      // every step of the launch)
-      projection_scores2<G::row_batch>(a.k, (bh * a.n + src_s[i]) * a.d, a.k,
+      // every step of the launch; the level-0 launch with ancestor scores keeps 2 on this path, which
+      // its raw nodes do not take, so that it does not set the launch's register count)
+      projection_scores2<ANC ? 2 : G::row_batch>(a.k, (bh * a.n + src_s[i]) * a.d, a.k,
                                        (bh * a.n + src_s[two ? i1 : i]) * a.d, two, a.d, a.dtype, vec, dir_s, s0, s1);
       key_s[i] = s0;
       if (two) key_s[i1] = s1;
