@@ -220,7 +220,10 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
 // instruction order, so a code-motion barrier stands in for the workgroup barrier).
 struct BlockGroup {
   static constexpr int threads = CMP_THREADS;
-  static constexpr int row_batch = 8;  // 16-byte units of a gathered key row in flight (projection_scores2)
+  // 16-byte units of a gathered key row in flight (projection_scores2): 4 keeps compress_kernel<false> at
+  // 75 registers, 6 workgroups per compute unit (8: 107 registers, 4 per unit; compressor of c4 0.241 ->
+  // 0.214 ms, of c2 0.037 -> 0.034 ms; 2: 59 registers, c4 0.206 but c2 0.039 ms)
+  static constexpr int row_batch = 4;
   int tid;
   __device__ __forceinline__ void sync() const { __syncthreads(); }
 };
