@@ -49,12 +49,25 @@ ANCESTOR_MIN_ROW_BYTES = 256
 # of at most 128 items (a wave sorts them in a quarter of the work of 256), groups above
 # (32 x 65536 tokens, 256-item calls: 9 launches 372-379 us, groups 355-372, waves 418-432;
 # 4 x 32 x 16384, 128-item calls: 9 launches 258-261 us, groups 271-281, waves 238-250);
-# "0": sta_compress_nodes level by level.  The nodes are the same bit for bit either way.
+# "0": sta_compress_nodes level by level.  The nodes are the same bit for bit either way.  "auto" also
+# keeps the level-by-level launches when the first subtree launch would have fewer workgroups than the
+# device has compute units (few heads: a subtree's levels run one after another on a few units, where
+# a level's own launch spreads its nodes over all of them; compressor of 1 x 65536 tokens 0.150 ->
+# 0.119 ms, 16 x 65536 0.251 -> 0.230 ms; 32 x 65536 keeps the subtrees, 0.332 against 0.338 ms).
 MERGE_LAUNCHES = os.environ.get("STA_MERGE_LAUNCHES", "auto")
 MERGE_GROUPS = int(os.environ.get("STA_MERGE_GROUPS", "4"))  # 256-thread groups per workgroup
 MERGE_BOTTOM = int(os.environ.get("STA_MERGE_BOTTOM", "16"))  # nodes of a subtree's lowest level
 
 _side_streams: Dict[str, "torch.cuda.Stream"] = {}
+_cu_counts: Dict[int, int] = {}
+
+
+def _compute_units(dev: torch.device) -> int:
+    """Compute units of the device (cached per device index)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cu_counts:
+        _cu_counts[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _cu_counts[idx]
 
 
 def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
@@ -400,6 +413,8 @@ def prefill(
                 return [(ln, _i32(ln.table, dev)) for ln in launches]
 
             merge_l = _on_device(("merges", gt, MERGE_GROUPS, MERGE_BOTTOM, dr.max_in, f64) + pkey, dev, build_merges)
+            if MERGE_LAUNCHES == "auto" and merge_l and merge_l[0][0].workgroups * bh < _compute_units(dev):
+                merge_l = []
 
     lrows, lld, _ = _native.moment_partials_layout(n, dv)
     low_num = torch.empty((bh, fsplit, lrows, lld), device=dev, dtype=torch.float32)
